@@ -1,0 +1,115 @@
+/* C ABI of the MI355X (gfx950) MTP-verify MoE path: libssmoe.so.
+ *
+ * Every pointer argument is a device pointer unless stated otherwise; `stream` is a hipStream_t (NULL = the
+ * legacy default stream). No entry point allocates device memory, synchronises the host, or uses atomics in a
+ * floating-point reduction; every call is capturable in a HIP graph. Each returns 0 on success or a nonzero
+ * status whose text is given by ssmoe_last_error() (argument errors: SSMOE_EINVAL; launch errors: SSMOE_EHIP).
+ * Reference files are cited as path:line in fortil/slotstream-spark.
+ */
+#ifndef SSMOE_H
+#define SSMOE_H
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSMOE_OK 0
+#define SSMOE_EINVAL 1
+#define SSMOE_EHIP 2
+
+/* Device status bits raised by kernels on bad input (the kernel skips the entry and continues). */
+#define SSMOE_ERR_EXPERT_ID 1 /* expert id outside [0, E) */
+#define SSMOE_ERR_SLOT 2      /* map entry outside [0, n_slots): expert not resident */
+#define SSMOE_ERR_TOKEN 4     /* draft token outside [0, V) */
+
+/* Text of the last error on this host thread ("" if none). */
+const char* ssmoe_last_error(void);
+
+/* ABI version (incremented on any signature change). */
+int ssmoe_version(void);
+
+/* Reads the status word of the current device into *flags (a host pointer) and clears it when clear != 0.
+ * Synchronises the device. No reference counterpart: the reference kernels do not check ids. */
+int ssmoe_device_error(int* flags, int clear);
+
+/* Diagnostics (no reference counterpart): when buf (device memory, >= 16384 uint64) is non-null, every later
+ * persistent MoE launch (ssmoe_moe_decode, ssmoe_moe_verify_layer) writes per-workgroup phase timestamps
+ * (s_memrealtime, 100 MHz) to buf[workgroup * 16 + phase]; NULL switches it off. Process-wide, not thread-safe. */
+int ssmoe_set_trace(void* buf, int64_t entries);
+
+/* Byte offsets of the nine pieces of one affine-4bit expert record (gate.w gate.s gate.b up.w up.s up.b
+ * down.w down.s down.b) followed by the record size, written to off[10] (host pointer).
+ * Replaces the constants of kernels/moe_gemv_affine.py:22-25 (RECORD_BYTES, O_*), parametrised by (H, I). */
+int ssmoe_record_layout(int H, int I, int64_t* off);
+
+/* Routed experts of one decode/verify step, router-free.
+ * Replaces moe_decode (kernels/moe_gemv_affine.py:113-147; kernels _gate_up :56-77, _down :80-97,
+ * _rank_sum :100-110). x: [R, H] bf16 (x_is_f32 = 0) or fp32 (1); expert_ids int32 [R, K]; weights fp32 [R, K];
+ * the record of expert e is at slot_ptr[map[layer * E + e]] (map int32 [map_len], slot_ptr int64 [n_slots]).
+ * Writes h_buf fp32 [R, K, I], o_buf fp32 [R, K, H] (o = (Wd h) * w), out fp32 [R, H] (rank-order sum).
+ * Constraints: H % 128 == 0, H <= 4096, I % 128 == 0, I <= 1024, 1 <= K <= 16. */
+int ssmoe_moe_decode(const void* x, int x_is_f32, const int32_t* expert_ids, const float* weights, int layer,
+                     const int32_t* map, int64_t map_len, const int64_t* slot_ptr, int64_t n_slots, float* h_buf,
+                     float* o_buf, float* out, int R, int H, int I, int K, int E, void* stream);
+
+/* Stable top-k per row. Replaces topk_stable (kernels/topk_stable.py:85-113, kernel :29-82).
+ * scores fp32 [R, N], N <= 65536; n_valid int32 [R] or NULL; out_idx int32 [R, k]; out_val fp32 [R, k] or NULL.
+ * k <= 16: sorted by (value desc, index asc); larger k: by index asc; short rows padded with -1 / -inf. */
+int ssmoe_topk_stable(const float* scores, const int32_t* n_valid, int32_t* out_idx, float* out_val, int R, int N,
+                      int k, void* stream);
+
+/* Dense bf16 projection out[t, n] = bf16(sum_k x[t, k] w[n, k]) with fp32 accumulation in a fixed order.
+ * Replaces lin() on bf16 weights (model/layers.py:62-76 -> kernels/gemv_affine.py:214-262 dense path).
+ * x bf16 [T, H], w bf16 [N, H], out bf16 [T, N]; H % 8 == 0, H <= 8192. */
+int ssmoe_dense_gemv_bf16(const uint16_t* x, const uint16_t* w, uint16_t* out, int T, int H, int N, void* stream);
+
+/* Router: logits = bf16(x router_w^T), scores = logits (+ bias), probs = softmax(scores) in fp32, top-k with
+ * ties to the lower index, weights = topk / sum(topk) in rank order.
+ * Replaces Segments.seg_router (model/layers.py:336-348) and reference_torch.moe_ref:121-124. bias fp32 [E] or
+ * NULL (the reference has no bias); logits bf16 [T, E] (required, scratch or output); probs fp32 [T, E] or NULL;
+ * ids int32 [T, K]; weights fp32 [T, K]. E <= 8192, K <= 16. */
+int ssmoe_router(const uint16_t* x, const uint16_t* router_w, const float* bias, uint16_t* logits, float* probs,
+                 int32_t* ids, float* weights, int T, int H, int E, int K, void* stream);
+
+/* Bytes of the workspace ssmoe_moe_verify_layer needs for T tokens. */
+int64_t ssmoe_verify_workspace_bytes(int T, int H, int I, int Is, int K, int E);
+
+/* One MoE layer of the verify step: router (as ssmoe_router) -> routed experts (as ssmoe_moe_decode) ->
+ * shared expert with its sigmoid gate -> y = bf16(routed) + shared, in bf16.
+ * Replaces GraphSet._moe + Segments.seg_router (runtime/graphs.py:160-169, model/layers.py:336-402) and
+ * reference_torch.moe_ref (:118-134). x bf16 [T, H]; router_w bf16 [E, H]; router_bias fp32 [E] or NULL;
+ * sh_gate, sh_up bf16 [Is, H]; sh_down bf16 [H, Is]; sh_g bf16 [1, H]; workspace of
+ * ssmoe_verify_workspace_bytes() bytes (256-byte aligned); outputs ids int32 [T, K], weights fp32 [T, K],
+ * y bf16 [T, H], routed_out fp32 [T, H] or NULL. */
+int ssmoe_moe_verify_layer(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
+                           const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
+                           const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,
+                           const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes,
+                           int32_t* ids, float* weights, uint16_t* y, float* routed_out, int T, int H, int I, int Is,
+                           int K, int E, void* stream);
+
+/* Bytes of the workspace the acceptance entry points need. */
+int64_t ssmoe_accept_workspace_bytes(int D, int V);
+
+/* Greedy verify acceptance. Replaces the acceptance loop of _mtp_decode (engine/generate.py:208-229) with
+ * Sampler.next at temperature 0 (engine/sampler.py:83-84, np.argmax: first maximum).
+ * target fp32 [D+1, V]; drafts int32 [D]; out int32 [D+5]: n_accept, n_emit, n_uniform (0), flags
+ * (1 = stopped at a non-finite row), tokens[D+1] (emitted tokens, -1 after the last). */
+int ssmoe_accept_greedy(const float* target, const int32_t* drafts, int D, int V, void* workspace,
+                        int64_t workspace_bytes, int32_t* out, void* stream);
+
+/* p/q speculative acceptance (Leviathan et al. 2023, Alg. 1). No reference counterpart: the reference samples
+ * each verify row with Sampler.next and compares (engine/generate.py:208-229); this entry point is the
+ * rejection-sampling verify the BASELINE asks for. target fp32 [D+1, V]; draft fp32 [D, V]; drafts int32 [D];
+ * uniforms fp32 [D+1] in [0, 1) (decision i uses uniforms[i], the final sample the next unused one);
+ * out int32 [D+5] as for ssmoe_accept_greedy (n_uniform = uniforms consumed; flags 1 = non-finite,
+ * 2 = draft token out of range, 4 = empty residual). */
+int ssmoe_accept_pq(const float* target, const float* draft, const int32_t* drafts, const float* uniforms, int D,
+                    int V, float temperature, void* workspace, int64_t workspace_bytes, int32_t* out,
+                    void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SSMOE_H */

@@ -1,0 +1,465 @@
+/* CPU restatement of the bit-exact parts of the MTP-verify MoE path. TEST INFRASTRUCTURE ONLY: the checker that
+ * tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg compare the HIP kernels against; nothing in the
+ * product links or calls it.
+ *
+ * Every function states the reference file:line whose semantics it follows and the fixed operation order it
+ * defines. Compiled with -ffp-contract=off: a*b+c is fused only where the code says fmaf.
+ *
+ * Pinned by (tests/test_oracle.py, tests/test_golden.py):
+ *   or_expf          fp64 exp over a dense sweep (<= 2 ulp), special values, exp(0) = 1.
+ *   or_bf16_*        every one of the 65536 bf16 patterns round-trips; RNE ties against numpy/torch.
+ *   or_dense_rows    fp64 dot + one rounding (agreement away from rounding boundaries); torch F.linear bf16
+ *                    golden fixtures written from reference_torch.moe_ref.
+ *   or_router_topk   ids: brute force stable sort of the probabilities; golden fixtures (moe_ref's torch.topk).
+ *   or_topk_stable   the reference's CPU spec _ref_row (tests/t0/test_topk_stable.py:14-31) with ties, NaN,
+ *                    +-inf, +-0, n_valid.
+ *   or_accept_greedy np.argmax + the accept-while-equal loop, brute force.
+ *   or_accept_pq     distributional check (chi-square: emitted token ~ p) on a small vocabulary, p == q always
+ *                    accepts, q(x) = 0 / p(x) = 0 edge cases, hierarchical sums vs fp64 totals.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------- scalars */
+static float f_from_u(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static uint32_t u_from_f(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+float or_bf16_to_f32(uint16_t b) { return f_from_u((uint32_t)b << 16); }
+
+/* Round to nearest even; NaN -> quiet NaN keeping the sign. */
+uint16_t or_f32_to_bf16(float f) {
+  uint32_t u = u_from_f(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (uint16_t)(((u >> 16) | 0x40u) & 0xFFFFu);
+  u += 0x7FFFu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static float round_bf16(float f) { return or_bf16_to_f32(or_f32_to_bf16(f)); }
+
+/* exp: Cody-Waite reduction with a 15-bit ln2 head, degree-7 Taylor polynomial (Horner, fmaf), 2^n scale. */
+float or_expf(float x) {
+  if (x != x) return x;
+  if (x > 88.72283935546875f) return f_from_u(0x7F800000u);
+  if (x < -103.97208404541015625f) return 0.0f;
+  const float n = rintf(x * 1.44269502162933349609375f);
+  float r = fmaf(-n, 0.693145751953125f, x);
+  r = fmaf(-n, 1.428606765330187045037746429443359375e-06f, r);
+  float p = 1.98412701138295233249664306640625e-04f;
+  p = fmaf(p, r, 1.38888892251998186111450195312500e-03f);
+  p = fmaf(p, r, 8.33333376795053482055664062500000e-03f);
+  p = fmaf(p, r, 4.16666679084300994873046875000000e-02f);
+  p = fmaf(p, r, 1.66666671633720397949218750000000e-01f);
+  p = fmaf(p, r, 0.5f);
+  p = fmaf(p, r, 1.0f);
+  p = fmaf(p, r, 1.0f);
+  int ni = (int)n;
+  if (ni > 127) {
+    p = p * 2.0f;
+    ni -= 1;
+  } else if (ni < -120) {
+    p = p * 5.42101086242752217003726400434970855712890625e-20f;
+    ni += 64;
+  }
+  return p * f_from_u((uint32_t)(ni + 127) << 23);
+}
+
+/* Order-preserving key: kernels/topk_stable.py:1-13 (NaN -> 0, negatives bitwise not, positives sign flip). */
+uint32_t or_key(float f) {
+  const uint32_t u = u_from_f(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0u;
+  return (u & 0x80000000u) ? ~u : (u ^ 0x80000000u);
+}
+
+/* 64-lane xor butterfly: lane l += lane l^32, then ^16 ... ^1; returns lane 0. */
+static float butterfly_sum(const float* v64) {
+  float a[64], b[64];
+  memcpy(a, v64, sizeof a);
+  for (int m = 32; m >= 1; m >>= 1) {
+    for (int l = 0; l < 64; ++l) b[l] = a[l] + a[l ^ m];
+    memcpy(a, b, sizeof a);
+  }
+  return a[0];
+}
+
+/* ---------------------------------------------------------------- dense bf16 rows
+ * out[t, n] = bf16(sum_k x[t, k] w[n, k]) (model/layers.py:62-76, reference_torch.py:121). Order: lane l of 64
+ * accumulates chunks j = 0, 1, ...: elements 512j + 8l .. 512j + 8l + 7 with fmaf from 0; then the butterfly. */
+void or_dense_rows(const uint16_t* x, const uint16_t* w, uint16_t* out, int T, int H, int N) {
+  const int h8 = H / 8, nj = (H + 511) / 512;
+  for (int t = 0; t < T; ++t) {
+    for (int n = 0; n < N; ++n) {
+      float lanes[64];
+      for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int j = 0; j < nj; ++j) {
+          const int k8 = 64 * j + l;
+          if (k8 >= h8) break;
+          for (int e = 0; e < 8; ++e) {
+            const int k = 8 * k8 + e;
+            acc = fmaf(or_bf16_to_f32(x[(size_t)t * H + k]), or_bf16_to_f32(w[(size_t)n * H + k]), acc);
+          }
+        }
+        lanes[l] = acc;
+      }
+      out[(size_t)t * N + n] = or_f32_to_bf16(butterfly_sum(lanes));
+    }
+  }
+}
+
+/* ---------------------------------------------------------------- router tail
+ * model/layers.py:340-347, reference_torch.py:122-124. scores s = bf16 logit (+ bias, one fp32 add);
+ * m = max (NaN ignored); e = exp(s - m); Z: lane l sums e[l], e[l+64], ... sequentially from 0, then the butterfly;
+ * p = e / Z; top-k: K rounds of (largest key, lowest index) among the untaken; w = p / S, S the sequential
+ * rank-order sum of the K probabilities. */
+void or_router_topk(const uint16_t* logits, const float* bias, float* probs, int32_t* ids, float* weights, int T,
+                    int E, int K, float* scratch /* [2E] */) {
+  float* s = scratch;
+  uint8_t* taken = (uint8_t*)(scratch + E);
+  for (int t = 0; t < T; ++t) {
+    float m = -INFINITY;
+    for (int e = 0; e < E; ++e) {
+      float v = or_bf16_to_f32(logits[(size_t)t * E + e]);
+      if (bias) v = v + bias[e];
+      s[e] = v;
+      m = fmaxf(m, v);
+      taken[e] = 0;
+    }
+    float lanes[64];
+    for (int l = 0; l < 64; ++l) lanes[l] = 0.0f;
+    for (int e = 0; e < E; ++e) {
+      const float v = or_expf(s[e] - m);
+      s[e] = v;
+      lanes[e % 64] = lanes[e % 64] + v;
+    }
+    const float z = butterfly_sum(lanes);
+    for (int e = 0; e < E; ++e) {
+      s[e] = s[e] / z;
+      if (probs) probs[(size_t)t * E + e] = s[e];
+    }
+    float tv[64];
+    for (int r = 0; r < K; ++r) {
+      uint32_t bk = 0;
+      int bi = 0x7FFFFFFF;
+      for (int e = 0; e < E; ++e) {
+        if (taken[e]) continue;
+        const uint32_t k = or_key(s[e]);
+        if (k > bk || (k == bk && e < bi)) {
+          bk = k;
+          bi = e;
+        }
+      }
+      taken[bi] = 1;
+      ids[(size_t)t * K + r] = bi;
+      tv[r] = s[bi];
+    }
+    float S = 0.0f;
+    for (int r = 0; r < K; ++r) S = S + tv[r];
+    for (int r = 0; r < K; ++r) weights[(size_t)t * K + r] = tv[r] / S;
+  }
+}
+
+/* ---------------------------------------------------------------- topk_stable
+ * kernels/topk_stable.py:85-113 with the CPU spec of tests/t0/test_topk_stable.py:14-31: stable order by
+ * (key desc, index asc) over the first n_valid entries; k <= 16 keeps that order, larger k re-sorts the selected
+ * indices ascending; missing entries are -1 / -inf. O(N * k) selection, fine for test sizes. */
+void or_topk_stable(const float* scores, const int32_t* n_valid, int32_t* idx, float* val, int R, int N, int k,
+                    uint8_t* taken /* [N] */) {
+  for (int r = 0; r < R; ++r) {
+    const float* x = scores + (size_t)r * N;
+    int nv = N;
+    if (n_valid) nv = n_valid[r] < 0 ? 0 : (n_valid[r] > N ? N : n_valid[r]);
+    const int want = k < nv ? k : nv;
+    memset(taken, 0, (size_t)N);
+    int32_t* oi = idx + (size_t)r * k;
+    for (int a = 0; a < want; ++a) {
+      uint32_t bk = 0;
+      int bi = -1;
+      for (int i = 0; i < nv; ++i) {
+        if (taken[i]) continue;
+        const uint32_t kk = or_key(x[i]);
+        if (bi < 0 || kk > bk) {
+          bk = kk;
+          bi = i;
+        }
+      }
+      taken[bi] = 1;
+      oi[a] = bi;
+    }
+    if (k > 16) { /* by index ascending */
+      int p = 0;
+      for (int i = 0; i < nv; ++i)
+        if (taken[i]) oi[p++] = i;
+    }
+    for (int a = 0; a < want; ++a)
+      if (val) val[(size_t)r * k + a] = x[oi[a]];
+    for (int a = want; a < k; ++a) {
+      oi[a] = -1;
+      if (val) val[(size_t)r * k + a] = -INFINITY;
+    }
+  }
+}
+
+/* ---------------------------------------------------------------- acceptance */
+#define SUB 16
+#define CHUNK 1024
+
+static int is_finite_f(float v) { return (u_from_f(v) & 0x7F800000u) != 0x7F800000u; }
+
+/* Greedy: engine/generate.py:208-229, engine/sampler.py:83-84 (np.argmax: first maximum). out as ssmoe.h. */
+void or_accept_greedy(const float* target, const int32_t* drafts, int D, int V, int32_t* out) {
+  int good = 0, emit = 0, flags = 0;
+  for (int i = 0; i <= D; ++i) {
+    const float* x = target + (size_t)i * V;
+    int bad = 0, bi = 0;
+    float best = -INFINITY;
+    int have = 0;
+    for (int j = 0; j < V; ++j) {
+      if (!is_finite_f(x[j])) bad = 1;
+      if (!have || x[j] > best) {
+        if (x[j] == x[j]) {
+          best = x[j];
+          bi = j;
+          have = 1;
+        }
+      }
+    }
+    if (bad) {
+      flags |= 1;
+      break;
+    }
+    out[4 + emit++] = bi;
+    if (i < D && bi == drafts[i]) {
+      ++good;
+      continue;
+    }
+    break;
+  }
+  for (int i = emit; i <= D; ++i) out[4 + i] = -1;
+  out[0] = good;
+  out[1] = emit;
+  out[2] = 0;
+  out[3] = flags;
+}
+
+typedef struct {
+  const float* row;
+  float m, z;
+} PRow;
+
+static float row_max_div(const float* x, int V, float temp) {
+  float m = -INFINITY;
+  for (int j = 0; j < V; ++j) m = fmaxf(m, x[j] / temp);
+  return m;
+}
+
+static int row_bad(const float* x, int V) {
+  for (int j = 0; j < V; ++j)
+    if (!is_finite_f(x[j])) return 1;
+  return 0;
+}
+
+/* Hierarchical sum of f(j): sub-chunk totals (sequential from 0), chunk totals (butterfly), row (sequential). */
+typedef float (*ValFn)(const void* ctx, int j);
+
+static float chunk_total(ValFn f, const void* ctx, int c, int V, float* sub /* [64] or NULL */) {
+  float lanes[64];
+  for (int b = 0; b < 64; ++b) {
+    float s = 0.0f;
+    for (int i = 0; i < SUB; ++i) {
+      const int j = c * CHUNK + b * SUB + i;
+      if (j < V) s = s + f(ctx, j);
+    }
+    lanes[b] = s;
+    if (sub) sub[b] = s;
+  }
+  return butterfly_sum(lanes);
+}
+
+typedef struct {
+  const float* x;
+  float temp, m;
+} ExpCtx;
+
+static float val_exp(const void* c, int j) {
+  const ExpCtx* e = (const ExpCtx*)c;
+  return or_expf(e->x[j] / e->temp - e->m);
+}
+
+typedef struct {
+  const float* p;
+  const float* q; /* NULL: plain p */
+  float temp, mp, zp, mq, zq;
+} SampCtx;
+
+static float val_sample(const void* c, int j) {
+  const SampCtx* s = (const SampCtx*)c;
+  const float p = or_expf(s->p[j] / s->temp - s->mp) / s->zp;
+  if (!s->q) return p;
+  const float q = or_expf(s->q[j] / s->temp - s->mq) / s->zq;
+  const float d = p - q;
+  return d > 0.0f ? d : 0.0f;
+}
+
+static float row_z(const float* x, int V, float temp, float m) {
+  ExpCtx c = {x, temp, m};
+  const int nch = (V + CHUNK - 1) / CHUNK;
+  float z = 0.0f;
+  for (int k = 0; k < nch; ++k) z = z + chunk_total(val_exp, &c, k, V, NULL);
+  return z;
+}
+
+/* p/q acceptance, Leviathan et al. 2023 Alg. 1 (no reference counterpart). out as ssmoe.h; work: >= nch*65 floats. */
+void or_accept_pq(const float* target, const float* draft, const int32_t* drafts, const float* uniforms, int D,
+                  int V, float temp, int32_t* out, float* work) {
+  const int nch = (V + CHUNK - 1) / CHUNK;
+  int good = 0, flags = 0, stop = 0, srow = D, sdraft = -1;
+  for (int i = 0; i < D; ++i) {
+    const float* t = target + (size_t)i * V;
+    const float* d = draft + (size_t)i * V;
+    if (row_bad(t, V) || row_bad(d, V)) {
+      flags |= 1;
+      stop = 1;
+      break;
+    }
+    const int x = drafts[i];
+    if (x < 0 || x >= V) {
+      flags |= 2;
+      srow = i;
+      sdraft = i;
+      break;
+    }
+    const float mp = row_max_div(t, V, temp), mq = row_max_div(d, V, temp);
+    const float zp = row_z(t, V, temp, mp), zq = row_z(d, V, temp, mq);
+    const float p = or_expf(t[x] / temp - mp) / zp;
+    const float q = or_expf(d[x] / temp - mq) / zq;
+    if (uniforms[i] * q < p) {
+      ++good;
+      continue;
+    }
+    srow = i;
+    sdraft = i;
+    break;
+  }
+  if (!stop && sdraft < 0 && row_bad(target + (size_t)D * V, V)) {
+    flags |= 1;
+    stop = 1;
+  }
+  const int uidx = good + (sdraft >= 0 ? 1 : 0);
+  for (int i = 0; i < good; ++i) out[4 + i] = drafts[i];
+  int emit = good;
+  if (!stop) {
+    SampCtx sc;
+    sc.p = target + (size_t)srow * V;
+    sc.q = sdraft >= 0 ? draft + (size_t)sdraft * V : NULL;
+    sc.temp = temp;
+    sc.mp = row_max_div(sc.p, V, temp);
+    sc.zp = row_z(sc.p, V, temp, sc.mp);
+    sc.mq = sc.q ? row_max_div(sc.q, V, temp) : 0.0f;
+    sc.zq = sc.q ? row_z(sc.q, V, temp, sc.mq) : 0.0f;
+    float* stot = work;            /* [nch][64] */
+    float* rtot = work + nch * 64; /* [nch] */
+    for (int c = 0; c < nch; ++c) rtot[c] = chunk_total(val_sample, &sc, c, V, stot + c * 64);
+    float S = 0.0f;
+    for (int c = 0; c < nch; ++c) S = S + rtot[c];
+    if (!(S > 0.0f)) flags |= 4;
+    const float target_u = uniforms[uidx] * S;
+    int cs = -1, clast = -1;
+    float base = 0.0f, run = 0.0f;
+    for (int c = 0; c < nch; ++c) {
+      const float nx = run + rtot[c];
+      if (rtot[c] > 0.0f) clast = c;
+      if (cs < 0 && nx > target_u) {
+        cs = c;
+        base = run;
+      }
+      run = nx;
+    }
+    if (cs < 0) {
+      cs = clast < 0 ? 0 : clast;
+      base = 0.0f;
+      for (int c = 0; c < cs; ++c) base = base + rtot[c];
+    }
+    int bs = -1, blast = -1;
+    float sbase = base;
+    run = base;
+    for (int b = 0; b < 64; ++b) {
+      const float t = stot[cs * 64 + b];
+      const float nx = run + t;
+      if (t > 0.0f) blast = b;
+      if (bs < 0 && nx > target_u) {
+        bs = b;
+        sbase = run;
+      }
+      run = nx;
+    }
+    if (bs < 0) {
+      bs = blast < 0 ? 0 : blast;
+      sbase = base;
+      for (int b = 0; b < bs; ++b) sbase = sbase + stot[cs * 64 + b];
+    }
+    int pick = -1, last = -1;
+    run = sbase;
+    for (int i = 0; i < SUB; ++i) {
+      const int j = cs * CHUNK + bs * SUB + i;
+      if (j >= V) break;
+      const float v = val_sample(&sc, j);
+      if (v > 0.0f) last = j;
+      run = run + v;
+      if (run > target_u) {
+        pick = j;
+        break;
+      }
+    }
+    if (pick < 0) {
+      const int first = cs * CHUNK + bs * SUB;
+      pick = last >= 0 ? last : (first < V - 1 ? first : V - 1);
+    }
+    out[4 + emit++] = pick;
+  }
+  for (int i = emit; i <= D; ++i) out[4 + i] = -1;
+  out[0] = good;
+  out[1] = emit;
+  out[2] = stop ? uidx : uidx + 1;
+  out[3] = flags;
+}
+
+/* Hierarchical total of exp(x/T - m) for one row (exposed for the sum-order tests). */
+float or_row_z(const float* x, int V, float temp) { return row_z(x, V, temp, row_max_div(x, V, temp)); }
+
+/* ---------------------------------------------------------------- shared expert (bf16 chain)
+ * reference_torch.py:132-133 / model/layers.py:398-402 in bf16: g, u = bf16 projections (or_dense_rows);
+ * hs = bf16(bf16(silu(g)) * u); sh = or_dense_rows(hs, Wd); gate = bf16(sigmoid(bf16 projection));
+ * sh2 = bf16(gate * sh). silu(v) = v / (1 + exp(-v)); sigmoid(v) = 1 / (1 + exp(-v)). */
+void or_shared_hs(const uint16_t* g, const uint16_t* u, uint16_t* hs, int n) {
+  for (int i = 0; i < n; ++i) {
+    const float gv = or_bf16_to_f32(g[i]), uv = or_bf16_to_f32(u[i]);
+    const float sv = round_bf16(gv / (1.0f + or_expf(-gv)));
+    hs[i] = or_f32_to_bf16(sv * uv);
+  }
+}
+
+/* y = bf16(bf16(routed) + bf16(bf16(sigmoid(sgl)) * sh)), all [T, H] except sgl [T]. */
+void or_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* sgl, uint16_t* y, int T, int H) {
+  for (int t = 0; t < T; ++t) {
+    const float s = or_bf16_to_f32(sgl[t]);
+    const float sg = round_bf16(1.0f / (1.0f + or_expf(-s)));
+    for (int n = 0; n < H; ++n) {
+      const float sh2 = round_bf16(sg * or_bf16_to_f32(sh[(size_t)t * H + n]));
+      y[(size_t)t * H + n] = or_f32_to_bf16(round_bf16(routed[(size_t)t * H + n]) + sh2);
+    }
+  }
+}
+
+/* Elementwise or_expf over an array (test helper). */
+void or_expf_vec(const float* x, float* y, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) y[i] = or_expf(x[i]);
+}

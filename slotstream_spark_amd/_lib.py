@@ -1,0 +1,91 @@
+"""ctypes binding of libssmoe.so (the C ABI declared in include/ssmoe.h).
+
+The library is built in-tree by slotstream_spark_amd.build. There is no fallback: a missing or stale library raises
+at the first call, so nothing can silently run another code path.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libssmoe.so"
+ABI_VERSION = 1
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+
+# name -> (restype, argtypes); the exact export list of include/ssmoe.h.
+SIGNATURES = {
+    "ssmoe_last_error": (ctypes.c_char_p, []),
+    "ssmoe_version": (_I, []),
+    "ssmoe_device_error": (_I, [_P, _I]),
+    "ssmoe_set_trace": (_I, [_P, _I64]),
+    "ssmoe_record_layout": (_I, [_I, _I, _P]),
+    "ssmoe_moe_decode": (_I, [_P, _I, _P, _P, _I, _P, _I64, _P, _I64, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
+    "ssmoe_topk_stable": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
+    "ssmoe_dense_gemv_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "ssmoe_router": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "ssmoe_verify_workspace_bytes": (_I64, [_I, _I, _I, _I, _I, _I]),
+    "ssmoe_moe_verify_layer": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _P, _I64, _P, _I64,
+                                    _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "ssmoe_accept_workspace_bytes": (_I64, [_I, _I]),
+    "ssmoe_accept_greedy": (_I, [_P, _P, _I, _I, _P, _I64, _P, _P]),
+    "ssmoe_accept_pq": (_I, [_P, _P, _P, _P, _I, _I, _F, _P, _I64, _P, _P]),
+}
+
+_lib = None
+
+
+class SsmoeError(RuntimeError):
+    pass
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library (raises when it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(f"{LIB_PATH} is missing: build it with `python -m slotstream_spark_amd.build`")
+        L = ctypes.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        if L.ssmoe_version() != ABI_VERSION:
+            raise RuntimeError(f"{LIB_PATH} has ABI {L.ssmoe_version()}, expected {ABI_VERSION}: rebuild it")
+        _lib = L
+    return _lib
+
+
+def check(rc: int) -> None:
+    if rc != 0:
+        msg = lib().ssmoe_last_error().decode(errors="replace")
+        raise SsmoeError(f"ssmoe status {rc}: {msg}")
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a tensor, None for None."""
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(t) -> int:
+    """The current torch stream on the tensor's device, as a hipStream_t handle."""
+    import torch
+
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def device_error(clear: bool = True) -> int:
+    """Status bits raised by kernels on the current device since the last clear (synchronises)."""
+    flags = ctypes.c_int(0)
+    check(lib().ssmoe_device_error(ctypes.byref(flags), 1 if clear else 0))
+    return flags.value
+
+
+def record_layout(H: int, I: int) -> tuple[list[int], int]:
+    """(nine piece offsets, record bytes) of an affine-4bit expert record for hidden H and intermediate I."""
+    off = (ctypes.c_int64 * 10)()
+    check(lib().ssmoe_record_layout(H, I, off))
+    return list(off[:9]), int(off[9])

@@ -1,0 +1,384 @@
+// Acceptance of one MTP verify round over the vocabulary.
+//
+// Greedy (engine/generate.py:208-229 with engine/sampler.py:83-84): t_i = argmax(target[i]) (first maximum);
+// the round accepts drafts while t_i == draft_i and emits t_0 .. t_good. A row with a non-finite logit stops
+// the round before it (generate.py:210-212).
+//
+// p/q (Leviathan et al. 2023, Alg. 1; not in the reference): p_i = softmax(target_i / T), q_i = softmax(draft_i / T);
+// draft x_i is accepted iff u_i * q_i(x_i) < p_i(x_i). The first rejection samples from norm(max(0, p_i - q_i))
+// with the next uniform; when every draft is accepted a bonus token is sampled from p_D.
+//
+// Every reduction has a fixed order, which the CPU restatement replays bit for bit:
+//   chunk = 1024 entries = 64 sub-chunks of 16; a sub-chunk total is the sequential fp32 sum of its entries
+//   (from 0); a chunk total is the xor-butterfly sum of its 64 sub-chunk totals; a row total is the sequential
+//   sum of the chunk totals. Inverse-CDF search: the first chunk whose running total exceeds u*S, then inside
+//   it the first sub-chunk (running total started at the chunk's base), then the first entry.
+#include "ss_common.hpp"
+#include "ss_launch.hpp"
+
+namespace ss {
+
+constexpr int kSub = 16;
+constexpr int kChunk = 64 * kSub;
+
+// Output header: out[0] n_accept, out[1] n_emit, out[2] uniforms used, out[3] flags, out[4..] tokens.
+enum { OUT_NACC = 0, OUT_NEMIT = 1, OUT_NUNI = 2, OUT_FLAGS = 3, OUT_TOK = 4 };
+enum { FLAG_NONFINITE = 1, FLAG_BAD_DRAFT = 2, FLAG_RESIDUAL_EMPTY = 4 };
+
+SS_DEV int nchunks_of(int V) { return (V + kChunk - 1) / kChunk; }
+
+int64_t accept_work_floats(int D, int V) {
+  const int nch = (V + kChunk - 1) / kChunk;
+  const int rows = 2 * D + 1;
+  return (int64_t)rows * nch * 3 + (int64_t)nch * 65 + 64;
+}
+
+// Workspace layout (floats).
+struct Work {
+  float* cmax;   // [rows][nch]
+  float* cbad;   // [rows][nch]
+  float* ctot;   // [rows][nch]
+  float* stot;   // [nch][64]  sub-chunk totals of the sampled row
+  float* rtot;   // [nch]      chunk totals of the sampled row
+  float* state;  // [64]
+};
+
+SS_DEV Work work_of(float* w, int rows, int nch) {
+  Work k;
+  k.cmax = w;
+  k.cbad = w + (size_t)rows * nch;
+  k.ctot = w + (size_t)rows * nch * 2;
+  k.stot = w + (size_t)rows * nch * 3;
+  k.rtot = k.stot + (size_t)nch * 64;
+  k.state = k.rtot + nch;
+  return k;
+}
+
+SS_DEV bool finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
+
+// ---------------------------------------------------------------- greedy
+__global__ __launch_bounds__(64) void greedy_chunk_kernel(const float* __restrict__ target, int V, float* work) {
+  const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
+  const int nch = gridDim.x, rows = gridDim.y;
+  Work k = work_of(work, rows, nch);
+  const float* x = target + (size_t)row * V;
+  float best = -__builtin_inff();
+  int bi = 0x7FFFFFFF;
+  int bad = 0;
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + i * 64 + lane;
+    if (j >= V) break;
+    const float v = x[j];
+    bad |= !finite(v);
+    if (v > best || (v == best && j < bi)) {
+      best = v;
+      bi = j;
+    }
+  }
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = ss_shfl_xor(best, m);
+    const int oi = ss_shfl_xor_i(bi, m);
+    if (ov > best || (ov == best && oi < bi)) {
+      best = ov;
+      bi = oi;
+    }
+    bad |= ss_shfl_xor_i(bad, m);
+  }
+  if (lane == 0) {
+    k.cmax[row * nch + c] = best;
+    k.ctot[row * nch + c] = __int_as_float(bi);
+    k.cbad[row * nch + c] = bad ? 1.f : 0.f;
+  }
+}
+
+__global__ __launch_bounds__(64) void greedy_finish_kernel(const int32_t* __restrict__ drafts, int D, int nch,
+                                                           float* work, int32_t* out) {
+  const int lane = threadIdx.x;
+  Work k = work_of(work, D + 1, nch);
+  __shared__ int tok[64];
+  __shared__ int bad[64];
+  for (int row = lane; row <= D; row += 64) {
+    float best = -__builtin_inff();
+    int bi = 0x7FFFFFFF, b = 0;
+    for (int c = 0; c < nch; ++c) {
+      const float v = k.cmax[row * nch + c];
+      const int i = __float_as_int(k.ctot[row * nch + c]);
+      b |= k.cbad[row * nch + c] != 0.f;
+      if (v > best || (v == best && i < bi)) {
+        best = v;
+        bi = i;
+      }
+    }
+    tok[row] = bi;
+    bad[row] = b;
+  }
+  __syncthreads();
+  if (lane == 0) {
+    int good = 0, emit = 0, flags = 0;
+    for (int i = 0; i <= D; ++i) {
+      if (bad[i]) {
+        flags |= FLAG_NONFINITE;
+        break;
+      }
+      out[OUT_TOK + emit++] = tok[i];
+      if (i < D && tok[i] == drafts[i]) {
+        ++good;
+        continue;
+      }
+      break;
+    }
+    for (int i = emit; i <= D; ++i) out[OUT_TOK + i] = -1;
+    out[OUT_NACC] = good;
+    out[OUT_NEMIT] = emit;
+    out[OUT_NUNI] = 0;
+    out[OUT_FLAGS] = flags;
+  }
+}
+
+hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st) {
+  const int nch = (a.V + kChunk - 1) / kChunk;
+  hipLaunchKernelGGL(greedy_chunk_kernel, dim3(nch, a.D + 1), dim3(64), 0, st, a.target, a.V, a.work);
+  hipLaunchKernelGGL(greedy_finish_kernel, dim3(1), dim3(64), 0, st, a.drafts, a.D, nch, a.work, a.out);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- p/q
+// Logical rows: target i -> i (0..D), draft i -> D + 1 + i.
+SS_DEV const float* row_ptr(const AcceptArgs& a, int row) {
+  return row <= a.D ? a.target + (size_t)row * a.V : a.draft + (size_t)(row - a.D - 1) * a.V;
+}
+
+__global__ __launch_bounds__(64) void pq_max_kernel(AcceptArgs a) {
+  const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
+  const int nch = gridDim.x, rows = gridDim.y;
+  Work k = work_of(a.work, rows, nch);
+  const float* x = row_ptr(a, row);
+  float m = -__builtin_inff();
+  int bad = 0;
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + i * 64 + lane;
+    if (j >= a.V) break;
+    const float v = x[j];
+    bad |= !finite(v);
+    m = fmaxf(m, v / a.temperature);
+  }
+  m = ss_wave_max(m);
+#pragma unroll
+  for (int s = 32; s >= 1; s >>= 1) bad |= ss_shfl_xor_i(bad, s);
+  if (lane == 0) {
+    k.cmax[row * nch + c] = m;
+    k.cbad[row * nch + c] = bad ? 1.f : 0.f;
+  }
+}
+
+SS_DEV float row_max(const Work& k, int row, int nch) {
+  float m = -__builtin_inff();
+  for (int c = 0; c < nch; ++c) m = fmaxf(m, k.cmax[row * nch + c]);
+  return m;
+}
+
+// Stage one chunk of a row (as e = exp(l/T - m)) into LDS with a 65-float stride per sub-chunk.
+SS_DEV void stage_exp(const AcceptArgs& a, int row, int c, float m, float* lds) {
+  const float* x = row_ptr(a, row);
+  const int lane = threadIdx.x;
+  for (int i = 0; i < kSub; ++i) {
+    const int e = i * 64 + lane;
+    const int j = c * kChunk + e;
+    float v = 0.f;
+    if (j < a.V) v = ss_expf(x[j] / a.temperature - m);
+    lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = v;
+  }
+}
+
+__global__ __launch_bounds__(64) void pq_sum_kernel(AcceptArgs a) {
+  __shared__ float lds[64 * (kSub + 1)];
+  const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
+  const int nch = gridDim.x, rows = gridDim.y;
+  Work k = work_of(a.work, rows, nch);
+  const float m = row_max(k, row, nch);
+  stage_exp(a, row, c, m, lds);
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
+  s = ss_wave_sum(s);
+  if (lane == 0) k.ctot[row * nch + c] = s;
+}
+
+// state: [0] sample target row, [1] sample draft row (-1 = plain p), [2] uniform index, [3] stop (no sample),
+//        [4..] per-row Z and m for the two sampled rows.
+__global__ __launch_bounds__(64) void pq_decide_kernel(AcceptArgs a, int nch) {
+  const int rows = 2 * a.D + 1;
+  Work k = work_of(a.work, rows, nch);
+  if (threadIdx.x != 0) return;
+  int good = 0, flags = 0, stop = 0;
+  int srow = a.D, sdraft = -1;
+  for (int i = 0; i < a.D; ++i) {
+    const int dr = a.D + 1 + i;
+    int badrow = 0;
+    for (int c = 0; c < nch; ++c) badrow |= (k.cbad[i * nch + c] != 0.f) | (k.cbad[dr * nch + c] != 0.f);
+    if (badrow) {
+      flags |= FLAG_NONFINITE;
+      stop = 1;
+      break;
+    }
+    const int x = a.drafts[i];
+    if (x < 0 || x >= a.V) {
+      flags |= FLAG_BAD_DRAFT;
+      ss_raise(a.err, SS_ERR_TOKEN);
+      srow = i;
+      sdraft = dr;
+      break;
+    }
+    float zp = 0.f, zq = 0.f;
+    for (int c = 0; c < nch; ++c) zp = zp + k.ctot[i * nch + c];
+    for (int c = 0; c < nch; ++c) zq = zq + k.ctot[dr * nch + c];
+    const float mp = row_max(k, i, nch), mq = row_max(k, dr, nch);
+    const float p = ss_expf(a.target[(size_t)i * a.V + x] / a.temperature - mp) / zp;
+    const float q = ss_expf(a.draft[(size_t)i * a.V + x] / a.temperature - mq) / zq;
+    if (a.uniforms[i] * q < p) {
+      ++good;
+      continue;
+    }
+    srow = i;
+    sdraft = dr;
+    break;
+  }
+  if (!stop && sdraft < 0) {
+    int badrow = 0;
+    for (int c = 0; c < nch; ++c) badrow |= k.cbad[a.D * nch + c] != 0.f;
+    if (badrow) {
+      flags |= FLAG_NONFINITE;
+      stop = 1;
+    }
+  }
+  k.state[0] = __int_as_float(srow);
+  k.state[1] = __int_as_float(sdraft);
+  k.state[2] = __int_as_float(good + (sdraft >= 0 ? 1 : 0));
+  k.state[3] = __int_as_float(stop);
+  k.state[4] = __int_as_float(good);
+  k.state[5] = __int_as_float(flags);
+  float zp = 0.f, zq = 0.f;
+  for (int c = 0; c < nch; ++c) zp = zp + k.ctot[srow * nch + c];
+  if (sdraft >= 0)
+    for (int c = 0; c < nch; ++c) zq = zq + k.ctot[sdraft * nch + c];
+  k.state[6] = zp;
+  k.state[7] = zq;
+  k.state[8] = row_max(k, srow, nch);
+  k.state[9] = sdraft >= 0 ? row_max(k, sdraft, nch) : 0.f;
+}
+
+// Value of entry j of the sampled distribution: p_j, or max(0, p_j - q_j) after a rejection.
+SS_DEV float sample_value(const AcceptArgs& a, const float* st, int j) {
+  const int srow = __float_as_int(st[0]), sdraft = __float_as_int(st[1]);
+  const float p = ss_expf(a.target[(size_t)srow * a.V + j] / a.temperature - st[8]) / st[6];
+  if (sdraft < 0) return p;
+  const float q = ss_expf(a.draft[(size_t)(sdraft - a.D - 1) * a.V + j] / a.temperature - st[9]) / st[7];
+  const float d = p - q;
+  return d > 0.f ? d : 0.f;
+}
+
+__global__ __launch_bounds__(64) void pq_residual_kernel(AcceptArgs a) {
+  __shared__ float lds[64 * (kSub + 1)];
+  const int c = blockIdx.x, lane = threadIdx.x, nch = gridDim.x;
+  Work k = work_of(a.work, 2 * a.D + 1, nch);
+  if (__float_as_int(k.state[3])) return;
+  for (int i = 0; i < kSub; ++i) {
+    const int e = i * 64 + lane;
+    const int j = c * kChunk + e;
+    lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? sample_value(a, k.state, j) : 0.f;
+  }
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
+  k.stot[c * 64 + lane] = s;
+  s = ss_wave_sum(s);
+  if (lane == 0) k.rtot[c] = s;
+}
+
+__global__ __launch_bounds__(64) void pq_search_kernel(AcceptArgs a, int nch) {
+  Work k = work_of(a.work, 2 * a.D + 1, nch);
+  if (threadIdx.x != 0) return;
+  const int good = __float_as_int(k.state[4]);
+  int flags = __float_as_int(k.state[5]);
+  const int stop = __float_as_int(k.state[3]);
+  const int uidx = __float_as_int(k.state[2]);
+  for (int i = 0; i < good; ++i) a.out[OUT_TOK + i] = a.drafts[i];
+  int emit = good;
+  if (!stop) {
+    float S = 0.f;
+    for (int c = 0; c < nch; ++c) S = S + k.rtot[c];
+    if (!(S > 0.f)) flags |= FLAG_RESIDUAL_EMPTY;
+    const float target = a.uniforms[uidx] * S;
+    // chunk
+    int cs = -1, clast = -1;
+    float base = 0.f, run = 0.f;
+    for (int c = 0; c < nch; ++c) {
+      const float nx = run + k.rtot[c];
+      if (k.rtot[c] > 0.f) clast = c;
+      if (cs < 0 && nx > target) {
+        cs = c;
+        base = run;
+      }
+      run = nx;
+    }
+    if (cs < 0) {
+      cs = clast < 0 ? 0 : clast;
+      base = 0.f;
+      for (int c = 0; c < cs; ++c) base = base + k.rtot[c];
+    }
+    // sub-chunk
+    int bs = -1, blast = -1;
+    float sbase = base;
+    run = base;
+    for (int b = 0; b < 64; ++b) {
+      const float t = k.stot[cs * 64 + b];
+      const float nx = run + t;
+      if (t > 0.f) blast = b;
+      if (bs < 0 && nx > target) {
+        bs = b;
+        sbase = run;
+      }
+      run = nx;
+    }
+    if (bs < 0) {
+      bs = blast < 0 ? 0 : blast;
+      sbase = base;
+      for (int b = 0; b < bs; ++b) sbase = sbase + k.stot[cs * 64 + b];
+    }
+    // entry
+    int pick = -1, last = -1;
+    run = sbase;
+    for (int i = 0; i < kSub; ++i) {
+      const int j = cs * kChunk + bs * kSub + i;
+      if (j >= a.V) break;
+      const float v = sample_value(a, k.state, j);
+      if (v > 0.f) last = j;
+      run = run + v;
+      if (run > target) {
+        pick = j;
+        break;
+      }
+    }
+    if (pick < 0) pick = last >= 0 ? last : min(cs * kChunk + bs * kSub, a.V - 1);
+    a.out[OUT_TOK + emit++] = pick;
+  }
+  for (int i = emit; i <= a.D; ++i) a.out[OUT_TOK + i] = -1;
+  a.out[OUT_NACC] = good;
+  a.out[OUT_NEMIT] = emit;
+  a.out[OUT_NUNI] = stop ? uidx : uidx + 1;
+  a.out[OUT_FLAGS] = flags;
+}
+
+hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st) {
+  const int nch = (a.V + kChunk - 1) / kChunk;
+  const int rows = 2 * a.D + 1;
+  hipLaunchKernelGGL(pq_max_kernel, dim3(nch, rows), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(pq_sum_kernel, dim3(nch, rows), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(pq_decide_kernel, dim3(1), dim3(64), 0, st, a, nch);
+  hipLaunchKernelGGL(pq_residual_kernel, dim3(nch), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(pq_search_kernel, dim3(1), dim3(64), 0, st, a, nch);
+  return hipGetLastError();
+}
+
+}  // namespace ss

@@ -1,0 +1,79 @@
+// Host-side launchers implemented by the kernel translation units and called by the C ABI (ssmoe_capi.hip).
+// Every launcher validates nothing: shapes were checked by the caller; each returns hipGetLastError().
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ss {
+
+// One dense bf16 row segment for launch_dense_rows: rows [0, n) of w (bf16 [n, H], row-major) against
+// every token; the fp32 dot is rounded once to bf16 and stored at out[t * out_ld + row].
+struct DenseSeg {
+  const uint16_t* w;
+  uint16_t* out;
+  int n;
+  int out_ld;
+};
+
+// Dot products in the defined order (lane l, chunk j: elements 512j + 8l .. +8, fmaf, then the xor butterfly).
+hipError_t launch_dense_rows(const uint16_t* x, int T, int H, const DenseSeg* segs, int nseg, hipStream_t st);
+
+// Router tail for T tokens: scores = bf16 logits (+ bias), fp32 softmax, top-k (ties -> lower index,
+// sorted by value desc), renormalised weights. probs may be null.
+hipError_t launch_router_topk(const uint16_t* logits, const float* bias, float* probs, int32_t* ids, float* weights,
+                              int T, int E, int K, hipStream_t st);
+
+// topk_stable over fp32 rows (kernels/topk_stable.py:85-113 semantics).
+hipError_t launch_topk_stable(const float* scores, const int32_t* n_valid, int32_t* idx, float* val, int R, int N,
+                              int k, hipStream_t st);
+
+// One persistent launch per block of <= 4 tokens: (verify mode) router + shared expert + routed experts +
+// combine, or (decode mode) the routed experts of given ids. See ss_verify.hip.
+struct VerifyArgs {
+  int mode;                 // 0 = verify layer (router on device, shared expert, y); 1 = moe_decode (ids given)
+  const void* x;            // [T, H] bf16, or fp32 when x_f32 (decode mode only)
+  int x_f32;
+  const uint16_t* router_w; // [E, H]
+  const float* bias;        // [E] or null
+  const uint16_t* sh_gate;  // [Is, H]
+  const uint16_t* sh_up;    // [Is, H]
+  const uint16_t* sh_down;  // [H, Is]
+  const uint16_t* sh_g;     // [1, H]
+  const int32_t* map;
+  int64_t map_len;
+  const int64_t* slot_ptr;
+  int64_t n_slots;
+  int64_t map_base;         // layer * E
+  const int32_t* ids_in;    // decode mode: [T, K]
+  const float* w_in;        // decode mode: [T, K]
+  int32_t* ids_out;         // verify mode: [T, K]
+  float* w_out;             // verify mode: [T, K]
+  uint16_t* y;              // verify mode: [T, H]
+  float* out;               // [T, H] routed rank-order sum (decode: required; verify: optional)
+  float* h_buf;             // [T, K, I] fp32 or null
+  float* o_buf;             // [T, K, H] fp32 or null
+  void* scratch;            // verify_scratch_bytes(), counters zero on entry (the kernel leaves them zero)
+  int T, H, I, Is, K, E;
+  int* err;
+  uint64_t* trace;          // null, or [grid][16] phase timestamps (s_memrealtime, 100 MHz)
+};
+size_t verify_scratch_bytes(int T, int H, int I, int Is, int K, int E);
+hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
+
+// Acceptance.
+struct AcceptArgs {
+  const float* target;   // [D+1, V]
+  const float* draft;    // [D, V] (p/q only)
+  const int32_t* drafts; // [D]
+  const float* uniforms; // [D+1] (p/q only)
+  int D, V;
+  float temperature;
+  int32_t* out;          // [D + 5]: n_accept, n_emit, n_uniform, flags, tokens[D+1]
+  float* work;           // workspace floats
+  int* err;
+};
+int64_t accept_work_floats(int D, int V);
+hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st);
+hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st);
+
+}  // namespace ss

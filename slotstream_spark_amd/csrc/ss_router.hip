@@ -1,0 +1,327 @@
+// Router of the MoE layer and the stable top-k.
+//
+//  * dense_rows_kernel: bf16 GEMV rows (router gate, shared-expert gate/up, shared_expert_gate) with a fixed fp32
+//    operation order, so the CPU restatement reproduces every bit (model/layers.py:339, :62-76;
+//    reference_torch.py:121, :132-133).
+//  * router_topk_kernel: fp32 softmax of the bf16 logits (+ optional routing bias), top-k with ties to the lower
+//    index, renormalisation in rank order (model/layers.py:340-347; reference_torch.py:122-124).
+//  * topk_stable_kernel: kernels/topk_stable.py:29-113 (order-preserving keys, NaN lowest, k <= 16 sorted by
+//    (value desc, index asc), larger k by index, rows shorter than k padded with -1 / -inf).
+#include "ss_common.hpp"
+#include "ss_launch.hpp"
+
+namespace ss {
+
+constexpr int kDenseTB = 4;  // tokens staged per pass
+
+struct SegPack {
+  DenseSeg s[4];
+  int nseg;
+};
+
+__global__ __launch_bounds__(256) void dense_rows_kernel(const uint16_t* __restrict__ x, int T, int H, SegPack segs,
+                                                         int total_rows) {
+  extern __shared__ uint4 xs[];  // [kDenseTB][H / 8]
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+  const int h8 = H >> 3;
+  const int nj = (H + 511) >> 9;
+  for (int t0 = 0; t0 < T; t0 += kDenseTB) {
+    const int nt = min(kDenseTB, T - t0);
+    __syncthreads();
+    for (int i = threadIdx.x; i < nt * h8; i += blockDim.x)
+      xs[i] = reinterpret_cast<const uint4*>(x + (size_t)(t0 + i / h8) * H)[i % h8];
+    __syncthreads();
+    for (int row = blockIdx.x * 4 + wid; row < total_rows; row += gridDim.x * 4) {
+      int r = row, si = 0;
+      while (si < segs.nseg - 1 && r >= segs.s[si].n) {
+        r -= segs.s[si].n;
+        ++si;
+      }
+      const uint4* wrow = reinterpret_cast<const uint4*>(segs.s[si].w + (size_t)r * H);
+      float acc[kDenseTB] = {0.f, 0.f, 0.f, 0.f};
+      for (int j = 0; j < nj; ++j) {
+        const int k8 = 64 * j + lane;
+        if (k8 >= h8) break;
+        const uint4 wv = wrow[k8];
+        const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+        for (int t = 0; t < kDenseTB; ++t) {
+          if (t >= nt) break;
+          const uint4 xv = xs[t * h8 + k8];
+          const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+          float a = acc[t];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float wf = __uint_as_float((e & 1) ? (ww[e >> 1] & 0xFFFF0000u) : (ww[e >> 1] << 16));
+            const float xf = __uint_as_float((e & 1) ? (xx[e >> 1] & 0xFFFF0000u) : (xx[e >> 1] << 16));
+            a = __builtin_fmaf(xf, wf, a);
+          }
+          acc[t] = a;
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < kDenseTB; ++t) {
+        if (t >= nt) break;
+        const float v = ss_wave_sum(acc[t]);
+        if (lane == 0) segs.s[si].out[(size_t)(t0 + t) * segs.s[si].out_ld + r] = (uint16_t)ss_f32_to_bf16(v);
+      }
+    }
+  }
+}
+
+hipError_t launch_dense_rows(const uint16_t* x, int T, int H, const DenseSeg* segs, int nseg, hipStream_t st) {
+  SegPack p{};
+  int total = 0;
+  for (int i = 0; i < nseg; ++i) {
+    p.s[i] = segs[i];
+    total += segs[i].n;
+  }
+  p.nseg = nseg;
+  const int grid = (total + 3) / 4;
+  const size_t lds = (size_t)kDenseTB * H * 2;
+  hipLaunchKernelGGL(dense_rows_kernel, dim3(grid), dim3(256), lds, st, x, T, H, p, total);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- router tail
+SS_DEV bool ss_better(uint32_t k1, int i1, uint32_t k2, int i2) { return k1 > k2 || (k1 == k2 && i1 < i2); }
+
+__global__ __launch_bounds__(64) void router_topk_kernel(const uint16_t* __restrict__ logits,
+                                                         const float* __restrict__ bias, float* __restrict__ probs,
+                                                         int32_t* __restrict__ ids, float* __restrict__ weights, int E,
+                                                         int K) {
+  extern __shared__ float sm[];  // E floats, then E taken flags (bytes)
+  uint8_t* taken = reinterpret_cast<uint8_t*>(sm + E);
+  __shared__ float tv[64];
+  __shared__ int ti[64];
+  const int t = blockIdx.x, lane = threadIdx.x;
+  const uint16_t* lg = logits + (size_t)t * E;
+  float m = -__builtin_inff();
+  for (int e = lane; e < E; e += 64) {
+    float s = ss_bf16_to_f32(lg[e]);
+    if (bias) s = s + bias[e];
+    sm[e] = s;
+    taken[e] = 0;
+    m = fmaxf(m, s);
+  }
+  m = ss_wave_max(m);
+  float acc = 0.f;
+  for (int e = lane; e < E; e += 64) {
+    const float v = ss_expf(sm[e] - m);
+    sm[e] = v;
+    acc = acc + v;
+  }
+  const float z = ss_wave_sum(acc);
+  for (int e = lane; e < E; e += 64) {
+    const float p = sm[e] / z;
+    sm[e] = p;
+    if (probs) probs[(size_t)t * E + e] = p;
+  }
+  __syncthreads();
+  for (int r = 0; r < K; ++r) {
+    uint32_t bk = 0;
+    int bi = 0x7FFFFFFF;
+    for (int e = lane; e < E; e += 64) {
+      if (taken[e]) continue;
+      const uint32_t k = ss_key(sm[e]);
+      if (ss_better(k, e, bk, bi)) {
+        bk = k;
+        bi = e;
+      }
+    }
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) {
+      const uint32_t ok = (uint32_t)ss_shfl_xor_i((int)bk, msk);
+      const int oi = ss_shfl_xor_i(bi, msk);
+      if (ss_better(ok, oi, bk, bi)) {
+        bk = ok;
+        bi = oi;
+      }
+    }
+    if (lane == 0) {
+      taken[bi] = 1;
+      ti[r] = bi;
+      tv[r] = sm[bi];
+    }
+    __syncthreads();
+  }
+  if (lane == 0) {
+    float s = 0.f;
+    for (int r = 0; r < K; ++r) s = s + tv[r];
+    for (int r = 0; r < K; ++r) {
+      ids[(size_t)t * K + r] = ti[r];
+      weights[(size_t)t * K + r] = tv[r] / s;
+    }
+  }
+}
+
+hipError_t launch_router_topk(const uint16_t* logits, const float* bias, float* probs, int32_t* ids, float* weights,
+                              int T, int E, int K, hipStream_t st) {
+  const size_t lds = (size_t)E * 4 + (size_t)E;
+  hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(64), lds, st, logits, bias, probs, ids, weights, E, K);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- topk_stable
+// One block of 256 threads per row; thread t owns the contiguous index range [t*C, (t+1)*C).
+constexpr int kTopkThreads = 256;
+
+__global__ __launch_bounds__(kTopkThreads) void topk_stable_kernel(const float* __restrict__ scores,
+                                                                   const int32_t* __restrict__ n_valid,
+                                                                   int32_t* __restrict__ out_idx,
+                                                                   float* __restrict__ out_val, int N, int k) {
+  __shared__ int hist[256];
+  __shared__ int scan_a[kTopkThreads], scan_b[kTopkThreads];
+  __shared__ uint32_t s_prefix;
+  __shared__ int s_need;
+  __shared__ uint32_t sel_key[16];
+  __shared__ int sel_idx[16];
+  const int row = blockIdx.x, tid = threadIdx.x;
+  const float* x = scores + (size_t)row * N;
+  int nv = N;
+  if (n_valid) nv = min(max(n_valid[row], 0), N);
+  const int C = (N + kTopkThreads - 1) / kTopkThreads;
+  const int lo = min(tid * C, nv), hi = min(lo + C, nv);
+  const int want = min(k, nv);  // entries that can be selected
+  // Radix select of the want-th largest key, 8 bits per pass from the top.
+  uint32_t prefix = 0;
+  int need = want;
+  if (want > 0) {
+    for (int pass = 0; pass < 4; ++pass) {
+      const int shift = 24 - 8 * pass;
+      const uint32_t mask_hi = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
+      hist[tid] = 0;
+      __syncthreads();
+      for (int i = lo; i < hi; ++i) {
+        const uint32_t key = ss_key(x[i]);
+        if ((key & mask_hi) == prefix) atomicAdd(&hist[(key >> shift) & 255], 1);
+      }
+      __syncthreads();
+      if (tid == 0) {
+        int cum = 0, d = 255;
+        for (; d > 0; --d) {
+          if (cum + hist[d] >= need) break;
+          cum += hist[d];
+        }
+        s_prefix = prefix | ((uint32_t)d << shift);
+        s_need = need - cum;
+      }
+      __syncthreads();
+      prefix = s_prefix;
+      need = s_need;
+      __syncthreads();
+    }
+  }
+  const uint32_t thr = prefix;
+  // Count greater / equal per thread, then exclusive scans (thread 0, fixed order).
+  int ng = 0, ne = 0;
+  if (want > 0) {
+    for (int i = lo; i < hi; ++i) {
+      const uint32_t key = ss_key(x[i]);
+      ng += key > thr;
+      ne += key == thr;
+    }
+  }
+  scan_a[tid] = ng;
+  scan_b[tid] = ne;
+  __syncthreads();
+  if (tid == 0) {
+    int a = 0, b = 0;
+    for (int i = 0; i < kTopkThreads; ++i) {
+      const int va = scan_a[i], vb = scan_b[i];
+      scan_a[i] = a;
+      scan_b[i] = b;
+      a += va;
+      b += vb;
+    }
+    s_need = a;  // total greater
+  }
+  __syncthreads();
+  const int total_greater = s_need;
+  const int budget = want - total_greater;
+  // Selected count per thread (greater, plus ties whose tie rank is inside the budget).
+  int tie = scan_b[tid], nsel = 0;
+  if (want > 0) {
+    for (int i = lo; i < hi; ++i) {
+      const uint32_t key = ss_key(x[i]);
+      if (key > thr) {
+        ++nsel;
+      } else if (key == thr) {
+        if (tie < budget) ++nsel;
+        ++tie;
+      }
+    }
+  }
+  __syncthreads();
+  scan_a[tid] = nsel;
+  __syncthreads();
+  if (tid == 0) {
+    int a = 0;
+    for (int i = 0; i < kTopkThreads; ++i) {
+      const int v = scan_a[i];
+      scan_a[i] = a;
+      a += v;
+    }
+  }
+  __syncthreads();
+  int pos = scan_a[tid];
+  tie = scan_b[tid];
+  int32_t* oi = out_idx + (size_t)row * k;
+  float* ov = out_val ? out_val + (size_t)row * k : nullptr;
+  const bool by_value = k <= 16;
+  if (want > 0) {
+    for (int i = lo; i < hi; ++i) {
+      const uint32_t key = ss_key(x[i]);
+      bool sel = false;
+      if (key > thr) {
+        sel = true;
+      } else if (key == thr) {
+        sel = tie < budget;
+        ++tie;
+      }
+      if (!sel) continue;
+      if (by_value) {
+        sel_key[pos] = key;
+        sel_idx[pos] = i;
+      } else {
+        oi[pos] = i;
+        if (ov) ov[pos] = x[i];
+      }
+      ++pos;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    if (by_value) {
+      // Insertion sort of the selected entries by (key desc, index asc); they arrive in index order.
+      for (int a = 1; a < want; ++a) {
+        const uint32_t kk = sel_key[a];
+        const int ii = sel_idx[a];
+        int b = a - 1;
+        while (b >= 0 && (sel_key[b] < kk || (sel_key[b] == kk && sel_idx[b] > ii))) {
+          sel_key[b + 1] = sel_key[b];
+          sel_idx[b + 1] = sel_idx[b];
+          --b;
+        }
+        sel_key[b + 1] = kk;
+        sel_idx[b + 1] = ii;
+      }
+      for (int a = 0; a < want; ++a) {
+        oi[a] = sel_idx[a];
+        if (ov) ov[a] = x[sel_idx[a]];
+      }
+    }
+    for (int a = want; a < k; ++a) {
+      oi[a] = -1;
+      if (ov) ov[a] = -__builtin_inff();
+    }
+  }
+}
+
+hipError_t launch_topk_stable(const float* scores, const int32_t* n_valid, int32_t* idx, float* val, int R, int N,
+                              int k, hipStream_t st) {
+  hipLaunchKernelGGL(topk_stable_kernel, dim3(R), dim3(kTopkThreads), 0, st, scores, n_valid, idx, val, N, k);
+  return hipGetLastError();
+}
+
+}  // namespace ss

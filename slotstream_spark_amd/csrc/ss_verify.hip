@@ -1,0 +1,913 @@
+// One persistent launch per MoE layer of a verify step (T <= 4 tokens), or per block of 4 rows of moe_decode.
+//
+// Phases (every workgroup resident: the grid is one workgroup per CU; 4 waves each):
+//   A  verify mode. Dense bf16 rows in the fixed fp32 order of dense_rows_kernel (the E router rows, the Is shared
+//      gate/up row pairs, the shared_expert_gate row) spread over every wave of the grid, while the layer's map and
+//      slot_ptr tables are staged into LDS. Each workgroup publishes its finished row counts (release).
+//   B  Each workgroup waits for all router rows (acquire) and computes the router tail for every token itself
+//      (softmax, top-k, renormalisation: the same bits everywhere), then the unique expert list of the block.
+//      Workgroups that own output rows then start direct-to-LDS loads of their down-projection weights for the
+//      first P experts, which stream while phase C runs.
+//   C  Routed gate/up items, one (unique expert u, 8-row tile p) per wave at a time over the full K: 16 columns =
+//      8 gate rows + 8 up rows, 16 x 16-byte loads per lane in flight, x A-fragments from LDS. The epilogue writes
+//      h as bf16 hi/lo MFMA A-fragments (the layout the down phase consumes), 8-element partial sums of h for the
+//      per-group bias term, and h_buf. Each workgroup publishes its item count.
+//   D  Workgroup b < H/16 owns output rows 16b..16b+15 for every expert. After all items (and, in verify mode, the
+//      shared rows) are published, it stages the h fragments into LDS, each wave runs the down MFMAs of the experts
+//      u = w (mod 4), the shared-expert down rows are added, and the rank-order combine writes o, out and y. No
+//      floating-point sum uses atomics; every sum has a fixed order.
+// The kernel is written with rolled loops and small unroll factors: each workgroup runs it once per launch, so its
+// instruction footprint, not only its arithmetic, bounds the time.
+// Device counters live at the start of the scratch; the last workgroup to leave resets them, so every launch starts
+// from zero. Waits are bounded: on timeout the kernel raises SS_ERR_TIMEOUT and finishes.
+//
+// Reference semantics: kernels/moe_gemv_affine.py:56-147, model/layers.py:336-402, reference_torch.py:118-134,
+// runtime/graphs.py:160-169.
+#include <type_traits>
+
+#include "ss_common.hpp"
+#include "ss_launch.hpp"
+
+namespace ss {
+
+constexpr int kTBv = 4;          // tokens per launch
+constexpr int kMaxEv = 512;      // experts per layer (LDS tables)
+constexpr int kMaxQv = 64;       // kTBv * K, K <= 16
+constexpr int kSpinMax = 1 << 22;
+constexpr int SS_ERR_TIMEOUT = 16;
+constexpr size_t kLdsBudget = 160 * 1024 - 16 * 1024;  // dynamic LDS left after the static part (< 16 KB)
+
+enum { CTR_ROUTER = 0, CTR_SHARED = 16, CTR_ITEMS = 32, CTR_EXIT = 48 };
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+// Pointers that reach the kernel through the argument struct or LDS are generic (flat) unless cast: flat accesses
+// wait on both the vector-memory and LDS counters, so every hot global access goes through a global-space pointer.
+#define SS_G __attribute__((address_space(1)))
+template <class T>
+SS_DEV SS_G T* gp(T* p) {
+  return (SS_G T*)p;
+}
+// 16-byte global load / store through the builtin vector type (HIP's uint4 class does not take address spaces).
+SS_DEV uint4 ldg16(const void* p) {
+  const ss_u32x4 v = *(const SS_G ss_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+SS_DEV void stg16(void* p, uint4 v) {
+  ss_u32x4 t;
+  t.x = v.x;
+  t.y = v.y;
+  t.z = v.z;
+  t.w = v.w;
+  *(SS_G ss_u32x4*)p = t;
+}
+
+struct VLayout {
+  size_t ctr, logits, gsh, ush, sgl, hfrag, hsum8, total;
+};
+
+static __host__ __device__ inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+static __host__ __device__ inline VLayout vlayout(int T, int I, int Is, int K, int E) {
+  VLayout l;
+  size_t o = 0;
+  l.ctr = o;
+  o = al256(o + 256);
+  l.logits = o;
+  o = al256(o + (size_t)T * E * 2);
+  l.gsh = o;
+  o = al256(o + (size_t)T * Is * 2);
+  l.ush = o;
+  o = al256(o + (size_t)T * Is * 2);
+  l.sgl = o;
+  o = al256(o + (size_t)T * 2);
+  l.hfrag = o;
+  o = al256(o + (size_t)T * K * I * 4);
+  l.hsum8 = o;
+  o = al256(o + (size_t)T * K * (I / 8) * 4);
+  l.total = o;
+  return l;
+}
+
+size_t verify_scratch_bytes(int T, int H, int I, int Is, int K, int E) {
+  (void)H;
+  return vlayout(T, I, Is, K, E).total;
+}
+
+// Dynamic LDS layout (bytes): x fragments, staged h fragments (also the router-tail scores), down-weight prefetch
+// slots (P experts), per-expert partial dots.
+struct DLayout {
+  size_t xfrag, hfrag, pref, part, total;
+  int P;           // experts whose down weights are prefetched per batch
+  int stage_h;     // 1: the h fragments are staged in LDS for the down phase; 0: read from global memory
+  size_t slot;     // bytes per prefetch slot
+};
+
+// Fits the budget for every supported shape: x fragments (<= 64 KB) + partial dots (<= 16 KB) + router scores
+// (<= 8 KB) + one prefetch slot (<= 12 KB); the h fragments are staged only when they fit beside one slot.
+static __host__ __device__ inline DLayout dlayout(int T, int H, int I, int K, int E, int x_f32, int verify) {
+  DLayout d;
+  const int nq = T * K;
+  const int nu_max = nq < E ? nq : E;
+  size_t o = 0;
+  d.xfrag = o;
+  o += (size_t)(H / 128) * 4 * 4 * kTBv * (x_f32 ? 2 : 1) * 16;
+  d.part = o;
+  o += (size_t)nu_max * 16 * kTBv * 4;
+  d.slot = (size_t)(I / 128) * 64 * (16 + 4 + 4);
+  d.hfrag = o;
+  const size_t hf = (size_t)nq * I * 4;
+  const size_t sc = verify ? (size_t)T * E * 4 : 0;
+  d.stage_h = o + (hf > sc ? hf : sc) + d.slot <= kLdsBudget;
+  o += d.stage_h ? (hf > sc ? hf : sc) : sc;
+  d.pref = o;
+  const long room = (long)kLdsBudget - (long)o;
+  int P = room > 0 ? (int)(room / (long)d.slot) : 0;
+  if (P > nu_max) P = nu_max;
+  d.P = P;
+  o += (size_t)P * d.slot;
+  d.total = o;
+  return d;
+}
+
+// Cross-workgroup hand-off. Producer: every wave waits for its own stores (s_waitcnt), the workgroup barrier orders
+// them, then one thread publishes with a single agent-scope release (one L2 write-back per workgroup). Consumer: one
+// thread polls with relaxed agent-scope loads (no cache maintenance per poll), then one agent-scope acquire fence,
+// then the workgroup barrier.
+SS_DEV void stores_done() { __builtin_amdgcn_s_waitcnt(0); }
+
+SS_DEV void signal_add(int* c, int v) { __hip_atomic_fetch_add(c, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT); }
+
+SS_DEV void wait_ge(int* c, int target, int* err) {
+  for (int it = 0;; ++it) {
+    if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+    if (it >= kSpinMax) {
+      ss_raise(err, SS_ERR_TIMEOUT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Direct-to-LDS loads: lane l's `size` bytes land at lds_wave_base + size * l (lds_wave_base is wave-uniform).
+SS_DEV void dma16(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+SS_DEV void dma4(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_wave_base, 4, 0, 0);
+}
+
+struct VSmem {
+  int map[kMaxEv];
+  const uint8_t* base_e[kMaxEv];  // record of every expert of the layer (verify mode)
+  const uint8_t* base[kMaxQv];    // per unique expert
+  uint32_t umask[kMaxQv][kTBv];
+  int use_u[kMaxQv];
+  int ids[kMaxQv];
+  float wts[kMaxQv];
+  float gx[64][kTBv];             // x group sums (H <= 4096)
+  float hsum[kMaxQv][16];         // h group sums per use (I <= 1024)
+  float shv[16][kTBv];
+  float xch[4][16 * kTBv];        // per-wave exchange of one item's 16 columns x 4 tokens
+  int nt, nu;
+};
+
+SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+SS_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+SS_DEV float pick_half(uint32_t pair, int hi) { return hi ? bf_hi(pair) : bf_lo(pair); }
+
+// bf16 pair (element d, element d+4) of 8 consecutive bf16 held as 4 words (e0e1, e2e3, e4e5, e6e7).
+SS_DEV uint4 perm_pairs(uint4 v) {
+  uint4 f;
+  f.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+  f.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+  f.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+  f.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+  return f;
+}
+
+SS_DEV ss_u32x4 as_v(uint4 v) {
+  ss_u32x4 r;
+  r.x = v.x;
+  r.y = v.y;
+  r.z = v.z;
+  r.w = v.w;
+  return r;
+}
+
+// Unique experts of the block in first-occurrence order from s.ids. Wave 0 only; caller syncs.
+SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
+  const int lane = threadIdx.x;
+  const int nq = s.nt * a.K;
+  int e = -1, slot = -1;
+  bool valid = false;
+  if (lane < nq) {
+    e = s.ids[lane];
+    if (e >= 0 && e < a.E) {
+      if (tables_in_lds) {
+        slot = s.map[e];
+      } else {
+        const int64_t mi = a.map_base + e;
+        if (mi >= 0 && mi < a.map_len) slot = a.map[mi];
+      }
+      valid = slot >= 0 && (int64_t)slot < a.n_slots;
+      if (!valid) ss_raise(a.err, SS_ERR_SLOT);
+    } else {
+      ss_raise(a.err, SS_ERR_EXPERT_ID);
+    }
+  }
+  int j0 = lane;
+#pragma unroll 1
+  for (int j = 0; j < 64; ++j) {
+    const int ej = __shfl(e, j, 64);
+    const int vj = __shfl((int)valid, j, 64);
+    if (j < lane && vj && valid && ej == e && j0 == lane) j0 = j;
+  }
+  const bool first = valid && j0 == lane;
+  const uint64_t mask = __ballot(first);
+  const int uidx = valid ? __popcll(mask & ((1ull << j0) - 1ull)) : -1;
+  if (first) s.base[uidx] = tables_in_lds ? s.base_e[e] : reinterpret_cast<const uint8_t*>(a.slot_ptr[slot]);
+  if (lane < nq) {
+    s.use_u[lane] = uidx;
+    if (valid) atomicOr(&s.umask[uidx][lane / a.K], 1u << (lane % a.K));
+  }
+  if (lane == 0) s.nu = __popcll(mask);
+}
+
+// Router tail of token t in one wave, scores staged in LDS (same operations and order as router_topk_kernel).
+SS_DEV void router_tail_wave(const VerifyArgs& a, const uint16_t* logits, int t, VSmem& s) {
+  const int lane = threadIdx.x & 63;
+  const int E = a.E, K = a.K;
+  constexpr int NV = kMaxEv / 64;
+  const SS_G uint16_t* lg = gp(logits) + (size_t)t * E;
+  float v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) v[i] = lane + 64 * i < E ? ss_bf16_to_f32(lg[lane + 64 * i]) : 0.f;
+  if (a.bias) {
+    const SS_G float* bs = gp(a.bias);
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i < E) v[i] = v[i] + bs[lane + 64 * i];
+  }
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < E) m = fmaxf(m, v[i]);
+  m = ss_wave_max(m);
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+    if (lane + 64 * i < E) {
+      v[i] = ss_expf(v[i] - m);
+      acc = acc + v[i];
+    }
+  const float z = ss_wave_sum(acc);
+  // Candidates packed as (key << 32) | ~index: the 64-bit maximum is the largest probability, ties to the lower
+  // index; taken or absent entries are 0, below every present entry.
+  uint64_t cand[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = v[i] / z;
+    cand[i] = e < E ? ((uint64_t)ss_key(v[i]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e) : 0ull;
+  }
+#pragma unroll 1
+  for (int r = 0; r < K; ++r) {
+    uint64_t best = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) best = cand[i] > best ? cand[i] : best;
+#pragma unroll
+    for (int msk = 32; msk >= 1; msk >>= 1) {
+      const uint32_t ohi = (uint32_t)ss_shfl_xor_i((int)(uint32_t)(best >> 32), msk);
+      const uint32_t olo = (uint32_t)ss_shfl_xor_i((int)(uint32_t)best, msk);
+      const uint64_t o = ((uint64_t)ohi << 32) | olo;
+      best = o > best ? o : best;
+    }
+    const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
+    float pv = 0.f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+      if (lane + 64 * i == bi) {
+        cand[i] = 0ull;
+        pv = v[i];
+      }
+    pv = __shfl(pv, bi & 63, 64);
+    if (lane == 0) {
+      s.ids[t * K + r] = bi;
+      s.wts[t * K + r] = pv;
+    }
+  }
+  if (lane == 0) {
+    float sum = 0.f;
+#pragma unroll 1
+    for (int r = 0; r < K; ++r) sum = sum + s.wts[t * K + r];
+#pragma unroll 1
+    for (int r = 0; r < K; ++r) s.wts[t * K + r] = s.wts[t * K + r] / sum;
+  }
+}
+
+// One dense bf16 row against up to 4 tokens in the dense_rows_kernel order; x rows in global memory.
+// xs: the x rows staged in LDS as uint4 [t][H / 8].
+template <int NJ>
+SS_DEV void dense_row(const uint4* xs, int nt, int H, const uint16_t* wrow_p, float out[kTBv]) {
+  const int lane = threadIdx.x & 63;
+  const int h8 = H >> 3;
+  uint4 wv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+    wv[j] = (64 * j + lane < h8) ? ldg16(wrow_p + 8 * (64 * j + lane)) : make_uint4(0u, 0u, 0u, 0u);
+  float acc[kTBv] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 1
+  for (int t = 0; t < nt; ++t) {
+    float ac = 0.f;
+    const uint4* xr = xs + (size_t)t * h8;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (64 * j + lane >= h8) break;
+      const uint4 xv = xr[64 * j + lane];
+      const uint32_t ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+      const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float wf = (e & 1) ? bf_hi(ww[e >> 1]) : bf_lo(ww[e >> 1]);
+        const float xf = (e & 1) ? bf_hi(xx[e >> 1]) : bf_lo(xx[e >> 1]);
+        ac = __builtin_fmaf(xf, wf, ac);
+      }
+    }
+    // acc[t] = ac with a runtime t: select into fixed registers
+#pragma unroll
+    for (int q = 0; q < kTBv; ++q)
+      if (q == t) acc[q] = ac;
+  }
+#pragma unroll
+  for (int t = 0; t < kTBv; ++t) out[t] = ss_wave_sum(acc[t]);
+}
+
+template <int NJG, int NJD, bool XF32>
+__global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec) {
+  extern __shared__ uint4 dsm[];
+  __shared__ VSmem s;
+  uint8_t* dl = reinterpret_cast<uint8_t*>(dsm);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int G = gridDim.x, bid = blockIdx.x;
+  const int n = lane & 15, g = lane >> 4;
+  const int T = a.T, H = a.H, I = a.I, K = a.K, E = a.E;
+  const bool verify = a.mode == 0;
+  const VLayout L = vlayout(T, I, verify ? a.Is : 0, K, verify ? E : 0);
+  const DLayout D = dlayout(T, H, I, K, E, XF32 ? 1 : 0, verify ? 1 : 0);
+  uint8_t* scr = static_cast<uint8_t*>(a.scratch);
+  int* ctr = reinterpret_cast<int*>(scr + L.ctr);
+  uint16_t* logits = reinterpret_cast<uint16_t*>(scr + L.logits);
+  uint16_t* gsh = reinterpret_cast<uint16_t*>(scr + L.gsh);
+  uint16_t* ush = reinterpret_cast<uint16_t*>(scr + L.ush);
+  uint16_t* sgl = reinterpret_cast<uint16_t*>(scr + L.sgl);
+  uint4* hfrag = reinterpret_cast<uint4*>(scr + L.hfrag);
+  float* hsum8 = reinterpret_cast<float*>(scr + L.hsum8);
+  uint4* xfl = reinterpret_cast<uint4*>(dl + D.xfrag);
+  uint4* hfl = reinterpret_cast<uint4*>(dl + D.hfrag);
+  float* partl = reinterpret_cast<float*>(dl + D.part);
+  uint8_t* prefl = dl + D.pref;
+  const int nt = T;
+#define SS_TRACE(k)                                                                               \
+  do {                                                                                            \
+    if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+
+  SS_TRACE(0);
+  if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + 12] = __builtin_amdgcn_s_memtime();
+  for (int i = tid; i < kMaxQv * kTBv; i += 256) (&s.umask[0][0])[i] = 0u;
+  if (tid == 0) s.nt = nt;
+
+  // ------------------------------------------------------------ phase A + B (verify) / ids (decode)
+  if (verify) {
+    // Stage x into the (not yet used) x-fragment region: uint4 [t][H / 8].
+    uint4* xs = xfl;
+    {
+      const uint16_t* xg = static_cast<const uint16_t*>(a.x);
+      for (int i = tid; i < nt * (H >> 3); i += 256) xs[i] = ldg16(xg + 8 * i);
+    }
+    __syncthreads();
+    const int Is = a.Is, J = E + Is + 1, W = G * 4;
+#pragma unroll 1
+    for (int j = bid * 4 + w; j < J; j += W) {
+      const int nrow = (j >= E && j < E + Is) ? 2 : 1;
+#pragma unroll 1
+      for (int rr = 0; rr < nrow; ++rr) {
+        const uint16_t* wr;
+        uint16_t* dst;
+        int ld;
+        if (j < E) {
+          wr = a.router_w + (size_t)j * H;
+          dst = logits + j;
+          ld = E;
+        } else if (j < E + Is) {
+          wr = (rr ? a.sh_up : a.sh_gate) + (size_t)(j - E) * H;
+          dst = (rr ? ush : gsh) + (j - E);
+          ld = Is;
+        } else {
+          wr = a.sh_g;
+          dst = sgl;
+          ld = 1;
+        }
+        float d[kTBv];
+        dense_row<(NJG + 3) / 4>(xs, nt, H, wr, d);
+        if (lane == 0)
+#pragma unroll 1
+          for (int t = 0; t < nt; ++t) gp(dst)[(size_t)t * ld] = (uint16_t)ss_f32_to_bf16(d[t]);
+      }
+    }
+    stores_done();
+    __syncthreads();
+    if (tid == 0) {
+      int nr = 0, ns = 0;
+      for (int ww = 0; ww < 4; ++ww)
+        for (int j = bid * 4 + ww; j < J; j += W) (j < E ? nr : ns) += 1;
+      if (nr) signal_add(ctr + CTR_ROUTER, nr);
+      if (ns) signal_add(ctr + CTR_SHARED, ns);
+      SS_TRACE(1);
+    }
+    // The layer's map / slot_ptr tables into LDS while the other workgroups finish their router rows.
+#pragma unroll 1
+    for (int e = tid; e < E; e += 256) {
+      const int64_t mi = a.map_base + e;
+      const int slot = mi < a.map_len ? a.map[mi] : -1;
+      s.map[e] = slot;
+      s.base_e[e] = (slot >= 0 && (int64_t)slot < a.n_slots) ? reinterpret_cast<const uint8_t*>(a.slot_ptr[slot])
+                                                             : nullptr;
+    }
+    if (tid == 0) {
+      wait_ge(ctr + CTR_ROUTER, E, a.err);
+      SS_TRACE(2);
+    }
+    __syncthreads();
+    if (w < nt) router_tail_wave(a, logits, w, s);
+    __syncthreads();
+    SS_TRACE(3);
+    if (bid == 0 && tid < nt * K) {
+      a.ids_out[tid] = s.ids[tid];
+      a.w_out[tid] = s.wts[tid];
+    }
+  } else {
+    if (tid < nt * K) {
+      s.ids[tid] = a.ids_in[tid];
+      s.wts[tid] = a.w_in[tid];
+    }
+    __syncthreads();
+  }
+  if (tid < 64) unique_setup(a, s, verify);
+  __syncthreads();
+  SS_TRACE(4);
+  const int nu = s.nu;
+  const int tiles = I >> 3;
+  const int n_items = nu * tiles;
+  const bool has_tile = bid < (H >> 4);
+  const int my_half = g >> 1, my_part = g & 1;
+  const int drow = 16 * bid + n;  // down row of this lane
+  const int64_t drow_b = I >> 1, dsb_b = (I >> 6) * 2;
+
+  // ------------------------------------------------------------ down prefetch: P experts into LDS
+  // Slot layout (per expert): [NJD][64 lanes] weight uint4, then [NJD][64 lanes] scale dword, [NJD][64] bias dword.
+  auto issue_down = [&](int u, int slotp) {
+    uint8_t* sl = prefl + (size_t)slotp * D.slot;
+    const uint8_t* base = s.base[u];
+    for (int j = 0; j < NJD; ++j) {
+      dma16(base + rec.dw + drow * drow_b + 64 * j + 16 * g, sl + (size_t)j * 1024);
+      dma4(base + rec.ds + drow * dsb_b + 4 * j, sl + (size_t)NJD * 1024 + (size_t)j * 256);
+      dma4(base + rec.db + drow * dsb_b + 4 * j, sl + (size_t)NJD * 1280 + (size_t)j * 256);
+    }
+  };
+  if (has_tile) {
+#pragma unroll 1
+    for (int u = w; u < nu && u < D.P; u += 4) issue_down(u, u);
+  }
+  uint4 shw[4];
+  if (verify && has_tile) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int srow = 16 * bid + 4 * w + rr;
+      shw[rr] = (8 * lane < a.Is) ? reinterpret_cast<const uint4*>(a.sh_down + (size_t)srow * a.Is)[lane]
+                                  : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  SS_TRACE(5);
+
+  // ------------------------------------------------------------ phase C: gate/up, one item per wave at a time
+  // Items go first to the workgroups without down rows (bid >= H/16), one per wave, then wrap around.
+  const int W = G * 4;
+  const int gw = ((bid - (H >> 4) + G) % G) * 4 + w;
+  int my_items = 0;
+  for (int ww = 0; ww < 4; ++ww) {
+    const int gq = ((bid - (H >> 4) + G) % G) * 4 + ww;
+    for (int it = gq; it < n_items; it += W) ++my_items;
+  }
+  if (my_items) {
+    // x group sums and the A fragments of every K iteration into LDS: frag[j][i][g][t][part], active lanes only.
+    for (int q = tid; q < (H >> 6) * kTBv; q += 256) {
+      const int Gi = q >> 2, t = q & 3;
+      float sum = 0.f;
+      if (t < nt) {
+        if (XF32) {
+          const float4* xp = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + (size_t)t * H + 64 * Gi);
+#pragma unroll 1
+          for (int k = 0; k < 16; ++k) {
+            const float4 v = xp[k];
+            sum = sum + v.x;
+            sum = sum + v.y;
+            sum = sum + v.z;
+            sum = sum + v.w;
+          }
+        } else {
+          const uint4* xp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + (size_t)t * H + 64 * Gi);
+#pragma unroll 1
+          for (int k = 0; k < 8; ++k) {
+            const uint4 v = xp[k];
+            sum = sum + bf_lo(v.x);
+            sum = sum + bf_hi(v.x);
+            sum = sum + bf_lo(v.y);
+            sum = sum + bf_hi(v.y);
+            sum = sum + bf_lo(v.z);
+            sum = sum + bf_hi(v.z);
+            sum = sum + bf_lo(v.w);
+            sum = sum + bf_hi(v.w);
+          }
+        }
+      }
+      s.gx[Gi][t] = sum;
+    }
+    const int nfrag = NJG * 4 * 4 * kTBv;  // (j, i, g, t)
+    for (int f = tid; f < nfrag; f += 256) {
+      const int t = f & 3, gg = (f >> 2) & 3, i = (f >> 4) & 3, j = f >> 6;
+      const int kb = 128 * j + 32 * gg + 8 * i;
+      uint4 hi4 = make_uint4(0u, 0u, 0u, 0u), lo4 = make_uint4(0u, 0u, 0u, 0u);
+      if (t < nt) {
+        if (XF32) {
+          const float4* xp = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + (size_t)t * H + kb);
+          const float4 v0 = xp[0], v1 = xp[1];
+          const float e0[4] = {v0.x, v0.y, v0.z, v0.w}, e1[4] = {v1.x, v1.y, v1.z, v1.w};
+          uint32_t h[4], l[4];
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t b0 = ss_f32_to_bf16(e0[d]), b1 = ss_f32_to_bf16(e1[d]);
+            h[d] = b0 | (b1 << 16);
+            l[d] = ss_f32_to_bf16(e0[d] - ss_bf16_to_f32(b0)) | (ss_f32_to_bf16(e1[d] - ss_bf16_to_f32(b1)) << 16);
+          }
+          hi4 = make_uint4(h[0], h[1], h[2], h[3]);
+          lo4 = make_uint4(l[0], l[1], l[2], l[3]);
+        } else {
+          hi4 = perm_pairs(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + (size_t)t * H + kb));
+        }
+      }
+      xfl[f * (XF32 ? 2 : 1)] = hi4;
+      if (XF32) xfl[f * 2 + 1] = lo4;
+    }
+    __syncthreads();
+    SS_TRACE(6);
+    const int m = lane & 15, at = m & 3, agrp = m >> 2, ahh = agrp >> 1, apart = agrp & 1;
+    const bool a_act = ahh == (g >> 1) && at < nt && (XF32 || apart == 0);
+    const int64_t row_b = H >> 1, sb_b = (H >> 6) * 2;
+    float* xch = s.xch[w];
+#pragma unroll 1
+    for (int item = gw; item < n_items; item += W) {
+      const int u = item / tiles, p = item - u * tiles;
+      const int r8 = 8 * p + (n & 7);
+      const uint8_t* base = s.base[u];
+      const uint8_t* wrow = base + (n < 8 ? rec.gw : rec.uw) + r8 * row_b + 16 * g;
+      const SS_G uint32_t* srow = (const SS_G uint32_t*)gp(base + (n < 8 ? rec.gs : rec.us) + r8 * sb_b);
+      const SS_G uint32_t* brow = (const SS_G uint32_t*)gp(base + (n < 8 ? rec.gb : rec.ub) + r8 * sb_b);
+      uint4 wv[NJG];
+      uint32_t sv[NJG], bv[NJG];
+#pragma unroll
+      for (int j = 0; j < NJG; ++j) {
+        wv[j] = ldg16(wrow + 64 * j);
+        sv[j] = srow[j];
+        bv[j] = brow[j];
+      }
+      float acc[kTBv] = {0.f, 0.f, 0.f, 0.f};
+      constexpr int JB = NJG % 4 == 0 ? 4 : 1;  // K iterations whose LDS operands are read before their MFMAs
+#pragma unroll
+      for (int j0 = 0; j0 < NJG; j0 += JB) {
+        uint4 av4[JB][4];
+        float4 gxv[JB];
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj) {
+          const int j = j0 + jj;
+          const uint4* fp = xfl + (size_t)(((j * 4) * 4 + g) * kTBv + at) * (XF32 ? 2 : 1) + (XF32 ? apart : 0);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) av4[jj][i] = fp[(size_t)i * 16 * (XF32 ? 2 : 1)];  // in bounds for every lane
+          gxv[jj] = reinterpret_cast<const float4*>(s.gx)[2 * j + my_half];
+        }
+#pragma unroll
+        for (int jj = 0; jj < JB; ++jj) {
+          const int j = j0 + jj;
+          ss_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            ss_u32x4 av = as_v(av4[jj][i]);
+            if (!a_act) av = ss_u32x4{0u, 0u, 0u, 0u};
+            const uint32_t wd = i == 0 ? wv[j].x : i == 1 ? wv[j].y : i == 2 ? wv[j].z : wv[j].w;
+            d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
+          }
+          const float sf = pick_half(sv[j], my_half);
+          const float bf = pick_half(bv[j], my_half);
+          const float s16 = sf * kNibbleScale;
+          const float bp = my_part ? 0.f : __builtin_fmaf(-kNibbleScale, sf, bf);
+          const float gxa[kTBv] = {gxv[jj].x, gxv[jj].y, gxv[jj].z, gxv[jj].w};
+#pragma unroll
+          for (int r = 0; r < kTBv; ++r) {
+            acc[r] = __builtin_fmaf(s16, d[r], acc[r]);
+            acc[r] = __builtin_fmaf(bp, gxa[r], acc[r]);
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kTBv; ++r) {
+        acc[r] = acc[r] + ss_shfl_xor(acc[r], 16);
+        acc[r] = acc[r] + ss_shfl_xor(acc[r], 32);
+        if (g == 0) xch[n * kTBv + r] = acc[r];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      if (lane < nt) {
+        const int r = lane;
+        float hv[8];
+        float sum8 = 0.f;
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const float gv = xch[c * kTBv + r], uv = xch[(c + 8) * kTBv + r];
+          hv[c] = gv / (1.f + ss_expf(-gv)) * uv;
+          sum8 = sum8 + hv[c];
+        }
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+          const uint32_t a0 = ss_f32_to_bf16(hv[d]), a1 = ss_f32_to_bf16(hv[d + 4]);
+          hw[d] = a0 | (a1 << 16);
+          lw[d] = ss_f32_to_bf16(hv[d] - ss_bf16_to_f32(a0)) | (ss_f32_to_bf16(hv[d + 4] - ss_bf16_to_f32(a1)) << 16);
+        }
+        const uint4 fhi = make_uint4(hw[0], hw[1], hw[2], hw[3]), flo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        const int jf = p >> 4, gf = (p & 15) >> 2, ifr = p & 3;
+        uint32_t mk = s.umask[u][r];
+        while (mk) {
+          const int k = __ffs(mk) - 1;
+          mk &= mk - 1;
+          const int q = r * K + k;
+          uint4* fpo = hfrag + (((size_t)q * NJD + jf) * 4 + gf) * 8 + ifr;
+          stg16(fpo, fhi);
+          stg16(fpo + 4, flo);
+          gp(hsum8)[(size_t)q * (I >> 3) + p] = sum8;
+          if (a.h_buf) {
+            float* hp = a.h_buf + ((size_t)r * K + k) * I + 8 * p;
+            stg16(hp, make_uint4(__float_as_uint(hv[0]), __float_as_uint(hv[1]), __float_as_uint(hv[2]),
+                                 __float_as_uint(hv[3])));
+            stg16(hp + 4, make_uint4(__float_as_uint(hv[4]), __float_as_uint(hv[5]), __float_as_uint(hv[6]),
+                                     __float_as_uint(hv[7])));
+          }
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+    stores_done();
+    __syncthreads();
+    if (tid == 0) signal_add(ctr + CTR_ITEMS, my_items);
+    SS_TRACE(7);
+  }
+
+  // ------------------------------------------------------------ phase D: down + combine
+  if (has_tile) {
+    if (tid == 0) {
+      wait_ge(ctr + CTR_ITEMS, n_items, a.err);
+      if (verify) wait_ge(ctr + CTR_SHARED, a.Is + 1, a.err);
+    }
+    __syncthreads();
+    SS_TRACE(8);
+    const int nq = nt * K;
+    // Stage the h fragments of every use into LDS (1 KB per wave instruction) and the h group sums.
+    const int hchunks = D.stage_h ? nq * I * 4 / 1024 : 0;
+#pragma unroll 1
+    for (int c = w; c < hchunks; c += 4) dma16(reinterpret_cast<const uint8_t*>(hfrag) + (size_t)c * 1024 + 16 * lane,
+                                               reinterpret_cast<uint8_t*>(hfl) + (size_t)c * 1024);
+    for (int idx = tid; idx < nq * (I >> 6); idx += 256) {
+      const int q = idx / (I >> 6), Gi = idx - q * (I >> 6);
+      float sum = 0.f;
+      if (s.use_u[q] >= 0) {
+        const float* hp = hsum8 + (size_t)q * (I >> 3) + 8 * Gi;
+#pragma unroll 1
+        for (int c = 0; c < 8; ++c) sum = sum + hp[c];
+      }
+      s.hsum[q][Gi] = sum;
+    }
+    stores_done();
+    __syncthreads();
+    SS_TRACE(9);
+    const int m = lane & 15, at = m & 3, agrp = m >> 2, ahh = agrp >> 1, apart = agrp & 1;
+    const bool a_lane = ahh == (g >> 1) && at < nt;
+#pragma unroll 1
+    for (int u0 = 0; u0 < nu; u0 += D.P) {
+      if (u0 > 0) {
+        __syncthreads();
+#pragma unroll 1
+        for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) issue_down(u, u - u0);
+        stores_done();
+        __syncthreads();
+      }
+      // One expert: every operand is read up front (weights, scales, h fragments, h group sums; inactive lanes read
+      // in-bounds index 0 and are zeroed by a select), then the MFMA chains run without intervening waits.
+      auto expert = [&](int u, auto staged) {
+        constexpr bool STAGED = decltype(staged)::value;
+        const uint8_t* sl = prefl + (size_t)(u - u0) * D.slot;
+        const uint32_t am = a_lane ? s.umask[u][at] : 0u;
+        const int aq = am ? at * K + __ffs(am) - 1 : 0;
+        int qr[kTBv];
+        bool vr[kTBv];
+#pragma unroll
+        for (int r = 0; r < kTBv; ++r) {
+          const uint32_t mr = r < nt ? s.umask[u][r] : 0u;
+          vr[r] = mr != 0u;
+          qr[r] = mr ? r * K + __ffs(mr) - 1 : 0;
+        }
+        uint4 wq[NJD], av4[NJD][4];
+        uint32_t svw[NJD], bvw[NJD];
+        float hsv[NJD][kTBv];
+#pragma unroll
+        for (int j = 0; j < NJD; ++j) {
+          wq[j] = reinterpret_cast<const uint4*>(sl + (size_t)j * 1024)[lane];
+          svw[j] = reinterpret_cast<const uint32_t*>(sl + (size_t)NJD * 1024 + (size_t)j * 256)[lane];
+          bvw[j] = reinterpret_cast<const uint32_t*>(sl + (size_t)NJD * 1280 + (size_t)j * 256)[lane];
+          const size_t fo = (((size_t)aq * NJD + j) * 4 + g) * 8 + apart * 4;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) av4[j][i] = STAGED ? hfl[fo + i] : ldg16(hfrag + fo + i);
+#pragma unroll
+          for (int r = 0; r < kTBv; ++r) hsv[j][r] = s.hsum[qr[r]][2 * j + my_half];
+        }
+        float acc[kTBv] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NJD; ++j) {
+          ss_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            ss_u32x4 av = as_v(av4[j][i]);
+            if (!am) av = ss_u32x4{0u, 0u, 0u, 0u};
+            const uint32_t wd = i == 0 ? wq[j].x : i == 1 ? wq[j].y : i == 2 ? wq[j].z : wq[j].w;
+            d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
+          }
+          const float sf = pick_half(svw[j], my_half);
+          const float bf = pick_half(bvw[j], my_half);
+          const float s16 = sf * kNibbleScale;
+          const float bp = my_part ? 0.f : __builtin_fmaf(-kNibbleScale, sf, bf);
+#pragma unroll
+          for (int r = 0; r < kTBv; ++r) {
+            acc[r] = __builtin_fmaf(s16, d[r], acc[r]);
+            acc[r] = __builtin_fmaf(bp, vr[r] ? hsv[j][r] : 0.f, acc[r]);
+          }
+        }
+#pragma unroll
+        for (int r = 0; r < kTBv; ++r) {
+          acc[r] = acc[r] + ss_shfl_xor(acc[r], 16);
+          acc[r] = acc[r] + ss_shfl_xor(acc[r], 32);
+          if (g == 0) partl[((size_t)u * 16 + n) * kTBv + r] = acc[r];
+        }
+      };
+      if (D.stage_h) {
+#pragma unroll 1
+        for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::true_type{});
+      } else {
+#pragma unroll 1
+        for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::false_type{});
+      }
+    }
+    SS_TRACE(10);
+    if (verify) {
+      // Shared-expert down rows 16b + 4w + rr in the dense_rows order; hs = bf16(bf16(silu(g)) * u).
+      const int Is = a.Is;
+      float sacc[4][kTBv];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+        for (int t = 0; t < kTBv; ++t) sacc[rr][t] = 0.f;
+      if (8 * lane < Is) {
+#pragma unroll 1
+        for (int t = 0; t < nt; ++t) {
+          const uint4 gq = reinterpret_cast<const uint4*>(gsh + (size_t)t * Is)[lane];
+          const uint4 uq = reinterpret_cast<const uint4*>(ush + (size_t)t * Is)[lane];
+          const uint32_t gw4[4] = {gq.x, gq.y, gq.z, gq.w}, uw4[4] = {uq.x, uq.y, uq.z, uq.w};
+          float hsv[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float gv = (e & 1) ? bf_hi(gw4[e >> 1]) : bf_lo(gw4[e >> 1]);
+            const float uv = (e & 1) ? bf_hi(uw4[e >> 1]) : bf_lo(uw4[e >> 1]);
+            const float sv = ss_round_bf16(gv / (1.f + ss_expf(-gv)));
+            hsv[e] = ss_round_bf16(sv * uv);
+          }
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const uint32_t ww[4] = {shw[rr].x, shw[rr].y, shw[rr].z, shw[rr].w};
+            float ac = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ac = __builtin_fmaf(hsv[e], (e & 1) ? bf_hi(ww[e >> 1]) : bf_lo(ww[e >> 1]), ac);
+#pragma unroll
+            for (int q = 0; q < kTBv; ++q)
+              if (q == t) sacc[rr][q] = ac;
+          }
+        }
+      }
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+        for (int t = 0; t < kTBv; ++t) {
+          const float v = ss_wave_sum(sacc[rr][t]);
+          if (lane == 0) s.shv[4 * w + rr][t] = v;
+        }
+    }
+    __syncthreads();
+    if (tid < 16 * kTBv) {
+      const int c = tid >> 2, r = tid & 3;
+      if (r < nt) {
+        float acc = 0.f;
+#pragma unroll 1
+        for (int k = 0; k < K; ++k) {
+          const int q = r * K + k, u = s.use_u[q];
+          float o = 0.f;
+          if (u >= 0) o = partl[((size_t)u * 16 + c) * kTBv + r] * s.wts[q];
+          if (a.o_buf) a.o_buf[((size_t)r * K + k) * H + 16 * bid + c] = o;
+          acc = k == 0 ? o : acc + o;
+        }
+        if (a.out) a.out[(size_t)r * H + 16 * bid + c] = acc;
+        if (verify) {
+          const float shb = ss_round_bf16(s.shv[c][r]);
+          const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-ss_bf16_to_f32(sgl[r]))));
+          const float sh2 = ss_round_bf16(sgv * shb);
+          a.y[(size_t)r * H + 16 * bid + c] = (uint16_t)ss_f32_to_bf16(ss_round_bf16(acc) + sh2);
+        }
+      }
+    }
+  }
+
+  // ------------------------------------------------------------ exit: the last workgroup resets the counters
+  __syncthreads();
+  SS_TRACE(11);
+  if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + 13] = __builtin_amdgcn_s_memtime();
+#undef SS_TRACE
+  if (tid == 0) {
+    const int ticket = __hip_atomic_fetch_add(ctr + CTR_EXIT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (ticket == G - 1) {
+      __hip_atomic_store(ctr + CTR_ROUTER, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctr + CTR_SHARED, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctr + CTR_ITEMS, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctr + CTR_EXIT, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
+template <int NJG, int NJD, bool XF32>
+static hipError_t launch_nj(const VerifyArgs& a, hipStream_t st) {
+  const SsRecord rec = ss_record_layout(a.H, a.I);
+  auto kern = verify_kernel<NJG, NJD, XF32>;
+  const DLayout dly = dlayout(a.T, a.H, a.I, a.K, a.E, XF32 ? 1 : 0, a.mode == 0 ? 1 : 0);
+  static size_t lds_set = 0, lds_static = 0;
+  static int grid = 0;
+  if (lds_set == 0) {
+    hipFuncAttributes attr;
+    hipError_t e = hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(kern));
+    if (e != hipSuccess) return e;
+    lds_static = attr.sharedSizeBytes;
+    e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern), hipFuncAttributeMaxDynamicSharedMemorySize,
+                            (int)kLdsBudget);
+    if (e != hipSuccess) return e;
+    lds_set = kLdsBudget;
+  }
+  // A workgroup may hold at most 160 KB of LDS on gfx950; refuse any shape whose layout would exceed it.
+  if (dly.P < 1 || dly.total > kLdsBudget || lds_static + dly.total > 160 * 1024) return hipErrorInvalidConfiguration;
+  if (grid == 0) {
+    int dev = 0, cus = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return e;
+    grid = cus;
+  }
+  if (grid < a.H / 16) return hipErrorInvalidConfiguration;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), dly.total, st, a, rec);
+  return hipGetLastError();
+}
+
+template <int NJG, int NJD>
+static hipError_t launch_x(const VerifyArgs& a, hipStream_t st) {
+  return a.x_f32 ? launch_nj<NJG, NJD, true>(a, st) : launch_nj<NJG, NJD, false>(a, st);
+}
+
+hipError_t launch_verify(const VerifyArgs& a, hipStream_t st) {
+  // Shapes with instantiated kernels: H in {1024, 2048, 2560, 4096} x I in {128, 256, 512, 640, 1024}.
+  const int njg = a.H / 128, njd = a.I / 128;
+#define SS_CASE(G_, D_) \
+  if (njg == G_ && njd == D_) return launch_x<G_, D_>(a, st);
+#define SS_ROW(G_) SS_CASE(G_, 1) SS_CASE(G_, 2) SS_CASE(G_, 4) SS_CASE(G_, 5) SS_CASE(G_, 8)
+  SS_ROW(8)
+  SS_ROW(16)
+  SS_ROW(20)
+  SS_ROW(32)
+#undef SS_ROW
+#undef SS_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ss

@@ -1,0 +1,333 @@
+// extern "C" entry points of libssmoe.so (declared in include/ssmoe.h): argument checks, workspace carving and
+// launches. No entry point allocates device memory or synchronises, except ssmoe_device_error.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/ssmoe.h"
+#include "ss_common.hpp"
+#include "ss_launch.hpp"
+
+// Per-device status word raised by kernels on bad input.
+__device__ int ss_status_storage;
+
+// Scratch of ssmoe_moe_decode, which (like the reference's moe_decode) takes no workspace argument: h fragments,
+// h partial sums and the persistent kernel's counters for one block of <= 4 rows. Zero at load; every launch leaves
+// its counters zero. Calls that overlap on one device share it and race.
+constexpr size_t kDecodeScratch = 320 * 1024;
+__device__ __align__(256) unsigned char ss_decode_scratch[kDecodeScratch];
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int ok() {
+  g_err.clear();
+  return SSMOE_OK;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(SSMOE_EHIP, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+constexpr int kMaxDevices = 64;
+int* g_status[kMaxDevices] = {nullptr};
+void* g_decode_scratch[kMaxDevices] = {nullptr};
+
+int current_device(int* dev) {
+  hipError_t e = hipGetDevice(dev);
+  if (e != hipSuccess) return hip_check(e, "hipGetDevice");
+  if (*dev < 0 || *dev >= kMaxDevices) return fail(SSMOE_EHIP, "device %d out of range", *dev);
+  return ok();
+}
+
+// Device addresses of the status word and the decode scratch on the current device (looked up once per device).
+int status_ptr(int** out) {
+  int dev = 0;
+  if (int rc = current_device(&dev)) return rc;
+  if (!g_status[dev]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(ss_status_storage));
+    if (e != hipSuccess) return hip_check(e, "hipGetSymbolAddress(status)");
+    g_status[dev] = static_cast<int*>(p);
+  }
+  *out = g_status[dev];
+  return ok();
+}
+
+int decode_scratch_ptr(void** out) {
+  int dev = 0;
+  if (int rc = current_device(&dev)) return rc;
+  if (!g_decode_scratch[dev]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(ss_decode_scratch));
+    if (e != hipSuccess) return hip_check(e, "hipGetSymbolAddress(decode scratch)");
+    g_decode_scratch[dev] = p;
+  }
+  *out = g_decode_scratch[dev];
+  return ok();
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+int check_moe_shape(int R, int H, int I, int K, int E) {
+  if (R < 1) return fail(SSMOE_EINVAL, "R must be >= 1, got %d", R);
+  if (H < 128 || H % 128 || H > 4096) return fail(SSMOE_EINVAL, "H must be a multiple of 128 in [128, 4096], got %d", H);
+  if (I < 128 || I % 128 || I > 1024) return fail(SSMOE_EINVAL, "I must be a multiple of 128 in [128, 1024], got %d", I);
+  if (K < 1 || K > 16) return fail(SSMOE_EINVAL, "K must be in [1, 16], got %d", K);
+  if (E < 1) return fail(SSMOE_EINVAL, "E must be >= 1, got %d", E);
+  return ok();
+}
+
+constexpr int kBlock = 4;  // rows per persistent launch
+uint64_t* g_trace = nullptr;  // diagnostics: phase timestamps of the persistent kernel (ssmoe_set_trace)
+
+}  // namespace
+
+extern "C" {
+
+const char* ssmoe_last_error(void) { return g_err.c_str(); }
+
+int ssmoe_version(void) { return 1; }
+
+int ssmoe_device_error(int* flags, int clear) {
+  if (!flags) return fail(SSMOE_EINVAL, "flags must be a host pointer");
+  int* p = nullptr;
+  if (int rc = status_ptr(&p)) return rc;
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return hip_check(e, "hipDeviceSynchronize");
+  e = hipMemcpy(flags, p, sizeof(int), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return hip_check(e, "hipMemcpy(status)");
+  if (clear) {
+    const int zero = 0;
+    e = hipMemcpy(p, &zero, sizeof(int), hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_check(e, "hipMemcpy(status clear)");
+  }
+  return ok();
+}
+
+int ssmoe_set_trace(void* buf, int64_t entries) {
+  if (buf && entries < 1024 * 16) return fail(SSMOE_EINVAL, "trace buffer needs >= %d entries", 1024 * 16);
+  g_trace = static_cast<uint64_t*>(buf);
+  return ok();
+}
+
+int ssmoe_record_layout(int H, int I, int64_t* off) {
+  if (!off) return fail(SSMOE_EINVAL, "off must be a host pointer to 10 int64");
+  if (H < 64 || H % 64 || I < 64 || I % 64) return fail(SSMOE_EINVAL, "H and I must be positive multiples of 64");
+  const SsRecord r = ss_record_layout(H, I);
+  const int64_t v[10] = {r.gw, r.gs, r.gb, r.uw, r.us, r.ub, r.dw, r.ds, r.db, r.bytes};
+  for (int i = 0; i < 10; ++i) off[i] = v[i];
+  return ok();
+}
+
+int ssmoe_moe_decode(const void* x, int x_is_f32, const int32_t* expert_ids, const float* weights, int layer,
+                     const int32_t* map, int64_t map_len, const int64_t* slot_ptr, int64_t n_slots, float* h_buf,
+                     float* o_buf, float* out, int R, int H, int I, int K, int E, void* stream) {
+  if (int rc = check_moe_shape(R, H, I, K, E)) return rc;
+  if (!x || !expert_ids || !weights || !map || !slot_ptr || !h_buf || !out)
+    return fail(SSMOE_EINVAL, "x, expert_ids, weights, map, slot_ptr, h_buf and out must be non-null");
+  if (layer < 0) return fail(SSMOE_EINVAL, "layer must be >= 0, got %d", layer);
+  if (!aligned(x, 16) || !aligned(h_buf, 16)) return fail(SSMOE_EINVAL, "x and h_buf must be 16-byte aligned");
+  if ((int64_t)(layer + 1) * E > map_len)
+    return fail(SSMOE_EINVAL, "map holds %lld entries, layer %d needs %lld", (long long)map_len, layer,
+                (long long)(layer + 1) * E);
+  if (ss::verify_scratch_bytes(kBlock, H, I, 0, K, 0) > kDecodeScratch)
+    return fail(SSMOE_EINVAL, "shape needs more decode scratch than the library holds");
+  int* err = nullptr;
+  void* scratch = nullptr;
+  if (int rc = status_ptr(&err)) return rc;
+  if (int rc = decode_scratch_ptr(&scratch)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const size_t xsz = x_is_f32 ? 4 : 2;
+  for (int r0 = 0; r0 < R; r0 += kBlock) {
+    ss::VerifyArgs a{};
+    a.mode = 1;
+    a.x = static_cast<const char*>(x) + (size_t)r0 * H * xsz;
+    a.x_f32 = x_is_f32 ? 1 : 0;
+    a.map = map;
+    a.map_len = map_len;
+    a.slot_ptr = slot_ptr;
+    a.n_slots = n_slots;
+    a.map_base = (int64_t)layer * E;
+    a.ids_in = expert_ids + (size_t)r0 * K;
+    a.w_in = weights + (size_t)r0 * K;
+    a.out = out + (size_t)r0 * H;
+    a.h_buf = h_buf + (size_t)r0 * K * I;
+    a.o_buf = o_buf ? o_buf + (size_t)r0 * K * H : nullptr;
+    a.scratch = scratch;
+    a.T = R - r0 < kBlock ? R - r0 : kBlock;
+    a.H = H;
+    a.I = I;
+    a.Is = 0;
+    a.K = K;
+    a.E = E;
+    a.err = err;
+    a.trace = g_trace;
+    if (int rc = hip_check(ss::launch_verify(a, st), "moe_decode launch")) return rc;
+  }
+  return ok();
+}
+
+int ssmoe_topk_stable(const float* scores, const int32_t* n_valid, int32_t* out_idx, float* out_val, int R, int N,
+                      int k, void* stream) {
+  if (R < 1 || N < 1 || N > 65536) return fail(SSMOE_EINVAL, "need R >= 1 and 1 <= N <= 65536 (R=%d N=%d)", R, N);
+  if (k < 1 || k > N) return fail(SSMOE_EINVAL, "need 1 <= k <= N, got k=%d N=%d", k, N);
+  if (!scores || !out_idx) return fail(SSMOE_EINVAL, "scores and out_idx must be non-null");
+  return hip_check(ss::launch_topk_stable(scores, n_valid, out_idx, out_val, R, N, k, static_cast<hipStream_t>(stream)),
+                   "topk_stable launch");
+}
+
+int ssmoe_dense_gemv_bf16(const uint16_t* x, const uint16_t* w, uint16_t* out, int T, int H, int N, void* stream) {
+  if (T < 1 || N < 1 || H < 8 || H % 8 || H > 8192)
+    return fail(SSMOE_EINVAL, "need T, N >= 1 and H a multiple of 8 in [8, 8192] (T=%d H=%d N=%d)", T, H, N);
+  if (!x || !w || !out) return fail(SSMOE_EINVAL, "x, w and out must be non-null");
+  if (!aligned(x, 16) || !aligned(w, 16)) return fail(SSMOE_EINVAL, "x and w must be 16-byte aligned");
+  ss::DenseSeg s{w, out, N, N};
+  return hip_check(ss::launch_dense_rows(x, T, H, &s, 1, static_cast<hipStream_t>(stream)), "dense gemv launch");
+}
+
+int ssmoe_router(const uint16_t* x, const uint16_t* router_w, const float* bias, uint16_t* logits, float* probs,
+                 int32_t* ids, float* weights, int T, int H, int E, int K, void* stream) {
+  if (T < 1 || H < 8 || H % 8 || H > 8192) return fail(SSMOE_EINVAL, "need T >= 1, H a multiple of 8 <= 8192");
+  if (E < 1 || E > 8192 || K < 1 || K > 16 || K > E) return fail(SSMOE_EINVAL, "need 1 <= K <= min(16, E), E <= 8192");
+  if (!x || !router_w || !logits || !ids || !weights)
+    return fail(SSMOE_EINVAL, "x, router_w, logits, ids and weights must be non-null");
+  if (!aligned(x, 16) || !aligned(router_w, 16)) return fail(SSMOE_EINVAL, "x and router_w must be 16-byte aligned");
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  ss::DenseSeg s{router_w, logits, E, E};
+  if (int rc = hip_check(ss::launch_dense_rows(x, T, H, &s, 1, st), "router gemv launch")) return rc;
+  return hip_check(ss::launch_router_topk(logits, bias, probs, ids, weights, T, E, K, st), "router topk launch");
+}
+
+int64_t ssmoe_verify_workspace_bytes(int T, int H, int I, int Is, int K, int E) {
+  if (T < 1 || Is < 1 || I < 1 || K < 1 || E < 1) return -1;
+  (void)T;
+  return (int64_t)ss::verify_scratch_bytes(kBlock, H, I, Is, K, E);
+}
+
+int ssmoe_moe_verify_layer(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
+                           const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
+                           const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,
+                           const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes,
+                           int32_t* ids, float* weights, uint16_t* y, float* routed_out, int T, int H, int I, int Is,
+                           int K, int E, void* stream) {
+  if (int rc = check_moe_shape(T, H, I, K, E)) return rc;
+  if (E > 512 || K > E) return fail(SSMOE_EINVAL, "need K <= E <= 512, got K=%d E=%d", K, E);
+  if (Is < 8 || Is % 8 || Is > 512) return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, 512], got %d", Is);
+  if (!x || !router_w || !sh_gate || !sh_up || !sh_down || !sh_g || !map || !slot_ptr || !workspace || !ids ||
+      !weights || !y)
+    return fail(SSMOE_EINVAL, "every pointer except router_bias and routed_out must be non-null");
+  if (!aligned(x, 16) || !aligned(router_w, 16) || !aligned(sh_gate, 16) || !aligned(sh_up, 16) ||
+      !aligned(sh_down, 16) || !aligned(sh_g, 16) || !aligned(workspace, 256))
+    return fail(SSMOE_EINVAL, "x and weights must be 16-byte aligned, workspace 256-byte aligned");
+  if (layer < 0 || (int64_t)(layer + 1) * E > map_len)
+    return fail(SSMOE_EINVAL, "map holds %lld entries, layer %d needs %lld", (long long)map_len, layer,
+                (long long)(layer + 1) * E);
+  const size_t need = ss::verify_scratch_bytes(kBlock, H, I, Is, K, E);
+  if (workspace_bytes < (int64_t)need)
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes, (long long)need);
+  int* err = nullptr;
+  if (int rc = status_ptr(&err)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  for (int r0 = 0; r0 < T; r0 += kBlock) {
+    ss::VerifyArgs a{};
+    a.mode = 0;
+    a.x = x + (size_t)r0 * H;
+    a.router_w = router_w;
+    a.bias = router_bias;
+    a.sh_gate = sh_gate;
+    a.sh_up = sh_up;
+    a.sh_down = sh_down;
+    a.sh_g = sh_g;
+    a.map = map;
+    a.map_len = map_len;
+    a.slot_ptr = slot_ptr;
+    a.n_slots = n_slots;
+    a.map_base = (int64_t)layer * E;
+    a.ids_out = ids + (size_t)r0 * K;
+    a.w_out = weights + (size_t)r0 * K;
+    a.y = y + (size_t)r0 * H;
+    a.out = routed_out ? routed_out + (size_t)r0 * H : nullptr;
+    a.scratch = workspace;
+    a.T = T - r0 < kBlock ? T - r0 : kBlock;
+    a.H = H;
+    a.I = I;
+    a.Is = Is;
+    a.K = K;
+    a.E = E;
+    a.err = err;
+    a.trace = g_trace;
+    if (int rc = hip_check(ss::launch_verify(a, st), "verify layer launch")) return rc;
+  }
+  return ok();
+}
+
+int64_t ssmoe_accept_workspace_bytes(int D, int V) {
+  if (D < 0 || V < 1) return -1;
+  return ss::accept_work_floats(D, V) * 4;
+}
+
+static int check_accept(int D, int V, void* workspace, int64_t workspace_bytes, int32_t* out) {
+  if (D < 0 || D > 60) return fail(SSMOE_EINVAL, "D must be in [0, 60], got %d", D);
+  if (V < 1) return fail(SSMOE_EINVAL, "V must be >= 1, got %d", V);
+  if (!workspace || !out) return fail(SSMOE_EINVAL, "workspace and out must be non-null");
+  if (workspace_bytes < ss::accept_work_floats(D, V) * 4)
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)(ss::accept_work_floats(D, V) * 4));
+  return ok();
+}
+
+int ssmoe_accept_greedy(const float* target, const int32_t* drafts, int D, int V, void* workspace,
+                        int64_t workspace_bytes, int32_t* out, void* stream) {
+  if (int rc = check_accept(D, V, workspace, workspace_bytes, out)) return rc;
+  if (!target || (D > 0 && !drafts)) return fail(SSMOE_EINVAL, "target and drafts must be non-null");
+  ss::AcceptArgs a{};
+  a.target = target;
+  a.drafts = drafts;
+  a.D = D;
+  a.V = V;
+  a.out = out;
+  a.work = static_cast<float*>(workspace);
+  return hip_check(ss::launch_accept_greedy(a, static_cast<hipStream_t>(stream)), "accept greedy launch");
+}
+
+int ssmoe_accept_pq(const float* target, const float* draft, const int32_t* drafts, const float* uniforms, int D,
+                    int V, float temperature, void* workspace, int64_t workspace_bytes, int32_t* out,
+                    void* stream) {
+  if (int rc = check_accept(D, V, workspace, workspace_bytes, out)) return rc;
+  if (!target || !uniforms || (D > 0 && (!draft || !drafts)))
+    return fail(SSMOE_EINVAL, "target, draft, drafts and uniforms must be non-null");
+  if (!(temperature > 0.f) || temperature != temperature)
+    return fail(SSMOE_EINVAL, "temperature must be > 0, got %g", (double)temperature);
+  int* err = nullptr;
+  if (int rc = status_ptr(&err)) return rc;
+  ss::AcceptArgs a{};
+  a.target = target;
+  a.draft = draft;
+  a.drafts = drafts;
+  a.uniforms = uniforms;
+  a.D = D;
+  a.V = V;
+  a.temperature = temperature;
+  a.out = out;
+  a.work = static_cast<float*>(workspace);
+  a.err = err;
+  return hip_check(ss::launch_accept_pq(a, static_cast<hipStream_t>(stream)), "accept pq launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,55 @@
+"""Seeded synthetic inputs of the BASELINE configurations (random-init weights; there is no checkpoint).
+
+Distributions: activations bf16 N(0, 1); router gate bf16 N(0, 0.02) [E, H]; shared
+expert gate/up [Is, H], down [H, Is] and shared_expert_gate [1, H] bf16 N(0, 0.02); expert records as in
+SlotPool.fill_random. Routing skew: Zipf(s) popularity over a seeded permutation of the experts, realised as an
+fp32 bias ln p_rank(e) added to the router logits. Verify logits: target N(0, 3) fp32, draft = rho * target +
+sqrt(1 - rho^2) * N(0, 3).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    return torch.Generator(device=torch.device(device)).manual_seed(seed)
+
+
+def normal_bf16(shape, std: float, seed: int, device="cuda") -> torch.Tensor:
+    g = _gen(seed, device)
+    return (torch.randn(shape, generator=g, device=device) * std).to(torch.bfloat16)
+
+
+def zipf_bias(experts: int, s: float = 1.1, seed: int = 1731, device="cuda") -> torch.Tensor:
+    """bias[e] = ln p_rank(e), p_r proportional to r^-s (r = 1..E) over a seeded permutation of the experts."""
+    g = torch.Generator().manual_seed(seed)
+    perm = torch.randperm(experts, generator=g)
+    r = torch.arange(1, experts + 1, dtype=torch.float64)
+    logp = -s * torch.log(r) - math.log(float((r ** -s).sum()))
+    bias = torch.empty(experts, dtype=torch.float64)
+    bias[perm] = logp
+    return bias.to(torch.float32).to(device)
+
+
+class LayerWeights:
+    """Router and shared-expert weights of one synthetic MoE layer."""
+
+    def __init__(self, hidden: int, experts: int, shared_inter: int, seed: int, device="cuda"):
+        self.router_w = normal_bf16((experts, hidden), 0.02, seed * 8 + 1, device)
+        self.sh_gate = normal_bf16((shared_inter, hidden), 0.02, seed * 8 + 2, device)
+        self.sh_up = normal_bf16((shared_inter, hidden), 0.02, seed * 8 + 3, device)
+        self.sh_down = normal_bf16((hidden, shared_inter), 0.02, seed * 8 + 4, device)
+        self.sh_g = normal_bf16((1, hidden), 0.02, seed * 8 + 5, device)
+
+    def nbytes(self) -> int:
+        return sum(t.numel() * 2 for t in (self.router_w, self.sh_gate, self.sh_up, self.sh_down, self.sh_g))
+
+
+def verify_logits(depth: int, vocab: int, seed: int, rho: float = 0.8, std: float = 3.0, device="cuda"):
+    """(target fp32 [depth+1, vocab], draft fp32 [depth, vocab]) with draft rows correlated rho to the target."""
+    g = _gen(seed, device)
+    z = torch.randn((depth + 1, vocab), generator=g, device=device) * std
+    n = torch.randn((depth, vocab), generator=g, device=device) * std
+    return z, rho * z[:depth] + math.sqrt(1.0 - rho * rho) * n
