@@ -4,8 +4,8 @@ Mirrors the MoE segment of the reference verify graph, GraphSet._moe + Segments.
 (slotstream_spark/runtime/graphs.py:160-178, model/layers.py:336-348): router logits, softmax, stable top-k and
 renormalisation, the routed experts (moe_decode), the shared expert gated by sigmoid(shared_expert_gate x), and
 y = routed.to(bf16) + shared, with the reference's bf16 rounding of every shared-expert projection. The whole layer
-is 4 launches on the caller's stream (dense rows, router tail, gate/up, down+combine) with no host sync, so a
-step over many layers can be captured in one HIP graph.
+is one persistent launch per block of up to 4 tokens on the caller's stream (csrc/ss_verify.hip) with no host
+sync, so a step over many layers can be captured in one HIP graph.
 """
 from __future__ import annotations
 

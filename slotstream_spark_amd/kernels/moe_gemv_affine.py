@@ -7,9 +7,10 @@ down.s down.b). h_buf receives h = silu(Wg x) * (Wu x), o_buf the weighted exper
 router-rank-order sum; no atomics, so a T-row call equals T one-row calls bit for bit and moving a record between
 slots changes no bit (moe_gemv_affine.py:1-13).
 
-The kernels (csrc/ss_moe.hip) stream each weight row with 16-byte loads, turn nibbles into bf16 (128 + q) in
-registers and run bf16 MFMA 16x16x32 with per-group scale/bias applied to fp32 partials; there are no tunable
-tiles, so `cfg` is validated like the reference's and otherwise ignored.
+The persistent kernel (csrc/ss_verify.hip, decode mode) streams each weight row with 16-byte loads, turns nibbles
+into bf16 1 + q/16 in registers and runs bf16 MFMA 16x16x32 with the per-group scale and bias applied to the fp32
+partials (w x = 16 s (sum (1 + q/16) x) + (b - 16 s) sum x); there are no tunable tiles, so `cfg` is validated like
+the reference's and otherwise ignored.
 """
 from __future__ import annotations
 

@@ -1,0 +1,153 @@
+"""The C ABI without a GPU: libssmoe.so loads, exports exactly what include/ssmoe.h declares, computes its host-side
+answers (record layout, workspace sizes) and rejects bad arguments with SSMOE_EINVAL before touching a device.
+The Python mirrors raise the reference's ValueErrors and refuse CPU tensors instead of falling back."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from slotstream_spark_amd import _lib
+from slotstream_spark_amd.kernels import moe_gemv_affine as mga
+from slotstream_spark_amd.kernels.topk_stable import topk_stable
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "ssmoe.h"
+EINVAL = 1
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ssmoe_\w+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def L():
+    if not _lib.LIB_PATH.exists():
+        pytest.skip("libssmoe.so not built (python -m slotstream_spark_amd.build)")
+    return _lib.lib()
+
+
+def test_exports_every_declared_symbol(L):
+    names = _declared()
+    assert len(names) >= 14
+    for n in names:
+        assert hasattr(L, n), n
+    assert sorted(_lib.SIGNATURES) == names  # the ctypes table binds exactly the header's list
+
+
+def test_version_and_error_text(L):
+    assert L.ssmoe_version() == _lib.ABI_VERSION
+    assert L.ssmoe_record_layout(100, 512, (ctypes.c_int64 * 10)()) == EINVAL
+    assert b"multiples of 64" in L.ssmoe_last_error()
+
+
+def test_record_layout(L):
+    offs, total = _lib.record_layout(2048, 512)
+    assert offs == [0, 524288, 557056, 589824, 1114112, 1146880, 1179648, 1703936, 1736704]
+    assert total == 1769472
+    offs, total = _lib.record_layout(2560, 640)  # the reference constants (moe_gemv_affine.py:22-25)
+    assert offs == [0, 819200, 870400, 921600, 1740800, 1792000, 1843200, 2662400, 2713600]
+    assert total == 2764800
+    assert mga.RECORD_BYTES == 1769472 and mga.O_DOWN_B == 1736704
+    assert L.ssmoe_record_layout(2048, 512, None) == EINVAL
+
+
+def test_workspace_sizes(L):
+    assert L.ssmoe_verify_workspace_bytes(2, 2048, 512, 512, 10, 512) > 0
+    assert L.ssmoe_verify_workspace_bytes(0, 2048, 512, 512, 10, 512) == -1
+    assert L.ssmoe_accept_workspace_bytes(3, 151936) >= 4 * ((151936 + 1023) // 1024)
+    assert L.ssmoe_accept_workspace_bytes(-1, 10) == -1
+
+
+def test_trace_switch(L):
+    assert L.ssmoe_set_trace(None, 0) == 0
+    assert L.ssmoe_set_trace(ctypes.c_void_p(256), 10) == EINVAL
+
+
+NONNULL = ctypes.c_void_p(4096)  # aligned dummy address; never dereferenced on an EINVAL path
+
+
+@pytest.mark.parametrize("R,H,I,K,E,msg", [
+    (0, 2048, 512, 10, 512, b"R must be"),
+    (2, 2000, 512, 10, 512, b"H must be"),
+    (2, 2048, 500, 10, 512, b"I must be"),
+    (2, 2048, 512, 17, 512, b"K must be"),
+])
+def test_moe_decode_rejects_shapes(L, R, H, I, K, E, msg):
+    p = NONNULL
+    rc = L.ssmoe_moe_decode(p, 0, p, p, 0, p, 512, p, 512, p, p, p, R, H, I, K, E, None)
+    assert rc == EINVAL and msg in L.ssmoe_last_error()
+
+
+def test_moe_decode_rejects_tables(L):
+    p = NONNULL
+    assert L.ssmoe_moe_decode(None, 0, p, p, 0, p, 512, p, 512, p, p, p, 2, 2048, 512, 10, 512, None) == EINVAL
+    assert L.ssmoe_moe_decode(p, 0, p, p, 1, p, 512, p, 512, p, p, p, 2, 2048, 512, 10, 512, None) == EINVAL
+    assert b"map holds 512 entries" in L.ssmoe_last_error()
+    assert L.ssmoe_moe_decode(ctypes.c_void_p(4100), 0, p, p, 0, p, 512, p, 512, p, p, p, 2, 2048, 512, 10, 512,
+                              None) == EINVAL
+
+
+def test_verify_layer_rejects(L):
+    p = NONNULL
+    args = lambda E, Is, ws: (p, p, None, p, p, p, p, 0, p, E, p, E, p, ws, p, p, p, None, 2, 2048, 512, Is, 10, E,
+                              None)
+    need = L.ssmoe_verify_workspace_bytes(2, 2048, 512, 512, 10, 512)
+    assert L.ssmoe_moe_verify_layer(*args(1024, 512, need)) == EINVAL
+    assert L.ssmoe_moe_verify_layer(*args(512, 500, need)) == EINVAL
+    assert L.ssmoe_moe_verify_layer(*args(512, 512, need - 1)) == EINVAL
+    assert b"workspace holds" in L.ssmoe_last_error()
+
+
+def test_topk_router_accept_reject(L):
+    p = NONNULL
+    assert L.ssmoe_topk_stable(p, None, p, None, 1, 70000, 10, None) == EINVAL
+    assert L.ssmoe_topk_stable(p, None, p, None, 1, 64, 65, None) == EINVAL
+    assert L.ssmoe_router(p, p, None, p, None, p, p, 1, 2048, 512, 17, None) == EINVAL
+    assert L.ssmoe_dense_gemv_bf16(p, p, p, 1, 2047, 8, None) == EINVAL
+    ws = L.ssmoe_accept_workspace_bytes(3, 1000)
+    assert L.ssmoe_accept_greedy(p, p, 61, 1000, p, ws, p, None) == EINVAL
+    assert L.ssmoe_accept_greedy(p, p, 3, 1000, p, ws - 4, p, None) == EINVAL
+    assert L.ssmoe_accept_pq(p, p, p, p, 3, 1000, 0.0, p, ws, p, None) == EINVAL
+    assert b"temperature" in L.ssmoe_last_error()
+
+
+# ---------------------------------------------------------------- Python mirrors
+def _decode_args(R=2, H=256, I=128, K=4, E=8, dtype=torch.bfloat16):
+    return dict(x=torch.zeros(R, H, dtype=dtype), expert_ids=torch.zeros(R, K, dtype=torch.int32),
+                weights=torch.zeros(R, K), layer=0, map_t=torch.zeros(E, dtype=torch.int32),
+                slot_ptr_t=torch.zeros(E, dtype=torch.int64), h_buf=torch.zeros(R, K, I),
+                o_buf=torch.zeros(R, K, H), out=torch.zeros(R, H))
+
+
+@pytest.mark.parametrize("field,bad,msg", [
+    ("x", torch.zeros(2, 256, dtype=torch.float16), "x must be"),
+    ("expert_ids", torch.zeros(2, 4, dtype=torch.int64), "expert_ids must be"),
+    ("weights", torch.zeros(2, 3), "weights must be"),
+    ("map_t", torch.zeros(8, dtype=torch.int64), "map_t must be int32"),
+    ("o_buf", torch.zeros(2, 4, 255), "buffer must be"),
+    ("out", torch.zeros(2, 256, dtype=torch.float64), "buffer must be"),
+])
+def test_moe_decode_value_errors(field, bad, msg):
+    a = _decode_args()
+    a[field] = bad
+    with pytest.raises(ValueError, match=msg):
+        mga.moe_decode(**a)
+
+
+def test_moe_decode_refuses_cpu_tensors():
+    with pytest.raises(ValueError, match="same GPU"):
+        mga.moe_decode(**_decode_args())
+    with pytest.raises(ValueError, match="multiples of 64"):
+        mga.moe_decode(**_decode_args(), cfg={"bk": 96})
+
+
+def test_topk_value_errors():
+    with pytest.raises(ValueError):
+        topk_stable(torch.zeros(2, 8, dtype=torch.float64), 2)
+    with pytest.raises(ValueError):
+        topk_stable(torch.zeros(2, 8), 9)
+    with pytest.raises(ValueError, match="GPU"):
+        topk_stable(torch.zeros(2, 8), 2)
