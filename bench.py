@@ -7,10 +7,13 @@ per layer behind a random slot permutation), captured as one HIP graph. Every la
 (no attention between layers), so the layers differ only in weights and routing; with 16 layers the touched bytes
 (about 44 MB per layer) exceed the 256 MB Infinity Cache, so each layer is read cold from HBM.
 
-Reported: value = microseconds per layer step (lower is better); the roofline of the dominant kernel pair
-(moe_decode: routed gate/up + down, timed with HIP events in its own graph of `--layers` launches on the same
-inputs); and the CPU baseline, the torch-CPU restatement of the reference's moe_ref (oracle.moe_ref) on the same
-layer, timed on this host.
+Reported: value = microseconds per layer step (lower is better). The dominant kernel is the persistent verify
+kernel (one launch per layer), so `roofline` is its algorithmic bytes per launch (the measured unique-expert count
+of each layer) over its average launch time, both from the same HIP-event-timed graph replays. Also reported: the
+routed-only moe_decode launch on the same routing (`--legs` decode) and the CPU baseline, the torch-CPU
+restatement of the reference's moe_ref (oracle.moe_ref) on the same layer, timed on this host.
+`--copy-calib` first runs three 256 MiB device-to-device copies, the known-size kernel that scales rocprofv3's
+FETCH_SIZE / WRITE_SIZE counters into bytes.
 """
 from __future__ import annotations
 
@@ -36,6 +39,16 @@ def log(msg):
 def layer_bytes(u: int, t: int) -> int:
     """Algorithmic HBM bytes of one verify layer."""
     return u * 1_769_472 + 2_097_152 + 6_291_456 + 4_096 + t * H * 4
+
+
+def traffic_of(kernel: str):
+    """HBM bytes per launch of `kernel` measured with rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a known-size copy),
+    as recorded in profiles/traffic.json next to the command that produced it; None when not measured."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    rec = json.loads(f.read_text()).get(kernel)
+    return None if rec is None else rec.get("bytes_per_launch")
 
 
 def cpu_baseline(layer_w, bias, pool, x, layer_idx, budget_s):
@@ -105,6 +118,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--legs", default="verify,decode", help="comma list of timed legs: verify, decode")
+    ap.add_argument("--copy-calib", action="store_true", help="run 3 x 256 MiB device copies first (PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one; the multi-GPU "
@@ -120,6 +135,15 @@ def main():
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    legs = set(args.legs.split(","))
+    if args.copy_calib:
+        a = torch.empty(256 << 20, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        del a, b
+        log("copy calibration: 3 x 268435456-byte device copies done")
     NL, T = args.layers, args.tokens
     log(f"allocating {NL} layers x {E} experts ({NL * E * 1_769_472 / 2**30:.1f} GiB of records)")
     pool = SlotPool(NL, E, H, I, device=dev)
@@ -165,35 +189,39 @@ def main():
     layer_gbs = bytes_step / (ms_step * 1e-3) / 1e9
     log(f"layer step {us_layer:.2f} us ({layer_gbs:.0f} GB/s algorithmic), unique experts {uniq}")
 
-    # Dominant kernel pair: moe_decode (routed gate/up + down) on the routing of the step, one graph of NL calls.
-    hb = [torch.empty((T, K, I), device=dev) for _ in range(NL)]
-    ob = [torch.empty((T, K, H), device=dev) for _ in range(NL)]
-    outb = [torch.empty((T, H), device=dev) for _ in range(NL)]
+    us_moe = moe_gbs = moe_bytes = None
+    if "decode" in legs:
+        # Routed experts only (moe_decode, decode mode of the same kernel) on the routing of the step, one graph of
+        # NL calls.
+        hb = [torch.empty((T, K, I), device=dev) for _ in range(NL)]
+        ob = [torch.empty((T, K, H), device=dev) for _ in range(NL)]
+        outb = [torch.empty((T, H), device=dev) for _ in range(NL)]
 
-    def routed():
-        for l in range(NL):
-            moe_decode(x, ids[l], wts[l], l, pool.map, pool.slot_ptr, hb[l], ob[l], outb[l], experts_per_layer=E)
+        def routed():
+            for l in range(NL):
+                moe_decode(x, ids[l], wts[l], l, pool.map, pool.slot_ptr, hb[l], ob[l], outb[l], experts_per_layer=E)
 
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        routed()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    g2 = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g2):
-        routed()
-    for _ in range(args.warmup):
-        g2.replay()
-    torch.cuda.synchronize()
-    ev0.record()
-    for _ in range(args.steps):
-        g2.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    us_moe = ev0.elapsed_time(ev1) * 1000.0 / (args.steps * NL)
-    moe_bytes = sum(u * 1_769_472 + T * H * 6 for u in uniq) / NL
-    moe_gbs = moe_bytes / (us_moe * 1e-6) / 1e9
-    log(f"moe_decode {us_moe:.2f} us per launch pair, {moe_gbs:.0f} GB/s algorithmic")
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            routed()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        g2 = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g2):
+            routed()
+        for _ in range(args.warmup):
+            g2.replay()
+        torch.cuda.synchronize()
+        ev0.record()
+        for _ in range(args.steps):
+            g2.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        us_moe = ev0.elapsed_time(ev1) * 1000.0 / (args.steps * NL)
+        moe_bytes = sum(u * 1_769_472 + T * H * 6 for u in uniq) / NL
+        moe_gbs = moe_bytes / (us_moe * 1e-6) / 1e9
+        log(f"moe_decode {us_moe:.2f} us per launch pair, {moe_gbs:.0f} GB/s algorithmic")
+
 
     cpu = None
     if not args.no_cpu:
@@ -220,12 +248,12 @@ def main():
                    "parallelism": "single GPU"},
         "hbm_gbs_layer": round(layer_gbs, 1),
         "tokens_per_s_layer": round(T / (us_layer * 1e-6), 1),
-        "roofline": {"bound": "hbm", "kernel": "moe_decode (routed gate/up + down+combine)",
-                     "achieved": round(moe_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(moe_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "us_per_launch": round(us_moe, 3), "bytes_per_launch": int(moe_bytes)},
-        "layer_roofline": {"bound": "hbm", "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                           "frac": round(layer_gbs / HBM_PEAK_GBS, 4)},
+        "roofline": {"bound": "hbm", "kernel": "verify_kernel (verify mode: router + routed + shared + combine)",
+                     "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of("verify_kernel"),
+                     "us_per_launch": round(us_layer, 3), "bytes_per_launch": int(bytes_step / NL)},
+        "moe_decode": None if us_moe is None else {
+            "us_per_launch": round(us_moe, 3), "bytes_per_launch": int(moe_bytes), "achieved_gbs": round(moe_gbs, 1)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -1,0 +1,34 @@
+"""Summaries of rocprofv3 result databases (rocpd SQLite), as committed under profiles/.
+
+  python -m slotstream_spark_amd.rocpd_summary kernels RUN_results.db        per-kernel calls / avg / min / max (us)
+  python -m slotstream_spark_amd.rocpd_summary counters RUN_results.db [pat]  per-kernel average of each counter
+"""
+from __future__ import annotations
+
+import sqlite3
+import sys
+
+
+def kernels(db: str) -> str:
+    c = sqlite3.connect(db)
+    rows = list(c.execute("""select name, count(*), avg(end - start), min(end - start), max(end - start),
+                                    sum(end - start) from kernels group by name order by sum(end - start) desc"""))
+    tot = sum(r[5] for r in rows) or 1
+    out = [f"{'kernel':70s} {'calls':>6s} {'avg_us':>9s} {'min_us':>9s} {'max_us':>9s} {'pct':>6s}"]
+    for n, cnt, avg, mn, mx, s in rows:
+        out.append(f"{n[:70]:70s} {cnt:6d} {avg / 1e3:9.2f} {mn / 1e3:9.2f} {mx / 1e3:9.2f} {100 * s / tot:6.1f}")
+    return "\n".join(out)
+
+
+def counters(db: str, pattern: str = "%") -> str:
+    c = sqlite3.connect(db)
+    rows = c.execute("""select kernel_name, counter_name, avg(value), min(value), max(value), count(*)
+                        from counters_collection where kernel_name like ? group by kernel_name, counter_name
+                        order by kernel_name""", (pattern,))
+    return "\n".join(f"{k[:60]:60s} {n:14s} avg {v:14.2f} min {lo:14.2f} max {hi:14.2f} ({cnt} dispatches)"
+                     for k, n, v, lo, hi, cnt in rows)
+
+
+if __name__ == "__main__":
+    what, db = sys.argv[1], sys.argv[2]
+    print(kernels(db) if what == "kernels" else counters(db, sys.argv[3] if len(sys.argv) > 3 else "%"))
