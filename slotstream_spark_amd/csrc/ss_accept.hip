@@ -62,29 +62,22 @@ __global__ __launch_bounds__(64) void greedy_chunk_kernel(const float* __restric
   const int nch = gridDim.x, rows = gridDim.y;
   Work k = work_of(work, rows, nch);
   const float* x = target + (size_t)row * V;
-  float best = -__builtin_inff();
-  int bi = 0x7FFFFFFF;
-  int bad = 0;
+  // (value, first index) as one 64-bit key: order-preserving value key (+-0 equal, as np.argmax compares) above
+  // the complemented index; a row holding a non-finite value is flagged and never decided on.
+  uint64_t bk = 0;
+  uint32_t bad = 0;
   for (int i = 0; i < kSub; ++i) {
     const int j = c * kChunk + i * 64 + lane;
     if (j >= V) break;
     const float v = x[j];
     bad |= !finite(v);
-    if (v > best || (v == best && j < bi)) {
-      best = v;
-      bi = j;
-    }
+    const uint64_t kv = ((uint64_t)ss_key(v == 0.f ? 0.f : v) << 32) | (0xFFFFFFFFu - (uint32_t)j);
+    bk = kv > bk ? kv : bk;
   }
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) {
-    const float ov = ss_shfl_xor(best, m);
-    const int oi = ss_shfl_xor_i(bi, m);
-    if (ov > best || (ov == best && oi < bi)) {
-      best = ov;
-      bi = oi;
-    }
-    bad |= ss_shfl_xor_i(bad, m);
-  }
+  bk = ss_wave_max_u64(bk);
+  bad = ss_wave_or(bad);
+  const int bi = (int)(0xFFFFFFFFu - (uint32_t)bk);
+  const float best = ss_unkey((uint32_t)(bk >> 32));
   if (lane == 0) {
     k.cmax[row * nch + c] = best;
     k.ctot[row * nch + c] = __int_as_float(bi);
@@ -164,8 +157,7 @@ __global__ __launch_bounds__(64) void pq_max_kernel(AcceptArgs a) {
     m = fmaxf(m, v / a.temperature);
   }
   m = ss_wave_max(m);
-#pragma unroll
-  for (int s = 32; s >= 1; s >>= 1) bad |= ss_shfl_xor_i(bad, s);
+  bad = (int)ss_wave_or((uint32_t)bad);
   if (lane == 0) {
     k.cmax[row * nch + c] = m;
     k.cbad[row * nch + c] = bad ? 1.f : 0.f;

@@ -41,10 +41,8 @@ SS_DEV uint32_t ss_pack_bf16(float lo, float hi) { return ss_f32_to_bf16(lo) | (
 // then the degree-7 Taylor polynomial of e^r on |r| <= ln2/2 in Horner form with fused multiply-adds
 // (truncation error < 6e-9 relative), then a scale by 2^n built from the exponent bits (two steps near
 // the subnormal range so only the last multiply rounds). The CPU restatement runs the same operations.
+// Written without branches (selects only): inside a wave every lane takes the same instructions.
 SS_DEV float ss_expf(float x) {
-  if (x != x) return x;
-  if (x > 88.72283935546875f) return __uint_as_float(0x7F800000u);
-  if (x < -103.97208404541015625f) return 0.0f;
   const float n = __builtin_rintf(x * 1.44269502162933349609375f);
   float r = __builtin_fmaf(-n, 0.693145751953125f, x);
   r = __builtin_fmaf(-n, 1.428606765330187045037746429443359375e-06f, r);
@@ -56,15 +54,15 @@ SS_DEV float ss_expf(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
-  int ni = (int)n;
-  if (ni > 127) {
-    p = p * 2.0f;
-    ni -= 1;
-  } else if (ni < -120) {
-    p = p * 5.42101086242752217003726400434970855712890625e-20f;  // 2^-64
-    ni += 64;
-  }
-  return p * __uint_as_float((uint32_t)(ni + 127) << 23);
+  // n is within [-150, 128] for every x the final selects keep; the clamp only keeps the conversion defined.
+  int ni = (int)__builtin_fminf(__builtin_fmaxf(n, -160.f), 160.f);
+  const bool big = ni > 127, tiny = ni < -120;
+  p = big ? p * 2.0f : (tiny ? p * 5.42101086242752217003726400434970855712890625e-20f : p);  // 2^-64
+  ni = big ? ni - 1 : (tiny ? ni + 64 : ni);
+  float y = p * __uint_as_float((uint32_t)(ni + 127) << 23);
+  y = x > 88.72283935546875f ? __uint_as_float(0x7F800000u) : y;
+  y = x < -103.97208404541015625f ? 0.0f : y;
+  return x != x ? x : y;
 }
 
 // ---------------------------------------------------------------- order-preserving keys
@@ -76,23 +74,113 @@ SS_DEV uint32_t ss_key(float f) {
   return (u & 0x80000000u) ? ~u : (u ^ 0x80000000u);
 }
 
-// ---------------------------------------------------------------- wave reductions (wave64)
-SS_DEV float ss_shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
-SS_DEV int ss_shfl_xor_i(int v, int m) { return __shfl_xor(v, m, 64); }
+// Inverse of ss_key for non-NaN values (key 0 maps back to a NaN).
+SS_DEV float ss_unkey(uint32_t k) { return __uint_as_float((k & 0x80000000u) ? (k ^ 0x80000000u) : ~k); }
 
-// Butterfly sum over the 64 lanes: lane l adds lane l^32, then l^16, ... l^1. Addition commutes, so
-// every lane ends with the same bits; the CPU restatement replays this exact tree.
-SS_DEV float ss_wave_sum(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = v + ss_shfl_xor(v, m);
+// ---------------------------------------------------------------- lane exchange (wave64, VALU only)
+// ss_xor_lane<M>(v) is v of lane l ^ M for M = 1, 2, 4, 8, from DPP moves inside a row of 16 lanes (GFX9
+// encodings): quad_perm xor 1 (0xB1), xor 2 (0x4E) and xor 3 (0x1B); row_half_mirror (0x141, lane l <- l ^ 7);
+// row_mirror (0x140, l <- l ^ 15). xor 4 = half_mirror then xor 3; xor 8 = mirror then half_mirror.
+// ss_pair<M>(v, lo, hi), M = 16 or 32: gfx950's v_permlane16_swap / v_permlane32_swap of a register with itself,
+// which leaves in every lane the values of both partner groups: lo = v[l & ~M], hi = v[l | M].
+// Every exchange needs the whole wave active. LDS-routed shuffles (ds_bpermute) cost several times more.
+template <int CTRL>
+SS_DEV uint32_t ss_dpp(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, true);
+}
+
+template <int M>
+SS_DEV uint32_t ss_xor_lane(uint32_t v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "DPP exchange inside a row");
+  if constexpr (M == 1) return ss_dpp<0xB1>(v);
+  if constexpr (M == 2) return ss_dpp<0x4E>(v);
+  if constexpr (M == 4) return ss_dpp<0x1B>(ss_dpp<0x141>(v));
+  return ss_dpp<0x141>(ss_dpp<0x140>(v));
+}
+
+template <int M>
+SS_DEV void ss_pair(uint32_t v, uint32_t& lo, uint32_t& hi) {
+  static_assert(M == 16 || M == 32, "row-pair exchange");
+  if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    lo = r[0];
+    hi = r[1];
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    lo = r[0];
+    hi = r[1];
+  }
+}
+
+SS_DEV float ss_uf(uint32_t u) { return __uint_as_float(u); }
+SS_DEV uint32_t ss_fu(float f) { return __float_as_uint(f); }
+
+// Xor butterfly over the 64 lanes with a commutative operation: lane l combines with lane l^32, then l^16, ...,
+// l^1. Because op(a, b) == op(b, a), every lane ends with the same bits, and the CPU restatement replays this
+// tree (pairs (l, l^32) first).
+template <class Op>
+SS_DEV uint32_t ss_butterfly(uint32_t v, Op op) {
+  uint32_t lo, hi;
+  ss_pair<32>(v, lo, hi);
+  v = op(lo, hi);
+  ss_pair<16>(v, lo, hi);
+  v = op(lo, hi);
+  v = op(v, ss_xor_lane<8>(v));
+  v = op(v, ss_xor_lane<4>(v));
+  v = op(v, ss_xor_lane<2>(v));
+  v = op(v, ss_xor_lane<1>(v));
   return v;
+}
+
+SS_DEV float ss_wave_sum(float v) {
+  return ss_uf(ss_butterfly(ss_fu(v), [](uint32_t a, uint32_t b) { return ss_fu(ss_uf(a) + ss_uf(b)); }));
 }
 
 SS_DEV float ss_wave_max(float v) {
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, ss_shfl_xor(v, m));
+  return ss_uf(ss_butterfly(ss_fu(v), [](uint32_t a, uint32_t b) { return ss_fu(fmaxf(ss_uf(a), ss_uf(b))); }));
+}
+
+SS_DEV uint32_t ss_wave_max_u32(uint32_t v) {
+  return ss_butterfly(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+
+SS_DEV uint32_t ss_wave_min_u32(uint32_t v) {
+  return ss_butterfly(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+
+SS_DEV uint32_t ss_wave_or(uint32_t v) {
+  return ss_butterfly(v, [](uint32_t a, uint32_t b) { return a | b; });
+}
+
+// 64-bit maximum over the wave (both halves exchanged per step).
+SS_DEV uint64_t ss_wave_max_u64(uint64_t v) {
+  auto mx = [](uint64_t a, uint64_t b) { return a > b ? a : b; };
+  auto join = [](uint32_t hi, uint32_t lo) { return ((uint64_t)hi << 32) | lo; };
+  uint32_t l0, h0, l1, h1;
+  ss_pair<32>((uint32_t)v, l0, h0);
+  ss_pair<32>((uint32_t)(v >> 32), l1, h1);
+  v = mx(join(l1, l0), join(h1, h0));
+  ss_pair<16>((uint32_t)v, l0, h0);
+  ss_pair<16>((uint32_t)(v >> 32), l1, h1);
+  v = mx(join(l1, l0), join(h1, h0));
+  v = mx(v, join(ss_xor_lane<8>((uint32_t)(v >> 32)), ss_xor_lane<8>((uint32_t)v)));
+  v = mx(v, join(ss_xor_lane<4>((uint32_t)(v >> 32)), ss_xor_lane<4>((uint32_t)v)));
+  v = mx(v, join(ss_xor_lane<2>((uint32_t)(v >> 32)), ss_xor_lane<2>((uint32_t)v)));
+  v = mx(v, join(ss_xor_lane<1>((uint32_t)(v >> 32)), ss_xor_lane<1>((uint32_t)v)));
   return v;
 }
+
+// Sum of the lanes l, l^16, l^32, l^48 (the four 16-lane rows) in the order (r0 + r1) + (r2 + r3) seen from the
+// lane's own row pair: every lane of column l & 15 gets the same bits.
+SS_DEV float ss_rows_sum(float v) {
+  uint32_t lo, hi;
+  ss_pair<16>(ss_fu(v), lo, hi);
+  const float s = ss_uf(lo) + ss_uf(hi);
+  ss_pair<32>(ss_fu(s), lo, hi);
+  return ss_uf(lo) + ss_uf(hi);
+}
+
+SS_DEV float ss_readlane_f(float v, int l) { return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l)); }
 
 // ---------------------------------------------------------------- status word
 // The word lives in the C-ABI translation unit; kernels receive its device address as an argument.
@@ -137,11 +225,20 @@ SS_DEV ss_f32x4 ss_mfma(const ss_u32x4& a, const ss_u32x4& b, const ss_f32x4& c)
 // order (q0,q4) (q1,q5) (q2,q6) (q3,q7): one shift and one and-or per pair. The constant part (1.0) is small next
 // to the spread of q/16, so the per-group correction (b - 16 s) * sum(x) cancels little of the MFMA dot.
 constexpr float kNibbleScale = 16.f;
+// (x & m) | c in one VOP3 instruction (the compiler emits separate and / or for this pattern). m lives in an SGPR,
+// c in a VGPR (one scalar operand per VALU instruction on gfx950).
+SS_DEV uint32_t ss_and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
+  return r;
+}
 SS_DEV ss_u32x4 ss_nibbles_to_bf16(uint32_t w) {
+  constexpr uint32_t M = 0x00780078u;
+  const uint32_t one = 0x3F803F80u;
   ss_u32x4 b;
-  b.x = ((w << 3) & 0x00780078u) | 0x3F803F80u;
-  b.y = ((w >> 1) & 0x00780078u) | 0x3F803F80u;
-  b.z = ((w >> 5) & 0x00780078u) | 0x3F803F80u;
-  b.w = ((w >> 9) & 0x00780078u) | 0x3F803F80u;
+  b.x = ss_and_or(w << 3, M, one);
+  b.y = ss_and_or(w >> 1, M, one);
+  b.z = ss_and_or(w >> 5, M, one);
+  b.w = ss_and_or(w >> 9, M, one);
   return b;
 }

@@ -84,8 +84,6 @@ hipError_t launch_dense_rows(const uint16_t* x, int T, int H, const DenseSeg* se
 }
 
 // ---------------------------------------------------------------- router tail
-SS_DEV bool ss_better(uint32_t k1, int i1, uint32_t k2, int i2) { return k1 > k2 || (k1 == k2 && i1 < i2); }
-
 __global__ __launch_bounds__(64) void router_topk_kernel(const uint16_t* __restrict__ logits,
                                                          const float* __restrict__ bias, float* __restrict__ probs,
                                                          int32_t* __restrict__ ids, float* __restrict__ weights, int E,
@@ -119,25 +117,15 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const uint16_t* __restr
   }
   __syncthreads();
   for (int r = 0; r < K; ++r) {
-    uint32_t bk = 0;
-    int bi = 0x7FFFFFFF;
+    // (key, lowest index) as one 64-bit key: key above the complemented index, 0 for taken entries.
+    uint64_t best = 0;
     for (int e = lane; e < E; e += 64) {
       if (taken[e]) continue;
-      const uint32_t k = ss_key(sm[e]);
-      if (ss_better(k, e, bk, bi)) {
-        bk = k;
-        bi = e;
-      }
+      const uint64_t kv = ((uint64_t)ss_key(sm[e]) << 32) | (0xFFFFFFFFu - (uint32_t)e);
+      best = kv > best ? kv : best;
     }
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) {
-      const uint32_t ok = (uint32_t)ss_shfl_xor_i((int)bk, msk);
-      const int oi = ss_shfl_xor_i(bi, msk);
-      if (ss_better(ok, oi, bk, bi)) {
-        bk = ok;
-        bi = oi;
-      }
-    }
+    best = ss_wave_max_u64(best);
+    const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
     if (lane == 0) {
       taken[bi] = 1;
       ti[r] = bi;

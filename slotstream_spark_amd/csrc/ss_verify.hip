@@ -129,13 +129,19 @@ static __host__ __device__ inline DLayout dlayout(int T, int H, int I, int K, in
   return d;
 }
 
-// Cross-workgroup hand-off. Producer: every wave waits for its own stores (s_waitcnt), the workgroup barrier orders
-// them, then one thread publishes with a single agent-scope release (one L2 write-back per workgroup). Consumer: one
-// thread polls with relaxed agent-scope loads (no cache maintenance per poll), then one agent-scope acquire fence,
-// then the workgroup barrier.
+// Cross-workgroup hand-off. The data that crosses workgroups (router logits, shared-expert rows, h fragments and
+// sums, counters) is written and read only with monotonic agent-scope accesses: on gfx950 these carry the sc1
+// scope bit, so they are coherent across the eight XCDs' L2 caches by themselves, and no whole-cache write-back
+// (buffer_wbl2) or invalidate (buffer_inv), which agent-scope release and acquire fences would emit, is needed.
+// Producer: every wave waits for its own stores to be acknowledged (s_waitcnt), the workgroup barrier orders them,
+// then one thread adds to the counter. Consumer: one thread polls the counter, then the workgroup barrier; the data
+// loads are issued after the poll has seen the count.
 SS_DEV void stores_done() { __builtin_amdgcn_s_waitcnt(0); }
 
-SS_DEV void signal_add(int* c, int v) { __hip_atomic_fetch_add(c, v, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT); }
+SS_DEV void signal_add(int* c, int v) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 SS_DEV void wait_ge(int* c, int target, int* err) {
   for (int it = 0;; ++it) {
@@ -146,12 +152,35 @@ SS_DEV void wait_ge(int* c, int target, int* err) {
     }
     __builtin_amdgcn_s_sleep(1);
   }
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <class T>
+SS_DEV void st_ag(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+SS_DEV T ld_ag(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+SS_DEV void st_ag16(void* p, uint4 v) {
+  uint64_t* q = static_cast<uint64_t*>(p);
+  st_ag(q, ((uint64_t)v.y << 32) | v.x);
+  st_ag(q + 1, ((uint64_t)v.w << 32) | v.z);
+}
+SS_DEV uint4 ld_ag16(const void* p) {
+  const uint64_t* q = static_cast<const uint64_t*>(p);
+  const uint64_t a = ld_ag(q), b = ld_ag(q + 1);
+  return make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
 }
 
 // Direct-to-LDS loads: lane l's `size` bytes land at lds_wave_base + size * l (lds_wave_base is wave-uniform).
 SS_DEV void dma16(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_wave_base, 16, 0, 0);
+}
+// The same with the sc1 (agent) scope bit, for data written by other workgroups in this launch.
+SS_DEV void dma16_ag(const void* src, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_wave_base, 16, 0, 16);
 }
 SS_DEV void dma4(const void* src, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(src, (lds_void_t*)lds_wave_base, 4, 0, 0);
@@ -169,6 +198,7 @@ struct VSmem {
   float hsum[kMaxQv][16];         // h group sums per use (I <= 1024)
   float shv[16][kTBv];
   float xch[4][16 * kTBv];        // per-wave exchange of one item's 16 columns x 4 tokens
+  alignas(16) int ekey[64];       // unique_setup keys
   int nt, nu;
 };
 
@@ -196,6 +226,8 @@ SS_DEV ss_u32x4 as_v(uint4 v) {
 }
 
 // Unique experts of the block in first-occurrence order from s.ids. Wave 0 only; caller syncs.
+// Each lane publishes a key (its expert, or a negative value no other lane has when the entry is unusable) and
+// finds the first lane with the same key by broadcast LDS reads.
 SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
   const int lane = threadIdx.x;
   const int nq = s.nt * a.K;
@@ -216,12 +248,19 @@ SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
       ss_raise(a.err, SS_ERR_EXPERT_ID);
     }
   }
-  int j0 = lane;
-#pragma unroll 1
-  for (int j = 0; j < 64; ++j) {
-    const int ej = __shfl(e, j, 64);
-    const int vj = __shfl((int)valid, j, 64);
-    if (j < lane && vj && valid && ej == e && j0 == lane) j0 = j;
+  const int key = valid ? e : -1 - lane;
+  s.ekey[lane] = key;
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  int j0 = 64;
+#pragma unroll 4
+  for (int j = 0; j < nq; j += 4) {
+    const int4 k4 = *reinterpret_cast<const int4*>(&s.ekey[j]);
+    if (j0 == 64 && k4.x == key) j0 = j;
+    if (j0 == 64 && k4.y == key) j0 = j + 1;
+    if (j0 == 64 && k4.z == key) j0 = j + 2;
+    if (j0 == 64 && k4.w == key) j0 = j + 3;
   }
   const bool first = valid && j0 == lane;
   const uint64_t mask = __ballot(first);
@@ -234,36 +273,37 @@ SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
   if (lane == 0) s.nu = __popcll(mask);
 }
 
-// Router tail of token t in one wave, scores staged in LDS (same operations and order as router_topk_kernel).
-SS_DEV void router_tail_wave(const VerifyArgs& a, const uint16_t* logits, int t, VSmem& s) {
+// Router tail of token t in one wave (the operations and order of router_topk_kernel): lane l holds the entries
+// e = l + 64 i. Each top-k round takes the 64-bit maximum of (key << 32 | ~e) over the untaken entries (taken or
+// absent entries are 0, below every present one), so ties go to the lower index.
+SS_DEV void router_tail_wave(const VerifyArgs& a, const uint16_t* logits, int t, VSmem& s,
+                             const float (&bias_r)[kMaxEv / 64]) {
   const int lane = threadIdx.x & 63;
   const int E = a.E, K = a.K;
   constexpr int NV = kMaxEv / 64;
-  const SS_G uint16_t* lg = gp(logits) + (size_t)t * E;
+  const uint16_t* lg = logits + (size_t)t * E;
   float v[NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) v[i] = lane + 64 * i < E ? ss_bf16_to_f32(lg[lane + 64 * i]) : 0.f;
-  if (a.bias) {
-    const SS_G float* bs = gp(a.bias);
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (lane + 64 * i < E) v[i] = v[i] + bs[lane + 64 * i];
+  for (int i = 0; i < NV; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = ss_bf16_to_f32(ld_ag(lg + (e < E ? e : 0)));
   }
+  if (a.bias) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = v[i] + bias_r[i];
+  }
+  // Selects instead of branches; an absent entry adds +0 to a non-negative sum, which changes no bit.
   float m = -__builtin_inff();
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (lane + 64 * i < E) m = fmaxf(m, v[i]);
+  for (int i = 0; i < NV; ++i) m = lane + 64 * i < E ? fmaxf(m, v[i]) : m;
   m = ss_wave_max(m);
   float acc = 0.f;
 #pragma unroll
-  for (int i = 0; i < NV; ++i)
-    if (lane + 64 * i < E) {
-      v[i] = ss_expf(v[i] - m);
-      acc = acc + v[i];
-    }
+  for (int i = 0; i < NV; ++i) {
+    v[i] = ss_expf(v[i] - m);
+    acc = acc + (lane + 64 * i < E ? v[i] : 0.f);
+  }
   const float z = ss_wave_sum(acc);
-  // Candidates packed as (key << 32) | ~index: the 64-bit maximum is the largest probability, ties to the lower
-  // index; taken or absent entries are 0, below every present entry.
   uint64_t cand[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
@@ -271,76 +311,148 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint16_t* logits, int t,
     v[i] = v[i] / z;
     cand[i] = e < E ? ((uint64_t)ss_key(v[i]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e) : 0ull;
   }
+  float mine = 0.f, sum = 0.f;
+  int my_id = 0;
 #pragma unroll 1
   for (int r = 0; r < K; ++r) {
     uint64_t best = 0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) best = cand[i] > best ? cand[i] : best;
-#pragma unroll
-    for (int msk = 32; msk >= 1; msk >>= 1) {
-      const uint32_t ohi = (uint32_t)ss_shfl_xor_i((int)(uint32_t)(best >> 32), msk);
-      const uint32_t olo = (uint32_t)ss_shfl_xor_i((int)(uint32_t)best, msk);
-      const uint64_t o = ((uint64_t)ohi << 32) | olo;
-      best = o > best ? o : best;
-    }
+    best = ss_wave_max_u64(best);
     const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
-    float pv = 0.f;
+    const int li = __builtin_amdgcn_readfirstlane(bi & 63), ii = __builtin_amdgcn_readfirstlane(bi >> 6);
+    float pl = v[0];
 #pragma unroll
-    for (int i = 0; i < NV; ++i)
-      if (lane + 64 * i == bi) {
-        cand[i] = 0ull;
-        pv = v[i];
-      }
-    pv = __shfl(pv, bi & 63, 64);
-    if (lane == 0) {
-      s.ids[t * K + r] = bi;
-      s.wts[t * K + r] = pv;
-    }
+    for (int i = 1; i < NV; ++i) pl = i == ii ? v[i] : pl;
+    const float pv = ss_readlane_f(pl, li);
+    const bool own = lane == li;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) cand[i] = own && i == ii ? 0ull : cand[i];
+    sum = sum + pv;  // rank-order sum of the top-k probabilities
+    mine = lane == r ? pv : mine;
+    my_id = lane == r ? bi : my_id;
   }
-  if (lane == 0) {
-    float sum = 0.f;
-#pragma unroll 1
-    for (int r = 0; r < K; ++r) sum = sum + s.wts[t * K + r];
-#pragma unroll 1
-    for (int r = 0; r < K; ++r) s.wts[t * K + r] = s.wts[t * K + r] / sum;
+  if (lane < K) {
+    s.ids[t * K + lane] = my_id;
+    s.wts[t * K + lane] = mine / sum;
   }
 }
 
-// One dense bf16 row against up to 4 tokens in the dense_rows_kernel order; x rows in global memory.
-// xs: the x rows staged in LDS as uint4 [t][H / 8].
-template <int NJ>
-SS_DEV void dense_row(const uint4* xs, int nt, int H, const uint16_t* wrow_p, float out[kTBv]) {
+// x A-fragment entry f = (((j * 4 + i) * 4 + g) * kTBv + t) holds elements kb .. kb + 7 of token t, kb = 128 j +
+// 32 g + 8 i, as the bf16 pairs (e0, e4) (e1, e5) (e2, e6) (e3, e7) (perm_pairs); with fp32 x the entry is two uint4,
+// the bf16 high parts and the bf16 residuals. Element e of an entry is word e & 3, half e >> 2.
+SS_DEV int xfrag_index(int kb, int t) {
+  return ((((kb >> 7) * 4 + ((kb >> 3) & 3)) * 4 + ((kb >> 5) & 3)) * kTBv) + t;
+}
+
+// Stage the x fragments (into xfl) and the 64-element group sums of x (into s.gx, sequential in element order).
+// Every global load of a thread is issued before its first use; tokens t >= nt read token 0 and are zeroed.
+template <int NJG, bool XF32>
+SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], int nt) {
+  const int tid = threadIdx.x;
+  const int H = a.H;
+  constexpr int NF = NJG * 16 * kTBv;  // (j, i, g, t)
+  constexpr int FPT = NF / 256;
+  static_assert(NF % 256 == 0, "whole fragment entries per thread");
+  uint4 fv[FPT][XF32 ? 2 : 1];
+#pragma unroll
+  for (int k = 0; k < FPT; ++k) {
+    const int f = tid + 256 * k;
+    const int t = f & 3, gg = (f >> 2) & 3, i = (f >> 4) & 3, j = f >> 6;
+    const int tt = t < nt ? t : 0;
+    const int kb = 128 * j + 32 * gg + 8 * i;
+    if (XF32) {
+      const float* xp = static_cast<const float*>(a.x) + (size_t)tt * H + kb;
+      fv[k][0] = ldg16(xp);
+      fv[k][XF32 ? 1 : 0] = ldg16(xp + 4);
+    } else {
+      fv[k][0] = ldg16(static_cast<const uint16_t*>(a.x) + (size_t)tt * H + kb);
+    }
+  }
+  // Group sums: thread q < (H / 64) * kTBv sums group q >> 2 of token q & 3.
+  constexpr int GV = XF32 ? 16 : 8;
+  uint4 gv[GV];
+  const int q = tid < (H >> 6) * kTBv ? tid : 0;
+  const int gt = (q & 3) < nt ? (q & 3) : 0;
+  const int Gi = q >> 2;
+#pragma unroll
+  for (int k = 0; k < GV; ++k) {
+    if (XF32)
+      gv[k] = ldg16(static_cast<const float*>(a.x) + (size_t)gt * H + 64 * Gi + 4 * k);
+    else
+      gv[k] = ldg16(static_cast<const uint16_t*>(a.x) + (size_t)gt * H + 64 * Gi + 8 * k);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < FPT; ++k) {
+    const int f = tid + 256 * k;
+    const bool live = (f & 3) < nt;
+    if (XF32) {
+      const uint4 v0 = fv[k][0], v1 = fv[k][XF32 ? 1 : 0];
+      const float e0[4] = {__uint_as_float(v0.x), __uint_as_float(v0.y), __uint_as_float(v0.z), __uint_as_float(v0.w)};
+      const float e1[4] = {__uint_as_float(v1.x), __uint_as_float(v1.y), __uint_as_float(v1.z), __uint_as_float(v1.w)};
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t b0 = ss_f32_to_bf16(e0[d]), b1 = ss_f32_to_bf16(e1[d]);
+        hw[d] = b0 | (b1 << 16);
+        lw[d] = ss_f32_to_bf16(e0[d] - ss_bf16_to_f32(b0)) | (ss_f32_to_bf16(e1[d] - ss_bf16_to_f32(b1)) << 16);
+      }
+      xfl[2 * f] = live ? make_uint4(hw[0], hw[1], hw[2], hw[3]) : make_uint4(0u, 0u, 0u, 0u);
+      xfl[2 * f + 1] = live ? make_uint4(lw[0], lw[1], lw[2], lw[3]) : make_uint4(0u, 0u, 0u, 0u);
+    } else {
+      xfl[f] = live ? perm_pairs(fv[k][0]) : make_uint4(0u, 0u, 0u, 0u);
+    }
+  }
+  if (tid < (H >> 6) * kTBv) {
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < GV; ++k) {
+      const uint4 v = gv[k];
+      if (XF32) {
+        sum = sum + __uint_as_float(v.x);
+        sum = sum + __uint_as_float(v.y);
+        sum = sum + __uint_as_float(v.z);
+        sum = sum + __uint_as_float(v.w);
+      } else {
+        sum = sum + bf_lo(v.x);
+        sum = sum + bf_hi(v.x);
+        sum = sum + bf_lo(v.y);
+        sum = sum + bf_hi(v.y);
+        sum = sum + bf_lo(v.z);
+        sum = sum + bf_hi(v.z);
+        sum = sum + bf_lo(v.w);
+        sum = sum + bf_hi(v.w);
+      }
+    }
+    gx[Gi][q & 3] = (q & 3) < nt ? sum : 0.f;
+  }
+}
+
+// One dense bf16 row (16-byte words wv[jj] = elements 512 jj + 8 lane .. +7, already in registers) against the
+// staged bf16 x fragments, in the dense_rows_kernel order: per lane, fused multiply-adds over its elements in order,
+// then the wave butterfly.
+template <int NJX>
+SS_DEV void dense_dot(const uint4 (&wv)[NJX], const uint4* xfl, int nt, float out[kTBv]) {
   const int lane = threadIdx.x & 63;
-  const int h8 = H >> 3;
-  uint4 wv[NJ];
 #pragma unroll
-  for (int j = 0; j < NJ; ++j)
-    wv[j] = (64 * j + lane < h8) ? ldg16(wrow_p + 8 * (64 * j + lane)) : make_uint4(0u, 0u, 0u, 0u);
-  float acc[kTBv] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 1
-  for (int t = 0; t < nt; ++t) {
+  for (int t = 0; t < kTBv; ++t) {
+    if (t >= nt) break;
     float ac = 0.f;
-    const uint4* xr = xs + (size_t)t * h8;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-      if (64 * j + lane >= h8) break;
-      const uint4 xv = xr[64 * j + lane];
-      const uint32_t ww[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+    for (int jj = 0; jj < NJX; ++jj) {
+      const uint4 xv = xfl[xfrag_index(512 * jj + 8 * lane, t)];
+      const uint32_t ww[4] = {wv[jj].x, wv[jj].y, wv[jj].z, wv[jj].w};
       const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float wf = (e & 1) ? bf_hi(ww[e >> 1]) : bf_lo(ww[e >> 1]);
-        const float xf = (e & 1) ? bf_hi(xx[e >> 1]) : bf_lo(xx[e >> 1]);
+        const float xf = (e >> 2) ? bf_hi(xx[e & 3]) : bf_lo(xx[e & 3]);
         ac = __builtin_fmaf(xf, wf, ac);
       }
     }
-    // acc[t] = ac with a runtime t: select into fixed registers
-#pragma unroll
-    for (int q = 0; q < kTBv; ++q)
-      if (q == t) acc[q] = ac;
+    out[t] = ss_wave_sum(ac);
   }
-#pragma unroll
-  for (int t = 0; t < kTBv; ++t) out[t] = ss_wave_sum(acc[t]);
 }
 
 template <int NJG, int NJD, bool XF32>
@@ -379,41 +491,64 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   if (tid == 0) s.nt = nt;
 
   // ------------------------------------------------------------ phase A + B (verify) / ids (decode)
-  if (verify) {
-    // Stage x into the (not yet used) x-fragment region: uint4 [t][H / 8].
-    uint4* xs = xfl;
-    {
-      const uint16_t* xg = static_cast<const uint16_t*>(a.x);
-      for (int i = tid; i < nt * (H >> 3); i += 256) xs[i] = ldg16(xg + 8 * i);
+  // Dense-row jobs (verify mode): j < E is router row j; E <= j < E + Is the shared gate and up rows j - E, and the
+  // last of those jobs also takes the shared_expert_gate row, so no workgroup that holds router rows waits for a
+  // second job. The rows of a wave's first job, this workgroup's map entries and x are all requested before any of
+  // them is used, so phase A costs one memory round trip.
+  constexpr int NJX = NJG / 4;  // 16-byte words per lane of one dense row (H / 512)
+  const int Is = a.Is, J = verify ? E + Is : 0, W = G * 4;
+  const int j_first = bid * 4 + w;
+  uint4 r0[NJX], r1[NJX], r2[NJX];
+  auto load_job = [&](int j) {
+    const uint16_t* w0 = j < E ? a.router_w + (size_t)j * H : a.sh_gate + (size_t)(j - E) * H;
+#pragma unroll
+    for (int jj = 0; jj < NJX; ++jj) r0[jj] = ldg16(w0 + 8 * (64 * jj + lane));
+    if (j >= E) {
+      const uint16_t* w1 = a.sh_up + (size_t)(j - E) * H;
+#pragma unroll
+      for (int jj = 0; jj < NJX; ++jj) r1[jj] = ldg16(w1 + 8 * (64 * jj + lane));
     }
-    __syncthreads();
-    const int Is = a.Is, J = E + Is + 1, W = G * 4;
+    if (j == J - 1) {
+#pragma unroll
+      for (int jj = 0; jj < NJX; ++jj) r2[jj] = ldg16(a.sh_g + 8 * (64 * jj + lane));
+    }
+  };
+  if (verify && j_first < J) load_job(j_first);
+  int slot_e[2] = {-1, -1};
+  if (verify) {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int e = tid + 256 * k;
+      const int64_t mi = a.map_base + e;
+      const bool ok = e < E && mi < a.map_len;
+      const int v = gp(a.map)[ok ? mi : 0];
+      slot_e[k] = ok ? v : -1;
+    }
+  }
+  stage_x<NJG, XF32>(a, xfl, s.gx, nt);
+  __syncthreads();
+  if (verify) {
 #pragma unroll 1
-    for (int j = bid * 4 + w; j < J; j += W) {
-      const int nrow = (j >= E && j < E + Is) ? 2 : 1;
+    for (int j = j_first; j < J; j += W) {
+      if (j != j_first) load_job(j);
+      float d[kTBv];
+      dense_dot<NJX>(r0, xfl, nt, d);
+      uint16_t* dst0 = j < E ? logits + j : gsh + (j - E);
+      const int ld = j < E ? E : Is;
+      if (lane == 0)
 #pragma unroll 1
-      for (int rr = 0; rr < nrow; ++rr) {
-        const uint16_t* wr;
-        uint16_t* dst;
-        int ld;
-        if (j < E) {
-          wr = a.router_w + (size_t)j * H;
-          dst = logits + j;
-          ld = E;
-        } else if (j < E + Is) {
-          wr = (rr ? a.sh_up : a.sh_gate) + (size_t)(j - E) * H;
-          dst = (rr ? ush : gsh) + (j - E);
-          ld = Is;
-        } else {
-          wr = a.sh_g;
-          dst = sgl;
-          ld = 1;
-        }
-        float d[kTBv];
-        dense_row<(NJG + 3) / 4>(xs, nt, H, wr, d);
+        for (int t = 0; t < nt; ++t) st_ag(dst0 + (size_t)t * ld, (uint16_t)ss_f32_to_bf16(d[t]));
+      if (j >= E) {
+        dense_dot<NJX>(r1, xfl, nt, d);
         if (lane == 0)
 #pragma unroll 1
-          for (int t = 0; t < nt; ++t) gp(dst)[(size_t)t * ld] = (uint16_t)ss_f32_to_bf16(d[t]);
+          for (int t = 0; t < nt; ++t) st_ag(ush + (size_t)(j - E) + (size_t)t * Is, (uint16_t)ss_f32_to_bf16(d[t]));
+      }
+      if (j == J - 1) {
+        dense_dot<NJX>(r2, xfl, nt, d);
+        if (lane == 0)
+#pragma unroll 1
+          for (int t = 0; t < nt; ++t) st_ag(sgl + t, (uint16_t)ss_f32_to_bf16(d[t]));
       }
     }
     stores_done();
@@ -421,26 +556,44 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     if (tid == 0) {
       int nr = 0, ns = 0;
       for (int ww = 0; ww < 4; ++ww)
-        for (int j = bid * 4 + ww; j < J; j += W) (j < E ? nr : ns) += 1;
+        for (int j = bid * 4 + ww; j < J; j += W) {
+          if (j < E) nr += 1;
+          else ns += j == J - 1 ? 2 : 1;
+        }
       if (nr) signal_add(ctr + CTR_ROUTER, nr);
       if (ns) signal_add(ctr + CTR_SHARED, ns);
       SS_TRACE(1);
     }
-    // The layer's map / slot_ptr tables into LDS while the other workgroups finish their router rows.
-#pragma unroll 1
-    for (int e = tid; e < E; e += 256) {
-      const int64_t mi = a.map_base + e;
-      const int slot = mi < a.map_len ? a.map[mi] : -1;
-      s.map[e] = slot;
-      s.base_e[e] = (slot >= 0 && (int64_t)slot < a.n_slots) ? reinterpret_cast<const uint8_t*>(a.slot_ptr[slot])
-                                                             : nullptr;
+    // The layer's slot pointers into LDS and the routing bias into the tail waves' registers while the other
+    // workgroups finish their router rows.
+    const uint8_t* base_k[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const bool ok = slot_e[k] >= 0 && (int64_t)slot_e[k] < a.n_slots;
+      const int64_t p = gp(a.slot_ptr)[ok ? slot_e[k] : 0];
+      base_k[k] = ok ? reinterpret_cast<const uint8_t*>(p) : nullptr;
+    }
+    constexpr int NV = kMaxEv / 64;
+    float bias_r[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      bias_r[i] = a.bias ? gp(a.bias)[e < E ? e : 0] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int e = tid + 256 * k;
+      if (e < E) {
+        s.map[e] = slot_e[k];
+        s.base_e[e] = base_k[k];
+      }
     }
     if (tid == 0) {
       wait_ge(ctr + CTR_ROUTER, E, a.err);
       SS_TRACE(2);
     }
     __syncthreads();
-    if (w < nt) router_tail_wave(a, logits, w, s);
+    if (w < nt) router_tail_wave(a, logits, w, s, bias_r);
     __syncthreads();
     SS_TRACE(3);
     if (bid == 0 && tid < nt * K) {
@@ -476,24 +629,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       dma4(base + rec.db + drow * dsb_b + 4 * j, sl + (size_t)NJD * 1280 + (size_t)j * 256);
     }
   };
-  if (has_tile) {
-#pragma unroll 1
-    for (int u = w; u < nu && u < D.P; u += 4) issue_down(u, u);
-  }
-  uint4 shw[4];
-  if (verify && has_tile) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int srow = 16 * bid + 4 * w + rr;
-      shw[rr] = (8 * lane < a.Is) ? reinterpret_cast<const uint4*>(a.sh_down + (size_t)srow * a.Is)[lane]
-                                  : make_uint4(0u, 0u, 0u, 0u);
-    }
-  }
   SS_TRACE(5);
 
   // ------------------------------------------------------------ phase C: gate/up, one item per wave at a time
   // Items go first to the workgroups without down rows (bid >= H/16), one per wave, then wrap around.
-  const int W = G * 4;
   const int gw = ((bid - (H >> 4) + G) % G) * 4 + w;
   int my_items = 0;
   for (int ww = 0; ww < 4; ++ww) {
@@ -501,66 +640,6 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     for (int it = gq; it < n_items; it += W) ++my_items;
   }
   if (my_items) {
-    // x group sums and the A fragments of every K iteration into LDS: frag[j][i][g][t][part], active lanes only.
-    for (int q = tid; q < (H >> 6) * kTBv; q += 256) {
-      const int Gi = q >> 2, t = q & 3;
-      float sum = 0.f;
-      if (t < nt) {
-        if (XF32) {
-          const float4* xp = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + (size_t)t * H + 64 * Gi);
-#pragma unroll 1
-          for (int k = 0; k < 16; ++k) {
-            const float4 v = xp[k];
-            sum = sum + v.x;
-            sum = sum + v.y;
-            sum = sum + v.z;
-            sum = sum + v.w;
-          }
-        } else {
-          const uint4* xp = reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + (size_t)t * H + 64 * Gi);
-#pragma unroll 1
-          for (int k = 0; k < 8; ++k) {
-            const uint4 v = xp[k];
-            sum = sum + bf_lo(v.x);
-            sum = sum + bf_hi(v.x);
-            sum = sum + bf_lo(v.y);
-            sum = sum + bf_hi(v.y);
-            sum = sum + bf_lo(v.z);
-            sum = sum + bf_hi(v.z);
-            sum = sum + bf_lo(v.w);
-            sum = sum + bf_hi(v.w);
-          }
-        }
-      }
-      s.gx[Gi][t] = sum;
-    }
-    const int nfrag = NJG * 4 * 4 * kTBv;  // (j, i, g, t)
-    for (int f = tid; f < nfrag; f += 256) {
-      const int t = f & 3, gg = (f >> 2) & 3, i = (f >> 4) & 3, j = f >> 6;
-      const int kb = 128 * j + 32 * gg + 8 * i;
-      uint4 hi4 = make_uint4(0u, 0u, 0u, 0u), lo4 = make_uint4(0u, 0u, 0u, 0u);
-      if (t < nt) {
-        if (XF32) {
-          const float4* xp = reinterpret_cast<const float4*>(static_cast<const float*>(a.x) + (size_t)t * H + kb);
-          const float4 v0 = xp[0], v1 = xp[1];
-          const float e0[4] = {v0.x, v0.y, v0.z, v0.w}, e1[4] = {v1.x, v1.y, v1.z, v1.w};
-          uint32_t h[4], l[4];
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const uint32_t b0 = ss_f32_to_bf16(e0[d]), b1 = ss_f32_to_bf16(e1[d]);
-            h[d] = b0 | (b1 << 16);
-            l[d] = ss_f32_to_bf16(e0[d] - ss_bf16_to_f32(b0)) | (ss_f32_to_bf16(e1[d] - ss_bf16_to_f32(b1)) << 16);
-          }
-          hi4 = make_uint4(h[0], h[1], h[2], h[3]);
-          lo4 = make_uint4(l[0], l[1], l[2], l[3]);
-        } else {
-          hi4 = perm_pairs(*reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(a.x) + (size_t)t * H + kb));
-        }
-      }
-      xfl[f * (XF32 ? 2 : 1)] = hi4;
-      if (XF32) xfl[f * 2 + 1] = lo4;
-    }
-    __syncthreads();
     SS_TRACE(6);
     const int m = lane & 15, at = m & 3, agrp = m >> 2, ahh = agrp >> 1, apart = agrp & 1;
     const bool a_act = ahh == (g >> 1) && at < nt && (XF32 || apart == 0);
@@ -581,6 +660,13 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
         wv[j] = ldg16(wrow + 64 * j);
         sv[j] = srow[j];
         bv[j] = brow[j];
+      }
+      // Keep every load of the item ahead of the first MFMA: otherwise the scheduler spreads them over the loop
+      // and the item pays one memory latency per batch.
+      __builtin_amdgcn_sched_barrier(0);
+      if (item == gw && w == 0) {
+        __builtin_amdgcn_s_waitcnt(0);
+        SS_TRACE(14);
       }
       float acc[kTBv] = {0.f, 0.f, 0.f, 0.f};
       constexpr int JB = NJG % 4 == 0 ? 4 : 1;  // K iterations whose LDS operands are read before their MFMAs
@@ -619,10 +705,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
           }
         }
       }
+      if (item == gw && w == 0) SS_TRACE(15);
 #pragma unroll
       for (int r = 0; r < kTBv; ++r) {
-        acc[r] = acc[r] + ss_shfl_xor(acc[r], 16);
-        acc[r] = acc[r] + ss_shfl_xor(acc[r], 32);
+        acc[r] = ss_rows_sum(acc[r]);
         if (g == 0) xch[n * kTBv + r] = acc[r];
       }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -653,9 +739,9 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
           mk &= mk - 1;
           const int q = r * K + k;
           uint4* fpo = hfrag + (((size_t)q * NJD + jf) * 4 + gf) * 8 + ifr;
-          stg16(fpo, fhi);
-          stg16(fpo + 4, flo);
-          gp(hsum8)[(size_t)q * (I >> 3) + p] = sum8;
+          st_ag16(fpo, fhi);
+          st_ag16(fpo + 4, flo);
+          st_ag(reinterpret_cast<uint32_t*>(hsum8) + (size_t)q * (I >> 3) + p, __float_as_uint(sum8));
           if (a.h_buf) {
             float* hp = a.h_buf + ((size_t)r * K + k) * I + 8 * p;
             stg16(hp, make_uint4(__float_as_uint(hv[0]), __float_as_uint(hv[1]), __float_as_uint(hv[2]),
@@ -673,6 +759,22 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     SS_TRACE(7);
   }
 
+  // The first batch of down-projection weights and the shared-expert down rows of this workgroup's output rows are
+  // requested only now, after the gate/up items are published: they are needed after the wait for every item, and
+  // requested earlier they would queue ahead of the items' own loads.
+  if (has_tile) {
+#pragma unroll 1
+    for (int u = w; u < nu && u < D.P; u += 4) issue_down(u, u);
+  }
+  uint4 shw[4];
+  if (verify && has_tile) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int srow = 16 * bid + 4 * w + rr;
+      shw[rr] = ldg16(a.sh_down + (size_t)srow * a.Is + 8 * (8 * lane < a.Is ? lane : 0));
+    }
+  }
+
   // ------------------------------------------------------------ phase D: down + combine
   if (has_tile) {
     if (tid == 0) {
@@ -685,15 +787,18 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     // Stage the h fragments of every use into LDS (1 KB per wave instruction) and the h group sums.
     const int hchunks = D.stage_h ? nq * I * 4 / 1024 : 0;
 #pragma unroll 1
-    for (int c = w; c < hchunks; c += 4) dma16(reinterpret_cast<const uint8_t*>(hfrag) + (size_t)c * 1024 + 16 * lane,
+    for (int c = w; c < hchunks; c += 4) dma16_ag(reinterpret_cast<const uint8_t*>(hfrag) + (size_t)c * 1024 + 16 * lane,
                                                reinterpret_cast<uint8_t*>(hfl) + (size_t)c * 1024);
     for (int idx = tid; idx < nq * (I >> 6); idx += 256) {
       const int q = idx / (I >> 6), Gi = idx - q * (I >> 6);
       float sum = 0.f;
       if (s.use_u[q] >= 0) {
         const float* hp = hsum8 + (size_t)q * (I >> 3) + 8 * Gi;
-#pragma unroll 1
-        for (int c = 0; c < 8; ++c) sum = sum + hp[c];
+        const uint4 h0 = ld_ag16(hp), h1 = ld_ag16(hp + 4);
+        const float hv[8] = {__uint_as_float(h0.x), __uint_as_float(h0.y), __uint_as_float(h0.z), __uint_as_float(h0.w),
+                             __uint_as_float(h1.x), __uint_as_float(h1.y), __uint_as_float(h1.z), __uint_as_float(h1.w)};
+#pragma unroll
+        for (int c = 0; c < 8; ++c) sum = sum + hv[c];
       }
       s.hsum[q][Gi] = sum;
     }
@@ -736,7 +841,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
           bvw[j] = reinterpret_cast<const uint32_t*>(sl + (size_t)NJD * 1280 + (size_t)j * 256)[lane];
           const size_t fo = (((size_t)aq * NJD + j) * 4 + g) * 8 + apart * 4;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) av4[j][i] = STAGED ? hfl[fo + i] : ldg16(hfrag + fo + i);
+          for (int i = 0; i < 4; ++i) av4[j][i] = STAGED ? hfl[fo + i] : ld_ag16(hfrag + fo + i);
 #pragma unroll
           for (int r = 0; r < kTBv; ++r) hsv[j][r] = s.hsum[qr[r]][2 * j + my_half];
         }
@@ -763,8 +868,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
         }
 #pragma unroll
         for (int r = 0; r < kTBv; ++r) {
-          acc[r] = acc[r] + ss_shfl_xor(acc[r], 16);
-          acc[r] = acc[r] + ss_shfl_xor(acc[r], 32);
+          acc[r] = ss_rows_sum(acc[r]);
           if (g == 0) partl[((size_t)u * 16 + n) * kTBv + r] = acc[r];
         }
       };
@@ -785,11 +889,20 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
         for (int t = 0; t < kTBv; ++t) sacc[rr][t] = 0.f;
+      uint4 gqv[kTBv], uqv[kTBv];
+      const int li = 8 * lane < Is ? lane : 0;
+#pragma unroll
+      for (int t = 0; t < kTBv; ++t) {
+        const int tt = t < nt ? t : 0;
+        gqv[t] = ld_ag16(gsh + (size_t)tt * Is + 8 * li);
+        uqv[t] = ld_ag16(ush + (size_t)tt * Is + 8 * li);
+      }
+      __builtin_amdgcn_sched_barrier(0);
       if (8 * lane < Is) {
-#pragma unroll 1
-        for (int t = 0; t < nt; ++t) {
-          const uint4 gq = reinterpret_cast<const uint4*>(gsh + (size_t)t * Is)[lane];
-          const uint4 uq = reinterpret_cast<const uint4*>(ush + (size_t)t * Is)[lane];
+#pragma unroll
+        for (int t = 0; t < kTBv; ++t) {
+          if (t >= nt) break;
+          const uint4 gq = gqv[t], uq = uqv[t];
           const uint32_t gw4[4] = {gq.x, gq.y, gq.z, gq.w}, uw4[4] = {uq.x, uq.y, uq.z, uq.w};
           float hsv[8];
 #pragma unroll
@@ -815,6 +928,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       for (int rr = 0; rr < 4; ++rr)
 #pragma unroll
         for (int t = 0; t < kTBv; ++t) {
+          if (t >= nt) break;
           const float v = ss_wave_sum(sacc[rr][t]);
           if (lane == 0) s.shv[4 * w + rr][t] = v;
         }
@@ -835,7 +949,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
         if (a.out) a.out[(size_t)r * H + 16 * bid + c] = acc;
         if (verify) {
           const float shb = ss_round_bf16(s.shv[c][r]);
-          const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-ss_bf16_to_f32(sgl[r]))));
+          const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-ss_bf16_to_f32(ld_ag(sgl + r)))));
           const float sh2 = ss_round_bf16(sgv * shb);
           a.y[(size_t)r * H + 16 * bid + c] = (uint16_t)ss_f32_to_bf16(ss_round_bf16(acc) + sh2);
         }
