@@ -37,7 +37,13 @@ constexpr int kSpinMax = 1 << 22;
 constexpr int SS_ERR_TIMEOUT = 16;
 constexpr size_t kLdsBudget = 160 * 1024 - 16 * 1024;  // dynamic LDS left after the static part (< 16 KB)
 
-enum { CTR_ROUTER = 0, CTR_SHARED = 16, CTR_ITEMS = 32, CTR_EXIT = 48 };
+// Counters are sharded: workgroup b adds to shard b % kShards of a counter, and a waiter sums the shards. Each
+// shard has a 128-byte line of its own; many workgroups adding to one address serialise at the memory-side atomic
+// unit (tens of ns each), which with 256 workgroups delays the moment the count is complete by microseconds.
+constexpr int kShards = 16;
+constexpr int kShardStride = 32;  // ints
+enum { CTR_ROUTER = 0, CTR_SHARED = 1, CTR_ITEMS = 2, CTR_EXIT = 3, CTR_TOP = 4, CTR_COUNT = 5 };
+SS_DEV int* shard(int* ctr, int c, int s) { return ctr + (c * kShards + s) * kShardStride; }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 // Pointers that reach the kernel through the argument struct or LDS are generic (flat) unless cast: flat accesses
@@ -71,7 +77,7 @@ static __host__ __device__ inline VLayout vlayout(int T, int I, int Is, int K, i
   VLayout l;
   size_t o = 0;
   l.ctr = o;
-  o = al256(o + 256);
+  o = al256(o + (size_t)CTR_COUNT * kShards * kShardStride * 4);
   l.logits = o;
   o = al256(o + (size_t)T * E * 2);
   l.gsh = o;
@@ -138,16 +144,21 @@ static __host__ __device__ inline DLayout dlayout(int T, int H, int I, int K, in
 // loads are issued after the poll has seen the count.
 SS_DEV void stores_done() { __builtin_amdgcn_s_waitcnt(0); }
 
-SS_DEV void signal_add(int* c, int v) {
+SS_DEV void signal_add(int* ctr, int c, int v) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-  __hip_atomic_fetch_add(c, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __hip_atomic_fetch_add(shard(ctr, c, blockIdx.x % kShards), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-SS_DEV void wait_ge(int* c, int target, int* err) {
+// Called by every lane of one wave: lanes 0 .. kShards-1 read one shard each, the butterfly sums them.
+SS_DEV void wait_ge(int* ctr, int c, int target, int* err) {
+  const int lane = threadIdx.x & 63;
+  int* p = shard(ctr, c, lane < kShards ? lane : 0);
   for (int it = 0;; ++it) {
-    if (__hip_atomic_load(c, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >= target) break;
+    const int v = lane < kShards ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+    const int total = (int)ss_butterfly((uint32_t)v, [](uint32_t x, uint32_t y) { return x + y; });
+    if (total >= target) break;
     if (it >= kSpinMax) {
-      ss_raise(err, SS_ERR_TIMEOUT);
+      if (lane == 0) ss_raise(err, SS_ERR_TIMEOUT);
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -304,30 +315,41 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint16_t* logits, int t,
     acc = acc + (lane + 64 * i < E ? v[i] : 0.f);
   }
   const float z = ss_wave_sum(acc);
-  uint64_t cand[NV];
+  // kp = key + 1 for a present, untaken entry (NaN probabilities have key 0, so kp 1), 0 once taken or absent.
+  uint32_t kp[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    const int e = lane + 64 * i;
     v[i] = v[i] / z;
-    cand[i] = e < E ? ((uint64_t)ss_key(v[i]) << 32) | (uint64_t)(0xFFFFFFFFu - (uint32_t)e) : 0ull;
+    kp[i] = lane + 64 * i < E ? ss_key(v[i]) + 1u : 0u;
   }
   float mine = 0.f, sum = 0.f;
   int my_id = 0;
 #pragma unroll 1
   for (int r = 0; r < K; ++r) {
-    uint64_t best = 0;
+    uint32_t lm = kp[0];
 #pragma unroll
-    for (int i = 0; i < NV; ++i) best = cand[i] > best ? cand[i] : best;
-    best = ss_wave_max_u64(best);
-    const int bi = (int)(0xFFFFFFFFu - (uint32_t)best);
-    const int li = __builtin_amdgcn_readfirstlane(bi & 63), ii = __builtin_amdgcn_readfirstlane(bi >> 6);
+    for (int i = 1; i < NV; ++i) lm = kp[i] > lm ? kp[i] : lm;
+    const uint32_t mx = ss_wave_max_u32(lm);
+    // The lowest index e = lane + 64 i holding mx: per lane the lowest such i, then across lanes the lowest e.
+    int li = NV;
+#pragma unroll
+    for (int i = NV - 1; i >= 0; --i) li = kp[i] == mx ? i : li;
+    const uint32_t code = (uint32_t)(li * 64 + lane);  // = e where this lane holds mx, >= 64 NV otherwise
+    const uint64_t holders = __ballot(li < NV);
+    uint32_t best;
+    if (__popcll(holders) == 1)
+      best = (uint32_t)__builtin_amdgcn_readlane((int)code, (int)__builtin_ctzll(holders));
+    else
+      best = ss_wave_min_u32(code);
+    const int bi = __builtin_amdgcn_readfirstlane((int)best);
+    const int wl = bi & 63, wi = bi >> 6;
     float pl = v[0];
 #pragma unroll
-    for (int i = 1; i < NV; ++i) pl = i == ii ? v[i] : pl;
-    const float pv = ss_readlane_f(pl, li);
-    const bool own = lane == li;
+    for (int i = 1; i < NV; ++i) pl = i == wi ? v[i] : pl;
+    const float pv = ss_readlane_f(pl, wl);
+    const bool own = lane == wl;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) cand[i] = own && i == ii ? 0ull : cand[i];
+    for (int i = 0; i < NV; ++i) kp[i] = own && i == wi ? 0u : kp[i];
     sum = sum + pv;  // rank-order sum of the top-k probabilities
     mine = lane == r ? pv : mine;
     my_id = lane == r ? bi : my_id;
@@ -455,6 +477,64 @@ SS_DEV void dense_dot(const uint4 (&wv)[NJX], const uint4* xfl, int nt, float ou
   }
 }
 
+// Shared-expert down rows 16 b + r0 + rr (rr < NR) of workgroup b, by one wave, in the dense_rows order:
+// hs = bf16(bf16(silu(g)) * u) from the bf16 gate / up projections, then the dot with the bf16 down row;
+// s.shv[r0 + rr][t] receives the fp32 sums. sh_w holds each row's 8 elements of this lane (Is <= 512).
+template <int NR>
+SS_DEV void shared_down_rows(const VerifyArgs& a, const uint16_t* gsh, const uint16_t* ush, const uint4 (&sh_w)[NR],
+                             int r0, int nt, VSmem& s) {
+  const int lane = threadIdx.x & 63;
+  const int Is = a.Is;
+  float sacc[NR][kTBv];
+#pragma unroll
+  for (int rr = 0; rr < NR; ++rr)
+#pragma unroll
+    for (int t = 0; t < kTBv; ++t) sacc[rr][t] = 0.f;
+  uint4 gqv[kTBv], uqv[kTBv];
+  const int li = 8 * lane < Is ? lane : 0;
+#pragma unroll
+  for (int t = 0; t < kTBv; ++t) {
+    const int tt = t < nt ? t : 0;
+    gqv[t] = ld_ag16(gsh + (size_t)tt * Is + 8 * li);
+    uqv[t] = ld_ag16(ush + (size_t)tt * Is + 8 * li);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (8 * lane < Is) {
+#pragma unroll
+    for (int t = 0; t < kTBv; ++t) {
+      if (t >= nt) break;
+      const uint4 gq = gqv[t], uq = uqv[t];
+      const uint32_t gw4[4] = {gq.x, gq.y, gq.z, gq.w}, uw4[4] = {uq.x, uq.y, uq.z, uq.w};
+      float hsv[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float gv = (e & 1) ? bf_hi(gw4[e >> 1]) : bf_lo(gw4[e >> 1]);
+        const float uv = (e & 1) ? bf_hi(uw4[e >> 1]) : bf_lo(uw4[e >> 1]);
+        const float sv = ss_round_bf16(gv / (1.f + ss_expf(-gv)));
+        hsv[e] = ss_round_bf16(sv * uv);
+      }
+#pragma unroll
+      for (int rr = 0; rr < NR; ++rr) {
+        const uint32_t ww[4] = {sh_w[rr].x, sh_w[rr].y, sh_w[rr].z, sh_w[rr].w};
+        float ac = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ac = __builtin_fmaf(hsv[e], (e & 1) ? bf_hi(ww[e >> 1]) : bf_lo(ww[e >> 1]), ac);
+#pragma unroll
+        for (int q = 0; q < kTBv; ++q)
+          if (q == t) sacc[rr][q] = ac;
+      }
+    }
+  }
+#pragma unroll
+  for (int rr = 0; rr < NR; ++rr)
+#pragma unroll
+    for (int t = 0; t < kTBv; ++t) {
+      if (t >= nt) break;
+      const float v = ss_wave_sum(sacc[rr][t]);
+      if (lane == 0) s.shv[r0 + rr][t] = v;
+    }
+}
+
 template <int NJG, int NJD, bool XF32>
 __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec) {
   extern __shared__ uint4 dsm[];
@@ -486,7 +566,6 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   } while (0)
 
   SS_TRACE(0);
-  if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + 12] = __builtin_amdgcn_s_memtime();
   for (int i = tid; i < kMaxQv * kTBv; i += 256) (&s.umask[0][0])[i] = 0u;
   if (tid == 0) s.nt = nt;
 
@@ -498,6 +577,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   constexpr int NJX = NJG / 4;  // 16-byte words per lane of one dense row (H / 512)
   const int Is = a.Is, J = verify ? E + Is : 0, W = G * 4;
   const int j_first = bid * 4 + w;
+  const bool has_tile = bid < (H >> 4);
+  // With at most two tokens, waves 2 and 3 are free during the router tail and do the shared-expert down rows.
+  const bool early_shared = verify && has_tile && nt <= 2;
+  uint4 shw8[8];
   uint4 r0[NJX], r1[NJX], r2[NJX];
   auto load_job = [&](int j) {
     const uint16_t* w0 = j < E ? a.router_w + (size_t)j * H : a.sh_gate + (size_t)(j - E) * H;
@@ -560,8 +643,8 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
           if (j < E) nr += 1;
           else ns += j == J - 1 ? 2 : 1;
         }
-      if (nr) signal_add(ctr + CTR_ROUTER, nr);
-      if (ns) signal_add(ctr + CTR_SHARED, ns);
+      if (nr) signal_add(ctr, CTR_ROUTER, nr);
+      if (ns) signal_add(ctr, CTR_SHARED, ns);
       SS_TRACE(1);
     }
     // The layer's slot pointers into LDS and the routing bias into the tail waves' registers while the other
@@ -588,12 +671,24 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
         s.base_e[e] = base_k[k];
       }
     }
-    if (tid == 0) {
-      wait_ge(ctr + CTR_ROUTER, E, a.err);
-      SS_TRACE(2);
+    if (early_shared && w >= 2) {
+#pragma unroll
+      for (int rr = 0; rr < 8; ++rr)
+        shw8[rr] = ldg16(a.sh_down + (size_t)(16 * bid + 8 * (w - 2) + rr) * Is + 8 * (8 * lane < Is ? lane : 0));
     }
+    if (w == 0) wait_ge(ctr, CTR_ROUTER, E, a.err);
+    SS_TRACE(2);
     __syncthreads();
-    if (w < nt) router_tail_wave(a, logits, w, s, bias_r);
+    if (w < nt) {
+      router_tail_wave(a, logits, w, s, bias_r);
+      if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + 12] = __builtin_amdgcn_s_memrealtime();
+    } else if (early_shared && w >= 2) {
+      // Waves the router tail leaves idle compute this workgroup's shared-expert down rows now (8 rows each),
+      // which takes them off the end of the launch.
+      wait_ge(ctr, CTR_SHARED, Is + 1, a.err);
+      shared_down_rows<8>(a, gsh, ush, shw8, 8 * (w - 2), nt, s);
+      if (a.trace && tid == 128) a.trace[(size_t)bid * 16 + 13] = __builtin_amdgcn_s_memrealtime();
+    }
     __syncthreads();
     SS_TRACE(3);
     if (bid == 0 && tid < nt * K) {
@@ -613,7 +708,6 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   const int nu = s.nu;
   const int tiles = I >> 3;
   const int n_items = nu * tiles;
-  const bool has_tile = bid < (H >> 4);
   const int my_half = g >> 1, my_part = g & 1;
   const int drow = 16 * bid + n;  // down row of this lane
   const int64_t drow_b = I >> 1, dsb_b = (I >> 6) * 2;
@@ -755,7 +849,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     }
     stores_done();
     __syncthreads();
-    if (tid == 0) signal_add(ctr + CTR_ITEMS, my_items);
+    if (tid == 0) signal_add(ctr, CTR_ITEMS, my_items);
     SS_TRACE(7);
   }
 
@@ -767,7 +861,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     for (int u = w; u < nu && u < D.P; u += 4) issue_down(u, u);
   }
   uint4 shw[4];
-  if (verify && has_tile) {
+  if (verify && has_tile && !early_shared) {
 #pragma unroll
     for (int rr = 0; rr < 4; ++rr) {
       const int srow = 16 * bid + 4 * w + rr;
@@ -777,9 +871,9 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 
   // ------------------------------------------------------------ phase D: down + combine
   if (has_tile) {
-    if (tid == 0) {
-      wait_ge(ctr + CTR_ITEMS, n_items, a.err);
-      if (verify) wait_ge(ctr + CTR_SHARED, a.Is + 1, a.err);
+    if (w == 0) {
+      wait_ge(ctr, CTR_ITEMS, n_items, a.err);
+      if (verify && !early_shared) wait_ge(ctr, CTR_SHARED, a.Is + 1, a.err);
     }
     __syncthreads();
     SS_TRACE(8);
@@ -881,58 +975,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       }
     }
     SS_TRACE(10);
-    if (verify) {
-      // Shared-expert down rows 16b + 4w + rr in the dense_rows order; hs = bf16(bf16(silu(g)) * u).
-      const int Is = a.Is;
-      float sacc[4][kTBv];
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-        for (int t = 0; t < kTBv; ++t) sacc[rr][t] = 0.f;
-      uint4 gqv[kTBv], uqv[kTBv];
-      const int li = 8 * lane < Is ? lane : 0;
-#pragma unroll
-      for (int t = 0; t < kTBv; ++t) {
-        const int tt = t < nt ? t : 0;
-        gqv[t] = ld_ag16(gsh + (size_t)tt * Is + 8 * li);
-        uqv[t] = ld_ag16(ush + (size_t)tt * Is + 8 * li);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-      if (8 * lane < Is) {
-#pragma unroll
-        for (int t = 0; t < kTBv; ++t) {
-          if (t >= nt) break;
-          const uint4 gq = gqv[t], uq = uqv[t];
-          const uint32_t gw4[4] = {gq.x, gq.y, gq.z, gq.w}, uw4[4] = {uq.x, uq.y, uq.z, uq.w};
-          float hsv[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            const float gv = (e & 1) ? bf_hi(gw4[e >> 1]) : bf_lo(gw4[e >> 1]);
-            const float uv = (e & 1) ? bf_hi(uw4[e >> 1]) : bf_lo(uw4[e >> 1]);
-            const float sv = ss_round_bf16(gv / (1.f + ss_expf(-gv)));
-            hsv[e] = ss_round_bf16(sv * uv);
-          }
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const uint32_t ww[4] = {shw[rr].x, shw[rr].y, shw[rr].z, shw[rr].w};
-            float ac = 0.f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) ac = __builtin_fmaf(hsv[e], (e & 1) ? bf_hi(ww[e >> 1]) : bf_lo(ww[e >> 1]), ac);
-#pragma unroll
-            for (int q = 0; q < kTBv; ++q)
-              if (q == t) sacc[rr][q] = ac;
-          }
-        }
-      }
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-#pragma unroll
-        for (int t = 0; t < kTBv; ++t) {
-          if (t >= nt) break;
-          const float v = ss_wave_sum(sacc[rr][t]);
-          if (lane == 0) s.shv[4 * w + rr][t] = v;
-        }
-    }
+    if (verify && !early_shared) shared_down_rows<4>(a, gsh, ush, shw, 4 * w, nt, s);
     __syncthreads();
     if (tid < 16 * kTBv) {
       const int c = tid >> 2, r = tid & 3;
@@ -960,15 +1003,20 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   // ------------------------------------------------------------ exit: the last workgroup resets the counters
   __syncthreads();
   SS_TRACE(11);
-  if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + 13] = __builtin_amdgcn_s_memtime();
 #undef SS_TRACE
   if (tid == 0) {
-    const int ticket = __hip_atomic_fetch_add(ctr + CTR_EXIT, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (ticket == G - 1) {
-      __hip_atomic_store(ctr + CTR_ROUTER, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctr + CTR_SHARED, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctr + CTR_ITEMS, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctr + CTR_EXIT, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Two-level exit ticket: the last workgroup of each shard takes a ticket on the top counter; the last of those
+    // resets every shard (all other workgroups have made their last counter access).
+    const int sh = bid % kShards;
+    const int in_shard = (G - sh + kShards - 1) / kShards;
+    const int t1 = __hip_atomic_fetch_add(shard(ctr, CTR_EXIT, sh), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t1 == in_shard - 1) {
+      const int t2 = __hip_atomic_fetch_add(shard(ctr, CTR_TOP, 0), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t2 == (G < kShards ? G : kShards) - 1) {
+        for (int c = 0; c < CTR_COUNT; ++c)
+          for (int q = 0; q < kShards; ++q)
+            __hip_atomic_store(shard(ctr, c, q), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
   }
 }
