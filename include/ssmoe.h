@@ -72,6 +72,12 @@ int ssmoe_dense_gemv_bf16(const uint16_t* x, const uint16_t* w, uint16_t* out, i
 int ssmoe_router(const uint16_t* x, const uint16_t* router_w, const float* bias, uint16_t* logits, float* probs,
                  int32_t* ids, float* weights, int T, int H, int E, int K, void* stream);
 
+/* The routing half of ssmoe_router from given bf16 logits [T, E] (prefill computes the logits with a GEMM):
+ * scores = logits (+ bias), fp32 softmax, top-k with ties to the lower index, renormalised weights.
+ * Replaces the softmax / topk_stable / renorm of Segments.seg_router (model/layers.py:340-347). */
+int ssmoe_router_topk(const uint16_t* logits, const float* bias, float* probs, int32_t* ids, float* weights, int T,
+                      int E, int K, void* stream);
+
 /* Bytes of the workspace ssmoe_moe_verify_layer needs for T tokens. */
 int64_t ssmoe_verify_workspace_bytes(int T, int H, int I, int Is, int K, int E);
 
@@ -108,6 +114,51 @@ int ssmoe_accept_greedy(const float* target, const int32_t* drafts, int D, int V
 int ssmoe_accept_pq(const float* target, const float* draft, const int32_t* drafts, const float* uniforms, int D,
                     int V, float temperature, void* workspace, int64_t workspace_bytes, int32_t* out,
                     void* stream);
+
+/* ---------------------------------------------------------------- prefill */
+
+/* Padded length of a moe_align plan: R + num_local * (block_m - 1), rounded up to a multiple of block_m.
+ * Replaces padded_rows (kernels/moe_align.py:11-14). Returns -1 on bad arguments. */
+int64_t ssmoe_padded_rows(int64_t R, int num_local, int block_m);
+
+/* Bytes of the scratch ssmoe_moe_align needs. */
+int64_t ssmoe_moe_align_workspace_bytes(int64_t R, int num_local);
+
+/* Stable counting sort of rows by local expert. Replaces moe_align (kernels/moe_align.py:17-48).
+ * local_expert int32 [R] (outside [0, num_local) = row skipped); outputs sorted_rows int32 [padded] (row ids,
+ * sentinel R in the padding), block_expert int32 [padded / block_m] (expert of each block, -1 past num_padded),
+ * num_padded int32 [1]. Deterministic: no order-dependent atomics. */
+int ssmoe_moe_align(const int32_t* local_expert, int64_t R, int num_local, int block_m, void* workspace,
+                    int64_t workspace_bytes, int32_t* sorted_rows, int32_t* block_expert, int32_t* num_padded,
+                    void* stream);
+
+/* Grouped affine-4bit MoE over an aligned plan (block_m = 64): h = bf16(silu(x Wg^T) * (x Wu^T)) with weights
+ * dequantized to bf16(q*s + b), bf16 MFMA and fp32 accumulation, then out_rows = (h Wd^T) * row_weight in fp32.
+ * Replaces fused_moe_affine's two launches (kernels/fused_moe_affine.py:136-161, kernels :39-108).
+ * x bf16 [T, H]; row_token int32 [R] (a token outside [0, T) reads as a zero row); row_weight fp32 [R];
+ * group_ptr int64 [num_local] record bases; h_buf bf16
+ * [R, I]; out_rows fp32 [R, H] (rows outside the plan are not written). H % 128 == 0, I % 64 == 0. */
+int ssmoe_fused_moe_affine(const uint16_t* x, const int32_t* row_token, const float* row_weight,
+                           const int32_t* sorted_rows, const int32_t* block_expert, const int32_t* num_padded,
+                           const int64_t* group_ptr, int num_local, uint16_t* h_buf, float* out_rows, int64_t R,
+                           int T, int H, int I, void* stream);
+
+/* out[t] = ((rows[t*K] + rows[t*K+1]) + ...) + rows[t*K+K-1], fp32, sequential in router rank order.
+ * Replaces combine_rank_order (kernels/fused_moe_affine.py:164-172). */
+int ssmoe_combine_rank_order(const float* out_rows, int T, int K, int H, float* out, void* stream);
+
+/* Bytes of the workspace ssmoe_moe_prefill needs. */
+int64_t ssmoe_moe_prefill_workspace_bytes(int64_t T, int K, int E);
+
+/* Routed experts of one layer over T prompt tokens with every expert resident: the sweep of SweepMoE.layer
+ * (model/moe_sweep.py:80-160, plan_sweep engine/sweep.py:34-58) as one plan over all E experts (no staging
+ * groups), i.e. moe_align + ssmoe_fused_moe_affine + ssmoe_combine_rank_order. expert_ids int32 [T, K];
+ * weights fp32 [T, K]; records at slot_ptr[map[layer * E + e]]; h_buf bf16 [T*K, I]; out_rows fp32 [T*K, H];
+ * out fp32 [T, H]. An expert id outside [0, E) or an unmapped expert raises a status bit and its row counts as 0. */
+int ssmoe_moe_prefill(const uint16_t* x, const int32_t* expert_ids, const float* weights, int layer,
+                      const int32_t* map, int64_t map_len, const int64_t* slot_ptr, int64_t n_slots, void* workspace,
+                      int64_t workspace_bytes, uint16_t* h_buf, float* out_rows, float* out, int64_t T, int H, int I,
+                      int K, int E, void* stream);
 
 #ifdef __cplusplus
 }

@@ -297,3 +297,84 @@ def uniforms(seed: int, n: int) -> np.ndarray:
         st = splitmix((st + 1) & _M64)
         out[i] = np.float32((st >> 11) / float(1 << 53))
     return out
+
+
+# ---------------------------------------------------------------- prefill (kernels/moe_align.py, fused_moe_affine.py)
+def padded_rows(r: int, num_local: int, block_m: int) -> int:
+    n = r + num_local * (block_m - 1)
+    return (n + block_m - 1) // block_m * block_m
+
+
+def moe_align(local_expert, num_local: int, block_m: int):
+    """kernels/moe_align.py:17-48 restated in numpy: (sorted_rows, block_expert, num_padded)."""
+    le = np.asarray(local_expert, dtype=np.int64)
+    r = le.size
+    p = padded_rows(r, num_local, block_m)
+    key = np.where((le >= 0) & (le < num_local), le, num_local)
+    order = np.argsort(key, kind="stable")
+    counts = np.bincount(key, minlength=num_local + 1)[:num_local]
+    padded = (counts + block_m - 1) // block_m * block_m
+    pad_end = np.cumsum(padded)
+    pad_start = pad_end - padded
+    start = np.cumsum(counts) - counts
+    sorted_rows = np.full(p, r, dtype=np.int32)
+    ks = key[order]
+    for j, (row, k) in enumerate(zip(order, ks)):
+        if k < num_local:
+            sorted_rows[pad_start[k] + j - start[k]] = row
+    nb = p // block_m
+    pos = np.arange(nb, dtype=np.int64) * block_m
+    idx = np.searchsorted(pad_end, pos, side="right")
+    block_expert = np.where(idx < num_local, idx, -1).astype(np.int32)
+    num_padded = int(pad_end[-1]) if num_local else 0
+    return sorted_rows, block_expert, num_padded
+
+
+def dequant_bf16(q, s_bits, b_bits, gs=64) -> np.ndarray:
+    """bf16(q * s + b) as float32 (the reference's _wtile, fused_moe_affine.py:39-50): q*s is exact in fp32, so the
+    fp32 value of q*s + b has one rounding whether or not it is fused."""
+    w = dequant(q, s_bits, b_bits, gs, np.float32)
+    return bf16_to_f32(f32_to_bf16(w))
+
+
+def expert_bf16(rec, H, I):
+    """(gate [I, H], up [I, H], down [H, I]) as float64 arrays of the bf16-rounded dequantized weights."""
+    return tuple(dequant_bf16(q, s, b).astype(np.float64) for (q, s, b) in unpack_record(rec, H, I))
+
+
+def prefill_rows(x, row_token, row_weight, row_expert, weights_of):
+    """fused_moe_affine semantics per row (fp64 accumulation of bf16 operands): h = bf16(silu(g) * u), then
+    out_rows[r] = fp32((Wd h) * w). x float array [T, H] holding bf16 values; weights_of(e) -> expert_bf16 tuple.
+    Rows whose expert is negative are zero. Returns (h float32 [R, I] of bf16 values, out_rows float32 [R, H])."""
+    x = np.asarray(x, np.float64)
+    row_expert = np.asarray(row_expert)
+    R = row_expert.size
+    H = x.shape[1]
+    I = None
+    out = np.zeros((R, H), np.float32)
+    hs = None
+    for e in np.unique(row_expert):
+        if e < 0:
+            continue
+        rows = np.nonzero(row_expert == e)[0]
+        g_w, u_w, d_w = weights_of(int(e))
+        if hs is None:
+            I = g_w.shape[0]
+            hs = np.zeros((R, I), np.float32)
+        xr = x[np.asarray(row_token)[rows]]
+        g = xr @ g_w.T
+        u = xr @ u_w.T
+        h = bf16_to_f32(f32_to_bf16((g / (1.0 + np.exp(-g)) * u).astype(np.float32)))
+        hs[rows] = h
+        o = (h.astype(np.float64) @ d_w.T) * np.asarray(row_weight, np.float64)[rows, None]
+        out[rows] = o.astype(np.float32)
+    return hs, out
+
+
+def combine_rank_order(out_rows, T, K):
+    """Sequential fp32 sum of each token's K rows in rank order (fused_moe_affine.py:164-172)."""
+    v = np.asarray(out_rows, np.float32).reshape(T, K, -1)
+    acc = v[:, 0].copy()
+    for k in range(1, K):
+        acc = (acc + v[:, k]).astype(np.float32)
+    return acc

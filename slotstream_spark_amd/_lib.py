@@ -27,12 +27,20 @@ SIGNATURES = {
     "ssmoe_topk_stable": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "ssmoe_dense_gemv_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
     "ssmoe_router": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "ssmoe_router_topk": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "ssmoe_verify_workspace_bytes": (_I64, [_I, _I, _I, _I, _I, _I]),
     "ssmoe_moe_verify_layer": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _P, _I64, _P, _I64,
                                     _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "ssmoe_accept_workspace_bytes": (_I64, [_I, _I]),
     "ssmoe_accept_greedy": (_I, [_P, _P, _I, _I, _P, _I64, _P, _P]),
     "ssmoe_accept_pq": (_I, [_P, _P, _P, _P, _I, _I, _F, _P, _I64, _P, _P]),
+    "ssmoe_padded_rows": (_I64, [_I64, _I, _I]),
+    "ssmoe_moe_align_workspace_bytes": (_I64, [_I64, _I]),
+    "ssmoe_moe_align": (_I, [_P, _I64, _I, _I, _P, _I64, _P, _P, _P, _P]),
+    "ssmoe_fused_moe_affine": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I64, _I, _I, _I, _P]),
+    "ssmoe_combine_rank_order": (_I, [_P, _I, _I, _I, _P, _P]),
+    "ssmoe_moe_prefill_workspace_bytes": (_I64, [_I64, _I, _I]),
+    "ssmoe_moe_prefill": (_I, [_P, _P, _P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I, _I, _I, _I, _P]),
 }
 
 _lib = None

@@ -3,6 +3,7 @@
 Usage: python -m slotstream_spark_amd.build  (or build() from Python). Always recompiles.
 """
 import os
+import re
 import subprocess
 import sys
 from concurrent.futures import ThreadPoolExecutor
@@ -25,14 +26,25 @@ FLAGS = [
 
 def _compile(src: Path) -> Path:
     obj = BUILD / (src.stem + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(src), "-o", str(obj)]
     r = subprocess.run(cmd, capture_output=True, text=True)
-    noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in (r.stderr or "").splitlines() if noise not in l)
+    noise = ("is not a recognized feature for this target", "kernel-resource-usage")
+    lines = (r.stderr or "").splitlines()
+    err = "\n".join(l for l in lines if not any(n in l for n in noise))
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
     if err.strip():
         print(err, file=sys.stderr)
+    # No kernel may use private scratch: a spill or a local array addressed at run time means a slow (and, for
+    # selects of whole vectors, once miscompiled) path, so the build refuses it.
+    name = None
+    for line in lines:
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            name = m.group(1)
+        m = re.search(r"ScratchSize \[bytes/lane\]: (\d+)", line)
+        if m and int(m.group(1)) > 0:
+            raise RuntimeError(f"{src.name}: kernel {name} uses {m.group(1)} bytes of private scratch per lane")
     return obj
 
 

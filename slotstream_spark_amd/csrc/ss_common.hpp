@@ -21,6 +21,28 @@ enum {
   SS_ERR_NONFINITE = 8,    // non-finite logits reached a p/q decision
 };
 
+// ---------------------------------------------------------------- global-space access
+// Pointers that reach the kernel through the argument struct or LDS are generic (flat) unless cast: flat accesses
+// wait on both the vector-memory and LDS counters, so every hot global access goes through a global-space pointer.
+#define SS_G __attribute__((address_space(1)))
+template <class T>
+SS_DEV SS_G T* gp(T* p) {
+  return (SS_G T*)p;
+}
+// 16-byte global load / store through the builtin vector type (HIP's uint4 class does not take address spaces).
+SS_DEV uint4 ldg16(const void* p) {
+  const ss_u32x4 v = *(const SS_G ss_u32x4*)p;
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+SS_DEV void stg16(void* p, uint4 v) {
+  ss_u32x4 t;
+  t.x = v.x;
+  t.y = v.y;
+  t.z = v.z;
+  t.w = v.w;
+  *(SS_G ss_u32x4*)p = t;
+}
+
 // ---------------------------------------------------------------- bf16 <-> fp32
 SS_DEV float ss_bf16_to_f32(uint32_t b) { return __uint_as_float((b & 0xFFFFu) << 16); }
 

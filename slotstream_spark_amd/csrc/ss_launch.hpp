@@ -60,6 +60,45 @@ struct VerifyArgs {
 size_t verify_scratch_bytes(int T, int H, int I, int Is, int K, int E);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
 
+// Prefill (ss_prefill.hip).
+struct AlignArgs {
+  const int32_t* local_expert;  // [R]: local expert of each row, outside [0, num_local) = skipped
+  int64_t R;
+  int num_local, block_m;
+  int32_t* sorted_rows;   // [padded_rows(R, num_local, block_m)]
+  int32_t* block_expert;  // [padded / block_m]
+  int32_t* num_padded;    // [1]
+  int32_t* scratch;       // align_scratch_ints(R, num_local) ints
+};
+int64_t padded_rows(int64_t R, int num_local, int block_m);
+int64_t align_scratch_ints(int64_t R, int num_local);
+hipError_t launch_moe_align(const AlignArgs& a, hipStream_t st);
+
+constexpr int kPrefillBlockM = 64;  // the moe_align block the grouped GEMM consumes
+struct PrefillArgs {
+  const uint16_t* x;            // bf16 [T, H]
+  const int32_t* row_token;     // [R]
+  const float* row_weight;      // [R]
+  const int32_t* sorted_rows;   // moe_align plan with block_m = kPrefillBlockM
+  const int32_t* block_expert;
+  const int32_t* num_padded;
+  const int64_t* group_ptr;     // [num_local] record base addresses
+  int num_local;
+  uint16_t* h_buf;              // bf16 [R, I]
+  float* out_rows;              // fp32 [R, H]
+  int64_t R;
+  int T, H, I;                  // T: rows of x (a row_token outside [0, T) reads zeros)
+};
+hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st);
+// out[t] = sum over k (in order) of rows[t * K + k]; a row whose row_local entry is negative counts as +0.
+hipError_t launch_combine(const float* rows, const int32_t* row_local, int T, int K, int H, float* out,
+                          hipStream_t st);
+// Resident-pool tables of a prefill: group_ptr[e] from map/slot_ptr, local[r] = ids[r] (or -1, raising a status
+// bit, when the expert is out of range or not resident), row_token[r] = r / K.
+hipError_t launch_prefill_tables(const int32_t* map, int64_t map_base, int64_t map_len, const int64_t* slot_ptr,
+                                 int64_t n_slots, int E, int64_t* gptr, const int32_t* ids, int64_t R, int K,
+                                 int32_t* local, int32_t* row_token, int* err, hipStream_t st);
+
 // Acceptance.
 struct AcceptArgs {
   const float* target;   // [D+1, V]

@@ -46,27 +46,6 @@ enum { CTR_ROUTER = 0, CTR_SHARED = 1, CTR_ITEMS = 2, CTR_EXIT = 3, CTR_TOP = 4,
 SS_DEV int* shard(int* ctr, int c, int s) { return ctr + (c * kShards + s) * kShardStride; }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
-// Pointers that reach the kernel through the argument struct or LDS are generic (flat) unless cast: flat accesses
-// wait on both the vector-memory and LDS counters, so every hot global access goes through a global-space pointer.
-#define SS_G __attribute__((address_space(1)))
-template <class T>
-SS_DEV SS_G T* gp(T* p) {
-  return (SS_G T*)p;
-}
-// 16-byte global load / store through the builtin vector type (HIP's uint4 class does not take address spaces).
-SS_DEV uint4 ldg16(const void* p) {
-  const ss_u32x4 v = *(const SS_G ss_u32x4*)p;
-  return make_uint4(v.x, v.y, v.z, v.w);
-}
-SS_DEV void stg16(void* p, uint4 v) {
-  ss_u32x4 t;
-  t.x = v.x;
-  t.y = v.y;
-  t.z = v.z;
-  t.w = v.w;
-  *(SS_G ss_u32x4*)p = t;
-}
-
 struct VLayout {
   size_t ctr, logits, gsh, ush, sgl, hfrag, hsum8, total;
 };
@@ -420,10 +399,11 @@ SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], int nt) 
         hw[d] = b0 | (b1 << 16);
         lw[d] = ss_f32_to_bf16(e0[d] - ss_bf16_to_f32(b0)) | (ss_f32_to_bf16(e1[d] - ss_bf16_to_f32(b1)) << 16);
       }
-      xfl[2 * f] = live ? make_uint4(hw[0], hw[1], hw[2], hw[3]) : make_uint4(0u, 0u, 0u, 0u);
-      xfl[2 * f + 1] = live ? make_uint4(lw[0], lw[1], lw[2], lw[3]) : make_uint4(0u, 0u, 0u, 0u);
+      xfl[2 * f] = make_uint4(live ? hw[0] : 0u, live ? hw[1] : 0u, live ? hw[2] : 0u, live ? hw[3] : 0u);
+      xfl[2 * f + 1] = make_uint4(live ? lw[0] : 0u, live ? lw[1] : 0u, live ? lw[2] : 0u, live ? lw[3] : 0u);
     } else {
-      xfl[f] = live ? perm_pairs(fv[k][0]) : make_uint4(0u, 0u, 0u, 0u);
+      const uint4 pv = perm_pairs(fv[k][0]);
+      xfl[f] = make_uint4(live ? pv.x : 0u, live ? pv.y : 0u, live ? pv.z : 0u, live ? pv.w : 0u);
     }
   }
   if (tid < (H >> 6) * kTBv) {

@@ -214,6 +214,15 @@ int ssmoe_router(const uint16_t* x, const uint16_t* router_w, const float* bias,
   return hip_check(ss::launch_router_topk(logits, bias, probs, ids, weights, T, E, K, st), "router topk launch");
 }
 
+int ssmoe_router_topk(const uint16_t* logits, const float* bias, float* probs, int32_t* ids, float* weights, int T,
+                      int E, int K, void* stream) {
+  if (T < 1 || E < 1 || E > 8192 || K < 1 || K > 16 || K > E)
+    return fail(SSMOE_EINVAL, "need T >= 1 and 1 <= K <= min(16, E), E <= 8192 (T=%d E=%d K=%d)", T, E, K);
+  if (!logits || !ids || !weights) return fail(SSMOE_EINVAL, "logits, ids and weights must be non-null");
+  return hip_check(ss::launch_router_topk(logits, bias, probs, ids, weights, T, E, K, static_cast<hipStream_t>(stream)),
+                   "router top-k launch");
+}
+
 int64_t ssmoe_verify_workspace_bytes(int T, int H, int I, int Is, int K, int E) {
   if (T < 1 || Is < 1 || I < 1 || K < 1 || E < 1) return -1;
   (void)T;
@@ -328,6 +337,187 @@ int ssmoe_accept_pq(const float* target, const float* draft, const int32_t* draf
   a.work = static_cast<float*>(workspace);
   a.err = err;
   return hip_check(ss::launch_accept_pq(a, static_cast<hipStream_t>(stream)), "accept pq launch");
+}
+
+// ---------------------------------------------------------------- prefill
+int64_t ssmoe_padded_rows(int64_t R, int num_local, int block_m) {
+  if (R < 0 || num_local < 1 || block_m < 1) return -1;
+  return ss::padded_rows(R, num_local, block_m);
+}
+
+int64_t ssmoe_moe_align_workspace_bytes(int64_t R, int num_local) {
+  if (R < 0 || num_local < 1) return -1;
+  return ss::align_scratch_ints(R, num_local) * 4;
+}
+
+static int check_align(int64_t R, int num_local, int block_m) {
+  if (R < 0 || R > (1ll << 30)) return fail(SSMOE_EINVAL, "R must be in [0, 2^30], got %lld", (long long)R);
+  if (num_local < 1 || num_local > 4096) return fail(SSMOE_EINVAL, "num_local must be in [1, 4096], got %d", num_local);
+  if (block_m < 1 || block_m > 1024) return fail(SSMOE_EINVAL, "block_m must be in [1, 1024], got %d", block_m);
+  return ok();
+}
+
+int ssmoe_moe_align(const int32_t* local_expert, int64_t R, int num_local, int block_m, void* workspace,
+                    int64_t workspace_bytes, int32_t* sorted_rows, int32_t* block_expert, int32_t* num_padded,
+                    void* stream) {
+  if (int rc = check_align(R, num_local, block_m)) return rc;
+  if ((R > 0 && !local_expert) || !workspace || !sorted_rows || !block_expert || !num_padded)
+    return fail(SSMOE_EINVAL, "local_expert, workspace and the three outputs must be non-null");
+  if (workspace_bytes < ss::align_scratch_ints(R, num_local) * 4)
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)(ss::align_scratch_ints(R, num_local) * 4));
+  ss::AlignArgs a{};
+  a.local_expert = local_expert;
+  a.R = R;
+  a.num_local = num_local;
+  a.block_m = block_m;
+  a.sorted_rows = sorted_rows;
+  a.block_expert = block_expert;
+  a.num_padded = num_padded;
+  a.scratch = static_cast<int32_t*>(workspace);
+  return hip_check(ss::launch_moe_align(a, static_cast<hipStream_t>(stream)), "moe_align launch");
+}
+
+static int check_prefill_shape(int64_t R, int H, int I) {
+  if (R < 0 || R > (1ll << 30)) return fail(SSMOE_EINVAL, "R must be in [0, 2^30], got %lld", (long long)R);
+  if (H < 128 || H % 128) return fail(SSMOE_EINVAL, "H must be a positive multiple of 128, got %d", H);
+  if (I < 64 || I % 64) return fail(SSMOE_EINVAL, "I must be a positive multiple of 64, got %d", I);
+  return ok();
+}
+
+int ssmoe_fused_moe_affine(const uint16_t* x, const int32_t* row_token, const float* row_weight,
+                           const int32_t* sorted_rows, const int32_t* block_expert, const int32_t* num_padded,
+                           const int64_t* group_ptr, int num_local, uint16_t* h_buf, float* out_rows, int64_t R,
+                           int T, int H, int I, void* stream) {
+  if (int rc = check_prefill_shape(R, H, I)) return rc;
+  if (T < 0) return fail(SSMOE_EINVAL, "T must be >= 0, got %d", T);
+  if (num_local < 1) return fail(SSMOE_EINVAL, "num_local must be >= 1, got %d", num_local);
+  if (R == 0) return ok();
+  if (!x || !row_token || !row_weight || !sorted_rows || !block_expert || !num_padded || !group_ptr || !h_buf ||
+      !out_rows)
+    return fail(SSMOE_EINVAL, "every pointer must be non-null");
+  if (!aligned(x, 16) || !aligned(h_buf, 16)) return fail(SSMOE_EINVAL, "x and h_buf must be 16-byte aligned");
+  ss::PrefillArgs p{};
+  p.x = x;
+  p.row_token = row_token;
+  p.row_weight = row_weight;
+  p.sorted_rows = sorted_rows;
+  p.block_expert = block_expert;
+  p.num_padded = num_padded;
+  p.group_ptr = group_ptr;
+  p.num_local = num_local;
+  p.h_buf = h_buf;
+  p.out_rows = out_rows;
+  p.R = R;
+  p.T = T;
+  p.H = H;
+  p.I = I;
+  return hip_check(ss::launch_prefill_gemm(p, static_cast<hipStream_t>(stream)), "fused_moe_affine launch");
+}
+
+int ssmoe_combine_rank_order(const float* out_rows, int T, int K, int H, float* out, void* stream) {
+  if (T < 0 || K < 1 || H < 4 || H % 4) return fail(SSMOE_EINVAL, "need T >= 0, K >= 1, H a multiple of 4");
+  if (T > 0 && (!out_rows || !out)) return fail(SSMOE_EINVAL, "out_rows and out must be non-null");
+  if (!aligned(out_rows, 16) || !aligned(out, 16)) return fail(SSMOE_EINVAL, "out_rows and out must be 16-byte aligned");
+  return hip_check(ss::launch_combine(out_rows, nullptr, T, K, H, out, static_cast<hipStream_t>(stream)),
+                   "combine launch");
+}
+
+// Workspace of ssmoe_moe_prefill: local [R], row_token [R], group_ptr [E] (8-byte), sorted_rows [P],
+// block_expert [P / 64], num_padded, then the moe_align scratch.
+struct PrefillWs {
+  int64_t local, row_token, gptr, sorted, bexp, npad, scratch, total;
+};
+static PrefillWs prefill_ws(int64_t T, int K, int E) {
+  const int64_t R = T * K;
+  const int64_t P = ss::padded_rows(R, E, ss::kPrefillBlockM);
+  auto up = [](int64_t v) { return (v + 255) / 256 * 256; };
+  PrefillWs w{};
+  int64_t o = 0;
+  w.local = o;
+  o = up(o + R * 4);
+  w.row_token = o;
+  o = up(o + R * 4);
+  w.gptr = o;
+  o = up(o + (int64_t)E * 8);
+  w.sorted = o;
+  o = up(o + P * 4);
+  w.bexp = o;
+  o = up(o + P / ss::kPrefillBlockM * 4);
+  w.npad = o;
+  o = up(o + 4);
+  w.scratch = o;
+  o = up(o + ss::align_scratch_ints(R, E) * 4);
+  w.total = o;
+  return w;
+}
+
+int64_t ssmoe_moe_prefill_workspace_bytes(int64_t T, int K, int E) {
+  if (T < 0 || K < 1 || E < 1) return -1;
+  return prefill_ws(T, K, E).total;
+}
+
+int ssmoe_moe_prefill(const uint16_t* x, const int32_t* expert_ids, const float* weights, int layer,
+                      const int32_t* map, int64_t map_len, const int64_t* slot_ptr, int64_t n_slots, void* workspace,
+                      int64_t workspace_bytes, uint16_t* h_buf, float* out_rows, float* out, int64_t T, int H, int I,
+                      int K, int E, void* stream) {
+  if (T < 0 || K < 1 || K > 64 || E < 1 || E > 4096) return fail(SSMOE_EINVAL, "need T >= 0, 1 <= K <= 64, 1 <= E <= 4096");
+  if (int rc = check_prefill_shape(T * K, H, I)) return rc;
+  if (layer < 0) return fail(SSMOE_EINVAL, "layer must be >= 0, got %d", layer);
+  if ((int64_t)(layer + 1) * E > map_len)
+    return fail(SSMOE_EINVAL, "map holds %lld entries, layer %d needs %lld", (long long)map_len, layer,
+                (long long)(layer + 1) * E);
+  if (T == 0) return ok();
+  if (!x || !expert_ids || !weights || !map || !slot_ptr || !workspace || !h_buf || !out_rows || !out)
+    return fail(SSMOE_EINVAL, "every pointer must be non-null");
+  if (!aligned(x, 16) || !aligned(h_buf, 16) || !aligned(out_rows, 16) || !aligned(out, 16) ||
+      !aligned(workspace, 256))
+    return fail(SSMOE_EINVAL, "x, h_buf, out_rows, out 16-byte and workspace 256-byte aligned");
+  const PrefillWs w = prefill_ws(T, K, E);
+  if (workspace_bytes < w.total)
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes, (long long)w.total);
+  int* err = nullptr;
+  if (int rc = status_ptr(&err)) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  int32_t* local = reinterpret_cast<int32_t*>(ws + w.local);
+  int32_t* row_token = reinterpret_cast<int32_t*>(ws + w.row_token);
+  int64_t* gptr = reinterpret_cast<int64_t*>(ws + w.gptr);
+  int32_t* sorted = reinterpret_cast<int32_t*>(ws + w.sorted);
+  int32_t* bexp = reinterpret_cast<int32_t*>(ws + w.bexp);
+  int32_t* npad = reinterpret_cast<int32_t*>(ws + w.npad);
+  const int64_t R = T * K;
+  if (int rc = hip_check(ss::launch_prefill_tables(map, (int64_t)layer * E, map_len, slot_ptr, n_slots, E, gptr,
+                                                   expert_ids, R, K, local, row_token, err, st),
+                         "prefill tables launch"))
+    return rc;
+  ss::AlignArgs al{};
+  al.local_expert = local;
+  al.R = R;
+  al.num_local = E;
+  al.block_m = ss::kPrefillBlockM;
+  al.sorted_rows = sorted;
+  al.block_expert = bexp;
+  al.num_padded = npad;
+  al.scratch = reinterpret_cast<int32_t*>(ws + w.scratch);
+  if (int rc = hip_check(ss::launch_moe_align(al, st), "moe_align launch")) return rc;
+  ss::PrefillArgs p{};
+  p.x = x;
+  p.row_token = row_token;
+  p.row_weight = weights;
+  p.sorted_rows = sorted;
+  p.block_expert = bexp;
+  p.num_padded = npad;
+  p.group_ptr = gptr;
+  p.num_local = E;
+  p.h_buf = h_buf;
+  p.out_rows = out_rows;
+  p.R = R;
+  p.T = (int)T;
+  p.H = H;
+  p.I = I;
+  if (int rc = hip_check(ss::launch_prefill_gemm(p, st), "prefill gemm launch")) return rc;
+  return hip_check(ss::launch_combine(out_rows, local, (int)T, K, H, out, st), "combine launch");
 }
 
 }  // extern "C"
