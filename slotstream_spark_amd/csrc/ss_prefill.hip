@@ -70,23 +70,50 @@ __global__ __launch_bounds__(1024) void align_scan_kernel(int64_t R, int nl, int
   int* tot = sm + nl + 1;
   const int tid = threadIdx.x;
   for (int e = tid; e < nl; e += 1024) {
+    // Sequential per key; the loads of 16 chunks are issued before their stores so the scan is not one memory
+    // round trip per chunk.
     int run = 0;
-    for (int c = 0; c < nch; ++c) {
-      const int v = chunk_cnt[(int64_t)c * nl + e];
-      chunk_cnt[(int64_t)c * nl + e] = run;
-      run += v;
+    for (int c0 = 0; c0 < nch; c0 += 16) {
+      int v[16];
+#pragma unroll
+      for (int q = 0; q < 16; ++q) v[q] = c0 + q < nch ? chunk_cnt[(int64_t)(c0 + q) * nl + e] : 0;
+#pragma unroll
+      for (int q = 0; q < 16; ++q) {
+        if (c0 + q < nch) chunk_cnt[(int64_t)(c0 + q) * nl + e] = run;
+        run += v[q];
+      }
     }
     tot[e] = run;
   }
   __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int e = 0; e < nl; ++e) {
-      ps[e] = run;
-      run += (tot[e] + bm - 1) / bm * bm;
-    }
-    ps[nl] = run;
-    *num_padded = run;
+  // Exclusive scan of the padded expert sizes: each thread sums up to 4 consecutive experts, a Hillis-Steele scan
+  // over the 1024 thread totals, then the per-thread prefixes (nl <= 4096).
+  __shared__ int part[1024];
+  int loc[4], sum = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = 4 * tid + q;
+    loc[q] = e < nl ? (tot[e] + bm - 1) / bm * bm : 0;
+    sum += loc[q];
+  }
+  part[tid] = sum;
+  __syncthreads();
+  for (int off = 1; off < 1024; off <<= 1) {
+    const int v = tid >= off ? part[tid - off] : 0;
+    __syncthreads();
+    part[tid] += v;
+    __syncthreads();
+  }
+  int run = part[tid] - sum;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int e = 4 * tid + q;
+    if (e < nl) ps[e] = run;
+    run += loc[q];
+  }
+  if (tid == 1023) {
+    ps[nl] = part[1023];
+    *num_padded = part[1023];
   }
   __syncthreads();
   for (int e = tid; e <= nl; e += 1024) pad[e] = ps[e];
@@ -136,150 +163,194 @@ hipError_t launch_moe_align(const AlignArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// ---------------------------------------------------------------- grouped GEMM tiles
-constexpr int kBM = 64;      // rows per block (the moe_align block)
-constexpr int kBN = 64;      // output columns per block and matrix
-constexpr int kBK = 64;      // K per step: one quantisation group
-constexpr int kLdsRow = 72;  // bf16 per LDS row (64 + 8 padding: rows 144 B apart spread the banks)
+// ---------------------------------------------------------------- grouped GEMM
+// Block: 256 threads, 64 sorted rows x 128 weight rows (gate/up: 64 gate + the same 64 up rows; down: 128 rows),
+// K in steps of 64 (one quantisation group). Each step's operands arrive in LDS by direct-to-LDS loads into a ring
+// of kStages slots, kStages - 1 steps ahead of the MFMAs:
+//   A    64 rows x 128 B of bf16 activations; the 16-byte chunk c of row r sits in slot c ^ (r & 7), so the 16 rows an
+//        MFMA operand read touches fall in different banks;
+//   W    128 weight rows x 32 B of packed nibbles;
+//   S, B the scale and bias dwords (two groups each) of the 128 rows.
+// The step's weights are then dequantized once into a bf16 tile (bf16(q*s + b), rows 144 B apart) that the four
+// waves read as MFMA B operands; each wave owns 32 rows x 64 columns of the output.
+constexpr int kBM = 64;
+constexpr int kBK = 64;
+constexpr int kNR = 128;               // weight rows per block
+constexpr int kStages = 4;
+constexpr int kOffA = 0, kOffW = 8192, kOffS = 12288, kOffB = 12800, kStageBytes = 13312;
+constexpr int kTileRow = 72;           // bf16 per row of the dequantized tile
+constexpr int kTileBytes = kNR * kTileRow * 2;
+constexpr size_t kGemmLds = (size_t)kStages * kStageBytes + kTileBytes;
 
-// v or zero, selected component by component (a select of whole vectors can turn into a load through a
-// selected private/global address).
-SS_DEV uint4 zero_if(bool z, uint4 v) {
-  return make_uint4(z ? 0u : v.x, z ? 0u : v.y, z ? 0u : v.z, z ? 0u : v.w);
-}
+typedef __bf16 ss_bf16x2 __attribute__((ext_vector_type(2)));
 
-SS_DEV uint32_t pack_bf16x2_rne(float lo, float hi) { return ss_f32_to_bf16(lo) | (ss_f32_to_bf16(hi) << 16); }
-
-// 32 nibbles (one 16-byte word group of a weight row: elements k .. k+31) -> 16 words of bf16 pairs
-// bf16(q * s + b) in element order.
-SS_DEV void dequant32(uint4 w, float s, float b, uint32_t out[16]) {
-  const uint32_t ww[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int d = 0; d < 4; ++d) {
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const float q0 = (float)((ww[d] >> (8 * p)) & 15u);
-      const float q1 = (float)((ww[d] >> (8 * p + 4)) & 15u);
-      out[4 * d + p] = pack_bf16x2_rne(__builtin_fmaf(q0, s, b), __builtin_fmaf(q1, s, b));
-    }
-  }
-}
-
-// One K step of a 64-row x (NT x 16)-column output tile per wave pair layout: waves (wm, wn) = (w >> 1, w & 1).
-// A: As[row][k] bf16 (kLdsRow stride); B: Bs[col][k] bf16 (kLdsRow stride).
-SS_DEV ss_u32x4 lds_frag(const uint16_t* base, int row, int k) {
-  return *reinterpret_cast<const ss_u32x4*>(base + row * kLdsRow + k);
+// bf16 pair (lo, hi) rounded to nearest even by the hardware conversion.
+SS_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
+  const ss_bf16x2 v = {(__bf16)lo, (__bf16)hi};
+  return __builtin_bit_cast(uint32_t, v);
 }
 
 struct GemmArgs {
-  const uint16_t* a;          // gate/up: x bf16 [T, H]; down: h bf16 [R, I]
-  const int32_t* row_token;   // [R] (gate/up)
-  const float* row_weight;    // [R] (down)
-  const int32_t* sorted_rows; // [P]
-  const int32_t* block_expert;// [P / kBM]
-  const int32_t* num_padded;  // [1]
-  const int64_t* group_ptr;   // [num_local] record base addresses
-  uint16_t* h;                // gate/up output bf16 [R, I]
-  float* out_rows;            // down output fp32 [R, H]
+  const uint16_t* a;           // gate/up: x bf16 [T, H]; down: h bf16 [R, I]
+  const int32_t* row_token;    // [R] (gate/up)
+  const float* row_weight;     // [R] (down)
+  const int32_t* sorted_rows;  // [P]
+  const int32_t* block_expert; // [P / kBM]
+  const int32_t* num_padded;   // [1]
+  const int64_t* group_ptr;    // [num_local] record base addresses
+  uint16_t* h;                 // gate/up output bf16 [R, I]
+  float* out_rows;             // down output fp32 [R, H]
   int64_t R;
   int T, H, I;
-  int64_t w_off, s_off, b_off;   // gate (or down) pieces
+  int64_t w_off, s_off, b_off;     // gate (or down) pieces
   int64_t w2_off, s2_off, b2_off;  // up pieces (gate/up)
 };
 
-// Gate/up: grid (I / kBN, P / kBM). Per block: 64 sorted rows x (64 gate + 64 up) columns, K = H.
-__global__ __launch_bounds__(256) void prefill_gate_up_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][2 * kBN * kLdsRow];
-  __shared__ int tok_s[kBM];
-  __shared__ int row_s[kBM];
+SS_DEV void waitcnt_vm(int n) {
+  // s_waitcnt with only vmcnt constrained (expcnt and lgkmcnt at their maxima); n in {0, 4, 8}.
+  if (n >= 8) __builtin_amdgcn_s_waitcnt(0xF78);
+  else if (n >= 4) __builtin_amdgcn_s_waitcnt(0xF74);
+  else __builtin_amdgcn_s_waitcnt(0xF70);
+}
+
+// The shared main loop. GATE_UP: rows 0..63 of the weight tile are gate rows n0 + r, rows 64..127 the up rows
+// n0 + r; otherwise 128 consecutive down rows n0 + r. kdim = the K extent, wstride = weight row bytes (kdim / 2),
+// sstride = scale row bytes (kdim / 32). acc[i][j]: output rows 32 wm + 16 i, tile columns 64 wn + 16 j.
+template <bool GATE_UP>
+SS_DEV void gemm_main(const GemmArgs& g, uint8_t* lds, const int* src_row, const uint8_t* base, int n0, int kdim,
+                      int astride, ss_f32x4 (&acc)[2][4]) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int pid_n = blockIdx.x, pid_m = blockIdx.y;
-  if ((int64_t)pid_m * kBM >= (int64_t)g.num_padded[0]) return;
-  const int e = g.block_expert[pid_m];
-  if (e < 0) return;
-  const uint8_t* base = reinterpret_cast<const uint8_t*>(g.group_ptr[e]);
-  const int H = g.H, I = g.I;
-  if (tid < kBM) {
-    const int r = g.sorted_rows[(int64_t)pid_m * kBM + tid];
-    row_s[tid] = r;
-    const int t = r < g.R ? g.row_token[r] : -1;
-    tok_s[tid] = (t >= 0 && t < g.T) ? t : -1;
+  uint8_t* tile = lds + kStages * kStageBytes;
+  const int nsteps = kdim / kBK;
+  const int64_t wstride = kdim / 2, sstride = kdim / 32;
+  // DMA sources of this lane (A: two instructions q = 2w, 2w+1 covering rows 8q .. 8q+7).
+  const uint16_t* asrc[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = 8 * (2 * w + i) + (lane >> 3);
+    const int chunk = (lane & 7) ^ (row & 7);
+    asrc[i] = g.a + (int64_t)src_row[row] * astride + 8 * chunk;
   }
-  __syncthreads();
-  // Loader roles. x: 64 rows x 8 chunks of 16 B -> two chunks per thread (rows tid / 8 and tid / 8 + 32).
-  const int xr0 = tid >> 3, xc = tid & 7;
-  const int t0 = tok_s[xr0], t1 = tok_s[xr0 + 32];
-  const uint16_t* xp0 = g.a + (int64_t)(t0 < 0 ? 0 : t0) * H + 8 * xc;
-  const uint16_t* xp1 = g.a + (int64_t)(t1 < 0 ? 0 : t1) * H + 8 * xc;
-  // Weights: 128 rows (64 gate, 64 up) x 2 halves of 32 nibbles -> one 16-byte word per thread.
-  const int wcol = tid >> 1, whalf = tid & 1;
-  const int nrow = pid_n * kBN + (wcol & 63);
-  const bool up = wcol >= 64;
-  const uint8_t* wp = base + (up ? g.w2_off : g.w_off) + (int64_t)nrow * (H / 2) + 16 * whalf;
-  const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + (up ? g.s2_off : g.s_off)) + (int64_t)nrow * (H / 64);
-  const uint16_t* bp = reinterpret_cast<const uint16_t*>(base + (up ? g.b2_off : g.b_off)) + (int64_t)nrow * (H / 64);
-  const int nsteps = H / kBK;
-
-  uint4 xv0, xv1, wv;
-  uint16_t sv, bv;
-  auto fetch = [&](int ks) {
+  const int wrow = 32 * w + (lane >> 1);
+  const bool up_row = GATE_UP && wrow >= 64;
+  const int64_t wrow_g = n0 + (GATE_UP ? (wrow & 63) : wrow);
+  const uint8_t* wsrc = base + (up_row ? g.w2_off : g.w_off) + wrow_g * wstride + 16 * (lane & 1);
+  // scale / bias dwords: waves 0, 1 scales of rows 64 w + lane; waves 2, 3 biases of rows 64 (w - 2) + lane.
+  const int srow = 64 * (w & 1) + lane;
+  const bool s_up = GATE_UP && srow >= 64;
+  const int64_t srow_g = n0 + (GATE_UP ? (srow & 63) : srow);
+  const int64_t soff = (w < 2) ? (s_up ? g.s2_off : g.s_off) : (s_up ? g.b2_off : g.b_off);
+  const uint8_t* ssrc = base + soff + srow_g * sstride;
+  auto issue = [&](int ks) {
+    uint8_t* st = lds + (ks % kStages) * kStageBytes;
     const int k0 = ks * kBK;
-    xv0 = ldg16(xp0 + k0);
-    xv1 = ldg16(xp1 + k0);
-    wv = ldg16(wp + k0 / 2);
-    sv = sp[ks];
-    bv = bp[ks];
-  };
-  auto stage = [&](int buf) {
-    *reinterpret_cast<uint4*>(&As[buf][xr0 * kLdsRow + 8 * xc]) = zero_if(t0 < 0, xv0);
-    *reinterpret_cast<uint4*>(&As[buf][(xr0 + 32) * kLdsRow + 8 * xc]) = zero_if(t1 < 0, xv1);
-    uint32_t d[16];
-    dequant32(wv, ss_bf16_to_f32(sv), ss_bf16_to_f32(bv), d);
-    uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][wcol * kLdsRow + 32 * whalf]);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = make_uint4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
+    for (int i = 0; i < 2; ++i)
+      __builtin_amdgcn_global_load_lds(asrc[i] + k0, (__attribute__((address_space(3))) void*)(st + kOffA + 1024 * (2 * w + i)), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(wsrc + k0 / 2, (__attribute__((address_space(3))) void*)(st + kOffW + 1024 * w), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(ssrc + ((2 * ks) & ~3), (__attribute__((address_space(3))) void*)(st + (w < 2 ? kOffS + 256 * w : kOffB + 256 * (w - 2))), 4, 0, 0);
   };
-
+#pragma unroll
+  for (int ks = 0; ks < kStages - 1; ++ks)
+    if (ks < nsteps) issue(ks);
   const int wm = w >> 1, wn = w & 1;
-  const int fr = lane & 15, fk = 8 * (lane >> 4);
-  ss_f32x4 accg[2][2], accu[2][2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      accg[i][j] = ss_f32x4{0.f, 0.f, 0.f, 0.f};
-      accu[i][j] = ss_f32x4{0.f, 0.f, 0.f, 0.f};
-    }
-  fetch(0);
-  stage(0);
-  __syncthreads();
+  const int fr = lane & 15, fq = lane >> 4;
+  const int drow = tid >> 1, dhalf = tid & 1;  // dequant role: one 16-byte word of one weight row
 #pragma unroll 1
   for (int ks = 0; ks < nsteps; ++ks) {
-    const int buf = ks & 1;
-    if (ks + 1 < nsteps) fetch(ks + 1);
+    const int ahead = nsteps - 1 - ks;
+    waitcnt_vm(4 * (ahead < kStages - 2 ? ahead : kStages - 2));
+    __syncthreads();
+    if (ks + kStages - 1 < nsteps) issue(ks + kStages - 1);
+    const uint8_t* st = lds + (ks % kStages) * kStageBytes;
+    {
+      const uint4 wv = *reinterpret_cast<const uint4*>(st + kOffW + 32 * drow + 16 * dhalf);
+      const uint32_t sw = *reinterpret_cast<const uint32_t*>(st + kOffS + 4 * drow);
+      const uint32_t bw = *reinterpret_cast<const uint32_t*>(st + kOffB + 4 * drow);
+      const float sc = __uint_as_float((ks & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
+      const float bi = __uint_as_float((ks & 1) ? (bw & 0xFFFF0000u) : (bw << 16));
+      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t o[16];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t lo = ww[d] & 0x0F0F0F0Fu, hi = (ww[d] >> 4) & 0x0F0F0F0Fu;
+        const float q0 = (float)((lo >> 0) & 0xFFu), q1 = (float)((hi >> 0) & 0xFFu);
+        const float q2 = (float)((lo >> 8) & 0xFFu), q3 = (float)((hi >> 8) & 0xFFu);
+        const float q4 = (float)((lo >> 16) & 0xFFu), q5 = (float)((hi >> 16) & 0xFFu);
+        const float q6 = (float)((lo >> 24) & 0xFFu), q7 = (float)((hi >> 24) & 0xFFu);
+        o[4 * d + 0] = cvt_pk_bf16(__builtin_fmaf(q0, sc, bi), __builtin_fmaf(q1, sc, bi));
+        o[4 * d + 1] = cvt_pk_bf16(__builtin_fmaf(q2, sc, bi), __builtin_fmaf(q3, sc, bi));
+        o[4 * d + 2] = cvt_pk_bf16(__builtin_fmaf(q4, sc, bi), __builtin_fmaf(q5, sc, bi));
+        o[4 * d + 3] = cvt_pk_bf16(__builtin_fmaf(q6, sc, bi), __builtin_fmaf(q7, sc, bi));
+      }
+      uint4* dst = reinterpret_cast<uint4*>(tile + (drow * kTileRow + 32 * dhalf) * 2);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
+    }
+    __syncthreads();
 #pragma unroll
     for (int kk = 0; kk < kBK; kk += 32) {
-      ss_u32x4 af[2], bg[2], bu[2];
+      ss_u32x4 af[2], bf[4];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = lds_frag(As[buf], 32 * wm + 16 * i + fr, kk + fk);
+      for (int i = 0; i < 2; ++i) {
+        const int m = 32 * wm + 16 * i + fr;
+        const int chunk = (kk >> 3) + fq;
+        af[i] = *reinterpret_cast<const ss_u32x4*>(st + kOffA + 128 * m + 16 * (chunk ^ (m & 7)));
+      }
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        bg[j] = lds_frag(Bs[buf], 32 * wn + 16 * j + fr, kk + fk);
-        bu[j] = lds_frag(Bs[buf], kBN + 32 * wn + 16 * j + fr, kk + fk);
+      for (int j = 0; j < 4; ++j) {
+        const int col = GATE_UP ? (j < 2 ? 32 * wn + 16 * j + fr : 64 + 32 * wn + 16 * (j - 2) + fr)
+                                : 64 * wn + 16 * j + fr;
+        bf[j] = *reinterpret_cast<const ss_u32x4*>(tile + (col * kTileRow + kk + 8 * fq) * 2);
       }
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          accg[i][j] = ss_mfma(af[i], bg[j], accg[i][j]);
-          accu[i][j] = ss_mfma(af[i], bu[j], accu[i][j]);
-        }
+        for (int j = 0; j < 4; ++j) acc[i][j] = ss_mfma(af[i], bf[j], acc[i][j]);
     }
-    if (ks + 1 < nsteps) stage(buf ^ 1);
-    __syncthreads();
   }
-  // Epilogue: D[m][n] of tile (i, j) sits in lane n + 16 (m / 4), element m % 4.
+}
+
+// Gate/up: one block per (M block, 64-column N tile), mapped by xcd_tile. Output h[r, n0 .. n0 + 63] = bf16(silu(g) * u).
+// Workgroups are dealt to the 8 XCDs round-robin (b % 8). Block b is mapped to M block m and N tile n so that
+// the N tiles of one M block run on one XCD, one after another: the gathered activation rows of the M block are
+// read once into that XCD's L2 instead of once per XCD.
+SS_DEV bool xcd_tile(int nt, int mb, int& pid_n, int& pid_m) {
+  const int b = blockIdx.x;
+  const int xcd = b & 7, j = b >> 3;
+  pid_m = (j / nt) * 8 + xcd;
+  pid_n = j % nt;
+  return pid_m < mb;
+}
+
+__global__ __launch_bounds__(256) void prefill_gate_up_kernel(GemmArgs g, int nt, int mb) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_g[];
+  __shared__ int src_row[kBM];
+  __shared__ int out_row[kBM];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  int pid_n, pid_m;
+  if (!xcd_tile(nt, mb, pid_n, pid_m)) return;
+  if ((int64_t)pid_m * kBM >= (int64_t)g.num_padded[0]) return;
+  const int e = g.block_expert[pid_m];
+  if (e < 0) return;
+  const uint8_t* base = reinterpret_cast<const uint8_t*>(g.group_ptr[e]);
+  if (tid < kBM) {
+    const int r = g.sorted_rows[(int64_t)pid_m * kBM + tid];
+    const int t = r < g.R ? g.row_token[r] : -1;
+    const bool ok = t >= 0 && t < g.T;
+    out_row[tid] = ok ? r : -1;
+    src_row[tid] = ok ? t : 0;  // padding rows read token 0; their outputs are never stored
+  }
+  __syncthreads();
+  ss_f32x4 acc[2][4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = ss_f32x4{0.f, 0.f, 0.f, 0.f};
+  const int n0 = pid_n * 64;
+  gemm_main<true>(g, lds_g, src_row, base, n0, g.H, g.H, acc);
+  const int wm = w >> 1, wn = w & 1;
+  // acc[i][0..1]: gate columns 32 wn + 16 j, acc[i][2..3]: the matching up columns.
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -287,94 +358,44 @@ __global__ __launch_bounds__(256) void prefill_gate_up_kernel(GemmArgs g) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = 32 * wm + 16 * i + 4 * (lane >> 4) + q;
-        const int r = row_s[m];
-        if (r >= g.R) continue;
-        const float gv = accg[i][j][q], uv = accu[i][j][q];
+        const int r = out_row[m];
+        if (r < 0) continue;
+        const float gv = acc[i][j][q], uv = acc[i][j + 2][q];
         const float hv = gv / (1.f + ss_expf(-gv)) * uv;
-        const int n = pid_n * kBN + 32 * wn + 16 * j + (lane & 15);
-        g.h[(int64_t)r * I + n] = (uint16_t)ss_f32_to_bf16(hv);
+        const int n = n0 + 32 * wn + 16 * j + (lane & 15);
+        g.h[(int64_t)r * g.I + n] = (uint16_t)ss_f32_to_bf16(hv);
       }
 }
 
-// Down: grid (H / (2 kBN), P / kBM). Per block: 64 sorted rows x 128 output columns, K = I.
-__global__ __launch_bounds__(256) void prefill_down_kernel(GemmArgs g) {
-  __shared__ __attribute__((aligned(16))) uint16_t As[2][kBM * kLdsRow];
-  __shared__ __attribute__((aligned(16))) uint16_t Bs[2][2 * kBN * kLdsRow];
-  __shared__ int row_s[kBM];
+// Down: one block per (M block, 128-row N tile), mapped by xcd_tile. Output out_rows[r, n0 .. n0 + 127] = (h Wd^T) * row_weight.
+__global__ __launch_bounds__(256) void prefill_down_kernel(GemmArgs g, int nt, int mb) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds_d[];
+  __shared__ int src_row[kBM];
+  __shared__ int out_row[kBM];
   __shared__ float wt_s[kBM];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int pid_n = blockIdx.x, pid_m = blockIdx.y;
+  int pid_n, pid_m;
+  if (!xcd_tile(nt, mb, pid_n, pid_m)) return;
   if ((int64_t)pid_m * kBM >= (int64_t)g.num_padded[0]) return;
   const int e = g.block_expert[pid_m];
   if (e < 0) return;
   const uint8_t* base = reinterpret_cast<const uint8_t*>(g.group_ptr[e]);
-  const int H = g.H, I = g.I;
   if (tid < kBM) {
     const int r = g.sorted_rows[(int64_t)pid_m * kBM + tid];
-    row_s[tid] = r;
-    wt_s[tid] = r < g.R ? g.row_weight[r] : 0.f;
+    const bool ok = r < g.R;
+    out_row[tid] = ok ? r : -1;
+    src_row[tid] = ok ? r : 0;
+    wt_s[tid] = ok ? g.row_weight[r] : 0.f;
   }
   __syncthreads();
-  const int ar0 = tid >> 3, ac = tid & 7;
-  const int r0 = row_s[ar0], r1 = row_s[ar0 + 32];
-  const uint16_t* ap0 = g.a + (int64_t)(r0 < g.R ? r0 : 0) * I + 8 * ac;
-  const uint16_t* ap1 = g.a + (int64_t)(r1 < g.R ? r1 : 0) * I + 8 * ac;
-  const int wcol = tid >> 1, whalf = tid & 1;
-  const int nrow = pid_n * 2 * kBN + wcol;
-  const uint8_t* wp = base + g.w_off + (int64_t)nrow * (I / 2) + 16 * whalf;
-  const uint16_t* sp = reinterpret_cast<const uint16_t*>(base + g.s_off) + (int64_t)nrow * (I / 64);
-  const uint16_t* bp = reinterpret_cast<const uint16_t*>(base + g.b_off) + (int64_t)nrow * (I / 64);
-  const int nsteps = I / kBK;
-
-  uint4 av0, av1, wv;
-  uint16_t sv, bv;
-  auto fetch = [&](int ks) {
-    const int k0 = ks * kBK;
-    av0 = ldg16(ap0 + k0);
-    av1 = ldg16(ap1 + k0);
-    wv = ldg16(wp + k0 / 2);
-    sv = sp[ks];
-    bv = bp[ks];
-  };
-  auto stage = [&](int buf) {
-    *reinterpret_cast<uint4*>(&As[buf][ar0 * kLdsRow + 8 * ac]) = zero_if(r0 >= g.R, av0);
-    *reinterpret_cast<uint4*>(&As[buf][(ar0 + 32) * kLdsRow + 8 * ac]) = zero_if(r1 >= g.R, av1);
-    uint32_t d[16];
-    dequant32(wv, ss_bf16_to_f32(sv), ss_bf16_to_f32(bv), d);
-    uint4* dst = reinterpret_cast<uint4*>(&Bs[buf][wcol * kLdsRow + 32 * whalf]);
-#pragma unroll
-    for (int q = 0; q < 4; ++q) dst[q] = make_uint4(d[4 * q], d[4 * q + 1], d[4 * q + 2], d[4 * q + 3]);
-  };
-
-  const int wm = w >> 1, wn = w & 1;
-  const int fr = lane & 15, fk = 8 * (lane >> 4);
   ss_f32x4 acc[2][4];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = ss_f32x4{0.f, 0.f, 0.f, 0.f};
-  fetch(0);
-  stage(0);
-  __syncthreads();
-#pragma unroll 1
-  for (int ks = 0; ks < nsteps; ++ks) {
-    const int buf = ks & 1;
-    if (ks + 1 < nsteps) fetch(ks + 1);
-#pragma unroll
-    for (int kk = 0; kk < kBK; kk += 32) {
-      ss_u32x4 af[2], bf[4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = lds_frag(As[buf], 32 * wm + 16 * i + fr, kk + fk);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = lds_frag(Bs[buf], 64 * wn + 16 * j + fr, kk + fk);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = ss_mfma(af[i], bf[j], acc[i][j]);
-    }
-    if (ks + 1 < nsteps) stage(buf ^ 1);
-    __syncthreads();
-  }
+  const int n0 = pid_n * kNR;
+  gemm_main<false>(g, lds_d, src_row, base, n0, g.I, g.I, acc);
+  const int wm = w >> 1, wn = w & 1;
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -382,17 +403,28 @@ __global__ __launch_bounds__(256) void prefill_down_kernel(GemmArgs g) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int m = 32 * wm + 16 * i + 4 * (lane >> 4) + q;
-        const int r = row_s[m];
-        if (r >= g.R) continue;
-        const int n = pid_n * 2 * kBN + 64 * wn + 16 * j + (lane & 15);
-        g.out_rows[(int64_t)r * H + n] = acc[i][j][q] * wt_s[m];
+        const int r = out_row[m];
+        if (r < 0) continue;
+        const int n = n0 + 64 * wn + 16 * j + (lane & 15);
+        g.out_rows[(int64_t)r * g.H + n] = acc[i][j][q] * wt_s[m];
       }
 }
 
 hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
-  const SsRecord rec = ss_record_layout(p.H, p.I);
   static_assert(kBM == kPrefillBlockM, "one block size for the plan and the GEMM");
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gate_up_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_down_kernel),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const SsRecord rec = ss_record_layout(p.H, p.I);
   const int64_t P = padded_rows(p.R, p.num_local, kBM);
+  if (P == 0 || p.R == 0) return hipSuccess;
   GemmArgs g{};
   g.row_token = p.row_token;
   g.row_weight = p.row_weight;
@@ -406,7 +438,6 @@ hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
   g.T = p.T;
   g.H = p.H;
   g.I = p.I;
-  if (P == 0) return hipSuccess;
   g.a = p.x;
   g.w_off = rec.gw;
   g.s_off = rec.gs;
@@ -414,12 +445,15 @@ hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
   g.w2_off = rec.uw;
   g.s2_off = rec.us;
   g.b2_off = rec.ub;
-  hipLaunchKernelGGL(prefill_gate_up_kernel, dim3(p.I / kBN, (unsigned)(P / kBM)), dim3(256), 0, st, g);
+  const int mb = (int)(P / kBM), mb8 = (mb + 7) / 8 * 8;
+  hipLaunchKernelGGL(prefill_gate_up_kernel, dim3((unsigned)(mb8 * (p.I / 64))), dim3(256), kGemmLds, st, g, p.I / 64,
+                     mb);
   g.a = p.h_buf;
   g.w_off = rec.dw;
   g.s_off = rec.ds;
   g.b_off = rec.db;
-  hipLaunchKernelGGL(prefill_down_kernel, dim3(p.H / (2 * kBN), (unsigned)(P / kBM)), dim3(256), 0, st, g);
+  hipLaunchKernelGGL(prefill_down_kernel, dim3((unsigned)(mb8 * (p.H / kNR))), dim3(256), kGemmLds, st, g, p.H / kNR,
+                     mb);
   return hipGetLastError();
 }
 
