@@ -41,6 +41,99 @@ def layer_bytes(u: int, t: int) -> int:
     return u * 1_769_472 + 2_097_152 + 6_291_456 + 4_096 + t * H * 4
 
 
+PREFILL_T = 2048
+# FLOP of one prefill layer (2 per multiply-add): routed gate/up/down over T*K rows, the shared expert's three
+# projections and the router, 2 T (K 3 H I + 3 H Is + H E).
+PREFILL_ROUTED_FLOP = 2 * PREFILL_T * K * 3 * H * I
+PREFILL_FLOP = 2 * PREFILL_T * (K * 3 * H * I + 3 * H * IS + H * E)
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def timed_graph(fn, steps, warmup, stream):
+    """Capture fn() in a HIP graph, replay it `warmup` times, then time `steps` replays with HIP events recorded on
+    the graph's stream. Returns ms per replay."""
+    import torch
+
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        fn()
+    with torch.cuda.stream(stream):
+        for _ in range(warmup):
+            g.replay()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(stream)
+        for _ in range(steps):
+            g.replay()
+        ev1.record(stream)
+    torch.cuda.synchronize()
+    return ev0.elapsed_time(ev1) / steps
+
+
+def prefill_leg(pool, weights, biases, nl, steps, warmup, dev):
+    """2048 bf16 tokens through `nl` config-1 layers (each a full prefill layer: router GEMM,
+    device top-k, moe_align, grouped gate/up and down, rank-order combine, shared expert), one HIP graph; and the
+    grouped GEMM pair alone (ssmoe_fused_moe_affine over each layer's aligned plan), the MFMA-bound kernels."""
+    import torch
+
+    from slotstream_spark_amd.engine.prefill import MoEPrefillLayer
+    from slotstream_spark_amd.kernels.fused_moe_affine import align_rows, fused_moe_affine
+    from slotstream_spark_amd.memory.synth import normal_bf16
+
+    TP = PREFILL_T
+    layers = [MoEPrefillLayer(pool, l, w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, top_k=K,
+                              router_bias=b, max_tokens=TP) for l, (w, b) in enumerate(zip(weights[:nl], biases[:nl]))]
+    xp = normal_bf16((TP, H), 1.0, 1733, dev)
+    outs = [None] * nl
+
+    def full():
+        for l in range(nl):
+            outs[l] = layers[l](xp)
+
+    s = torch.cuda.Stream(device=dev)
+    ms = timed_graph(full, steps, warmup, s)
+    us_layer = ms * 1000.0 / nl
+    # the same layers' routing, aligned once, for the GEMM-pair leg
+    R = TP * K
+    row_token = (torch.arange(R, device=dev) // K).to(torch.int32)
+    plans = []
+    for l in range(nl):
+        ids, w = outs[l][1], outs[l][2]
+        row_expert = ids.reshape(-1).contiguous()
+        emap = torch.arange(E, dtype=torch.int32, device=dev)
+        gptr = pool.slot_ptr[pool.map[l * E:(l + 1) * E].long()].contiguous()
+        plans.append((row_expert, w.reshape(-1).contiguous(), emap, gptr, align_rows(row_expert, emap, E)))
+    uniq = [int(torch.unique(p[0]).numel()) for p in plans]
+    padded = [int(p[4][2].item()) for p in plans]
+
+    def gemms():
+        for l in range(nl):
+            row_expert, rw, emap, gptr, al = plans[l]
+            fused_moe_affine(xp, row_token, rw, emap, gptr, layers[l].out_rows, row_expert=row_expert,
+                             h_buf=layers[l].h_buf, aligned=al)
+
+    ms_g = timed_graph(gemms, steps, warmup, s)
+    us_g = ms_g * 1000.0 / nl
+    tflops = PREFILL_FLOP / (us_layer * 1e-6) / 1e12
+    g_tflops = PREFILL_ROUTED_FLOP / (us_g * 1e-6) / 1e12
+    wbytes = sum(uniq) / nl * 1_769_472
+    log(f"prefill layer {us_layer:.1f} us ({tflops:.1f} TFLOP/s); grouped GEMM pair {us_g:.1f} us "
+        f"({g_tflops:.1f} TFLOP/s routed); unique experts {uniq}; padded rows {padded}")
+    return {"tokens": TP, "layers": nl, "us_per_layer": round(us_layer, 2), "tflops": round(tflops, 2),
+            "flop_per_layer": PREFILL_FLOP, "unique_experts_mean": sum(uniq) / nl,
+            "padded_rows_mean": sum(padded) / nl,
+            "roofline": {"bound": "mfma", "kernel": "prefill_gate_up_kernel + prefill_down_kernel (grouped GEMM pair)",
+                         "achieved": round(g_tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                         "frac": round(g_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic_of("prefill_gemm"),
+                         "us_per_launch": round(us_g, 2), "flop_per_launch": PREFILL_ROUTED_FLOP,
+                         "expert_bytes_per_launch": int(wbytes),
+                         "expert_stream_gbs": round(wbytes / (us_g * 1e-6) / 1e9, 1)}}
+
+
 def traffic_of(kernel: str):
     """HBM bytes per launch of `kernel` measured with rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a known-size copy),
     as recorded in profiles/traffic.json next to the command that produced it; None when not measured."""
@@ -118,7 +211,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="verify,decode", help="comma list of timed legs: verify, decode")
+    ap.add_argument("--legs", default="verify,decode,prefill",
+                    help="comma list of timed legs: verify, decode, prefill")
+    ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--copy-calib", action="store_true", help="run 3 x 256 MiB device copies first (PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -223,6 +318,11 @@ def main():
         log(f"moe_decode {us_moe:.2f} us per launch pair, {moe_gbs:.0f} GB/s algorithmic")
 
 
+    prefill = None
+    if "prefill" in legs:
+        prefill = prefill_leg(pool, weights, biases, min(args.prefill_layers, NL), max(args.steps // 5, 3),
+                              max(args.warmup // 5, 1), dev)
+
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline")
@@ -254,6 +354,7 @@ def main():
                      "us_per_launch": round(us_layer, 3), "bytes_per_launch": int(bytes_step / NL)},
         "moe_decode": None if us_moe is None else {
             "us_per_launch": round(us_moe, 3), "bytes_per_launch": int(moe_bytes), "achieved_gbs": round(moe_gbs, 1)},
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
