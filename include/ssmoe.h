@@ -132,12 +132,12 @@ int ssmoe_moe_align(const int32_t* local_expert, int64_t R, int num_local, int b
                     int64_t workspace_bytes, int32_t* sorted_rows, int32_t* block_expert, int32_t* num_padded,
                     void* stream);
 
-/* Grouped affine-4bit MoE over an aligned plan (block_m = 64): h = bf16(silu(x Wg^T) * (x Wu^T)) with weights
+/* Grouped affine-4bit MoE over an aligned plan (block_m = 128): h = bf16(silu(x Wg^T) * (x Wu^T)) with weights
  * dequantized to bf16(q*s + b), bf16 MFMA and fp32 accumulation, then out_rows = (h Wd^T) * row_weight in fp32.
  * Replaces fused_moe_affine's two launches (kernels/fused_moe_affine.py:136-161, kernels :39-108).
  * x bf16 [T, H]; row_token int32 [R] (a token outside [0, T) reads as a zero row); row_weight fp32 [R];
  * group_ptr int64 [num_local] record bases; h_buf bf16
- * [R, I]; out_rows fp32 [R, H] (rows outside the plan are not written). H % 128 == 0, I % 64 == 0. */
+ * [R, I]; out_rows fp32 [R, H] (rows outside the plan are not written). H % 256 == 0, I % 128 == 0, H, I <= 4096. */
 int ssmoe_fused_moe_affine(const uint16_t* x, const int32_t* row_token, const float* row_weight,
                            const int32_t* sorted_rows, const int32_t* block_expert, const int32_t* num_padded,
                            const int64_t* group_ptr, int num_local, uint16_t* h_buf, float* out_rows, int64_t R,

@@ -74,7 +74,7 @@ int64_t padded_rows(int64_t R, int num_local, int block_m);
 int64_t align_scratch_ints(int64_t R, int num_local);
 hipError_t launch_moe_align(const AlignArgs& a, hipStream_t st);
 
-constexpr int kPrefillBlockM = 64;  // the moe_align block the grouped GEMM consumes
+constexpr int kPrefillBlockM = 128;  // the moe_align block the grouped GEMM consumes
 struct PrefillArgs {
   const uint16_t* x;            // bf16 [T, H]
   const int32_t* row_token;     // [R]

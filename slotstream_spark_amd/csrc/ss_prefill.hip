@@ -1,5 +1,5 @@
 // Prefill MoE: rows sorted into expert-contiguous blocks, a grouped bf16 MFMA GEMM over affine-4bit records
-// dequantized into LDS, and the rank-order combine.
+// dequantized into MFMA registers, and the rank-order combine.
 //
 // Semantics follow kernels/moe_align.py:11-48, kernels/fused_moe_affine.py:39-172 (the reference's prefill path):
 //  * moe_align: a stable counting sort of the rows by local expert (rows outside [0, num_local) are skipped); each
@@ -11,7 +11,9 @@
 //    in fp32, so one rounding of q*s + b, fused or not, gives the same value).
 //  * down: out_rows[r, n] = (sum_k h[r, k] * bf16(q*s + b)[n, k]) * row_weight[r], fp32.
 //  * combine: out[t] = ((o[t,0] + o[t,1]) + ...) + o[t,K-1], sequential fp32.
-// Tiles are constants of the kernel (64 rows x 64 columns x 64 K), never functions of R.
+// Tiles are constants of the kernel (128 rows x 256 weight rows x 64 K), never functions of R.
+#include <type_traits>
+
 #include "ss_common.hpp"
 #include "ss_launch.hpp"
 
@@ -164,30 +166,65 @@ hipError_t launch_moe_align(const AlignArgs& a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------- grouped GEMM
-// Block: 256 threads, 64 sorted rows x 128 weight rows (gate/up: 64 gate + the same 64 up rows; down: 128 rows),
-// K in steps of 64 (one quantisation group). Each step's operands arrive in LDS by direct-to-LDS loads into a ring
-// of kStages slots, kStages - 1 steps ahead of the MFMAs:
-//   A    64 rows x 128 B of bf16 activations; the 16-byte chunk c of row r sits in slot c ^ (r & 7), so the 16 rows an
-//        MFMA operand read touches fall in different banks;
-//   W    128 weight rows x 32 B of packed nibbles;
-//   S, B the scale and bias dwords (two groups each) of the 128 rows.
-// The step's weights are then dequantized once into a bf16 tile (bf16(q*s + b), rows 144 B apart) that the four
-// waves read as MFMA B operands; each wave owns 32 rows x 64 columns of the output.
-constexpr int kBM = 64;
+// Block: 256 threads (4 waves) x 128 sorted rows (one expert) x 256 weight rows, K in steps of 64 (one
+// quantisation group). Each wave owns 64 weight rows (four 16-column MFMA B fragments) for all 128 rows of the
+// block, so every weight of the block is dequantized exactly once, by the wave that multiplies it, straight into
+// MFMA B registers. Gate/up: wave w owns gate rows n0 + 32 w .. + 31 (fragments 0, 1) and the same up rows
+// (fragments 2, 3), so silu(g) * u is formed in registers. Down: wave w owns rows n0 + 64 w .. + 63.
+// K order inside a group: lane quad q (lane >> 4) holds packed words 2q, 2q + 1 of its weight row's group
+// (elements 16 q .. 16 q + 15); MFMA slice s (0, 1) uses word 2q + s, i.e. elements 16 q + 8 s .. + 7, and the A
+// fragment of slice s holds the same elements of each row. A dot product does not depend on which MFMA lanes its
+// K terms go to, only on the accumulation, which the MFMA unit fixes.
+// Memory paths:
+//  * A (activations for gate/up, h for down): global -> registers -> LDS, two stages, one K step ahead of the
+//    MFMAs; each load instruction covers 8 whole 128-byte rows (8 lanes per row). The register-staged path keeps
+//    every wait precise (a direct-to-LDS load in flight makes the compiler wait for it before any LDS read).
+//  * Scales and biases of the block's 256 weight rows for the whole K range: read once, coalesced, into LDS as
+//    (s, b) dword pairs.
+//  * Packed weights: 8 bytes per lane per K step straight into registers, two steps ahead.
+// 16-byte chunk c of A row m sits at chunk position a_pos(m, c) of the row's 128 bytes, so the 16 rows one MFMA
+// operand read touches (and each group of 8 of them) fall on distinct banks. Rows past the block's valid count
+// get no MFMAs beyond the last 32-row pair of fragments that holds a valid row.
+constexpr int kBM = 128;
 constexpr int kBK = 64;
-constexpr int kNR = 128;               // weight rows per block
-constexpr int kStages = 4;
-constexpr int kOffA = 0, kOffW = 8192, kOffS = 12288, kOffB = 12800, kStageBytes = 13312;
-constexpr int kTileRow = 72;           // bf16 per row of the dequantized tile
-constexpr int kTileBytes = kNR * kTileRow * 2;
-constexpr size_t kGemmLds = (size_t)kStages * kStageBytes + kTileBytes;
+constexpr int kAStage = kBM * kBK * 2;  // 16 KB
+constexpr int kGateUpTileN = 128;       // gate (and up) rows per block
+constexpr int kDownTileN = 256;         // down rows per block
+constexpr int kBN = 256;                // weight rows per block (both kernels)
+constexpr int kMaxGroups = 64;          // K / 64 <= 64 (H, I <= 4096)
+// Dynamic LDS of one block: the two A stages, then the (s, b) table of kBN rows x (G + 1) dwords (G = K / 64; the
+// extra dword per row staggers the banks). Two blocks per CU fit for G <= 60.
+static size_t gemm_lds_bytes(int G) { return 2 * (size_t)kAStage + (size_t)kBN * (G + 1) * 4; }
+constexpr size_t kGemmLdsMax = 2 * kAStage + (size_t)kBN * (kMaxGroups + 1) * 4;
 
 typedef __bf16 ss_bf16x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t ss_u32x2 __attribute__((ext_vector_type(2)));
 
 // bf16 pair (lo, hi) rounded to nearest even by the hardware conversion.
 SS_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
   const ss_bf16x2 v = {(__bf16)lo, (__bf16)hi};
   return __builtin_bit_cast(uint32_t, v);
+}
+
+SS_DEV uint32_t and_opaque(uint32_t x, uint32_t m) {
+  uint32_t r;
+  asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(m), "v"(x));
+  return r;
+}
+
+// 8 nibbles (element e at bits 4e) -> bf16(q * s + b) x 8 as an MFMA operand (pairs low element first). q * s is
+// exact in fp32 (4-bit by 8-bit mantissas), so the fused q * s + b has the one rounding of the reference's fp32
+// q * s + b, then one rounding to bf16.
+SS_DEV ss_u32x4 dequant8(uint32_t w, float sc, float bi) {
+  // The masks are opaque to the compiler, so each byte converts with one v_cvt_f32_ubyteN (folded into a
+  // bit-field extract they would cost two instructions).
+  const uint32_t lo = and_opaque(w, 0x0F0F0F0Fu), hi = and_opaque(w >> 4, 0x0F0F0F0Fu);
+  ss_u32x4 r;
+  r.x = cvt_pk_bf16(__builtin_fmaf((float)(lo & 0xFFu), sc, bi), __builtin_fmaf((float)(hi & 0xFFu), sc, bi));
+  r.y = cvt_pk_bf16(__builtin_fmaf((float)((lo >> 8) & 0xFFu), sc, bi), __builtin_fmaf((float)((hi >> 8) & 0xFFu), sc, bi));
+  r.z = cvt_pk_bf16(__builtin_fmaf((float)((lo >> 16) & 0xFFu), sc, bi), __builtin_fmaf((float)((hi >> 16) & 0xFFu), sc, bi));
+  r.w = cvt_pk_bf16(__builtin_fmaf((float)(lo >> 24), sc, bi), __builtin_fmaf((float)(hi >> 24), sc, bi));
+  return r;
 }
 
 struct GemmArgs {
@@ -206,222 +243,278 @@ struct GemmArgs {
   int64_t w2_off, s2_off, b2_off;  // up pieces (gate/up)
 };
 
-SS_DEV void waitcnt_vm(int n) {
-  // s_waitcnt with only vmcnt constrained (expcnt and lgkmcnt at their maxima); n in {0, 4, 8}.
-  if (n >= 8) __builtin_amdgcn_s_waitcnt(0xF78);
-  else if (n >= 4) __builtin_amdgcn_s_waitcnt(0xF74);
-  else __builtin_amdgcn_s_waitcnt(0xF70);
+// LDS barrier for data exchanged through LDS only: waits for this wave's LDS operations, not for its global loads
+// in flight (which a workgroup-scope fence would also wait for).
+SS_DEV void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// The shared main loop. GATE_UP: rows 0..63 of the weight tile are gate rows n0 + r, rows 64..127 the up rows
-// n0 + r; otherwise 128 consecutive down rows n0 + r. kdim = the K extent, wstride = weight row bytes (kdim / 2),
-// sstride = scale row bytes (kdim / 32). acc[i][j]: output rows 32 wm + 16 i, tile columns 64 wn + 16 j.
-template <bool GATE_UP>
-SS_DEV void gemm_main(const GemmArgs& g, uint8_t* lds, const int* src_row, const uint8_t* base, int n0, int kdim,
-                      int astride, ss_f32x4 (&acc)[2][4]) {
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  uint8_t* tile = lds + kStages * kStageBytes;
-  const int nsteps = kdim / kBK;
-  const int64_t wstride = kdim / 2, sstride = kdim / 32;
-  // DMA sources of this lane (A: two instructions q = 2w, 2w+1 covering rows 8q .. 8q+7).
-  const uint16_t* asrc[2];
-#pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int row = 8 * (2 * w + i) + (lane >> 3);
-    const int chunk = (lane & 7) ^ (row & 7);
-    asrc[i] = g.a + (int64_t)src_row[row] * astride + 8 * chunk;
-  }
-  const int wrow = 32 * w + (lane >> 1);
-  const bool up_row = GATE_UP && wrow >= 64;
-  const int64_t wrow_g = n0 + (GATE_UP ? (wrow & 63) : wrow);
-  const uint8_t* wsrc = base + (up_row ? g.w2_off : g.w_off) + wrow_g * wstride + 16 * (lane & 1);
-  // scale / bias dwords: waves 0, 1 scales of rows 64 w + lane; waves 2, 3 biases of rows 64 (w - 2) + lane.
-  const int srow = 64 * (w & 1) + lane;
-  const bool s_up = GATE_UP && srow >= 64;
-  const int64_t srow_g = n0 + (GATE_UP ? (srow & 63) : srow);
-  const int64_t soff = (w < 2) ? (s_up ? g.s2_off : g.s_off) : (s_up ? g.b2_off : g.b_off);
-  const uint8_t* ssrc = base + soff + srow_g * sstride;
-  auto issue = [&](int ks) {
-    uint8_t* st = lds + (ks % kStages) * kStageBytes;
-    const int k0 = ks * kBK;
-#pragma unroll
-    for (int i = 0; i < 2; ++i)
-      __builtin_amdgcn_global_load_lds(asrc[i] + k0, (__attribute__((address_space(3))) void*)(st + kOffA + 1024 * (2 * w + i)), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(wsrc + k0 / 2, (__attribute__((address_space(3))) void*)(st + kOffW + 1024 * w), 16, 0, 0);
-    __builtin_amdgcn_global_load_lds(ssrc + ((2 * ks) & ~3), (__attribute__((address_space(3))) void*)(st + (w < 2 ? kOffS + 256 * w : kOffB + 256 * (w - 2))), 4, 0, 0);
-  };
-#pragma unroll
-  for (int ks = 0; ks < kStages - 1; ++ks)
-    if (ks < nsteps) issue(ks);
-  const int wm = w >> 1, wn = w & 1;
-  const int fr = lane & 15, fq = lane >> 4;
-  const int drow = tid >> 1, dhalf = tid & 1;  // dequant role: one 16-byte word of one weight row
-#pragma unroll 1
-  for (int ks = 0; ks < nsteps; ++ks) {
-    const int ahead = nsteps - 1 - ks;
-    waitcnt_vm(4 * (ahead < kStages - 2 ? ahead : kStages - 2));
-    __syncthreads();
-    if (ks + kStages - 1 < nsteps) issue(ks + kStages - 1);
-    const uint8_t* st = lds + (ks % kStages) * kStageBytes;
-    {
-      const uint4 wv = *reinterpret_cast<const uint4*>(st + kOffW + 32 * drow + 16 * dhalf);
-      const uint32_t sw = *reinterpret_cast<const uint32_t*>(st + kOffS + 4 * drow);
-      const uint32_t bw = *reinterpret_cast<const uint32_t*>(st + kOffB + 4 * drow);
-      const float sc = __uint_as_float((ks & 1) ? (sw & 0xFFFF0000u) : (sw << 16));
-      const float bi = __uint_as_float((ks & 1) ? (bw & 0xFFFF0000u) : (bw << 16));
-      const uint32_t ww[4] = {wv.x, wv.y, wv.z, wv.w};
-      uint32_t o[16];
-#pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t lo = ww[d] & 0x0F0F0F0Fu, hi = (ww[d] >> 4) & 0x0F0F0F0Fu;
-        const float q0 = (float)((lo >> 0) & 0xFFu), q1 = (float)((hi >> 0) & 0xFFu);
-        const float q2 = (float)((lo >> 8) & 0xFFu), q3 = (float)((hi >> 8) & 0xFFu);
-        const float q4 = (float)((lo >> 16) & 0xFFu), q5 = (float)((hi >> 16) & 0xFFu);
-        const float q6 = (float)((lo >> 24) & 0xFFu), q7 = (float)((hi >> 24) & 0xFFu);
-        o[4 * d + 0] = cvt_pk_bf16(__builtin_fmaf(q0, sc, bi), __builtin_fmaf(q1, sc, bi));
-        o[4 * d + 1] = cvt_pk_bf16(__builtin_fmaf(q2, sc, bi), __builtin_fmaf(q3, sc, bi));
-        o[4 * d + 2] = cvt_pk_bf16(__builtin_fmaf(q4, sc, bi), __builtin_fmaf(q5, sc, bi));
-        o[4 * d + 3] = cvt_pk_bf16(__builtin_fmaf(q6, sc, bi), __builtin_fmaf(q7, sc, bi));
-      }
-      uint4* dst = reinterpret_cast<uint4*>(tile + (drow * kTileRow + 32 * dhalf) * 2);
-#pragma unroll
-      for (int q = 0; q < 4; ++q) dst[q] = make_uint4(o[4 * q], o[4 * q + 1], o[4 * q + 2], o[4 * q + 3]);
-    }
-    __syncthreads();
-#pragma unroll
-    for (int kk = 0; kk < kBK; kk += 32) {
-      ss_u32x4 af[2], bf[4];
-#pragma unroll
-      for (int i = 0; i < 2; ++i) {
-        const int m = 32 * wm + 16 * i + fr;
-        const int chunk = (kk >> 3) + fq;
-        af[i] = *reinterpret_cast<const ss_u32x4*>(st + kOffA + 128 * m + 16 * (chunk ^ (m & 7)));
-      }
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int col = GATE_UP ? (j < 2 ? 32 * wn + 16 * j + fr : 64 + 32 * wn + 16 * (j - 2) + fr)
-                                : 64 * wn + 16 * j + fr;
-        bf[j] = *reinterpret_cast<const ss_u32x4*>(tile + (col * kTileRow + kk + 8 * fq) * 2);
-      }
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = ss_mfma(af[i], bf[j], acc[i][j]);
-    }
-  }
-}
-
-// Gate/up: one block per (M block, 64-column N tile), mapped by xcd_tile. Output h[r, n0 .. n0 + 63] = bf16(silu(g) * u).
-// Workgroups are dealt to the 8 XCDs round-robin (b % 8). Block b is mapped to M block m and N tile n so that
-// the N tiles of one M block run on one XCD, one after another: the gathered activation rows of the M block are
-// read once into that XCD's L2 instead of once per XCD.
-SS_DEV bool xcd_tile(int nt, int mb, int& pid_n, int& pid_m) {
+// Block index -> (M block, N tile). The plan's M blocks times the N tiles are split into 8 contiguous ranges, one
+// per XCD (workgroups are dealt to the XCDs round-robin, b % 8): the M blocks of one expert, which share its
+// weights, and the N tiles of one M block, which share its activation rows, stay on one XCD and its L2.
+SS_DEV bool xcd_tile(int mb, int nt, int& pid_m, int& pid_n) {
   const int b = blockIdx.x;
-  const int xcd = b & 7, j = b >> 3;
-  pid_m = (j / nt) * 8 + xcd;
-  pid_n = j % nt;
-  return pid_m < mb;
+  const int total = mb * nt;
+  const int per = (total + 7) >> 3;
+  const int slot = b >> 3;
+  const int L = (b & 7) * per + slot;
+  if (slot >= per || L >= total) return false;
+  pid_m = L / nt;
+  pid_n = L - pid_m * nt;
+  return true;
 }
 
-__global__ __launch_bounds__(256) void prefill_gate_up_kernel(GemmArgs g, int nt, int mb) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds_g[];
-  __shared__ int src_row[kBM];
-  __shared__ int out_row[kBM];
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  int pid_n, pid_m;
-  if (!xcd_tile(nt, mb, pid_n, pid_m)) return;
-  if ((int64_t)pid_m * kBM >= (int64_t)g.num_padded[0]) return;
-  const int e = g.block_expert[pid_m];
-  if (e < 0) return;
-  const uint8_t* base = reinterpret_cast<const uint8_t*>(g.group_ptr[e]);
-  if (tid < kBM) {
-    const int r = g.sorted_rows[(int64_t)pid_m * kBM + tid];
-    const int t = r < g.R ? g.row_token[r] : -1;
-    const bool ok = t >= 0 && t < g.T;
-    out_row[tid] = ok ? r : -1;
-    src_row[tid] = ok ? t : 0;  // padding rows read token 0; their outputs are never stored
-  }
-  __syncthreads();
-  ss_f32x4 acc[2][4];
+// 16-byte chunk c of A row m sits at chunk position a_pos(m, c) of the row's 128 bytes.
+SS_DEV int a_pos(int m, int c) { return c ^ (m & 7) ^ ((m >> 3) & 1); }
+
+// Local index of weight row (fragment j, lane row n) of wave w: 64 w + 16 j + n; the (s, b) table row stride is
+// G + 1 dwords, so 16 consecutive rows at one group fall on distinct banks.
+
+// The K loop for NF live 16-row fragments (fragments NF .. 7 are all padding and get no MFMAs).
+template <int NF>
+SS_DEV void gemm_loop(uint8_t* lds, const uint32_t* sbt, int nsteps, int aoff0, int aoff1, ss_f32x4 (&acc)[8][4],
+                      const uint16_t* const (&asrc)[4], int arow0, int achunk, const uint8_t* wbase,
+                      const int64_t (&wc)[4], uint32_t lw, int sb_lane, int sb_stride) {
+  uint4 areg[4];
+  auto load_a = [&](int k) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int c = 0; c < 4; ++c) areg[c] = ldg16(asrc[c] + (size_t)k * kBK);
+  };
+  auto store_a = [&](int stage) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = ss_f32x4{0.f, 0.f, 0.f, 0.f};
-  const int n0 = pid_n * 64;
-  gemm_main<true>(g, lds_g, src_row, base, n0, g.H, g.H, acc);
-  const int wm = w >> 1, wn = w & 1;
-  // acc[i][0..1]: gate columns 32 wn + 16 j, acc[i][2..3]: the matching up columns.
+    for (int c = 0; c < 4; ++c) {
+      const int m = arow0 + 8 * c;
+      *reinterpret_cast<uint4*>(lds + stage * kAStage + m * (kBK * 2) + 16 * a_pos(m, achunk)) = areg[c];
+    }
+  };
+  ss_u32x2 bw[2][4];
+  auto load_b = [&](int k, const int slot) {
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int j = 0; j < 4; ++j) bw[slot][j] = *(const SS_G ss_u32x2*)(wbase + wc[j] + lw + 32 * k);
+  };
+  load_a(0);
+  load_b(0, 0);
+  store_a(0);
+  load_a(1);
+  load_b(1, 1);
+  lds_barrier();
+  // One K step on register slot SLOT (= k & 1, a constant so that both slots stay in fixed registers and every wait
+  // the compiler inserts covers exactly the loads of this step).
+  auto step = [&](int k, auto slot_c) {
+    constexpr int SLOT = decltype(slot_c)::value;
+    const uint8_t* st = lds + SLOT * kAStage;
+    float sc[4], bi[4];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t sb = sbt[sb_lane + 16 * j * sb_stride + k];
+      sc[j] = __uint_as_float(sb << 16);
+      bi[j] = __uint_as_float(sb & 0xFFFF0000u);
+    }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = 32 * wm + 16 * i + 4 * (lane >> 4) + q;
-        const int r = out_row[m];
-        if (r < 0) continue;
-        const float gv = acc[i][j][q], uv = acc[i][j + 2][q];
-        const float hv = gv / (1.f + ss_expf(-gv)) * uv;
-        const int n = n0 + 32 * wn + 16 * j + (lane & 15);
-        g.h[(int64_t)r * g.I + n] = (uint16_t)ss_f32_to_bf16(hv);
+    for (int s = 0; s < 2; ++s) {
+      ss_u32x4 bf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bf[j] = dequant8(s ? bw[SLOT][j].y : bw[SLOT][j].x, sc[j], bi[j]);
+      const uint8_t* ap = st + (s ? aoff1 : aoff0);
+      // A fragments in batches of up to four: one LDS wait per batch. The scheduling barriers keep one slice's
+      // operands live at a time (the register budget of two waves per SIMD); the two waves of a SIMD overlap one
+      // wave's dequantization with the other's MFMAs.
+#pragma unroll
+      for (int i0 = 0; i0 < NF; i0 += 4) {
+        constexpr int NB = NF < 4 ? NF : 4;
+        ss_u32x4 av[NB];
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+          if (i0 + i < NF) av[i] = *reinterpret_cast<const ss_u32x4*>(ap + (i0 + i) * 16 * (kBK * 2));
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+          if (i0 + i < NF)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[i0 + i][j] = ss_mfma(av[i], bf[j], acc[i0 + i][j]);
+        __builtin_amdgcn_sched_barrier(0);
       }
+    }
+    // The steps past the end reload the last one (never used): every iteration issues the same loads.
+    store_a(SLOT ^ 1);
+    const int kn = k + 2 < nsteps ? k + 2 : nsteps - 1;
+    load_a(kn);
+    load_b(kn, SLOT);
+    lds_barrier();
+  };
+#pragma unroll 1
+  for (int k = 0; k < nsteps; k += 2) {
+    step(k, std::integral_constant<int, 0>{});
+    step(k + 1, std::integral_constant<int, 1>{});
+  }
 }
 
-// Down: one block per (M block, 128-row N tile), mapped by xcd_tile. Output out_rows[r, n0 .. n0 + 127] = (h Wd^T) * row_weight.
-__global__ __launch_bounds__(256) void prefill_down_kernel(GemmArgs g, int nt, int mb) {
-  extern __shared__ __attribute__((aligned(16))) uint8_t lds_d[];
-  __shared__ int src_row[kBM];
+template <bool GATE_UP>
+__global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs g, int nt) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ int64_t a_off[kBM];  // element offset of each row's A operand, -1 for a zero row
   __shared__ int out_row[kBM];
   __shared__ float wt_s[kBM];
+  uint32_t* sbt = reinterpret_cast<uint32_t*>(lds + 2 * kAStage);  // [kBN][G + 1] (s | b << 16)
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  int pid_n, pid_m;
-  if (!xcd_tile(nt, mb, pid_n, pid_m)) return;
-  if ((int64_t)pid_m * kBM >= (int64_t)g.num_padded[0]) return;
+  const int mb = g.num_padded[0] / kBM;
+  int pid_m, pid_n;
+  if (!xcd_tile(mb, nt, pid_m, pid_n)) return;
   const int e = g.block_expert[pid_m];
   if (e < 0) return;
   const uint8_t* base = reinterpret_cast<const uint8_t*>(g.group_ptr[e]);
+  const int kdim = GATE_UP ? g.H : g.I;
+  const int G = kdim / 64, sb_stride = G + 1;
+  bool valid = false;
   if (tid < kBM) {
     const int r = g.sorted_rows[(int64_t)pid_m * kBM + tid];
-    const bool ok = r < g.R;
-    out_row[tid] = ok ? r : -1;
-    src_row[tid] = ok ? r : 0;
-    wt_s[tid] = ok ? g.row_weight[r] : 0.f;
+    valid = r < g.R;
+    int64_t off = -1;  // -1: a zero row (a token outside [0, T))
+    if (valid) {
+      if (GATE_UP) {
+        const int t = g.row_token[r];
+        if (t >= 0 && t < g.T) off = (int64_t)t * g.H;
+      } else {
+        off = (int64_t)r * g.I;
+      }
+    }
+    a_off[tid] = off;
+    out_row[tid] = valid ? r : -1;
+    if (!GATE_UP) wt_s[tid] = valid ? g.row_weight[r] : 0.f;
   }
-  __syncthreads();
-  ss_f32x4 acc[2][4];
+  // Global weight row of local row lr (0 .. 255) and its piece: gate/up local rows 64 w + 16 j + n map to gate rows
+  // (j < 2) or up rows (j >= 2) n0 + 32 w + 16 (j & 1) + n; down local rows are rows n0 + lr.
+  auto grow = [&](int lr, bool& up) -> int64_t {
+    if (GATE_UP) {
+      const int ww = lr >> 6, j = (lr >> 4) & 3, nn = lr & 15;
+      up = j >= 2;
+      return (int64_t)pid_n * kGateUpTileN + 32 * ww + 16 * (j & 1) + nn;
+    }
+    up = false;
+    return (int64_t)pid_n * kDownTileN + lr;
+  };
+  // (s, b) table: thread t fills local rows t (one row, all G groups; 16-byte loads of 8 groups).
+  {
+    bool up;
+    const int64_t row = grow(tid, up);
+    const uint8_t* srow = base + (up ? g.s2_off : g.s_off) + row * G * 2;
+    const uint8_t* brow = base + (up ? g.b2_off : g.b_off) + row * G * 2;
+    uint32_t* dst = sbt + tid * sb_stride;
+    if (G % 8 == 0) {
+      for (int c = 0; c < G; c += 8) {
+        const uint4 sv = ldg16(srow + 2 * c), bv = ldg16(brow + 2 * c);
+        const uint32_t s4[4] = {sv.x, sv.y, sv.z, sv.w}, b4[4] = {bv.x, bv.y, bv.z, bv.w};
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+        for (int d = 0; d < 4; ++d) {
+          dst[c + 2 * d] = (s4[d] & 0xFFFFu) | (b4[d] << 16);
+          dst[c + 2 * d + 1] = (s4[d] >> 16) | (b4[d] & 0xFFFF0000u);
+        }
+      }
+    } else {  // G is even (K is a multiple of 128): two groups per dword
+      for (int c = 0; c < G; c += 2) {
+        const uint32_t sv = *(const SS_G uint32_t*)(srow + 2 * c), bv = *(const SS_G uint32_t*)(brow + 2 * c);
+        dst[c] = (sv & 0xFFFFu) | (bv << 16);
+        dst[c + 1] = (sv >> 16) | (bv & 0xFFFF0000u);
+      }
+    }
+  }
+  // Valid rows are a prefix of the block (each expert's rows come first in its padded range).
+  const int nvalid = __syncthreads_count(valid);
+
+  // A staging: load instruction c of thread (w, lane) covers row arow0 + 8 c (arow0 = 32 w + (lane >> 3)), 16-byte
+  // chunk lane & 7. A padding row or a zero row reads the first kdim elements of the expert record (always
+  // present): a padding row's MFMA output row is never stored, and a zero row's h is stored as 0 (silu(0) * 0).
+  const int arow0 = 32 * w + (lane >> 3), achunk = lane & 7;
+  const uint16_t* asrc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const int m = arow0 + 8 * c;
+    const int64_t off = a_off[m];
+    asrc[c] = (m < nvalid && off >= 0 ? g.a + off : reinterpret_cast<const uint16_t*>(base)) + 8 * achunk;
+  }
+  // B: lane (n = lane & 15, q = lane >> 4) of fragment j reads words 2q, 2q + 1 of its row's group.
+  const int n = lane & 15, q = lane >> 4;
+  const int64_t wrow_b = kdim / 2;
+  int64_t wc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    bool up;
+    const int64_t row0 = grow(64 * w + 16 * j, up);
+    wc[j] = (up ? g.w2_off : g.w_off) + row0 * wrow_b;
+  }
+  const uint32_t lw = (uint32_t)(n * wrow_b + 8 * q);
+  const int sb_lane = (64 * w + n) * sb_stride;
+
+  ss_f32x4 acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) acc[i][j] = ss_f32x4{0.f, 0.f, 0.f, 0.f};
-  const int n0 = pid_n * kNR;
-  gemm_main<false>(g, lds_d, src_row, base, n0, g.I, g.I, acc);
-  const int wm = w >> 1, wn = w & 1;
+
+  // Lane offsets of the A fragments (slice s): row 16 i + n, chunk 2q + s (a_pos depends on n only).
+  const int aoff0 = n * (kBK * 2) + 16 * a_pos(n, 2 * q);
+  const int aoff1 = n * (kBK * 2) + 16 * a_pos(n, 2 * q + 1);
+  const int nsteps = kdim / kBK;  // even: kdim is a multiple of 128
+  const int nf2 = (nvalid + 31) >> 5;  // live fragment pairs (1..4)
+  if (nf2 >= 4)
+    gemm_loop<8>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
+  else if (nf2 == 3)
+    gemm_loop<6>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
+  else if (nf2 == 2)
+    gemm_loop<4>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
+  else
+    gemm_loop<2>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
+
+  if (GATE_UP) {
+    // h = bf16(silu(g) * u) into an LDS tile [128 rows][128 columns], then 16-byte row-contiguous stores.
+    uint16_t* ht = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = 32 * wm + 16 * i + 4 * (lane >> 4) + q;
-        const int r = out_row[m];
-        if (r < 0) continue;
-        const int n = n0 + 64 * wn + 16 * j + (lane & 15);
-        g.out_rows[(int64_t)r * g.H + n] = acc[i][j][q] * wt_s[m];
+        for (int r = 0; r < 4; ++r) {
+          const int m = 16 * i + 4 * q + r;
+          const float gv = acc[i][j][r], uv = acc[i][j + 2][r];
+          // silu with the hardware exp2 and reciprocal (about 1 ulp each): h is rounded to bf16 next, which
+          // hides fp32 differences of a few ulp except at a rounding tie.
+          const float sig = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(gv * -1.4426950408889634f));
+          const float hv = a_off[m] >= 0 ? gv * sig * uv : 0.f;
+          ht[m * kGateUpTileN + 32 * w + 16 * j + n] = (uint16_t)ss_f32_to_bf16(hv);
+        }
+    lds_barrier();
+    const int n0 = pid_n * kGateUpTileN;
+#pragma unroll
+    for (int u = 0; u < (kBM * kGateUpTileN * 2) / (16 * 256); ++u) {
+      const int id = u * 256 + tid;
+      const int m = id >> 4, cc = id & 15;
+      const int r = out_row[m];
+      if (r >= 0) {
+        const uint4 v = *reinterpret_cast<const uint4*>(ht + m * kGateUpTileN + 8 * cc);
+        stg16(g.h + (int64_t)r * g.I + n0 + 8 * cc, v);
       }
+    }
+  } else {
+    const int n0 = pid_n * kDownTileN + 64 * w;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * i + 4 * q + r;
+        const int orow = out_row[m];
+        if (orow >= 0) {
+          const float wt = wt_s[m];
+          float* dst = g.out_rows + (int64_t)orow * g.H + n0 + n;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dst[16 * j] = acc[i][j][r] * wt;
+        }
+      }
+  }
 }
 
 hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
   static_assert(kBM == kPrefillBlockM, "one block size for the plan and the GEMM");
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gate_up_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_down_kernel),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLds);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
   const SsRecord rec = ss_record_layout(p.H, p.I);
   const int64_t P = padded_rows(p.R, p.num_local, kBM);
   if (P == 0 || p.R == 0) return hipSuccess;
@@ -445,15 +538,29 @@ hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
   g.w2_off = rec.uw;
   g.s2_off = rec.us;
   g.b2_off = rec.ub;
-  const int mb = (int)(P / kBM), mb8 = (mb + 7) / 8 * 8;
-  hipLaunchKernelGGL(prefill_gate_up_kernel, dim3((unsigned)(mb8 * (p.I / 64))), dim3(256), kGemmLds, st, g, p.I / 64,
-                     mb);
+  // Grids cover the plan's upper bound of M blocks, rounded to whole XCD rounds; blocks past the device-side
+  // count exit at once.
+  static bool attr = false;
+  if (!attr) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gemm_kernel<true>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLdsMax);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gemm_kernel<false>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLdsMax);
+    if (e != hipSuccess) return e;
+    attr = true;
+  }
+  const int64_t mb = P / kBM;
+  const int nt_gu = p.I / kGateUpTileN, nt_d = p.H / kDownTileN;
+  auto grid_of = [&](int nt) { return (unsigned)(((mb * nt + 7) / 8) * 8); };
+  hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(grid_of(nt_gu)), dim3(256), gemm_lds_bytes(p.H / 64), st, g,
+                     nt_gu);
   g.a = p.h_buf;
   g.w_off = rec.dw;
   g.s_off = rec.ds;
   g.b_off = rec.db;
-  hipLaunchKernelGGL(prefill_down_kernel, dim3((unsigned)(mb8 * (p.H / kNR))), dim3(256), kGemmLds, st, g, p.H / kNR,
-                     mb);
+  hipLaunchKernelGGL(prefill_gemm_kernel<false>, dim3(grid_of(nt_d)), dim3(256), gemm_lds_bytes(p.I / 64), st, g,
+                     nt_d);
   return hipGetLastError();
 }
 

@@ -380,8 +380,8 @@ int ssmoe_moe_align(const int32_t* local_expert, int64_t R, int num_local, int b
 
 static int check_prefill_shape(int64_t R, int H, int I) {
   if (R < 0 || R > (1ll << 30)) return fail(SSMOE_EINVAL, "R must be in [0, 2^30], got %lld", (long long)R);
-  if (H < 128 || H % 128) return fail(SSMOE_EINVAL, "H must be a positive multiple of 128, got %d", H);
-  if (I < 64 || I % 64) return fail(SSMOE_EINVAL, "I must be a positive multiple of 64, got %d", I);
+  if (H < 256 || H % 256 || H > 4096) return fail(SSMOE_EINVAL, "H must be a multiple of 256 in [256, 4096], got %d", H);
+  if (I < 128 || I % 128 || I > 4096) return fail(SSMOE_EINVAL, "I must be a multiple of 128 in [128, 4096], got %d", I);
   return ok();
 }
 
@@ -424,7 +424,7 @@ int ssmoe_combine_rank_order(const float* out_rows, int T, int K, int H, float* 
 }
 
 // Workspace of ssmoe_moe_prefill: local [R], row_token [R], group_ptr [E] (8-byte), sorted_rows [P],
-// block_expert [P / 64], num_padded, then the moe_align scratch.
+// block_expert [P / kPrefillBlockM], num_padded, then the moe_align scratch.
 struct PrefillWs {
   int64_t local, row_token, gptr, sorted, bexp, npad, scratch, total;
 };

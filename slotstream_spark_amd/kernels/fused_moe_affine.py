@@ -1,10 +1,12 @@
 """Grouped affine 4-bit MoE for prefill on gfx950 (drop-in for slotstream_spark/kernels/fused_moe_affine.py).
 
-Two launches over an aligned plan (BLOCK_M = 64): gate/up writes h = silu(x Wg^T) * (x Wu^T) as bf16 [R, I]; down
-writes y = (h Wd^T) * w as fp32 [R, H] into `out_rows`. Each block stages 64 sorted rows of activations and the
-expert's weight tile, dequantized to bf16(q*s + b) (the reference's _wtile rounding), in LDS and runs bf16 MFMA
-16x16x32 with fp32 accumulation; global loads of the next K step overlap the MFMAs of the current one. Tiles are
-constants (64 x 64 x 64), never functions of R, so a row's bits depend on that row and that record only.
+Two launches over an aligned plan (BLOCK_M = 128): gate/up writes h = silu(x Wg^T) * (x Wu^T) as bf16 [R, I]; down
+writes y = (h Wd^T) * w as fp32 [R, H] into `out_rows`. Each block takes 128 sorted rows of one expert and 256 of
+its weight rows: the weights are dequantized to bf16(q*s + b) (the reference's _wtile rounding) straight into MFMA
+registers, the activation rows are staged in LDS, and bf16 MFMA 16x16x32 accumulates in fp32; the loads of the next
+K steps overlap the MFMAs of the current one. Tiles are constants (128 x 256 x 64), never functions of R, so a
+row's bits depend on that row and that record only. The reference's BLOCK_M is 64; a plan here is aligned to 128
+(align_rows produces it), which only changes the padding, never a row's result.
 
 Differences from the reference interface: the shape is read from the tensors (the reference fixes H 2560, I 640)
 and a group may hold up to 4096 experts, because every expert of a layer is resident in HBM and one plan covers
@@ -17,7 +19,7 @@ import torch
 from .. import _lib
 from .moe_align import moe_align
 
-BLOCK_M = 64
+BLOCK_M = 128
 GROUP_MAX = 4096
 
 

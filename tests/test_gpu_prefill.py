@@ -8,7 +8,7 @@ import torch
 from oracle import oracle as O
 from slotstream_spark_amd import _lib
 from slotstream_spark_amd.engine.prefill import MoEPrefillLayer
-from slotstream_spark_amd.kernels.fused_moe_affine import align_rows, combine_rank_order, fused_moe_affine
+from slotstream_spark_amd.kernels.fused_moe_affine import BLOCK_M, align_rows, combine_rank_order, fused_moe_affine
 from slotstream_spark_amd.kernels.moe_align import moe_align
 from slotstream_spark_amd.memory.synth import LayerWeights, normal_bf16, zipf_bias
 from tests.gpu_util import DenseCache, bits, make_pool, rand_ids, rand_weights
@@ -119,7 +119,7 @@ def test_fused_moe_affine_group_semantics():
     assert np.all(got[~in_group] == 7.0)
     assert O.rel_l2(got[in_group], rows_ref[in_group]) < 2e-3
     s, b, n = align_rows(row_expert, emap.cuda(), len(group))
-    rs, rb, rn = O.moe_align(np.where(in_group, emap.numpy()[row_expert.cpu().numpy()], -1), len(group), 64)
+    rs, rb, rn = O.moe_align(np.where(in_group, emap.numpy()[row_expert.cpu().numpy()], -1), len(group), BLOCK_M)
     assert np.array_equal(s.cpu().numpy(), rs) and int(n.item()) == rn
 
 
