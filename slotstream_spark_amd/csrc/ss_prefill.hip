@@ -206,24 +206,27 @@ SS_DEV uint32_t cvt_pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// 8 nibbles (element e at bits 4e) -> bf16(q * s + b) x 8 as an MFMA operand (pairs low element first).
+// A nibble q in a byte of its own is the OCP fp8 e4m3 value q * 2^-9 exactly (q < 8 subnormal, q >= 8 with
+// exponent field 1), so one v_cvt_pk_f32_fp8 turns two nibbles into fp32. s9 = s * 2^9 (exact), hence
+// (q * 2^-9) * s9 = q * s exactly and the fused multiply-add rounds q * s + b once, as the reference's fp32
+// q * s + b does (q * s is exact in fp32: 4-bit by 8-bit mantissas); then one rounding to bf16. (A scale of 2^119
+// or more would overflow s9; bf16 weight scales are far below that.) The masks are opaque to the compiler, so it
+// keeps them as two v_and_b32 instead of folding them into per-nibble bit-field extracts.
 SS_DEV uint32_t and_opaque(uint32_t x, uint32_t m) {
   uint32_t r;
   asm("v_and_b32 %0, %1, %2" : "=v"(r) : "s"(m), "v"(x));
   return r;
 }
-
-// 8 nibbles (element e at bits 4e) -> bf16(q * s + b) x 8 as an MFMA operand (pairs low element first). q * s is
-// exact in fp32 (4-bit by 8-bit mantissas), so the fused q * s + b has the one rounding of the reference's fp32
-// q * s + b, then one rounding to bf16.
-SS_DEV ss_u32x4 dequant8(uint32_t w, float sc, float bi) {
-  // The masks are opaque to the compiler, so each byte converts with one v_cvt_f32_ubyteN (folded into a
-  // bit-field extract they would cost two instructions).
-  const uint32_t lo = and_opaque(w, 0x0F0F0F0Fu), hi = and_opaque(w >> 4, 0x0F0F0F0Fu);
+SS_DEV ss_u32x4 dequant8(uint32_t w, float s9, float bi) {
+  const int lo = (int)and_opaque(w, 0x0F0F0F0Fu), hi = (int)and_opaque(w >> 4, 0x0F0F0F0Fu);  // n0 n2 n4 n6 / n1 n3 n5 n7
+  const auto e02 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, false), e46 = __builtin_amdgcn_cvt_pk_f32_fp8(lo, true);
+  const auto e13 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, false), e57 = __builtin_amdgcn_cvt_pk_f32_fp8(hi, true);
   ss_u32x4 r;
-  r.x = cvt_pk_bf16(__builtin_fmaf((float)(lo & 0xFFu), sc, bi), __builtin_fmaf((float)(hi & 0xFFu), sc, bi));
-  r.y = cvt_pk_bf16(__builtin_fmaf((float)((lo >> 8) & 0xFFu), sc, bi), __builtin_fmaf((float)((hi >> 8) & 0xFFu), sc, bi));
-  r.z = cvt_pk_bf16(__builtin_fmaf((float)((lo >> 16) & 0xFFu), sc, bi), __builtin_fmaf((float)((hi >> 16) & 0xFFu), sc, bi));
-  r.w = cvt_pk_bf16(__builtin_fmaf((float)(lo >> 24), sc, bi), __builtin_fmaf((float)(hi >> 24), sc, bi));
+  r.x = cvt_pk_bf16(__builtin_fmaf(e02[0], s9, bi), __builtin_fmaf(e13[0], s9, bi));
+  r.y = cvt_pk_bf16(__builtin_fmaf(e02[1], s9, bi), __builtin_fmaf(e13[1], s9, bi));
+  r.z = cvt_pk_bf16(__builtin_fmaf(e46[0], s9, bi), __builtin_fmaf(e57[0], s9, bi));
+  r.w = cvt_pk_bf16(__builtin_fmaf(e46[1], s9, bi), __builtin_fmaf(e57[1], s9, bi));
   return r;
 }
 
@@ -309,7 +312,7 @@ SS_DEV void gemm_loop(uint8_t* lds, const uint32_t* sbt, int nsteps, int aoff0, 
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t sb = sbt[sb_lane + 16 * j * sb_stride + k];
-      sc[j] = __uint_as_float(sb << 16);
+      sc[j] = __uint_as_float(sb << 16) * 512.f;  // s * 2^9, exact
       bi[j] = __uint_as_float(sb & 0xFFFF0000u);
     }
 #pragma unroll
