@@ -60,37 +60,41 @@ __global__ __launch_bounds__(kAlignChunk) void align_count_kernel(const int32_t*
   for (int e = tid; e < nl; e += kAlignChunk) chunk_cnt[(int64_t)blockIdx.x * nl + e] = sm_cnt[e];
 }
 
-// One workgroup: exclusive chunk offsets per key (sequential over chunks), padded expert ranges, block experts,
-// the sentinel padding and num_padded.
-__global__ __launch_bounds__(1024) void align_scan_kernel(int64_t R, int nl, int bm, int nch, int64_t P,
-                                                          int32_t* __restrict__ chunk_cnt, int32_t* __restrict__ pad,
-                                                          int32_t* __restrict__ sorted_rows,
-                                                          int32_t* __restrict__ block_expert,
-                                                          int32_t* __restrict__ num_padded) {
-  extern __shared__ int sm[];  // pad_start [nl + 1], total [nl]
-  int* ps = sm;
-  int* tot = sm + nl + 1;
-  const int tid = threadIdx.x;
-  for (int e = tid; e < nl; e += 1024) {
-    // Sequential per key; the loads of 16 chunks are issued before their stores so the scan is not one memory
-    // round trip per chunk.
-    int run = 0;
-    for (int c0 = 0; c0 < nch; c0 += 16) {
-      int v[16];
+__global__ void align_zero_kernel(int nl, int32_t* __restrict__ tot) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e < nl) tot[e] = 0;
+}
+
+// Per key: exclusive offsets of the key's rows in each chunk (chunk order) and the key's total. One thread per key;
+// its nch loads are independent, so they are all in flight at once.
+__global__ __launch_bounds__(256) void align_keyscan_kernel(int nl, int nch, int32_t* __restrict__ chunk_cnt,
+                                                            int32_t* __restrict__ tot) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= nl) return;
+  int run = 0;
+  for (int c0 = 0; c0 < nch; c0 += 32) {
+    int v[32];
 #pragma unroll
-      for (int q = 0; q < 16; ++q) v[q] = c0 + q < nch ? chunk_cnt[(int64_t)(c0 + q) * nl + e] : 0;
+    for (int q = 0; q < 32; ++q) v[q] = c0 + q < nch ? chunk_cnt[(int64_t)(c0 + q) * nl + e] : 0;
 #pragma unroll
-      for (int q = 0; q < 16; ++q) {
-        if (c0 + q < nch) chunk_cnt[(int64_t)(c0 + q) * nl + e] = run;
-        run += v[q];
-      }
+    for (int q = 0; q < 32; ++q) {
+      if (c0 + q < nch) chunk_cnt[(int64_t)(c0 + q) * nl + e] = run;
+      run += v[q];
     }
-    tot[e] = run;
   }
-  __syncthreads();
-  // Exclusive scan of the padded expert sizes: each thread sums up to 4 consecutive experts, a Hillis-Steele scan
-  // over the 1024 thread totals, then the per-thread prefixes (nl <= 4096).
+  tot[e] = run;
+}
+
+// One workgroup: exclusive scan of the padded key sizes -> pad[0 .. nl] (pad[nl] = num_padded), and the expert of
+// every block of bm positions (-1 past num_padded).
+__global__ __launch_bounds__(1024) void align_padscan_kernel(int nl, int bm, int64_t nb, const int32_t* __restrict__ tot,
+                                                             int32_t* __restrict__ pad, int32_t* __restrict__ block_expert,
+                                                             int32_t* __restrict__ num_padded) {
+  extern __shared__ int ps[];  // [nl + 1]
   __shared__ int part[1024];
+  const int tid = threadIdx.x;
+  // Each thread sums up to 4 consecutive keys, a Hillis-Steele scan over the 1024 thread totals, then the per-thread
+  // prefixes (nl <= 4096).
   int loc[4], sum = 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
@@ -119,23 +123,28 @@ __global__ __launch_bounds__(1024) void align_scan_kernel(int64_t R, int nl, int
   }
   __syncthreads();
   for (int e = tid; e <= nl; e += 1024) pad[e] = ps[e];
-  const int64_t nb = P / bm;
   for (int64_t q = tid; q < nb; q += 1024) {
     const int64_t pos = q * bm;
-    // expert whose padded range holds pos: the last e with ps[e] <= pos (binary search), -1 past the end
+    // the last key e with ps[e] <= pos (binary search), -1 past the end
     int lo = 0, hi = nl;
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
       if (ps[mid] <= pos) lo = mid;
       else hi = mid - 1;
     }
-    const int e = pos < ps[nl] ? lo : -1;
-    block_expert[q] = e;
-    for (int m = 0; m < bm; ++m) {
-      const int64_t p = pos + m;
-      if (e < 0 || p - ps[e] >= tot[e]) sorted_rows[p] = (int32_t)R;
-    }
+    block_expert[q] = pos < ps[nl] ? lo : -1;
   }
+}
+
+// Sentinel R at every position that holds no row: past a key's rows inside its padded range, and past num_padded.
+__global__ __launch_bounds__(256) void align_fill_kernel(int64_t R, int nl, int bm, int64_t P,
+                                                         const int32_t* __restrict__ pad, const int32_t* __restrict__ tot,
+                                                         const int32_t* __restrict__ block_expert,
+                                                         int32_t* __restrict__ sorted_rows) {
+  const int64_t p = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (p >= P) return;
+  const int e = block_expert[p / bm];
+  if (e < 0 || p - pad[e] >= tot[e]) sorted_rows[p] = (int32_t)R;
 }
 
 __global__ __launch_bounds__(kAlignChunk) void align_scatter_kernel(const int32_t* __restrict__ le, int64_t R, int nl,
@@ -153,12 +162,21 @@ hipError_t launch_moe_align(const AlignArgs& a, hipStream_t st) {
   int32_t* rank = a.scratch;
   int32_t* chunk = rank + a.R;
   int32_t* pad = chunk + (int64_t)nch * a.num_local;
+  int32_t* tot = pad + a.num_local + 1;
   const int64_t P = padded_rows(a.R, a.num_local, a.block_m);
-  if (nch > 0)
+  if (nch > 0) {
     hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(kAlignChunk), (size_t)a.num_local * 4, st, a.local_expert,
                        a.R, a.num_local, rank, chunk);
-  hipLaunchKernelGGL(align_scan_kernel, dim3(1), dim3(1024), (size_t)(2 * a.num_local + 1) * 4, st, a.R, a.num_local,
-                     a.block_m, nch, P, chunk, pad, a.sorted_rows, a.block_expert, a.num_padded);
+    hipLaunchKernelGGL(align_keyscan_kernel, dim3((a.num_local + 255) / 256), dim3(256), 0, st, a.num_local, nch,
+                       chunk, tot);
+  } else {
+    hipLaunchKernelGGL(align_zero_kernel, dim3((a.num_local + 255) / 256), dim3(256), 0, st, a.num_local, tot);
+  }
+  hipLaunchKernelGGL(align_padscan_kernel, dim3(1), dim3(1024), (size_t)(a.num_local + 1) * 4, st, a.num_local,
+                     a.block_m, P / a.block_m, tot, pad, a.block_expert, a.num_padded);
+  if (P > 0)
+    hipLaunchKernelGGL(align_fill_kernel, dim3((unsigned)((P + 255) / 256)), dim3(256), 0, st, a.R, a.num_local,
+                       a.block_m, P, pad, tot, a.block_expert, a.sorted_rows);
   if (nch > 0)
     hipLaunchKernelGGL(align_scatter_kernel, dim3(nch), dim3(kAlignChunk), 0, st, a.local_expert, a.R, a.num_local,
                        rank, chunk, pad, a.sorted_rows);

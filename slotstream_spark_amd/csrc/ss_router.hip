@@ -143,8 +143,95 @@ __global__ __launch_bounds__(64) void router_topk_kernel(const uint16_t* __restr
   }
 }
 
+// The same router tail with the scores in registers: one wave per token (four per block), lane l holding entries
+// l + 64 i (E <= 64 NV). The operations and their order are those of router_topk_kernel: max, exp(s - m) summed per
+// lane in i order then by the butterfly, one division per entry; each top-k round takes the largest
+// (key + 1) over the untaken entries and, among lanes holding it, the lowest index; the weights divide by the
+// rank-order sum of the selected probabilities.
+template <int NV>
+__global__ __launch_bounds__(256) void router_topk_reg_kernel(const uint16_t* __restrict__ logits,
+                                                              const float* __restrict__ bias, float* __restrict__ probs,
+                                                              int32_t* __restrict__ ids, float* __restrict__ weights,
+                                                              int T, int E, int K) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= T) return;
+  const uint16_t* lg = logits + (size_t)t * E;
+  float v[NV];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = lane + 64 * i;
+    float sc = ss_bf16_to_f32(lg[e < E ? e : 0]);
+    if (bias) sc = sc + bias[e < E ? e : 0];
+    v[i] = sc;
+  }
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < NV; ++i) m = lane + 64 * i < E ? fmaxf(m, v[i]) : m;
+  m = ss_wave_max(m);
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    v[i] = ss_expf(v[i] - m);
+    acc = acc + (lane + 64 * i < E ? v[i] : 0.f);
+  }
+  const float z = ss_wave_sum(acc);
+  uint32_t kp[NV];  // key + 1 of a present, untaken entry; 0 once taken or absent
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = v[i] / z;
+    kp[i] = e < E ? ss_key(v[i]) + 1u : 0u;
+    if (probs && e < E) probs[(size_t)t * E + e] = v[i];
+  }
+  float mine = 0.f, sum = 0.f;
+  int my_id = 0;
+#pragma unroll 1
+  for (int r = 0; r < K; ++r) {
+    uint32_t lm = kp[0];
+#pragma unroll
+    for (int i = 1; i < NV; ++i) lm = kp[i] > lm ? kp[i] : lm;
+    const uint32_t mx = ss_wave_max_u32(lm);
+    int li = NV;
+#pragma unroll
+    for (int i = NV - 1; i >= 0; --i) li = kp[i] == mx ? i : li;
+    const uint32_t code = (uint32_t)(li * 64 + lane);  // the entry index where this lane holds mx
+    const uint64_t holders = __ballot(li < NV);
+    uint32_t best;
+    if (__popcll(holders) == 1)
+      best = (uint32_t)__builtin_amdgcn_readlane((int)code, (int)__builtin_ctzll(holders));
+    else
+      best = ss_wave_min_u32(code);
+    const int bi = __builtin_amdgcn_readfirstlane((int)best);
+    const int wl = bi & 63, wi = bi >> 6;
+    float pl = v[0];
+#pragma unroll
+    for (int i = 1; i < NV; ++i) pl = i == wi ? v[i] : pl;
+    const float pv = ss_readlane_f(pl, wl);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) kp[i] = (lane == wl && i == wi) ? 0u : kp[i];
+    sum = sum + pv;
+    mine = lane == r ? pv : mine;
+    my_id = lane == r ? bi : my_id;
+  }
+  if (lane < K) {
+    ids[(size_t)t * K + lane] = my_id;
+    weights[(size_t)t * K + lane] = mine / sum;
+  }
+}
+
 hipError_t launch_router_topk(const uint16_t* logits, const float* bias, float* probs, int32_t* ids, float* weights,
                               int T, int E, int K, hipStream_t st) {
+  if (E <= 512 && K <= 64) {
+    const dim3 grid((unsigned)((T + 3) / 4));
+    if (E <= 128)
+      hipLaunchKernelGGL(router_topk_reg_kernel<2>, grid, dim3(256), 0, st, logits, bias, probs, ids, weights, T, E, K);
+    else if (E <= 256)
+      hipLaunchKernelGGL(router_topk_reg_kernel<4>, grid, dim3(256), 0, st, logits, bias, probs, ids, weights, T, E, K);
+    else
+      hipLaunchKernelGGL(router_topk_reg_kernel<8>, grid, dim3(256), 0, st, logits, bias, probs, ids, weights, T, E, K);
+    return hipGetLastError();
+  }
   const size_t lds = (size_t)E * 4 + (size_t)E;
   hipLaunchKernelGGL(router_topk_kernel, dim3(T), dim3(64), lds, st, logits, bias, probs, ids, weights, E, K);
   return hipGetLastError();
