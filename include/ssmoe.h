@@ -160,6 +160,20 @@ int ssmoe_moe_prefill(const uint16_t* x, const int32_t* expert_ids, const float*
                       int64_t workspace_bytes, uint16_t* h_buf, float* out_rows, float* out, int64_t T, int H, int I,
                       int K, int E, void* stream);
 
+/* ---------------------------------------------------------------- shared expert (prefill) */
+
+/* hs[t, i] = bf16(bf16(silu(g)) * u), g = proj[t, i], u = proj[t, Is + i], and sgl[t] = proj[t, 2 Is]: the F.silu and
+ * bf16 product of the shared expert (model/layers.py:398-402, reference_torch.py:132-133) applied to one bf16
+ * projection [T, ld] that holds the shared gate, up and shared_expert_gate outputs side by side.
+ * hs bf16 [T, Is]; sgl bf16 [T]. */
+int ssmoe_shared_hs(const uint16_t* proj, int64_t ld, int T, int Is, uint16_t* hs, uint16_t* sgl, void* stream);
+
+/* y = bf16(bf16(routed) + bf16(bf16(sigmoid(sgl)) * sh)): routed.to(bf16) + sigmoid(x w_sg) * sh with the reference's
+ * bf16 rounding of each op (model/layers.py:398-402, reference_torch.py:132-134). routed fp32 [T, H] (16-byte
+ * aligned); sh bf16 [T, H]; sgl bf16 [T]; y bf16 [T, H]; H % 4 == 0. */
+int ssmoe_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* sgl, uint16_t* y, int T, int H,
+                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -163,6 +163,15 @@ def shared_expert(x_bits, gate_bits, up_bits, down_bits, sg_bits):
     return sh, sgl
 
 
+def shared_hs(g_bits, u_bits) -> np.ndarray:
+    """hs = bf16(bf16(silu(g)) * u) elementwise on bf16 bits (the shared expert's F.silu and product)."""
+    g = _c(g_bits, np.uint16)
+    u = _c(u_bits, np.uint16)
+    hs = np.empty_like(g)
+    lib().or_shared_hs(_p(g), _p(u), _p(hs), g.size)
+    return hs
+
+
 def combine_shared(routed, sh_bits, sgl_bits) -> np.ndarray:
     r = _c(routed, np.float32)
     sh = _c(sh_bits, np.uint16)

@@ -41,6 +41,8 @@ SIGNATURES = {
     "ssmoe_combine_rank_order": (_I, [_P, _I, _I, _I, _P, _P]),
     "ssmoe_moe_prefill_workspace_bytes": (_I64, [_I64, _I, _I]),
     "ssmoe_moe_prefill": (_I, [_P, _P, _P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I, _I, _I, _I, _P]),
+    "ssmoe_shared_hs": (_I, [_P, _I64, _I, _I, _P, _P, _P]),
+    "ssmoe_combine_shared": (_I, [_P, _P, _P, _P, _I, _I, _P]),
 }
 
 _lib = None

@@ -23,6 +23,14 @@ hipError_t launch_dense_rows(const uint16_t* x, int T, int H, const DenseSeg* se
 hipError_t launch_router_topk(const uint16_t* logits, const float* bias, float* probs, int32_t* ids, float* weights,
                               int T, int E, int K, hipStream_t st);
 
+// Shared-expert elementwise chain (ss_router.hip): hs = bf16(bf16(silu(g)) * u) and the shared_expert_gate logit from
+// one [T, ld] bf16 projection (g at columns [0, Is), u at [Is, 2 Is), the gate logit at 2 Is); and
+// y = bf16(bf16(routed) + bf16(bf16(sigmoid(sgl)) * sh)).
+hipError_t launch_shared_hs(const uint16_t* proj, int64_t ld, int T, int Is, uint16_t* hs, uint16_t* sgl,
+                            hipStream_t st);
+hipError_t launch_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* sgl, uint16_t* y, int T,
+                                 int H, hipStream_t st);
+
 // topk_stable over fp32 rows (kernels/topk_stable.py:85-113 semantics).
 hipError_t launch_topk_stable(const float* scores, const int32_t* n_valid, int32_t* idx, float* val, int R, int N,
                               int k, hipStream_t st);

@@ -399,4 +399,62 @@ hipError_t launch_topk_stable(const float* scores, const int32_t* n_valid, int32
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- shared expert elementwise chain
+// hs[t, i] = bf16(bf16(silu(g)) * u) with g = proj[t, i], u = proj[t, Is + i] (bf16), and sgl[t] = proj[t, 2 Is]:
+// the rounding of F.silu and of the bf16 product in the reference's shared expert (model/layers.py:398-402,
+// reference_torch.py:132-133), whose gate, up and shared_expert_gate projections arrive as one bf16 GEMM output
+// with row stride ld.
+__global__ __launch_bounds__(256) void shared_hs_kernel(const uint16_t* __restrict__ proj, int64_t ld, int T, int Is,
+                                                        uint16_t* __restrict__ hs, uint16_t* __restrict__ sgl) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)T * Is) return;
+  const int64_t t = idx / Is, i = idx - t * Is;
+  const uint16_t* row = proj + t * ld;
+  const float gv = ss_bf16_to_f32(row[i]), uv = ss_bf16_to_f32(row[Is + i]);
+  const float sv = ss_round_bf16(gv / (1.f + ss_expf(-gv)));
+  hs[idx] = (uint16_t)ss_f32_to_bf16(sv * uv);
+  if (i == 0) sgl[t] = row[2 * Is];
+}
+
+hipError_t launch_shared_hs(const uint16_t* proj, int64_t ld, int T, int Is, uint16_t* hs, uint16_t* sgl,
+                            hipStream_t st) {
+  const int64_t n = (int64_t)T * Is;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(shared_hs_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, proj, ld, T, Is, hs, sgl);
+  return hipGetLastError();
+}
+
+// y = bf16(bf16(routed) + bf16(bf16(sigmoid(sgl)) * sh)): routed.to(bf16) + sigmoid(x w_sg) * sh with the reference's
+// bf16 rounding of each op (model/layers.py:398-402). Four elements per thread.
+__global__ __launch_bounds__(256) void combine_shared_kernel(const float* __restrict__ routed,
+                                                             const uint16_t* __restrict__ sh,
+                                                             const uint16_t* __restrict__ sgl, uint16_t* __restrict__ y,
+                                                             int T, int H) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int h4 = H >> 2;
+  if (idx >= (int64_t)T * h4) return;
+  const int64_t t = idx / h4;
+  const float sg = ss_round_bf16(1.f / (1.f + ss_expf(-ss_bf16_to_f32(sgl[t]))));
+  const float4 r = reinterpret_cast<const float4*>(routed)[idx];
+  const uint2 s2 = reinterpret_cast<const uint2*>(sh)[idx];
+  const float rv[4] = {r.x, r.y, r.z, r.w};
+  const uint32_t sv[4] = {s2.x & 0xFFFFu, s2.x >> 16, s2.y & 0xFFFFu, s2.y >> 16};
+  uint32_t o[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float sh2 = ss_round_bf16(sg * ss_bf16_to_f32(sv[c]));
+    o[c] = ss_f32_to_bf16(ss_round_bf16(rv[c]) + sh2);
+  }
+  reinterpret_cast<uint2*>(y)[idx] = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+}
+
+hipError_t launch_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* sgl, uint16_t* y, int T,
+                                 int H, hipStream_t st) {
+  const int64_t n = (int64_t)T * (H / 4);
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(combine_shared_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, routed, sh, sgl, y, T,
+                     H);
+  return hipGetLastError();
+}
+
 }  // namespace ss

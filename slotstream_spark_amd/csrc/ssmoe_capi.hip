@@ -520,4 +520,23 @@ int ssmoe_moe_prefill(const uint16_t* x, const int32_t* expert_ids, const float*
   return hip_check(ss::launch_combine(out_rows, local, (int)T, K, H, out, st), "combine launch");
 }
 
+// ---------------------------------------------------------------- shared expert (prefill)
+int ssmoe_shared_hs(const uint16_t* proj, int64_t ld, int T, int Is, uint16_t* hs, uint16_t* sgl, void* stream) {
+  if (T < 0 || Is < 1 || ld < 2 * (int64_t)Is + 1)
+    return fail(SSMOE_EINVAL, "need T >= 0, Is >= 1, ld >= 2 Is + 1 (T=%d Is=%d ld=%lld)", T, Is, (long long)ld);
+  if (T > 0 && (!proj || !hs || !sgl)) return fail(SSMOE_EINVAL, "proj, hs and sgl must be non-null");
+  return hip_check(ss::launch_shared_hs(proj, ld, T, Is, hs, sgl, static_cast<hipStream_t>(stream)),
+                   "shared_hs launch");
+}
+
+int ssmoe_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* sgl, uint16_t* y, int T, int H,
+                         void* stream) {
+  if (T < 0 || H < 4 || H % 4) return fail(SSMOE_EINVAL, "need T >= 0 and H a positive multiple of 4");
+  if (T > 0 && (!routed || !sh || !sgl || !y)) return fail(SSMOE_EINVAL, "every pointer must be non-null");
+  if (!aligned(routed, 16) || !aligned(sh, 8) || !aligned(y, 8))
+    return fail(SSMOE_EINVAL, "routed must be 16-byte aligned, sh and y 8-byte aligned");
+  return hip_check(ss::launch_combine_shared(routed, sh, sgl, y, T, H, static_cast<hipStream_t>(stream)),
+                   "combine_shared launch");
+}
+
 }  // extern "C"

@@ -4,8 +4,10 @@ Mirrors SweepMoE.layer (slotstream_spark/model/moe_sweep.py:80-160) plus the rou
 (model/layers.py:336-348, 398-402): router logits lin(x, W_gate) as a bf16 GEMM, softmax / stable top-k /
 renormalisation on the device (ssmoe_router_topk), the routed experts as one plan over all E experts
 (ssmoe_moe_prefill: moe_align, grouped gate/up, down, rank-order combine), and y = bf16(routed) + shared.
-The dense projections (router, shared expert) are plain bf16 GEMMs and run on the platform BLAS through torch;
-the routed experts, the routing and the combine run in libssmoe.
+The dense projections are plain bf16 GEMMs on the platform BLAS through torch: the router, one GEMM for the shared
+expert's gate, up and shared_expert_gate rows together (their weights concatenated once at construction), and the
+shared down projection. The routed experts, the routing, the shared expert's elementwise chain (ssmoe_shared_hs) and
+the final y (ssmoe_combine_shared) run in libssmoe, with the reference's bf16 rounding of every op.
 """
 from __future__ import annotations
 
@@ -30,6 +32,11 @@ class MoEPrefillLayer:
             if t.dtype != torch.bfloat16 or not t.is_contiguous():
                 raise ValueError("router and shared-expert weights must be contiguous bf16")
         self.max_tokens = max_tokens
+        self.shared_inter = sh_gate.shape[0]
+        # shared gate, up and shared_expert_gate rows in one weight [2 Is + 1 (padded to 8), H]
+        n_sh = 2 * self.shared_inter + 1
+        pad = (-n_sh) % 8
+        self.sh_cat = torch.cat([sh_gate, sh_up, sh_g] + ([sh_g.new_zeros((pad, self.hidden))] if pad else [])).contiguous()
         dev, R = pool.device, max_tokens * top_k
         L = _lib.lib()
         nb = L.ssmoe_moe_prefill_workspace_bytes(max_tokens, top_k, self.experts)
@@ -58,16 +65,28 @@ class MoEPrefillLayer:
             self.inter, self.top_k, self.experts, _lib.stream_of(x)))
         return out
 
-    def shared(self, x: torch.Tensor) -> torch.Tensor:
-        sh = F.linear(F.silu(F.linear(x, self.sh_gate)) * F.linear(x, self.sh_up), self.sh_down)
-        return torch.sigmoid(F.linear(x, self.sh_g)) * sh
+    def shared(self, x: torch.Tensor):
+        """(sh bf16 [T, H] = F.linear(bf16(silu(g)) * u, sh_down), shared_expert_gate logits bf16 [T])."""
+        t = x.shape[0]
+        proj = F.linear(x, self.sh_cat)
+        hs = torch.empty((t, self.shared_inter), dtype=torch.bfloat16, device=x.device)
+        sgl = torch.empty((t,), dtype=torch.bfloat16, device=x.device)
+        _lib.check(_lib.lib().ssmoe_shared_hs(proj.data_ptr(), proj.shape[1], t, self.shared_inter, hs.data_ptr(),
+                                              sgl.data_ptr(), _lib.stream_of(x)))
+        return F.linear(hs, self.sh_down), sgl
 
     def __call__(self, x: torch.Tensor):
-        """x bf16 [T, H] -> (y bf16 [T, H], ids int32 [T, K], weights fp32 [T, K], routed fp32 [T, H])."""
+        """x bf16 [T, H] -> (y bf16 [T, H], ids int32 [T, K], weights fp32 [T, K], routed fp32 [T, H]);
+        y = routed.to(bf16) + sigmoid(x w_sg) * shared(x), each op rounded to bf16 as in the reference."""
         if x.dtype != torch.bfloat16 or x.dim() != 2 or x.shape[1] != self.hidden or not x.is_contiguous():
             raise ValueError(f"x must be a contiguous bf16 [T, {self.hidden}] tensor")
         if x.shape[0] > self.max_tokens:
             raise ValueError(f"at most {self.max_tokens} tokens per call, got {x.shape[0]}")
+        t = x.shape[0]
         ids, w = self.route(x)
         routed = self.routed_experts(x, ids, w)
-        return routed.to(torch.bfloat16) + self.shared(x), ids, w, routed
+        sh, sgl = self.shared(x)
+        y = torch.empty((t, self.hidden), dtype=torch.bfloat16, device=x.device)
+        _lib.check(_lib.lib().ssmoe_combine_shared(routed.data_ptr(), sh.data_ptr(), sgl.data_ptr(), y.data_ptr(), t,
+                                                   self.hidden, _lib.stream_of(x)))
+        return y, ids, w, routed

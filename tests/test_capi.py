@@ -151,3 +151,16 @@ def test_topk_value_errors():
         topk_stable(torch.zeros(2, 8), 9)
     with pytest.raises(ValueError, match="GPU"):
         topk_stable(torch.zeros(2, 8), 2)
+
+
+def test_shared_entry_points_reject_bad_arguments(L):
+    p = ctypes.c_void_p(4096)
+    assert L.ssmoe_shared_hs(p, 16, 4, 8, p, p, None) == EINVAL  # ld < 2 Is + 1
+    assert b"ld >= 2 Is + 1" in L.ssmoe_last_error()
+    assert L.ssmoe_shared_hs(None, 17, 4, 8, p, p, None) == EINVAL
+    assert L.ssmoe_shared_hs(None, 17, 0, 8, None, None, None) == 0  # nothing to do
+    assert L.ssmoe_combine_shared(p, p, p, p, 2, 6, None) == EINVAL  # H % 4
+    assert L.ssmoe_combine_shared(ctypes.c_void_p(4100), p, p, p, 2, 8, None) == EINVAL  # routed alignment
+    assert b"16-byte aligned" in L.ssmoe_last_error()
+    assert L.ssmoe_combine_shared(None, None, None, None, 0, 8, None) == 0
+

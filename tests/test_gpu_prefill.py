@@ -167,4 +167,37 @@ def test_prefill_layer_end_to_end():
     assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
     _, rows_ref = _oracle_rows(pool, x, ids, w)
     assert O.rel_l2(routed.cpu().numpy(), O.combine_rank_order(rows_ref, T, K)) < 2e-3
+    # the shared expert's elementwise chain and y, bit for bit, from the GEMMs' own bf16 outputs
+    proj = torch.nn.functional.linear(x, layer.sh_cat)
+    Is = lw.sh_gate.shape[0]
+    pb = bits(proj)
+    hs_ref = O.shared_hs(pb[:, :Is], pb[:, Is:2 * Is])
+    sh = torch.nn.functional.linear(torch.from_numpy(hs_ref.view(np.int16)).view(torch.bfloat16).cuda(), lw.sh_down)
+    y_ref = O.combine_shared(routed.cpu().numpy(), bits(sh), pb[:, 2 * Is].copy())
+    assert np.array_equal(bits(y), y_ref)
     assert torch.isfinite(y.float()).all()
+
+
+@pytest.mark.parametrize("T,Is,ld", [(1, 8, 17), (37, 512, 1032), (300, 640, 1288)])
+def test_shared_hs_bitwise(T, Is, ld):
+    g = torch.Generator(device="cuda").manual_seed(T)
+    proj = (torch.randn((T, ld), generator=g, device="cuda") * 4).to(torch.bfloat16)
+    hs = torch.empty((T, Is), dtype=torch.bfloat16, device="cuda")
+    sgl = torch.empty((T,), dtype=torch.bfloat16, device="cuda")
+    _lib.check(_lib.lib().ssmoe_shared_hs(proj.data_ptr(), ld, T, Is, hs.data_ptr(), sgl.data_ptr(), 0))
+    torch.cuda.synchronize()
+    pb = bits(proj)
+    assert np.array_equal(bits(hs), O.shared_hs(pb[:, :Is], pb[:, Is:2 * Is]))
+    assert np.array_equal(bits(sgl), pb[:, 2 * Is])
+
+
+@pytest.mark.parametrize("T,H", [(1, 4), (33, 2048), (129, 2560)])
+def test_combine_shared_bitwise(T, H):
+    g = torch.Generator(device="cuda").manual_seed(H + T)
+    routed = torch.randn((T, H), generator=g, device="cuda") * 3
+    sh = (torch.randn((T, H), generator=g, device="cuda")).to(torch.bfloat16)
+    sgl = (torch.randn((T,), generator=g, device="cuda") * 5).to(torch.bfloat16)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device="cuda")
+    _lib.check(_lib.lib().ssmoe_combine_shared(routed.data_ptr(), sh.data_ptr(), sgl.data_ptr(), y.data_ptr(), T, H, 0))
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(y), O.combine_shared(routed.cpu().numpy(), bits(sh), bits(sgl)))
