@@ -78,8 +78,11 @@ size_t verify_scratch_bytes(int T, int H, int I, int Is, int K, int E) {
   return vlayout(T, I, Is, K, E).total;
 }
 
-// Dynamic LDS layout (bytes): x fragments, staged h fragments (also the router-tail scores), down-weight prefetch
-// slots (P experts), per-expert partial dots.
+// Dynamic LDS layout (bytes): per-expert partial dots, staged h fragments, then one region that holds the x
+// fragments while phases A-C run and the down-weight prefetch slots afterwards (a workgroup issues its prefetch only
+// once its own gate/up items are done, the last use of x).
+// Prefetch slot (one expert, the workgroup's 16 down rows): [NJD][64 lanes] 16-byte weight words, then the scale
+// dwords [16 rows][NJD] and the bias dwords [16 rows][NJD] (dword j of a row holds groups 2j, 2j + 1).
 struct DLayout {
   size_t xfrag, hfrag, pref, part, total;
   int P;           // experts whose down weights are prefetched per batch
@@ -87,30 +90,30 @@ struct DLayout {
   size_t slot;     // bytes per prefetch slot
 };
 
-// Fits the budget for every supported shape: x fragments (<= 64 KB) + partial dots (<= 16 KB) + router scores
-// (<= 8 KB) + one prefetch slot (<= 12 KB); the h fragments are staged only when they fit beside one slot.
+static __host__ __device__ inline size_t dslot_bytes(int I) { return (size_t)(I / 128) * (1024 + 2 * 16 * 4); }
+
 static __host__ __device__ inline DLayout dlayout(int T, int H, int I, int K, int E, int x_f32, int verify) {
+  (void)verify;
   DLayout d;
   const int nq = T * K;
   const int nu_max = nq < E ? nq : E;
+  const size_t xf = (size_t)(H / 128) * 4 * 4 * kTBv * (x_f32 ? 2 : 1) * 16;
+  d.slot = dslot_bytes(I);
   size_t o = 0;
-  d.xfrag = o;
-  o += (size_t)(H / 128) * 4 * 4 * kTBv * (x_f32 ? 2 : 1) * 16;
   d.part = o;
   o += (size_t)nu_max * 16 * kTBv * 4;
-  d.slot = (size_t)(I / 128) * 64 * (16 + 4 + 4);
   d.hfrag = o;
   const size_t hf = (size_t)nq * I * 4;
-  const size_t sc = verify ? (size_t)T * E * 4 : 0;
-  d.stage_h = o + (hf > sc ? hf : sc) + d.slot <= kLdsBudget;
-  o += d.stage_h ? (hf > sc ? hf : sc) : sc;
-  d.pref = o;
+  const size_t tail = xf > d.slot ? xf : d.slot;  // the shared region holds x, or at least one slot
+  d.stage_h = o + hf + tail <= kLdsBudget;
+  if (d.stage_h) o += hf;
+  d.pref = d.xfrag = o;
   const long room = (long)kLdsBudget - (long)o;
   int P = room > 0 ? (int)(room / (long)d.slot) : 0;
   if (P > nu_max) P = nu_max;
   d.P = P;
-  o += (size_t)P * d.slot;
-  d.total = o;
+  const size_t pb = (size_t)P * d.slot;
+  d.total = o + (pb > xf ? pb : xf);
   return d;
 }
 
@@ -697,10 +700,16 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   auto issue_down = [&](int u, int slotp) {
     uint8_t* sl = prefl + (size_t)slotp * D.slot;
     const uint8_t* base = s.base[u];
-    for (int j = 0; j < NJD; ++j) {
-      dma16(base + rec.dw + drow * drow_b + 64 * j + 16 * g, sl + (size_t)j * 1024);
-      dma4(base + rec.ds + drow * dsb_b + 4 * j, sl + (size_t)NJD * 1024 + (size_t)j * 256);
-      dma4(base + rec.db + drow * dsb_b + 4 * j, sl + (size_t)NJD * 1280 + (size_t)j * 256);
+    for (int j = 0; j < NJD; ++j) dma16(base + rec.dw + drow * drow_b + 64 * j + 16 * g, sl + (size_t)j * 1024);
+    // scale and bias dwords: entry idx = row * NJD + j of the 16 rows (NJD dwords each)
+    for (int k0 = 0; k0 < 16 * NJD; k0 += 64) {
+      const int idx = k0 + lane;
+      if (idx < 16 * NJD) {
+        const int row = idx / NJD, jj = idx - row * NJD;
+        const int64_t ro = (int64_t)(16 * bid + row) * dsb_b + 4 * jj;
+        dma4(base + rec.ds + ro, sl + (size_t)NJD * 1024 + (size_t)k0 * 4);
+        dma4(base + rec.db + ro, sl + (size_t)NJD * 1024 + (size_t)16 * NJD * 4 + (size_t)k0 * 4);
+      }
     }
   };
   SS_TRACE(5);
@@ -911,8 +920,8 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 #pragma unroll
         for (int j = 0; j < NJD; ++j) {
           wq[j] = reinterpret_cast<const uint4*>(sl + (size_t)j * 1024)[lane];
-          svw[j] = reinterpret_cast<const uint32_t*>(sl + (size_t)NJD * 1024 + (size_t)j * 256)[lane];
-          bvw[j] = reinterpret_cast<const uint32_t*>(sl + (size_t)NJD * 1280 + (size_t)j * 256)[lane];
+          svw[j] = reinterpret_cast<const uint32_t*>(sl + (size_t)NJD * 1024)[n * NJD + j];
+          bvw[j] = reinterpret_cast<const uint32_t*>(sl + (size_t)NJD * 1024 + (size_t)16 * NJD * 4)[n * NJD + j];
           const size_t fo = (((size_t)aq * NJD + j) * 4 + g) * 8 + apart * 4;
 #pragma unroll
           for (int i = 0; i < 4; ++i) av4[j][i] = STAGED ? hfl[fo + i] : ld_ag16(hfrag + fo + i);
