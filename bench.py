@@ -126,7 +126,7 @@ def prefill_leg(pool, weights, biases, nl, steps, warmup, dev):
     return {"tokens": TP, "layers": nl, "us_per_layer": round(us_layer, 2), "tflops": round(tflops, 2),
             "flop_per_layer": PREFILL_FLOP, "unique_experts_mean": sum(uniq) / nl,
             "padded_rows_mean": sum(padded) / nl,
-            "roofline": {"bound": "mfma", "kernel": "prefill_gate_up_kernel + prefill_down_kernel (grouped GEMM pair)",
+            "roofline": {"bound": "mfma", "kernel": "prefill_gemm_kernel<true> + prefill_gemm_kernel<false> (grouped gate/up + down GEMM pair)",
                          "achieved": round(g_tflops, 2), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                          "frac": round(g_tflops / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": traffic_of("prefill_gemm"),
                          "us_per_launch": round(us_g, 2), "flop_per_launch": PREFILL_ROUTED_FLOP,
