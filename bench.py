@@ -134,6 +134,140 @@ def prefill_leg(pool, weights, biases, nl, steps, warmup, dev):
                          "expert_stream_gbs": round(wbytes / (us_g * 1e-6) / 1e9, 1)}}
 
 
+def config2_leg(pool, lw, bias, steps, dev):
+    """an MTP chain of depth 3 (T=4 verify) through the config-1 layer, then acceptance over
+    vocab 151,936: greedy argmax-match and p/q at temperature 0.7, on 1000 seeded steps of synthetic fp32 logits
+    (target N(0,3), draft correlated rho=0.8; drafts = the draft rows' argmax; uniforms from the sampler's
+    splitmix64 stream seeded per step). Every step's logits, drafts and uniforms are resident in HBM before the
+    timed region; the steps are captured as HIP graphs (100 steps each) and replayed once, timed with HIP events."""
+    import numpy as np
+    import torch
+
+    from slotstream_spark_amd.engine.accept import Acceptor, AcceptResult, RoundStats, UniformStream
+    from slotstream_spark_amd.engine.verify import MoEVerifyLayer
+    from slotstream_spark_amd.memory.synth import normal_bf16, verify_logits
+
+    D, V, TEMP, T = 3, 151936, 0.7, 4
+    layer = MoEVerifyLayer(pool, 0, lw.router_w, lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_g, top_k=K,
+                           router_bias=bias, max_tokens=4)
+    x = normal_bf16((T, H), 1.0, 1734, dev)
+    y = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+    tgt = torch.empty((steps, D + 1, V), device=dev)
+    drf = torch.empty((steps, D, V), device=dev)
+    for st in range(steps):
+        tgt[st], drf[st] = verify_logits(D, V, 10_000 + st, device=dev)
+    drafts = drf.argmax(dim=2).to(torch.int32).contiguous()
+    uni = torch.from_numpy(np.stack([UniformStream(20_000 + st).peek(D + 1) for st in range(steps)])).to(dev)
+    acc = Acceptor(D, V, device=dev)
+    out_g = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
+    out_p = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
+    chunk = 100
+
+    def run(lo, hi, verify=True, greedy=True, pq=True):
+        for st in range(lo, hi):
+            if verify:
+                layer(x, y=y, ids=ids, weights=wts)
+            if greedy:
+                out_g[st].copy_(acc.greedy_async(tgt[st], drafts[st]))
+            if pq:
+                out_p[st].copy_(acc.pq_async(tgt[st], drf[st], drafts[st], uni[st], TEMP))
+
+    s_ = torch.cuda.Stream(device=dev)
+    res = {}
+    for name, kw in (("step", {}), ("verify", dict(greedy=False, pq=False)), ("greedy", dict(verify=False, pq=False)),
+                     ("pq", dict(verify=False, greedy=False))):
+        total = 0.0
+        for lo in range(0, steps, chunk):
+            total += timed_graph(lambda: run(lo, min(steps, lo + chunk), **kw), 1, 0, s_) * 1000.0
+        res[name] = total / steps
+    g = [AcceptResult.from_out(o) for o in out_g.cpu()]
+    q = [AcceptResult.from_out(o) for o in out_p.cpu()]
+    stats = {}
+    for name, rs in (("greedy", g), ("pq", q)):
+        st = RoundStats()
+        for r in rs:
+            st.add(D, r)
+        stats[name] = {"acceptance_length": round(st.acceptance_length, 4),
+                       "accepted_by_depth": st.accepted_by_depth, "attempts_by_depth": st.attempts_by_depth}
+    tok_s = stats["pq"]["acceptance_length"] / (res["step"] * 1e-6)
+    log(f"config2: step {res['step']:.1f} us (verify T=4 {res['verify']:.1f}, greedy {res['greedy']:.1f}, "
+        f"p/q {res['pq']:.1f}); acceptance length greedy {stats['greedy']['acceptance_length']}, "
+        f"p/q {stats['pq']['acceptance_length']}")
+    return {"steps": steps, "depth": D, "vocab": V, "temperature": TEMP,
+            "us_per_step": round(res["step"], 2), "us_verify_T4": round(res["verify"], 2),
+            "us_accept_greedy": round(res["greedy"], 2), "us_accept_pq": round(res["pq"], 2),
+            "tokens_per_s_pq": round(tok_s, 1), "greedy": stats["greedy"], "pq": stats["pq"],
+            "timing": "HIP graphs of 100 steps (verify layer + greedy + p/q per step), events on the graph stream"}
+
+
+def config4_leg(pool, weights, biases, steps, dev):
+    """a 48-layer routed-MoE stack (config-1 shape, all experts resident) run as an MTP loop of
+    `steps` decode steps at T=2: per step, the 48 verify layers chained (layer l reads layer l-1's y) in one HIP
+    graph, then greedy acceptance (D=1) on that step's synthetic fp32 logits (vocab 151,936, rho=0.8 draft).
+    Effective tokens/s = emitted tokens / wall time of the whole loop, attention excluded."""
+    import torch
+
+    from slotstream_spark_amd.engine.accept import Acceptor, AcceptResult, RoundStats
+    from slotstream_spark_amd.engine.verify import MoEVerifyLayer
+    from slotstream_spark_amd.memory.synth import normal_bf16, verify_logits
+
+    NL4, D, V, T = len(weights), 1, 151936, 2
+    layers = [MoEVerifyLayer(pool, l, w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, top_k=K, router_bias=b)
+              for l, (w, b) in enumerate(zip(weights, biases))]
+    xs = [normal_bf16((T, H), 1.0, 1735, dev)] + [torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+                                                  for _ in range(NL4)]
+    ids = torch.empty((T, K), dtype=torch.int32, device=dev)
+    wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+    tgt = torch.empty((steps, D + 1, V), device=dev)
+    drf = torch.empty((steps, D, V), device=dev)
+    for st in range(steps):
+        tgt[st], drf[st] = verify_logits(D, V, 30_000 + st, device=dev)
+    drafts = drf.argmax(dim=2).to(torch.int32).contiguous()
+    acc = Acceptor(D, V, device=dev)
+    out_g = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
+
+    def stack():
+        for l in range(NL4):
+            layers[l](xs[l], y=xs[l + 1], ids=ids, weights=wts)
+
+    s_ = torch.cuda.Stream(device=dev)
+    s_.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s_):
+        stack()
+    torch.cuda.current_stream().wait_stream(s_)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s_):
+        stack()
+    with torch.cuda.stream(s_):
+        for _ in range(2):
+            g.replay()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record(s_)
+        for st in range(steps):
+            g.replay()
+            out_g[st].copy_(acc.greedy_async(tgt[st], drafts[st]))
+        ev1.record(s_)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    rs = RoundStats()
+    for o in out_g.cpu():
+        rs.add(D, AcceptResult.from_out(o))
+    emitted = sum(rs.emitted_by_round)
+    tok_s = emitted / (ms * 1e-3)
+    log(f"config4: {NL4} layers x {steps} steps in {ms:.1f} ms ({ms * 1000 / steps:.1f} us/step, "
+        f"{ms * 1000 / steps / NL4:.2f} us/layer); {emitted} tokens emitted, {tok_s:.0f} tokens/s")
+    return {"layers": NL4, "steps": steps, "tokens": T, "ms_total": round(ms, 3),
+            "us_per_step": round(ms * 1000 / steps, 2), "us_per_layer": round(ms * 1000 / steps / NL4, 3),
+            "emitted_tokens": emitted, "acceptance_length": round(rs.acceptance_length, 4),
+            "effective_tokens_per_s": round(tok_s, 1),
+            "resident_expert_bytes": NL4 * E * 1_769_472,
+            "timing": "one HIP graph of the 48 chained layers per step + greedy acceptance launches, events around "
+                      "the whole loop"}
+
+
 def traffic_of(kernel: str):
     """HBM bytes per launch of `kernel` measured with rocprofv3 FETCH_SIZE + WRITE_SIZE (scaled by a known-size copy),
     as recorded in profiles/traffic.json next to the command that produced it; None when not measured."""
@@ -211,9 +345,12 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="verify,decode,prefill",
-                    help="comma list of timed legs: verify, decode, prefill")
+    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4",
+                    help="comma list of timed legs: verify, decode, prefill, config2, config4")
     ap.add_argument("--prefill-layers", type=int, default=4)
+    ap.add_argument("--config2-steps", type=int, default=1000)
+    ap.add_argument("--config4-layers", type=int, default=48)
+    ap.add_argument("--config4-steps", type=int, default=256)
     ap.add_argument("--copy-calib", action="store_true", help="run 3 x 256 MiB device copies first (PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -240,14 +377,15 @@ def main():
         del a, b
         log("copy calibration: 3 x 268435456-byte device copies done")
     NL, T = args.layers, args.tokens
-    log(f"allocating {NL} layers x {E} experts ({NL * E * 1_769_472 / 2**30:.1f} GiB of records)")
-    pool = SlotPool(NL, E, H, I, device=dev)
+    NP = max(NL, args.config4_layers if "config4" in legs else 0)
+    log(f"allocating {NP} layers x {E} experts ({NP * E * 1_769_472 / 2**30:.1f} GiB of records)")
+    pool = SlotPool(NP, E, H, I, device=dev)
     pool.fill_random(1729)
     pool.place_permuted(1732)
-    weights = [LayerWeights(H, E, IS, seed=1729 + l, device=dev) for l in range(NL)]
-    biases = [zipf_bias(E, 1.1, 1731 + l, device=dev) for l in range(NL)]
+    weights = [LayerWeights(H, E, IS, seed=1729 + l, device=dev) for l in range(NP)]
+    biases = [zipf_bias(E, 1.1, 1731 + l, device=dev) for l in range(NP)]
     layers = [MoEVerifyLayer(pool, l, w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, top_k=K,
-                             router_bias=b, max_tokens=max(T, 4)) for l, (w, b) in enumerate(zip(weights, biases))]
+                             router_bias=b, max_tokens=max(T, 4)) for l, (w, b) in enumerate(zip(weights[:NL], biases[:NL]))]
     x = normal_bf16((T, H), 1.0, 1730, dev)
     ys = [torch.empty((T, H), dtype=torch.bfloat16, device=dev) for _ in range(NL)]
     ids = [torch.empty((T, K), dtype=torch.int32, device=dev) for _ in range(NL)]
@@ -323,6 +461,12 @@ def main():
         prefill = prefill_leg(pool, weights, biases, min(args.prefill_layers, NL), max(args.steps // 5, 3),
                               max(args.warmup // 5, 1), dev)
 
+    c2 = c4 = None
+    if "config2" in legs:
+        c2 = config2_leg(pool, weights[0], biases[0], args.config2_steps, dev)
+    if "config4" in legs:
+        c4 = config4_leg(pool, weights[:args.config4_layers], biases[:args.config4_layers], args.config4_steps, dev)
+
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline")
@@ -355,6 +499,8 @@ def main():
         "moe_decode": None if us_moe is None else {
             "us_per_launch": round(us_moe, 3), "bytes_per_launch": int(moe_bytes), "achieved_gbs": round(moe_gbs, 1)},
         "prefill": prefill,
+        "config2": c2,
+        "config4": c4,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
