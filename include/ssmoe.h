@@ -95,7 +95,7 @@ int ssmoe_moe_verify_layer(const uint16_t* x, const uint16_t* router_w, const fl
                            int32_t* ids, float* weights, uint16_t* y, float* routed_out, int T, int H, int I, int Is,
                            int K, int E, void* stream);
 
-/* Bytes of the workspace the acceptance entry points need. */
+/* Bytes of the workspace the acceptance entry points need (1 <= V <= 1,048,576, 0 <= D <= 60). */
 int64_t ssmoe_accept_workspace_bytes(int D, int V);
 
 /* Greedy verify acceptance. Replaces the acceptance loop of _mtp_decode (engine/generate.py:208-229) with

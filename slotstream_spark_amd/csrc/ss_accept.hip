@@ -56,6 +56,49 @@ SS_DEV Work work_of(float* w, int rows, int nch) {
 
 SS_DEV bool finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
 
+// Wave-wide helpers over per-chunk arrays of n <= 64 * kMaxPerLane entries (called by all 64 lanes; every lane
+// returns the same value). Entry c is loaded by lane c % 64 into register c / 64, so all loads are in flight at
+// once; a sum that must keep its sequential order is then formed in index order from the lanes' registers.
+constexpr int kMaxPerLane = 16;  // V <= 16 * 64 * 1024 entries
+struct WaveVals {
+  float v[kMaxPerLane];
+};
+SS_DEV WaveVals wave_load(const float* arr, int n) {
+  WaveVals w;
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int k = 0; k < kMaxPerLane; ++k) {
+    const int c = lane + 64 * k;
+    w.v[k] = c < n ? arr[c] : 0.f;
+  }
+  return w;
+}
+// ((v[0] + v[1]) + ...) + v[n-1] from 0.f, fp32, in index order.
+SS_DEV float wave_seq_sum(const WaveVals& w, int n) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < kMaxPerLane; ++k) {
+    if (64 * k >= n) break;
+    const int m = n - 64 * k < 64 ? n - 64 * k : 64;
+    for (int l = 0; l < m; ++l) s = s + ss_readlane_f(w.v[k], l);
+  }
+  return s;
+}
+SS_DEV float wave_max_of(const WaveVals& w, int n) {
+  const int lane = threadIdx.x & 63;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int k = 0; k < kMaxPerLane; ++k) m = lane + 64 * k < n ? fmaxf(m, w.v[k]) : m;
+  return ss_wave_max(m);
+}
+SS_DEV bool wave_any_nonzero(const WaveVals& w, int n) {
+  const int lane = threadIdx.x & 63;
+  uint32_t b = 0;
+#pragma unroll
+  for (int k = 0; k < kMaxPerLane; ++k) b |= (lane + 64 * k < n && w.v[k] != 0.f) ? 1u : 0u;
+  return ss_wave_or(b) != 0u;
+}
+
 // ---------------------------------------------------------------- greedy
 __global__ __launch_bounds__(64) void greedy_chunk_kernel(const float* __restrict__ target, int V, float* work) {
   const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
@@ -91,20 +134,27 @@ __global__ __launch_bounds__(64) void greedy_finish_kernel(const int32_t* __rest
   Work k = work_of(work, D + 1, nch);
   __shared__ int tok[64];
   __shared__ int bad[64];
-  for (int row = lane; row <= D; row += 64) {
-    float best = -__builtin_inff();
-    int bi = 0x7FFFFFFF, b = 0;
-    for (int c = 0; c < nch; ++c) {
-      const float v = k.cmax[row * nch + c];
-      const int i = __float_as_int(k.ctot[row * nch + c]);
-      b |= k.cbad[row * nch + c] != 0.f;
-      if (v > best || (v == best && i < bi)) {
-        best = v;
-        bi = i;
+  // Row i's first maximum over its chunk maxima: the largest (value key, complemented index) over the wave.
+  for (int row = 0; row <= D; ++row) {
+    uint64_t bk = 0;
+    uint32_t b = 0;
+#pragma unroll
+    for (int q = 0; q < kMaxPerLane; ++q) {
+      const int c = lane + 64 * q;
+      if (c < nch) {
+        const float v = k.cmax[row * nch + c];
+        const int i = __float_as_int(k.ctot[row * nch + c]);
+        b |= k.cbad[row * nch + c] != 0.f ? 1u : 0u;
+        const uint64_t kv = ((uint64_t)ss_key(v == 0.f ? 0.f : v) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+        bk = kv > bk ? kv : bk;
       }
     }
-    tok[row] = bi;
-    bad[row] = b;
+    bk = ss_wave_max_u64(bk);
+    b = ss_wave_or(b);
+    if (lane == 0) {
+      tok[row] = (int)(0xFFFFFFFFu - (uint32_t)bk);
+      bad[row] = (int)b;
+    }
   }
   __syncthreads();
   if (lane == 0) {
@@ -164,11 +214,8 @@ __global__ __launch_bounds__(64) void pq_max_kernel(AcceptArgs a) {
   }
 }
 
-SS_DEV float row_max(const Work& k, int row, int nch) {
-  float m = -__builtin_inff();
-  for (int c = 0; c < nch; ++c) m = fmaxf(m, k.cmax[row * nch + c]);
-  return m;
-}
+// Row maximum over the chunk maxima (order-free), by the whole wave.
+SS_DEV float row_max(const Work& k, int row, int nch) { return wave_max_of(wave_load(k.cmax + (size_t)row * nch, nch), nch); }
 
 // Stage one chunk of a row (as e = exp(l/T - m)) into LDS with a 65-float stride per sub-chunk.
 SS_DEV void stage_exp(const AcceptArgs& a, int row, int c, float m, float* lds) {
@@ -200,16 +247,16 @@ __global__ __launch_bounds__(64) void pq_sum_kernel(AcceptArgs a) {
 // state: [0] sample target row, [1] sample draft row (-1 = plain p), [2] uniform index, [3] stop (no sample),
 //        [4..] per-row Z and m for the two sampled rows.
 __global__ __launch_bounds__(64) void pq_decide_kernel(AcceptArgs a, int nch) {
+  // Run by the whole wave (every lane computes the same values); lane 0 writes the state.
   const int rows = 2 * a.D + 1;
   Work k = work_of(a.work, rows, nch);
-  if (threadIdx.x != 0) return;
+  auto row_sum = [&](int row) { return wave_seq_sum(wave_load(k.ctot + (size_t)row * nch, nch), nch); };
+  auto row_bad = [&](int row) { return wave_any_nonzero(wave_load(k.cbad + (size_t)row * nch, nch), nch); };
   int good = 0, flags = 0, stop = 0;
   int srow = a.D, sdraft = -1;
   for (int i = 0; i < a.D; ++i) {
     const int dr = a.D + 1 + i;
-    int badrow = 0;
-    for (int c = 0; c < nch; ++c) badrow |= (k.cbad[i * nch + c] != 0.f) | (k.cbad[dr * nch + c] != 0.f);
-    if (badrow) {
+    if (row_bad(i) || row_bad(dr)) {
       flags |= FLAG_NONFINITE;
       stop = 1;
       break;
@@ -217,14 +264,12 @@ __global__ __launch_bounds__(64) void pq_decide_kernel(AcceptArgs a, int nch) {
     const int x = a.drafts[i];
     if (x < 0 || x >= a.V) {
       flags |= FLAG_BAD_DRAFT;
-      ss_raise(a.err, SS_ERR_TOKEN);
+      if (threadIdx.x == 0) ss_raise(a.err, SS_ERR_TOKEN);
       srow = i;
       sdraft = dr;
       break;
     }
-    float zp = 0.f, zq = 0.f;
-    for (int c = 0; c < nch; ++c) zp = zp + k.ctot[i * nch + c];
-    for (int c = 0; c < nch; ++c) zq = zq + k.ctot[dr * nch + c];
+    const float zp = row_sum(i), zq = row_sum(dr);
     const float mp = row_max(k, i, nch), mq = row_max(k, dr, nch);
     const float p = ss_expf(a.target[(size_t)i * a.V + x] / a.temperature - mp) / zp;
     const float q = ss_expf(a.draft[(size_t)i * a.V + x] / a.temperature - mq) / zq;
@@ -236,28 +281,26 @@ __global__ __launch_bounds__(64) void pq_decide_kernel(AcceptArgs a, int nch) {
     sdraft = dr;
     break;
   }
-  if (!stop && sdraft < 0) {
-    int badrow = 0;
-    for (int c = 0; c < nch; ++c) badrow |= k.cbad[a.D * nch + c] != 0.f;
-    if (badrow) {
-      flags |= FLAG_NONFINITE;
-      stop = 1;
-    }
+  if (!stop && sdraft < 0 && row_bad(a.D)) {
+    flags |= FLAG_NONFINITE;
+    stop = 1;
   }
-  k.state[0] = __int_as_float(srow);
-  k.state[1] = __int_as_float(sdraft);
-  k.state[2] = __int_as_float(good + (sdraft >= 0 ? 1 : 0));
-  k.state[3] = __int_as_float(stop);
-  k.state[4] = __int_as_float(good);
-  k.state[5] = __int_as_float(flags);
-  float zp = 0.f, zq = 0.f;
-  for (int c = 0; c < nch; ++c) zp = zp + k.ctot[srow * nch + c];
-  if (sdraft >= 0)
-    for (int c = 0; c < nch; ++c) zq = zq + k.ctot[sdraft * nch + c];
-  k.state[6] = zp;
-  k.state[7] = zq;
-  k.state[8] = row_max(k, srow, nch);
-  k.state[9] = sdraft >= 0 ? row_max(k, sdraft, nch) : 0.f;
+  const float zp = row_sum(srow);
+  const float zq = sdraft >= 0 ? row_sum(sdraft) : 0.f;
+  const float ms = row_max(k, srow, nch);
+  const float md = sdraft >= 0 ? row_max(k, sdraft, nch) : 0.f;
+  if (threadIdx.x == 0) {
+    k.state[0] = __int_as_float(srow);
+    k.state[1] = __int_as_float(sdraft);
+    k.state[2] = __int_as_float(good + (sdraft >= 0 ? 1 : 0));
+    k.state[3] = __int_as_float(stop);
+    k.state[4] = __int_as_float(good);
+    k.state[5] = __int_as_float(flags);
+    k.state[6] = zp;
+    k.state[7] = zq;
+    k.state[8] = ms;
+    k.state[9] = md;
+  }
 }
 
 // Value of entry j of the sampled distribution: p_j, or max(0, p_j - q_j) after a rejection.
@@ -288,43 +331,57 @@ __global__ __launch_bounds__(64) void pq_residual_kernel(AcceptArgs a) {
   if (lane == 0) k.rtot[c] = s;
 }
 
+// Inverse-CDF search, by the whole wave: the running sums keep their sequential order (index order, from the
+// chunk's base), formed from the lanes' registers; every lane follows the same scan.
 __global__ __launch_bounds__(64) void pq_search_kernel(AcceptArgs a, int nch) {
   Work k = work_of(a.work, 2 * a.D + 1, nch);
-  if (threadIdx.x != 0) return;
+  const int lane = threadIdx.x;
   const int good = __float_as_int(k.state[4]);
   int flags = __float_as_int(k.state[5]);
   const int stop = __float_as_int(k.state[3]);
   const int uidx = __float_as_int(k.state[2]);
-  for (int i = 0; i < good; ++i) a.out[OUT_TOK + i] = a.drafts[i];
   int emit = good;
+  int pick = -1;
   if (!stop) {
-    float S = 0.f;
-    for (int c = 0; c < nch; ++c) S = S + k.rtot[c];
+    const WaveVals rt = wave_load(k.rtot, nch);
+    const float S = wave_seq_sum(rt, nch);
     if (!(S > 0.f)) flags |= FLAG_RESIDUAL_EMPTY;
     const float target = a.uniforms[uidx] * S;
-    // chunk
+    // chunk: the first whose running total exceeds the target (else the last nonzero one, based at its prefix)
     int cs = -1, clast = -1;
     float base = 0.f, run = 0.f;
-    for (int c = 0; c < nch; ++c) {
-      const float nx = run + k.rtot[c];
-      if (k.rtot[c] > 0.f) clast = c;
-      if (cs < 0 && nx > target) {
-        cs = c;
-        base = run;
+#pragma unroll
+    for (int q = 0; q < kMaxPerLane; ++q) {
+      if (64 * q >= nch) break;
+      const int m = nch - 64 * q < 64 ? nch - 64 * q : 64;
+      for (int l = 0; l < m; ++l) {
+        const float t = ss_readlane_f(rt.v[q], l);
+        const float nx = run + t;
+        if (t > 0.f) clast = 64 * q + l;
+        if (cs < 0 && nx > target) {
+          cs = 64 * q + l;
+          base = run;
+        }
+        run = nx;
       }
-      run = nx;
     }
     if (cs < 0) {
       cs = clast < 0 ? 0 : clast;
       base = 0.f;
-      for (int c = 0; c < cs; ++c) base = base + k.rtot[c];
+#pragma unroll
+      for (int q = 0; q < kMaxPerLane; ++q) {
+        if (64 * q >= cs) break;
+        const int m = cs - 64 * q < 64 ? cs - 64 * q : 64;
+        for (int l = 0; l < m; ++l) base = base + ss_readlane_f(rt.v[q], l);
+      }
     }
-    // sub-chunk
+    // sub-chunk: lane b holds the sub-chunk total b of chunk cs
+    const float st_b = k.stot[cs * 64 + lane];
     int bs = -1, blast = -1;
     float sbase = base;
     run = base;
     for (int b = 0; b < 64; ++b) {
-      const float t = k.stot[cs * 64 + b];
+      const float t = ss_readlane_f(st_b, b);
       const float nx = run + t;
       if (t > 0.f) blast = b;
       if (bs < 0 && nx > target) {
@@ -336,15 +393,18 @@ __global__ __launch_bounds__(64) void pq_search_kernel(AcceptArgs a, int nch) {
     if (bs < 0) {
       bs = blast < 0 ? 0 : blast;
       sbase = base;
-      for (int b = 0; b < bs; ++b) sbase = sbase + k.stot[cs * 64 + b];
+      for (int b = 0; b < bs; ++b) sbase = sbase + ss_readlane_f(st_b, b);
     }
-    // entry
-    int pick = -1, last = -1;
+    // entry: lane i < 16 holds the value of entry i of sub-chunk bs
+    const int j0 = cs * kChunk + bs * kSub;
+    const int jl = j0 + (lane & (kSub - 1));
+    const float val = jl < a.V ? sample_value(a, k.state, jl) : 0.f;
+    int last = -1;
     run = sbase;
     for (int i = 0; i < kSub; ++i) {
-      const int j = cs * kChunk + bs * kSub + i;
+      const int j = j0 + i;
       if (j >= a.V) break;
-      const float v = sample_value(a, k.state, j);
+      const float v = ss_readlane_f(val, i);
       if (v > 0.f) last = j;
       run = run + v;
       if (run > target) {
@@ -352,14 +412,17 @@ __global__ __launch_bounds__(64) void pq_search_kernel(AcceptArgs a, int nch) {
         break;
       }
     }
-    if (pick < 0) pick = last >= 0 ? last : min(cs * kChunk + bs * kSub, a.V - 1);
-    a.out[OUT_TOK + emit++] = pick;
+    if (pick < 0) pick = last >= 0 ? last : min(j0, a.V - 1);
   }
-  for (int i = emit; i <= a.D; ++i) a.out[OUT_TOK + i] = -1;
-  a.out[OUT_NACC] = good;
-  a.out[OUT_NEMIT] = emit;
-  a.out[OUT_NUNI] = stop ? uidx : uidx + 1;
-  a.out[OUT_FLAGS] = flags;
+  if (lane == 0) {
+    for (int i = 0; i < good; ++i) a.out[OUT_TOK + i] = a.drafts[i];
+    if (!stop) a.out[OUT_TOK + emit++] = pick;
+    for (int i = emit; i <= a.D; ++i) a.out[OUT_TOK + i] = -1;
+    a.out[OUT_NACC] = good;
+    a.out[OUT_NEMIT] = emit;
+    a.out[OUT_NUNI] = stop ? uidx : uidx + 1;
+    a.out[OUT_FLAGS] = flags;
+  }
 }
 
 hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st) {

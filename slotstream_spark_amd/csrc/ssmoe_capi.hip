@@ -293,7 +293,7 @@ int64_t ssmoe_accept_workspace_bytes(int D, int V) {
 
 static int check_accept(int D, int V, void* workspace, int64_t workspace_bytes, int32_t* out) {
   if (D < 0 || D > 60) return fail(SSMOE_EINVAL, "D must be in [0, 60], got %d", D);
-  if (V < 1) return fail(SSMOE_EINVAL, "V must be >= 1, got %d", V);
+  if (V < 1 || V > (1 << 20)) return fail(SSMOE_EINVAL, "V must be in [1, 1048576], got %d", V);
   if (!workspace || !out) return fail(SSMOE_EINVAL, "workspace and out must be non-null");
   if (workspace_bytes < ss::accept_work_floats(D, V) * 4)
     return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
