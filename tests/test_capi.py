@@ -111,8 +111,9 @@ def test_topk_router_accept_reject(L):
     assert L.ssmoe_accept_greedy(p, p, 61, 1000, p, ws, p, None) == EINVAL
     assert L.ssmoe_accept_greedy(p, p, 3, 1000, p, ws - 4, p, None) == EINVAL
     assert L.ssmoe_accept_pq(p, p, p, p, 3, 1000, 0.0, p, ws, p, None) == EINVAL
-    assert L.ssmoe_accept_greedy(p, p, 3, (1 << 20) + 1, p, 1 << 40, p, None) == EINVAL
     assert b"temperature" in L.ssmoe_last_error()
+    assert L.ssmoe_accept_greedy(p, p, 3, (1 << 20) + 1, p, 1 << 40, p, None) == EINVAL
+    assert b"1048576" in L.ssmoe_last_error()
 
 
 # ---------------------------------------------------------------- Python mirrors
