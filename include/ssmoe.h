@@ -160,6 +160,23 @@ int ssmoe_moe_prefill(const uint16_t* x, const int32_t* expert_ids, const float*
                       int64_t workspace_bytes, uint16_t* h_buf, float* out_rows, float* out, int64_t T, int H, int I,
                       int K, int E, void* stream);
 
+/* ---------------------------------------------------------------- reference sampler */
+
+/* Bytes of the workspace ssmoe_sample needs for a V-token row (-1 outside 1 <= V <= 1,048,576). */
+int64_t ssmoe_sample_workspace_bytes(int V);
+
+/* One draw of the reference sampler. Replaces Sampler.next (engine/sampler.py:76-108) for one row of fp32 logits
+ * [V], with the parameters already sanitized (SampleParams.sanitized, :45-64): temperature >= 0 (0: argmax of the
+ * penalized logits), top_p in (0, 1], top_k >= 0 (0 or >= V: off), min_p in [0, 1], finite presence_penalty;
+ * generated int32 [n_generated] the tokens generated so far, sorted ascending without repeats; u a device pointer to
+ * the draw's uniform (float32((state >> 11) / 2^53) of the sampler's splitmix64 stream, :101-102). Writes out int32
+ * [2]: the token and flags (1 = the kept mass was not finite and > 0: argmax of the raw logits, :105-106).
+ * The reference's float32 operations in its order; the order of each sum is this library's (hierarchical, as the
+ * acceptance sums), and exp is this library's. */
+int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_generated, float temperature,
+                 float top_p, int top_k, float min_p, float presence_penalty, const float* u, void* workspace,
+                 int64_t workspace_bytes, int32_t* out, void* stream);
+
 /* ---------------------------------------------------------------- shared expert (prefill) */
 
 /* hs[t, i] = bf16(bf16(silu(g)) * u), g = proj[t, i], u = proj[t, Is + i], and sgl[t] = proj[t, 2 Is]: the F.silu and

@@ -50,6 +50,8 @@ def lib():
         L.or_row_z.argtypes, L.or_row_z.restype = [P, i32, f32], f32
         L.or_shared_hs.argtypes, L.or_shared_hs.restype = [P, P, P, i32], None
         L.or_combine_shared.argtypes, L.or_combine_shared.restype = [P, P, P, P, i32, i32], None
+        L.or_sample.argtypes = [P, i32, P, i32, f32, f32, i32, f32, f32, f32, P, P]
+        L.or_sample.restype = None
         _lib = L
     return _lib
 
@@ -161,6 +163,18 @@ def shared_expert(x_bits, gate_bits, up_bits, down_bits, sg_bits):
     sh = dense_rows(hs, down_bits)
     sgl = dense_rows(x_bits, sg_bits)[:, 0].copy()
     return sh, sgl
+
+
+def sample(logits, generated, temperature, top_p, top_k, min_p, presence_penalty, u):
+    """The device sampler's definition (Sampler.next, engine/sampler.py:76-108, with this build's sum order and
+    exp): (token, flags). Parameters must already be sanitized; `generated` is any iterable of token ids."""
+    x = _c(logits, np.float32)
+    g = np.array(sorted(set(int(t) for t in generated)), dtype=np.int32)
+    out = np.zeros(2, np.int32)
+    work = np.empty(2 * x.size, np.float32)
+    lib().or_sample(_p(x), x.size, _p(g) if g.size else None, int(g.size), float(temperature), float(top_p),
+                    int(top_k), float(min_p), float(presence_penalty), float(u), _p(out), _p(work))
+    return int(out[0]), int(out[1])
 
 
 def shared_hs(g_bits, u_bits) -> np.ndarray:

@@ -463,3 +463,192 @@ void or_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* 
 void or_expf_vec(const float* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) y[i] = or_expf(x[i]);
 }
+
+/* ---------------------------------------------------------------- reference sampler (engine/sampler.py:76-108)
+ * Sampler.next with sanitized parameters, in the order of the reference: presence penalty on the raw logits
+ * (:80-82), argmax at temperature <= 0 (:83-84), division by the temperature (:85), top-k threshold (:86-88),
+ * softmax (:89, :67-69), top-p (:90-97), min-p (:98-100), inverse CDF with the uniform u (:101-108). Every float op
+ * is the reference's float32 op; the order of each sum is this build's (the reference's comes from numpy: its
+ * pairwise e.sum() and sequential cumsums, and its exp is numpy's):
+ *   z, the top-p cumulative mass and the final total use the hierarchical order of the acceptance sums (sub-chunks
+ *   of 16 summed sequentially, 64 sub-chunk totals of a 1024-entry chunk by the xor butterfly, chunk totals
+ *   sequentially); exp is or_expf.
+ *   top-p: entry j ranks by rho_j = key(p_j) << 20 | (2^20 - 1 - j) (probability descending, then index
+ *   ascending, the stable argsort of :91); cum(rho) = hierarchical sum of p_i over rho_i > rho; j is kept iff
+ *   cum(rho_j) < top_p (the reference's (cum - srt) < top_p with cum - srt = the mass ranked before j).
+ *   draw: cdf_j is the hierarchical running sum (chunk base, then sub-chunk base, then the entries of the
+ *   sub-chunk); the pick is the first entry with cdf_j >= u * total (u == 0: cdf_j > 0), found chunk, then
+ *   sub-chunk, then entry, each level falling back to the last nonzero one; the reference counts cdf < u * total.
+ * out[0] = token, out[1] = flags (1 = the total was not finite and > 0: argmax of the raw logits, :105-106). */
+static int in_sorted(const int32_t* g, int n, int j) {
+  int lo = 0, hi = n - 1;
+  while (lo <= hi) {
+    const int mid = (lo + hi) >> 1;
+    if (g[mid] == j) return 1;
+    if (g[mid] < j) lo = mid + 1;
+    else hi = mid - 1;
+  }
+  return 0;
+}
+
+/* np.argmax: the first maximum, NaN counting as the largest (its first occurrence wins); -0 == +0. */
+static int argmax_np(const float* x, int V) {
+  int bi = 0;
+  for (int j = 0; j < V; ++j) {
+    const float v = x[j], b = x[bi];
+    if (b != b) break;
+    if (v != v || v > b) bi = j;
+  }
+  return bi;
+}
+
+/* NaN-largest order-preserving key with -0 == +0 (np.sort order of :87). */
+static uint32_t nkey(float v) {
+  if (v != v) return 0xFFFFFFFFu;
+  return or_key(v == 0.0f ? 0.0f : v);
+}
+
+typedef struct {
+  const float* w;
+} ArrCtx;
+static float val_arr(const void* c, int j) { return ((const ArrCtx*)c)->w[j]; }
+
+typedef struct {
+  const float* p;
+  uint64_t rho;
+} CumCtx;
+static uint64_t rho_of(float p, int j) { return ((uint64_t)or_key(p) << 20) | (uint64_t)((1u << 20) - 1u - (uint32_t)j); }
+static float val_cum(const void* c, int j) {
+  const CumCtx* k = (const CumCtx*)c;
+  return rho_of(k->p[j], j) > k->rho ? k->p[j] : 0.0f;
+}
+
+static float hsum(ValFn f, const void* ctx, int V) {
+  const int nch = (V + CHUNK - 1) / CHUNK;
+  float s = 0.0f;
+  for (int c = 0; c < nch; ++c) s = s + chunk_total(f, ctx, c, V, NULL);
+  return s;
+}
+
+/* The first entry whose hierarchical running sum reaches the target (ge: >=, else >), with fallbacks. */
+static int hsearch(const float* w, int V, float target, int ge) {
+  ArrCtx ctx = {w};
+  const int nch = (V + CHUNK - 1) / CHUNK;
+  float sub[64];
+  int cs = -1, clast = -1;
+  float base = 0.0f, run = 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    const float t = chunk_total(val_arr, &ctx, c, V, NULL);
+    const float nx = run + t;
+    if (t > 0.0f) clast = c;
+    if (cs < 0 && (ge ? nx >= target : nx > target)) {
+      cs = c;
+      base = run;
+    }
+    run = nx;
+  }
+  if (cs < 0) {
+    cs = clast < 0 ? 0 : clast;
+    base = 0.0f;
+    for (int c = 0; c < cs; ++c) base = base + chunk_total(val_arr, &ctx, c, V, NULL);
+  }
+  chunk_total(val_arr, &ctx, cs, V, sub);
+  int bs = -1, blast = -1;
+  float sbase = base;
+  run = base;
+  for (int b = 0; b < 64; ++b) {
+    const float nx = run + sub[b];
+    if (sub[b] > 0.0f) blast = b;
+    if (bs < 0 && (ge ? nx >= target : nx > target)) {
+      bs = b;
+      sbase = run;
+    }
+    run = nx;
+  }
+  if (bs < 0) {
+    bs = blast < 0 ? 0 : blast;
+    sbase = base;
+    for (int b = 0; b < bs; ++b) sbase = sbase + sub[b];
+  }
+  int pick = -1, last = -1;
+  run = sbase;
+  for (int i = 0; i < SUB; ++i) {
+    const int j = cs * CHUNK + bs * SUB + i;
+    if (j >= V) break;
+    if (w[j] > 0.0f) last = j;
+    run = run + w[j];
+    if (ge ? run >= target : run > target) {
+      pick = j;
+      break;
+    }
+  }
+  if (pick < 0) pick = last >= 0 ? last : (cs * CHUNK + bs * SUB < V ? cs * CHUNK + bs * SUB : V - 1);
+  return pick;
+}
+
+/* work: >= 2 V floats. */
+void or_sample(const float* x, int V, const int32_t* gen, int n_gen, float temperature, float top_p, int top_k,
+               float min_p, float presence_penalty, float u, int32_t* out, float* work) {
+  float* l = work;
+  float* p = work + V;
+  for (int j = 0; j < V; ++j)
+    l[j] = (presence_penalty != 0.0f && n_gen > 0 && in_sorted(gen, n_gen, j)) ? x[j] - presence_penalty : x[j];
+  out[1] = 0;
+  if (temperature <= 0.0f) {
+    out[0] = argmax_np(l, V);
+    return;
+  }
+  for (int j = 0; j < V; ++j) l[j] = l[j] / temperature;
+  if (top_k > 0 && top_k < V) {
+    /* the top_k-th largest key (counting multiplicity), by a bitwise search from the top */
+    uint32_t kk = 0;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = kk | (1u << bit);
+      int cnt = 0;
+      for (int j = 0; j < V; ++j) cnt += nkey(l[j]) >= cand;
+      if (cnt >= top_k) kk = cand;
+    }
+    float kth = 0.0f;
+    for (int j = 0; j < V; ++j)
+      if (nkey(l[j]) == kk) {
+        kth = l[j];
+        break;
+      }
+    for (int j = 0; j < V; ++j) l[j] = l[j] < kth ? -INFINITY : l[j];
+  }
+  float m = -INFINITY;
+  int nan = 0;
+  for (int j = 0; j < V; ++j) {
+    nan |= l[j] != l[j];
+    m = fmaxf(m, l[j]);
+  }
+  if (nan) m = NAN;
+  for (int j = 0; j < V; ++j) p[j] = or_expf(l[j] - m);
+  ArrCtx pc = {p};
+  const float z = hsum(val_arr, &pc, V);
+  for (int j = 0; j < V; ++j) p[j] = p[j] / z;
+  if (top_p < 1.0f) {
+    /* the smallest rho with cum(rho) < top_p (cum falls as rho grows); bits 52..0 from the top */
+    uint64_t r = 0;
+    for (int bit = 51; bit >= 0; --bit) {
+      const uint64_t hi = r | (((uint64_t)1 << bit) - 1) ; /* candidate: the largest value with this bit 0 */
+      CumCtx cc = {p, hi};
+      if (!(hsum(val_cum, &cc, V) < top_p)) r |= (uint64_t)1 << bit;
+    }
+    for (int j = 0; j < V; ++j) l[j] = rho_of(p[j], j) >= r ? p[j] : 0.0f;
+    memcpy(p, l, sizeof(float) * (size_t)V);
+  }
+  if (min_p > 0.0f) {
+    float pm = -INFINITY;
+    for (int j = 0; j < V; ++j) pm = fmaxf(pm, p[j]);
+    const float cutoff = pm * min_p;
+    for (int j = 0; j < V; ++j) p[j] = p[j] < cutoff ? 0.0f : p[j];
+  }
+  const float total = hsum(val_arr, &pc, V);
+  if (!is_finite_f(total) || !(total > 0.0f)) {
+    out[0] = argmax_np(x, V);
+    out[1] = 1;
+    return;
+  }
+  out[0] = u == 0.0f ? hsearch(p, V, 0.0f, 0) : hsearch(p, V, u * total, 1);
+}

@@ -107,6 +107,11 @@ hipError_t launch_prefill_tables(const int32_t* map, int64_t map_base, int64_t m
                                  int64_t n_slots, int E, int64_t* gptr, const int32_t* ids, int64_t R, int K,
                                  int32_t* local, int32_t* row_token, int* err, hipStream_t st);
 
+// Reference sampler (ss_sampler.hip): Sampler.next over one row with sanitized parameters; u a device float.
+int64_t sample_workspace_bytes(int V);
+hipError_t launch_sample(const float* x, int V, const int32_t* gen, int n_gen, float temperature, float top_p,
+                         int top_k, float min_p, float pp, const float* u, void* work, int32_t* out, hipStream_t st);
+
 // Acceptance.
 struct AcceptArgs {
   const float* target;   // [D+1, V]

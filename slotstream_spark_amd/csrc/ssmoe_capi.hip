@@ -539,4 +539,33 @@ int ssmoe_combine_shared(const float* routed, const uint16_t* sh, const uint16_t
                    "combine_shared launch");
 }
 
+// ---------------------------------------------------------------- reference sampler
+int64_t ssmoe_sample_workspace_bytes(int V) {
+  if (V < 1 || V > (1 << 20)) return -1;
+  return ss::sample_workspace_bytes(V);
+}
+
+int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_generated, float temperature,
+                 float top_p, int top_k, float min_p, float presence_penalty, const float* u, void* workspace,
+                 int64_t workspace_bytes, int32_t* out, void* stream) {
+  if (V < 1 || V > (1 << 20)) return fail(SSMOE_EINVAL, "V must be in [1, 1048576], got %d", V);
+  if (!(temperature >= 0.f) || temperature > 3.4e38f) return fail(SSMOE_EINVAL, "temperature must be finite and >= 0");
+  if (!(top_p > 0.f && top_p <= 1.f)) return fail(SSMOE_EINVAL, "top_p must be in (0, 1], got %g", (double)top_p);
+  if (!(min_p >= 0.f && min_p <= 1.f)) return fail(SSMOE_EINVAL, "min_p must be in [0, 1], got %g", (double)min_p);
+  if (top_k < 0) return fail(SSMOE_EINVAL, "top_k must be >= 0, got %d", top_k);
+  if (!(presence_penalty == presence_penalty) || presence_penalty > 3.4e38f || presence_penalty < -3.4e38f)
+    return fail(SSMOE_EINVAL, "presence_penalty must be finite");
+  if (n_generated < 0 || (n_generated > 0 && !generated))
+    return fail(SSMOE_EINVAL, "generated must hold n_generated >= 0 token ids");
+  if (!logits || !u || !workspace || !out) return fail(SSMOE_EINVAL, "logits, u, workspace and out must be non-null");
+  if (!aligned(workspace, 256)) return fail(SSMOE_EINVAL, "workspace must be 256-byte aligned");
+  if (workspace_bytes < ss::sample_workspace_bytes(V))
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)ss::sample_workspace_bytes(V));
+  return hip_check(ss::launch_sample(logits, V, generated, n_generated, temperature, top_p, top_k, min_p,
+                                     presence_penalty, u, workspace, out, static_cast<hipStream_t>(stream)),
+                   "sample launch");
+}
+
 }  // extern "C"
+

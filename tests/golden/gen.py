@@ -34,3 +34,46 @@ def record(seed: int, e: int, H: int, I: int) -> np.ndarray:
         s[...] = sv
         b[...] = orc.f32_to_bf16(-8.0 * orc.bf16_to_f32(sv))
     return rec
+
+
+_M64 = (1 << 64) - 1
+
+
+def _splitmix(v: int) -> int:
+    v = (v + 0x9E3779B97F4A7C15) & _M64
+    v = ((v ^ (v >> 30)) * 0xBF58476D1CE4E5B9) & _M64
+    v = ((v ^ (v >> 27)) * 0x94D049BB133111EB) & _M64
+    return v ^ (v >> 31)
+
+
+def sampler_logits(vocab: int, seed: int) -> np.ndarray:
+    """The logits the sampler fixtures were drawn over: the reference helper make_logits (engine/sampler.py:27-32),
+    uniform in [-4, 4) from the splitmix64 stream, float32 arithmetic."""
+    st, out = seed, np.empty(vocab, np.float32)
+    for i in range(vocab):
+        st = _splitmix(st)
+        out[i] = np.float32(st >> 40) / np.float32(1 << 24) * np.float32(8.0) - np.float32(4.0)
+    return out
+
+
+def sampler_uniform(state: int):
+    """(next state, u) of the sampler's stream (engine/sampler.py:101-102)."""
+    state = _splitmix((state + 1) & _M64)
+    return state, np.float32((state >> 11) / float(1 << 53))
+
+
+def replay_sampler_case(case, logits, draw):
+    """Replays one fixture case: draw(logits, generated, params..., u) -> token, with the fixture's seed, penalty
+    and accumulation; returns the 16 tokens."""
+    state = case["seed"] if case["seed"] != 0 else 0xDEADBEEF
+    gen, toks = set(), []
+    for _ in range(len(case["tokens"])):
+        u = np.float32(0.0)
+        if case["temperature"] > 0:
+            state, u = sampler_uniform(state)
+        tok = draw(logits, gen if case["presence_penalty"] != 0 else (), case["temperature"], case["top_p"],
+                   case["top_k"], case["min_p"], case["presence_penalty"], u)
+        toks.append(tok)
+        if case["accumulate"]:
+            gen.add(tok)
+    return toks

@@ -166,3 +166,24 @@ def test_shared_entry_points_reject_bad_arguments(L):
     assert b"16-byte aligned" in L.ssmoe_last_error()
     assert L.ssmoe_combine_shared(None, None, None, None, 0, 8, None) == 0
 
+
+
+def test_sample_rejects_bad_arguments(L):
+    p = ctypes.c_void_p(4096)
+    ws = L.ssmoe_sample_workspace_bytes(1000)
+    assert ws > 2 * 1000 * 4 and L.ssmoe_sample_workspace_bytes(0) == -1
+    assert L.ssmoe_sample_workspace_bytes((1 << 20) + 1) == -1
+    good = dict(t=0.8, tp=0.9, tk=40, mp=0.0, pp=0.0)
+
+    def call(V=1000, n=0, g=None, t=0.8, tp=0.9, tk=40, mp=0.0, pp=0.0, w=ws):
+        return L.ssmoe_sample(p, V, g, n, t, tp, tk, mp, pp, p, ctypes.c_void_p(4096), w, p, None)
+    assert call(t=-1.0) == EINVAL and b"temperature" in L.ssmoe_last_error()
+    assert call(t=float("nan")) == EINVAL
+    assert call(tp=0.0) == EINVAL and b"top_p" in L.ssmoe_last_error()
+    assert call(tp=1.5) == EINVAL
+    assert call(mp=-0.1) == EINVAL and b"min_p" in L.ssmoe_last_error()
+    assert call(tk=-1) == EINVAL and b"top_k" in L.ssmoe_last_error()
+    assert call(pp=float("inf")) == EINVAL
+    assert call(n=3) == EINVAL and b"generated" in L.ssmoe_last_error()
+    assert call(w=ws - 1) == EINVAL and b"workspace holds" in L.ssmoe_last_error()
+    assert call(V=0) == EINVAL

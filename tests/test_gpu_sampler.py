@@ -1,0 +1,105 @@
+"""The reference sampler on the GPU (ssmoe_sample through engine.sampler.Sampler) against its definition
+(oracle.sample): token and flags bit for bit over the reference's fixture grid and over random rows with every
+filter, edge values (NaN, -inf, ties, tiny and large vocabularies); and the reference's own draws."""
+import json
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from slotstream_spark_amd import _lib
+from slotstream_spark_amd.engine.sampler import SampleParams, Sampler
+from tests.golden.gen import replay_sampler_case, sampler_logits
+
+pytestmark = pytest.mark.gpu
+GOLD = json.loads((Path(__file__).resolve().parent / "golden" / "sampler_ref.json").read_text())
+
+
+class Dev:
+    """One device sampler row: draw(...) -> (token, flags) with an explicit uniform."""
+
+    def __init__(self, v):
+        self.work = torch.empty(int(_lib.lib().ssmoe_sample_workspace_bytes(v)), dtype=torch.uint8, device="cuda")
+        self.out = torch.empty(2, dtype=torch.int32, device="cuda")
+        self.u = torch.empty(1, dtype=torch.float32, device="cuda")
+
+    def draw(self, x, gen, t, tp, tk, mp, pp, u):
+        g = sorted(set(int(a) for a in gen))
+        gt = torch.tensor(g, dtype=torch.int32, device="cuda") if g else None
+        self.u.fill_(float(u))
+        _lib.check(_lib.lib().ssmoe_sample(x.data_ptr(), x.numel(), _lib.ptr(gt), len(g), float(t), float(tp), int(tk),
+                                           float(mp), float(pp), self.u.data_ptr(), self.work.data_ptr(),
+                                           self.work.numel(), self.out.data_ptr(), 0))
+        o = self.out.cpu().numpy()
+        return int(o[0]), int(o[1])
+
+
+@pytest.mark.parametrize("vocab", [256, 4096, 151936])
+def test_fixture_grid_bitwise_and_reference(vocab):
+    print(f"[sampler] fixture grid vocab={vocab}", flush=True)
+    x = sampler_logits(vocab, 99)
+    xd = torch.from_numpy(x).cuda()
+    dev = Dev(vocab)
+    ok = tot = 0
+    for case in [c for c in GOLD["cases"] if c["vocab"] == vocab]:
+        got = replay_sampler_case(case, xd, lambda l, g, *a: dev.draw(l, g, *a)[0])
+        want = replay_sampler_case(case, x, lambda l, g, *a: O.sample(l, g, *a)[0])
+        assert got == want, case
+        ok += sum(a == b for a, b in zip(got, case["tokens"]))
+        tot += len(got)
+    assert ok >= tot - 2  # the reference's own draws (see tests/test_sampler_oracle.py)
+
+
+EDGE_PARAMS = [(0.0, 1.0, 0, 0.0, 0.0), (0.7, 1.0, 0, 0.0, 0.0), (1.0, 0.9, 0, 0.0, 0.0), (0.6, 0.5, 40, 0.05, 1.5),
+               (1.3, 1.0, 1, 0.0, 0.0), (0.9, 0.95, 0, 0.2, -0.7), (0.8, 1e-6, 0, 0.0, 0.0), (1.0, 1.0, 0, 1.0, 0.0),
+               (2.0, 0.3, 7, 0.0, 3.0)]
+
+
+@pytest.mark.parametrize("v,seed", [(1, 0), (7, 1), (1023, 2), (1024, 3), (1025, 4), (5000, 5), (248320, 6)])
+def test_random_rows_bitwise(v, seed):
+    print(f"[sampler] random rows v={v}", flush=True)
+    rng = np.random.default_rng(seed)
+    dev = Dev(v)
+    for r in range(4):
+        x = (rng.standard_normal(v) * (1 + 3 * r)).astype(np.float32)
+        if r == 1 and v > 4:
+            x[rng.integers(0, v, 3)] = -np.inf
+        if r == 2 and v > 4:
+            x[: v // 2] = np.float32(1.25)  # large tie groups
+        xd = torch.from_numpy(x).cuda()
+        gen = set(rng.integers(0, v, min(v, 20)).tolist())
+        for (t, tp, tk, mp, pp) in EDGE_PARAMS:
+            u = np.float32(rng.random())
+            assert dev.draw(xd, gen, t, tp, tk, mp, pp, u) == O.sample(x, gen, t, tp, tk, mp, pp, u), (r, t, tp, tk)
+        for u in (np.float32(0.0), np.float32(1.0)):
+            assert dev.draw(xd, (), 1.0, 0.8, 0, 0.0, 0.0, u) == O.sample(x, (), 1.0, 0.8, 0, 0.0, 0.0, u)
+
+
+def test_nonfinite_rows_fall_back_to_argmax():
+    x = np.random.default_rng(9).standard_normal(3000).astype(np.float32)
+    x[1234] = np.nan
+    xd = torch.from_numpy(x).cuda()
+    dev = Dev(3000)
+    for params in [(1.0, 1.0, 0, 0.0, 0.0), (0.7, 0.9, 10, 0.1, 0.0), (0.0, 1.0, 0, 0.0, 0.0)]:
+        assert dev.draw(xd, (), *params, np.float32(0.3)) == O.sample(x, (), *params, 0.3)
+    assert O.sample(x, (), 1.0, 1.0, 0, 0.0, 0.0, 0.3) == (1234, 1)  # numpy's max propagates NaN: argmax fallback
+
+
+def test_sampler_api_advances_like_the_reference():
+    v = 4096
+    x = sampler_logits(v, 99)
+    case = [c for c in GOLD["cases"] if c["vocab"] == v and c["temperature"] > 0][0]
+    s = Sampler(case["seed"])
+    p = SampleParams(temperature=case["temperature"], top_p=case["top_p"], top_k=case["top_k"], min_p=case["min_p"],
+                     presence_penalty=case["presence_penalty"])
+    xd = torch.from_numpy(x).cuda()
+    gen, toks = set(), []
+    for _ in range(16):
+        t = s.next(xd, p, gen)
+        toks.append(t)
+        if case["accumulate"]:
+            gen.add(t)
+    want = replay_sampler_case(case, x, lambda l, g, *a: O.sample(l, g, *a)[0])
+    assert toks == want
