@@ -136,7 +136,9 @@ def prefill_leg(pool, weights, biases, nl, steps, warmup, dev):
 
 def config2_leg(pool, lw, bias, steps, dev):
     """an MTP chain of depth 3 (T=4 verify) through the config-1 layer, then acceptance over
-    vocab 151,936: greedy argmax-match and p/q at temperature 0.7, on 1000 seeded steps of synthetic fp32 logits
+    vocab 151,936: greedy argmax-match, p/q at temperature 0.7, and (beside the step, as the reference's own sampled
+    round) the reference sampler at temperature 0.7 with its default top-p 0.95 / top-k 40, on 1000 seeded steps of
+    synthetic fp32 logits
     (target N(0,3), draft correlated rho=0.8; drafts = the draft rows' argmax; uniforms from the sampler's
     splitmix64 stream seeded per step). Every step's logits, drafts and uniforms are resident in HBM before the
     timed region; the steps are captured as HIP graphs (100 steps each) and replayed once, timed with HIP events."""
@@ -144,10 +146,12 @@ def config2_leg(pool, lw, bias, steps, dev):
     import torch
 
     from slotstream_spark_amd.engine.accept import Acceptor, AcceptResult, RoundStats, UniformStream
+    from slotstream_spark_amd.engine.sampler import SampleParams
     from slotstream_spark_amd.engine.verify import MoEVerifyLayer
     from slotstream_spark_amd.memory.synth import normal_bf16, verify_logits
 
     D, V, TEMP, T = 3, 151936, 0.7, 4
+    sp = SampleParams(temperature=TEMP)
     layer = MoEVerifyLayer(pool, 0, lw.router_w, lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_g, top_k=K,
                            router_bias=bias, max_tokens=4)
     x = normal_bf16((T, H), 1.0, 1734, dev)
@@ -163,9 +167,11 @@ def config2_leg(pool, lw, bias, steps, dev):
     acc = Acceptor(D, V, device=dev)
     out_g = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
     out_p = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
+    out_s = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
+    acc_s = Acceptor(D, V, device=dev)
     chunk = 100
 
-    def run(lo, hi, verify=True, greedy=True, pq=True):
+    def run(lo, hi, verify=True, greedy=True, pq=True, sampled=False):
         for st in range(lo, hi):
             if verify:
                 layer(x, y=y, ids=ids, weights=wts)
@@ -173,19 +179,23 @@ def config2_leg(pool, lw, bias, steps, dev):
                 out_g[st].copy_(acc.greedy_async(tgt[st], drafts[st]))
             if pq:
                 out_p[st].copy_(acc.pq_async(tgt[st], drf[st], drafts[st], uni[st], TEMP))
+            if sampled:
+                out_s[st].copy_(acc_s.sampled_async(tgt[st], drafts[st], sp, (), uni[st]))
 
     s_ = torch.cuda.Stream(device=dev)
     res = {}
     for name, kw in (("step", {}), ("verify", dict(greedy=False, pq=False)), ("greedy", dict(verify=False, pq=False)),
-                     ("pq", dict(verify=False, greedy=False))):
+                     ("pq", dict(verify=False, greedy=False)),
+                     ("sampled", dict(verify=False, greedy=False, pq=False, sampled=True))):
         total = 0.0
         for lo in range(0, steps, chunk):
             total += timed_graph(lambda: run(lo, min(steps, lo + chunk), **kw), 1, 0, s_) * 1000.0
         res[name] = total / steps
     g = [AcceptResult.from_out(o) for o in out_g.cpu()]
     q = [AcceptResult.from_out(o) for o in out_p.cpu()]
+    sm = [AcceptResult.from_out(o) for o in out_s.cpu()]
     stats = {}
-    for name, rs in (("greedy", g), ("pq", q)):
+    for name, rs in (("greedy", g), ("pq", q), ("sampled", sm)):
         st = RoundStats()
         for r in rs:
             st.add(D, r)
@@ -193,13 +203,17 @@ def config2_leg(pool, lw, bias, steps, dev):
                        "accepted_by_depth": st.accepted_by_depth, "attempts_by_depth": st.attempts_by_depth}
     tok_s = stats["pq"]["acceptance_length"] / (res["step"] * 1e-6)
     log(f"config2: step {res['step']:.1f} us (verify T=4 {res['verify']:.1f}, greedy {res['greedy']:.1f}, "
-        f"p/q {res['pq']:.1f}); acceptance length greedy {stats['greedy']['acceptance_length']}, "
-        f"p/q {stats['pq']['acceptance_length']}")
+        f"p/q {res['pq']:.1f}; sampled round {res['sampled']:.1f}); acceptance length greedy "
+        f"{stats['greedy']['acceptance_length']}, p/q {stats['pq']['acceptance_length']}, "
+        f"sampled {stats['sampled']['acceptance_length']}")
     return {"steps": steps, "depth": D, "vocab": V, "temperature": TEMP,
             "us_per_step": round(res["step"], 2), "us_verify_T4": round(res["verify"], 2),
             "us_accept_greedy": round(res["greedy"], 2), "us_accept_pq": round(res["pq"], 2),
             "tokens_per_s_pq": round(tok_s, 1), "greedy": stats["greedy"], "pq": stats["pq"],
-            "timing": "HIP graphs of 100 steps (verify layer + greedy + p/q per step), events on the graph stream"}
+            "us_accept_sampled": round(res["sampled"], 2),
+            "sampled": dict(stats["sampled"], params="temperature 0.7, top_p 0.95, top_k 40 (SampleParams defaults)"),
+            "timing": "HIP graphs of 100 steps (verify layer + greedy + p/q per step; the sampled round in graphs "
+                      "of its own), events on the graph stream"}
 
 
 def config4_leg(pool, weights, biases, steps, dev):

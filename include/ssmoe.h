@@ -177,6 +177,23 @@ int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_gen
                  float top_p, int top_k, float min_p, float presence_penalty, const float* u, void* workspace,
                  int64_t workspace_bytes, int32_t* out, void* stream);
 
+/* Bytes of the workspace ssmoe_accept_sampled needs (D+1 rows of ssmoe_sample's; -1 on bad arguments). */
+int64_t ssmoe_accept_sampled_workspace_bytes(int D, int V);
+
+/* The sampled verify round. Replaces the acceptance loop of _mtp_decode (engine/generate.py:208-229) at
+ * temperature > 0 or with a presence penalty: for row i = 0..D of target fp32 [D+1, V], a row holding a non-finite
+ * logit ends the round without a draw (flag 1, :210-212); otherwise the row draws as ssmoe_sample with uniforms[i]
+ * and the penalty set seen + the tokens emitted before it (seen.add, :214), and the round goes on while the token
+ * equals drafts[i] (i < D). seen int32 [n_seen] sorted ascending without repeats; workspace of
+ * ssmoe_accept_sampled_workspace_bytes(D, V) bytes; out int32 [D+5] as ssmoe_accept_greedy (n_accept, n_emit,
+ * n_uniform = draws at temperature > 0, flags 1 = non-finite row, 2 = draft out of range, 8 = a draw took the argmax
+ * fallback, then the emitted tokens, -1 past n_emit). 0 <= D <= 60. Row i is reached only when rows 0..i-1 drew
+ * their drafts, so all rows are drawn at once with penalty set seen + drafts[0..i); the launch sequence depends
+ * only on the parameters and can be captured in a graph. */
+int ssmoe_accept_sampled(const float* target, const int32_t* drafts, int D, int V, const int32_t* seen, int n_seen,
+                         float temperature, float top_p, int top_k, float min_p, float presence_penalty,
+                         const float* uniforms, void* workspace, int64_t workspace_bytes, int32_t* out, void* stream);
+
 /* ---------------------------------------------------------------- shared expert (prefill) */
 
 /* hs[t, i] = bf16(bf16(silu(g)) * u), g = proj[t, i], u = proj[t, Is + i], and sgl[t] = proj[t, 2 Is]: the F.silu and

@@ -177,6 +177,38 @@ def sample(logits, generated, temperature, top_p, top_k, min_p, presence_penalty
     return int(out[0]), int(out[1])
 
 
+def accept_sampled(target, drafts, seen, temperature, top_p, top_k, min_p, presence_penalty, uniforms):
+    """The sampled verify round (engine/generate.py:208-229): row i stops the round if it holds a non-finite logit
+    (:210-212), else draws with `sample` (uniforms[i], penalty set seen + tokens emitted so far, :213-214) and the
+    round continues while the token equals drafts[i]. Returns int32 [D+5]: n_accept, n_emit, n_uniform, flags
+    (1 non-finite row, 2 draft out of range, 8 argmax fallback), tokens (-1 past n_emit)."""
+    t = _c(target, np.float32)
+    D, V = t.shape[0] - 1, t.shape[1]
+    out = np.zeros(D + 5, np.int32)
+    out[4:] = -1
+    gen = set(int(v) for v in seen)
+    for i in range(D + 1):
+        if not np.isfinite(t[i]).all():
+            out[3] |= 1
+            break
+        tok, fb = sample(t[i], gen, temperature, top_p, top_k, min_p, presence_penalty, uniforms[i])
+        out[4 + i] = tok
+        out[1] = i + 1
+        if temperature > 0:
+            out[2] = i + 1
+        out[3] |= 8 if fb else 0
+        gen.add(tok)
+        if i < D:
+            d = int(drafts[i])
+            if d < 0 or d >= V:
+                out[3] |= 2
+            if tok == d:
+                out[0] = i + 1
+                continue
+        break
+    return out
+
+
 def shared_hs(g_bits, u_bits) -> np.ndarray:
     """hs = bf16(bf16(silu(g)) * u) elementwise on bf16 bits (the shared expert's F.silu and product)."""
     g = _c(g_bits, np.uint16)

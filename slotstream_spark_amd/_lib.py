@@ -45,6 +45,8 @@ SIGNATURES = {
     "ssmoe_combine_shared": (_I, [_P, _P, _P, _P, _I, _I, _P]),
     "ssmoe_sample_workspace_bytes": (_I64, [_I]),
     "ssmoe_sample": (_I, [_P, _I, _P, _I, _F, _F, _I, _F, _F, _P, _P, _I64, _P, _P]),
+    "ssmoe_accept_sampled_workspace_bytes": (_I64, [_I, _I]),
+    "ssmoe_accept_sampled": (_I, [_P, _P, _I, _I, _P, _I, _F, _F, _I, _F, _F, _P, _P, _I64, _P, _P]),
 }
 
 _lib = None

@@ -111,6 +111,9 @@ hipError_t launch_prefill_tables(const int32_t* map, int64_t map_base, int64_t m
 int64_t sample_workspace_bytes(int V);
 hipError_t launch_sample(const float* x, int V, const int32_t* gen, int n_gen, float temperature, float top_p,
                          int top_k, float min_p, float pp, const float* u, void* work, int32_t* out, hipStream_t st);
+hipError_t launch_accept_sampled(const float* target, const int32_t* drafts, int D, int V, const int32_t* seen,
+                                 int n_seen, float temperature, float top_p, int top_k, float min_p, float pp,
+                                 const float* uniforms, void* work, int32_t* out, hipStream_t st);
 
 // Acceptance.
 struct AcceptArgs {

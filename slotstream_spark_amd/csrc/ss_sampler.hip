@@ -1,9 +1,9 @@
-// The reference sampler on the device: Sampler.next (engine/sampler.py:76-108) over one row of logits.
+// The reference sampler on the device: Sampler.next (engine/sampler.py:76-108) over rows of logits.
 //
 // The steps and their float32 operations are the reference's, in its order: presence penalty on the raw logits
 // (:80-82), argmax at temperature <= 0 (:83-84), division by the temperature (:85), the top-k threshold (:86-88),
 // softmax (:89, :67-69), top-p (:90-97), min-p (:98-100) and the inverse-CDF draw with the caller's uniform
-// (:101-108). The parameters arrive sanitized (SampleParams.sanitized, :45-64) and the uniform from the sampler's
+// (:101-108). The parameters arrive sanitized (SampleParams.sanitized, :45-64) and the uniforms from the sampler's
 // splitmix64 stream, both on the host. The order of every sum is defined here (the reference's comes from numpy):
 //   * z, the top-p mass and the final total are hierarchical sums: a sub-chunk of 16 entries summed sequentially
 //     from 0, the 64 sub-chunk totals of a 1024-entry chunk by the xor butterfly, the chunk totals sequentially;
@@ -14,6 +14,14 @@
 //   * the draw takes the first entry whose hierarchical running sum reaches u * total (u == 0: exceeds 0),
 //     chunk, then sub-chunk, then entry, each level falling back to the last nonzero one.
 // exp is ss_expf. A total that is not finite and > 0 falls back to the argmax of the raw logits (:105-106).
+// Entries below the top-k threshold get weight exactly 0 (exp(-inf - m) = 0 for finite m; when m is not finite the
+// total is NaN whatever the masked weights are, and the draw takes the fallback).
+//
+// Every launch covers R rows at once (blockIdx.y). Accept mode is the sampled verify round of _mtp_decode
+// (engine/generate.py:208-229) over D+1 rows: row i is reached only if rows 0..i-1 drew their drafts, so its
+// penalty set is seen + drafts[0..i) and all rows are drawn together; a last one-wave kernel walks the rows in
+// order (a non-finite row ends the round without a draw, :210-212; the round goes on while the token equals the
+// draft). The launch sequence depends only on the parameters, so it can be captured in a graph.
 #include "ss_common.hpp"
 #include "ss_launch.hpp"
 
@@ -25,8 +33,11 @@ constexpr int kSub = 16;
 constexpr int kChunk = 64 * kSub;
 constexpr int kPerLane = 16;  // chunk arrays of up to 1024 chunks (V <= 2^20)
 constexpr int kRhoBits = 52;  // 32 key bits above 20 index bits
+constexpr int kRounds = kRhoBits / 4;
+constexpr int kFlagNonfinite = 1, kFlagBadDraft = 2, kFlagFallback = 8;
 
 SS_DEV bool is_nan(float v) { return v != v; }
+SS_DEV bool is_finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
 
 // NaN-largest order-preserving key with -0 == +0 (the order np.sort gives :87).
 SS_DEV uint32_t nkey(float v) { return is_nan(v) ? 0xFFFFFFFFu : ss_key(v == 0.f ? 0.f : v); }
@@ -38,55 +49,80 @@ SS_DEV uint64_t rho_of(float p, int j) {
 // argmax key: the first maximum, NaN counting as the largest (np.argmax).
 SS_DEV uint64_t amax_key(float v, int j) { return ((uint64_t)nkey(v) << 32) | (0xFFFFFFFFu - (uint32_t)j); }
 
-struct SW {  // workspace views
-  float* L;        // [V] logits after penalty / temperature / top-k mask
-  float* P;        // [V] probabilities, then the final weights
-  float* cmax;     // [nch]
-  int* cnan;       // [nch]
-  uint64_t* ckey;  // [nch] argmax keys of the penalized logits
-  uint64_t* craw;  // [nch] argmax keys of the raw logits
-  float* ctot;     // [nch]
-  float* tsum;     // [16][nch]
-  float* stot;     // [nch][64]
-  float* state;    // [16]: 0 kth, 1 pmax, 2..3 r* (u64), 4 total
+// Byte offsets of one row's workspace; rows follow each other `bytes` apart.
+struct Layout {
+  size_t L, P, cmax, cnan, ckey, craw, cbad, etot, ftot, tsum, stot, hist, rr, res, bytes;
 };
 
-SS_DEV SW sw_of(void* w, int V, int nch) {
-  SW s;
-  uint8_t* b = static_cast<uint8_t*>(w);
-  auto take = [&](size_t bytes) {
-    uint8_t* p = b;
-    b += (bytes + 255) & ~(size_t)255;
+__host__ __device__ inline Layout layout_of(int V, int nch) {
+  Layout l{};
+  size_t o = 0;
+  auto take = [&o](size_t b) {
+    const size_t p = o;
+    o += (b + 255) & ~(size_t)255;
     return p;
   };
-  s.L = reinterpret_cast<float*>(take((size_t)V * 4));
-  s.P = reinterpret_cast<float*>(take((size_t)V * 4));
-  s.cmax = reinterpret_cast<float*>(take((size_t)nch * 4));
-  s.cnan = reinterpret_cast<int*>(take((size_t)nch * 4));
-  s.ckey = reinterpret_cast<uint64_t*>(take((size_t)nch * 8));
-  s.craw = reinterpret_cast<uint64_t*>(take((size_t)nch * 8));
-  s.ctot = reinterpret_cast<float*>(take((size_t)nch * 4));
-  s.tsum = reinterpret_cast<float*>(take((size_t)16 * nch * 4));
-  s.stot = reinterpret_cast<float*>(take((size_t)64 * nch * 4));
-  s.state = reinterpret_cast<float*>(take(64));
+  l.L = take((size_t)V * 4);                // logits after penalty and temperature
+  l.P = take((size_t)V * 4);                // exp, then probabilities, then the final weights
+  l.cmax = take((size_t)nch * 4);           // chunk maxima of the logits, later of the kept probabilities
+  l.cnan = take((size_t)nch * 4);
+  l.ckey = take((size_t)nch * 8);           // argmax keys of the penalized logits
+  l.craw = take((size_t)nch * 8);           // argmax keys of the raw logits
+  l.cbad = take((size_t)nch * 4);           // chunk holds a non-finite raw logit
+  l.etot = take((size_t)nch * 4);           // chunk totals of exp
+  l.ftot = take((size_t)nch * 4);           // chunk totals of the final weights
+  l.tsum = take((size_t)2 * 16 * nch * 4);  // top-p candidate masses, two rounds alternating
+  l.stot = take((size_t)64 * nch * 4);      // sub-chunk totals of the final weights
+  l.hist = take(4 * 256 * 4);               // top-k radix histograms, one per 8-bit pass
+  l.rr = take((size_t)(kRounds + 1) * 8);   // top-p prefix at the start of each round
+  l.res = take(16);                         // token, fallback flag, non-finite row
+  l.bytes = o;
+  return l;
+}
+
+struct SW {
+  float *L, *P, *cmax;
+  int* cnan;
+  uint64_t *ckey, *craw;
+  int* cbad;
+  float *etot, *ftot, *tsum, *stot;
+  int* hist;
+  uint64_t* rr;
+  int* res;
+};
+
+SS_DEV SW sw_of(void* work, int V, int nch, int row) {
+  const Layout l = layout_of(V, nch);
+  uint8_t* b = static_cast<uint8_t*>(work) + (size_t)row * l.bytes;
+  SW s;
+  s.L = reinterpret_cast<float*>(b + l.L);
+  s.P = reinterpret_cast<float*>(b + l.P);
+  s.cmax = reinterpret_cast<float*>(b + l.cmax);
+  s.cnan = reinterpret_cast<int*>(b + l.cnan);
+  s.ckey = reinterpret_cast<uint64_t*>(b + l.ckey);
+  s.craw = reinterpret_cast<uint64_t*>(b + l.craw);
+  s.cbad = reinterpret_cast<int*>(b + l.cbad);
+  s.etot = reinterpret_cast<float*>(b + l.etot);
+  s.ftot = reinterpret_cast<float*>(b + l.ftot);
+  s.tsum = reinterpret_cast<float*>(b + l.tsum);
+  s.stot = reinterpret_cast<float*>(b + l.stot);
+  s.hist = reinterpret_cast<int*>(b + l.hist);
+  s.rr = reinterpret_cast<uint64_t*>(b + l.rr);
+  s.res = reinterpret_cast<int*>(b + l.res);
   return s;
 }
 
-size_t sw_bytes(int V, int nch) {
-  auto r = [](size_t b) { return (b + 255) & ~(size_t)255; };
-  return r((size_t)V * 4) * 2 + r((size_t)nch * 4) * 3 + r((size_t)nch * 8) * 2 + r((size_t)16 * nch * 4) +
-         r((size_t)64 * nch * 4) + r(64);
-}
-
 struct SampArgs {
-  const float* x;
-  int V, nch;
-  const int32_t* gen;
+  const float* x;  // [R, V]
+  int V, nch, R;
+  const int32_t* gen;  // sorted penalty set
   int n_gen;
+  const int32_t* drafts;  // accept mode: [R - 1]; row i also penalizes drafts[0..i)
   float temperature, top_p, min_p, pp;
   int top_k;
-  const float* u;
-  int32_t* out;
+  const float* u;  // [R]
+  int32_t* out;    // single row: [2] (token, flags); accept mode: [R + 4]
+  int accept;
   void* work;
 };
 
@@ -102,6 +138,14 @@ SS_DEV bool in_sorted(const int32_t* g, int n, int j) {
   return false;
 }
 
+SS_DEV bool penalized(const SampArgs& a, int row, int j) {
+  if (a.pp == 0.f) return false;
+  if (a.n_gen > 0 && in_sorted(a.gen, a.n_gen, j)) return true;
+  for (int k = 0; k < row; ++k)
+    if (a.drafts[k] == j) return true;
+  return false;
+}
+
 // Chunk c's hierarchical total of the lane values v[i] (entries c*1024 + 16*lane + i): sequential per lane, then
 // the butterfly; `sub` receives the lane's sub-chunk total.
 SS_DEV float chunk_sum(const float (&v)[kSub], float& sub) {
@@ -112,19 +156,26 @@ SS_DEV float chunk_sum(const float (&v)[kSub], float& sub) {
   return ss_wave_sum(s);
 }
 
-// Every lane: ((a[0] + a[1]) + ...) + a[n-1] of a chunk array, from the lanes' registers (entry c in lane c % 64).
-SS_DEV float seq_sum(const float* a, int n) {
+// Stages a chunk array [n <= 1024] in LDS for the sequential scans below (one wave, every lane).
+SS_DEV const float* stage(const float* a, int n) {
+  __shared__ float buf[kPerLane * 64];
   const int lane = threadIdx.x & 63;
   float v[kPerLane];
 #pragma unroll
   for (int k = 0; k < kPerLane; ++k) v[k] = lane + 64 * k < n ? a[lane + 64 * k] : 0.f;
-  float s = 0.f;
 #pragma unroll
-  for (int k = 0; k < kPerLane; ++k) {
-    if (64 * k >= n) break;
-    const int m = n - 64 * k < 64 ? n - 64 * k : 64;
-    for (int l = 0; l < m; ++l) s = s + ss_readlane_f(v[k], l);
-  }
+  for (int k = 0; k < kPerLane; ++k)
+    if (lane + 64 * k < n) buf[lane + 64 * k] = v[k];
+  __syncthreads();
+  return buf;
+}
+
+// Every lane: ((a[0] + a[1]) + ...) + a[n-1] of a chunk array.
+SS_DEV float seq_sum(const float* a, int n) {
+  const float* b = stage(a, n);
+  float s = 0.f;
+#pragma unroll 8
+  for (int q = 0; q < n; ++q) s = s + b[q];
   return s;
 }
 
@@ -137,220 +188,297 @@ SS_DEV uint64_t max_u64_of(const uint64_t* a, int n) {
   return ss_wave_max_u64(m);
 }
 
-}  // namespace
-
-// 1. penalty and temperature; argmax keys of the penalized and of the raw logits.
-__global__ __launch_bounds__(64) void samp_prep_kernel(SampArgs a) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int c = blockIdx.x, lane = threadIdx.x;
-  uint64_t kp = 0, kr = 0;
-  for (int i = 0; i < kSub; ++i) {
-    const int j = c * kChunk + i * 64 + lane;
-    if (j >= a.V) break;
-    const float x = a.x[j];
-    float l = (a.pp != 0.f && a.n_gen > 0 && in_sorted(a.gen, a.n_gen, j)) ? x - a.pp : x;
-    const uint64_t k1 = amax_key(l, j), k2 = amax_key(x, j);
-    kp = k1 > kp ? k1 : kp;
-    kr = k2 > kr ? k2 : kr;
-    if (a.temperature > 0.f) l = l / a.temperature;
-    w.L[j] = l;
-  }
-  kp = ss_wave_max_u64(kp);
-  kr = ss_wave_max_u64(kr);
-  if (lane == 0) {
-    w.ckey[c] = kp;
-    w.craw[c] = kr;
-  }
-}
-
-// Temperature <= 0: the argmax of the penalized logits.
-__global__ __launch_bounds__(64) void samp_argmax_kernel(SampArgs a) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const uint64_t k = max_u64_of(w.ckey, a.nch);
-  if (threadIdx.x == 0) {
-    a.out[0] = (int32_t)(0xFFFFFFFFu - (uint32_t)k);
-    a.out[1] = 0;
-  }
-}
-
-// 2. top-k threshold: the top_k-th largest NaN-largest key (counting multiplicity), by a radix select over the
-// row, 8 bits per pass; state[0] = its value.
-__global__ __launch_bounds__(1024) void samp_kth_kernel(SampArgs a) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  __shared__ int hist[256];
-  __shared__ uint32_t s_prefix;
-  __shared__ int s_need;
-  const int tid = threadIdx.x;
-  if (tid == 0) {
-    s_prefix = 0;
-    s_need = a.top_k;
-  }
-  for (int pass = 0; pass < 4; ++pass) {
-    const int shift = 24 - 8 * pass;
-    for (int i = tid; i < 256; i += 1024) hist[i] = 0;
-    __syncthreads();
-    const uint32_t prefix = s_prefix;
-    const uint32_t hmask = pass == 0 ? 0u : (0xFFFFFFFFu << (shift + 8));
-    for (int j = tid; j < a.V; j += 1024) {
-      const uint32_t k = nkey(w.L[j]);
-      if ((k & hmask) == prefix) atomicAdd(&hist[(k >> shift) & 255], 1);  // integer counts: order-free
-    }
-    __syncthreads();
-    if (tid == 0) {
-      int need = s_need, b = 255;
-      for (; b > 0; --b) {
-        if (hist[b] >= need) break;
-        need -= hist[b];
-      }
-      s_need = need;
-      s_prefix = prefix | ((uint32_t)b << shift);
-    }
-    __syncthreads();
-  }
-  if (tid == 0) {
-    const uint32_t k = s_prefix;
-    w.state[0] = k == 0xFFFFFFFFu ? __uint_as_float(0x7FC00000u) : ss_unkey(k);
-  }
-}
-
-// 3. top-k mask (when has_k) and the chunk maxima / NaN flags of the masked logits.
-__global__ __launch_bounds__(64) void samp_max_kernel(SampArgs a, int has_k) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int c = blockIdx.x, lane = threadIdx.x;
-  const float kth = has_k ? w.state[0] : 0.f;
-  float m = -__builtin_inff();
-  int nan = 0;
-  for (int i = 0; i < kSub; ++i) {
-    const int j = c * kChunk + i * 64 + lane;
-    if (j >= a.V) break;
-    float l = w.L[j];
-    if (has_k && l < kth) {
-      l = -__builtin_inff();
-      w.L[j] = l;
-    }
-    nan |= is_nan(l);
-    m = fmaxf(m, l);
-  }
-  m = ss_wave_max(m);
-  nan = (int)ss_wave_or((uint32_t)nan);
-  if (lane == 0) {
-    w.cmax[c] = m;
-    w.cnan[c] = nan;
-  }
-}
-
-// 4. e = exp(l - m) into P and the chunk totals (m = NaN when any logit is NaN, as numpy's max).
-__global__ __launch_bounds__(64) void samp_exp_kernel(SampArgs a) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int c = blockIdx.x, lane = threadIdx.x;
+// Every lane: the logits' maximum over the chunk maxima (NaN when any chunk holds a NaN, as numpy's max).
+SS_DEV float row_max(const SW& w, int nch) {
+  const int lane = threadIdx.x & 63;
   float m = -__builtin_inff();
   uint32_t nan = 0;
 #pragma unroll
   for (int k = 0; k < kPerLane; ++k) {
     const int q = lane + 64 * k;
-    if (q < a.nch) {
+    if (q < nch) {
       m = fmaxf(m, w.cmax[q]);
       nan |= (uint32_t)w.cnan[q];
     }
   }
   m = ss_wave_max(m);
-  if (ss_wave_or(nan)) m = __uint_as_float(0x7FC00000u);
+  return ss_wave_or(nan) ? __uint_as_float(0x7FC00000u) : m;
+}
+
+// One 8-bit radix step of the top-k select, whole wave: the bin of the need-th largest key among those counted in
+// `hist` (bins descending, counting multiplicity); need becomes its rank inside the bin. Every lane gets the same.
+SS_DEV void select_pass(const int* hist, int& need, uint32_t& prefix, int shift) {
+  const int lane = threadIdx.x & 63;
+  int h[4], s = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    h[q] = hist[255 - 4 * lane - q];
+    s += h[q];
+  }
+  int incl = s;  // inclusive prefix over lanes = count of keys in bins >= 252 - 4 * lane
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int t = __shfl_up(incl, off);
+    if (lane >= off) incl += t;
+  }
+  const int above = incl - s;
+  const bool mine = above < need && need <= incl;
+  const uint64_t bal = __ballot(mine);
+  const int src = bal ? (int)__builtin_ctzll(bal) : 0;
+  int b = 0, nn = need - above;
+  if (mine) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (h[q] >= nn) {
+        b = 255 - 4 * lane - q;
+        break;
+      }
+      nn -= h[q];
+    }
+  }
+  b = __shfl(b, src);
+  nn = __shfl(nn, src);
+  need = nn;
+  prefix |= (uint32_t)b << shift;
+}
+
+// One wave: the 4-bit top-p digit of a round from its candidate masses (lane d sums candidate d's chunk totals in
+// chunk order): the smallest d whose mass is below top_p (candidate 15 always is: it is the previous round's bound).
+// All lanes stage the masses in LDS first, so the loads are in flight together.
+SS_DEV int topp_digit(const float* tsum, int nch, float top_p) {
+  constexpr int B = 32;
+  __shared__ float tb[16 * kPerLane * 64];
+  const int lane = threadIdx.x & 63;
+  const int n = 16 * nch;
+  for (int i0 = 0; i0 < n; i0 += 64 * B) {
+    float v[B];
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+      const int idx = i0 + 64 * q + lane;
+      v[q] = idx < n ? tsum[idx] : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < B; ++q) {
+      const int idx = i0 + 64 * q + lane;
+      if (idx < n) tb[idx] = v[q];
+    }
+  }
+  __syncthreads();
+  const float* t = tb + (lane & 15) * nch;
+  float cum = 0.f;
+#pragma unroll 8
+  for (int c = 0; c < nch; ++c) cum = cum + t[c];
+  const uint64_t ok = __ballot(lane < 16 && cum < top_p);
+  return ok ? (int)__builtin_ctzll(ok) : 15;
+}
+
+}  // namespace
+
+// Clears the top-k histograms of every row.
+__global__ __launch_bounds__(256) void samp_begin_kernel(SampArgs a) {
+  SW w = sw_of(a.work, a.V, a.nch, blockIdx.x);
+  for (int i = threadIdx.x; i < 4 * 256; i += 256) w.hist[i] = 0;
+}
+
+// 1. penalty and temperature into L; argmax keys of the penalized and of the raw logits; non-finite flags; chunk
+// maxima; (has_k) the first top-k histogram (top 8 key bits).
+__global__ __launch_bounds__(64) void samp_prep_kernel(SampArgs a, int has_k) {
+  const int c = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  SW w = sw_of(a.work, a.V, a.nch, row);
+  const float* x = a.x + (size_t)row * a.V;
+  __shared__ int hist[256];
+  if (has_k) {
+    for (int i = lane; i < 256; i += 64) hist[i] = 0;
+    __syncthreads();
+  }
+  float xv[kSub];
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + lane * kSub + i;
+    xv[i] = j < a.V ? x[j] : 0.f;
+  }
+  const bool sampled = a.temperature > 0.f;
+  uint64_t kp = 0, kr = 0;
+  uint32_t bad = 0, nan = 0;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + lane * kSub + i;
+    if (j < a.V) {
+      const float xx = xv[i];
+      bad |= !is_finite(xx);
+      float l = penalized(a, row, j) ? xx - a.pp : xx;
+      const uint64_t k1 = amax_key(l, j), k2 = amax_key(xx, j);
+      kp = k1 > kp ? k1 : kp;
+      kr = k2 > kr ? k2 : kr;
+      if (sampled) {
+        l = l / a.temperature;
+        w.L[j] = l;
+        m = fmaxf(m, l);
+        nan |= is_nan(l);
+        if (has_k) atomicAdd(&hist[nkey(l) >> 24], 1);  // integer counts: order-free
+      }
+    }
+  }
+  kp = ss_wave_max_u64(kp);
+  kr = ss_wave_max_u64(kr);
+  bad = ss_wave_or(bad);
+  nan = ss_wave_or(nan);
+  m = ss_wave_max(m);
+  if (lane == 0) {
+    w.ckey[c] = kp;
+    w.craw[c] = kr;
+    w.cbad[c] = (int)bad;
+    w.cmax[c] = m;
+    w.cnan[c] = (int)nan;
+  }
+  if (has_k) {
+    __syncthreads();
+    for (int b = lane; b < 256; b += 64)
+      if (hist[b]) atomicAdd(&w.hist[b], hist[b]);
+  }
+}
+
+// 2. top-k histogram pass 1..3: keys matching the prefix the earlier passes selected, next 8 bits.
+__global__ __launch_bounds__(64) void samp_hist_kernel(SampArgs a, int pass) {
+  const int c = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  SW w = sw_of(a.work, a.V, a.nch, row);
+  __shared__ int hist[256];
+  for (int i = lane; i < 256; i += 64) hist[i] = 0;
+  int need = a.top_k;
+  uint32_t prefix = 0;
+  for (int p = 0; p < pass; ++p) select_pass(w.hist + 256 * p, need, prefix, 24 - 8 * p);
+  const int shift = 24 - 8 * pass;
+  const uint32_t hmask = 0xFFFFFFFFu << (shift + 8);
+  float lv[kSub];
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + lane * kSub + i;
+    lv[i] = j < a.V ? w.L[j] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + lane * kSub + i;
+    const uint32_t k = nkey(lv[i]);
+    if (j < a.V && (k & hmask) == prefix) atomicAdd(&hist[(k >> shift) & 255], 1);
+  }
+  __syncthreads();
+  for (int b = lane; b < 256; b += 64)
+    if (hist[b]) atomicAdd(&w.hist[256 * pass + b], hist[b]);
+}
+
+// 3. e = exp(l - m) into P (0 below the top-k threshold) and the chunk totals.
+__global__ __launch_bounds__(64) void samp_exp_kernel(SampArgs a, int has_k) {
+  const int c = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  SW w = sw_of(a.work, a.V, a.nch, row);
+  float kth = -__builtin_inff();
+  if (has_k) {
+    int need = a.top_k;
+    uint32_t prefix = 0;
+    for (int p = 0; p < 4; ++p) select_pass(w.hist + 256 * p, need, prefix, 24 - 8 * p);
+    kth = prefix == 0xFFFFFFFFu ? __uint_as_float(0x7FC00000u) : ss_unkey(prefix);
+  }
+  const float m = row_max(w, a.nch);
   float v[kSub];
 #pragma unroll
   for (int i = 0; i < kSub; ++i) {
     const int j = c * kChunk + lane * kSub + i;
-    v[i] = j < a.V ? ss_expf(w.L[j] - m) : 0.f;
+    const float l = j < a.V ? w.L[j] : 0.f;
+    v[i] = j < a.V ? (l < kth ? 0.f : ss_expf(l - m)) : 0.f;
     if (j < a.V) w.P[j] = v[i];
   }
   float sub;
   const float t = chunk_sum(v, sub);
-  if (lane == 0) w.ctot[c] = t;
+  if (lane == 0) w.etot[c] = t;
 }
 
-// 5. p = e / z.
-__global__ __launch_bounds__(64) void samp_norm_kernel(SampArgs a) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int c = blockIdx.x, lane = threadIdx.x;
-  const float z = seq_sum(w.ctot, a.nch);
+// 4. top-p round k: fold the previous round's digit into the prefix r, then chunk c's hierarchical masses of p over
+// rho > r | d << s | (2^s - 1), d = 0..15. Round 0 also normalizes p = e / z.
+__global__ __launch_bounds__(64) void samp_topp_kernel(SampArgs a, int round) {
+  const int c = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  SW w = sw_of(a.work, a.V, a.nch, row);
+  const int nch = a.nch;
+  const int s = kRhoBits - 4 - 4 * round;
+  float pv[kSub];
+#pragma unroll
   for (int i = 0; i < kSub; ++i) {
-    const int j = c * kChunk + i * 64 + lane;
-    if (j < a.V) w.P[j] = w.P[j] / z;
+    const int j = c * kChunk + lane * kSub + i;
+    pv[i] = j < a.V ? w.P[j] : 0.f;
   }
-}
-
-// 6. r* = 0 before the top-p rounds (a kernel, not a memset, so the launch sequence is safe to capture).
-__global__ void samp_zero_r_kernel(SampArgs a) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  if (threadIdx.x == 0) *reinterpret_cast<uint64_t*>(w.state + 2) = 0;
-}
-
-// 6a. top-p round: chunk c's hierarchical totals of p over rho > r | d << s | (2^s - 1), d = 0..15.
-__global__ __launch_bounds__(64) void samp_topp_sums_kernel(SampArgs a, int s) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int c = blockIdx.x, lane = threadIdx.x;
-  const uint64_t r = *reinterpret_cast<const uint64_t*>(w.state + 2);
-  const uint64_t ones = ((uint64_t)1 << s) - 1;
+  uint64_t r = 0;
+  if (round > 0)
+    r = w.rr[round - 1] | ((uint64_t)topp_digit(w.tsum + ((round - 1) & 1) * 16 * nch, nch, a.top_p) << (s + 4));
+  if (c == 0 && lane == 0) w.rr[round] = r;
+  if (round == 0) {
+    const float z = seq_sum(w.etot, nch);
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) {
+      const int j = c * kChunk + lane * kSub + i;
+      pv[i] = pv[i] / z;
+      if (j < a.V) w.P[j] = pv[i];
+    }
+  }
+  // rho > r | d << s | (2^s - 1) holds for every d when rho is above r in the bits over the round's digit, and for
+  // d < t when those bits equal r's and t is rho's digit; p = 0 adds nothing, so zero entries are skipped.
+  const uint64_t r_hi = r >> (s + 4);
   float acc[16];
 #pragma unroll
   for (int d = 0; d < 16; ++d) acc[d] = 0.f;
 #pragma unroll
   for (int i = 0; i < kSub; ++i) {
     const int j = c * kChunk + lane * kSub + i;
-    const float p = j < a.V ? w.P[j] : 0.f;
-    const uint64_t rho = j < a.V ? rho_of(p, j) : 0;
+    const float p = pv[i];
+    if (j < a.V && p != 0.f) {
+      const uint64_t rho = rho_of(p, j);
+      const uint64_t hi = rho >> (s + 4);
+      const int lim = hi > r_hi ? 16 : (hi == r_hi ? (int)((rho >> s) & 15) : 0);
 #pragma unroll
-    for (int d = 0; d < 16; ++d) {
-      const uint64_t hi = r | ((uint64_t)d << s) | ones;
-      acc[d] = acc[d] + (rho > hi ? p : 0.f);
+      for (int d = 0; d < 16; ++d) acc[d] = acc[d] + (d < lim ? p : 0.f);
     }
   }
+  float* out = w.tsum + (round & 1) * 16 * nch;
 #pragma unroll
   for (int d = 0; d < 16; ++d) {
     const float t = ss_wave_sum(acc[d]);
-    if (lane == 0) w.tsum[d * a.nch + c] = t;
+    if (lane == 0) out[d * nch + c] = t;
   }
 }
 
-// 6b. top-p round: lane d sums candidate d's chunk totals in chunk order; the digit is the smallest d whose mass
-// is below top_p (candidate 15 always is: it is the previous round's bound).
-__global__ __launch_bounds__(64) void samp_topp_pick_kernel(SampArgs a, int s) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int lane = threadIdx.x;
-  const int d = lane < 16 ? lane : 15;
-  float cum = 0.f;
-  for (int c = 0; c < a.nch; ++c) cum = cum + w.tsum[d * a.nch + c];
-  const uint64_t ok = __ballot(lane < 16 && cum < a.top_p);
-  const int digit = ok ? (int)__builtin_ctzll(ok) : 15;
-  if (lane == 0) {
-    uint64_t* rp = reinterpret_cast<uint64_t*>(w.state + 2);
-    *rp = *rp | ((uint64_t)digit << s);
-  }
-}
-
-// 6c. keep rho >= r*; 7. (min_p > 0) chunk maxima of the kept probabilities.
-__global__ __launch_bounds__(64) void samp_keep_kernel(SampArgs a, int has_p) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int c = blockIdx.x, lane = threadIdx.x;
-  const uint64_t r = has_p ? *reinterpret_cast<const uint64_t*>(w.state + 2) : 0;
-  float m = -__builtin_inff();
+// 5. (has_p) keep rho >= r*; (min_p > 0) chunk maxima of the kept probabilities. `norm`: p = e / z here.
+__global__ __launch_bounds__(64) void samp_keep_kernel(SampArgs a, int has_p, int norm) {
+  const int c = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  SW w = sw_of(a.work, a.V, a.nch, row);
+  const int nch = a.nch;
+  float pv[kSub];
+#pragma unroll
   for (int i = 0; i < kSub; ++i) {
-    const int j = c * kChunk + i * 64 + lane;
-    if (j >= a.V) break;
-    float p = w.P[j];
-    if (has_p && !(rho_of(p, j) >= r)) {
-      p = 0.f;
-      w.P[j] = p;
+    const int j = c * kChunk + lane * kSub + i;
+    pv[i] = j < a.V ? w.P[j] : 0.f;
+  }
+  uint64_t r = 0;
+  if (has_p) r = w.rr[kRounds - 1] | (uint64_t)topp_digit(w.tsum + ((kRounds - 1) & 1) * 16 * nch, nch, a.top_p);
+  const float z = norm ? seq_sum(w.etot, nch) : 1.f;
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + lane * kSub + i;
+    if (j < a.V) {
+      float p = norm ? pv[i] / z : pv[i];
+      const bool drop = has_p && !(rho_of(p, j) >= r);
+      if (drop) p = 0.f;
+      if (drop || norm) w.P[j] = p;
+      m = fmaxf(m, p);
     }
-    m = fmaxf(m, p);
   }
   m = ss_wave_max(m);
   if (lane == 0) w.cmax[c] = m;
 }
 
-// 8. min-p cutoff (when min_p > 0) and the hierarchical totals of the final weights.
-__global__ __launch_bounds__(64) void samp_total_kernel(SampArgs a, int has_minp) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int c = blockIdx.x, lane = threadIdx.x;
+// 6. min-p cutoff (has_minp) and the hierarchical totals of the final weights. `norm`: p = e / z here.
+__global__ __launch_bounds__(64) void samp_total_kernel(SampArgs a, int has_minp, int norm) {
+  const int c = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
+  SW w = sw_of(a.work, a.V, a.nch, row);
   float cutoff = 0.f;
   if (has_minp) {
     float pm = -__builtin_inff();
@@ -359,77 +487,92 @@ __global__ __launch_bounds__(64) void samp_total_kernel(SampArgs a, int has_minp
       if (lane + 64 * k < a.nch) pm = fmaxf(pm, w.cmax[lane + 64 * k]);
     cutoff = ss_wave_max(pm) * a.min_p;
   }
+  const float z = norm ? seq_sum(w.etot, a.nch) : 1.f;
   float v[kSub];
 #pragma unroll
   for (int i = 0; i < kSub; ++i) {
     const int j = c * kChunk + lane * kSub + i;
-    float p = j < a.V ? w.P[j] : 0.f;
-    if (has_minp && p < cutoff) {
-      p = 0.f;
-      if (j < a.V) w.P[j] = p;
-    }
-    v[i] = p;
+    v[i] = j < a.V ? w.P[j] : 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + lane * kSub + i;
+    float p = norm ? v[i] / z : v[i];
+    const bool drop = has_minp && p < cutoff;
+    if (drop) p = 0.f;
+    if (j < a.V && (drop || norm)) w.P[j] = p;
+    v[i] = j < a.V ? p : 0.f;
   }
   float sub;
   const float t = chunk_sum(v, sub);
   w.stot[c * 64 + lane] = sub;
-  if (lane == 0) w.ctot[c] = t;
+  if (lane == 0) w.ftot[c] = t;
 }
 
-// 9. the draw (one wave; every lane follows the same scan).
+// 7. the draw, one wave per row (every lane follows the same scan); greedy rows take the argmax.
 __global__ __launch_bounds__(64) void samp_draw_kernel(SampArgs a) {
-  SW w = sw_of(a.work, a.V, a.nch);
-  const int lane = threadIdx.x;
+  const int row = blockIdx.x, lane = threadIdx.x;
+  SW w = sw_of(a.work, a.V, a.nch, row);
   const int nch = a.nch;
-  float v[kPerLane];
-#pragma unroll
-  for (int k = 0; k < kPerLane; ++k) v[k] = lane + 64 * k < nch ? w.ctot[lane + 64 * k] : 0.f;
-  float total = 0.f;
-#pragma unroll
-  for (int k = 0; k < kPerLane; ++k) {
-    if (64 * k >= nch) break;
-    const int m = nch - 64 * k < 64 ? nch - 64 * k : 64;
-    for (int l = 0; l < m; ++l) total = total + ss_readlane_f(v[k], l);
-  }
-  const bool finite = (__float_as_uint(total) & 0x7F800000u) != 0x7F800000u;
-  if (!finite || !(total > 0.f)) {
-    const uint64_t k = max_u64_of(w.craw, nch);
-    if (lane == 0) {
-      a.out[0] = (int32_t)(0xFFFFFFFFu - (uint32_t)k);
-      a.out[1] = 1;
+  auto finish = [&](int tok, int fb, int nonfinite) {
+    if (lane != 0) return;
+    if (a.accept) {
+      w.res[0] = tok;
+      w.res[1] = fb;
+      w.res[2] = nonfinite;
+    } else {
+      a.out[0] = tok;
+      a.out[1] = fb;
     }
+  };
+  if (a.accept) {
+    uint32_t b = 0;
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k)
+      if (lane + 64 * k < nch) b |= (uint32_t)w.cbad[lane + 64 * k];
+    if (ss_wave_or(b)) {
+      finish(-1, 0, 1);
+      return;
+    }
+  }
+  if (!(a.temperature > 0.f)) {
+    const uint64_t k = max_u64_of(w.ckey, nch);
+    finish((int)(0xFFFFFFFFu - (uint32_t)k), 0, 0);
     return;
   }
-  const float u = *a.u;
+  const float* ct = stage(w.ftot, nch);
+  float total = 0.f;
+#pragma unroll 8
+  for (int q = 0; q < nch; ++q) total = total + ct[q];
+  if (!is_finite(total) || !(total > 0.f)) {
+    const uint64_t k = max_u64_of(w.craw, nch);
+    finish((int)(0xFFFFFFFFu - (uint32_t)k), 1, 0);
+    return;
+  }
+  const float u = a.u[row];
   const bool ge = u != 0.f;
   const float target = ge ? u * total : 0.f;
   auto hit = [&](float x) { return ge ? x >= target : x > target; };
   int cs = -1, clast = -1;
   float base = 0.f, run = 0.f;
+  for (int q0 = 0; q0 < nch; q0 += 8) {
+    float t[8];
 #pragma unroll
-  for (int k = 0; k < kPerLane; ++k) {
-    if (64 * k >= nch) break;
-    const int m = nch - 64 * k < 64 ? nch - 64 * k : 64;
-    for (int l = 0; l < m; ++l) {
-      const float t = ss_readlane_f(v[k], l);
-      const float nx = run + t;
-      if (t > 0.f) clast = 64 * k + l;
-      if (cs < 0 && hit(nx)) {
-        cs = 64 * k + l;
-        base = run;
-      }
+    for (int i = 0; i < 8; ++i) t[i] = q0 + i < nch ? ct[q0 + i] : 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float nx = run + t[i];
+      const bool found = cs < 0 && hit(nx);
+      cs = found ? q0 + i : cs;
+      base = found ? run : base;
+      clast = t[i] > 0.f ? q0 + i : clast;
       run = nx;
     }
   }
   if (cs < 0) {
     cs = clast < 0 ? 0 : clast;
     base = 0.f;
-#pragma unroll
-    for (int k = 0; k < kPerLane; ++k) {
-      if (64 * k >= cs) break;
-      const int m = cs - 64 * k < 64 ? cs - 64 * k : 64;
-      for (int l = 0; l < m; ++l) base = base + ss_readlane_f(v[k], l);
-    }
+    for (int q = 0; q < cs; ++q) base = base + ct[q];
   }
   const float st = w.stot[cs * 64 + lane];
   int bs = -1, blast = -1;
@@ -467,23 +610,46 @@ __global__ __launch_bounds__(64) void samp_draw_kernel(SampArgs a) {
     }
   }
   if (pick < 0) pick = last >= 0 ? last : (j0 < a.V ? j0 : a.V - 1);
-  if (lane == 0) {
-    a.out[0] = pick;
-    a.out[1] = 0;
+  finish(pick, 0, 0);
+}
+
+// 8. accept mode: the round, walking the rows in order (n_accept, n_emit, n_uniform, flags, tokens).
+__global__ __launch_bounds__(64) void samp_decide_kernel(SampArgs a) {
+  if (threadIdx.x != 0) return;
+  const int D = a.R - 1;
+  int na = 0, ne = 0, nu = 0, fl = 0;
+  for (int i = 0; i <= D; ++i) {
+    const SW w = sw_of(a.work, a.V, a.nch, i);
+    if (w.res[2]) {
+      fl |= kFlagNonfinite;
+      break;
+    }
+    const int tok = w.res[0];
+    a.out[4 + i] = tok;
+    ne = i + 1;
+    if (a.temperature > 0.f) nu = i + 1;
+    if (w.res[1]) fl |= kFlagFallback;
+    if (i == D) break;
+    const int d = a.drafts[i];
+    if (d < 0 || d >= a.V) fl |= kFlagBadDraft;
+    if (tok != d) break;
+    na = i + 1;
   }
+  for (int i = ne; i <= D; ++i) a.out[4 + i] = -1;
+  a.out[0] = na;
+  a.out[1] = ne;
+  a.out[2] = nu;
+  a.out[3] = fl;
 }
 
-int64_t sample_workspace_bytes(int V) {
-  const int nch = (V + kChunk - 1) / kChunk;
-  return (int64_t)sw_bytes(V, nch);
-}
+namespace {
 
-hipError_t launch_sample(const float* x, int V, const int32_t* gen, int n_gen, float temperature, float top_p,
-                         int top_k, float min_p, float pp, const float* u, void* work, int32_t* out, hipStream_t st) {
+SampArgs args_of(int V, int R, const int32_t* gen, int n_gen, float temperature, float top_p, int top_k,
+                 float min_p, float pp, void* work) {
   SampArgs a{};
-  a.x = x;
   a.V = V;
   a.nch = (V + kChunk - 1) / kChunk;
+  a.R = R;
   a.gen = gen;
   a.n_gen = n_gen;
   a.temperature = temperature;
@@ -491,32 +657,61 @@ hipError_t launch_sample(const float* x, int V, const int32_t* gen, int n_gen, f
   a.top_k = top_k;
   a.min_p = min_p;
   a.pp = pp;
+  a.work = work;
+  return a;
+}
+
+// The rows' launch sequence; which kernels run depends only on the parameters.
+void launch_rows(const SampArgs& a, hipStream_t st) {
+  const dim3 g(a.nch, a.R), b(64);
+  if (!(a.temperature > 0.f)) {
+    hipLaunchKernelGGL(samp_prep_kernel, g, b, 0, st, a, 0);
+    hipLaunchKernelGGL(samp_draw_kernel, dim3(a.R), b, 0, st, a);
+    return;
+  }
+  const int has_k = a.top_k > 0 && a.top_k < a.V;
+  const int has_p = a.top_p < 1.f;
+  const int has_minp = a.min_p > 0.f;
+  if (has_k) hipLaunchKernelGGL(samp_begin_kernel, dim3(a.R), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(samp_prep_kernel, g, b, 0, st, a, has_k);
+  if (has_k)
+    for (int pass = 1; pass < 4; ++pass) hipLaunchKernelGGL(samp_hist_kernel, g, b, 0, st, a, pass);
+  hipLaunchKernelGGL(samp_exp_kernel, g, b, 0, st, a, has_k);
+  if (has_p)
+    for (int round = 0; round < kRounds; ++round) hipLaunchKernelGGL(samp_topp_kernel, g, b, 0, st, a, round);
+  if (has_p || has_minp) hipLaunchKernelGGL(samp_keep_kernel, g, b, 0, st, a, has_p, has_p ? 0 : 1);
+  hipLaunchKernelGGL(samp_total_kernel, g, b, 0, st, a, has_minp, (has_p || has_minp) ? 0 : 1);
+  hipLaunchKernelGGL(samp_draw_kernel, dim3(a.R), b, 0, st, a);
+}
+
+}  // namespace
+
+int64_t sample_workspace_bytes(int V) {
+  const int nch = (V + kChunk - 1) / kChunk;
+  return (int64_t)layout_of(V, nch).bytes;
+}
+
+hipError_t launch_sample(const float* x, int V, const int32_t* gen, int n_gen, float temperature, float top_p,
+                         int top_k, float min_p, float pp, const float* u, void* work, int32_t* out, hipStream_t st) {
+  SampArgs a = args_of(V, 1, gen, n_gen, temperature, top_p, top_k, min_p, pp, work);
+  a.x = x;
   a.u = u;
   a.out = out;
-  a.work = work;
-  const dim3 g(a.nch), b(64);
-  hipLaunchKernelGGL(samp_prep_kernel, g, b, 0, st, a);
-  if (!(temperature > 0.f)) {
-    hipLaunchKernelGGL(samp_argmax_kernel, dim3(1), b, 0, st, a);
-    return hipGetLastError();
-  }
-  const int has_k = top_k > 0 && top_k < V;
-  if (has_k) hipLaunchKernelGGL(samp_kth_kernel, dim3(1), dim3(1024), 0, st, a);
-  hipLaunchKernelGGL(samp_max_kernel, g, b, 0, st, a, has_k);
-  hipLaunchKernelGGL(samp_exp_kernel, g, b, 0, st, a);
-  hipLaunchKernelGGL(samp_norm_kernel, g, b, 0, st, a);
-  const int has_p = top_p < 1.f;
-  if (has_p) {
-    hipLaunchKernelGGL(samp_zero_r_kernel, dim3(1), dim3(64), 0, st, a);
-    for (int s = kRhoBits - 4; s >= 0; s -= 4) {
-      hipLaunchKernelGGL(samp_topp_sums_kernel, g, b, 0, st, a, s);
-      hipLaunchKernelGGL(samp_topp_pick_kernel, dim3(1), b, 0, st, a, s);
-    }
-  }
-  const int has_minp = min_p > 0.f;
-  if (has_p || has_minp) hipLaunchKernelGGL(samp_keep_kernel, g, b, 0, st, a, has_p);
-  hipLaunchKernelGGL(samp_total_kernel, g, b, 0, st, a, has_minp);
-  hipLaunchKernelGGL(samp_draw_kernel, dim3(1), b, 0, st, a);
+  launch_rows(a, st);
+  return hipGetLastError();
+}
+
+hipError_t launch_accept_sampled(const float* target, const int32_t* drafts, int D, int V, const int32_t* seen,
+                                 int n_seen, float temperature, float top_p, int top_k, float min_p, float pp,
+                                 const float* uniforms, void* work, int32_t* out, hipStream_t st) {
+  SampArgs a = args_of(V, D + 1, seen, n_seen, temperature, top_p, top_k, min_p, pp, work);
+  a.x = target;
+  a.u = uniforms;
+  a.drafts = drafts;
+  a.out = out;
+  a.accept = 1;
+  launch_rows(a, st);
+  hipLaunchKernelGGL(samp_decide_kernel, dim3(1), dim3(64), 0, st, a);
   return hipGetLastError();
 }
 

@@ -545,9 +545,9 @@ int64_t ssmoe_sample_workspace_bytes(int V) {
   return ss::sample_workspace_bytes(V);
 }
 
-int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_generated, float temperature,
-                 float top_p, int top_k, float min_p, float presence_penalty, const float* u, void* workspace,
-                 int64_t workspace_bytes, int32_t* out, void* stream) {
+static int check_sample(int V, float temperature, float top_p, int top_k, float min_p, float presence_penalty,
+                        const int32_t* generated, int n_generated, void* workspace, int64_t workspace_bytes,
+                        int64_t rows) {
   if (V < 1 || V > (1 << 20)) return fail(SSMOE_EINVAL, "V must be in [1, 1048576], got %d", V);
   if (!(temperature >= 0.f) || temperature > 3.4e38f) return fail(SSMOE_EINVAL, "temperature must be finite and >= 0");
   if (!(top_p > 0.f && top_p <= 1.f)) return fail(SSMOE_EINVAL, "top_p must be in (0, 1], got %g", (double)top_p);
@@ -557,14 +557,45 @@ int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_gen
     return fail(SSMOE_EINVAL, "presence_penalty must be finite");
   if (n_generated < 0 || (n_generated > 0 && !generated))
     return fail(SSMOE_EINVAL, "generated must hold n_generated >= 0 token ids");
-  if (!logits || !u || !workspace || !out) return fail(SSMOE_EINVAL, "logits, u, workspace and out must be non-null");
+  if (!workspace) return fail(SSMOE_EINVAL, "workspace must be non-null");
   if (!aligned(workspace, 256)) return fail(SSMOE_EINVAL, "workspace must be 256-byte aligned");
-  if (workspace_bytes < ss::sample_workspace_bytes(V))
+  if (workspace_bytes < rows * ss::sample_workspace_bytes(V))
     return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
-                (long long)ss::sample_workspace_bytes(V));
+                (long long)(rows * ss::sample_workspace_bytes(V)));
+  return ok();
+}
+
+int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_generated, float temperature,
+                 float top_p, int top_k, float min_p, float presence_penalty, const float* u, void* workspace,
+                 int64_t workspace_bytes, int32_t* out, void* stream) {
+  if (int rc = check_sample(V, temperature, top_p, top_k, min_p, presence_penalty, generated, n_generated, workspace,
+                            workspace_bytes, 1))
+    return rc;
+  if (!logits || !u || !out) return fail(SSMOE_EINVAL, "logits, u and out must be non-null");
   return hip_check(ss::launch_sample(logits, V, generated, n_generated, temperature, top_p, top_k, min_p,
                                      presence_penalty, u, workspace, out, static_cast<hipStream_t>(stream)),
                    "sample launch");
+}
+
+int64_t ssmoe_accept_sampled_workspace_bytes(int D, int V) {
+  if (D < 0 || D > 60 || V < 1 || V > (1 << 20)) return -1;
+  return (int64_t)(D + 1) * ss::sample_workspace_bytes(V);
+}
+
+int ssmoe_accept_sampled(const float* target, const int32_t* drafts, int D, int V, const int32_t* seen, int n_seen,
+                         float temperature, float top_p, int top_k, float min_p, float presence_penalty,
+                         const float* uniforms, void* workspace, int64_t workspace_bytes, int32_t* out,
+                         void* stream) {
+  if (D < 0 || D > 60) return fail(SSMOE_EINVAL, "D must be in [0, 60], got %d", D);
+  if (int rc = check_sample(V, temperature, top_p, top_k, min_p, presence_penalty, seen, n_seen, workspace,
+                            workspace_bytes, D + 1))
+    return rc;
+  if (!target || !uniforms || !out || (D > 0 && !drafts))
+    return fail(SSMOE_EINVAL, "target, drafts, uniforms and out must be non-null");
+  return hip_check(ss::launch_accept_sampled(target, drafts, D, V, seen, n_seen, temperature, top_p, top_k, min_p,
+                                             presence_penalty, uniforms, workspace, out,
+                                             static_cast<hipStream_t>(stream)),
+                   "accept sampled launch");
 }
 
 }  // extern "C"

@@ -3,7 +3,9 @@
 Greedy follows the acceptance loop of _mtp_decode (slotstream_spark/engine/generate.py:208-229) at temperature 0
 (Sampler.next -> np.argmax, engine/sampler.py:83-84): row i's token is the first maximum of its logits; the round
 accepts drafts while they equal those tokens and emits tokens 0..good; a row holding a non-finite logit stops the
-round before it (generate.py:210-212). p/q is Leviathan et al. 2023, Alg. 1, which the reference does not have.
+round before it (generate.py:210-212). `sampled` is the same loop with the full reference sampler (temperature,
+top-k, top-p, min-p, presence penalty over the tokens seen so far). p/q is Leviathan et al. 2023, Alg. 1, which the
+reference does not have.
 
 The uniforms come from the reference sampler's splitmix64 stream (engine/sampler.py:20-24, 101-102), drawn on the
 host: decision i consumes uniforms[i], the final sample the next one; `n_uniform` reports how many were used, so
@@ -18,7 +20,7 @@ import torch
 
 from .. import _lib
 
-FLAG_NONFINITE, FLAG_BAD_DRAFT, FLAG_RESIDUAL_EMPTY = 1, 2, 4
+FLAG_NONFINITE, FLAG_BAD_DRAFT, FLAG_RESIDUAL_EMPTY, FLAG_FALLBACK = 1, 2, 4, 8
 
 _M64 = (1 << 64) - 1
 
@@ -71,6 +73,7 @@ class Acceptor:
         nb = _lib.lib().ssmoe_accept_workspace_bytes(depth, vocab)
         self.work = torch.empty(int(nb), dtype=torch.uint8, device=device)
         self.out = torch.empty(depth + 5, dtype=torch.int32, device=device)
+        self._swork = None
 
     def _check(self, target, draft=None):
         d, v = self.depth, self.vocab
@@ -103,6 +106,36 @@ class Acceptor:
                                               self.work.data_ptr(), self.work.numel(), self.out.data_ptr(),
                                               _lib.stream_of(target)))
         return self.out
+
+    def sampled_async(self, target, drafts, params, seen=(), uniforms=None) -> torch.Tensor:
+        """Launch the sampled round; returns the device output int32 [D+5]. `params` is a SampleParams (sanitized
+        here), `seen` the tokens generated before the round, `uniforms` fp32 [D+1] on the device."""
+        self._check(target)
+        if drafts.dtype != torch.int32 or drafts.numel() != self.depth:
+            raise ValueError(f"drafts must be int32 [{self.depth}]")
+        if uniforms is None or uniforms.dtype != torch.float32 or uniforms.numel() != self.depth + 1:
+            raise ValueError(f"uniforms must be fp32 [{self.depth + 1}]")
+        p = params.sanitized()
+        if self._swork is None:
+            nb = int(_lib.lib().ssmoe_accept_sampled_workspace_bytes(self.depth, self.vocab))
+            self._swork = torch.empty(nb, dtype=torch.uint8, device=target.device)
+        s = sorted(set(int(t) for t in seen)) if p.presence_penalty != 0 else []
+        st = torch.tensor(s, dtype=torch.int32, device=target.device) if s else None
+        _lib.check(_lib.lib().ssmoe_accept_sampled(
+            target.data_ptr(), drafts.data_ptr(), self.depth, self.vocab, _lib.ptr(st), len(s), float(p.temperature),
+            float(p.top_p), int(p.top_k), float(p.min_p), float(p.presence_penalty), uniforms.data_ptr(),
+            self._swork.data_ptr(), self._swork.numel(), self.out.data_ptr(), _lib.stream_of(target)))
+        return self.out
+
+    def sampled(self, target, drafts, params, seen, stream: UniformStream) -> AcceptResult:
+        """One sampled round with the sampler's stream: consumes one uniform per draw at temperature > 0, as
+        Sampler.next does, and adds the emitted tokens to `seen` when it is a set (generate.py:214)."""
+        u = torch.from_numpy(stream.peek(self.depth + 1)).to(target.device)
+        res = AcceptResult.from_out(self.sampled_async(target, drafts, params, seen, u).cpu())
+        stream.advance(res.n_uniform)
+        if isinstance(seen, set):
+            seen.update(res.tokens)
+        return res
 
     def greedy(self, target, drafts) -> AcceptResult:
         return AcceptResult.from_out(self.greedy_async(target, drafts).cpu())

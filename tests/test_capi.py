@@ -187,3 +187,20 @@ def test_sample_rejects_bad_arguments(L):
     assert call(n=3) == EINVAL and b"generated" in L.ssmoe_last_error()
     assert call(w=ws - 1) == EINVAL and b"workspace holds" in L.ssmoe_last_error()
     assert call(V=0) == EINVAL
+
+
+def test_accept_sampled_rejects_bad_arguments(L):
+    p = ctypes.c_void_p(4096)
+    ws = L.ssmoe_accept_sampled_workspace_bytes(3, 1000)
+    assert ws == 4 * L.ssmoe_sample_workspace_bytes(1000) and L.ssmoe_accept_sampled_workspace_bytes(61, 1000) == -1
+
+    def call(D=3, V=1000, drafts=p, t=0.8, tp=0.9, w=ws):
+        return L.ssmoe_accept_sampled(p, drafts, D, V, None, 0, t, tp, 40, 0.0, 0.0, p, ctypes.c_void_p(4096), w,
+                                      p, None)
+    assert call(D=61) == EINVAL and b"D must be" in L.ssmoe_last_error()
+    assert call(D=-1) == EINVAL
+    assert call(drafts=None) == EINVAL and b"non-null" in L.ssmoe_last_error()
+    assert call(t=-0.5) == EINVAL and b"temperature" in L.ssmoe_last_error()
+    assert call(tp=2.0) == EINVAL
+    assert call(w=ws - 256) == EINVAL and b"workspace holds" in L.ssmoe_last_error()
+    assert call(V=(1 << 20) + 1) == EINVAL

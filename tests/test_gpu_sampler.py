@@ -103,3 +103,76 @@ def test_sampler_api_advances_like_the_reference():
             gen.add(t)
     want = replay_sampler_case(case, x, lambda l, g, *a: O.sample(l, g, *a)[0])
     assert toks == want
+
+
+# ---- the sampled verify round on the device (ssmoe_accept_sampled) against oracle.accept_sampled
+
+def _self_drafts(t, seen, params, u):
+    """Drafts equal to the round's own draws, so every row is reached (the penalty set grows through the round)."""
+    d = t.shape[0] - 1
+    drafts = np.full(d, -1, np.int32)
+    for i in range(d):
+        out = O.accept_sampled(t, drafts, seen, *params, u)
+        drafts[i] = out[4 + i]
+    return drafts
+
+
+ROUND_PARAMS = [(0.7, 1.0, 0, 0.0, 0.0), (0.8, 0.95, 40, 0.0, 0.0), (0.7, 0.9, 0, 0.05, 1.2), (0.0, 1.0, 0, 0.0, 2.0),
+                (1.1, 0.5, 5, 0.0, -0.5)]
+
+
+@pytest.mark.parametrize("v", [3000, 151936])
+def test_accept_sampled_bitwise(v):
+    from slotstream_spark_amd.engine.accept import Acceptor, AcceptResult
+    print(f"[sampler] accept_sampled v={v}", flush=True)
+    rng = np.random.default_rng(v)
+    D = 3
+    acc = Acceptor(D, v)
+    for k, params in enumerate(ROUND_PARAMS):
+        t = (rng.standard_normal((D + 1, v)) * 3).astype(np.float32)
+        u = rng.random(D + 1).astype(np.float32)
+        seen = set(rng.integers(0, v, 12).tolist())
+        for drafts in (_self_drafts(t, seen, params, u), rng.integers(0, v, D).astype(np.int32)):
+            want = O.accept_sampled(t, drafts, seen, *params, u)
+            sp = SampleParams(temperature=params[0], top_p=params[1], top_k=params[2], min_p=params[3],
+                              presence_penalty=params[4])
+            got = acc.sampled_async(torch.from_numpy(t).cuda(), torch.from_numpy(drafts).cuda(), sp, seen,
+                                    torch.from_numpy(u).cuda()).cpu().numpy()
+            assert got[:4].tolist() == want[:4].tolist(), (k, got, want)
+            assert got[4: 4 + got[1]].tolist() == want[4: 4 + want[1]].tolist(), (k, got, want)
+        if k == 0:
+            assert want[0] >= 0 and AcceptResult.from_out(got).n_emit == want[1]
+    # a non-finite row ends the round before its draw
+    t = (rng.standard_normal((D + 1, v)) * 3).astype(np.float32)
+    u = rng.random(D + 1).astype(np.float32)
+    drafts = _self_drafts(t, (), ROUND_PARAMS[1], u)
+    t[2, v // 3] = np.nan
+    want = O.accept_sampled(t, drafts, (), *ROUND_PARAMS[1], u)
+    got = acc.sampled_async(torch.from_numpy(t).cuda(), torch.from_numpy(drafts).cuda(), SampleParams(), (),
+                            torch.from_numpy(u).cuda()).cpu().numpy()
+    assert want[:4].tolist() == [2, 2, 2, 1] and got[:6].tolist() == want[:6].tolist()
+
+
+def test_accept_sampled_stream_and_seen_follow_the_reference_loop():
+    """Acceptor.sampled advances the sampler's stream by the draws made and adds the emitted tokens to seen, so two
+    rounds in a row equal the oracle rounds fed from the same stream."""
+    from slotstream_spark_amd.engine.accept import Acceptor, UniformStream
+    v, D = 4096, 3
+    rng = np.random.default_rng(5)
+    acc = Acceptor(D, v)
+    params = SampleParams(temperature=0.7, top_p=0.95, top_k=40, presence_penalty=0.8)
+    dev_stream, ref_stream = UniformStream(77), UniformStream(77)
+    dev_seen, ref_seen = {1, 2, 3}, {1, 2, 3}
+    for _ in range(3):
+        t = (rng.standard_normal((D + 1, v)) * 3).astype(np.float32)
+        u = ref_stream.peek(D + 1)
+        p = params.sanitized()
+        drafts = _self_drafts(t, ref_seen, (p.temperature, p.top_p, p.top_k, p.min_p, p.presence_penalty), u)
+        drafts[2] = (drafts[2] + 1) % v
+        want = O.accept_sampled(t, drafts, ref_seen, p.temperature, p.top_p, p.top_k, p.min_p, p.presence_penalty, u)
+        ref_stream.advance(int(want[2]))
+        ref_seen.update(want[4: 4 + want[1]].tolist())
+        res = acc.sampled(torch.from_numpy(t).cuda(), torch.from_numpy(drafts).cuda(), params, dev_seen, dev_stream)
+        assert (res.n_accept, res.n_emit, res.n_uniform) == (2, 3, 3)
+        assert res.tokens == want[4: 4 + want[1]].tolist()
+        assert dev_stream.state == ref_stream.state and dev_seen == ref_seen

@@ -98,3 +98,57 @@ def test_sanitized_matches_the_reference_clamps():
                      max_tokens=0).sanitized()
     assert (p.temperature, p.top_p, p.top_k, p.min_p, p.presence_penalty, p.max_tokens) == (0.0, 1.0, 0, 1.0, 0.0,
                                                                                               32768)
+
+
+# ---- the sampled verify round (engine/generate.py:208-229) built on the sampler
+
+def _round_rows(rng, d, v):
+    t = (rng.standard_normal((d + 1, v)) * 3).astype(np.float32)
+    drafts = np.argmax(t[:d] + rng.standard_normal((d, v)).astype(np.float32) * 0.5, axis=1).astype(np.int32)
+    return t, drafts
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_accept_sampled_at_temperature_zero_is_greedy(seed):
+    """Temperature 0 without a penalty is the greedy round, an independent implementation (incl. non-finite rows)."""
+    rng = np.random.default_rng(seed)
+    t, drafts = _round_rows(rng, 3, 500)
+    drafts[: seed % 4] = np.argmax(t[: seed % 4], axis=1)  # force acceptance of the first rows
+    if seed == 4:
+        t[1, 7] = np.nan
+    if seed == 5:
+        t[2, 9] = np.inf
+    u = np.zeros(4, np.float32)
+    got = O.accept_sampled(t, drafts, (), 0.0, 1.0, 0, 0.0, 0.0, u)
+    want = O.accept_greedy(t, drafts)
+    assert got[:4].tolist() == want[:4].tolist()
+    assert got[4: 4 + got[1]].tolist() == want[4: 4 + want[1]].tolist()
+
+
+def test_accept_sampled_top_k_one_is_greedy_and_consumes_one_uniform_per_draw():
+    rng = np.random.default_rng(11)
+    t, _ = _round_rows(rng, 3, 800)
+    drafts = np.argmax(t[:3], axis=1).astype(np.int32)
+    drafts[2] = (drafts[2] + 1) % 800
+    u = rng.random(4).astype(np.float32)
+    got = O.accept_sampled(t, drafts, (), 0.9, 0.95, 1, 0.0, 0.0, u)
+    assert got[:4].tolist() == [2, 3, 3, 0]
+    assert got[4:7].tolist() == np.argmax(t[:3], axis=1).tolist()
+
+
+def test_accept_sampled_penalizes_tokens_emitted_earlier_in_the_round():
+    """seen.add(tok) (generate.py:214): row 1's best token was emitted by row 0, so a penalty of 1 moves it below
+    the runner-up (5.0 - 1 < 4.5); without the penalty, or with it on another token, row 1 keeps it."""
+    v = 64
+    t = np.zeros((3, v), np.float32)
+    t[0, 10] = 9.0
+    t[1, 10], t[1, 20] = 5.0, 4.5
+    t[2, 30] = 1.0
+    drafts = np.array([10, 20], np.int32)
+    u = np.zeros(3, np.float32)
+    with_pen = O.accept_sampled(t, drafts, (), 0.0, 1.0, 0, 0.0, 1.0, u)
+    assert with_pen[:2].tolist() == [2, 3] and with_pen[4:7].tolist() == [10, 20, 30]
+    no_pen = O.accept_sampled(t, drafts, (), 0.0, 1.0, 0, 0.0, 0.0, u)
+    assert no_pen[:2].tolist() == [1, 2] and no_pen[4:6].tolist() == [10, 10]
+    pre_seen = O.accept_sampled(t, drafts, (10,), 0.0, 1.0, 0, 0.0, 9.5, u)  # seen before the round
+    assert pre_seen[4] != 10
