@@ -42,7 +42,8 @@ constexpr size_t kLdsBudget = 160 * 1024 - 16 * 1024;  // dynamic LDS left after
 // unit (tens of ns each), which with 256 workgroups delays the moment the count is complete by microseconds.
 constexpr int kShards = 16;
 constexpr int kShardStride = 32;  // ints
-enum { CTR_ROUTER = 0, CTR_SHARED = 1, CTR_ITEMS = 2, CTR_EXIT = 3, CTR_TOP = 4, CTR_COUNT = 5 };
+// CTR_EPOCH counts launches on this workspace: it is never reset, and the last workgroup of a launch adds one.
+enum { CTR_SHARED = 0, CTR_ITEMS = 1, CTR_EXIT = 2, CTR_TOP = 3, CTR_EPOCH = 4, CTR_COUNT = 5 };
 SS_DEV int* shard(int* ctr, int c, int s) { return ctr + (c * kShards + s) * kShardStride; }
 
 typedef __attribute__((address_space(3))) void lds_void_t;
@@ -52,13 +53,13 @@ struct VLayout {
 
 static __host__ __device__ inline size_t al256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-static __host__ __device__ inline VLayout vlayout(int T, int I, int Is, int K, int E) {
+static __host__ __device__ inline VLayout vlayout(int T, int H, int I, int Is, int K, int E) {
   VLayout l;
   size_t o = 0;
   l.ctr = o;
   o = al256(o + (size_t)CTR_COUNT * kShards * kShardStride * 4);
-  l.logits = o;
-  o = al256(o + (size_t)T * E * 2);
+  l.logits = o;  // [T][E] words: tag << 32 | bf16 logit
+  o = al256(o + (size_t)T * E * 8);
   l.gsh = o;
   o = al256(o + (size_t)T * Is * 2);
   l.ush = o;
@@ -74,8 +75,7 @@ static __host__ __device__ inline VLayout vlayout(int T, int I, int Is, int K, i
 }
 
 size_t verify_scratch_bytes(int T, int H, int I, int Is, int K, int E) {
-  (void)H;
-  return vlayout(T, I, Is, K, E).total;
+  return vlayout(T, H, I, Is, K, E).total;
 }
 
 // Dynamic LDS layout (bytes): per-expert partial dots, staged h fragments, then one region that holds the x
@@ -269,18 +269,33 @@ SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
 // Router tail of token t in one wave (the operations and order of router_topk_kernel): lane l holds the entries
 // e = l + 64 i. Each top-k round takes the 64-bit maximum of (key << 32 | ~e) over the untaken entries (taken or
 // absent entries are 0, below every present one), so ties go to the lower index.
-SS_DEV void router_tail_wave(const VerifyArgs& a, const uint16_t* logits, int t, VSmem& s,
+SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32_t tag, int t, VSmem& s,
                              const float (&bias_r)[kMaxEv / 64]) {
   const int lane = threadIdx.x & 63;
   const int E = a.E, K = a.K;
   constexpr int NV = kMaxEv / 64;
-  const uint16_t* lg = logits + (size_t)t * E;
+  const uint64_t* lg = logits + (size_t)t * E;
+  // Every logit word carries the launch's tag: the wave polls the words themselves until all of its token's E
+  // logits are this launch's (bounded like wait_ge), so no counter round trip precedes the data.
+  uint64_t wv[NV];
+  for (int it = 0;; ++it) {
+    bool fresh = true;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const int e = lane + 64 * i;
+      wv[i] = ld_ag(lg + (e < E ? e : 0));
+      fresh = fresh && (e >= E || (uint32_t)(wv[i] >> 32) == tag);
+    }
+    if (__all(fresh)) break;
+    if (it >= kSpinMax) {
+      if (lane == 0) ss_raise(a.err, SS_ERR_TIMEOUT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
   float v[NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    const int e = lane + 64 * i;
-    v[i] = ss_bf16_to_f32(ld_ag(lg + (e < E ? e : 0)));
-  }
+  for (int i = 0; i < NV; ++i) v[i] = ss_bf16_to_f32((uint16_t)wv[i]);
   if (a.bias) {
 #pragma unroll
     for (int i = 0; i < NV; ++i) v[i] = v[i] + bias_r[i];
@@ -460,42 +475,65 @@ SS_DEV void dense_dot(const uint4 (&wv)[NJX], const uint4* xfl, int nt, float ou
   }
 }
 
-// Shared-expert down rows 16 b + r0 + rr (rr < NR) of workgroup b, by one wave, in the dense_rows order:
-// hs = bf16(bf16(silu(g)) * u) from the bf16 gate / up projections, then the dot with the bf16 down row;
-// s.shv[r0 + rr][t] receives the fp32 sums. sh_w holds each row's 8 elements of this lane (Is <= 512).
-template <int NR>
-SS_DEV void shared_down_rows(const VerifyArgs& a, const uint16_t* gsh, const uint16_t* ush, const uint4 (&sh_w)[NR],
-                             int r0, int nt, VSmem& s) {
+// The shared-expert gate / up projections of this lane's 8 elements for every token (tokens >= nt read token 0).
+struct SharedIn {
+  uint4 g[kTBv], u[kTBv];
+};
+
+SS_DEV SharedIn shared_load(const VerifyArgs& a, const uint16_t* gsh, const uint16_t* ush, int nt) {
   const int lane = threadIdx.x & 63;
-  const int Is = a.Is;
+  const int li = 8 * lane < a.Is ? lane : 0;
+  SharedIn in;
+#pragma unroll
+  for (int t = 0; t < kTBv; ++t) {
+    const int tt = t < nt ? t : 0;
+    in.g[t] = ld_ag16(gsh + (size_t)tt * a.Is + 8 * li);
+    in.u[t] = ld_ag16(ush + (size_t)tt * a.Is + 8 * li);
+  }
+  return in;
+}
+
+// hs = bf16(bf16(silu(g)) * u) of the shared expert (the F.silu and product of the reference, in bf16), split over
+// the workgroup's four waves: wave w computes elements 8 l + 2 w and 8 l + 2 w + 1 of lane l's eight for every
+// token and stores them to hsl [nt][Is] (LDS).
+SS_DEV void shared_hs_part(const VerifyArgs& a, const SharedIn& in, int w, int nt, float* hsl) {
+  const int lane = threadIdx.x & 63;
+  if (8 * lane >= a.Is) return;
+#pragma unroll
+  for (int t = 0; t < kTBv; ++t) {
+    if (t >= nt) break;
+    const uint32_t gw4[4] = {in.g[t].x, in.g[t].y, in.g[t].z, in.g[t].w};
+    const uint32_t uw4[4] = {in.u[t].x, in.u[t].y, in.u[t].z, in.u[t].w};
+    const uint32_t gw = w == 0 ? gw4[0] : w == 1 ? gw4[1] : w == 2 ? gw4[2] : gw4[3];
+    const uint32_t uw = w == 0 ? uw4[0] : w == 1 ? uw4[1] : w == 2 ? uw4[2] : uw4[3];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float gv = h ? bf_hi(gw) : bf_lo(gw);
+      const float uv = h ? bf_hi(uw) : bf_lo(uw);
+      const float sv = ss_round_bf16(gv / (1.f + ss_expf(-gv)));
+      hsl[t * a.Is + 8 * lane + 2 * w + h] = ss_round_bf16(sv * uv);
+    }
+  }
+}
+
+// Shared-expert down rows of one wave, in the dense_rows order: the dot of hs (hsl) with the bf16 down rows;
+// out[rr][t] receives the fp32 sums (every lane). sh_w holds each row's 8 elements of this lane (Is <= 512).
+template <int NR>
+SS_DEV void shared_down_rows(const VerifyArgs& a, const float* hsl, const uint4 (&sh_w)[NR], int nt,
+                             float (&out)[NR][kTBv]) {
+  const int lane = threadIdx.x & 63;
   float sacc[NR][kTBv];
 #pragma unroll
   for (int rr = 0; rr < NR; ++rr)
 #pragma unroll
     for (int t = 0; t < kTBv; ++t) sacc[rr][t] = 0.f;
-  uint4 gqv[kTBv], uqv[kTBv];
-  const int li = 8 * lane < Is ? lane : 0;
-#pragma unroll
-  for (int t = 0; t < kTBv; ++t) {
-    const int tt = t < nt ? t : 0;
-    gqv[t] = ld_ag16(gsh + (size_t)tt * Is + 8 * li);
-    uqv[t] = ld_ag16(ush + (size_t)tt * Is + 8 * li);
-  }
-  __builtin_amdgcn_sched_barrier(0);
-  if (8 * lane < Is) {
+  if (8 * lane < a.Is) {
 #pragma unroll
     for (int t = 0; t < kTBv; ++t) {
       if (t >= nt) break;
-      const uint4 gq = gqv[t], uq = uqv[t];
-      const uint32_t gw4[4] = {gq.x, gq.y, gq.z, gq.w}, uw4[4] = {uq.x, uq.y, uq.z, uq.w};
       float hsv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float gv = (e & 1) ? bf_hi(gw4[e >> 1]) : bf_lo(gw4[e >> 1]);
-        const float uv = (e & 1) ? bf_hi(uw4[e >> 1]) : bf_lo(uw4[e >> 1]);
-        const float sv = ss_round_bf16(gv / (1.f + ss_expf(-gv)));
-        hsv[e] = ss_round_bf16(sv * uv);
-      }
+      for (int e = 0; e < 8; ++e) hsv[e] = hsl[t * a.Is + 8 * lane + e];
 #pragma unroll
       for (int rr = 0; rr < NR; ++rr) {
         const uint32_t ww[4] = {sh_w[rr].x, sh_w[rr].y, sh_w[rr].z, sh_w[rr].w};
@@ -511,11 +549,7 @@ SS_DEV void shared_down_rows(const VerifyArgs& a, const uint16_t* gsh, const uin
 #pragma unroll
   for (int rr = 0; rr < NR; ++rr)
 #pragma unroll
-    for (int t = 0; t < kTBv; ++t) {
-      if (t >= nt) break;
-      const float v = ss_wave_sum(sacc[rr][t]);
-      if (lane == 0) s.shv[r0 + rr][t] = v;
-    }
+    for (int t = 0; t < kTBv; ++t) out[rr][t] = t < nt ? ss_wave_sum(sacc[rr][t]) : 0.f;
 }
 
 template <int NJG, int NJD, bool XF32>
@@ -528,11 +562,12 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   const int n = lane & 15, g = lane >> 4;
   const int T = a.T, H = a.H, I = a.I, K = a.K, E = a.E;
   const bool verify = a.mode == 0;
-  const VLayout L = vlayout(T, I, verify ? a.Is : 0, K, verify ? E : 0);
+  const VLayout L = vlayout(T, H, I, verify ? a.Is : 0, K, verify ? E : 0);
   const DLayout D = dlayout(T, H, I, K, E, XF32 ? 1 : 0, verify ? 1 : 0);
   uint8_t* scr = static_cast<uint8_t*>(a.scratch);
   int* ctr = reinterpret_cast<int*>(scr + L.ctr);
-  uint16_t* logits = reinterpret_cast<uint16_t*>(scr + L.logits);
+  uint64_t* logits = reinterpret_cast<uint64_t*>(scr + L.logits);
+  const uint32_t tag = (uint32_t)ld_ag(shard(ctr, CTR_EPOCH, 0)) + 1u;  // this launch's logit tag
   uint16_t* gsh = reinterpret_cast<uint16_t*>(scr + L.gsh);
   uint16_t* ush = reinterpret_cast<uint16_t*>(scr + L.ush);
   uint16_t* sgl = reinterpret_cast<uint16_t*>(scr + L.sgl);
@@ -561,9 +596,6 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   const int Is = a.Is, J = verify ? E + Is : 0, W = G * 4;
   const int j_first = bid * 4 + w;
   const bool has_tile = bid < (H >> 4);
-  // With at most two tokens, waves 2 and 3 are free during the router tail and do the shared-expert down rows.
-  const bool early_shared = verify && has_tile && nt <= 2;
-  uint4 shw8[8];
   uint4 r0[NJX], r1[NJX], r2[NJX];
   auto load_job = [&](int j) {
     const uint16_t* w0 = j < E ? a.router_w + (size_t)j * H : a.sh_gate + (size_t)(j - E) * H;
@@ -599,11 +631,16 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       if (j != j_first) load_job(j);
       float d[kTBv];
       dense_dot<NJX>(r0, xfl, nt, d);
-      uint16_t* dst0 = j < E ? logits + j : gsh + (j - E);
-      const int ld = j < E ? E : Is;
-      if (lane == 0)
+      if (lane == 0) {
+        if (j < E) {
 #pragma unroll 1
-        for (int t = 0; t < nt; ++t) st_ag(dst0 + (size_t)t * ld, (uint16_t)ss_f32_to_bf16(d[t]));
+          for (int t = 0; t < nt; ++t)
+            st_ag(logits + (size_t)t * E + j, ((uint64_t)tag << 32) | (uint64_t)ss_f32_to_bf16(d[t]));
+        } else {
+#pragma unroll 1
+          for (int t = 0; t < nt; ++t) st_ag(gsh + (j - E) + (size_t)t * Is, (uint16_t)ss_f32_to_bf16(d[t]));
+        }
+      }
       if (j >= E) {
         dense_dot<NJX>(r1, xfl, nt, d);
         if (lane == 0)
@@ -620,13 +657,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     stores_done();
     __syncthreads();
     if (tid == 0) {
-      int nr = 0, ns = 0;
+      int ns = 0;
       for (int ww = 0; ww < 4; ++ww)
-        for (int j = bid * 4 + ww; j < J; j += W) {
-          if (j < E) nr += 1;
-          else ns += j == J - 1 ? 2 : 1;
-        }
-      if (nr) signal_add(ctr, CTR_ROUTER, nr);
+        for (int j = bid * 4 + ww; j < J; j += W)
+          if (j >= E) ns += j == J - 1 ? 2 : 1;
       if (ns) signal_add(ctr, CTR_SHARED, ns);
       SS_TRACE(1);
     }
@@ -654,23 +688,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
         s.base_e[e] = base_k[k];
       }
     }
-    if (early_shared && w >= 2) {
-#pragma unroll
-      for (int rr = 0; rr < 8; ++rr)
-        shw8[rr] = ldg16(a.sh_down + (size_t)(16 * bid + 8 * (w - 2) + rr) * Is + 8 * (8 * lane < Is ? lane : 0));
-    }
-    if (w == 0) wait_ge(ctr, CTR_ROUTER, E, a.err);
     SS_TRACE(2);
-    __syncthreads();
     if (w < nt) {
-      router_tail_wave(a, logits, w, s, bias_r);
+      router_tail_wave(a, logits, tag, w, s, bias_r);
       if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + 12] = __builtin_amdgcn_s_memrealtime();
-    } else if (early_shared && w >= 2) {
-      // Waves the router tail leaves idle compute this workgroup's shared-expert down rows now (8 rows each),
-      // which takes them off the end of the launch.
-      wait_ge(ctr, CTR_SHARED, Is + 1, a.err);
-      shared_down_rows<8>(a, gsh, ush, shw8, 8 * (w - 2), nt, s);
-      if (a.trace && tid == 128) a.trace[(size_t)bid * 16 + 13] = __builtin_amdgcn_s_memrealtime();
     }
     __syncthreads();
     SS_TRACE(3);
@@ -842,30 +863,33 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     SS_TRACE(7);
   }
 
-  // The first batch of down-projection weights and the shared-expert down rows of this workgroup's output rows are
-  // requested only now, after the gate/up items are published: they are needed after the wait for every item, and
-  // requested earlier they would queue ahead of the items' own loads.
+  // Shared-expert down rows (verify mode): their weights and the first batch of down-projection weights are
+  // requested only now, after the gate/up items are published (requested earlier they would queue ahead of the
+  // items' own loads); the gate / up inputs follow the DMAs, and the rows are computed after the down experts, when
+  // every load has landed, so nothing here waits on the critical path.
+  uint4 shw[4];
+  SharedIn shin;
+  if (verify && has_tile) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr)
+      shw[rr] = ldg16(a.sh_down + (size_t)(16 * bid + 4 * w + rr) * a.Is + 8 * (8 * lane < a.Is ? lane : 0));
+  }
   if (has_tile) {
 #pragma unroll 1
     for (int u = w; u < nu && u < D.P; u += 4) issue_down(u, u);
   }
-  uint4 shw[4];
-  if (verify && has_tile && !early_shared) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr) {
-      const int srow = 16 * bid + 4 * w + rr;
-      shw[rr] = ldg16(a.sh_down + (size_t)srow * a.Is + 8 * (8 * lane < a.Is ? lane : 0));
-    }
+  if (verify && has_tile) {
+    wait_ge(ctr, CTR_SHARED, a.Is + 1, a.err);
+    shin = shared_load(a, gsh, ush, nt);
   }
 
   // ------------------------------------------------------------ phase D: down + combine
   if (has_tile) {
-    if (w == 0) {
-      wait_ge(ctr, CTR_ITEMS, n_items, a.err);
-      if (verify && !early_shared) wait_ge(ctr, CTR_SHARED, a.Is + 1, a.err);
-    }
+    if (w == 0) wait_ge(ctr, CTR_ITEMS, n_items, a.err);
     __syncthreads();
     SS_TRACE(8);
+    // The combine's shared-expert gate logit, requested now and used at the end.
+    const uint16_t sgl_pre = verify && tid < 16 * kTBv ? ld_ag(sgl + ((tid & 3) < nt ? (tid & 3) : 0)) : 0;
     const int nq = nt * K;
     // Stage the h fragments of every use into LDS (1 KB per wave instruction) and the h group sums.
     const int hchunks = D.stage_h ? nq * I * 4 / 1024 : 0;
@@ -964,7 +988,21 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       }
     }
     SS_TRACE(10);
-    if (verify && !early_shared) shared_down_rows<4>(a, gsh, ush, shw, 4 * w, nt, s);
+    if (verify) {
+      // The prefetch region is free once every wave is past its down experts; hs goes there.
+      __syncthreads();
+      float* hsl = reinterpret_cast<float*>(prefl);
+      shared_hs_part(a, shin, w, nt, hsl);
+      __syncthreads();
+      float o[4][kTBv];
+      shared_down_rows<4>(a, hsl, shw, nt, o);
+      if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + 13] = __builtin_amdgcn_s_memrealtime();
+      if (lane == 0)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr)
+#pragma unroll
+          for (int t = 0; t < kTBv; ++t) s.shv[4 * w + rr][t] = o[rr][t];
+    }
     __syncthreads();
     if (tid < 16 * kTBv) {
       const int c = tid >> 2, r = tid & 3;
@@ -981,7 +1019,8 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
         if (a.out) a.out[(size_t)r * H + 16 * bid + c] = acc;
         if (verify) {
           const float shb = ss_round_bf16(s.shv[c][r]);
-          const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-ss_bf16_to_f32(ld_ag(sgl + r)))));
+          const float sgx = ss_bf16_to_f32(sgl_pre);
+          const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-sgx)));
           const float sh2 = ss_round_bf16(sgv * shb);
           a.y[(size_t)r * H + 16 * bid + c] = (uint16_t)ss_f32_to_bf16(ss_round_bf16(acc) + sh2);
         }
@@ -1003,8 +1042,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       const int t2 = __hip_atomic_fetch_add(shard(ctr, CTR_TOP, 0), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (t2 == (G < kShards ? G : kShards) - 1) {
         for (int c = 0; c < CTR_COUNT; ++c)
-          for (int q = 0; q < kShards; ++q)
-            __hip_atomic_store(shard(ctr, c, q), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (c != CTR_EPOCH)
+            for (int q = 0; q < kShards; ++q)
+              __hip_atomic_store(shard(ctr, c, q), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(shard(ctr, CTR_EPOCH, 0), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
@@ -1029,6 +1070,8 @@ static hipError_t launch_nj(const VerifyArgs& a, hipStream_t st) {
   }
   // A workgroup may hold at most 160 KB of LDS on gfx950; refuse any shape whose layout would exceed it.
   if (dly.P < 1 || dly.total > kLdsBudget || lds_static + dly.total > 160 * 1024) return hipErrorInvalidConfiguration;
+  // The shared expert's hs [T][Is] fp32 reuses the prefetch region at the end of phase D.
+  if (a.mode == 0 && (size_t)a.T * a.Is * 4 > dly.total - dly.pref) return hipErrorInvalidConfiguration;
   if (grid == 0) {
     int dev = 0, cus = 0;
     hipError_t e = hipGetDevice(&dev);
