@@ -194,6 +194,27 @@ int ssmoe_accept_sampled(const float* target, const int32_t* drafts, int D, int 
                          float temperature, float top_p, int top_k, float min_p, float presence_penalty,
                          const float* uniforms, void* workspace, int64_t workspace_bytes, int32_t* out, void* stream);
 
+/* ---------------------------------------------------------------- affine 4-bit GEMV (lm_head) */
+
+/* y = x W^T with W the MLX affine 4-bit weight (q int32 [N][K/8], nibble i of a word at bits 4i; s, b bf16
+ * [N][K/64]; w = q s + b), fp32 accumulation. Replaces gemv (kernels/gemv_affine.py:214-262) for
+ * AffineWeight(bits=4, gs=64), e.g. the lm_head (248,320 x 2560). x [R][K] bf16 (x_f32 = 0) or fp32 (x_f32 = 1,
+ * split into bf16 high part and residual); y fp32 [R][N]. K in {1024, 2048, 2560, 4096}; x and q 16-byte aligned.
+ * Row r of y depends on x row r alone: an R-row call equals R one-row calls bit for bit. */
+int ssmoe_gemv_affine4(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s, const uint16_t* b,
+                       int N, float* y, void* stream);
+
+/* Bytes of the workspace ssmoe_lm_head_greedy needs (-1 on bad arguments). */
+int64_t ssmoe_lm_head_greedy_workspace_bytes(int D, int N);
+
+/* The lm_head GEMV over the D+1 verify rows fused with the greedy round after it (engine/generate.py:208-229 at
+ * temperature 0): each 16-row tile of the vocabulary reduces to one argmax key and a non-finite flag per row, so the
+ * round reads no logits. out int32 [D+5] as ssmoe_accept_greedy (n_accept, n_emit, 0, flags 1 = non-finite row,
+ * 2 = draft out of range, tokens). logits fp32 [D+1][N] is written too when non-null. 0 <= D <= 60. */
+int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
+                         const uint16_t* b, int N, const int32_t* drafts, void* workspace, int64_t workspace_bytes,
+                         float* logits, int32_t* out, void* stream);
+
 /* ---------------------------------------------------------------- shared expert (prefill) */
 
 /* hs[t, i] = bf16(bf16(silu(g)) * u), g = proj[t, i], u = proj[t, Is + i], and sgl[t] = proj[t, 2 Is]: the F.silu and

@@ -249,6 +249,14 @@ def dequant(q, s_bits, b_bits, gs=64, dtype=np.float32) -> np.ndarray:
     return u * np.repeat(s, gs, axis=1) + np.repeat(b, gs, axis=1)
 
 
+def gemv_affine4_fp64(x, q, s_bits, b_bits, gs=64):
+    """gemv (kernels/gemv_affine.py:214-262) in fp64 on the exactly dequantized weights: (y [R, N], bound [R, N])
+    with bound = sum_k |x_k w_k|, the scale a fp32 accumulation error is measured against."""
+    w = dequant(q, s_bits, b_bits, gs, np.float64)
+    x64 = np.asarray(x, dtype=np.float64)
+    return x64 @ w.T, np.abs(x64) @ np.abs(w).T
+
+
 def record_offsets(H, I):
     """Piece offsets of one record (reference order, kernels/moe_gemv_affine.py:22-25 scaled to (H, I))."""
     w_gu, sb_gu = I * H // 2, I * (H // 64) * 2

@@ -46,6 +46,9 @@ SIGNATURES = {
     "ssmoe_sample_workspace_bytes": (_I64, [_I]),
     "ssmoe_sample": (_I, [_P, _I, _P, _I, _F, _F, _I, _F, _F, _P, _P, _I64, _P, _P]),
     "ssmoe_accept_sampled_workspace_bytes": (_I64, [_I, _I]),
+    "ssmoe_gemv_affine4": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P, _P]),
+    "ssmoe_lm_head_greedy_workspace_bytes": (_I64, [_I, _I]),
+    "ssmoe_lm_head_greedy": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P, _P, _I64, _P, _P, _P]),
     "ssmoe_accept_sampled": (_I, [_P, _P, _I, _I, _P, _I, _F, _F, _I, _F, _F, _P, _P, _I64, _P, _P]),
 }
 

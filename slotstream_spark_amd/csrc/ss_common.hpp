@@ -244,23 +244,30 @@ SS_DEV ss_f32x4 ss_mfma(const ss_u32x4& a, const ss_u32x4& b, const ss_f32x4& c)
 }
 
 // 8 nibbles of one word -> 8 bf16 values 1 + q/16 (q in the top 4 mantissa bits of 1.0 = 0x3F80), in the pair
-// order (q0,q4) (q1,q5) (q2,q6) (q3,q7): one shift and one and-or per pair. The constant part (1.0) is small next
-// to the spread of q/16, so the per-group correction (b - 16 s) * sum(x) cancels little of the MFMA dot.
+// order (q0,q4) (q1,q5) (q2,q6) (q3,q7). The constant part (1.0) is small next to the spread of q/16, so the
+// per-group correction (b - 16 s) * sum(x) cancels little of the MFMA dot.
 constexpr float kNibbleScale = 16.f;
-// (x & m) | c in one VOP3 instruction (the compiler emits separate and / or for this pattern). m lives in an SGPR,
-// c in a VGPR (one scalar operand per VALU instruction on gfx950).
-SS_DEV uint32_t ss_and_or(uint32_t x, uint32_t m, uint32_t c) {
+// (x & m) | c, for words that only feed other VALU instructions.
+SS_DEV uint32_t ss_and_or(uint32_t x, uint32_t m, uint32_t c) { return (x & m) | c; }
+// The same as one v_and_or_b32 (the compiler emits a separate and / or for this pattern). Its result must never be
+// an MFMA operand: the compiler does not see an inline-asm write when it inserts the wait states a VALU write needs
+// before an MFMA reads the register (one instruction apart, the MFMA read the register's previous value).
+SS_DEV uint32_t ss_and_or_v(uint32_t x, uint32_t m, uint32_t c) {
   uint32_t r;
   asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "s"(m), "v"(c));
   return r;
 }
+// Two and-ors put nibble 2k (a) and 2k+1 (b) at bits 3..6 of byte k with bit 7 set, 0x80 | q << 3 (the low byte of
+// bf16 1 + q/16); four byte permutes (compiler-generated, so the wait states before the MFMA are its own) pair each
+// with the high byte 0x3F.
 SS_DEV ss_u32x4 ss_nibbles_to_bf16(uint32_t w) {
-  constexpr uint32_t M = 0x00780078u;
-  const uint32_t one = 0x3F803F80u;
-  ss_u32x4 b;
-  b.x = ss_and_or(w << 3, M, one);
-  b.y = ss_and_or(w >> 1, M, one);
-  b.z = ss_and_or(w >> 5, M, one);
-  b.w = ss_and_or(w >> 9, M, one);
-  return b;
+  const uint32_t a = ss_and_or_v(w << 3, 0x78787878u, 0x80808080u);  // q0 q2 q4 q6
+  const uint32_t b = ss_and_or_v(w >> 1, 0x78787878u, 0x80808080u);  // q1 q3 q5 q7
+  const uint32_t hi = 0x3F3F3F3Fu;
+  ss_u32x4 r;
+  r.x = __builtin_amdgcn_perm(hi, a, 0x04020400u);  // (q0, q4)
+  r.y = __builtin_amdgcn_perm(hi, b, 0x04020400u);  // (q1, q5)
+  r.z = __builtin_amdgcn_perm(hi, a, 0x04030401u);  // (q2, q6)
+  r.w = __builtin_amdgcn_perm(hi, b, 0x04030401u);  // (q3, q7)
+  return r;
 }

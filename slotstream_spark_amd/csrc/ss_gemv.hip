@@ -1,0 +1,411 @@
+// Affine 4-bit GEMV: y[r][n] = sum_k x[r][k] * (q[n][k] * s[n][k/64] + b[n][k/64]) in fp32, the gemv of
+// kernels/gemv_affine.py:214-262 for AffineWeight(bits=4, gs=64) (the lm_head is its largest instance, 248,320 x
+// 2560). Weights are the MLX affine format: q int32 [N][K/8] (nibble i of a word at bits 4i), s and b bf16
+// [N][K/64].
+//
+// A wave computes one tile of 16 weight rows for up to 4 rows of x with v_mfma_f32_16x16x32_bf16: the weight
+// nibbles become bf16 1 + q/16 in registers (B operand, exact), x is staged once per workgroup as bf16 A fragments
+// (fp32 x as bf16 high part plus bf16 residual), and each 64-element group adds 16 s * D + (b - 16 s) * sum(x) in
+// fp32, the same factoring as the reference (sc * sum(q x) + bi * sum(x), :71-76). The 16 A rows carry (token,
+// K half, x part), so one MFMA yields both groups of a 128-element chunk. Row r's result depends on x row r alone,
+// so an R-row call equals R one-row calls bit for bit (the reference's invariance rule, kernels/tuning.py:1-10).
+//
+// The greedy epilogue reduces each tile to one 64-bit argmax key per x row (first maximum, as np.argmax) and a
+// non-finite flag, so the acceptance round after the lm_head (engine/generate.py:208-229) reads 16x fewer words
+// than the logits.
+#include "ss_common.hpp"
+#include "ss_launch.hpp"
+
+namespace ss {
+
+namespace {
+
+constexpr int kGR = 4;  // x rows per launch
+
+struct GemvArgs {
+  const void* x;  // [R][K] bf16 or fp32
+  int R, K, N, ntiles;
+  const uint32_t* q;
+  const uint16_t* s;
+  const uint16_t* b;
+  float* y;         // [R][N] or null
+  uint64_t* tkey;   // [R][ntiles] or null
+  int* tbad;        // [R][ntiles] (with tkey)
+};
+
+SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+SS_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
+SS_DEV float pick_half(uint32_t pair, int hi) { return hi ? bf_hi(pair) : bf_lo(pair); }
+
+// bf16 pair (element d, element d+4) of 8 consecutive bf16 held as 4 words (e0e1, e2e3, e4e5, e6e7): the element
+// order ss_nibbles_to_bf16 gives the weights.
+SS_DEV uint4 perm_pairs(uint4 v) {
+  uint4 f;
+  f.x = __builtin_amdgcn_perm(v.z, v.x, 0x05040100u);
+  f.y = __builtin_amdgcn_perm(v.z, v.x, 0x07060302u);
+  f.z = __builtin_amdgcn_perm(v.w, v.y, 0x05040100u);
+  f.w = __builtin_amdgcn_perm(v.w, v.y, 0x07060302u);
+  return f;
+}
+
+SS_DEV ss_u32x4 as_v(uint4 v) { return ss_u32x4{v.x, v.y, v.z, v.w}; }
+
+SS_DEV bool is_nan(float v) { return v != v; }
+
+// argmax key: the first maximum, NaN counting as the largest (np.argmax).
+SS_DEV uint64_t amax_key(float v, int j) {
+  const uint32_t k = is_nan(v) ? 0xFFFFFFFFu : ss_key(v == 0.f ? 0.f : v);
+  return ((uint64_t)k << 32) | (0xFFFFFFFFu - (uint32_t)j);
+}
+
+// x A-fragment entry f = (((j * 4 + i) * 4 + g) * kGR + t) holds elements kb .. kb + 7 of x row t, kb = 128 j +
+// 32 g + 8 i, as perm_pairs; fp32 x takes two entries (bf16 high parts, bf16 residuals). gx[G][t] = sum of group
+// G of x row t, sequential in element order.
+template <int NJG, bool XF32>
+SS_DEV void stage_x(const GemvArgs& a, uint4* xfl, float (*gx)[kGR]) {
+  const int tid = threadIdx.x;
+  const int K = a.K, nt = a.R;
+  constexpr int NF = NJG * 16 * kGR;
+  constexpr int FPT = NF / 256;
+  static_assert(NF % 256 == 0, "whole fragment entries per thread");
+  uint4 fv[FPT][XF32 ? 2 : 1];
+#pragma unroll
+  for (int k = 0; k < FPT; ++k) {
+    const int f = tid + 256 * k;
+    const int t = f & 3, gg = (f >> 2) & 3, i = (f >> 4) & 3, j = f >> 6;
+    const int tt = t < nt ? t : 0;
+    const int kb = 128 * j + 32 * gg + 8 * i;
+    if (XF32) {
+      const float* xp = static_cast<const float*>(a.x) + (size_t)tt * K + kb;
+      fv[k][0] = ldg16(xp);
+      fv[k][XF32 ? 1 : 0] = ldg16(xp + 4);
+    } else {
+      fv[k][0] = ldg16(static_cast<const uint16_t*>(a.x) + (size_t)tt * K + kb);
+    }
+  }
+  constexpr int GV = XF32 ? 16 : 8;
+  uint4 gv[GV];
+  const int q = tid < (K >> 6) * kGR ? tid : 0;
+  const int gt = (q & 3) < nt ? (q & 3) : 0;
+  const int Gi = q >> 2;
+#pragma unroll
+  for (int k = 0; k < GV; ++k) {
+    if (XF32)
+      gv[k] = ldg16(static_cast<const float*>(a.x) + (size_t)gt * K + 64 * Gi + 4 * k);
+    else
+      gv[k] = ldg16(static_cast<const uint16_t*>(a.x) + (size_t)gt * K + 64 * Gi + 8 * k);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < FPT; ++k) {
+    const int f = tid + 256 * k;
+    const bool live = (f & 3) < nt;
+    if (XF32) {
+      const uint4 v0 = fv[k][0], v1 = fv[k][XF32 ? 1 : 0];
+      const float e0[4] = {__uint_as_float(v0.x), __uint_as_float(v0.y), __uint_as_float(v0.z), __uint_as_float(v0.w)};
+      const float e1[4] = {__uint_as_float(v1.x), __uint_as_float(v1.y), __uint_as_float(v1.z), __uint_as_float(v1.w)};
+      uint32_t hw[4], lw[4];
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
+        const uint32_t b0 = ss_f32_to_bf16(e0[d]), b1 = ss_f32_to_bf16(e1[d]);
+        hw[d] = b0 | (b1 << 16);
+        lw[d] = ss_f32_to_bf16(e0[d] - ss_bf16_to_f32(b0)) | (ss_f32_to_bf16(e1[d] - ss_bf16_to_f32(b1)) << 16);
+      }
+      xfl[2 * f] = make_uint4(live ? hw[0] : 0u, live ? hw[1] : 0u, live ? hw[2] : 0u, live ? hw[3] : 0u);
+      xfl[2 * f + 1] = make_uint4(live ? lw[0] : 0u, live ? lw[1] : 0u, live ? lw[2] : 0u, live ? lw[3] : 0u);
+    } else {
+      const uint4 pv = perm_pairs(fv[k][0]);
+      xfl[f] = make_uint4(live ? pv.x : 0u, live ? pv.y : 0u, live ? pv.z : 0u, live ? pv.w : 0u);
+    }
+  }
+  if (tid < (K >> 6) * kGR) {
+    float sum = 0.f;
+#pragma unroll
+    for (int k = 0; k < GV; ++k) {
+      const uint4 v = gv[k];
+      if (XF32) {
+        sum = sum + __uint_as_float(v.x);
+        sum = sum + __uint_as_float(v.y);
+        sum = sum + __uint_as_float(v.z);
+        sum = sum + __uint_as_float(v.w);
+      } else {
+        sum = sum + bf_lo(v.x);
+        sum = sum + bf_hi(v.x);
+        sum = sum + bf_lo(v.y);
+        sum = sum + bf_hi(v.y);
+        sum = sum + bf_lo(v.z);
+        sum = sum + bf_hi(v.z);
+        sum = sum + bf_lo(v.w);
+        sum = sum + bf_hi(v.w);
+      }
+    }
+    gx[Gi][q & 3] = (q & 3) < nt ? sum : 0.f;
+  }
+}
+
+}  // namespace
+
+// Every wave walks the 16-row tiles t = 4 * block + wave, + 4 * grid.
+template <int NJG, bool XF32>
+__global__ __launch_bounds__(256, 2) void gemv_affine4_kernel(GemvArgs a) {
+  __shared__ uint4 xfl[NJG * 16 * kGR * (XF32 ? 2 : 1)];
+  __shared__ float gx[NJG * 2][kGR];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int nt = a.R, K = a.K, N = a.N;
+  stage_x<NJG, XF32>(a, xfl, gx);
+  __syncthreads();
+  const int m = lane & 15, at = m & 3, agrp = m >> 2, ahh = agrp >> 1, apart = agrp & 1;
+  const bool a_act = ahh == (g >> 1) && at < nt && (XF32 || apart == 0);
+  const int my_half = g >> 1, my_part = g & 1;
+  const int stride = 4 * gridDim.x;
+#pragma unroll 1
+  for (int tile = 4 * blockIdx.x + w; tile < a.ntiles; tile += stride) {
+    const int row = tile * 16 + n;
+    const int rr = row < N ? row : N - 1;
+    const uint32_t* qrow = a.q + (size_t)rr * (K >> 3) + 4 * g;
+    const uint32_t* srow = reinterpret_cast<const uint32_t*>(a.s + (size_t)rr * (K >> 6));
+    const uint32_t* brow = reinterpret_cast<const uint32_t*>(a.b + (size_t)rr * (K >> 6));
+    uint4 wv[NJG];
+    uint32_t sv[NJG], bv[NJG];
+#pragma unroll
+    for (int j = 0; j < NJG; ++j) {
+      wv[j] = ldg16(qrow + 16 * j);
+      sv[j] = gp(srow)[j];
+      bv[j] = gp(brow)[j];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    float acc[kGR] = {0.f, 0.f, 0.f, 0.f};
+    constexpr int JB = NJG >= 32 ? 2 : (NJG % 4 == 0 ? 4 : 1);  // chunks whose LDS operands are read ahead
+#pragma unroll
+    for (int j0 = 0; j0 < NJG; j0 += JB) {
+      uint4 av4[JB][4];
+      float4 gxv[JB];
+#pragma unroll
+      for (int jj = 0; jj < JB; ++jj) {
+        const int j = j0 + jj;
+        const uint4* fp = xfl + (size_t)(((j * 4) * 4 + g) * kGR + at) * (XF32 ? 2 : 1) + (XF32 ? apart : 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) av4[jj][i] = fp[(size_t)i * 16 * (XF32 ? 2 : 1)];
+        gxv[jj] = reinterpret_cast<const float4*>(gx)[2 * j + my_half];
+      }
+#pragma unroll
+      for (int jj = 0; jj < JB; ++jj) {
+        const int j = j0 + jj;
+        ss_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          ss_u32x4 av = as_v(av4[jj][i]);
+          if (!a_act) av = ss_u32x4{0u, 0u, 0u, 0u};
+          const uint32_t wd = i == 0 ? wv[j].x : i == 1 ? wv[j].y : i == 2 ? wv[j].z : wv[j].w;
+          d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
+        }
+        const float sf = pick_half(sv[j], my_half);
+        const float bf = pick_half(bv[j], my_half);
+        const float s16 = sf * kNibbleScale;
+        const float bp = my_part ? 0.f : __builtin_fmaf(-kNibbleScale, sf, bf);
+        const float gxa[kGR] = {gxv[jj].x, gxv[jj].y, gxv[jj].z, gxv[jj].w};
+#pragma unroll
+        for (int r = 0; r < kGR; ++r) {
+          acc[r] = __builtin_fmaf(s16, d[r], acc[r]);
+          acc[r] = __builtin_fmaf(bp, gxa[r], acc[r]);
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < kGR; ++r) acc[r] = ss_rows_sum(acc[r]);
+    if (a.y && g == 0 && row < N) {
+#pragma unroll
+      for (int r = 0; r < kGR; ++r)
+        if (r < nt) a.y[(size_t)r * N + row] = acc[r];
+    }
+    if (a.tkey) {
+#pragma unroll
+      for (int r = 0; r < kGR; ++r) {
+        if (r >= nt) break;
+        const bool valid = row < N;
+        const uint64_t key = valid ? amax_key(acc[r], row) : 0;
+        const uint32_t bad = valid && (__float_as_uint(acc[r]) & 0x7F800000u) == 0x7F800000u;
+        const uint64_t mk = ss_wave_max_u64(key);
+        const uint32_t anyb = ss_wave_or(bad);
+        if (lane == 0) {
+          a.tkey[(size_t)r * a.ntiles + tile] = mk;
+          a.tbad[(size_t)r * a.ntiles + tile] = (int)anyb;
+        }
+      }
+    }
+  }
+}
+
+// Per x row: the argmax over the tile keys and the non-finite flag (block r, 256 threads).
+__global__ __launch_bounds__(256) void gemv_row_argmax_kernel(const uint64_t* tkey, const int* tbad, int ntiles,
+                                                              uint64_t* rkey, int* rbad) {
+  const int r = blockIdx.x, tid = threadIdx.x;
+  __shared__ uint64_t sk[4];
+  __shared__ uint32_t sb[4];
+  uint64_t m = 0;
+  uint32_t bad = 0;
+  const uint64_t* kp = tkey + (size_t)r * ntiles;
+  const int* bp = tbad + (size_t)r * ntiles;
+  for (int i0 = 0; i0 < ntiles; i0 += 256 * 8) {
+    uint64_t kv[8];
+    int bv[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i = i0 + 256 * u + tid;
+      kv[u] = i < ntiles ? kp[i] : 0;
+      bv[u] = i < ntiles ? bp[i] : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      m = kv[u] > m ? kv[u] : m;
+      bad |= (uint32_t)bv[u];
+    }
+  }
+  m = ss_wave_max_u64(m);
+  bad = ss_wave_or(bad);
+  if ((tid & 63) == 0) {
+    sk[tid >> 6] = m;
+    sb[tid >> 6] = bad;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t mm = sk[0];
+    uint32_t bb = sb[0];
+    for (int k = 1; k < 4; ++k) {
+      mm = sk[k] > mm ? sk[k] : mm;
+      bb |= sb[k];
+    }
+    rkey[r] = mm;
+    rbad[r] = (int)bb;
+  }
+}
+
+// The greedy round (engine/generate.py:208-229 at temperature 0): row i's token is its argmax; a row holding a
+// non-finite logit ends the round before it (flag 1); drafts are accepted while equal. out as ssmoe_accept_greedy.
+__global__ void gemv_greedy_decide_kernel(const uint64_t* rkey, const int* rbad, const int32_t* drafts, int D, int V,
+                                          int32_t* out) {
+  if (threadIdx.x != 0) return;
+  int na = 0, ne = 0, fl = 0;
+  for (int i = 0; i <= D; ++i) {
+    if (rbad[i]) {
+      fl |= 1;
+      break;
+    }
+    const int tok = (int)(0xFFFFFFFFu - (uint32_t)rkey[i]);
+    out[4 + i] = tok;
+    ne = i + 1;
+    if (i == D) break;
+    const int d = drafts[i];
+    if (d < 0 || d >= V) fl |= 2;
+    if (tok != d) break;
+    na = i + 1;
+  }
+  for (int i = ne; i <= D; ++i) out[4 + i] = -1;
+  out[0] = na;
+  out[1] = ne;
+  out[2] = 0;
+  out[3] = fl;
+}
+
+namespace {
+
+// One resident wave of work per SIMD slot: the grid is the occupancy of this instantiation times the CU count.
+template <int NJG, bool XF32>
+hipError_t launch_tiles(const GemvArgs& a, hipStream_t st) {
+  static int grid = 0;
+  if (grid == 0) {
+    int dev = 0, cus = 0, per_cu = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess)
+      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_affine4_kernel<NJG, XF32>, 256, 0);
+    if (e != hipSuccess) return e;
+    grid = (per_cu > 0 ? per_cu : 1) * cus;
+  }
+  const int need = (a.ntiles + 3) / 4;
+  hipLaunchKernelGGL((gemv_affine4_kernel<NJG, XF32>), dim3(need < grid ? need : grid), dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+template <int NJG>
+hipError_t launch_x(const GemvArgs& a, int x_f32, hipStream_t st) {
+  return x_f32 ? launch_tiles<NJG, true>(a, st) : launch_tiles<NJG, false>(a, st);
+}
+
+hipError_t launch_chunk(const GemvArgs& a, int x_f32, hipStream_t st) {
+  switch (a.K >> 7) {
+    case 8: return launch_x<8>(a, x_f32, st);
+    case 16: return launch_x<16>(a, x_f32, st);
+    case 20: return launch_x<20>(a, x_f32, st);
+    case 32: return launch_x<32>(a, x_f32, st);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool gemv_affine4_shape_ok(int K) { return K == 1024 || K == 2048 || K == 2560 || K == 4096; }
+
+int64_t gemv_tiles(int N) { return ((int64_t)N + 15) / 16; }
+
+hipError_t launch_gemv_affine4(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s,
+                               const uint16_t* b, int N, float* y, hipStream_t st) {
+  GemvArgs a{};
+  a.K = K;
+  a.N = N;
+  a.ntiles = (int)gemv_tiles(N);
+  a.q = reinterpret_cast<const uint32_t*>(q);
+  a.s = s;
+  a.b = b;
+  const size_t xrow = (size_t)K * (x_f32 ? 4 : 2);
+  for (int r0 = 0; r0 < R; r0 += kGR) {
+    a.x = static_cast<const uint8_t*>(x) + (size_t)r0 * xrow;
+    a.R = R - r0 < kGR ? R - r0 : kGR;
+    a.y = y + (size_t)r0 * N;
+    hipError_t e = launch_chunk(a, x_f32, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+int64_t lm_head_greedy_workspace_bytes(int D, int N) {
+  const int64_t nt = gemv_tiles(N);
+  auto r = [](int64_t v) { return (v + 255) & ~(int64_t)255; };
+  return r((int64_t)(D + 1) * nt * 8) + r((int64_t)(D + 1) * nt * 4) + r((int64_t)(D + 1) * 8) + r((int64_t)(D + 1) * 4);
+}
+
+hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
+                                 const uint16_t* b, int N, const int32_t* drafts, void* work, float* logits,
+                                 int32_t* out, hipStream_t st) {
+  const int64_t nt = gemv_tiles(N);
+  auto r = [](int64_t v) { return (v + 255) & ~(int64_t)255; };
+  uint8_t* w = static_cast<uint8_t*>(work);
+  uint64_t* tkey = reinterpret_cast<uint64_t*>(w);
+  int* tbad = reinterpret_cast<int*>(w + r((int64_t)(D + 1) * nt * 8));
+  uint64_t* rkey = reinterpret_cast<uint64_t*>(w + r((int64_t)(D + 1) * nt * 8) + r((int64_t)(D + 1) * nt * 4));
+  int* rbad = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rkey) + r((int64_t)(D + 1) * 8));
+  GemvArgs a{};
+  a.K = K;
+  a.N = N;
+  a.ntiles = (int)nt;
+  a.q = reinterpret_cast<const uint32_t*>(q);
+  a.s = s;
+  a.b = b;
+  const int R = D + 1;
+  const size_t xrow = (size_t)K * (x_f32 ? 4 : 2);
+  for (int r0 = 0; r0 < R; r0 += kGR) {
+    a.x = static_cast<const uint8_t*>(x) + (size_t)r0 * xrow;
+    a.R = R - r0 < kGR ? R - r0 : kGR;
+    a.y = logits ? logits + (size_t)r0 * N : nullptr;
+    a.tkey = tkey + (size_t)r0 * nt;
+    a.tbad = tbad + (size_t)r0 * nt;
+    hipError_t e = launch_chunk(a, x_f32, st);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(gemv_row_argmax_kernel, dim3(R), dim3(256), 0, st, tkey, tbad, (int)nt, rkey, rbad);
+  hipLaunchKernelGGL(gemv_greedy_decide_kernel, dim3(1), dim3(64), 0, st, rkey, rbad, drafts, D, N, out);
+  return hipGetLastError();
+}
+
+}  // namespace ss

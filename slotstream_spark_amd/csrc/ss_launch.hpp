@@ -115,6 +115,15 @@ hipError_t launch_accept_sampled(const float* target, const int32_t* drafts, int
                                  int n_seen, float temperature, float top_p, int top_k, float min_p, float pp,
                                  const float* uniforms, void* work, int32_t* out, hipStream_t st);
 
+// Affine 4-bit GEMV (ss_gemv.hip).
+bool gemv_affine4_shape_ok(int K);
+hipError_t launch_gemv_affine4(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s,
+                               const uint16_t* b, int N, float* y, hipStream_t st);
+int64_t lm_head_greedy_workspace_bytes(int D, int N);
+hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
+                                 const uint16_t* b, int N, const int32_t* drafts, void* work, float* logits,
+                                 int32_t* out, hipStream_t st);
+
 // Acceptance.
 struct AcceptArgs {
   const float* target;   // [D+1, V]

@@ -598,5 +598,44 @@ int ssmoe_accept_sampled(const float* target, const int32_t* drafts, int D, int 
                    "accept sampled launch");
 }
 
+static int check_gemv(const void* x, int K, const int32_t* q, const uint16_t* s, const uint16_t* b, int N) {
+  if (!ss::gemv_affine4_shape_ok(K)) return fail(SSMOE_EINVAL, "K must be 1024, 2048, 2560 or 4096, got %d", K);
+  if (N < 1) return fail(SSMOE_EINVAL, "N must be >= 1, got %d", N);
+  if (!x || !q || !s || !b) return fail(SSMOE_EINVAL, "x, q, s and b must be non-null");
+  if (!aligned(x, 16) || !aligned(q, 16)) return fail(SSMOE_EINVAL, "x and q must be 16-byte aligned");
+  if (!aligned(s, 4) || !aligned(b, 4)) return fail(SSMOE_EINVAL, "s and b must be 4-byte aligned");
+  return ok();
+}
+
+int ssmoe_gemv_affine4(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s, const uint16_t* b,
+                       int N, float* y, void* stream) {
+  if (R < 0) return fail(SSMOE_EINVAL, "R must be >= 0, got %d", R);
+  if (int rc = check_gemv(x, K, q, s, b, N)) return rc;
+  if (!y) return fail(SSMOE_EINVAL, "y must be non-null");
+  if (R == 0) return ok();
+  return hip_check(ss::launch_gemv_affine4(x, x_f32 ? 1 : 0, R, K, q, s, b, N, y, static_cast<hipStream_t>(stream)),
+                   "gemv launch");
+}
+
+int64_t ssmoe_lm_head_greedy_workspace_bytes(int D, int N) {
+  if (D < 0 || D > 60 || N < 1) return -1;
+  return ss::lm_head_greedy_workspace_bytes(D, N);
+}
+
+int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
+                         const uint16_t* b, int N, const int32_t* drafts, void* workspace, int64_t workspace_bytes,
+                         float* logits, int32_t* out, void* stream) {
+  if (D < 0 || D > 60) return fail(SSMOE_EINVAL, "D must be in [0, 60], got %d", D);
+  if (int rc = check_gemv(x, K, q, s, b, N)) return rc;
+  if (!out || (D > 0 && !drafts)) return fail(SSMOE_EINVAL, "drafts and out must be non-null");
+  if (!workspace || !aligned(workspace, 256)) return fail(SSMOE_EINVAL, "workspace must be non-null and 256-byte aligned");
+  if (workspace_bytes < ss::lm_head_greedy_workspace_bytes(D, N))
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)ss::lm_head_greedy_workspace_bytes(D, N));
+  return hip_check(ss::launch_lm_head_greedy(x, x_f32 ? 1 : 0, D, K, q, s, b, N, drafts, workspace, logits, out,
+                                             static_cast<hipStream_t>(stream)),
+                   "lm_head greedy launch");
+}
+
 }  // extern "C"
 

@@ -204,3 +204,25 @@ def test_accept_sampled_rejects_bad_arguments(L):
     assert call(tp=2.0) == EINVAL
     assert call(w=ws - 256) == EINVAL and b"workspace holds" in L.ssmoe_last_error()
     assert call(V=(1 << 20) + 1) == EINVAL
+
+
+def test_gemv_rejects_bad_arguments(L):
+    p = ctypes.c_void_p(4096)
+
+    def call(R=2, K=2560, N=100, x=p, y=p, s=p):
+        return L.ssmoe_gemv_affine4(x, 0, R, K, p, s, p, N, y, None)
+    assert call(K=3000) == EINVAL and b"K must be" in L.ssmoe_last_error()
+    assert call(N=0) == EINVAL and b"N must be" in L.ssmoe_last_error()
+    assert call(R=-1) == EINVAL
+    assert call(x=None) == EINVAL and b"non-null" in L.ssmoe_last_error()
+    assert call(x=ctypes.c_void_p(4096 + 8)) == EINVAL and b"16-byte" in L.ssmoe_last_error()
+    assert call(s=ctypes.c_void_p(4096 + 2)) == EINVAL and b"4-byte" in L.ssmoe_last_error()
+    assert call(R=0) == 0  # nothing to do, no launch
+    ws = L.ssmoe_lm_head_greedy_workspace_bytes(3, 248320)
+    assert ws > 4 * 15520 * 12 and L.ssmoe_lm_head_greedy_workspace_bytes(61, 10) == -1
+
+    def head(D=3, w=ws, drafts=p):
+        return L.ssmoe_lm_head_greedy(p, 0, D, 2560, p, p, p, 248320, drafts, ctypes.c_void_p(4096), w, None, p, None)
+    assert head(D=61) == EINVAL and b"D must be" in L.ssmoe_last_error()
+    assert head(w=ws - 1) == EINVAL and b"workspace holds" in L.ssmoe_last_error()
+    assert head(drafts=None) == EINVAL
