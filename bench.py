@@ -216,6 +216,53 @@ def config2_leg(pool, lw, bias, steps, dev):
                       "of its own), events on the graph stream"}
 
 
+def lm_head_leg(steps, dev):
+    """The lm_head as the reference builds it (affine 4-bit gs64, 248,320 x 2560: gemv, kernels/gemv_affine.py:214-262)
+    over R = 1, 2 and 4 verify rows, and over the 4 rows of a depth-3 round fused with the greedy acceptance
+    (LMHeadGreedy). Two copies of the weights alternate so that every call streams its 358 MB from HBM (together
+    they exceed the 256 MB Infinity Cache). Algorithmic bytes per call = N (K/2 + 4 K/64) + R K 2 + R N 4 (logits)."""
+    import torch
+
+    from slotstream_spark_amd.kernels.gemv_affine import AffineWeight, LMHeadGreedy, gemv
+    from slotstream_spark_amd.memory.synth import normal_bf16
+
+    N, KH = 248320, 2560
+    g = torch.Generator(device=dev).manual_seed(2718)
+    ws = []
+    for c in range(2):
+        q = torch.randint(-2**31, 2**31 - 1, (N, KH // 8), generator=g, device=dev, dtype=torch.int32)
+        sc = (torch.randn((N, KH // 64), generator=g, device=dev) * 0.02).abs().to(torch.bfloat16)
+        ws.append(AffineWeight(q, sc, (-8 * sc.float()).to(torch.bfloat16), 4, 64, N, KH))
+    wbytes = N * (KH // 2 + 4 * (KH // 64))
+    s_ = torch.cuda.Stream(device=dev)
+    res = {}
+    for R in (1, 2, 4):
+        x = normal_bf16((R, KH), 1.0, 2719, dev)
+        outs = [torch.empty((R, N), device=dev) for _ in range(2)]
+        ms = timed_graph(lambda: [gemv(x, ws[i % 2], out=outs[i % 2]) for i in range(10)], steps, 2, s_)
+        us = ms * 1000.0 / 10
+        nbytes = wbytes + R * KH * 2 + R * N * 4
+        res[f"R{R}"] = {"us_per_call": round(us, 2), "bytes_per_call": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    D = 3
+    x4 = normal_bf16((D + 1, KH), 1.0, 2720, dev)
+    heads = [LMHeadGreedy(w, D, device=dev) for w in ws]
+    drafts = torch.zeros(D, dtype=torch.int32, device=dev)
+    ms = timed_graph(lambda: [heads[i % 2].run_async(x4, drafts) for i in range(10)], steps, 2, s_)
+    us = ms * 1000.0 / 10
+    fbytes = wbytes + (D + 1) * KH * 2
+    res["greedy_round_D3"] = {"us_per_call": round(us, 2), "bytes_per_call": fbytes,
+                              "gbs": round(fbytes / (us * 1e-6) / 1e9, 1)}
+    r4 = res["R4"]
+    res["roofline"] = {"bound": "hbm", "kernel": "gemv_affine4_kernel (R = 4)", "achieved": r4["gbs"],
+                       "peak": HBM_PEAK_GBS, "unit": "GB/s", "frac": round(r4["gbs"] / HBM_PEAK_GBS, 4),
+                       "traffic": traffic_of("lm_head_gemv"), "us_per_launch": r4["us_per_call"],
+                       "bytes_per_launch": r4["bytes_per_call"]}
+    res["shape"] = "N 248320 x K 2560, affine 4-bit gs64 (357.6 MB of weights), bf16 x"
+    log(f"lm_head: R1 {res['R1']['us_per_call']} us, R2 {res['R2']['us_per_call']} us, R4 {r4['us_per_call']} us "
+        f"({r4['gbs']} GB/s), fused greedy round D=3 {res['greedy_round_D3']['us_per_call']} us")
+    return res
+
+
 def config4_leg(pool, weights, biases, steps, dev):
     """a 48-layer routed-MoE stack (config-1 shape, all experts resident) run as an MTP loop of
     `steps` decode steps at T=2: per step, the 48 verify layers chained (layer l reads layer l-1's y) in one HIP
@@ -359,8 +406,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4",
-                    help="comma list of timed legs: verify, decode, prefill, config2, config4")
+    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4,lm_head",
+                    help="comma list of timed legs: verify, decode, prefill, config2, config4, lm_head")
     ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--config2-steps", type=int, default=1000)
     ap.add_argument("--config4-layers", type=int, default=48)
@@ -481,6 +528,10 @@ def main():
     if "config4" in legs:
         c4 = config4_leg(pool, weights[:args.config4_layers], biases[:args.config4_layers], args.config4_steps, dev)
 
+    lmh = None
+    if "lm_head" in legs:
+        lmh = lm_head_leg(max(args.steps // 5, 3), dev)
+
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline")
@@ -515,6 +566,7 @@ def main():
         "prefill": prefill,
         "config2": c2,
         "config4": c4,
+        "lm_head": lmh,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

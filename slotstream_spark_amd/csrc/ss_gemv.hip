@@ -10,9 +10,10 @@
 // K half, x part), so one MFMA yields both groups of a 128-element chunk. Row r's result depends on x row r alone,
 // so an R-row call equals R one-row calls bit for bit (the reference's invariance rule, kernels/tuning.py:1-10).
 //
-// The greedy epilogue reduces each tile to one 64-bit argmax key per x row (first maximum, as np.argmax) and a
-// non-finite flag, so the acceptance round after the lm_head (engine/generate.py:208-229) reads 16x fewer words
-// than the logits.
+// The greedy epilogue keeps a running 64-bit argmax key per x row (first maximum, as np.argmax) and a non-finite
+// flag in each wave, reduces them over the workgroup and combines workgroups with one atomic max per row (max is
+// order-free, so the result does not depend on timing): the acceptance round after the lm_head
+// (engine/generate.py:208-229) reads no logits.
 #include "ss_common.hpp"
 #include "ss_launch.hpp"
 
@@ -29,8 +30,8 @@ struct GemvArgs {
   const uint16_t* s;
   const uint16_t* b;
   float* y;         // [R][N] or null
-  uint64_t* tkey;   // [R][ntiles] or null
-  int* tbad;        // [R][ntiles] (with tkey)
+  uint64_t* rkey;   // [R] argmax keys, combined with atomic max (zeroed before the launch), or null
+  int* rbad;        // [R] non-finite flags, combined with atomic or (with rkey)
 };
 
 SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -148,35 +149,48 @@ SS_DEV void stage_x(const GemvArgs& a, uint4* xfl, float (*gx)[kGR]) {
 // Every wave walks the 16-row tiles t = 4 * block + wave, + 4 * grid.
 template <int NJG, bool XF32>
 __global__ __launch_bounds__(256, 2) void gemv_affine4_kernel(GemvArgs a) {
-  __shared__ uint4 xfl[NJG * 16 * kGR * (XF32 ? 2 : 1)];
+  constexpr int NXF = NJG * 16 * kGR * (XF32 ? 2 : 1);
+  // x fragments, then as many zero entries: a lane whose A row is inactive reads the zeros at the same offsets, so
+  // no MFMA operand needs a select.
+  __shared__ uint4 xfl[2 * NXF];
   __shared__ float gx[NJG * 2][kGR];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int n = lane & 15, g = lane >> 4;
   const int nt = a.R, K = a.K, N = a.N;
   stage_x<NJG, XF32>(a, xfl, gx);
+  for (int i = tid; i < NXF; i += 256) xfl[NXF + i] = make_uint4(0u, 0u, 0u, 0u);
   __syncthreads();
   const int m = lane & 15, at = m & 3, agrp = m >> 2, ahh = agrp >> 1, apart = agrp & 1;
   const bool a_act = ahh == (g >> 1) && at < nt && (XF32 || apart == 0);
+  const uint4* xbase = a_act ? xfl : xfl + NXF;
   const int my_half = g >> 1, my_part = g & 1;
   const int stride = 4 * gridDim.x;
+  uint64_t run_key[kGR] = {0, 0, 0, 0};
+  uint32_t run_bad = 0;
 #pragma unroll 1
   for (int tile = 4 * blockIdx.x + w; tile < a.ntiles; tile += stride) {
     const int row = tile * 16 + n;
     const int rr = row < N ? row : N - 1;
     const uint32_t* qrow = a.q + (size_t)rr * (K >> 3) + 4 * g;
-    const uint32_t* srow = reinterpret_cast<const uint32_t*>(a.s + (size_t)rr * (K >> 6));
-    const uint32_t* brow = reinterpret_cast<const uint32_t*>(a.b + (size_t)rr * (K >> 6));
-    uint4 wv[NJG];
+    const uint16_t* srow = a.s + (size_t)rr * (K >> 6);
+    const uint16_t* brow = a.b + (size_t)rr * (K >> 6);
+    uint4 wv[NJG], sq[NJG / 4], bq[NJG / 4];  // a row's scales and biases: NJG dwords each, as 16-byte words
+#pragma unroll
+    for (int j = 0; j < NJG; ++j) wv[j] = ldg16(qrow + 16 * j);
+#pragma unroll
+    for (int c = 0; c < NJG / 4; ++c) {
+      sq[c] = ldg16(srow + 8 * c);
+      bq[c] = ldg16(brow + 8 * c);
+    }
     uint32_t sv[NJG], bv[NJG];
 #pragma unroll
-    for (int j = 0; j < NJG; ++j) {
-      wv[j] = ldg16(qrow + 16 * j);
-      sv[j] = gp(srow)[j];
-      bv[j] = gp(brow)[j];
+    for (int c = 0; c < NJG / 4; ++c) {
+      sv[4 * c] = sq[c].x, sv[4 * c + 1] = sq[c].y, sv[4 * c + 2] = sq[c].z, sv[4 * c + 3] = sq[c].w;
+      bv[4 * c] = bq[c].x, bv[4 * c + 1] = bq[c].y, bv[4 * c + 2] = bq[c].z, bv[4 * c + 3] = bq[c].w;
     }
     __builtin_amdgcn_sched_barrier(0);
     float acc[kGR] = {0.f, 0.f, 0.f, 0.f};
-    constexpr int JB = NJG >= 32 ? 2 : (NJG % 4 == 0 ? 4 : 1);  // chunks whose LDS operands are read ahead
+    constexpr int JB = NJG >= 32 ? 1 : (NJG % 4 == 0 ? 2 : 1);  // chunks whose LDS operands are read ahead
 #pragma unroll
     for (int j0 = 0; j0 < NJG; j0 += JB) {
       uint4 av4[JB][4];
@@ -184,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void gemv_affine4_kernel(GemvArgs a) {
 #pragma unroll
       for (int jj = 0; jj < JB; ++jj) {
         const int j = j0 + jj;
-        const uint4* fp = xfl + (size_t)(((j * 4) * 4 + g) * kGR + at) * (XF32 ? 2 : 1) + (XF32 ? apart : 0);
+        const uint4* fp = xbase + (size_t)(((j * 4) * 4 + g) * kGR + at) * (XF32 ? 2 : 1) + (XF32 ? apart : 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) av4[jj][i] = fp[(size_t)i * 16 * (XF32 ? 2 : 1)];
         gxv[jj] = reinterpret_cast<const float4*>(gx)[2 * j + my_half];
@@ -196,7 +210,6 @@ __global__ __launch_bounds__(256, 2) void gemv_affine4_kernel(GemvArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           ss_u32x4 av = as_v(av4[jj][i]);
-          if (!a_act) av = ss_u32x4{0u, 0u, 0u, 0u};
           const uint32_t wd = i == 0 ? wv[j].x : i == 1 ? wv[j].y : i == 2 ? wv[j].z : wv[j].w;
           d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
         }
@@ -219,65 +232,49 @@ __global__ __launch_bounds__(256, 2) void gemv_affine4_kernel(GemvArgs a) {
       for (int r = 0; r < kGR; ++r)
         if (r < nt) a.y[(size_t)r * N + row] = acc[r];
     }
-    if (a.tkey) {
+    if (a.rkey) {
 #pragma unroll
       for (int r = 0; r < kGR; ++r) {
-        if (r >= nt) break;
-        const bool valid = row < N;
+        const bool valid = row < N && r < nt;
         const uint64_t key = valid ? amax_key(acc[r], row) : 0;
-        const uint32_t bad = valid && (__float_as_uint(acc[r]) & 0x7F800000u) == 0x7F800000u;
-        const uint64_t mk = ss_wave_max_u64(key);
-        const uint32_t anyb = ss_wave_or(bad);
-        if (lane == 0) {
-          a.tkey[(size_t)r * a.ntiles + tile] = mk;
-          a.tbad[(size_t)r * a.ntiles + tile] = (int)anyb;
-        }
+        run_key[r] = key > run_key[r] ? key : run_key[r];
+        run_bad |= (valid && (__float_as_uint(acc[r]) & 0x7F800000u) == 0x7F800000u) ? 1u << r : 0u;
       }
+    }
+  }
+  if (a.rkey) {
+    // The workgroup's maxima: wave, then the four waves in LDS, then one atomic max per x row (max is order-free).
+    __shared__ uint64_t wkey[4][kGR];
+    __shared__ uint32_t wbad[4];
+#pragma unroll
+    for (int r = 0; r < kGR; ++r) run_key[r] = ss_wave_max_u64(run_key[r]);
+    run_bad = ss_wave_or(run_bad);
+    if (lane == 0) {
+#pragma unroll
+      for (int r = 0; r < kGR; ++r) wkey[w][r] = run_key[r];
+      wbad[w] = run_bad;
+    }
+    __syncthreads();
+    if (tid < nt) {
+      uint64_t m = wkey[0][tid];
+      uint32_t b = wbad[0];
+      for (int ww = 1; ww < 4; ++ww) {
+        m = wkey[ww][tid] > m ? wkey[ww][tid] : m;
+        b |= wbad[ww];
+      }
+      atomicMax(reinterpret_cast<unsigned long long*>(a.rkey + tid), (unsigned long long)m);
+      if ((b >> tid) & 1u) atomicOr(a.rbad + tid, 1);
     }
   }
 }
 
-// Per x row: the argmax over the tile keys and the non-finite flag (block r, 256 threads).
-__global__ __launch_bounds__(256) void gemv_row_argmax_kernel(const uint64_t* tkey, const int* tbad, int ntiles,
-                                                              uint64_t* rkey, int* rbad) {
-  const int r = blockIdx.x, tid = threadIdx.x;
-  __shared__ uint64_t sk[4];
-  __shared__ uint32_t sb[4];
-  uint64_t m = 0;
-  uint32_t bad = 0;
-  const uint64_t* kp = tkey + (size_t)r * ntiles;
-  const int* bp = tbad + (size_t)r * ntiles;
-  for (int i0 = 0; i0 < ntiles; i0 += 256 * 8) {
-    uint64_t kv[8];
-    int bv[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int i = i0 + 256 * u + tid;
-      kv[u] = i < ntiles ? kp[i] : 0;
-      bv[u] = i < ntiles ? bp[i] : 0;
-    }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      m = kv[u] > m ? kv[u] : m;
-      bad |= (uint32_t)bv[u];
-    }
-  }
-  m = ss_wave_max_u64(m);
-  bad = ss_wave_or(bad);
-  if ((tid & 63) == 0) {
-    sk[tid >> 6] = m;
-    sb[tid >> 6] = bad;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    uint64_t mm = sk[0];
-    uint32_t bb = sb[0];
-    for (int k = 1; k < 4; ++k) {
-      mm = sk[k] > mm ? sk[k] : mm;
-      bb |= sb[k];
-    }
-    rkey[r] = mm;
-    rbad[r] = (int)bb;
+// Zeroes the per-row argmax keys and flags before the GEMV combines into them (a kernel, not a memset, so the
+// launch sequence is safe to capture).
+__global__ void gemv_key_init_kernel(uint64_t* rkey, int* rbad, int R) {
+  const int t = threadIdx.x;
+  if (t < R) {
+    rkey[t] = 0;
+    rbad[t] = 0;
   }
 }
 
@@ -370,40 +367,35 @@ hipError_t launch_gemv_affine4(const void* x, int x_f32, int R, int K, const int
 }
 
 int64_t lm_head_greedy_workspace_bytes(int D, int N) {
-  const int64_t nt = gemv_tiles(N);
-  auto r = [](int64_t v) { return (v + 255) & ~(int64_t)255; };
-  return r((int64_t)(D + 1) * nt * 8) + r((int64_t)(D + 1) * nt * 4) + r((int64_t)(D + 1) * 8) + r((int64_t)(D + 1) * 4);
+  (void)N;
+  return ((int64_t)(D + 1) * 8 + 255) / 256 * 256 + ((int64_t)(D + 1) * 4 + 255) / 256 * 256;
 }
 
 hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
                                  const uint16_t* b, int N, const int32_t* drafts, void* work, float* logits,
                                  int32_t* out, hipStream_t st) {
-  const int64_t nt = gemv_tiles(N);
-  auto r = [](int64_t v) { return (v + 255) & ~(int64_t)255; };
   uint8_t* w = static_cast<uint8_t*>(work);
-  uint64_t* tkey = reinterpret_cast<uint64_t*>(w);
-  int* tbad = reinterpret_cast<int*>(w + r((int64_t)(D + 1) * nt * 8));
-  uint64_t* rkey = reinterpret_cast<uint64_t*>(w + r((int64_t)(D + 1) * nt * 8) + r((int64_t)(D + 1) * nt * 4));
-  int* rbad = reinterpret_cast<int*>(reinterpret_cast<uint8_t*>(rkey) + r((int64_t)(D + 1) * 8));
+  uint64_t* rkey = reinterpret_cast<uint64_t*>(w);
+  int* rbad = reinterpret_cast<int*>(w + ((int64_t)(D + 1) * 8 + 255) / 256 * 256);
+  const int R = D + 1;
+  hipLaunchKernelGGL(gemv_key_init_kernel, dim3(1), dim3(64), 0, st, rkey, rbad, R);
   GemvArgs a{};
   a.K = K;
   a.N = N;
-  a.ntiles = (int)nt;
+  a.ntiles = (int)gemv_tiles(N);
   a.q = reinterpret_cast<const uint32_t*>(q);
   a.s = s;
   a.b = b;
-  const int R = D + 1;
   const size_t xrow = (size_t)K * (x_f32 ? 4 : 2);
   for (int r0 = 0; r0 < R; r0 += kGR) {
     a.x = static_cast<const uint8_t*>(x) + (size_t)r0 * xrow;
     a.R = R - r0 < kGR ? R - r0 : kGR;
     a.y = logits ? logits + (size_t)r0 * N : nullptr;
-    a.tkey = tkey + (size_t)r0 * nt;
-    a.tbad = tbad + (size_t)r0 * nt;
+    a.rkey = rkey + r0;
+    a.rbad = rbad + r0;
     hipError_t e = launch_chunk(a, x_f32, st);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(gemv_row_argmax_kernel, dim3(R), dim3(256), 0, st, tkey, tbad, (int)nt, rkey, rbad);
   hipLaunchKernelGGL(gemv_greedy_decide_kernel, dim3(1), dim3(64), 0, st, rkey, rbad, drafts, D, N, out);
   return hipGetLastError();
 }

@@ -219,7 +219,7 @@ def test_gemv_rejects_bad_arguments(L):
     assert call(s=ctypes.c_void_p(4096 + 2)) == EINVAL and b"4-byte" in L.ssmoe_last_error()
     assert call(R=0) == 0  # nothing to do, no launch
     ws = L.ssmoe_lm_head_greedy_workspace_bytes(3, 248320)
-    assert ws > 4 * 15520 * 12 and L.ssmoe_lm_head_greedy_workspace_bytes(61, 10) == -1
+    assert ws >= 4 * 12 and L.ssmoe_lm_head_greedy_workspace_bytes(61, 10) == -1
 
     def head(D=3, w=ws, drafts=p):
         return L.ssmoe_lm_head_greedy(p, 0, D, 2560, p, p, p, 248320, drafts, ctypes.c_void_p(4096), w, None, p, None)
