@@ -17,6 +17,8 @@ extern "C" {
 #define SSMOE_OK 0
 #define SSMOE_EINVAL 1
 #define SSMOE_EHIP 2
+#define SSMOE_EXHAUSTED 3 /* the pool has too few unpinned slots (slotio::Exhausted); nothing changed */
+#define SSMOE_EIO 4       /* a record could not be read (slotio::IoError); nothing published */
 
 /* Device status bits raised by kernels on bad input (the kernel skips the entry and continues). */
 #define SSMOE_ERR_EXPERT_ID 1 /* expert id outside [0, E) */
@@ -214,6 +216,42 @@ int64_t ssmoe_lm_head_greedy_workspace_bytes(int D, int N);
 int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
                          const uint16_t* b, int N, const int32_t* drafts, void* workspace, int64_t workspace_bytes,
                          float* logits, int32_t* out, void* stream);
+
+/* ---------------------------------------------------------------- expert slot pool */
+
+/* An expert slot pool in HBM fed from experts.bin (layout slotstream-pool-layer-expert-piece-v1: the record of
+ * layer L, expert e at (L * experts + e) * record_bytes, docs/model-and-repack.md:37-57). Replaces slotio::Pool +
+ * Ensurer (slotio/include/slotio/pool.hpp:39-165, slotio/src/ensure.cpp) behind runtime/pool.py's ExpertPool.
+ * map int32 [layers * experts] and slot_ptr int64 [max_slots] are the caller's device tables (the ones the kernels
+ * read); the pool keeps them current. Slots are device chunks of chunk_bytes; a slot is record_bytes rounded up
+ * to 256. Returns SSMOE_EIO if the file cannot be opened. */
+int ssmoe_pool_open(const char* experts_path, int layers, int experts, int64_t record_bytes, int max_slots,
+                    int64_t chunk_bytes, int32_t* map, int64_t* slot_ptr, void** pool);
+int ssmoe_pool_close(void* pool);
+
+/* Grow or shrink to `slots` slots (Pool::resize_slots): shrinking unmaps every slot >= slots and drops its pin. */
+int ssmoe_pool_resize(void* pool, int slots);
+
+/* The slot of every requested expert of `layer` (host arrays, input order, duplicates allowed), reading the missing
+ * ones from the file into CLOCK victims (Ensurer::ensure). Every returned slot is pinned with generation `gen` until
+ * ssmoe_pool_retire_below passes it. Transactional: SSMOE_EXHAUSTED when the unpinned slots cannot hold the misses
+ * (nothing changes), SSMOE_EIO when a read fails (pins restored, victims left unmapped, nothing published).
+ * timing int64 [6] (may be NULL): hits, misses, bytes read, total ns, read ns, copy ns. */
+int ssmoe_pool_ensure(void* pool, int layer, const int32_t* experts, int n, uint64_t gen, int32_t* slots,
+                      int64_t* timing);
+
+/* Unpin every slot pinned with a generation below `progress` (Pins::retire_below). */
+int ssmoe_pool_retire_below(void* pool, uint64_t progress);
+
+/* Progress word (host memory, e.g. pinned and advanced by a kernel at the end of a step): every ensure first
+ * retires the pins below its value (Ensurer::set_progress_ptr). NULL detaches it. */
+int ssmoe_pool_set_progress(void* pool, const uint64_t* progress);
+
+/* Copy `bytes` of slot `slot` to dst (host or device memory), the reference's slot_view. */
+int ssmoe_pool_copy_slot(void* pool, int slot, void* dst, int64_t bytes);
+
+/* stats int64 [8]: slots, chunks, pinned slots, owned bytes, slot stride, hits, misses, bytes read. */
+int ssmoe_pool_stats(void* pool, int64_t* stats);
 
 /* ---------------------------------------------------------------- shared expert (prefill) */
 

@@ -46,6 +46,14 @@ SIGNATURES = {
     "ssmoe_sample_workspace_bytes": (_I64, [_I]),
     "ssmoe_sample": (_I, [_P, _I, _P, _I, _F, _F, _I, _F, _F, _P, _P, _I64, _P, _P]),
     "ssmoe_accept_sampled_workspace_bytes": (_I64, [_I, _I]),
+    "ssmoe_pool_open": (_I, [ctypes.c_char_p, _I, _I, _I64, _I, _I64, _P, _P, ctypes.POINTER(_P)]),
+    "ssmoe_pool_close": (_I, [_P]),
+    "ssmoe_pool_resize": (_I, [_P, _I]),
+    "ssmoe_pool_ensure": (_I, [_P, _I, _P, _I, ctypes.c_uint64, _P, _P]),
+    "ssmoe_pool_retire_below": (_I, [_P, ctypes.c_uint64]),
+    "ssmoe_pool_stats": (_I, [_P, _P]),
+    "ssmoe_pool_set_progress": (_I, [_P, _P]),
+    "ssmoe_pool_copy_slot": (_I, [_P, _I, _P, _I64]),
     "ssmoe_gemv_affine4": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P, _P]),
     "ssmoe_lm_head_greedy_workspace_bytes": (_I64, [_I, _I]),
     "ssmoe_lm_head_greedy": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P, _P, _I64, _P, _P, _P]),
@@ -57,6 +65,17 @@ _lib = None
 
 class SsmoeError(RuntimeError):
     pass
+
+
+SSMOE_EXHAUSTED, SSMOE_EIO = 3, 4
+
+
+class Exhausted(SsmoeError):
+    """The pool has too few unpinned slots for the request (slotio.Exhausted); nothing changed."""
+
+
+class IoError(SsmoeError):
+    """A record could not be read (slotio.IoError); nothing was published."""
 
 
 def lib() -> ctypes.CDLL:
@@ -79,7 +98,8 @@ def lib() -> ctypes.CDLL:
 def check(rc: int) -> None:
     if rc != 0:
         msg = lib().ssmoe_last_error().decode(errors="replace")
-        raise SsmoeError(f"ssmoe status {rc}: {msg}")
+        cls = {SSMOE_EXHAUSTED: Exhausted, SSMOE_EIO: IoError}.get(rc, SsmoeError)
+        raise cls(f"ssmoe status {rc}: {msg}")
 
 
 def ptr(t) -> int | None:

@@ -2,6 +2,8 @@
 // Every launcher validates nothing: shapes were checked by the caller; each returns hipGetLastError().
 #pragma once
 #include <hip/hip_runtime.h>
+
+#include <string>
 #include <stdint.h>
 
 namespace ss {
@@ -114,6 +116,26 @@ hipError_t launch_sample(const float* x, int V, const int32_t* gen, int n_gen, f
 hipError_t launch_accept_sampled(const float* target, const int32_t* drafts, int D, int V, const int32_t* seen,
                                  int n_seen, float temperature, float top_p, int top_k, float min_p, float pp,
                                  const float* uniforms, void* work, int32_t* out, hipStream_t st);
+
+// Expert slot pool (ss_pool.hip).
+struct Pool;
+enum class PoolStatus { Ok, Invalid, Exhausted, Io };
+struct EnsureTiming {
+  int64_t hits, misses, bytes, total_ns, read_ns, copy_ns;
+};
+struct PoolStats {
+  int64_t slots, chunks, pinned, owned_bytes, stride, hits, misses, bytes;
+};
+hipError_t pool_open(const char* path, int layers, int experts, int64_t record_bytes, int max_slots,
+                     int64_t chunk_bytes, int32_t* map_dev, int64_t* ptr_dev, Pool** out, std::string* err);
+void pool_close(Pool* p);
+hipError_t pool_resize(Pool* p, int n, std::string* err);
+void pool_retire_below(Pool* p, uint64_t progress);
+PoolStatus pool_ensure(Pool* p, int layer, const int32_t* experts, int n, uint64_t gen, int32_t* out,
+                       EnsureTiming* t, std::string* err);
+void pool_info(Pool* p, PoolStats* s);
+void pool_set_progress(Pool* p, const uint64_t* progress);
+hipError_t pool_copy_slot(Pool* p, int slot, void* dst, int64_t bytes, std::string* err);
 
 // Affine 4-bit GEMV (ss_gemv.hip).
 bool gemv_affine4_shape_ok(int K);

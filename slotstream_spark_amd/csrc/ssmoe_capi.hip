@@ -637,5 +637,84 @@ int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* 
                    "lm_head greedy launch");
 }
 
+int ssmoe_pool_open(const char* experts_path, int layers, int experts, int64_t record_bytes, int max_slots,
+                    int64_t chunk_bytes, int32_t* map, int64_t* slot_ptr, void** pool) {
+  if (!experts_path || !map || !slot_ptr || !pool) return fail(SSMOE_EINVAL, "path, map, slot_ptr and pool must be non-null");
+  if (layers < 1 || experts < 1 || (int64_t)layers * experts > (1LL << 30))
+    return fail(SSMOE_EINVAL, "need layers >= 1, experts >= 1, layers * experts <= 2^30 (got %d x %d)", layers, experts);
+  if (record_bytes < 1 || max_slots < 0 || chunk_bytes < record_bytes)
+    return fail(SSMOE_EINVAL, "need record_bytes >= 1, max_slots >= 0, chunk_bytes >= record_bytes");
+  if (!aligned(slot_ptr, 8) || !aligned(map, 4)) return fail(SSMOE_EINVAL, "map / slot_ptr misaligned");
+  ss::Pool* p = nullptr;
+  std::string err;
+  hipError_t e = ss::pool_open(experts_path, layers, experts, record_bytes, max_slots, chunk_bytes, map, slot_ptr, &p, &err);
+  if (e == hipErrorFileNotFound) return fail(SSMOE_EIO, "%s", err.c_str());
+  if (e != hipSuccess) return fail(SSMOE_EHIP, "%s: %s", err.c_str(), hipGetErrorString(e));
+  *pool = p;
+  return ok();
+}
+
+int ssmoe_pool_close(void* pool) {
+  ss::pool_close(static_cast<ss::Pool*>(pool));
+  return ok();
+}
+
+int ssmoe_pool_resize(void* pool, int slots) {
+  if (!pool) return fail(SSMOE_EINVAL, "pool must be non-null");
+  std::string err;
+  hipError_t e = ss::pool_resize(static_cast<ss::Pool*>(pool), slots, &err);
+  if (e == hipErrorInvalidValue) return fail(SSMOE_EINVAL, "%s", err.c_str());
+  if (e != hipSuccess) return fail(SSMOE_EHIP, "pool resize: %s %s", err.c_str(), hipGetErrorString(e));
+  return ok();
+}
+
+int ssmoe_pool_ensure(void* pool, int layer, const int32_t* experts, int n, uint64_t gen, int32_t* slots,
+                      int64_t* timing) {
+  if (!pool || n < 0 || (n > 0 && (!experts || !slots)))
+    return fail(SSMOE_EINVAL, "pool, experts and slots must be non-null, n >= 0");
+  std::string err;
+  ss::EnsureTiming t{};
+  const ss::PoolStatus st = ss::pool_ensure(static_cast<ss::Pool*>(pool), layer, experts, n, gen, slots, &t, &err);
+  if (timing) {
+    const int64_t v[6] = {t.hits, t.misses, t.bytes, t.total_ns, t.read_ns, t.copy_ns};
+    for (int k = 0; k < 6; ++k) timing[k] = v[k];
+  }
+  switch (st) {
+    case ss::PoolStatus::Ok: return ok();
+    case ss::PoolStatus::Invalid: return fail(SSMOE_EINVAL, "%s", err.c_str());
+    case ss::PoolStatus::Exhausted: return fail(SSMOE_EXHAUSTED, "%s", err.c_str());
+    default: return fail(SSMOE_EIO, "%s", err.c_str());
+  }
+}
+
+int ssmoe_pool_retire_below(void* pool, uint64_t progress) {
+  if (!pool) return fail(SSMOE_EINVAL, "pool must be non-null");
+  ss::pool_retire_below(static_cast<ss::Pool*>(pool), progress);
+  return ok();
+}
+
+int ssmoe_pool_set_progress(void* pool, const uint64_t* progress) {
+  if (!pool) return fail(SSMOE_EINVAL, "pool must be non-null");
+  ss::pool_set_progress(static_cast<ss::Pool*>(pool), progress);
+  return ok();
+}
+
+int ssmoe_pool_copy_slot(void* pool, int slot, void* dst, int64_t bytes) {
+  if (!pool || !dst) return fail(SSMOE_EINVAL, "pool and dst must be non-null");
+  std::string err;
+  hipError_t e = ss::pool_copy_slot(static_cast<ss::Pool*>(pool), slot, dst, bytes, &err);
+  if (e == hipErrorInvalidValue) return fail(SSMOE_EINVAL, "%s", err.c_str());
+  return hip_check(e, "pool slot copy");
+}
+
+int ssmoe_pool_stats(void* pool, int64_t* stats) {
+  if (!pool || !stats) return fail(SSMOE_EINVAL, "pool and stats must be non-null");
+  ss::PoolStats s{};
+  ss::pool_info(static_cast<ss::Pool*>(pool), &s);
+  const int64_t v[8] = {s.slots, s.chunks, s.pinned, s.owned_bytes, s.stride, s.hits, s.misses, s.bytes};
+  for (int k = 0; k < 8; ++k) stats[k] = v[k];
+  return ok();
+}
+
 }  // extern "C"
 
