@@ -263,6 +263,68 @@ def lm_head_leg(steps, dev):
     return res
 
 
+def pool_leg(dev, calls=4):
+    """The slot pool loading records from experts.bin (ExpertPool / ssmoe_pool_*): 256 records of the reference's
+    2,764,800-byte layout (hidden 2560, moe_intermediate 640) in a 2 x 128 file, a 128-slot pool, and ensures of a
+    whole layer (128 misses each, every call after the first evicting the other layer) with 1, 4 and 8 reader
+    lanes, buffered (the file was just written, so reads come from the page cache) and, where the file system
+    takes it, O_DIRECT. Also the hit path: an ensure of 10 resident experts, the per-layer call of a decode step."""
+    import shutil
+    import tempfile
+
+    import numpy as np
+
+    from slotstream_spark_amd import _lib
+    from slotstream_spark_amd.memory.expert_pool import ExpertPool
+
+    rec, layers, experts = 2_764_800, 2, 128
+    d = Path(tempfile.mkdtemp(prefix="ssmoe-pool-"))
+    res = {"record_bytes": rec, "records": layers * experts, "slots": experts}
+    try:
+        (d / "experts.bin").write_bytes(np.random.default_rng(5).bytes(layers * experts * rec))
+        (d / "experts.manifest.json").write_text(json.dumps(
+            {"record_bytes": rec, "layers": layers, "experts": experts, "alignment": 4096}))
+        ids = np.arange(experts, dtype=np.int32)
+        for lanes, direct in ((1, False), (4, False), (8, False), (8, True)):
+            try:
+                ep = ExpertPool(d, experts, lanes=lanes, direct=direct, device=dev)
+            except _lib.IoError as e:
+                res["direct"] = f"unsupported here: {e}"
+                continue
+            key = f"{'direct' if direct else 'buffered'}_lanes{lanes}"
+            try:
+                ep.ensure(0, ids, gen=1)
+                t0 = time.perf_counter()
+                for c in range(calls):
+                    ep.retire_below(c + 2)
+                    ep.ensure((c + 1) % 2, ids, gen=c + 2)
+                dt = time.perf_counter() - t0
+            except _lib.IoError as e:
+                res[key] = f"read failed: {e}"
+                log(f"pool {key}: {e}")
+                ep.close()
+                continue
+            gbs = calls * experts * rec / dt / 1e9
+            res[key] = {"gbs": round(gbs, 2), "ms_per_layer": round(dt * 1000 / calls, 2),
+                        "read_ms_last": round(ep.last_timing["read_ns"] / 1e6, 2)}
+            log(f"pool {key}: {gbs:.2f} GB/s, {dt * 1000 / calls:.1f} ms per 128-record layer")
+            if lanes == 8 and not direct:
+                rng = np.random.default_rng(6)
+                picks = [rng.choice(experts, 10, replace=False).astype(np.int32) for _ in range(1000)]
+                layer = calls % 2
+                for i in range(50):
+                    ep.ensure(layer, picks[i])
+                t0 = time.perf_counter()
+                for p in picks:
+                    ep.ensure(layer, p)
+                res["hit_us_per_ensure_10"] = round((time.perf_counter() - t0) * 1e6 / len(picks), 2)
+                log(f"pool hit path: {res['hit_us_per_ensure_10']} us per ensure of 10 resident experts")
+            ep.close()
+    finally:
+        shutil.rmtree(d, ignore_errors=True)
+    return res
+
+
 def config4_leg(pool, weights, biases, steps, dev):
     """a 48-layer routed-MoE stack (config-1 shape, all experts resident) run as an MTP loop of
     `steps` decode steps at T=2: per step, the 48 verify layers chained (layer l reads layer l-1's y) in one HIP
@@ -406,8 +468,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4,lm_head",
-                    help="comma list of timed legs: verify, decode, prefill, config2, config4, lm_head")
+    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4,lm_head,pool",
+                    help="comma list of timed legs: verify, decode, prefill, config2, config4, lm_head, pool")
     ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--config2-steps", type=int, default=1000)
     ap.add_argument("--config4-layers", type=int, default=48)
@@ -532,6 +594,10 @@ def main():
     if "lm_head" in legs:
         lmh = lm_head_leg(max(args.steps // 5, 3), dev)
 
+    pl = None
+    if "pool" in legs:
+        pl = pool_leg(dev)
+
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline")
@@ -567,6 +633,7 @@ def main():
         "config2": c2,
         "config4": c4,
         "lm_head": lmh,
+        "pool": pl,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -229,6 +229,12 @@ int ssmoe_pool_open(const char* experts_path, int layers, int experts, int64_t r
                     int64_t chunk_bytes, int32_t* map, int64_t* slot_ptr, void** pool);
 int ssmoe_pool_close(void* pool);
 
+/* Reader set-up (slotio Reader::Config lanes, reader.hpp:1; File::open_direct): the misses of an ensure are spread
+ * over `lanes` (1..12) reader threads, each with two pinned staging buffers and its own stream, so reads and
+ * host-to-device copies overlap. direct != 0 reads with O_DIRECT (record_bytes must be a multiple of 4096;
+ * SSMOE_EIO if the file system refuses it). A new pool has 1 lane, buffered. */
+int ssmoe_pool_set_reader(void* pool, int lanes, int direct);
+
 /* Grow or shrink to `slots` slots (Pool::resize_slots): shrinking unmaps every slot >= slots and drops its pin. */
 int ssmoe_pool_resize(void* pool, int slots);
 
@@ -250,7 +256,8 @@ int ssmoe_pool_set_progress(void* pool, const uint64_t* progress);
 /* Copy `bytes` of slot `slot` to dst (host or device memory), the reference's slot_view. */
 int ssmoe_pool_copy_slot(void* pool, int slot, void* dst, int64_t bytes);
 
-/* stats int64 [8]: slots, chunks, pinned slots, owned bytes, slot stride, hits, misses, bytes read. */
+/* stats int64 [10]: slots, chunks, pinned slots, owned bytes, slot stride, hits, misses, bytes read, lanes,
+ * direct. */
 int ssmoe_pool_stats(void* pool, int64_t* stats);
 
 /* ---------------------------------------------------------------- shared expert (prefill) */

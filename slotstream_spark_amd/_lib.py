@@ -48,6 +48,7 @@ SIGNATURES = {
     "ssmoe_accept_sampled_workspace_bytes": (_I64, [_I, _I]),
     "ssmoe_pool_open": (_I, [ctypes.c_char_p, _I, _I, _I64, _I, _I64, _P, _P, ctypes.POINTER(_P)]),
     "ssmoe_pool_close": (_I, [_P]),
+    "ssmoe_pool_set_reader": (_I, [_P, _I, _I]),
     "ssmoe_pool_resize": (_I, [_P, _I]),
     "ssmoe_pool_ensure": (_I, [_P, _I, _P, _I, ctypes.c_uint64, _P, _P]),
     "ssmoe_pool_retire_below": (_I, [_P, ctypes.c_uint64]),

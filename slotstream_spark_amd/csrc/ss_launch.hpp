@@ -124,11 +124,12 @@ struct EnsureTiming {
   int64_t hits, misses, bytes, total_ns, read_ns, copy_ns;
 };
 struct PoolStats {
-  int64_t slots, chunks, pinned, owned_bytes, stride, hits, misses, bytes;
+  int64_t slots, chunks, pinned, owned_bytes, stride, hits, misses, bytes, lanes, direct;
 };
 hipError_t pool_open(const char* path, int layers, int experts, int64_t record_bytes, int max_slots,
                      int64_t chunk_bytes, int32_t* map_dev, int64_t* ptr_dev, Pool** out, std::string* err);
 void pool_close(Pool* p);
+hipError_t pool_set_reader(Pool* p, int lanes, bool direct, std::string* err);
 hipError_t pool_resize(Pool* p, int n, std::string* err);
 void pool_retire_below(Pool* p, uint64_t progress);
 PoolStatus pool_ensure(Pool* p, int layer, const int32_t* experts, int n, uint64_t gen, int32_t* out,

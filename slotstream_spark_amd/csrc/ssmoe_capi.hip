@@ -659,6 +659,15 @@ int ssmoe_pool_close(void* pool) {
   return ok();
 }
 
+int ssmoe_pool_set_reader(void* pool, int lanes, int direct) {
+  if (!pool) return fail(SSMOE_EINVAL, "pool must be non-null");
+  std::string err;
+  hipError_t e = ss::pool_set_reader(static_cast<ss::Pool*>(pool), lanes, direct != 0, &err);
+  if (e == hipErrorInvalidValue) return fail(SSMOE_EINVAL, "%s", err.c_str());
+  if (e == hipErrorFileNotFound) return fail(SSMOE_EIO, "%s", err.c_str());
+  return hip_check(e, "pool reader set-up");
+}
+
 int ssmoe_pool_resize(void* pool, int slots) {
   if (!pool) return fail(SSMOE_EINVAL, "pool must be non-null");
   std::string err;
@@ -711,8 +720,9 @@ int ssmoe_pool_stats(void* pool, int64_t* stats) {
   if (!pool || !stats) return fail(SSMOE_EINVAL, "pool and stats must be non-null");
   ss::PoolStats s{};
   ss::pool_info(static_cast<ss::Pool*>(pool), &s);
-  const int64_t v[8] = {s.slots, s.chunks, s.pinned, s.owned_bytes, s.stride, s.hits, s.misses, s.bytes};
-  for (int k = 0; k < 8; ++k) stats[k] = v[k];
+  const int64_t v[10] = {s.slots, s.chunks, s.pinned, s.owned_bytes, s.stride, s.hits, s.misses, s.bytes,
+                         s.lanes, s.direct};
+  for (int k = 0; k < 10; ++k) stats[k] = v[k];
   return ok();
 }
 

@@ -112,11 +112,13 @@ class ExpertPool:
     """Slots of expert records read from experts.bin with an exact, transactional ensure (runtime/pool.py:27-112).
 
     `hidden` / `inter` name the record layout for the kernels (inferred from record_bytes for the known shapes).
-    `mem_type` is accepted for the reference's signature: the slots are always HBM here."""
+    `lanes` reader threads (1..12) read the misses of one ensure in parallel; `direct` reads with O_DIRECT (the
+    reference's File.open_direct). `mem_type` is accepted for the reference's signature: the slots are always HBM
+    here."""
 
     def __init__(self, packed_dir, slots, mem_type=None, *, experts_name="experts.bin",
                  manifest_name="experts.manifest.json", chunk_bytes=1 << 30, max_slots=25088, hidden=None,
-                 inter=None, device="cuda"):
+                 inter=None, device="cuda", lanes=4, direct=False):
         packed = Path(packed_dir)
         man = read_manifest(packed, manifest_name)
         self.record_bytes = int(man["record_bytes"])
@@ -146,6 +148,7 @@ class ExpertPool:
         self._progress = None
         self.last_timing = None
         self.pool = PoolView(self)
+        self.set_reader(lanes, direct)
         self.resize_slots(slots)
 
     # The table names of the reference (runtime/pool.py:89-100) and of the resident SlotPool.
@@ -176,6 +179,15 @@ class ExpertPool:
             self.last_timing = dict(zip(("hits", "misses", "bytes", "total_ns", "read_ns", "copy_ns"), t.tolist()))
         return out
 
+    def set_reader(self, lanes: int, direct: bool = False) -> None:
+        _lib.check(_lib.lib().ssmoe_pool_set_reader(self._h, int(lanes), int(bool(direct))))
+
+    def load_all(self, layers=None, gen=None) -> None:
+        """Every expert of the given layers (default: all the file holds) resident, one ensure per layer: the
+        pre-fill of a pool with a slot for every record."""
+        for layer in range(self.layers if layers is None else layers):
+            self.ensure(layer, np.arange(self.experts, dtype=np.int32), gen)
+
     def resize_slots(self, n) -> None:
         _lib.check(_lib.lib().ssmoe_pool_resize(self._h, int(n)))
 
@@ -204,10 +216,10 @@ class ExpertPool:
         return self.stats()["owned_bytes"]
 
     def stats(self) -> dict:
-        s = np.zeros(8, dtype=np.int64)
+        s = np.zeros(10, dtype=np.int64)
         _lib.check(_lib.lib().ssmoe_pool_stats(self._h, s.ctypes.data))
-        return dict(zip(("slots", "chunks", "pinned", "owned_bytes", "stride", "hits", "misses", "bytes"),
-                        (int(v) for v in s)))
+        return dict(zip(("slots", "chunks", "pinned", "owned_bytes", "stride", "hits", "misses", "bytes", "lanes",
+                         "direct"), (int(v) for v in s)))
 
     def close(self) -> None:
         if getattr(self, "_h", None):

@@ -49,10 +49,12 @@ def _device_records(ep, idxs):
     return out
 
 
-def test_pool_bytes_duplicates_and_eviction(packed):
+@pytest.mark.parametrize("lanes", [1, 4, 8])
+def test_pool_bytes_duplicates_and_eviction(packed, lanes):
     d, data = packed
-    ep = ExpertPool(d, 16, chunk_bytes=1 << 26)
+    ep = ExpertPool(d, 16, chunk_bytes=1 << 26, lanes=lanes)
     try:
+        assert ep.stats()["lanes"] == lanes
         assert ep.layers == 49 and ep.map.numel() == 49 * 512    # the MTP layer shares the table
         ids = np.array([3, 9, 40, 9], dtype=np.int32)
         slots = ep.ensure(0, ids)
@@ -78,6 +80,23 @@ def test_pool_bytes_duplicates_and_eviction(packed):
         assert ep.stats()["misses"] == 19 and ep.stats()["bytes"] == 19 * REC
     finally:
         ep.close()
+
+
+def test_direct_reads(packed):
+    """O_DIRECT reads (File.open_direct) give the same records; skipped where the file system refuses O_DIRECT."""
+    d, data = packed
+    ep = ExpertPool(d, 16, chunk_bytes=1 << 26, lanes=1)
+    try:
+        ep.set_reader(4, direct=True)
+    except _lib.IoError as e:
+        ep.close()
+        pytest.skip(f"file system refuses O_DIRECT: {e}")
+    ids = np.array([0, 17, 63, 5, 17], dtype=np.int32)
+    slots = ep.ensure(0, ids, gen=1)
+    for e, s in zip(ids, slots):
+        assert ep.pool.slot_view(int(s)).tobytes() == _rec(data, int(e)).tobytes()
+    assert ep.stats()["direct"] == 1
+    ep.close()
 
 
 def test_overwrite_slot(packed):

@@ -102,4 +102,5 @@ def test_pool_capi_rejects_bad_arguments(tmp_path):
     assert L.ssmoe_pool_open(str(tmp_path / "missing.bin").encode(), 1, 1, 10, 4, 100, p, p,
                              ctypes.byref(h)) == 4 and b"cannot open" in L.ssmoe_last_error()
     assert L.ssmoe_pool_resize(None, 3) == 1
+    assert L.ssmoe_pool_set_reader(None, 4, 0) == 1
     assert L.ssmoe_pool_ensure(None, 0, None, 0, 1, None, None) == 1
