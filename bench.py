@@ -263,6 +263,47 @@ def lm_head_leg(steps, dev):
     return res
 
 
+def step_leg(pool, weights, biases, steps, dev):
+    """§8(f) row 1: the whole verify round in one HIP graph (engine/step.py MTPStepGraph) at full size: 48 chained
+    config-1 layers (residual + RMSNorm between them), the 248,320 x 2048 affine 4-bit lm_head fused with the greedy
+    round, and the MTP head's MoE (map layer 48), for depth 1 (T = 2) and depth 3 (T = 4). Timed with HIP events
+    around `steps` replays; one int32 result vector per round is the only thing the host would read back."""
+    import torch
+
+    from slotstream_spark_amd.engine.step import MoEWeights, MTPStepGraph
+    from slotstream_spark_amd.kernels.gemv_affine import AffineWeight
+    from slotstream_spark_amd.memory.synth import normal_bf16
+
+    N, NL = 248320, 48
+    g = torch.Generator(device=dev).manual_seed(2721)
+    q = torch.randint(-2**31, 2**31 - 1, (N, H // 8), generator=g, device=dev, dtype=torch.int32)
+    sc = (torch.randn((N, H // 64), generator=g, device=dev) * 0.02).abs().to(torch.bfloat16)
+    lm = AffineWeight(q, sc, (-8 * sc.float()).to(torch.bfloat16), 4, 64, N, H)
+    mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, b) for w, b in zip(weights, biases)]
+    res = {"layers": NL, "head_layer": NL, "lm_head": f"{N} x {H} affine 4-bit gs64"}
+    for depth in (1, 3):
+        sg = MTPStepGraph(pool, mw[:NL], lm, depth, head=mw[NL], top_k=K, device=dev)
+        sg.step(normal_bf16((depth + 1, H), 1.0, 2722, dev), torch.zeros(depth, dtype=torch.int32, device=dev))
+        for _ in range(2):
+            sg.step()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(steps):
+            sg.step()
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1000.0 / steps
+        uniq = [len(set(sg.ids[l].cpu().flatten().tolist())) for l in range(NL)]
+        res[f"T{depth + 1}"] = {"us_per_round": round(us, 1), "us_per_layer_incl_norm": round(us / NL, 2),
+                                "unique_experts_mean": round(sum(uniq) / NL, 2),
+                                "finite": bool(torch.isfinite(sg.mixed[NL].float()).all().item())}
+        log(f"step graph T={depth + 1}: {us:.1f} us per round ({NL} layers + head MoE + lm_head greedy), "
+            f"mean unique experts {sum(uniq) / NL:.1f}")
+        del sg
+    return res
+
+
 def pool_leg(dev, calls=4):
     """The slot pool loading records from experts.bin (ExpertPool / ssmoe_pool_*): 256 records of the reference's
     2,764,800-byte layout (hidden 2560, moe_intermediate 640) in a 2 x 128 file, a 128-slot pool, and ensures of a
@@ -468,8 +509,8 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4,lm_head,pool",
-                    help="comma list of timed legs: verify, decode, prefill, config2, config4, lm_head, pool")
+    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4,lm_head,step,pool",
+                    help="comma list of timed legs: verify, decode, prefill, config2, config4, lm_head, step, pool")
     ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--config2-steps", type=int, default=1000)
     ap.add_argument("--config4-layers", type=int, default=48)
@@ -500,7 +541,7 @@ def main():
         del a, b
         log("copy calibration: 3 x 268435456-byte device copies done")
     NL, T = args.layers, args.tokens
-    NP = max(NL, args.config4_layers if "config4" in legs else 0)
+    NP = max(NL, args.config4_layers if "config4" in legs else 0, 49 if "step" in legs else 0)
     log(f"allocating {NP} layers x {E} experts ({NP * E * 1_769_472 / 2**30:.1f} GiB of records)")
     pool = SlotPool(NP, E, H, I, device=dev)
     pool.fill_random(1729)
@@ -594,6 +635,10 @@ def main():
     if "lm_head" in legs:
         lmh = lm_head_leg(max(args.steps // 5, 3), dev)
 
+    stp = None
+    if "step" in legs:
+        stp = step_leg(pool, weights, biases, max(args.steps // 5, 5), dev)
+
     pl = None
     if "pool" in legs:
         pl = pool_leg(dev)
@@ -633,6 +678,7 @@ def main():
         "config2": c2,
         "config4": c4,
         "lm_head": lmh,
+        "step_graph": stp,
         "pool": pl,
         "cpu_baseline": cpu,
     }

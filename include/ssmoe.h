@@ -268,6 +268,13 @@ int ssmoe_pool_stats(void* pool, int64_t* stats);
  * hs bf16 [T, Is]; sgl bf16 [T]. */
 int ssmoe_shared_hs(const uint16_t* proj, int64_t ld, int T, int Is, uint16_t* hs, uint16_t* sgl, void* stream);
 
+/* Residual stream and RMSNorm between chained layers: s = bf16(resid + y) stored to stream_out (skipped when y is
+ * NULL: s = resid), mixed = bf16((s * r) * w), r = 1 / sqrt(sum(s^2) / H + eps), weight NULL = ones. Follows the
+ * residual add of GraphSet._moe (runtime/graphs.py:169) with one stream and unit injection, and rmsnorm
+ * (model/reference_torch.py:30-38) with a fixed reduction order. bf16 [R, H] rows; stream_out may equal resid. */
+int ssmoe_residual_rmsnorm(const uint16_t* resid, const uint16_t* y, const uint16_t* weight, float eps, int R, int H,
+                           uint16_t* stream_out, uint16_t* mixed, void* stream);
+
 /* y = bf16(bf16(routed) + bf16(bf16(sigmoid(sgl)) * sh)): routed.to(bf16) + sigmoid(x w_sg) * sh with the reference's
  * bf16 rounding of each op (model/layers.py:398-402, reference_torch.py:132-134). routed fp32 [T, H] (16-byte
  * aligned); sh bf16 [T, H]; sgl bf16 [T]; y bf16 [T, H]; H % 4 == 0. */

@@ -50,6 +50,8 @@ def lib():
         L.or_row_z.argtypes, L.or_row_z.restype = [P, i32, f32], f32
         L.or_shared_hs.argtypes, L.or_shared_hs.restype = [P, P, P, i32], None
         L.or_combine_shared.argtypes, L.or_combine_shared.restype = [P, P, P, P, i32, i32], None
+        L.or_residual_rmsnorm.argtypes = [P, P, P, f32, i32, i32, P, P]
+        L.or_residual_rmsnorm.restype = None
         L.or_sample.argtypes = [P, i32, P, i32, f32, f32, i32, f32, f32, f32, P, P]
         L.or_sample.restype = None
         _lib = L
@@ -226,6 +228,19 @@ def combine_shared(routed, sh_bits, sgl_bits) -> np.ndarray:
     y = np.empty((T, H), np.uint16)
     lib().or_combine_shared(_p(r), _p(sh), _p(sg), _p(y), T, H)
     return y
+
+
+def residual_rmsnorm(resid_bits, y_bits=None, w_bits=None, eps=1e-6):
+    """(stream_out, mixed) uint16 bf16 bits [R, H]: s = bf16(resid + y), mixed = bf16((s r) w) (or_residual_rmsnorm)."""
+    x = _c(resid_bits, np.uint16)
+    R, H = x.shape
+    y = None if y_bits is None else _c(y_bits, np.uint16)
+    w = None if w_bits is None else _c(w_bits, np.uint16)
+    so = np.empty((R, H), np.uint16)
+    mx = np.empty((R, H), np.uint16)
+    lib().or_residual_rmsnorm(_p(x), None if y is None else _p(y), None if w is None else _p(w), eps, R, H, _p(so),
+                              _p(mx))
+    return so, mx
 
 
 # ---------------------------------------------------------------- affine 4-bit (kernels/affine_ref.py:10-30)

@@ -459,6 +459,32 @@ void or_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* 
   }
 }
 
+/* Residual add + RMSNorm (runtime/graphs.py:169 with one stream, model/reference_torch.py:30-38):
+ * s = bf16(resid + y) (y NULL: s = resid), r = 1 / sqrt(sum(s^2) / H + eps) with the sum of lane l over elements
+ * 512 j + 8 l .. + 7 by fmaf from 0 then the butterfly, mixed = bf16((s * r) * w) (w NULL: 1). */
+void or_residual_rmsnorm(const uint16_t* resid, const uint16_t* y, const uint16_t* w, float eps, int R, int H,
+                         uint16_t* stream_out, uint16_t* mixed) {
+  for (int t = 0; t < R; ++t) {
+    const uint16_t* xr = resid + (size_t)t * H;
+    uint16_t* sr = stream_out + (size_t)t * H;
+    for (int k = 0; k < H; ++k)
+      sr[k] = y ? or_f32_to_bf16(or_bf16_to_f32(xr[k]) + or_bf16_to_f32(y[(size_t)t * H + k])) : xr[k];
+    float lanes[64];
+    for (int l = 0; l < 64; ++l) {
+      float acc = 0.0f;
+      for (int k8 = l; k8 < H / 8; k8 += 64)
+        for (int e = 0; e < 8; ++e) {
+          const float v = or_bf16_to_f32(sr[8 * k8 + e]);
+          acc = fmaf(v, v, acc);
+        }
+      lanes[l] = acc;
+    }
+    const float r = 1.0f / sqrtf(butterfly_sum(lanes) / (float)H + eps);
+    for (int k = 0; k < H; ++k)
+      mixed[(size_t)t * H + k] = or_f32_to_bf16((or_bf16_to_f32(sr[k]) * r) * (w ? or_bf16_to_f32(w[k]) : 1.0f));
+  }
+}
+
 /* Elementwise or_expf over an array (test helper). */
 void or_expf_vec(const float* x, float* y, int64_t n) {
   for (int64_t i = 0; i < n; ++i) y[i] = or_expf(x[i]);

@@ -43,6 +43,7 @@ SIGNATURES = {
     "ssmoe_moe_prefill": (_I, [_P, _P, _P, _I, _P, _I64, _P, _I64, _P, _I64, _P, _P, _P, _I64, _I, _I, _I, _I, _P]),
     "ssmoe_shared_hs": (_I, [_P, _I64, _I, _I, _P, _P, _P]),
     "ssmoe_combine_shared": (_I, [_P, _P, _P, _P, _I, _I, _P]),
+    "ssmoe_residual_rmsnorm": (_I, [_P, _P, _P, ctypes.c_float, _I, _I, _P, _P, _P]),
     "ssmoe_sample_workspace_bytes": (_I64, [_I]),
     "ssmoe_sample": (_I, [_P, _I, _P, _I, _F, _F, _I, _F, _F, _P, _P, _I64, _P, _P]),
     "ssmoe_accept_sampled_workspace_bytes": (_I64, [_I, _I]),

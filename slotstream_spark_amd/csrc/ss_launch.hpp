@@ -30,6 +30,8 @@ hipError_t launch_router_topk(const uint16_t* logits, const float* bias, float* 
 // y = bf16(bf16(routed) + bf16(bf16(sigmoid(sgl)) * sh)).
 hipError_t launch_shared_hs(const uint16_t* proj, int64_t ld, int T, int Is, uint16_t* hs, uint16_t* sgl,
                             hipStream_t st);
+hipError_t launch_residual_rmsnorm(const uint16_t* resid, const uint16_t* y, const uint16_t* w, float eps, int R,
+                                   int H, uint16_t* stream_out, uint16_t* mixed, hipStream_t st);
 hipError_t launch_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* sgl, uint16_t* y, int T,
                                  int H, hipStream_t st);
 

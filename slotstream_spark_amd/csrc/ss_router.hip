@@ -457,4 +457,72 @@ hipError_t launch_combine_shared(const float* routed, const uint16_t* sh, const 
   return hipGetLastError();
 }
 
+// ---------------------------------------------------------------- residual stream and RMSNorm between layers
+// s = bf16(resid + y): the residual add of GraphSet._moe (runtime/graphs.py:169) with one stream and unit injection;
+// mixed = bf16((s * r) * w), r = 1 / sqrt(sum(s^2) / H + eps): rmsnorm (model/reference_torch.py:30-38) with the
+// reduction order fixed. One wave per row: lane l accumulates s^2 over elements 512 j + 8 l .. 512 j + 8 l + 7,
+// j = 0, 1, ..., with fma from 0, then the xor butterfly. y == nullptr: s = resid (no add, nothing stored). The
+// second pass reads s back from stream_out (the lane's own stores), so stream_out may be resid itself.
+__global__ __launch_bounds__(256) void residual_rmsnorm_kernel(const uint16_t* resid, const uint16_t* __restrict__ y,
+                                                               const uint16_t* __restrict__ w, float eps, int R, int H,
+                                                               uint16_t* stream_out, uint16_t* __restrict__ mixed) {
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= R) return;  // whole waves; no workgroup barrier follows
+  const int h8 = H >> 3;
+  const uint4* xs = reinterpret_cast<const uint4*>(resid + (size_t)row * H);
+  uint4* so = y ? reinterpret_cast<uint4*>(stream_out + (size_t)row * H) : nullptr;
+  float acc = 0.f;
+  for (int k8 = lane; k8 < h8; k8 += 64) {
+    const uint4 a = xs[k8];
+    uint32_t v[4] = {a.x, a.y, a.z, a.w};
+    if (y) {
+      const uint4 b = reinterpret_cast<const uint4*>(y + (size_t)row * H)[k8];
+      const uint32_t bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const uint32_t lo = ss_f32_to_bf16(ss_bf16_to_f32(v[c] & 0xFFFFu) + ss_bf16_to_f32(bv[c] & 0xFFFFu));
+        const uint32_t hi = ss_f32_to_bf16(ss_bf16_to_f32(v[c] >> 16) + ss_bf16_to_f32(bv[c] >> 16));
+        v[c] = lo | (hi << 16);
+      }
+      so[k8] = make_uint4(v[0], v[1], v[2], v[3]);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float e0 = ss_bf16_to_f32(v[c] & 0xFFFFu), e1 = ss_bf16_to_f32(v[c] >> 16);
+      acc = fmaf(e0, e0, acc);
+      acc = fmaf(e1, e1, acc);
+    }
+  }
+  const float r = 1.f / sqrtf(ss_wave_sum(acc) / (float)H + eps);
+  const uint4* src = y ? reinterpret_cast<const uint4*>(so) : xs;
+  const uint4* ws = w ? reinterpret_cast<const uint4*>(w) : nullptr;
+  uint4* mo = reinterpret_cast<uint4*>(mixed + (size_t)row * H);
+  for (int k8 = lane; k8 < h8; k8 += 64) {
+    const uint4 a = src[k8];
+    const uint32_t v[4] = {a.x, a.y, a.z, a.w};
+    uint32_t wv[4] = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
+    if (ws) {
+      const uint4 b = ws[k8];
+      wv[0] = b.x, wv[1] = b.y, wv[2] = b.z, wv[3] = b.w;
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const uint32_t lo = ss_f32_to_bf16((ss_bf16_to_f32(v[c] & 0xFFFFu) * r) * ss_bf16_to_f32(wv[c] & 0xFFFFu));
+      const uint32_t hi = ss_f32_to_bf16((ss_bf16_to_f32(v[c] >> 16) * r) * ss_bf16_to_f32(wv[c] >> 16));
+      o[c] = lo | (hi << 16);
+    }
+    mo[k8] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+hipError_t launch_residual_rmsnorm(const uint16_t* resid, const uint16_t* y, const uint16_t* w, float eps, int R,
+                                   int H, uint16_t* stream_out, uint16_t* mixed, hipStream_t st) {
+  if (R == 0) return hipSuccess;
+  hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, st, resid, y, w, eps, R, H,
+                     stream_out, mixed);
+  return hipGetLastError();
+}
+
 }  // namespace ss

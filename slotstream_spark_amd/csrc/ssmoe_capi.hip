@@ -2,6 +2,7 @@
 // launches. No entry point allocates device memory or synchronises, except ssmoe_device_error.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <string>
@@ -527,6 +528,22 @@ int ssmoe_shared_hs(const uint16_t* proj, int64_t ld, int T, int Is, uint16_t* h
   if (T > 0 && (!proj || !hs || !sgl)) return fail(SSMOE_EINVAL, "proj, hs and sgl must be non-null");
   return hip_check(ss::launch_shared_hs(proj, ld, T, Is, hs, sgl, static_cast<hipStream_t>(stream)),
                    "shared_hs launch");
+}
+
+int ssmoe_residual_rmsnorm(const uint16_t* resid, const uint16_t* y, const uint16_t* weight, float eps, int R, int H,
+                           uint16_t* stream_out, uint16_t* mixed, void* stream) {
+  if (!resid || !mixed || (y && !stream_out)) return fail(SSMOE_EINVAL, "resid and mixed (and stream_out with y) must be non-null");
+  if (R < 0 || R > 65536 || H < 8 || H > 65536 || H % 8 != 0)
+    return fail(SSMOE_EINVAL, "need 0 <= R <= 65536 and H a multiple of 8 in [8, 65536] (got R=%d H=%d)", R, H);
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(SSMOE_EINVAL, "eps must be finite and >= 0");
+  if (!aligned(resid, 16) || !aligned(mixed, 16) || (y && !aligned(y, 16)) || (weight && !aligned(weight, 16)) ||
+      (stream_out && !aligned(stream_out, 16)))
+    return fail(SSMOE_EINVAL, "all rows must be 16-byte aligned");
+  if (mixed == resid || mixed == y || mixed == stream_out || (y && (y == stream_out)))
+    return fail(SSMOE_EINVAL, "mixed must not alias the stream, and y must not alias stream_out");
+  return hip_check(ss::launch_residual_rmsnorm(resid, y, weight, eps, R, H, stream_out, mixed,
+                                               static_cast<hipStream_t>(stream)),
+                   "residual_rmsnorm launch");
 }
 
 int ssmoe_combine_shared(const float* routed, const uint16_t* sh, const uint16_t* sgl, uint16_t* y, int T, int H,

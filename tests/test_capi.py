@@ -226,3 +226,18 @@ def test_gemv_rejects_bad_arguments(L):
     assert head(D=61) == EINVAL and b"D must be" in L.ssmoe_last_error()
     assert head(w=ws - 1) == EINVAL and b"workspace holds" in L.ssmoe_last_error()
     assert head(drafts=None) == EINVAL
+
+
+def test_residual_rmsnorm_rejects_bad_arguments(L):
+    p = ctypes.c_void_p(4096)
+    rr = L.ssmoe_residual_rmsnorm
+    assert rr(None, None, None, ctypes.c_float(1e-6), 2, 2048, None, p, None) == EINVAL
+    assert rr(p, p, None, ctypes.c_float(1e-6), 2, 2048, None, ctypes.c_void_p(8192), None) == EINVAL  # y, no stream_out
+    assert rr(p, None, None, ctypes.c_float(1e-6), 2, 2044, None, ctypes.c_void_p(8192), None) == EINVAL
+    assert rr(p, None, None, ctypes.c_float(-1.0), 2, 2048, None, ctypes.c_void_p(8192), None) == EINVAL
+    assert rr(p, None, None, ctypes.c_float(1e-6), 2, 2048, None, p, None) == EINVAL              # mixed aliases resid
+    assert rr(ctypes.c_void_p(4098), None, None, ctypes.c_float(1e-6), 2, 2048, None, p, None) == EINVAL  # misaligned
+    from slotstream_spark_amd.engine.step import residual_rmsnorm
+    x = torch.zeros(2, 2048, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU"):
+        residual_rmsnorm(x, None, torch.zeros_like(x))

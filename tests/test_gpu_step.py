@@ -1,0 +1,147 @@
+"""The whole verify round in one HIP graph (engine/step.py, MTPStepGraph) on the GPU: the residual + RMSNorm kernel
+against or_residual_rmsnorm bit for bit; graph replays equal to the eager launches on every replay, with eager
+work between replays; each layer of the chain against the oracle on that layer's own input (router ids and weights
+bit for bit, y within the north-star bound, the stream and the next norm bit for bit); the fused greedy round equal
+to or_accept_greedy on the kept logits; the head MoE equal to a separate verify call of map layer NL."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from slotstream_spark_amd.engine.step import MoEWeights, MTPStepGraph, residual_rmsnorm
+from slotstream_spark_amd.kernels.gemv_affine import AffineWeight
+from slotstream_spark_amd.memory.synth import LayerWeights, normal_bf16, zipf_bias
+from tests.gpu_util import DenseCache, bits, make_pool
+
+pytestmark = pytest.mark.gpu
+
+REL_Y = 2e-2
+H, I, E, K, NL, V = 2048, 512, 64, 4, 3, 12_352
+
+
+def _dev_bits(a):
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+
+
+@pytest.mark.parametrize("r,h,with_y,with_w,inplace", [(1, 2048, True, False, False), (4, 2048, True, True, False),
+                                                       (3, 2560, False, True, False), (5, 520, True, True, True),
+                                                       (9, 8, True, False, False), (2, 4096, False, False, False)])
+def test_residual_rmsnorm_bitwise(r, h, with_y, with_w, inplace):
+    print(f"[norm] R={r} H={h} y={with_y} w={with_w} inplace={inplace}", flush=True)
+    rng = np.random.default_rng(r * 1000 + h)
+    x = O.f32_to_bf16(rng.standard_normal((r, h)).astype(np.float32) * 3)
+    y = O.f32_to_bf16(rng.standard_normal((r, h)).astype(np.float32)) if with_y else None
+    w = O.f32_to_bf16(1 + 0.1 * rng.standard_normal(h).astype(np.float32)) if with_w else None
+    eps = 1e-6 if h > 8 else 0.5
+    so_ref, mx_ref = O.residual_rmsnorm(x, y, w, eps)
+    xt = _dev_bits(x)
+    so = xt if inplace else torch.empty_like(xt)
+    mx = torch.empty_like(xt)
+    residual_rmsnorm(xt, None if y is None else _dev_bits(y), mx, stream_out=so if with_y else None,
+                     weight=None if w is None else _dev_bits(w), eps=eps)
+    torch.cuda.synchronize()
+    assert np.array_equal(bits(mx), mx_ref)
+    if with_y:
+        assert np.array_equal(bits(so), so_ref)
+
+
+@pytest.fixture(scope="module")
+def step():
+    print(f"[step] {NL} layers + head, E={E} K={K}, lm_head {V} x {H}", flush=True)
+    pool = make_pool(E, H, I, seed=404, layers=NL + 1)
+    lws = [LayerWeights(H, E, 512, seed=410 + l) for l in range(NL + 1)]
+    mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, zipf_bias(E, 1.1, 420 + l))
+          for l, w in enumerate(lws)]
+    g = torch.Generator(device="cuda").manual_seed(430)
+    q = torch.randint(-2**31, 2**31 - 1, (V, H // 8), generator=g, device="cuda", dtype=torch.int32)
+    sc = (torch.randn((V, H // 64), generator=g, device="cuda") * 0.02).abs().to(torch.bfloat16)
+    lm = AffineWeight(q, sc, (-8 * sc.float()).to(torch.bfloat16), 4, 64, V, H)
+    norms = [None] + [normal_bf16((H,), 0.1, 440 + l) + 1 for l in range(NL)]
+    sg = MTPStepGraph(pool, mw[:NL], lm, depth=3, head=mw[NL], norm_weights=norms, top_k=K, keep_logits=True)
+    return pool, mw, lm, norms, sg
+
+
+def _snapshot(sg):
+    keep = [sg.out, sg.logits, sg.head_y, sg.head_ids, sg.ids, sg.weights] + sg.streams[1:] + sg.mixed + sg.ys
+    return [t.clone() for t in keep]
+
+
+def test_graph_replays_equal_eager(step):
+    _, _, _, _, sg = step
+    x1, x2 = normal_bf16((4, H), 1.0, 450), normal_bf16((4, H), 1.0, 451)
+    d1 = torch.tensor([5, 77, 4000], dtype=torch.int32, device="cuda")
+    d2 = torch.tensor([1, 2, 3], dtype=torch.int32, device="cuda")
+    ref = {}
+    for key, (x, d) in {"a": (x1, d1), "b": (x2, d2)}.items():
+        sg.x_in.copy_(x)
+        sg.drafts.copy_(d)
+        sg.run_eager()
+        torch.cuda.synchronize()
+        ref[key] = _snapshot(sg)
+    assert not torch.equal(ref["a"][1], ref["b"][1])
+    for i, key in enumerate(["a", "b", "a", "a", "b"]):
+        x, d = (x1, d1) if key == "a" else (x2, d2)
+        sg.step(x, d)
+        torch.cuda.synchronize()
+        got = _snapshot(sg)
+        for n, (u, v) in enumerate(zip(got, ref[key])):
+            assert torch.equal(u, v), (i, key, n)
+        torch.randn(1000, device="cuda").sum().item()     # eager work and a sync between replays
+
+
+def test_chain_against_oracle_layer_by_layer(step):
+    pool, mw, lm, norms, sg = step
+    sg.step(normal_bf16((4, H), 1.0, 452), torch.tensor([9, 99, 999], dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    m0_ref = O.residual_rmsnorm(bits(sg.x_in))[1]
+    assert np.array_equal(bits(sg.mixed[0]), m0_ref)
+    for l in range(NL):
+        xb = bits(sg.mixed[l])
+        w = mw[l]
+        _, _, rids, rw = O.router(xb, bits(w.router_w), K, w.router_bias.cpu().numpy())
+        assert np.array_equal(sg.ids[l].cpu().numpy(), rids), l
+        assert np.array_equal(sg.weights[l].cpu().numpy().view(np.uint32), rw.view(np.uint32)), l
+        routed = O.moe_routed_fp64(O.bf16_to_f32(xb), rids, rw, DenseCache(pool, layer=l)).astype(np.float32)
+        sh, sgl = O.shared_expert(xb, bits(w.sh_gate), bits(w.sh_up), bits(w.sh_down), bits(w.sh_g))
+        ry = O.combine_shared(routed, sh, sgl)
+        assert O.rel_l2(O.bf16_to_f32(bits(sg.ys[l])), O.bf16_to_f32(ry)) <= REL_Y, l
+        so, mx = O.residual_rmsnorm(bits(sg.streams[l]), bits(sg.ys[l]), bits(norms[l + 1]))
+        assert np.array_equal(bits(sg.streams[l + 1]), so), l
+        assert np.array_equal(bits(sg.mixed[l + 1]), mx), l
+    # the chain keeps its scale: every mixed row has unit RMS up to the norm weights
+    rms = O.bf16_to_f32(bits(sg.mixed[NL])).astype(np.float64)
+    assert np.all(np.abs(np.sqrt((rms ** 2).mean(axis=1)) - 1.0) < 0.1)
+
+
+def test_round_acceptance_and_logits(step):
+    pool, mw, lm, norms, sg = step
+    x = normal_bf16((4, H), 1.0, 453)
+    sg.step(x, torch.zeros(3, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    logits = sg.logits.cpu().numpy()
+    greedy = logits.argmax(axis=1).astype(np.int32)
+    for drafts in ([greedy[0], greedy[1], greedy[2]], [greedy[0], greedy[1] ^ 1, 7], [greedy[0] ^ 1, 0, 0]):
+        d = torch.tensor(drafts, dtype=torch.int32, device="cuda")
+        out = sg.step(x, d)
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), O.accept_greedy(logits, np.array(drafts, np.int32))), drafts
+        assert torch.equal(sg.logits.cpu(), torch.from_numpy(logits))
+    xm = O.bf16_to_f32(bits(sg.mixed[NL]))
+    y64, bound = O.gemv_affine4_fp64(xm, lm.q.cpu().numpy(), bits(lm.s), bits(lm.b))
+    assert np.max(np.abs(logits - y64) / bound) <= 2e-5
+    res = sg.result()
+    assert res.n_accept == 0 and res.n_emit == 1
+
+
+def test_head_moe_is_map_layer_nl(step):
+    pool, mw, lm, norms, sg = step
+    from slotstream_spark_amd.engine.verify import MoEVerifyLayer
+    sg.step(normal_bf16((4, H), 1.0, 454), torch.zeros(3, dtype=torch.int32, device="cuda"))
+    torch.cuda.synchronize()
+    w = mw[NL]
+    sep = MoEVerifyLayer(pool, NL, w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, top_k=K, router_bias=w.router_bias)
+    y, ids, wt = sep(sg.mixed[NL].clone())
+    torch.cuda.synchronize()
+    assert torch.equal(y, sg.head_y) and torch.equal(ids, sg.head_ids) and torch.equal(wt, sg.head_weights)
+    _, _, rids, _ = O.router(bits(sg.mixed[NL]), bits(w.router_w), K, w.router_bias.cpu().numpy())
+    assert np.array_equal(sg.head_ids.cpu().numpy(), rids)
