@@ -368,22 +368,21 @@ def pool_leg(dev, calls=4):
 
 def config4_leg(pool, weights, biases, steps, dev):
     """a 48-layer routed-MoE stack (config-1 shape, all experts resident) run as an MTP loop of
-    `steps` decode steps at T=2: per step, the 48 verify layers chained (layer l reads layer l-1's y) in one HIP
-    graph, then greedy acceptance (D=1) on that step's synthetic fp32 logits (vocab 151,936, rho=0.8 draft).
-    Effective tokens/s = emitted tokens / wall time of the whole loop, attention excluded."""
+    `steps` decode steps at T=2: per step, the 48 verify layers chained in one HIP graph (engine/step.py with the
+    lm_head left out: each launch stages the RMSNorm of the residual stream and writes the next stream, so the chain
+    keeps its scale and its routing stays well defined), then greedy acceptance (D=1) on that step's synthetic fp32
+    logits (vocab 151,936, rho=0.8 draft). Effective tokens/s = emitted tokens / wall time of the whole loop,
+    attention excluded."""
     import torch
 
     from slotstream_spark_amd.engine.accept import Acceptor, AcceptResult, RoundStats
-    from slotstream_spark_amd.engine.verify import MoEVerifyLayer
+    from slotstream_spark_amd.engine.step import MoEWeights, MTPStepGraph
     from slotstream_spark_amd.memory.synth import normal_bf16, verify_logits
 
     NL4, D, V, T = len(weights), 1, 151936, 2
-    layers = [MoEVerifyLayer(pool, l, w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, top_k=K, router_bias=b)
-              for l, (w, b) in enumerate(zip(weights, biases))]
-    xs = [normal_bf16((T, H), 1.0, 1735, dev)] + [torch.empty((T, H), dtype=torch.bfloat16, device=dev)
-                                                  for _ in range(NL4)]
-    ids = torch.empty((T, K), dtype=torch.int32, device=dev)
-    wts = torch.empty((T, K), dtype=torch.float32, device=dev)
+    mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, b) for w, b in zip(weights, biases)]
+    sg = MTPStepGraph(pool, mw, None, depth=D, top_k=K, device=dev)
+    sg.x_in.copy_(normal_bf16((T, H), 1.0, 1735, dev))
     tgt = torch.empty((steps, D + 1, V), device=dev)
     drf = torch.empty((steps, D, V), device=dev)
     for st in range(steps):
@@ -391,27 +390,15 @@ def config4_leg(pool, weights, biases, steps, dev):
     drafts = drf.argmax(dim=2).to(torch.int32).contiguous()
     acc = Acceptor(D, V, device=dev)
     out_g = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
-
-    def stack():
-        for l in range(NL4):
-            layers[l](xs[l], y=xs[l + 1], ids=ids, weights=wts)
-
-    s_ = torch.cuda.Stream(device=dev)
-    s_.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s_):
-        stack()
-    torch.cuda.current_stream().wait_stream(s_)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g, stream=s_):
-        stack()
+    sg.capture()
+    s_ = sg.stream
     with torch.cuda.stream(s_):
         for _ in range(2):
-            g.replay()
+            sg.graph.replay()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         ev0.record(s_)
         for st in range(steps):
-            g.replay()
+            sg.graph.replay()
             out_g[st].copy_(acc.greedy_async(tgt[st], drafts[st]))
         ev1.record(s_)
     torch.cuda.synchronize()
@@ -421,15 +408,18 @@ def config4_leg(pool, weights, biases, steps, dev):
         rs.add(D, AcceptResult.from_out(o))
     emitted = sum(rs.emitted_by_round)
     tok_s = emitted / (ms * 1e-3)
+    uniq = [len(set(sg.ids[l].cpu().flatten().tolist())) for l in range(NL4)]
+    finite = bool(torch.isfinite(sg.streams[NL4].float()).all().item())
     log(f"config4: {NL4} layers x {steps} steps in {ms:.1f} ms ({ms * 1000 / steps:.1f} us/step, "
-        f"{ms * 1000 / steps / NL4:.2f} us/layer); {emitted} tokens emitted, {tok_s:.0f} tokens/s")
+        f"{ms * 1000 / steps / NL4:.2f} us/layer); {emitted} tokens emitted, {tok_s:.0f} tokens/s; "
+        f"mean unique experts {sum(uniq) / NL4:.1f}, stream finite {finite}")
     return {"layers": NL4, "steps": steps, "tokens": T, "ms_total": round(ms, 3),
             "us_per_step": round(ms * 1000 / steps, 2), "us_per_layer": round(ms * 1000 / steps / NL4, 3),
             "emitted_tokens": emitted, "acceptance_length": round(rs.acceptance_length, 4),
-            "effective_tokens_per_s": round(tok_s, 1),
-            "resident_expert_bytes": NL4 * E * 1_769_472,
-            "timing": "one HIP graph of the 48 chained layers per step + greedy acceptance launches, events around "
-                      "the whole loop"}
+            "effective_tokens_per_s": round(tok_s, 1), "unique_experts_mean": round(sum(uniq) / NL4, 2),
+            "stream_finite": finite, "resident_expert_bytes": NL4 * E * 1_769_472,
+            "timing": "one HIP graph of the 48 chained layers (norm and residual add inside each verify launch) per "
+                      "step + greedy acceptance launches, events around the whole loop"}
 
 
 def traffic_of(kernel: str):

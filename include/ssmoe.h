@@ -97,6 +97,20 @@ int ssmoe_moe_verify_layer(const uint16_t* x, const uint16_t* router_w, const fl
                            int32_t* ids, float* weights, uint16_t* y, float* routed_out, int T, int H, int I, int Is,
                            int K, int E, void* stream);
 
+/* One layer of a chain of MoE layers: the layer of ssmoe_moe_verify_layer run on
+ * x = bf16(rmsnorm(stream_in) * norm_w) (exactly ssmoe_residual_rmsnorm with y NULL; norm_w NULL = ones), and, when
+ * stream_out is non-null, stream_out = bf16(stream_in + y), the residual stream of the next layer. The norm of the next
+ * seg_router and the residual add of GraphSet._moe (runtime/graphs.py:169, one stream, unit injection) folded into
+ * the verify launch, so a chain needs no launch between layers. H a multiple of 512; stream_out must not alias
+ * stream_in or y. */
+int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm_w, float eps,
+                                 const uint16_t* router_w, const float* router_bias, const uint16_t* sh_gate,
+                                 const uint16_t* sh_up, const uint16_t* sh_down, const uint16_t* sh_g, int layer,
+                                 const int32_t* map, int64_t map_len, const int64_t* slot_ptr, int64_t n_slots,
+                                 void* workspace, int64_t workspace_bytes, int32_t* ids, float* weights, uint16_t* y,
+                                 uint16_t* stream_out, float* routed_out, int T, int H, int I, int Is, int K, int E,
+                                 void* stream);
+
 /* Bytes of the workspace the acceptance entry points need (1 <= V <= 1,048,576, 0 <= D <= 60). */
 int64_t ssmoe_accept_workspace_bytes(int D, int V);
 

@@ -68,6 +68,13 @@ struct VerifyArgs {
   int T, H, I, Is, K, E;
   int* err;
   uint64_t* trace;          // null, or [grid][16] phase timestamps (s_memrealtime, 100 MHz)
+  // Chained layers (verify mode, bf16 x): with norm_in, x is the residual stream and the layer runs on
+  // bf16((x * r) * norm_w), r = 1 / sqrt(sum(x^2) / H + norm_eps) (the order of ssmoe_residual_rmsnorm; norm_w null =
+  // ones); with x_plus_y the combine also writes bf16(x + y) [T, H] there.
+  int norm_in;
+  const uint16_t* norm_w;
+  float norm_eps;
+  uint16_t* x_plus_y;
 };
 size_t verify_scratch_bytes(int T, int H, int I, int Is, int K, int E);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);

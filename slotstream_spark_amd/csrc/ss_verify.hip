@@ -190,6 +190,7 @@ struct VSmem {
   float gx[64][kTBv];             // x group sums (H <= 4096)
   float hsum[kMaxQv][16];         // h group sums per use (I <= 1024)
   float shv[16][kTBv];
+  float rnorm[kTBv];              // 1 / rms of each token (chained layers)
   float xch[4][16 * kTBv];        // per-wave exchange of one item's 16 columns x 4 tokens
   alignas(16) int ekey[64];       // unique_setup keys
   int nt, nu;
@@ -366,10 +367,22 @@ SS_DEV int xfrag_index(int kb, int t) {
 
 // Stage the x fragments (into xfl) and the 64-element group sums of x (into s.gx, sequential in element order).
 // Every global load of a thread is issued before its first use; tokens t >= nt read token 0 and are zeroed.
+// With a.norm_in (bf16 x only) every element is first replaced by bf16((x * r_t) * norm_w): wave w computes r of
+// token w in the ssmoe_residual_rmsnorm order (lane l: elements 512 j + 8 l .. + 7 by fma from 0, then the
+// butterfly), so every workgroup stages the same values the separate norm kernel would write.
 template <int NJG, bool XF32>
-SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], int nt) {
+SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], float* rnorm, int nt) {
   const int tid = threadIdx.x;
   const int H = a.H;
+  constexpr int NJX = NJG / 4;
+  const bool norm = !XF32 && a.norm_in;
+  uint4 nv[NJX];
+  if (norm) {
+    const int tn = (tid >> 6) < nt ? (tid >> 6) : 0;
+#pragma unroll
+    for (int jj = 0; jj < NJX; ++jj)
+      nv[jj] = ldg16(static_cast<const uint16_t*>(a.x) + (size_t)tn * H + 8 * (64 * jj + (tid & 63)));
+  }
   constexpr int NF = NJG * 16 * kTBv;  // (j, i, g, t)
   constexpr int FPT = NF / 256;
   static_assert(NF % 256 == 0, "whole fragment entries per thread");
@@ -402,6 +415,43 @@ SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], int nt) 
       gv[k] = ldg16(static_cast<const uint16_t*>(a.x) + (size_t)gt * H + 64 * Gi + 8 * k);
   }
   __builtin_amdgcn_sched_barrier(0);
+  if (norm) {
+    float acc = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < NJX; ++jj) {
+      const uint32_t v[4] = {nv[jj].x, nv[jj].y, nv[jj].z, nv[jj].w};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float e0 = bf_lo(v[c]), e1 = bf_hi(v[c]);
+        acc = fmaf(e0, e0, acc);
+        acc = fmaf(e1, e1, acc);
+      }
+    }
+    const float ssum = ss_wave_sum(acc);
+    if ((tid & 63) == 0) rnorm[tid >> 6] = 1.f / sqrtf(ssum / (float)H + a.norm_eps);
+    __syncthreads();
+    // bf16((v * r) * w) of the 8 elements of a 16-byte word, w from norm_w at element k0 (ones when null)
+    auto scale8 = [&](uint4 v, float r, int k0) {
+      uint4 wv = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+      if (a.norm_w) wv = ldg16(a.norm_w + k0);
+      const uint32_t x4[4] = {v.x, v.y, v.z, v.w}, w4[4] = {wv.x, wv.y, wv.z, wv.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        o[c] = ss_f32_to_bf16((bf_lo(x4[c]) * r) * bf_lo(w4[c])) |
+               (ss_f32_to_bf16((bf_hi(x4[c]) * r) * bf_hi(w4[c])) << 16);
+      return make_uint4(o[0], o[1], o[2], o[3]);
+    };
+#pragma unroll
+    for (int k = 0; k < FPT; ++k) {
+      const int f = tid + 256 * k;
+      const int t = f & 3, gg = (f >> 2) & 3, i = (f >> 4) & 3, j = f >> 6;
+      const int tt = t < nt ? t : 0;
+      fv[k][0] = scale8(fv[k][0], rnorm[tt], 128 * j + 32 * gg + 8 * i);
+    }
+#pragma unroll
+    for (int k = 0; k < GV; ++k) gv[k] = scale8(gv[k], rnorm[gt], 64 * Gi + 8 * k);
+  }
 #pragma unroll
   for (int k = 0; k < FPT; ++k) {
     const int f = tid + 256 * k;
@@ -623,7 +673,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       slot_e[k] = ok ? v : -1;
     }
   }
-  stage_x<NJG, XF32>(a, xfl, s.gx, nt);
+  stage_x<NJG, XF32>(a, xfl, s.gx, s.rnorm, nt);
   __syncthreads();
   if (verify) {
 #pragma unroll 1
@@ -1022,7 +1072,12 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
           const float sgx = ss_bf16_to_f32(sgl_pre);
           const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-sgx)));
           const float sh2 = ss_round_bf16(sgv * shb);
-          a.y[(size_t)r * H + 16 * bid + c] = (uint16_t)ss_f32_to_bf16(ss_round_bf16(acc) + sh2);
+          const uint32_t yb = ss_f32_to_bf16(ss_round_bf16(acc) + sh2);
+          a.y[(size_t)r * H + 16 * bid + c] = (uint16_t)yb;
+          if (a.x_plus_y) {  // the residual stream of the next layer
+            const float xv = ss_bf16_to_f32(static_cast<const uint16_t*>(a.x)[(size_t)r * H + 16 * bid + c]);
+            a.x_plus_y[(size_t)r * H + 16 * bid + c] = (uint16_t)ss_f32_to_bf16(xv + ss_bf16_to_f32(yb));
+          }
         }
       }
     }

@@ -230,12 +230,13 @@ int64_t ssmoe_verify_workspace_bytes(int T, int H, int I, int Is, int K, int E) 
   return (int64_t)ss::verify_scratch_bytes(kBlock, H, I, Is, K, E);
 }
 
-int ssmoe_moe_verify_layer(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
-                           const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
-                           const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,
-                           const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes,
-                           int32_t* ids, float* weights, uint16_t* y, float* routed_out, int T, int H, int I, int Is,
-                           int K, int E, void* stream) {
+static int verify_layer_impl(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
+                             const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
+                             const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,
+                             const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes,
+                             int32_t* ids, float* weights, uint16_t* y, float* routed_out, int T, int H, int I, int Is,
+                             int K, int E, void* stream, int norm_in, const uint16_t* norm_w, float norm_eps,
+                             uint16_t* x_plus_y) {
   if (int rc = check_moe_shape(T, H, I, K, E)) return rc;
   if (E > 512 || K > E) return fail(SSMOE_EINVAL, "need K <= E <= 512, got K=%d E=%d", K, E);
   if (Is < 8 || Is % 8 || Is > 512) return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, 512], got %d", Is);
@@ -282,9 +283,42 @@ int ssmoe_moe_verify_layer(const uint16_t* x, const uint16_t* router_w, const fl
     a.E = E;
     a.err = err;
     a.trace = g_trace;
+    a.norm_in = norm_in;
+    a.norm_w = norm_w;
+    a.norm_eps = norm_eps;
+    a.x_plus_y = x_plus_y ? x_plus_y + (size_t)r0 * H : nullptr;
     if (int rc = hip_check(ss::launch_verify(a, st), "verify layer launch")) return rc;
   }
   return ok();
+}
+
+int ssmoe_moe_verify_layer(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
+                           const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
+                           const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,
+                           const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes,
+                           int32_t* ids, float* weights, uint16_t* y, float* routed_out, int T, int H, int I, int Is,
+                           int K, int E, void* stream) {
+  return verify_layer_impl(x, router_w, router_bias, sh_gate, sh_up, sh_down, sh_g, layer, map, map_len, slot_ptr,
+                           n_slots, workspace, workspace_bytes, ids, weights, y, routed_out, T, H, I, Is, K, E, stream,
+                           0, nullptr, 0.f, nullptr);
+}
+
+int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm_w, float eps,
+                                 const uint16_t* router_w, const float* router_bias, const uint16_t* sh_gate,
+                                 const uint16_t* sh_up, const uint16_t* sh_down, const uint16_t* sh_g, int layer,
+                                 const int32_t* map, int64_t map_len, const int64_t* slot_ptr, int64_t n_slots,
+                                 void* workspace, int64_t workspace_bytes, int32_t* ids, float* weights, uint16_t* y,
+                                 uint16_t* stream_out, float* routed_out, int T, int H, int I, int Is, int K, int E,
+                                 void* stream) {
+  if (H % 512 != 0) return fail(SSMOE_EINVAL, "chained layers need H a multiple of 512, got %d", H);
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(SSMOE_EINVAL, "eps must be finite and >= 0");
+  if (norm_w && !aligned(norm_w, 16)) return fail(SSMOE_EINVAL, "norm_w must be 16-byte aligned");
+  if (stream_out && (stream_out == stream_in || stream_out == y))
+    return fail(SSMOE_EINVAL, "stream_out must not alias stream_in or y (other workgroups still read stream_in)");
+  if (stream_out && !aligned(stream_out, 16)) return fail(SSMOE_EINVAL, "stream_out must be 16-byte aligned");
+  return verify_layer_impl(stream_in, router_w, router_bias, sh_gate, sh_up, sh_down, sh_g, layer, map, map_len,
+                           slot_ptr, n_slots, workspace, workspace_bytes, ids, weights, y, routed_out, T, H, I, Is, K,
+                           E, stream, 1, norm_w, eps, stream_out);
 }
 
 int64_t ssmoe_accept_workspace_bytes(int D, int V) {

@@ -70,11 +70,15 @@ class MTPStepGraph:
     `pool` holds the records of every layer and, when `head` is given, of map layer len(layers) (the MTP layer shares
     the table, runtime/pool.py:37-38). `norm_weights` (len(layers) + 1 bf16 [H] tensors, or None for ones) are the
     norms before each MoE and before the lm_head. Fill `x_in` [rows, H] bf16 and `drafts` int32 [depth], then
-    `step()`; `result()` reads back the AcceptResult. `keep_logits` keeps the fp32 logits [rows, V] in `logits`."""
+    `step()`; `result()` reads back the AcceptResult. `keep_logits` keeps the fp32 logits [rows, V] in `logits`.
+    `fused` folds each norm and residual add into the verify launch (ssmoe_moe_verify_layer_chain, one launch per
+    layer, `mixed[l]` for l < NL then not written); `fused=False` runs ssmoe_residual_rmsnorm between the layers.
+    Both give the same bits. `lm_head=None` leaves the lm_head and the acceptance out of the graph."""
 
     def __init__(self, pool, layers: list[MoEWeights], lm_head: AffineWeight, depth: int,
                  head: MoEWeights | None = None, norm_weights: list[torch.Tensor | None] | None = None,
-                 eps: float = 1e-6, top_k: int = 10, keep_logits: bool = False, device="cuda"):
+                 eps: float = 1e-6, top_k: int = 10, keep_logits: bool = False, fused: bool = True,
+                 device="cuda"):
         if not 1 <= depth <= 3:
             raise ValueError("depth must be 1..3 (the verify kernel takes up to 4 rows)")
         self.depth, self.rows = depth, depth + 1
@@ -84,10 +88,11 @@ class MTPStepGraph:
         if pool.map.numel() < (self.nl + (1 if head is not None else 0)) * pool.experts:
             raise ValueError("the pool's map has fewer layers than the step needs")
         H = pool.hidden
-        if lm_head.k != H:
+        if lm_head is not None and lm_head.k != H:
             raise ValueError(f"lm_head takes K = {lm_head.k}, the layers H = {H}")
         self.device = torch.device(device)
         self.eps = float(eps)
+        self.fused = bool(fused)
         self.norm_weights = list(norm_weights) if norm_weights is not None else [None] * (self.nl + 1)
         if len(self.norm_weights) != self.nl + 1:
             raise ValueError(f"need {self.nl + 1} norm weights (one per layer and the final norm)")
@@ -110,21 +115,29 @@ class MTPStepGraph:
         self.head_y = torch.zeros((R, H), **bf)
         self.head_ids = torch.zeros((R, top_k), dtype=torch.int32, device=dev)
         self.head_weights = torch.zeros((R, top_k), dtype=torch.float32, device=dev)
-        self.logits = torch.zeros((R, lm_head.n), dtype=torch.float32, device=dev) if keep_logits else None
-        self.lm_head = LMHeadGreedy(lm_head, depth, device=dev)
-        self.out = self.lm_head.out
+        self.logits = (torch.zeros((R, lm_head.n), dtype=torch.float32, device=dev)
+                       if keep_logits and lm_head is not None else None)
+        self.lm_head = LMHeadGreedy(lm_head, depth, device=dev) if lm_head is not None else None
+        self.out = self.lm_head.out if lm_head is not None else None
         self.stream = torch.cuda.Stream(device=dev)
         self.graph = None
 
     def _body(self) -> None:
         """Every launch of the round on the current stream, reading only the static buffers."""
         w = self.norm_weights
-        residual_rmsnorm(self.x_in, None, self.mixed[0], weight=w[0], eps=self.eps)
-        for l, layer in enumerate(self.layers):
-            layer(self.mixed[l], y=self.ys[l], ids=self.ids[l], weights=self.weights[l])
-            residual_rmsnorm(self.streams[l], self.ys[l], self.mixed[l + 1], stream_out=self.streams[l + 1],
-                             weight=w[l + 1], eps=self.eps)
-        self.lm_head.run_async(self.mixed[self.nl], self.drafts, logits=self.logits)
+        if self.fused:
+            for l, layer in enumerate(self.layers):
+                layer.chain(self.streams[l], self.ys[l], self.ids[l], self.weights[l], stream_out=self.streams[l + 1],
+                            norm_weight=w[l], eps=self.eps)
+            residual_rmsnorm(self.streams[self.nl], None, self.mixed[self.nl], weight=w[self.nl], eps=self.eps)
+        else:
+            residual_rmsnorm(self.x_in, None, self.mixed[0], weight=w[0], eps=self.eps)
+            for l, layer in enumerate(self.layers):
+                layer(self.mixed[l], y=self.ys[l], ids=self.ids[l], weights=self.weights[l])
+                residual_rmsnorm(self.streams[l], self.ys[l], self.mixed[l + 1], stream_out=self.streams[l + 1],
+                                 weight=w[l + 1], eps=self.eps)
+        if self.lm_head is not None:
+            self.lm_head.run_async(self.mixed[self.nl], self.drafts, logits=self.logits)
         if self.head is not None:
             self.head(self.mixed[self.nl], y=self.head_y, ids=self.head_ids, weights=self.head_weights)
 

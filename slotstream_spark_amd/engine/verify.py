@@ -62,3 +62,33 @@ class MoEVerifyLayer:
             _lib.ptr(routed), t, self.hidden, self.inter, self.shared_inter, self.top_k, self.experts,
             _lib.stream_of(x)))
         return y, ids, weights
+
+    def chain(self, stream: torch.Tensor, y: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
+              stream_out: torch.Tensor | None = None, norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+              routed: torch.Tensor | None = None):
+        """The layer on bf16(rmsnorm(stream) * norm_weight), writing y and, when given, stream_out = bf16(stream + y):
+        one launch per layer of a chain (ssmoe_moe_verify_layer_chain), the same values as residual_rmsnorm followed
+        by __call__."""
+        t = stream.shape[0]
+        for name, b in (("stream", stream), ("y", y), ("stream_out", stream_out)):
+            if b is not None and (b.dtype != torch.bfloat16 or tuple(b.shape) != (t, self.hidden)
+                                  or not b.is_contiguous() or not b.is_cuda):
+                raise ValueError(f"{name} must be a contiguous bf16 [T, {self.hidden}] GPU tensor")
+        if t > self.max_tokens:
+            raise ValueError(f"at most {self.max_tokens} tokens per call, got {t}")
+        if tuple(ids.shape) != (t, self.top_k) or ids.dtype != torch.int32 or not ids.is_contiguous():
+            raise ValueError(f"ids must be contiguous int32 [{t}, {self.top_k}]")
+        if tuple(weights.shape) != (t, self.top_k) or weights.dtype != torch.float32 or not weights.is_contiguous():
+            raise ValueError(f"weights must be contiguous fp32 [{t}, {self.top_k}]")
+        if norm_weight is not None and (norm_weight.dtype != torch.bfloat16 or norm_weight.numel() != self.hidden):
+            raise ValueError(f"norm_weight must be bf16 [{self.hidden}]")
+        if routed is not None and (tuple(routed.shape) != (t, self.hidden) or routed.dtype != torch.float32):
+            raise ValueError(f"routed must be fp32 [{t}, {self.hidden}]")
+        _lib.check(_lib.lib().ssmoe_moe_verify_layer_chain(
+            stream.data_ptr(), _lib.ptr(norm_weight), float(eps), self.router_w.data_ptr(), _lib.ptr(self.router_bias),
+            self.sh_gate.data_ptr(), self.sh_up.data_ptr(), self.sh_down.data_ptr(), self.sh_g.data_ptr(), self.layer,
+            self.pool.map.data_ptr(), self.pool.map.numel(), self.pool.slot_ptr.data_ptr(), self.pool.slot_ptr.numel(),
+            self.workspace.data_ptr(), self.workspace.numel(), ids.data_ptr(), weights.data_ptr(), y.data_ptr(),
+            _lib.ptr(stream_out), _lib.ptr(routed), t, self.hidden, self.inter, self.shared_inter, self.top_k,
+            self.experts, _lib.stream_of(stream)))
+        return y, ids, weights

@@ -241,3 +241,15 @@ def test_residual_rmsnorm_rejects_bad_arguments(L):
     x = torch.zeros(2, 2048, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="GPU"):
         residual_rmsnorm(x, None, torch.zeros_like(x))
+
+
+def test_verify_chain_rejects_bad_arguments(L):
+    p = ctypes.c_void_p(1 << 20)
+    f = ctypes.c_float
+    args = lambda H, eps, so: (p, None, f(eps), p, None, p, p, p, p, 0, p, 512, p, 512, p, 1 << 24, p, p, p, so, None,
+                               2, H, 512, 512, 10, 512, None)
+    assert L.ssmoe_moe_verify_layer_chain(*args(2304, 1e-6, None)) == EINVAL          # H not a multiple of 512
+    assert b"multiple of 512" in L.ssmoe_last_error()
+    assert L.ssmoe_moe_verify_layer_chain(*args(2048, -1.0, None)) == EINVAL
+    assert L.ssmoe_moe_verify_layer_chain(*args(2048, 1e-6, p)) == EINVAL             # stream_out aliases stream_in
+    assert b"alias" in L.ssmoe_last_error()

@@ -61,9 +61,32 @@ def step():
     return pool, mw, lm, norms, sg
 
 
+@pytest.fixture(scope="module")
+def step_unfused(step):
+    pool, mw, lm, norms, _ = step
+    return MTPStepGraph(pool, mw[:NL], lm, depth=3, head=mw[NL], norm_weights=norms, top_k=K, keep_logits=True,
+                        fused=False)
+
+
 def _snapshot(sg):
-    keep = [sg.out, sg.logits, sg.head_y, sg.head_ids, sg.ids, sg.weights] + sg.streams[1:] + sg.mixed + sg.ys
+    keep = [sg.out, sg.logits, sg.head_y, sg.head_ids, sg.ids, sg.weights, sg.mixed[NL]] + sg.streams[1:] + sg.ys
     return [t.clone() for t in keep]
+
+
+def test_fused_chain_equals_separate_norm_launches(step, step_unfused):
+    """ssmoe_moe_verify_layer_chain (norm staged inside the verify launch, residual add in its combine) gives the
+    same bits as ssmoe_residual_rmsnorm + ssmoe_moe_verify_layer."""
+    _, _, _, _, sg = step
+    x = normal_bf16((4, H), 1.0, 455)
+    d = torch.tensor([3, 30, 300], dtype=torch.int32, device="cuda")
+    for g in (sg, step_unfused):
+        g.step(x, d)
+        torch.cuda.synchronize()
+    for n, (u, v) in enumerate(zip(_snapshot(sg), _snapshot(step_unfused))):
+        assert torch.equal(u, v), n
+    for l in range(NL + 1):   # the unfused graph wrote every norm: the fused launch staged the same inputs
+        want = O.residual_rmsnorm(bits(sg.streams[l]), None, None if step[3][l] is None else bits(step[3][l]))[1]
+        assert np.array_equal(bits(step_unfused.mixed[l]), want), l
 
 
 def test_graph_replays_equal_eager(step):
@@ -93,10 +116,9 @@ def test_chain_against_oracle_layer_by_layer(step):
     pool, mw, lm, norms, sg = step
     sg.step(normal_bf16((4, H), 1.0, 452), torch.tensor([9, 99, 999], dtype=torch.int32, device="cuda"))
     torch.cuda.synchronize()
-    m0_ref = O.residual_rmsnorm(bits(sg.x_in))[1]
-    assert np.array_equal(bits(sg.mixed[0]), m0_ref)
     for l in range(NL):
-        xb = bits(sg.mixed[l])
+        # the layer's input: the norm of its residual stream (staged inside the fused launch, recomputed here)
+        xb = O.residual_rmsnorm(bits(sg.streams[l]), None, None if norms[l] is None else bits(norms[l]))[1]
         w = mw[l]
         _, _, rids, rw = O.router(xb, bits(w.router_w), K, w.router_bias.cpu().numpy())
         assert np.array_equal(sg.ids[l].cpu().numpy(), rids), l
@@ -107,7 +129,7 @@ def test_chain_against_oracle_layer_by_layer(step):
         assert O.rel_l2(O.bf16_to_f32(bits(sg.ys[l])), O.bf16_to_f32(ry)) <= REL_Y, l
         so, mx = O.residual_rmsnorm(bits(sg.streams[l]), bits(sg.ys[l]), bits(norms[l + 1]))
         assert np.array_equal(bits(sg.streams[l + 1]), so), l
-        assert np.array_equal(bits(sg.mixed[l + 1]), mx), l
+    assert np.array_equal(bits(sg.mixed[NL]), mx)
     # the chain keeps its scale: every mixed row has unit RMS up to the norm weights
     rms = O.bf16_to_f32(bits(sg.mixed[NL])).astype(np.float64)
     assert np.all(np.abs(np.sqrt((rms ** 2).mean(axis=1)) - 1.0) < 0.1)
