@@ -47,11 +47,12 @@ SS_DEV void stg16(void* p, uint4 v) {
 SS_DEV float ss_bf16_to_f32(uint32_t b) { return __uint_as_float((b & 0xFFFFu) << 16); }
 
 // Round to nearest even; NaN stays a quiet NaN with its sign.
+// Round to nearest even with the hardware conversion (v_cvt_pk_bf16_f32), NaN -> the input's high half with the
+// quiet bit set (selected, not branched on).
 SS_DEV uint32_t ss_f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return ((u >> 16) | 0x40u) & 0xFFFFu;
-  u += 0x7FFFu + ((u >> 16) & 1u);
-  return u >> 16;
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t h = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  return (u & 0x7FFFFFFFu) > 0x7F800000u ? (((u >> 16) | 0x40u) & 0xFFFFu) : h;
 }
 
 SS_DEV float ss_round_bf16(float f) { return ss_bf16_to_f32(ss_f32_to_bf16(f)); }

@@ -409,6 +409,7 @@ SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], float* r
   const int Gi = q >> 2;
 #pragma unroll
   for (int k = 0; k < GV; ++k) {
+    if (norm) break;  // the norm path sums the staged values instead
     if (XF32)
       gv[k] = ldg16(static_cast<const float*>(a.x) + (size_t)gt * H + 64 * Gi + 4 * k);
     else
@@ -430,16 +431,22 @@ SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], float* r
     const float ssum = ss_wave_sum(acc);
     if ((tid & 63) == 0) rnorm[tid >> 6] = 1.f / sqrtf(ssum / (float)H + a.norm_eps);
     __syncthreads();
-    // bf16((v * r) * w) of the 8 elements of a 16-byte word, w from norm_w at element k0 (ones when null)
+    // bf16((v * r) * w) of the 8 elements of a 16-byte word (w = norm_w at element k0; without norm_w, bf16(v * r))
     auto scale8 = [&](uint4 v, float r, int k0) {
-      uint4 wv = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-      if (a.norm_w) wv = ldg16(a.norm_w + k0);
-      const uint32_t x4[4] = {v.x, v.y, v.z, v.w}, w4[4] = {wv.x, wv.y, wv.z, wv.w};
+      const uint32_t x4[4] = {v.x, v.y, v.z, v.w};
       uint32_t o[4];
+      if (a.norm_w) {
+        const uint4 wv = ldg16(a.norm_w + k0);
+        const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        o[c] = ss_f32_to_bf16((bf_lo(x4[c]) * r) * bf_lo(w4[c])) |
-               (ss_f32_to_bf16((bf_hi(x4[c]) * r) * bf_hi(w4[c])) << 16);
+        for (int c = 0; c < 4; ++c)
+          o[c] = ss_f32_to_bf16((bf_lo(x4[c]) * r) * bf_lo(w4[c])) |
+                 (ss_f32_to_bf16((bf_hi(x4[c]) * r) * bf_hi(w4[c])) << 16);
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          o[c] = ss_f32_to_bf16(bf_lo(x4[c]) * r) | (ss_f32_to_bf16(bf_hi(x4[c]) * r) << 16);
+      }
       return make_uint4(o[0], o[1], o[2], o[3]);
     };
 #pragma unroll
@@ -449,8 +456,6 @@ SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], float* r
       const int tt = t < nt ? t : 0;
       fv[k][0] = scale8(fv[k][0], rnorm[tt], 128 * j + 32 * gg + 8 * i);
     }
-#pragma unroll
-    for (int k = 0; k < GV; ++k) gv[k] = scale8(gv[k], rnorm[gt], 64 * Gi + 8 * k);
   }
 #pragma unroll
   for (int k = 0; k < FPT; ++k) {
@@ -473,6 +478,28 @@ SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], float* r
       const uint4 pv = perm_pairs(fv[k][0]);
       xfl[f] = make_uint4(live ? pv.x : 0u, live ? pv.y : 0u, live ? pv.z : 0u, live ? pv.w : 0u);
     }
+  }
+  if (norm) {
+    // The group sums of the normalised values, read back in element order from the staged fragments (entry
+    // elements e0..e7 are the halves lo(x) lo(y) lo(z) lo(w) hi(x) hi(y) hi(z) hi(w)).
+    __syncthreads();
+    if (tid < (H >> 6) * kTBv) {
+      float sum = 0.f;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint4 v = xfl[xfrag_index(64 * Gi + 8 * k, gt)];
+        sum = sum + bf_lo(v.x);
+        sum = sum + bf_lo(v.y);
+        sum = sum + bf_lo(v.z);
+        sum = sum + bf_lo(v.w);
+        sum = sum + bf_hi(v.x);
+        sum = sum + bf_hi(v.y);
+        sum = sum + bf_hi(v.z);
+        sum = sum + bf_hi(v.w);
+      }
+      gx[Gi][q & 3] = (q & 3) < nt ? sum : 0.f;
+    }
+    return;
   }
   if (tid < (H >> 6) * kTBv) {
     float sum = 0.f;
