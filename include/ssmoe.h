@@ -111,7 +111,9 @@ int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm
                                  uint16_t* stream_out, float* routed_out, int T, int H, int I, int Is, int K, int E,
                                  void* stream);
 
-/* Bytes of the workspace the acceptance entry points need (1 <= V <= 1,048,576, 0 <= D <= 60). */
+/* Bytes of the workspace the acceptance entry points need (1 <= V <= 1,048,576, 0 <= D <= 60). Its first 16384
+ * bytes hold cross-workgroup arrival counters: they must be zero before the first call (allocate
+ * the workspace zeroed), and every call leaves them zero. Calls that share a workspace must not overlap. */
 int64_t ssmoe_accept_workspace_bytes(int D, int V);
 
 /* Greedy verify acceptance. Replaces the acceptance loop of _mtp_decode (engine/generate.py:208-229) with

@@ -20,6 +20,12 @@ namespace ss {
 
 constexpr int kSub = 16;
 constexpr int kChunk = 64 * kSub;
+constexpr int kMaxRows = 128;        // 2 D + 1 <= 121
+constexpr int kArrShards = 32;       // arrival counters: shards of one counter, 128 bytes apart
+constexpr int kArrStride = 32;       // ints
+constexpr int kArrCounters = 3;      // greedy, p/q sums, p/q residual
+constexpr int kHeadFloats = 4096;  // 16 KB: kArrCounters x (kArrShards + 1) x kArrStride ints and spare
+static_assert(kArrCounters * (kArrShards + 1) * kArrStride <= kHeadFloats, "header");
 
 // Output header: out[0] n_accept, out[1] n_emit, out[2] uniforms used, out[3] flags, out[4..] tokens.
 enum { OUT_NACC = 0, OUT_NEMIT = 1, OUT_NUNI = 2, OUT_FLAGS = 3, OUT_TOK = 4 };
@@ -30,28 +36,84 @@ SS_DEV int nchunks_of(int V) { return (V + kChunk - 1) / kChunk; }
 int64_t accept_work_floats(int D, int V) {
   const int nch = (V + kChunk - 1) / kChunk;
   const int rows = 2 * D + 1;
-  return (int64_t)rows * nch * 3 + (int64_t)nch * 65 + 64;
+  return kHeadFloats + (int64_t)rows * nch * 3 + (int64_t)nch * 65 + 64;
 }
 
-// Workspace layout (floats).
+// Workspace layout (floats). The header holds the arrival counters of the launches whose last workgroup finishes
+// the round; it must be zero before the first call, and every launch sequence leaves it zero.
 struct Work {
-  float* cmax;   // [rows][nch]
-  float* cbad;   // [rows][nch]
-  float* ctot;   // [rows][nch]
-  float* stot;   // [nch][64]  sub-chunk totals of the sampled row
-  float* rtot;   // [nch]      chunk totals of the sampled row
-  float* state;  // [64]
+  int* ctr;         // arrival counters (header)
+  float* cmax;      // [rows][nch] chunk maxima (greedy: the maximum's value)
+  float* cbad;      // [rows][nch] chunk holds a non-finite value
+  float* ctot;      // [rows][nch] chunk totals (greedy: the maximum's index)
+  float* stot;      // [nch][64]  sub-chunk totals of the sampled row
+  float* rtot;      // [nch]      chunk totals of the sampled row
+  float* state;     // [64]
 };
 
 SS_DEV Work work_of(float* w, int rows, int nch) {
   Work k;
-  k.cmax = w;
-  k.cbad = w + (size_t)rows * nch;
-  k.ctot = w + (size_t)rows * nch * 2;
-  k.stot = w + (size_t)rows * nch * 3;
+  k.ctr = reinterpret_cast<int*>(w);
+  float* b = w + kHeadFloats;
+  k.cmax = b;
+  k.cbad = b + (size_t)rows * nch;
+  k.ctot = b + (size_t)rows * nch * 2;
+  k.stot = b + (size_t)rows * nch * 3;
   k.rtot = k.stot + (size_t)nch * 64;
   k.state = k.rtot + nch;
   return k;
+}
+
+template <class T>
+SS_DEV void st_ag(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+SS_DEV T ld_ag(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One-wave workgroups: true (in every lane) for the workgroup that arrives last of `total` at counter c. Arrivals
+// are counted on up to 32 shards (workgroup `id` on shard id % shards, each shard on its own 128-byte line), and the
+// workgroup completing a shard counts on the top counter, so no address takes more than total / 32 + 32 atomics.
+// The wave's agent-scope stores are performed before its arrival is counted, and the last workgroup issues its
+// agent-scope loads only after it has seen the count, so it reads every other workgroup's results. The last
+// workgroup clears the counter (arrival_clear).
+SS_DEV int* arrival_ctr(int* ctr, int c, int s) { return ctr + (c * (kArrShards + 1) + s) * kArrStride; }
+SS_DEV bool arrive_last(int* ctr, int c, int id, int total) {
+  __builtin_amdgcn_s_waitcnt(0);
+  int last = 0;
+  if ((threadIdx.x & 63) == 0) {
+    const int shards = total < kArrShards ? total : kArrShards;
+    const int sh = id % shards;
+    const int n_sh = total / shards + (sh < total % shards ? 1 : 0);
+    if (__hip_atomic_fetch_add(arrival_ctr(ctr, c, sh), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_sh - 1)
+      last = __hip_atomic_fetch_add(arrival_ctr(ctr, c, kArrShards), 1, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT) == shards - 1;
+  }
+  return __builtin_amdgcn_readfirstlane(last) != 0;
+}
+SS_DEV void arrival_clear(int* ctr, int c) {
+  const int lane = threadIdx.x & 63;
+  if (lane <= kArrShards) __hip_atomic_store(arrival_ctr(ctr, c, lane), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Copies n floats written by other workgroups (agent-scope loads, 32 per lane in flight) into LDS.
+SS_DEV void stage_ag(const float* src, int n, float* lds) {
+  const int lane = threadIdx.x & 63;
+  for (int b = 0; b < n; b += 64 * 32) {
+    float v[32];
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+      const int i = b + lane + 64 * q;
+      v[q] = i < n ? __hip_atomic_load(const_cast<float*>(src) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+      const int i = b + lane + 64 * q;
+      if (i < n) lds[i] = v[q];
+    }
+  }
 }
 
 SS_DEV bool finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
@@ -99,95 +161,183 @@ SS_DEV bool wave_any_nonzero(const WaveVals& w, int n) {
   return ss_wave_or(b) != 0u;
 }
 
-// ---------------------------------------------------------------- greedy
-__global__ __launch_bounds__(64) void greedy_chunk_kernel(const float* __restrict__ target, int V, float* work) {
-  const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
-  const int nch = gridDim.x, rows = gridDim.y;
-  Work k = work_of(work, rows, nch);
-  const float* x = target + (size_t)row * V;
-  // (value, first index) as one 64-bit key: order-preserving value key (+-0 equal, as np.argmax compares) above
-  // the complemented index; a row holding a non-finite value is flagged and never decided on.
-  uint64_t bk = 0;
-  uint32_t bad = 0;
-  for (int i = 0; i < kSub; ++i) {
-    const int j = c * kChunk + i * 64 + lane;
-    if (j >= V) break;
-    const float v = x[j];
-    bad |= !finite(v);
-    const uint64_t kv = ((uint64_t)ss_key(v == 0.f ? 0.f : v) << 32) | (0xFFFFFFFFu - (uint32_t)j);
-    bk = kv > bk ? kv : bk;
+// Sequential sums and scans over LDS arrays that are 16-byte aligned and padded with zeros to a multiple of 16
+// entries: every 16 entries are read as four unconditional 16-byte loads before their (dependent, in-order) adds,
+// and the bound n is applied by selects.
+SS_DEV float lds_seq_sum(const float* v, int n, float s) {
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  for (int b = 0; b < n; b += 16) {
+    const float4 a0 = v4[b / 4], a1 = v4[b / 4 + 1], a2 = v4[b / 4 + 2], a3 = v4[b / 4 + 3];
+    const float t[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float nx = s + t[i];
+      s = b + i < n ? nx : s;
+    }
   }
-  bk = ss_wave_max_u64(bk);
-  bad = ss_wave_or(bad);
-  const int bi = (int)(0xFFFFFFFFu - (uint32_t)bk);
-  const float best = ss_unkey((uint32_t)(bk >> 32));
-  if (lane == 0) {
-    k.cmax[row * nch + c] = best;
-    k.ctot[row * nch + c] = __int_as_float(bi);
-    k.cbad[row * nch + c] = bad ? 1.f : 0.f;
+  return s;
+}
+// Running sum from `start` over v[0..n): the first index whose running sum exceeds `target` (and the running sum
+// before it), and the last nonzero index.
+struct Scan {
+  int first, last;
+  float base;
+};
+SS_DEV Scan lds_scan(const float* v, int n, float start, float target) {
+  Scan r{-1, -1, start};
+  float run = start;
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  for (int b = 0; b < n; b += 16) {
+    const float4 a0 = v4[b / 4], a1 = v4[b / 4 + 1], a2 = v4[b / 4 + 2], a3 = v4[b / 4 + 3];
+    const float t[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {  // selects only: every lane holds the same values
+      const bool in = b + i < n;
+      const float nx = run + t[i];
+      r.last = in && t[i] > 0.f ? b + i : r.last;
+      const bool hit = in && r.first < 0 && nx > target;
+      r.base = hit ? run : r.base;
+      r.first = hit ? b + i : r.first;
+      run = in ? nx : run;
+    }
+  }
+  return r;
+}
+
+// Stages rows [nr][nch] written by other workgroups (agent-scope loads, 32 per lane in flight) into LDS at a row
+// stride of nchp = nch rounded up to 16, the padding zeroed.
+SS_DEV void stage_rows_ag(const float* src, int nr, int nch, int nchp, float* lds) {
+  const int lane = threadIdx.x & 63;
+  const int n = nr * nch;
+  for (int i = lane; i < nr * nchp; i += 64) lds[i] = 0.f;
+  for (int b = 0; b < n; b += 64 * 32) {
+    float v[32];
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+      const int i = b + lane + 64 * q;
+      v[q] = i < n ? __hip_atomic_load(const_cast<float*>(src) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < 32; ++q) {
+      const int i = b + lane + 64 * q;
+      if (i < n) {
+        const int r = i / nch;
+        lds[r * nchp + (i - r * nch)] = v[q];
+      }
+    }
   }
 }
 
-__global__ __launch_bounds__(64) void greedy_finish_kernel(const int32_t* __restrict__ drafts, int D, int nch,
-                                                           float* work, int32_t* out) {
-  const int lane = threadIdx.x;
-  Work k = work_of(work, D + 1, nch);
-  __shared__ int tok[64];
-  __shared__ int bad[64];
-  // Row i's first maximum over its chunk maxima: the largest (value key, complemented index) over the wave.
-  for (int row = 0; row <= D; ++row) {
-    uint64_t bk = 0;
-    uint32_t b = 0;
+// ---------------------------------------------------------------- greedy
+// One launch: every (chunk, row) workgroup reduces its chunk to its first maximum and a non-finite flag; the last
+// workgroup to arrive reduces the chunks of every row (order-free: the largest (value key, complemented index)),
+// decides the round and clears its counter. The order-preserving value key counts +-0 as equal (as np.argmax
+// compares); the complemented index makes the first maximum win.
+constexpr int kStage = 2048;  // chunk results staged per batch of rows by a finishing workgroup
+
+__global__ __launch_bounds__(64) void greedy_kernel(AcceptArgs a) {
+  __shared__ float sv[kStage], si[kStage], sb[kStage];
+  __shared__ int s_tok[kMaxRows], s_bad[kMaxRows];
+  const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
+  const int nch = gridDim.x, rows = gridDim.y;
+  Work k = work_of(a.work, rows, nch);
+  {
+    const float* x = a.target + (size_t)row * a.V;
+    float v[kSub];
 #pragma unroll
-    for (int q = 0; q < kMaxPerLane; ++q) {
-      const int c = lane + 64 * q;
-      if (c < nch) {
-        const float v = k.cmax[row * nch + c];
-        const int i = __float_as_int(k.ctot[row * nch + c]);
-        b |= k.cbad[row * nch + c] != 0.f ? 1u : 0u;
-        const uint64_t kv = ((uint64_t)ss_key(v == 0.f ? 0.f : v) << 32) | (0xFFFFFFFFu - (uint32_t)i);
+    for (int i = 0; i < kSub; ++i) {
+      const int j = c * kChunk + i * 64 + lane;
+      v[i] = j < a.V ? x[j] : 0.f;
+    }
+    uint64_t bk = 0;
+    uint32_t bad = 0;
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) {
+      const int j = c * kChunk + i * 64 + lane;
+      if (j < a.V) {
+        bad |= !finite(v[i]);
+        const uint64_t kv = ((uint64_t)ss_key(v[i] == 0.f ? 0.f : v[i]) << 32) | (0xFFFFFFFFu - (uint32_t)j);
         bk = kv > bk ? kv : bk;
       }
     }
     bk = ss_wave_max_u64(bk);
-    b = ss_wave_or(b);
+    bad = ss_wave_or(bad);
     if (lane == 0) {
-      tok[row] = (int)(0xFFFFFFFFu - (uint32_t)bk);
-      bad[row] = (int)b;
+      const size_t o = (size_t)row * nch + c;
+      st_ag(k.cmax + o, ss_unkey((uint32_t)(bk >> 32)));
+      st_ag(k.ctot + o, __int_as_float((int)(0xFFFFFFFFu - (uint32_t)bk)));
+      st_ag(k.cbad + o, bad ? 1.f : 0.f);
     }
   }
+  if (!arrive_last(k.ctr, 0, row * nch + c, nch * rows)) return;
+  arrival_clear(k.ctr, 0);
+  const int per = kStage / nch;
+  for (int r0 = 0; r0 < rows; r0 += per) {
+    const int nr = rows - r0 < per ? rows - r0 : per;
+    const size_t o = (size_t)r0 * nch;
+    stage_ag(k.cmax + o, nr * nch, sv);
+    stage_ag(k.ctot + o, nr * nch, si);
+    stage_ag(k.cbad + o, nr * nch, sb);
+    __syncthreads();
+    for (int rr = 0; rr < nr; ++rr) {
+      uint64_t bk = 0;
+      uint32_t b = 0;
+      for (int cc = lane; cc < nch; cc += 64) {
+        const float v = sv[rr * nch + cc];
+        const int ix = __float_as_int(si[rr * nch + cc]);
+        b |= sb[rr * nch + cc] != 0.f ? 1u : 0u;
+        const uint64_t kv = ((uint64_t)ss_key(v == 0.f ? 0.f : v) << 32) | (0xFFFFFFFFu - (uint32_t)ix);
+        bk = kv > bk ? kv : bk;
+      }
+      bk = ss_wave_max_u64(bk);
+      b = ss_wave_or(b);
+      if (lane == 0) {
+        s_tok[r0 + rr] = (int)(0xFFFFFFFFu - (uint32_t)bk);
+        s_bad[r0 + rr] = (int)b;
+      }
+    }
+    __syncthreads();
+  }
+  __shared__ int s_dr[64];
+  for (int i = lane; i < a.D; i += 64) s_dr[i] = a.drafts[i];
   __syncthreads();
   if (lane == 0) {
+    const int D = a.D;
     int good = 0, emit = 0, flags = 0;
     for (int i = 0; i <= D; ++i) {
-      if (bad[i]) {
+      if (s_bad[i]) {
         flags |= FLAG_NONFINITE;
         break;
       }
-      out[OUT_TOK + emit++] = tok[i];
-      if (i < D && tok[i] == drafts[i]) {
+      const int t = s_tok[i];
+      a.out[OUT_TOK + emit++] = t;
+      if (i < D && t == s_dr[i]) {
         ++good;
         continue;
       }
       break;
     }
-    for (int i = emit; i <= D; ++i) out[OUT_TOK + i] = -1;
-    out[OUT_NACC] = good;
-    out[OUT_NEMIT] = emit;
-    out[OUT_NUNI] = 0;
-    out[OUT_FLAGS] = flags;
+    for (int i = emit; i <= D; ++i) a.out[OUT_TOK + i] = -1;
+    a.out[OUT_NACC] = good;
+    a.out[OUT_NEMIT] = emit;
+    a.out[OUT_NUNI] = 0;
+    a.out[OUT_FLAGS] = flags;
   }
 }
 
 hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st) {
   const int nch = (a.V + kChunk - 1) / kChunk;
-  hipLaunchKernelGGL(greedy_chunk_kernel, dim3(nch, a.D + 1), dim3(64), 0, st, a.target, a.V, a.work);
-  hipLaunchKernelGGL(greedy_finish_kernel, dim3(1), dim3(64), 0, st, a.drafts, a.D, nch, a.work, a.out);
+  hipLaunchKernelGGL(greedy_kernel, dim3(nch, a.D + 1), dim3(64), 0, st, a);
   return hipGetLastError();
 }
 
 // ---------------------------------------------------------------- p/q
-// Logical rows: target i -> i (0..D), draft i -> D + 1 + i.
+// Three launches: (1) chunk maxima of l / T and non-finite flags; (2) e = exp(l / T - m) chunk totals, then the
+// last workgroup forms each row's total (sequential over its chunk totals), maximum and flag and decides the
+// drafts; (3) the chunk and sub-chunk totals of the sampled distribution, then the last workgroup searches them and
+// writes the round. Logical rows: target i -> i (0..D), draft i -> D + 1 + i.
 SS_DEV const float* row_ptr(const AcceptArgs& a, int row) {
   return row <= a.D ? a.target + (size_t)row * a.V : a.draft + (size_t)(row - a.D - 1) * a.V;
 }
@@ -197,14 +347,21 @@ __global__ __launch_bounds__(64) void pq_max_kernel(AcceptArgs a) {
   const int nch = gridDim.x, rows = gridDim.y;
   Work k = work_of(a.work, rows, nch);
   const float* x = row_ptr(a, row);
-  float m = -__builtin_inff();
-  int bad = 0;
+  float v[kSub];
+#pragma unroll
   for (int i = 0; i < kSub; ++i) {
     const int j = c * kChunk + i * 64 + lane;
-    if (j >= a.V) break;
-    const float v = x[j];
-    bad |= !finite(v);
-    m = fmaxf(m, v / a.temperature);
+    v[i] = j < a.V ? x[j] : 0.f;
+  }
+  float m = -__builtin_inff();
+  int bad = 0;
+#pragma unroll
+  for (int i = 0; i < kSub; ++i) {
+    const int j = c * kChunk + i * 64 + lane;
+    if (j < a.V) {
+      bad |= !finite(v[i]);
+      m = fmaxf(m, v[i] / a.temperature);
+    }
   }
   m = ss_wave_max(m);
   bad = (int)ss_wave_or((uint32_t)bad);
@@ -214,92 +371,130 @@ __global__ __launch_bounds__(64) void pq_max_kernel(AcceptArgs a) {
   }
 }
 
-// Row maximum over the chunk maxima (order-free), by the whole wave.
-SS_DEV float row_max(const Work& k, int row, int nch) { return wave_max_of(wave_load(k.cmax + (size_t)row * nch, nch), nch); }
-
-// Stage one chunk of a row (as e = exp(l/T - m)) into LDS with a 65-float stride per sub-chunk.
-SS_DEV void stage_exp(const AcceptArgs& a, int row, int c, float m, float* lds) {
-  const float* x = row_ptr(a, row);
-  const int lane = threadIdx.x;
-  for (int i = 0; i < kSub; ++i) {
-    const int e = i * 64 + lane;
-    const int j = c * kChunk + e;
-    float v = 0.f;
-    if (j < a.V) v = ss_expf(x[j] / a.temperature - m);
-    lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = v;
-  }
-}
-
 __global__ __launch_bounds__(64) void pq_sum_kernel(AcceptArgs a) {
   __shared__ float lds[64 * (kSub + 1)];
+  __shared__ __attribute__((aligned(16))) float sv[kStage], sm[kStage], sb[kStage];
+  __shared__ float zrow[kMaxRows], mrow[kMaxRows];
+  __shared__ int brow[kMaxRows];
   const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
   const int nch = gridDim.x, rows = gridDim.y;
   Work k = work_of(a.work, rows, nch);
-  const float m = row_max(k, row, nch);
-  stage_exp(a, row, c, m, lds);
-  __syncthreads();
-  float s = 0.f;
-  for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
-  s = ss_wave_sum(s);
-  if (lane == 0) k.ctot[row * nch + c] = s;
-}
-
-// state: [0] sample target row, [1] sample draft row (-1 = plain p), [2] uniform index, [3] stop (no sample),
-//        [4..] per-row Z and m for the two sampled rows.
-__global__ __launch_bounds__(64) void pq_decide_kernel(AcceptArgs a, int nch) {
-  // Run by the whole wave (every lane computes the same values); lane 0 writes the state.
-  const int rows = 2 * a.D + 1;
-  Work k = work_of(a.work, rows, nch);
-  auto row_sum = [&](int row) { return wave_seq_sum(wave_load(k.ctot + (size_t)row * nch, nch), nch); };
-  auto row_bad = [&](int row) { return wave_any_nonzero(wave_load(k.cbad + (size_t)row * nch, nch), nch); };
-  int good = 0, flags = 0, stop = 0;
-  int srow = a.D, sdraft = -1;
-  for (int i = 0; i < a.D; ++i) {
-    const int dr = a.D + 1 + i;
-    if (row_bad(i) || row_bad(dr)) {
-      flags |= FLAG_NONFINITE;
-      stop = 1;
-      break;
+  {
+    // the row maximum over the chunk maxima (order-free) and this chunk, all requested at once
+    const float* x = row_ptr(a, row);
+    float xv[kSub], cm[kMaxPerLane];
+#pragma unroll
+    for (int q = 0; q < kMaxPerLane; ++q) {
+      const int cc = lane + 64 * q;
+      cm[q] = cc < nch ? k.cmax[row * nch + cc] : -__builtin_inff();
     }
-    const int x = a.drafts[i];
-    if (x < 0 || x >= a.V) {
-      flags |= FLAG_BAD_DRAFT;
-      if (threadIdx.x == 0) ss_raise(a.err, SS_ERR_TOKEN);
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) {
+      const int j = c * kChunk + i * 64 + lane;
+      xv[i] = j < a.V ? x[j] : 0.f;
+    }
+    float m = -__builtin_inff();
+#pragma unroll
+    for (int q = 0; q < kMaxPerLane; ++q) m = fmaxf(m, cm[q]);
+    m = ss_wave_max(m);
+    // e = exp(l/T - m) staged with a 17-float stride per sub-chunk of 16
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) {
+      const int e = i * 64 + lane;
+      const int j = c * kChunk + e;
+      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? ss_expf(xv[i] / a.temperature - m) : 0.f;
+    }
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
+    s = ss_wave_sum(s);
+    if (lane == 0) st_ag(k.ctot + (size_t)row * nch + c, s);
+  }
+  if (!arrive_last(k.ctr, 1, row * nch + c, nch * rows)) return;
+  arrival_clear(k.ctr, 1);
+  // Per row: the total (sequential over its chunk totals, from 0), the maximum and the non-finite flag, lane r
+  // taking row r of each staged batch.
+  const int nchp = (nch + 15) & ~15;
+  const int per = kStage / nchp;
+  for (int r0 = 0; r0 < rows; r0 += per) {
+    const int nr = rows - r0 < per ? rows - r0 : per;
+    const size_t o = (size_t)r0 * nch;
+    stage_rows_ag(k.ctot + o, nr, nch, nchp, sv);
+    stage_rows_ag(k.cmax + o, nr, nch, nchp, sm);
+    stage_rows_ag(k.cbad + o, nr, nch, nchp, sb);
+    __syncthreads();
+    for (int rr = lane; rr < nr; rr += 64) {
+      const float4* m4 = reinterpret_cast<const float4*>(sm + rr * nchp);
+      const float4* b4 = reinterpret_cast<const float4*>(sb + rr * nchp);
+      float m = -__builtin_inff(), b = 0.f;
+      for (int q = 0; q < nchp / 4; ++q) {
+        const float4 mv = m4[q], bv = b4[q];
+        const float mm[4] = {mv.x, mv.y, mv.z, mv.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) m = 4 * q + e < nch ? fmaxf(m, mm[e]) : m;
+        b = fmaxf(b, fmaxf(fmaxf(bv.x, bv.y), fmaxf(bv.z, bv.w)));  // flags are 0 or 1, the padding 0
+      }
+      zrow[r0 + rr] = lds_seq_sum(sv + rr * nchp, nch, 0.f);
+      mrow[r0 + rr] = m;
+      brow[r0 + rr] = b != 0.f;
+    }
+    __syncthreads();
+  }
+  // the draft positions' logits, the drafts and the uniforms, requested at once
+  __shared__ int s_x[64];
+  __shared__ float s_lt[64], s_lq[64], s_u[64];
+  for (int i = lane; i < a.D; i += 64) {
+    const int xi = a.drafts[i];
+    const bool xok = xi >= 0 && xi < a.V;
+    s_x[i] = xi;
+    s_lt[i] = xok ? a.target[(size_t)i * a.V + xi] : 0.f;
+    s_lq[i] = xok ? a.draft[(size_t)i * a.V + xi] : 0.f;
+    s_u[i] = a.uniforms[i];
+  }
+  __syncthreads();
+  if (lane == 0) {
+    const int D = a.D;
+    int good = 0, flags = 0, stop = 0;
+    int srow = D, sdraft = -1;
+    for (int i = 0; i < D; ++i) {
+      const int dr = D + 1 + i;
+      if (brow[i] || brow[dr]) {
+        flags |= FLAG_NONFINITE;
+        stop = 1;
+        break;
+      }
+      const int x = s_x[i];
+      if (x < 0 || x >= a.V) {
+        flags |= FLAG_BAD_DRAFT;
+        ss_raise(a.err, SS_ERR_TOKEN);
+        srow = i;
+        sdraft = dr;
+        break;
+      }
+      const float p = ss_expf(s_lt[i] / a.temperature - mrow[i]) / zrow[i];
+      const float q = ss_expf(s_lq[i] / a.temperature - mrow[dr]) / zrow[dr];
+      if (s_u[i] * q < p) {
+        ++good;
+        continue;
+      }
       srow = i;
       sdraft = dr;
       break;
     }
-    const float zp = row_sum(i), zq = row_sum(dr);
-    const float mp = row_max(k, i, nch), mq = row_max(k, dr, nch);
-    const float p = ss_expf(a.target[(size_t)i * a.V + x] / a.temperature - mp) / zp;
-    const float q = ss_expf(a.draft[(size_t)i * a.V + x] / a.temperature - mq) / zq;
-    if (a.uniforms[i] * q < p) {
-      ++good;
-      continue;
+    if (!stop && sdraft < 0 && brow[D]) {
+      flags |= FLAG_NONFINITE;
+      stop = 1;
     }
-    srow = i;
-    sdraft = dr;
-    break;
-  }
-  if (!stop && sdraft < 0 && row_bad(a.D)) {
-    flags |= FLAG_NONFINITE;
-    stop = 1;
-  }
-  const float zp = row_sum(srow);
-  const float zq = sdraft >= 0 ? row_sum(sdraft) : 0.f;
-  const float ms = row_max(k, srow, nch);
-  const float md = sdraft >= 0 ? row_max(k, sdraft, nch) : 0.f;
-  if (threadIdx.x == 0) {
     k.state[0] = __int_as_float(srow);
     k.state[1] = __int_as_float(sdraft);
     k.state[2] = __int_as_float(good + (sdraft >= 0 ? 1 : 0));
     k.state[3] = __int_as_float(stop);
     k.state[4] = __int_as_float(good);
     k.state[5] = __int_as_float(flags);
-    k.state[6] = zp;
-    k.state[7] = zq;
-    k.state[8] = ms;
-    k.state[9] = md;
+    k.state[6] = zrow[srow];
+    k.state[7] = sdraft >= 0 ? zrow[sdraft] : 0.f;
+    k.state[8] = mrow[srow];
+    k.state[9] = sdraft >= 0 ? mrow[sdraft] : 0.f;
   }
 }
 
@@ -313,28 +508,12 @@ SS_DEV float sample_value(const AcceptArgs& a, const float* st, int j) {
   return d > 0.f ? d : 0.f;
 }
 
-__global__ __launch_bounds__(64) void pq_residual_kernel(AcceptArgs a) {
-  __shared__ float lds[64 * (kSub + 1)];
-  const int c = blockIdx.x, lane = threadIdx.x, nch = gridDim.x;
-  Work k = work_of(a.work, 2 * a.D + 1, nch);
-  if (__float_as_int(k.state[3])) return;
-  for (int i = 0; i < kSub; ++i) {
-    const int e = i * 64 + lane;
-    const int j = c * kChunk + e;
-    lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? sample_value(a, k.state, j) : 0.f;
-  }
-  __syncthreads();
-  float s = 0.f;
-  for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
-  k.stot[c * 64 + lane] = s;
-  s = ss_wave_sum(s);
-  if (lane == 0) k.rtot[c] = s;
-}
-
-// Inverse-CDF search, by the whole wave: the running sums keep their sequential order (index order, from the
-// chunk's base), formed from the lanes' registers; every lane follows the same scan.
-__global__ __launch_bounds__(64) void pq_search_kernel(AcceptArgs a, int nch) {
-  Work k = work_of(a.work, 2 * a.D + 1, nch);
+// Inverse-CDF search by the finishing workgroup. Every lane forms the same running sums (index order, from the
+// chunk's base) from LDS broadcast reads: the chunk, then the sub-chunk, then the entry, each falling back to the
+// last nonzero one.
+SS_DEV void pq_search(const AcceptArgs& a, const Work& k, int nch, float* srt) {
+  __shared__ __attribute__((aligned(16))) float s_st[64];
+  __shared__ float s_val[kSub];
   const int lane = threadIdx.x;
   const int good = __float_as_int(k.state[4]);
   int flags = __float_as_int(k.state[5]);
@@ -343,68 +522,38 @@ __global__ __launch_bounds__(64) void pq_search_kernel(AcceptArgs a, int nch) {
   int emit = good;
   int pick = -1;
   if (!stop) {
-    const WaveVals rt = wave_load(k.rtot, nch);
-    const float S = wave_seq_sum(rt, nch);
+    stage_rows_ag(k.rtot, 1, nch, (nch + 15) & ~15, srt);
+    __syncthreads();
+    const float S = lds_seq_sum(srt, nch, 0.f);
     if (!(S > 0.f)) flags |= FLAG_RESIDUAL_EMPTY;
     const float target = a.uniforms[uidx] * S;
     // chunk: the first whose running total exceeds the target (else the last nonzero one, based at its prefix)
-    int cs = -1, clast = -1;
-    float base = 0.f, run = 0.f;
-#pragma unroll
-    for (int q = 0; q < kMaxPerLane; ++q) {
-      if (64 * q >= nch) break;
-      const int m = nch - 64 * q < 64 ? nch - 64 * q : 64;
-      for (int l = 0; l < m; ++l) {
-        const float t = ss_readlane_f(rt.v[q], l);
-        const float nx = run + t;
-        if (t > 0.f) clast = 64 * q + l;
-        if (cs < 0 && nx > target) {
-          cs = 64 * q + l;
-          base = run;
-        }
-        run = nx;
-      }
-    }
+    const Scan ch = lds_scan(srt, nch, 0.f, target);
+    int cs = ch.first;
+    float base = ch.base;
     if (cs < 0) {
-      cs = clast < 0 ? 0 : clast;
-      base = 0.f;
-#pragma unroll
-      for (int q = 0; q < kMaxPerLane; ++q) {
-        if (64 * q >= cs) break;
-        const int m = cs - 64 * q < 64 ? cs - 64 * q : 64;
-        for (int l = 0; l < m; ++l) base = base + ss_readlane_f(rt.v[q], l);
-      }
+      cs = ch.last < 0 ? 0 : ch.last;
+      base = lds_seq_sum(srt, cs, 0.f);
     }
-    // sub-chunk: lane b holds the sub-chunk total b of chunk cs
-    const float st_b = k.stot[cs * 64 + lane];
-    int bs = -1, blast = -1;
-    float sbase = base;
-    run = base;
-    for (int b = 0; b < 64; ++b) {
-      const float t = ss_readlane_f(st_b, b);
-      const float nx = run + t;
-      if (t > 0.f) blast = b;
-      if (bs < 0 && nx > target) {
-        bs = b;
-        sbase = run;
-      }
-      run = nx;
-    }
+    __syncthreads();
+    s_st[lane] = __hip_atomic_load(k.stot + cs * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    const Scan sc = lds_scan(s_st, 64, base, target);
+    int bs = sc.first;
+    float sbase = sc.base;
     if (bs < 0) {
-      bs = blast < 0 ? 0 : blast;
-      sbase = base;
-      for (int b = 0; b < bs; ++b) sbase = sbase + ss_readlane_f(st_b, b);
+      bs = sc.last < 0 ? 0 : sc.last;
+      sbase = lds_seq_sum(s_st, bs, base);
     }
-    // entry: lane i < 16 holds the value of entry i of sub-chunk bs
     const int j0 = cs * kChunk + bs * kSub;
-    const int jl = j0 + (lane & (kSub - 1));
-    const float val = jl < a.V ? sample_value(a, k.state, jl) : 0.f;
+    if (lane < kSub) s_val[lane] = j0 + lane < a.V ? sample_value(a, k.state, j0 + lane) : 0.f;
+    __syncthreads();
     int last = -1;
-    run = sbase;
+    float run = sbase;
     for (int i = 0; i < kSub; ++i) {
       const int j = j0 + i;
       if (j >= a.V) break;
-      const float v = ss_readlane_f(val, i);
+      const float v = s_val[i];
       if (v > 0.f) last = j;
       run = run + v;
       if (run > target) {
@@ -425,14 +574,36 @@ __global__ __launch_bounds__(64) void pq_search_kernel(AcceptArgs a, int nch) {
   }
 }
 
+__global__ __launch_bounds__(64) void pq_residual_kernel(AcceptArgs a) {
+  __shared__ __attribute__((aligned(16))) float lds[kMaxPerLane * 64 + 64];
+  const int c = blockIdx.x, lane = threadIdx.x, nch = gridDim.x;
+  Work k = work_of(a.work, 2 * a.D + 1, nch);
+  if (!__float_as_int(k.state[3])) {
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) {
+      const int e = i * 64 + lane;
+      const int j = c * kChunk + e;
+      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? sample_value(a, k.state, j) : 0.f;
+    }
+    __syncthreads();
+    float s = 0.f;
+    for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
+    st_ag(k.stot + c * 64 + lane, s);
+    s = ss_wave_sum(s);
+    if (lane == 0) st_ag(k.rtot + c, s);
+  }
+  if (!arrive_last(k.ctr, 2, c, nch)) return;
+  arrival_clear(k.ctr, 2);
+  __syncthreads();
+  pq_search(a, k, nch, lds);
+}
+
 hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st) {
   const int nch = (a.V + kChunk - 1) / kChunk;
   const int rows = 2 * a.D + 1;
   hipLaunchKernelGGL(pq_max_kernel, dim3(nch, rows), dim3(64), 0, st, a);
   hipLaunchKernelGGL(pq_sum_kernel, dim3(nch, rows), dim3(64), 0, st, a);
-  hipLaunchKernelGGL(pq_decide_kernel, dim3(1), dim3(64), 0, st, a, nch);
   hipLaunchKernelGGL(pq_residual_kernel, dim3(nch), dim3(64), 0, st, a);
-  hipLaunchKernelGGL(pq_search_kernel, dim3(1), dim3(64), 0, st, a, nch);
   return hipGetLastError();
 }
 

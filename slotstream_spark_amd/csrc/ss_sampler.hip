@@ -157,27 +157,39 @@ SS_DEV float chunk_sum(const float (&v)[kSub], float& sub) {
 }
 
 // Stages a chunk array [n <= 1024] in LDS for the sequential scans below (one wave, every lane).
+// A chunk array into LDS, zero-padded to a multiple of 16 entries (16-byte aligned).
 SS_DEV const float* stage(const float* a, int n) {
-  __shared__ float buf[kPerLane * 64];
+  __shared__ __attribute__((aligned(16))) float buf[kPerLane * 64];
   const int lane = threadIdx.x & 63;
   float v[kPerLane];
 #pragma unroll
   for (int k = 0; k < kPerLane; ++k) v[k] = lane + 64 * k < n ? a[lane + 64 * k] : 0.f;
 #pragma unroll
   for (int k = 0; k < kPerLane; ++k)
-    if (lane + 64 * k < n) buf[lane + 64 * k] = v[k];
+    if (lane + 64 * k < ((n + 15) & ~15)) buf[lane + 64 * k] = v[k];
   __syncthreads();
   return buf;
 }
 
-// Every lane: ((a[0] + a[1]) + ...) + a[n-1] of a chunk array.
-SS_DEV float seq_sum(const float* a, int n) {
-  const float* b = stage(a, n);
-  float s = 0.f;
-#pragma unroll 8
-  for (int q = 0; q < n; ++q) s = s + b[q];
+// ((s + b[0]) + b[1]) + ... + b[n-1] over a zero-padded, 16-byte aligned LDS array: 16 entries read as four
+// unconditional 16-byte loads before their in-order adds, the bound applied by selects.
+SS_DEV float lds_seq_sum(const float* b, int n, float s) {
+  const float4* b4 = reinterpret_cast<const float4*>(b);
+  for (int q = 0; q < n; q += 16) {
+    const float4 a0 = b4[q / 4], a1 = b4[q / 4 + 1], a2 = b4[q / 4 + 2], a3 = b4[q / 4 + 3];
+    const float t[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float nx = s + t[i];
+      s = q + i < n ? nx : s;
+    }
+  }
   return s;
 }
+
+// Every lane: ((a[0] + a[1]) + ...) + a[n-1] of a chunk array.
+SS_DEV float seq_sum(const float* a, int n) { return lds_seq_sum(stage(a, n), n, 0.f); }
 
 SS_DEV uint64_t max_u64_of(const uint64_t* a, int n) {
   const int lane = threadIdx.x & 63;
@@ -245,11 +257,16 @@ SS_DEV void select_pass(const int* hist, int& need, uint32_t& prefix, int shift)
 // One wave: the 4-bit top-p digit of a round from its candidate masses (lane d sums candidate d's chunk totals in
 // chunk order): the smallest d whose mass is below top_p (candidate 15 always is: it is the previous round's bound).
 // All lanes stage the masses in LDS first, so the loads are in flight together.
+// The 16 candidate rows go to dynamic LDS (topp_lds_bytes(nch) at launch) at a zero-padded stride, so a launch
+// holds only what its vocabulary needs.
 SS_DEV int topp_digit(const float* tsum, int nch, float top_p) {
   constexpr int B = 32;
-  __shared__ float tb[16 * kPerLane * 64];
+  extern __shared__ float4 topp_dyn[];
+  float* tb = reinterpret_cast<float*>(topp_dyn);
   const int lane = threadIdx.x & 63;
+  const int nchp = (nch + 15) & ~15;
   const int n = 16 * nch;
+  for (int i = lane; i < 16 * nchp; i += 64) tb[i] = 0.f;
   for (int i0 = 0; i0 < n; i0 += 64 * B) {
     float v[B];
 #pragma unroll
@@ -260,14 +277,14 @@ SS_DEV int topp_digit(const float* tsum, int nch, float top_p) {
 #pragma unroll
     for (int q = 0; q < B; ++q) {
       const int idx = i0 + 64 * q + lane;
-      if (idx < n) tb[idx] = v[q];
+      if (idx < n) {
+        const int d = idx / nch;
+        tb[d * nchp + (idx - d * nch)] = v[q];
+      }
     }
   }
   __syncthreads();
-  const float* t = tb + (lane & 15) * nch;
-  float cum = 0.f;
-#pragma unroll 8
-  for (int c = 0; c < nch; ++c) cum = cum + t[c];
+  const float cum = lds_seq_sum(tb + (lane & 15) * nchp, nch, 0.f);
   const uint64_t ok = __ballot(lane < 16 && cum < top_p);
   return ok ? (int)__builtin_ctzll(ok) : 15;
 }
@@ -661,6 +678,8 @@ SampArgs args_of(int V, int R, const int32_t* gen, int n_gen, float temperature,
   return a;
 }
 
+size_t topp_lds_bytes(int nch) { return (size_t)16 * ((nch + 15) & ~15) * sizeof(float); }
+
 // The rows' launch sequence; which kernels run depends only on the parameters.
 void launch_rows(const SampArgs& a, hipStream_t st) {
   const dim3 g(a.nch, a.R), b(64);
@@ -678,8 +697,10 @@ void launch_rows(const SampArgs& a, hipStream_t st) {
     for (int pass = 1; pass < 4; ++pass) hipLaunchKernelGGL(samp_hist_kernel, g, b, 0, st, a, pass);
   hipLaunchKernelGGL(samp_exp_kernel, g, b, 0, st, a, has_k);
   if (has_p)
-    for (int round = 0; round < kRounds; ++round) hipLaunchKernelGGL(samp_topp_kernel, g, b, 0, st, a, round);
-  if (has_p || has_minp) hipLaunchKernelGGL(samp_keep_kernel, g, b, 0, st, a, has_p, has_p ? 0 : 1);
+    for (int round = 0; round < kRounds; ++round)
+      hipLaunchKernelGGL(samp_topp_kernel, g, b, topp_lds_bytes(a.nch), st, a, round);
+  if (has_p || has_minp)
+    hipLaunchKernelGGL(samp_keep_kernel, g, b, has_p ? topp_lds_bytes(a.nch) : 0, st, a, has_p, has_p ? 0 : 1);
   hipLaunchKernelGGL(samp_total_kernel, g, b, 0, st, a, has_minp, (has_p || has_minp) ? 0 : 1);
   hipLaunchKernelGGL(samp_draw_kernel, dim3(a.R), b, 0, st, a);
 }

@@ -71,7 +71,7 @@ class Acceptor:
     def __init__(self, depth: int, vocab: int, device="cuda"):
         self.depth, self.vocab = depth, vocab
         nb = _lib.lib().ssmoe_accept_workspace_bytes(depth, vocab)
-        self.work = torch.empty(int(nb), dtype=torch.uint8, device=device)
+        self.work = torch.zeros(int(nb), dtype=torch.uint8, device=device)  # header zero before the first call
         self.out = torch.empty(depth + 5, dtype=torch.int32, device=device)
         self._swork = None
 
