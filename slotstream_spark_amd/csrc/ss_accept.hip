@@ -206,6 +206,35 @@ SS_DEV Scan lds_scan(const float* v, int n, float start, float target) {
   return r;
 }
 
+// Stages the same rows of three arrays (as stage_rows_ag) with every load of a batch in flight before any store.
+SS_DEV void stage_rows3_ag(const float* s0, const float* s1, const float* s2, int nr, int nch, int nchp, float* d0,
+                           float* d1, float* d2) {
+  const int lane = threadIdx.x & 63;
+  const int n = nr * nch;
+  for (int i = lane; i < nr * nchp; i += 64) d0[i] = d1[i] = d2[i] = 0.f;
+  for (int b = 0; b < n; b += 64 * 16) {
+    float v0[16], v1[16], v2[16];
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int i = b + lane + 64 * q;
+      const bool in = i < n;
+      v0[q] = in ? __hip_atomic_load(const_cast<float*>(s0) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      v1[q] = in ? __hip_atomic_load(const_cast<float*>(s1) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+      v2[q] = in ? __hip_atomic_load(const_cast<float*>(s2) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
+    }
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int i = b + lane + 64 * q;
+      if (i < n) {
+        const int r = i / nch, o = r * nchp + (i - r * nch);
+        d0[o] = v0[q];
+        d1[o] = v1[q];
+        d2[o] = v2[q];
+      }
+    }
+  }
+}
+
 // Stages rows [nr][nch] written by other workgroups (agent-scope loads, 32 per lane in flight) into LDS at a row
 // stride of nchp = nch rounded up to 16, the padding zeroed.
 SS_DEV void stage_rows_ag(const float* src, int nr, int nch, int nchp, float* lds) {
@@ -371,40 +400,49 @@ __global__ __launch_bounds__(64) void pq_max_kernel(AcceptArgs a) {
   }
 }
 
-__global__ __launch_bounds__(64) void pq_sum_kernel(AcceptArgs a) {
+__global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
   __shared__ float lds[64 * (kSub + 1)];
   __shared__ __attribute__((aligned(16))) float sv[kStage], sm[kStage], sb[kStage];
   __shared__ float zrow[kMaxRows], mrow[kMaxRows];
   __shared__ int brow[kMaxRows];
-  const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
+  __shared__ float s_m;
+  const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nch = gridDim.x, rows = gridDim.y;
   Work k = work_of(a.work, rows, nch);
   {
-    // the row maximum over the chunk maxima (order-free) and this chunk, all requested at once
+    // wave 0: the row maximum over the chunk maxima (order-free); all waves: a quarter of the chunk each
     const float* x = row_ptr(a, row);
-    float xv[kSub], cm[kMaxPerLane];
+    constexpr int NQ = kSub / 4;
+    float xv[NQ];
 #pragma unroll
-    for (int q = 0; q < kMaxPerLane; ++q) {
-      const int cc = lane + 64 * q;
-      cm[q] = cc < nch ? k.cmax[row * nch + cc] : -__builtin_inff();
+    for (int ii = 0; ii < NQ; ++ii) {
+      const int j = c * kChunk + (w * NQ + ii) * 64 + lane;
+      xv[ii] = j < a.V ? x[j] : 0.f;
     }
+    if (w == 0) {
+      float cm[kMaxPerLane];
 #pragma unroll
-    for (int i = 0; i < kSub; ++i) {
-      const int j = c * kChunk + i * 64 + lane;
-      xv[i] = j < a.V ? x[j] : 0.f;
-    }
-    float m = -__builtin_inff();
+      for (int q = 0; q < kMaxPerLane; ++q) {
+        const int cc = lane + 64 * q;
+        cm[q] = cc < nch ? k.cmax[row * nch + cc] : -__builtin_inff();
+      }
+      float m = -__builtin_inff();
 #pragma unroll
-    for (int q = 0; q < kMaxPerLane; ++q) m = fmaxf(m, cm[q]);
-    m = ss_wave_max(m);
-    // e = exp(l/T - m) staged with a 17-float stride per sub-chunk of 16
-#pragma unroll
-    for (int i = 0; i < kSub; ++i) {
-      const int e = i * 64 + lane;
-      const int j = c * kChunk + e;
-      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? ss_expf(xv[i] / a.temperature - m) : 0.f;
+      for (int q = 0; q < kMaxPerLane; ++q) m = fmaxf(m, cm[q]);
+      m = ss_wave_max(m);
+      if (lane == 0) s_m = m;
     }
     __syncthreads();
+    const float m = s_m;
+    // e = exp(l/T - m) staged with a 17-float stride per sub-chunk of 16
+#pragma unroll
+    for (int ii = 0; ii < NQ; ++ii) {
+      const int e = (w * NQ + ii) * 64 + lane;
+      const int j = c * kChunk + e;
+      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? ss_expf(xv[ii] / a.temperature - m) : 0.f;
+    }
+    __syncthreads();
+    if (w != 0) return;
     float s = 0.f;
     for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
     s = ss_wave_sum(s);
@@ -419,9 +457,7 @@ __global__ __launch_bounds__(64) void pq_sum_kernel(AcceptArgs a) {
   for (int r0 = 0; r0 < rows; r0 += per) {
     const int nr = rows - r0 < per ? rows - r0 : per;
     const size_t o = (size_t)r0 * nch;
-    stage_rows_ag(k.ctot + o, nr, nch, nchp, sv);
-    stage_rows_ag(k.cmax + o, nr, nch, nchp, sm);
-    stage_rows_ag(k.cbad + o, nr, nch, nchp, sb);
+    stage_rows3_ag(k.ctot + o, k.cmax + o, k.cbad + o, nr, nch, nchp, sv, sm, sb);
     __syncthreads();
     for (int rr = lane; rr < nr; rr += 64) {
       const float4* m4 = reinterpret_cast<const float4*>(sm + rr * nchp);
@@ -574,18 +610,24 @@ SS_DEV void pq_search(const AcceptArgs& a, const Work& k, int nch, float* srt) {
   }
 }
 
-__global__ __launch_bounds__(64) void pq_residual_kernel(AcceptArgs a) {
+// Four waves per chunk compute the sampled distribution's values (its divisions and exps are the chunk's latency);
+// wave 0 then forms the sub-chunk and chunk totals and, in the last workgroup, runs the search.
+__global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[kMaxPerLane * 64 + 64];
-  const int c = blockIdx.x, lane = threadIdx.x, nch = gridDim.x;
+  const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nch = gridDim.x;
   Work k = work_of(a.work, 2 * a.D + 1, nch);
-  if (!__float_as_int(k.state[3])) {
+  const bool run = !__float_as_int(k.state[3]);
+  if (run) {
 #pragma unroll
-    for (int i = 0; i < kSub; ++i) {
-      const int e = i * 64 + lane;
+    for (int ii = 0; ii < kSub / 4; ++ii) {
+      const int e = (w * (kSub / 4) + ii) * 64 + lane;
       const int j = c * kChunk + e;
       lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? sample_value(a, k.state, j) : 0.f;
     }
-    __syncthreads();
+  }
+  __syncthreads();
+  if (w != 0) return;
+  if (run) {
     float s = 0.f;
     for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
     st_ag(k.stot + c * 64 + lane, s);
@@ -594,7 +636,6 @@ __global__ __launch_bounds__(64) void pq_residual_kernel(AcceptArgs a) {
   }
   if (!arrive_last(k.ctr, 2, c, nch)) return;
   arrival_clear(k.ctr, 2);
-  __syncthreads();
   pq_search(a, k, nch, lds);
 }
 
@@ -602,8 +643,8 @@ hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st) {
   const int nch = (a.V + kChunk - 1) / kChunk;
   const int rows = 2 * a.D + 1;
   hipLaunchKernelGGL(pq_max_kernel, dim3(nch, rows), dim3(64), 0, st, a);
-  hipLaunchKernelGGL(pq_sum_kernel, dim3(nch, rows), dim3(64), 0, st, a);
-  hipLaunchKernelGGL(pq_residual_kernel, dim3(nch), dim3(64), 0, st, a);
+  hipLaunchKernelGGL(pq_sum_kernel, dim3(nch, rows), dim3(256), 0, st, a);
+  hipLaunchKernelGGL(pq_residual_kernel, dim3(nch), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
