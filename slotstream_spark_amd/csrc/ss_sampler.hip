@@ -35,6 +35,7 @@ constexpr int kPerLane = 16;  // chunk arrays of up to 1024 chunks (V <= 2^20)
 constexpr int kRhoBits = 52;  // 32 key bits above 20 index bits
 constexpr int kRounds = kRhoBits / 4;
 constexpr int kFlagNonfinite = 1, kFlagBadDraft = 2, kFlagFallback = 8;
+constexpr int kSlot = 128;  // nonzero exp entries a top-k chunk lists for the compact top-p search
 
 SS_DEV bool is_nan(float v) { return v != v; }
 SS_DEV bool is_finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
@@ -51,7 +52,7 @@ SS_DEV uint64_t amax_key(float v, int j) { return ((uint64_t)nkey(v) << 32) | (0
 
 // Byte offsets of one row's workspace; rows follow each other `bytes` apart.
 struct Layout {
-  size_t L, P, cmax, cnan, ckey, craw, cbad, etot, ftot, tsum, stot, hist, rr, res, bytes;
+  size_t L, P, cmax, cnan, ckey, craw, cbad, etot, ftot, tsum, stot, hist, rr, res, cnz, surv, cres, bytes;
 };
 
 __host__ __device__ inline Layout layout_of(int V, int nch) {
@@ -76,6 +77,9 @@ __host__ __device__ inline Layout layout_of(int V, int nch) {
   l.hist = take(4 * 256 * 4);               // top-k radix histograms, one per 8-bit pass
   l.rr = take((size_t)(kRounds + 1) * 8);   // top-p prefix at the start of each round
   l.res = take(16);                         // token, fallback flag, non-finite row
+  l.cnz = take((size_t)nch * 4);            // nonzero exp entries per chunk (top-k rows)
+  l.surv = take((size_t)nch * kSlot * 8);   // a chunk's nonzero entries (index << 32 | e bits), up to kSlot
+  l.cres = take(16);                        // compact top-p: r* (uint64), then 1 when it was found
   l.bytes = o;
   return l;
 }
@@ -89,6 +93,9 @@ struct SW {
   int* hist;
   uint64_t* rr;
   int* res;
+  int* cnz;
+  uint64_t* surv;
+  uint64_t* cres;  // [0] r*, [1] found (1) or not (0)
 };
 
 SS_DEV SW sw_of(void* work, int V, int nch, int row) {
@@ -109,6 +116,9 @@ SS_DEV SW sw_of(void* work, int V, int nch, int row) {
   s.hist = reinterpret_cast<int*>(b + l.hist);
   s.rr = reinterpret_cast<uint64_t*>(b + l.rr);
   s.res = reinterpret_cast<int*>(b + l.res);
+  s.cnz = reinterpret_cast<int*>(b + l.cnz);
+  s.surv = reinterpret_cast<uint64_t*>(b + l.surv);
+  s.cres = reinterpret_cast<uint64_t*>(b + l.cres);
   return s;
 }
 
@@ -407,14 +417,200 @@ __global__ __launch_bounds__(64) void samp_exp_kernel(SampArgs a, int has_k) {
   }
   float sub;
   const float t = chunk_sum(v, sub);
+  if (has_k) {
+    // the chunk's nonzero entries in index order (lane-major: entry lane * 16 + i), up to kSlot of them
+    int nz = 0;
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) nz += v[i] != 0.f;
+    int incl = nz;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+      const int o = __shfl_up(incl, d);
+      incl += lane >= d ? o : 0;
+    }
+    int pos = incl - nz;
+#pragma unroll
+    for (int i = 0; i < kSub; ++i) {
+      if (v[i] != 0.f) {
+        if (pos < kSlot) {
+          const uint32_t j = (uint32_t)(c * kChunk + lane * kSub + i);
+          w.surv[(size_t)c * kSlot + pos] = ((uint64_t)j << 32) | __float_as_uint(v[i]);
+        }
+        ++pos;
+      }
+    }
+    if (lane == 63) w.cnz[c] = incl;
+  }
   if (lane == 0) w.etot[c] = t;
+}
+
+// 4'. Compact top-p (top-k rows, one workgroup per row). Only the top-k survivors carry weight, so cum(r) (the
+// hierarchical mass of p over rho > r) is a step function of the survivors: with S(m) the masked hierarchical sum of
+// the m survivors of largest rho (S grows with m: every partial sum is a monotone function of nonnegative terms),
+// the smallest r with cum(r) < top_p is the rho of the m'-th survivor, m' the smallest m with S(m) >= top_p, or 0
+// when S(all) < top_p: exactly the r* the 13 radix rounds find. S(m) is formed as the rounds form their masses:
+// per chunk, lane b sums sub-chunk b's included entries in index order, the wave butterfly gives the chunk total,
+// the chunk totals are summed in order. Four waves evaluate four values of m at a time. Rows with more than
+// kCompact survivors, or a non-finite z, leave cres[1] = 0 and the rounds run as before.
+constexpr int kCompact = 512;
+constexpr int kCompactChunks = 160;  // active chunks the compact search holds (more: the rounds run)
+
+__global__ __launch_bounds__(256) void samp_topp_compact_kernel(SampArgs a) {
+  __shared__ int s_cnt[kPerLane * 64];   // nonzero count of active chunk q, then its chunk index
+  __shared__ int s_ach[kPerLane * 64];
+  __shared__ int s_aoff[kPerLane * 64 + 1];
+  __shared__ int s_j[kCompact], s_rank[kCompact];
+  __shared__ float s_p[kCompact];
+  __shared__ uint64_t s_rho[kCompact];
+  __shared__ int s_na, s_ok;
+  const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  SW sw = sw_of(a.work, a.V, a.nch, row);
+  const int nch = a.nch;
+  // wave 0: the active chunks (nonzero count) in order, their survivor offsets, and whether every count fits
+  if (w == 0) {
+    int run = 0, na = 0, ok = 1;
+    int cv[kPerLane];
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) cv[k] = lane + 64 * k < nch ? sw.cnz[lane + 64 * k] : 0;
+#pragma unroll
+    for (int k = 0; k < kPerLane; ++k) {
+      const int v = cv[k];
+      ok &= v <= kSlot;
+      const uint64_t act = __ballot(v > 0);
+      const int before = __popcll(act & ((1ull << lane) - 1ull));
+      int incl = v;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(incl, d);
+        incl += lane >= d ? o : 0;
+      }
+      if (v > 0) {
+        s_ach[na + before] = lane + 64 * k;
+        s_aoff[na + before] = run + incl - v;
+        s_cnt[na + before] = v;
+      }
+      run += __shfl(incl, 63);
+      na += __popcll(act);
+    }
+    ok = ss_wave_or((uint32_t)!ok) ? 0 : 1;
+    if (lane == 0) {
+      s_aoff[na] = run;
+      s_na = na;
+      s_ok = ok && run <= kCompact && na <= kCompactChunks;
+    }
+  }
+  __syncthreads();
+  const int na = s_na;
+  const int n = s_aoff[na];
+  const float z = seq_sum(sw.etot, nch);  // the z round 0 would form
+  if (!s_ok || !(z > 0.f) || !(z < __builtin_inff())) {
+    if (tid == 0) {
+      sw.cres[0] = 0;
+      sw.cres[1] = 0;
+    }
+    return;
+  }
+  // gather: survivor q of the row is entry q - aoff[t] of active chunk t (binary search); one batch of loads
+  for (int q = tid; q < n; q += 256) {
+    int lo = 0, hi = na - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_aoff[mid] <= q) lo = mid;
+      else hi = mid - 1;
+    }
+    const uint64_t e = sw.surv[(size_t)s_ach[lo] * kSlot + (q - s_aoff[lo])];
+    const int j = (int)(e >> 32);
+    const float pj = __uint_as_float((uint32_t)e) / z;
+    s_j[q] = j;
+    s_p[q] = pj;
+    s_rho[q] = rho_of(pj, j);
+  }
+  __syncthreads();
+  // rank by rho, descending (rho values are distinct: they end in the index)
+  for (int q = tid; q < n; q += 256) {
+    const uint64_t r = s_rho[q];
+    int rk = 0;
+    for (int t = 0; t < n; ++t) rk += s_rho[t] > r;
+    s_rank[q] = rk;
+  }
+  __syncthreads();
+  // S(m) by the workgroup: leaf (active chunk t, sub-chunk b) = its survivors of rank < m summed in index order
+  // (a leaf's survivors are adjacent in the list; its first one sums them), the wave butterfly over each chunk's 64
+  // leaves, then the chunk totals in order. The leaf matrix is kept zero between evaluations.
+  __shared__ __attribute__((aligned(16))) float s_leaf[kCompactChunks * 64];
+  __shared__ __attribute__((aligned(16))) float s_ct[kCompactChunks];
+  __shared__ float s_S;
+  for (int q = tid; q < na * 64; q += 256) s_leaf[q] = 0.f;
+  for (int q = tid; q < n; q += 256) {  // the leaf of survivor q and whether it starts its leaf
+    int lo2 = 0, hi2 = na - 1;
+    while (lo2 < hi2) {
+      const int mid = (lo2 + hi2 + 1) >> 1;
+      if (s_aoff[mid] <= q) lo2 = mid;
+      else hi2 = mid - 1;
+    }
+    const int leaf = lo2 * 64 + ((s_j[q] & (kChunk - 1)) >> 4);
+    const bool first = q == s_aoff[lo2] || ((s_j[q - 1] & (kChunk - 1)) >> 4) != ((s_j[q] & (kChunk - 1)) >> 4);
+    s_cnt[q] = first ? leaf : -1;  // reused: leaf index at a leaf's first survivor, -1 elsewhere
+  }
+  __syncthreads();
+  auto eval = [&](int m) {
+    for (int q = tid; q < n; q += 256) {
+      const int leaf = s_cnt[q];
+      if (leaf >= 0) {
+        float v = 0.f;
+        for (int r = q; r < n && (r == q || s_cnt[r] < 0); ++r) {
+          if (r != q && ((s_j[r] & (kChunk - 1)) >> 4) != ((s_j[q] & (kChunk - 1)) >> 4)) break;
+          const float nx = v + s_p[r];
+          v = s_rank[r] < m ? nx : v;
+        }
+        s_leaf[leaf] = v;
+      }
+    }
+    __syncthreads();
+    for (int t = w; t < na; t += 4) {
+      const float ct = ss_wave_sum(s_leaf[t * 64 + lane]);
+      if (lane == 0) s_ct[t] = ct;
+    }
+    __syncthreads();
+    if (tid == 0) {
+      float S = 0.f;
+      for (int t = 0; t < na; t += 4) {
+        const float4 c4 = *reinterpret_cast<const float4*>(s_ct + t);
+        const float cv[4] = {c4.x, c4.y, c4.z, c4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float nx = S + cv[e];
+          S = t + e < na ? nx : S;
+        }
+      }
+      s_S = S;
+    }
+    __syncthreads();
+    return s_S;
+  };
+  // smallest m in [0, n] with S(m) >= top_p (n + 1 when none): binary search, S(lo) < top_p <= S(hi)
+  int lo = 0, hi = n + 1;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (eval(mid) >= a.top_p) hi = mid;
+    else lo = mid;
+  }
+  if (tid == 0) {
+    uint64_t rs = 0;
+    if (hi <= n)
+      for (int q = 0; q < n; ++q)
+        if (s_rank[q] == hi - 1) rs = s_rho[q];
+    sw.cres[0] = rs;
+    sw.cres[1] = 1;
+  }
 }
 
 // 4. top-p round k: fold the previous round's digit into the prefix r, then chunk c's hierarchical masses of p over
 // rho > r | d << s | (2^s - 1), d = 0..15. Round 0 also normalizes p = e / z.
-__global__ __launch_bounds__(64) void samp_topp_kernel(SampArgs a, int round) {
+__global__ __launch_bounds__(64) void samp_topp_kernel(SampArgs a, int round, int compact) {
   const int c = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
   SW w = sw_of(a.work, a.V, a.nch, row);
+  if (compact && w.cres[1]) return;  // r* is known
   const int nch = a.nch;
   const int s = kRhoBits - 4 - 4 * round;
   float pv[kSub];
@@ -463,7 +659,8 @@ __global__ __launch_bounds__(64) void samp_topp_kernel(SampArgs a, int round) {
 }
 
 // 5. (has_p) keep rho >= r*; (min_p > 0) chunk maxima of the kept probabilities. `norm`: p = e / z here.
-__global__ __launch_bounds__(64) void samp_keep_kernel(SampArgs a, int has_p, int norm) {
+// With `compact` and r* found by samp_topp_compact_kernel, the rounds did not run: r = r* and P still holds e.
+__global__ __launch_bounds__(64) void samp_keep_kernel(SampArgs a, int has_p, int norm, int compact) {
   const int c = blockIdx.x, row = blockIdx.y, lane = threadIdx.x;
   SW w = sw_of(a.work, a.V, a.nch, row);
   const int nch = a.nch;
@@ -474,7 +671,12 @@ __global__ __launch_bounds__(64) void samp_keep_kernel(SampArgs a, int has_p, in
     pv[i] = j < a.V ? w.P[j] : 0.f;
   }
   uint64_t r = 0;
-  if (has_p) r = w.rr[kRounds - 1] | (uint64_t)topp_digit(w.tsum + ((kRounds - 1) & 1) * 16 * nch, nch, a.top_p);
+  if (compact && w.cres[1]) {
+    r = w.cres[0];
+    norm = 1;
+  } else if (has_p) {
+    r = w.rr[kRounds - 1] | (uint64_t)topp_digit(w.tsum + ((kRounds - 1) & 1) * 16 * nch, nch, a.top_p);
+  }
   const float z = norm ? seq_sum(w.etot, nch) : 1.f;
   float m = -__builtin_inff();
 #pragma unroll
@@ -696,11 +898,16 @@ void launch_rows(const SampArgs& a, hipStream_t st) {
   if (has_k)
     for (int pass = 1; pass < 4; ++pass) hipLaunchKernelGGL(samp_hist_kernel, g, b, 0, st, a, pass);
   hipLaunchKernelGGL(samp_exp_kernel, g, b, 0, st, a, has_k);
+  // top-k rows: the compact search finds r* from the survivors; the rounds then exit at once (they still run, from
+  // the same launch sequence, when a row has more than kCompact survivors)
+  const int compact = has_k && has_p;
+  if (compact) hipLaunchKernelGGL(samp_topp_compact_kernel, dim3(a.R), dim3(256), 0, st, a);
   if (has_p)
     for (int round = 0; round < kRounds; ++round)
-      hipLaunchKernelGGL(samp_topp_kernel, g, b, topp_lds_bytes(a.nch), st, a, round);
+      hipLaunchKernelGGL(samp_topp_kernel, g, b, topp_lds_bytes(a.nch), st, a, round, compact);
   if (has_p || has_minp)
-    hipLaunchKernelGGL(samp_keep_kernel, g, b, has_p ? topp_lds_bytes(a.nch) : 0, st, a, has_p, has_p ? 0 : 1);
+    hipLaunchKernelGGL(samp_keep_kernel, g, b, has_p ? topp_lds_bytes(a.nch) : 0, st, a, has_p, has_p ? 0 : 1,
+                       compact);
   hipLaunchKernelGGL(samp_total_kernel, g, b, 0, st, a, has_minp, (has_p || has_minp) ? 0 : 1);
   hipLaunchKernelGGL(samp_draw_kernel, dim3(a.R), b, 0, st, a);
 }

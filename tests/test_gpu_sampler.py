@@ -176,3 +176,23 @@ def test_accept_sampled_stream_and_seen_follow_the_reference_loop():
         assert (res.n_accept, res.n_emit, res.n_uniform) == (2, 3, 3)
         assert res.tokens == want[4: 4 + want[1]].tolist()
         assert dev_stream.state == ref_stream.state and dev_seen == ref_seen
+
+
+@pytest.mark.parametrize("v", [5000, 151936])
+def test_compact_top_p_and_its_fallback_bitwise(v):
+    """Top-k rows find the top-p threshold from their survivors (up to 512) instead of the 13 radix rounds; rows with
+    more survivors (a large top-k, or ties at the k-th value) run the rounds. Both equal or_sample bit for bit."""
+    print(f"[sampler] compact top-p v={v}", flush=True)
+    rng = np.random.default_rng(v + 17)
+    dev = Dev(v)
+    rows = [(rng.standard_normal(v) * 4).astype(np.float32), np.full(v, 1.25, np.float32)]
+    tied = (rng.standard_normal(v) * 2).astype(np.float32)
+    tied[rng.permutation(v)[:700]] = np.float32(9.0)  # 700 ties at the top: k = 40 keeps all 700
+    rows.append(tied)
+    for ri, x in enumerate(rows):
+        xd = torch.from_numpy(x).cuda()
+        for (t, tp, tk, mp, pp) in [(0.7, 0.95, 40, 0.0, 0.0), (1.0, 0.9, 300, 0.0, 0.0), (1.0, 0.99, 512, 0.02, 0.0),
+                                    (0.9, 0.8, 600, 0.0, 0.0), (1.2, 0.5, 2, 0.0, 0.0), (0.5, 0.999, 100, 0.0, 1.0)]:
+            for u in (np.float32(0.0), np.float32(rng.random()), np.float32(0.9999)):
+                gen = set(rng.integers(0, v, 8).tolist())
+                assert dev.draw(xd, gen, t, tp, tk, mp, pp, u) == O.sample(x, gen, t, tp, tk, mp, pp, u), (ri, tk, u)
