@@ -35,7 +35,8 @@ constexpr int kPerLane = 16;  // chunk arrays of up to 1024 chunks (V <= 2^20)
 constexpr int kRhoBits = 52;  // 32 key bits above 20 index bits
 constexpr int kRounds = kRhoBits / 4;
 constexpr int kFlagNonfinite = 1, kFlagBadDraft = 2, kFlagFallback = 8;
-constexpr int kSlot = 128;  // nonzero exp entries a top-k chunk lists for the compact top-p search
+constexpr int kSlot = 512;  // nonzero exp entries a top-k chunk lists for the compact top-p search
+constexpr int kHistShards = 8;  // copies of each top-k histogram; chunk c adds to copy c % 8 (fewer atomics per bin)
 
 SS_DEV bool is_nan(float v) { return v != v; }
 SS_DEV bool is_finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
@@ -74,7 +75,7 @@ __host__ __device__ inline Layout layout_of(int V, int nch) {
   l.ftot = take((size_t)nch * 4);           // chunk totals of the final weights
   l.tsum = take((size_t)2 * 16 * nch * 4);  // top-p candidate masses, two rounds alternating
   l.stot = take((size_t)64 * nch * 4);      // sub-chunk totals of the final weights
-  l.hist = take(4 * 256 * 4);               // top-k radix histograms, one per 8-bit pass
+  l.hist = take(4 * kHistShards * 256 * 4);  // top-k radix histograms, one per 8-bit pass, kHistShards copies
   l.rr = take((size_t)(kRounds + 1) * 8);   // top-p prefix at the start of each round
   l.res = take(16);                         // token, fallback flag, non-finite row
   l.cnz = take((size_t)nch * 4);            // nonzero exp entries per chunk (top-k rows)
@@ -231,10 +232,17 @@ SS_DEV float row_max(const SW& w, int nch) {
 // `hist` (bins descending, counting multiplicity); need becomes its rank inside the bin. Every lane gets the same.
 SS_DEV void select_pass(const int* hist, int& need, uint32_t& prefix, int shift) {
   const int lane = threadIdx.x & 63;
+  int hs[kHistShards][4];
+#pragma unroll
+  for (int c = 0; c < kHistShards; ++c)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) hs[c][q] = hist[256 * c + 255 - 4 * lane - q];
   int h[4], s = 0;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    h[q] = hist[255 - 4 * lane - q];
+    h[q] = 0;
+#pragma unroll
+    for (int c = 0; c < kHistShards; ++c) h[q] += hs[c][q];
     s += h[q];
   }
   int incl = s;  // inclusive prefix over lanes = count of keys in bins >= 252 - 4 * lane
@@ -304,7 +312,7 @@ SS_DEV int topp_digit(const float* tsum, int nch, float top_p) {
 // Clears the top-k histograms of every row.
 __global__ __launch_bounds__(256) void samp_begin_kernel(SampArgs a) {
   SW w = sw_of(a.work, a.V, a.nch, blockIdx.x);
-  for (int i = threadIdx.x; i < 4 * 256; i += 256) w.hist[i] = 0;
+  for (int i = threadIdx.x; i < 4 * kHistShards * 256; i += 256) w.hist[i] = 0;
 }
 
 // 1. penalty and temperature into L; argmax keys of the penalized and of the raw logits; non-finite flags; chunk
@@ -362,7 +370,7 @@ __global__ __launch_bounds__(64) void samp_prep_kernel(SampArgs a, int has_k) {
   if (has_k) {
     __syncthreads();
     for (int b = lane; b < 256; b += 64)
-      if (hist[b]) atomicAdd(&w.hist[b], hist[b]);
+      if (hist[b]) atomicAdd(&w.hist[256 * (c % kHistShards) + b], hist[b]);
   }
 }
 
@@ -374,7 +382,7 @@ __global__ __launch_bounds__(64) void samp_hist_kernel(SampArgs a, int pass) {
   for (int i = lane; i < 256; i += 64) hist[i] = 0;
   int need = a.top_k;
   uint32_t prefix = 0;
-  for (int p = 0; p < pass; ++p) select_pass(w.hist + 256 * p, need, prefix, 24 - 8 * p);
+  for (int p = 0; p < pass; ++p) select_pass(w.hist + kHistShards * 256 * p, need, prefix, 24 - 8 * p);
   const int shift = 24 - 8 * pass;
   const uint32_t hmask = 0xFFFFFFFFu << (shift + 8);
   float lv[kSub];
@@ -392,7 +400,7 @@ __global__ __launch_bounds__(64) void samp_hist_kernel(SampArgs a, int pass) {
   }
   __syncthreads();
   for (int b = lane; b < 256; b += 64)
-    if (hist[b]) atomicAdd(&w.hist[256 * pass + b], hist[b]);
+    if (hist[b]) atomicAdd(&w.hist[kHistShards * 256 * pass + 256 * (c % kHistShards) + b], hist[b]);
 }
 
 // 3. e = exp(l - m) into P (0 below the top-k threshold) and the chunk totals.
@@ -403,7 +411,7 @@ __global__ __launch_bounds__(64) void samp_exp_kernel(SampArgs a, int has_k) {
   if (has_k) {
     int need = a.top_k;
     uint32_t prefix = 0;
-    for (int p = 0; p < 4; ++p) select_pass(w.hist + 256 * p, need, prefix, 24 - 8 * p);
+    for (int p = 0; p < 4; ++p) select_pass(w.hist + kHistShards * 256 * p, need, prefix, 24 - 8 * p);
     kth = prefix == 0xFFFFFFFFu ? __uint_as_float(0x7FC00000u) : ss_unkey(prefix);
   }
   const float m = row_max(w, a.nch);
@@ -462,7 +470,10 @@ __global__ __launch_bounds__(256) void samp_topp_compact_kernel(SampArgs a) {
   __shared__ int s_j[kCompact], s_rank[kCompact];
   __shared__ float s_p[kCompact];
   __shared__ uint64_t s_rho[kCompact];
-  __shared__ int s_na, s_ok;
+  __shared__ int s_na, s_ok, s_digit;
+  __shared__ __attribute__((aligned(16))) float s_leaf[kCompactChunks * 64];  // leaves; the fallback's masses
+  __shared__ __attribute__((aligned(16))) float s_ct[kCompactChunks];
+  __shared__ float s_S;
   const int row = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   SW sw = sw_of(a.work, a.V, a.nch, row);
   const int nch = a.nch;
@@ -504,9 +515,54 @@ __global__ __launch_bounds__(256) void samp_topp_compact_kernel(SampArgs a) {
   const int n = s_aoff[na];
   const float z = seq_sum(sw.etot, nch);  // the z round 0 would form
   if (!s_ok || !(z > 0.f) || !(z < __builtin_inff())) {
+    // The 13 radix rounds of samp_topp_kernel inside the workgroup (same masses, digits and order; p = e / z formed
+    // as round 0 forms it, P keeps e): r* = the digits at shifts 48, 44, ..., 0. Four waves take the chunks.
+    float* tsl = s_leaf;  // [16][nch], nch <= 640
+    uint64_t r = 0;
+    for (int round = 0; round < kRounds; ++round) {
+      const int sft = kRhoBits - 4 - 4 * round;
+      const uint64_t r_hi = r >> (sft + 4);
+      for (int c = w; c < nch; c += 4) {
+        float pv[kSub];
+#pragma unroll
+        for (int i = 0; i < kSub; ++i) {
+          const int j = c * kChunk + lane * kSub + i;
+          pv[i] = j < a.V ? sw.P[j] / z : 0.f;
+        }
+        float acc[16];
+#pragma unroll
+        for (int d = 0; d < 16; ++d) acc[d] = 0.f;
+#pragma unroll
+        for (int i = 0; i < kSub; ++i) {
+          const int j = c * kChunk + lane * kSub + i;
+          const float pp = pv[i];
+          if (j < a.V && pp != 0.f) {
+            const uint64_t rho = rho_of(pp, j);
+            const uint64_t hi = rho >> (sft + 4);
+            const int lim = hi > r_hi ? 16 : (hi == r_hi ? (int)((rho >> sft) & 15) : 0);
+#pragma unroll
+            for (int d = 0; d < 16; ++d) acc[d] = acc[d] + (d < lim ? pp : 0.f);
+          }
+        }
+#pragma unroll
+        for (int d = 0; d < 16; ++d) {
+          const float t = ss_wave_sum(acc[d]);
+          if (lane == 0) tsl[d * nch + c] = t;
+        }
+      }
+      __syncthreads();
+      if (w == 0) {
+        float cum = 0.f;
+        for (int c = 0; c < nch; ++c) cum = cum + tsl[(lane & 15) * nch + c];
+        const uint64_t okb = __ballot(lane < 16 && cum < a.top_p);
+        if (lane == 0) s_digit = okb ? (int)__builtin_ctzll(okb) : 15;
+      }
+      __syncthreads();
+      r |= (uint64_t)s_digit << sft;
+    }
     if (tid == 0) {
-      sw.cres[0] = 0;
-      sw.cres[1] = 0;
+      sw.cres[0] = r;
+      sw.cres[1] = 1;
     }
     return;
   }
@@ -537,9 +593,6 @@ __global__ __launch_bounds__(256) void samp_topp_compact_kernel(SampArgs a) {
   // S(m) by the workgroup: leaf (active chunk t, sub-chunk b) = its survivors of rank < m summed in index order
   // (a leaf's survivors are adjacent in the list; its first one sums them), the wave butterfly over each chunk's 64
   // leaves, then the chunk totals in order. The leaf matrix is kept zero between evaluations.
-  __shared__ __attribute__((aligned(16))) float s_leaf[kCompactChunks * 64];
-  __shared__ __attribute__((aligned(16))) float s_ct[kCompactChunks];
-  __shared__ float s_S;
   for (int q = tid; q < na * 64; q += 256) s_leaf[q] = 0.f;
   for (int q = tid; q < n; q += 256) {  // the leaf of survivor q and whether it starts its leaf
     int lo2 = 0, hi2 = na - 1;
@@ -671,7 +724,7 @@ __global__ __launch_bounds__(64) void samp_keep_kernel(SampArgs a, int has_p, in
     pv[i] = j < a.V ? w.P[j] : 0.f;
   }
   uint64_t r = 0;
-  if (compact && w.cres[1]) {
+  if (compact) {
     r = w.cres[0];
     norm = 1;
   } else if (has_p) {
@@ -898,13 +951,13 @@ void launch_rows(const SampArgs& a, hipStream_t st) {
   if (has_k)
     for (int pass = 1; pass < 4; ++pass) hipLaunchKernelGGL(samp_hist_kernel, g, b, 0, st, a, pass);
   hipLaunchKernelGGL(samp_exp_kernel, g, b, 0, st, a, has_k);
-  // top-k rows: the compact search finds r* from the survivors; the rounds then exit at once (they still run, from
-  // the same launch sequence, when a row has more than kCompact survivors)
-  const int compact = has_k && has_p;
+  // top-k rows (k <= kCompact): one workgroup per row finds r* (from the survivors, or by the radix rounds in the
+  // workgroup when a row has more); otherwise the 13 rounds run as launches
+  const int compact = has_k && has_p && a.top_k <= kCompact && a.nch <= kCompactChunks * 4;
   if (compact) hipLaunchKernelGGL(samp_topp_compact_kernel, dim3(a.R), dim3(256), 0, st, a);
-  if (has_p)
+  else if (has_p)
     for (int round = 0; round < kRounds; ++round)
-      hipLaunchKernelGGL(samp_topp_kernel, g, b, topp_lds_bytes(a.nch), st, a, round, compact);
+      hipLaunchKernelGGL(samp_topp_kernel, g, b, topp_lds_bytes(a.nch), st, a, round, 0);
   if (has_p || has_minp)
     hipLaunchKernelGGL(samp_keep_kernel, g, b, has_p ? topp_lds_bytes(a.nch) : 0, st, a, has_p, has_p ? 0 : 1,
                        compact);
