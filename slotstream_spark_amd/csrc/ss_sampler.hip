@@ -812,10 +812,8 @@ __global__ __launch_bounds__(64) void samp_draw_kernel(SampArgs a) {
     finish((int)(0xFFFFFFFFu - (uint32_t)k), 0, 0);
     return;
   }
-  const float* ct = stage(w.ftot, nch);
-  float total = 0.f;
-#pragma unroll 8
-  for (int q = 0; q < nch; ++q) total = total + ct[q];
+  const float* ct = stage(w.ftot, nch);  // zero-padded to a multiple of 16
+  const float total = lds_seq_sum(ct, nch, 0.f);
   if (!is_finite(total) || !(total > 0.f)) {
     const uint64_t k = max_u64_of(w.craw, nch);
     finish((int)(0xFFFFFFFFu - (uint32_t)k), 1, 0);
@@ -827,24 +825,25 @@ __global__ __launch_bounds__(64) void samp_draw_kernel(SampArgs a) {
   auto hit = [&](float x) { return ge ? x >= target : x > target; };
   int cs = -1, clast = -1;
   float base = 0.f, run = 0.f;
-  for (int q0 = 0; q0 < nch; q0 += 8) {
-    float t[8];
+  const float4* c4 = reinterpret_cast<const float4*>(ct);
+  for (int q0 = 0; q0 < nch; q0 += 16) {  // 16 unconditional reads (the padding is zero), then the in-order scan
+    const float4 a0 = c4[q0 / 4], a1 = c4[q0 / 4 + 1], a2 = c4[q0 / 4 + 2], a3 = c4[q0 / 4 + 3];
+    const float t[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
+                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
 #pragma unroll
-    for (int i = 0; i < 8; ++i) t[i] = q0 + i < nch ? ct[q0 + i] : 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < 16; ++i) {
+      const bool in = q0 + i < nch;
       const float nx = run + t[i];
-      const bool found = cs < 0 && hit(nx);
+      const bool found = in && cs < 0 && hit(nx);
       cs = found ? q0 + i : cs;
       base = found ? run : base;
-      clast = t[i] > 0.f ? q0 + i : clast;
-      run = nx;
+      clast = in && t[i] > 0.f ? q0 + i : clast;
+      run = in ? nx : run;
     }
   }
   if (cs < 0) {
     cs = clast < 0 ? 0 : clast;
-    base = 0.f;
-    for (int q = 0; q < cs; ++q) base = base + ct[q];
+    base = lds_seq_sum(ct, cs, 0.f);
   }
   const float st = w.stot[cs * 64 + lane];
   int bs = -1, blast = -1;
