@@ -64,6 +64,7 @@ struct Pool {
   std::string path;
   bool direct = false;
   int n_lanes = 1;
+  int device = 0;  // the device current at open: slots, tables, streams and every lane thread use it
   std::vector<Lane> lanes;
   std::vector<void*> chunk_dev;
   int32_t* map_dev = nullptr;    // caller's device table [layers * experts]
@@ -150,6 +151,10 @@ void free_lane(Lane& ln) {
 // or a HIP error; the other lanes stop at their next record. Waits for the lane's copies before returning.
 void read_lane(Pool* p, Lane& ln, const std::vector<int64_t>& offs, const std::vector<int32_t>& victims, size_t first,
                size_t step, std::atomic<bool>& ok, std::atomic<int64_t>& read_ns, std::atomic<int>& read_errno) {
+  if (hipSetDevice(p->device) != hipSuccess) {  // a new thread starts on device 0
+    ok = false;
+    return;
+  }
   const int fd = p->direct ? p->fd_direct : p->fd;
   int used = 0;
   for (size_t k = first; k < offs.size() && ok.load(std::memory_order_relaxed); k += step, ++used) {
@@ -198,6 +203,7 @@ hipError_t pool_open(const char* path, int layers, int experts, int64_t record_b
   Pool* p = new Pool();
   p->fd = fd;
   p->path = path;
+  if (hipGetDevice(&p->device) != hipSuccess) p->device = 0;
   p->file_bytes = sb.st_size;
   p->layers = layers;
   p->experts = experts;

@@ -140,9 +140,10 @@ class ExpertPool:
         self.map = torch.full((self.layers * experts,), -1, dtype=torch.int32, device=self.device)
         self.slot_ptr = torch.zeros(self.max_slots, dtype=torch.int64, device=self.device)
         h = ctypes.c_void_p()
-        _lib.check(_lib.lib().ssmoe_pool_open(str(packed / experts_name).encode(), self.layers, experts,
-                                              self.record_bytes, self.max_slots, int(chunk_bytes),
-                                              self.map.data_ptr(), self.slot_ptr.data_ptr(), ctypes.byref(h)))
+        with torch.cuda.device(self.device):  # the native pool allocates on, and stays bound to, this device
+            _lib.check(_lib.lib().ssmoe_pool_open(str(packed / experts_name).encode(), self.layers, experts,
+                                                  self.record_bytes, self.max_slots, int(chunk_bytes),
+                                                  self.map.data_ptr(), self.slot_ptr.data_ptr(), ctypes.byref(h)))
         self._h = h
         self._gen = 0
         self._progress = None
@@ -173,14 +174,16 @@ class ExpertPool:
         out = np.empty(ids.size, dtype=np.int32)
         t = np.zeros(6, dtype=np.int64)
         try:
-            _lib.check(_lib.lib().ssmoe_pool_ensure(self._h, int(layer), ids.ctypes.data, ids.size, int(gen),
-                                                    out.ctypes.data, t.ctypes.data))
+            with torch.cuda.device(self.device):
+                _lib.check(_lib.lib().ssmoe_pool_ensure(self._h, int(layer), ids.ctypes.data, ids.size, int(gen),
+                                                        out.ctypes.data, t.ctypes.data))
         finally:
             self.last_timing = dict(zip(("hits", "misses", "bytes", "total_ns", "read_ns", "copy_ns"), t.tolist()))
         return out
 
     def set_reader(self, lanes: int, direct: bool = False) -> None:
-        _lib.check(_lib.lib().ssmoe_pool_set_reader(self._h, int(lanes), int(bool(direct))))
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().ssmoe_pool_set_reader(self._h, int(lanes), int(bool(direct))))
 
     def load_all(self, layers=None, gen=None) -> None:
         """Every expert of the given layers (default: all the file holds) resident, one ensure per layer: the
@@ -189,7 +192,8 @@ class ExpertPool:
             self.ensure(layer, np.arange(self.experts, dtype=np.int32), gen)
 
     def resize_slots(self, n) -> None:
-        _lib.check(_lib.lib().ssmoe_pool_resize(self._h, int(n)))
+        with torch.cuda.device(self.device):
+            _lib.check(_lib.lib().ssmoe_pool_resize(self._h, int(n)))
 
     @property
     def slots(self) -> int:
