@@ -40,24 +40,40 @@ SS_DEV int align_key(const int32_t* le, int64_t i, int64_t R, int nl) {
 }
 
 // Per chunk: the rank of each row among the earlier rows of the chunk with the same key, and per-key counts.
+// Inside a wave the rank is the number of lower lanes holding the same key (one ballot per distinct key of the
+// wave, taken in lane order); the earlier waves of the chunk add their counts of that key from LDS.
 __global__ __launch_bounds__(kAlignChunk) void align_count_kernel(const int32_t* __restrict__ le, int64_t R, int nl,
                                                                   int32_t* __restrict__ rank,
                                                                   int32_t* __restrict__ chunk_cnt) {
-  extern __shared__ int sm_cnt[];  // [nl]
-  __shared__ int keys[kAlignChunk];
-  const int tid = threadIdx.x;
+  extern __shared__ uint8_t sm_cnt[];  // [kAlignChunk / 64 waves][nl + 2]: per-wave counts (<= 64) of every key
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  constexpr int NW = kAlignChunk / 64;
+  const int nk = nl + 2;  // keys 0 .. nl + 1 (nl: outside [0, nl), nl + 1: past R)
   const int64_t i = (int64_t)blockIdx.x * kAlignChunk + tid;
   const int key = align_key(le, i, R, nl);
-  keys[tid] = key;
-  for (int e = tid; e < nl; e += kAlignChunk) sm_cnt[e] = 0;
+  for (int e = tid; e < NW * nk; e += kAlignChunk) sm_cnt[e] = 0;
   __syncthreads();
-  int r = 0;
-#pragma unroll 8
-  for (int j = 0; j < kAlignChunk; ++j) r += (j < tid && keys[j] == key) ? 1 : 0;
+  // rank inside the wave: walk the wave's distinct keys in the order of their lowest lane
+  int r_in = 0;
+  uint64_t todo = ~0ull;
+  while (todo) {
+    const int l0 = (int)__builtin_ctzll(todo);
+    const int k0 = __builtin_amdgcn_readlane(key, l0);
+    const uint64_t same = __ballot(key == k0);
+    if (key == k0) r_in = __popcll(same & ((1ull << lane) - 1ull));
+    if (lane == l0) sm_cnt[w * nk + k0] = (uint8_t)__popcll(same);
+    todo &= ~same;
+  }
+  __syncthreads();
+  int r = r_in;
+  for (int v = 0; v < w; ++v) r += sm_cnt[v * nk + key];
   if (i < R) rank[i] = r;
-  if (key < nl) atomicAdd(&sm_cnt[key], 1);  // integer counts: any order gives the same totals
-  __syncthreads();
-  for (int e = tid; e < nl; e += kAlignChunk) chunk_cnt[(int64_t)blockIdx.x * nl + e] = sm_cnt[e];
+  for (int e = tid; e < nl; e += kAlignChunk) {
+    int c = 0;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) c += sm_cnt[v * nk + e];
+    chunk_cnt[(int64_t)blockIdx.x * nl + e] = c;
+  }
 }
 
 __global__ void align_zero_kernel(int nl, int32_t* __restrict__ tot) {
@@ -165,7 +181,8 @@ hipError_t launch_moe_align(const AlignArgs& a, hipStream_t st) {
   int32_t* tot = pad + a.num_local + 1;
   const int64_t P = padded_rows(a.R, a.num_local, a.block_m);
   if (nch > 0) {
-    hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(kAlignChunk), (size_t)a.num_local * 4, st, a.local_expert,
+    hipLaunchKernelGGL(align_count_kernel, dim3(nch), dim3(kAlignChunk), (size_t)(kAlignChunk / 64) * (a.num_local + 2),
+                       st, a.local_expert,
                        a.R, a.num_local, rank, chunk);
     hipLaunchKernelGGL(align_keyscan_kernel, dim3((a.num_local + 255) / 256), dim3(256), 0, st, a.num_local, nch,
                        chunk, tot);
