@@ -258,8 +258,50 @@ def lm_head_leg(steps, dev):
                        "traffic": traffic_of("lm_head_gemv"), "us_per_launch": r4["us_per_call"],
                        "bytes_per_launch": r4["bytes_per_call"]}
     res["shape"] = "N 248320 x K 2560, affine 4-bit gs64 (357.6 MB of weights), bf16 x"
+    res["reference_gb10_gbs"] = 232.95  # the reference's lm_head GEMV (tuning_gb10.json `248320x2560x4x64`)
+    res["speedup_vs_reference_gb10"] = round(r4["gbs"] / 232.95, 2)
     log(f"lm_head: R1 {res['R1']['us_per_call']} us, R2 {res['R2']['us_per_call']} us, R4 {r4['us_per_call']} us "
         f"({r4['gbs']} GB/s), fused greedy round D=3 {res['greedy_round_D3']['us_per_call']} us")
+    return res
+
+
+def ref_decode_leg(steps, dev):
+    """The reference's own published moe_decode benchmark, at its shape: hidden 2560, moe_intermediate 640, affine
+    4-bit gs64 records of 2,764,800 B, 1 row x 10 experts (27,648,000 B per step), cold (152.23 us / 181.6 GB/s on
+    GB10, slotstream_spark/kernels/tuning_gb10.json `moe`; records in pinned host memory there, in HBM here). Cold
+    here: 16 layers of 64 experts, each call on its own layer with 10 distinct experts, 442 MB per graph replay
+    (above the 256 MB Infinity Cache)."""
+    import torch
+
+    from slotstream_spark_amd.kernels.moe_gemv_affine import moe_decode
+    from slotstream_spark_amd.memory.slot_pool import SlotPool
+    from slotstream_spark_amd.memory.synth import normal_bf16
+
+    HR, IR, ER, NLR, KR = 2560, 640, 64, 16, 10
+    pool = SlotPool(NLR, ER, HR, IR, device=dev)
+    pool.fill_random(4242)
+    pool.place_permuted(4243)
+    g = torch.Generator().manual_seed(4244)
+    ids = [torch.randperm(ER, generator=g)[:KR].to(torch.int32).reshape(1, KR).to(dev) for _ in range(NLR)]
+    wts = [torch.softmax(torch.randn(1, KR, generator=g), dim=-1).to(dev) for _ in range(NLR)]
+    x = normal_bf16((1, HR), 1.0, 4245, dev)
+    hb = [torch.empty((1, KR, IR), device=dev) for _ in range(NLR)]
+    ob = [torch.empty((1, KR, HR), device=dev) for _ in range(NLR)]
+    outs = [torch.empty((1, HR), device=dev) for _ in range(NLR)]
+
+    def run():
+        for l in range(NLR):
+            moe_decode(x, ids[l], wts[l], l, pool.map, pool.slot_ptr, hb[l], ob[l], outs[l], experts_per_layer=ER)
+
+    ms = timed_graph(run, steps, 3, torch.cuda.Stream(device=dev))
+    us = ms * 1000.0 / NLR
+    nbytes = KR * 2_764_800
+    res = {"shape": "H 2560, I 640, 1 row x 10 experts, affine 4-bit gs64 (the reference model's)",
+           "us_per_step": round(us, 2), "bytes_per_step": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+           "reference_gb10_us_per_step": 152.23, "reference_gb10_gbs": 181.63,
+           "speedup_vs_reference_gb10": round(152.23 / us, 2)}
+    log(f"reference-shape moe_decode: {us:.2f} us per step ({res['gbs']} GB/s); GB10 reference 152.23 us")
+    del pool
     return res
 
 
@@ -499,8 +541,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4,lm_head,step,pool",
-                    help="comma list of timed legs: verify, decode, prefill, config2, config4, lm_head, step, pool")
+    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4,lm_head,step,pool,ref_decode",
+                    help="comma list of timed legs: verify, decode, prefill, config2, config4, lm_head, step, pool, "
+                         "ref_decode")
     ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--config2-steps", type=int, default=1000)
     ap.add_argument("--config4-layers", type=int, default=48)
@@ -629,6 +672,10 @@ def main():
     if "step" in legs:
         stp = step_leg(pool, weights, biases, max(args.steps // 5, 5), dev)
 
+    rd = None
+    if "ref_decode" in legs:
+        rd = ref_decode_leg(max(args.steps // 2, 10), dev)
+
     pl = None
     if "pool" in legs:
         pl = pool_leg(dev)
@@ -669,6 +716,7 @@ def main():
         "config4": c4,
         "lm_head": lmh,
         "step_graph": stp,
+        "reference_shape_moe_decode": rd,
         "pool": pl,
         "cpu_baseline": cpu,
     }
