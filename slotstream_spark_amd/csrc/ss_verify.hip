@@ -188,7 +188,10 @@ struct VSmem {
   int ids[kMaxQv];
   float wts[kMaxQv];
   float gx[64][kTBv];             // x group sums (H <= 4096)
-  float hsum[kMaxQv][16];         // h group sums per use (I <= 1024)
+  union alignas(16) {
+    float hsum[kMaxQv][16];       // h group sums per use (I <= 1024), phase D
+    uint64_t cand[kTBv][64];      // router-tail candidates of each token, phase B
+  };
   float shv[16][kTBv];
   float rnorm[kTBv];              // 1 / rms of each token (chained layers)
   float xch[4][16 * kTBv];        // per-wave exchange of one item's 16 columns x 4 tokens
@@ -268,8 +271,9 @@ SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
 }
 
 // Router tail of token t in one wave (the operations and order of router_topk_kernel): lane l holds the entries
-// e = l + 64 i. Each top-k round takes the 64-bit maximum of (key << 32 | ~e) over the untaken entries (taken or
-// absent entries are 0, below every present one), so ties go to the lower index.
+// e = l + 64 i. The top K in (probability desc, index asc) order come from a threshold and a rank count (below);
+// the K dependent rounds of router_topk_kernel remain for the rows that path does not take. Both give the same
+// ids, and the weights are summed in rank order either way.
 SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32_t tag, int t, VSmem& s,
                              const float (&bias_r)[kMaxEv / 64]) {
   const int lane = threadIdx.x & 63;
@@ -294,6 +298,7 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32
     }
     __builtin_amdgcn_s_sleep(1);
   }
+  if (a.trace && threadIdx.x == 0) a.trace[(size_t)blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();  // logits in
   float v[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) v[i] = ss_bf16_to_f32((uint16_t)wv[i]);
@@ -319,6 +324,66 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32
   for (int i = 0; i < NV; ++i) {
     v[i] = v[i] / z;
     kp[i] = lane + 64 * i < E ? ss_key(v[i]) + 1u : 0u;
+  }
+  // tau: the largest threshold with zero low 16 bits that at least K lane maxima reach. Those K entries are >= tau,
+  // so every entry of the top K is too. The entries >= tau (a few more than K on router rows) go to LDS in index
+  // order as (kp << 32 | 0xFFFF - e), a key whose order is the selection order; each candidate's rank is the number
+  // of larger keys. With more than 64 candidates, or no such tau (NaN probabilities have kp 1), the rounds run.
+  {
+    uint32_t lmax = kp[0];
+#pragma unroll
+    for (int i = 1; i < NV; ++i) lmax = kp[i] > lmax ? kp[i] : lmax;
+    uint32_t tau = 0;
+#pragma unroll
+    for (int b = 31; b >= 16; --b) {
+      const uint32_t c = tau | (1u << b);
+      tau = __popcll(__ballot(lmax >= c)) >= K ? c : tau;
+    }
+    uint64_t bal[NV];
+    int nc = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      bal[i] = __ballot(kp[i] >= tau);
+      nc += __popcll(bal[i]);
+    }
+    if (tau != 0 && nc <= 64) {
+      uint64_t* cs = s.cand[t];
+      int off = 0;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const uint64_t b = bal[i];
+        const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(b >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)b, 0u));
+        if ((b >> lane) & 1ull) cs[off + below] = ((uint64_t)kp[i] << 32) | (uint64_t)(0xFFFFu - (uint32_t)(lane + 64 * i));
+        off += __popcll(b);
+      }
+      const int ncp = (nc + 7) & ~7;  // zero keys pad the list to whole groups of 8; they rank below every key
+      if (lane >= nc && lane < ncp) cs[lane] = 0ull;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const uint64_t my = lane < nc ? cs[lane] : 0ull;
+      int rank = 0;
+#pragma unroll 1
+      for (int j = 0; j < ncp; j += 8) {
+        const ulonglong2* q = reinterpret_cast<const ulonglong2*>(cs + j);
+        const ulonglong2 q0 = q[0], q1 = q[1], q2 = q[2], q3 = q[3];
+        rank += (q0.x > my) + (q0.y > my) + (q1.x > my) + (q1.y > my) + (q2.x > my) + (q2.y > my) + (q3.x > my) +
+                (q3.y > my);
+      }
+      if (lane < nc && rank < K) {
+        s.ids[t * K + rank] = (int)(0xFFFFu - (uint32_t)my);
+        s.wts[t * K + rank] = ss_unkey((uint32_t)(my >> 32) - 1u);  // the probability itself (kp = key + 1)
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      const float pv = lane < K ? s.wts[t * K + lane] : 0.f;
+      float sum = 0.f;
+#pragma unroll 1
+      for (int r = 0; r < K; ++r) sum = sum + ss_readlane_f(pv, r);  // rank-order sum of the top-k probabilities
+      if (lane < K) s.wts[t * K + lane] = pv / sum;
+      return;
+    }
   }
   float mine = 0.f, sum = 0.f;
   int my_id = 0;
@@ -810,7 +875,6 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       }
     }
   };
-  SS_TRACE(5);
 
   // ------------------------------------------------------------ phase C: gate/up, one item per wave at a time
   // Items go first to the workgroups without down rows (bid >= H/16), one per wave, then wrap around.
