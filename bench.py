@@ -574,7 +574,10 @@ def main():
         del a, b
         log("copy calibration: 3 x 268435456-byte device copies done")
     NL, T = args.layers, args.tokens
-    NP = max(NL, args.config4_layers if "config4" in legs else 0, 49 if "step" in legs else 0)
+    # The records are placed by a permutation over every slot, so the pool's size fixes which weights each expert
+    # gets: config4 and the step graph both allocate one layer past config4's stack (the MTP layer), whichever legs
+    # run, so that their routing and unique-expert counts do not depend on the leg list.
+    NP = max(NL, args.config4_layers + 1 if "config4" in legs else 0, 49 if "step" in legs else 0)
     log(f"allocating {NP} layers x {E} experts ({NP * E * 1_769_472 / 2**30:.1f} GiB of records)")
     pool = SlotPool(NP, E, H, I, device=dev)
     pool.fill_random(1729)

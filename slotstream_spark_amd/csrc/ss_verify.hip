@@ -34,6 +34,7 @@ constexpr int kTBv = 4;          // tokens per launch
 constexpr int kMaxEv = 512;      // experts per layer (LDS tables)
 constexpr int kMaxQv = 64;       // kTBv * K, K <= 16
 constexpr int kSpinMax = 1 << 22;
+constexpr int kXZero = 98;       // uint4 zeros an inactive A lane reads in phase C: offsets 0 .. 48 * 2 (fp32 x)
 constexpr int SS_ERR_TIMEOUT = 16;
 constexpr size_t kLdsBudget = 160 * 1024 - 16 * 1024;  // dynamic LDS left after the static part (< 16 KB)
 
@@ -196,8 +197,11 @@ struct VSmem {
   float rnorm[kTBv];              // 1 / rms of each token (chained layers)
   float xch[4][16 * kTBv];        // per-wave exchange of one item's 16 columns x 4 tokens
   alignas(16) int ekey[64];       // unique_setup keys
+  alignas(16) uint4 zero_h[4];    // zeros: the h operand of A rows that do not use the expert (phase D)
   int nt, nu;
 };
+
+static_assert(kXZero * sizeof(uint4) <= sizeof(float) * kMaxQv * 16, "phase C zeros fit in hsum");
 
 SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 SS_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
@@ -727,6 +731,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 
   SS_TRACE(0);
   for (int i = tid; i < kMaxQv * kTBv; i += 256) (&s.umask[0][0])[i] = 0u;
+  if (tid < 4) s.zero_h[tid] = make_uint4(0u, 0u, 0u, 0u);
   if (tid == 0) s.nt = nt;
 
   // ------------------------------------------------------------ phase A + B (verify) / ids (decode)
@@ -771,29 +776,31 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 #pragma unroll 1
     for (int j = j_first; j < J; j += W) {
       if (j != j_first) load_job(j);
-      float d[kTBv];
-      dense_dot<NJX>(r0, xfl, nt, d);
-      if (lane == 0) {
-        if (j < E) {
+      // The job's rows (router or shared gate, then shared up, then the shared_expert_gate row) pass through r0 in
+      // turn, so the dot product has one copy in the code: each workgroup runs this phase once per launch, and its
+      // instruction footprint counts with its arithmetic.
+      const int nrow = j < E ? 1 : (j == J - 1 ? 3 : 2);
 #pragma unroll 1
-          for (int t = 0; t < nt; ++t)
-            st_ag(logits + (size_t)t * E + j, ((uint64_t)tag << 32) | (uint64_t)ss_f32_to_bf16(d[t]));
-        } else {
+      for (int q = 0; q < nrow; ++q) {
+        float d[kTBv];
+        dense_dot<NJX>(r0, xfl, nt, d);
+        if (lane == 0) {
+          if (j < E) {
 #pragma unroll 1
-          for (int t = 0; t < nt; ++t) st_ag(gsh + (j - E) + (size_t)t * Is, (uint16_t)ss_f32_to_bf16(d[t]));
+            for (int t = 0; t < nt; ++t)
+              st_ag(logits + (size_t)t * E + j, ((uint64_t)tag << 32) | (uint64_t)ss_f32_to_bf16(d[t]));
+          } else {
+            uint16_t* dst = q == 0 ? gsh + (j - E) : (q == 1 ? ush + (j - E) : sgl);
+            const size_t ts = q == 2 ? 1 : (size_t)Is;
+#pragma unroll 1
+            for (int t = 0; t < nt; ++t) st_ag(dst + (size_t)t * ts, (uint16_t)ss_f32_to_bf16(d[t]));
+          }
         }
-      }
-      if (j >= E) {
-        dense_dot<NJX>(r1, xfl, nt, d);
-        if (lane == 0)
-#pragma unroll 1
-          for (int t = 0; t < nt; ++t) st_ag(ush + (size_t)(j - E) + (size_t)t * Is, (uint16_t)ss_f32_to_bf16(d[t]));
-      }
-      if (j == J - 1) {
-        dense_dot<NJX>(r2, xfl, nt, d);
-        if (lane == 0)
-#pragma unroll 1
-          for (int t = 0; t < nt; ++t) st_ag(sgl + t, (uint16_t)ss_f32_to_bf16(d[t]));
+#pragma unroll
+        for (int jj = 0; jj < NJX; ++jj) {
+          r0[jj] = r1[jj];
+          r1[jj] = r2[jj];
+        }
       }
     }
     stores_done();
@@ -848,7 +855,13 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     }
     __syncthreads();
   }
-  if (tid < 64) unique_setup(a, s, verify);
+  if (tid < 64) {
+    unique_setup(a, s, verify);
+  } else {
+    // Zeros that phase C's A lanes outside their row block read instead of x (the router-tail candidates that
+    // share this memory are dead; phase D writes hsum only after every item is done).
+    for (int i = tid - 64; i < kXZero; i += 192) reinterpret_cast<uint4*>(s.hsum)[i] = make_uint4(0u, 0u, 0u, 0u);
+  }
   __syncthreads();
   SS_TRACE(4);
   const int nu = s.nu;
@@ -922,7 +935,8 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 #pragma unroll
         for (int jj = 0; jj < JB; ++jj) {
           const int j = j0 + jj;
-          const uint4* fp = xfl + (size_t)(((j * 4) * 4 + g) * kTBv + at) * (XF32 ? 2 : 1) + (XF32 ? apart : 0);
+          const uint4* fp = a_act ? xfl + (size_t)(((j * 4) * 4 + g) * kTBv + at) * (XF32 ? 2 : 1) + (XF32 ? apart : 0)
+                                  : reinterpret_cast<const uint4*>(s.hsum);  // zeros (kXZero entries)
 #pragma unroll
           for (int i = 0; i < 4; ++i) av4[jj][i] = fp[(size_t)i * 16 * (XF32 ? 2 : 1)];  // in bounds for every lane
           gxv[jj] = reinterpret_cast<const float4*>(s.gx)[2 * j + my_half];
@@ -934,7 +948,6 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             ss_u32x4 av = as_v(av4[jj][i]);
-            if (!a_act) av = ss_u32x4{0u, 0u, 0u, 0u};
             const uint32_t wd = i == 0 ? wv[j].x : i == 1 ? wv[j].y : i == 2 ? wv[j].z : wv[j].w;
             d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
           }
@@ -1089,7 +1102,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
           bvw[j] = reinterpret_cast<const uint32_t*>(sl + (size_t)NJD * 1024 + (size_t)16 * NJD * 4)[n * NJD + j];
           const size_t fo = (((size_t)aq * NJD + j) * 4 + g) * 8 + apart * 4;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) av4[j][i] = STAGED ? hfl[fo + i] : ld_ag16(hfrag + fo + i);
+          for (int i = 0; i < 4; ++i) av4[j][i] = STAGED ? (am ? hfl + fo : s.zero_h)[i] : ld_ag16(hfrag + fo + i);
 #pragma unroll
           for (int r = 0; r < kTBv; ++r) hsv[j][r] = s.hsum[qr[r]][2 * j + my_half];
         }
@@ -1100,7 +1113,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             ss_u32x4 av = as_v(av4[j][i]);
-            if (!am) av = ss_u32x4{0u, 0u, 0u, 0u};
+            if (!STAGED && !am) av = ss_u32x4{0u, 0u, 0u, 0u};  // staged: zero_h was read instead
             const uint32_t wd = i == 0 ? wq[j].x : i == 1 ? wq[j].y : i == 2 ? wq[j].z : wq[j].w;
             d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
           }
