@@ -1079,15 +1079,18 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       }
       // One expert: every operand is read up front (weights, scales, h fragments, h group sums; inactive lanes read
       // in-bounds index 0 and are zeroed by a select), then the MFMA chains run without intervening waits.
-      auto expert = [&](int u, auto staged) {
+      // NTK = 2 when T <= 2: the accumulators, h group sums and row sums of the two absent token rows are skipped
+      // (the combine reads rows r < T only).
+      auto expert = [&](int u, auto staged, auto ntk) {
         constexpr bool STAGED = decltype(staged)::value;
+        constexpr int NTK = decltype(ntk)::value;
         const uint8_t* sl = prefl + (size_t)(u - u0) * D.slot;
         const uint32_t am = a_lane ? s.umask[u][at] : 0u;
         const int aq = am ? at * K + __ffs(am) - 1 : 0;
         int qr[kTBv];
         bool vr[kTBv];
 #pragma unroll
-        for (int r = 0; r < kTBv; ++r) {
+        for (int r = 0; r < NTK; ++r) {
           const uint32_t mr = r < nt ? s.umask[u][r] : 0u;
           vr[r] = mr != 0u;
           qr[r] = mr ? r * K + __ffs(mr) - 1 : 0;
@@ -1104,7 +1107,7 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 #pragma unroll
           for (int i = 0; i < 4; ++i) av4[j][i] = STAGED ? (am ? hfl + fo : s.zero_h)[i] : ld_ag16(hfrag + fo + i);
 #pragma unroll
-          for (int r = 0; r < kTBv; ++r) hsv[j][r] = s.hsum[qr[r]][2 * j + my_half];
+          for (int r = 0; r < NTK; ++r) hsv[j][r] = s.hsum[qr[r]][2 * j + my_half];
         }
         float acc[kTBv] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1122,23 +1125,28 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
           const float s16 = sf * kNibbleScale;
           const float bp = my_part ? 0.f : __builtin_fmaf(-kNibbleScale, sf, bf);
 #pragma unroll
-          for (int r = 0; r < kTBv; ++r) {
+          for (int r = 0; r < NTK; ++r) {
             acc[r] = __builtin_fmaf(s16, d[r], acc[r]);
             acc[r] = __builtin_fmaf(bp, vr[r] ? hsv[j][r] : 0.f, acc[r]);
           }
         }
 #pragma unroll
-        for (int r = 0; r < kTBv; ++r) {
+        for (int r = 0; r < NTK; ++r) {
           acc[r] = ss_rows_sum(acc[r]);
           if (g == 0) partl[((size_t)u * 16 + n) * kTBv + r] = acc[r];
         }
       };
-      if (D.stage_h) {
+      using Two = std::integral_constant<int, 2>;
+      using Four = std::integral_constant<int, kTBv>;
+      if (D.stage_h && nt <= 2) {
 #pragma unroll 1
-        for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::true_type{});
+        for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::true_type{}, Two{});
+      } else if (D.stage_h) {
+#pragma unroll 1
+        for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::true_type{}, Four{});
       } else {
 #pragma unroll 1
-        for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::false_type{});
+        for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::false_type{}, Four{});
       }
     }
     SS_TRACE(10);
