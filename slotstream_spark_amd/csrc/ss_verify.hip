@@ -972,14 +972,24 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      {
+        // h = silu(gate) * up of one (token r, row c) per lane 8 r + c, written over that gate value.
+        const int r = lane >> 3, c = lane & 7;
+        if (r < nt) {
+          const float gv = xch[c * kTBv + r], uv = xch[(c + 8) * kTBv + r];
+          xch[c * kTBv + r] = gv / (1.f + ss_expf(-gv)) * uv;
+        }
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
       if (lane < nt) {
         const int r = lane;
         float hv[8];
         float sum8 = 0.f;
 #pragma unroll
         for (int c = 0; c < 8; ++c) {
-          const float gv = xch[c * kTBv + r], uv = xch[(c + 8) * kTBv + r];
-          hv[c] = gv / (1.f + ss_expf(-gv)) * uv;
+          hv[c] = xch[c * kTBv + r];
           sum8 = sum8 + hv[c];
         }
         uint32_t hw[4], lw[4];
