@@ -1179,14 +1179,23 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
     if (tid < 16 * kTBv) {
       const int c = tid >> 2, r = tid & 3;
       if (r < nt) {
+        // Every operand of the K terms is read before the first sum (K <= kMaxQv / kTBv; absent terms read entry 0
+        // and are dropped by the select), then the terms are added in rank order.
+        constexpr int KM = kMaxQv / kTBv;
+        float ov[KM];
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          const int q = r * K + (k < K ? k : 0), u = s.use_u[q];
+          const float pv = partl[((size_t)(u >= 0 ? u : 0) * 16 + c) * kTBv + r];
+          ov[k] = k < K && u >= 0 ? pv * s.wts[q] : 0.f;
+        }
         float acc = 0.f;
-#pragma unroll 1
-        for (int k = 0; k < K; ++k) {
-          const int q = r * K + k, u = s.use_u[q];
-          float o = 0.f;
-          if (u >= 0) o = partl[((size_t)u * 16 + c) * kTBv + r] * s.wts[q];
-          if (a.o_buf) a.o_buf[((size_t)r * K + k) * H + 16 * bid + c] = o;
-          acc = k == 0 ? o : acc + o;
+#pragma unroll
+        for (int k = 0; k < KM; ++k) {
+          if (k < K) {
+            if (a.o_buf) a.o_buf[((size_t)r * K + k) * H + 16 * bid + c] = ov[k];
+            acc = k == 0 ? ov[k] : acc + ov[k];
+          }
         }
         if (a.out) a.out[(size_t)r * H + 16 * bid + c] = acc;
         if (verify) {
