@@ -424,7 +424,10 @@ def config4_leg(pool, weights, biases, steps, dev):
     NL4, D, V, T = len(weights), 1, 151936, 2
     mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, b) for w, b in zip(weights, biases)]
     sg = MTPStepGraph(pool, mw, None, depth=D, top_k=K, device=dev)
-    sg.x_in.copy_(normal_bf16((T, H), 1.0, 1735, dev))
+    # every step verifies new rows (in the real loop: the embeddings of the tokens accepted so far), so the routing,
+    # and with it the experts each layer reads, changes from step to step
+    x_steps = normal_bf16((steps + 2, T, H), 1.0, 1735, dev)
+    sg.x_in.copy_(x_steps[0])
     tgt = torch.empty((steps, D + 1, V), device=dev)
     drf = torch.empty((steps, D, V), device=dev)
     for st in range(steps):
@@ -435,13 +438,18 @@ def config4_leg(pool, weights, biases, steps, dev):
     sg.capture()
     s_ = sg.stream
     with torch.cuda.stream(s_):
-        for _ in range(2):
+        for w_ in range(2):
+            sg.x_in.copy_(x_steps[steps + w_])
             sg.graph.replay()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        uniq_steps = []
         ev0.record(s_)
         for st in range(steps):
+            sg.x_in.copy_(x_steps[st])
             sg.graph.replay()
             out_g[st].copy_(acc.greedy_async(tgt[st], drafts[st]))
+            if st % 64 == 63:
+                uniq_steps.append(sg.ids.clone())
         ev1.record(s_)
     torch.cuda.synchronize()
     ms = ev0.elapsed_time(ev1)
@@ -450,18 +458,24 @@ def config4_leg(pool, weights, biases, steps, dev):
         rs.add(D, AcceptResult.from_out(o))
     emitted = sum(rs.emitted_by_round)
     tok_s = emitted / (ms * 1e-3)
-    uniq = [len(set(sg.ids[l].cpu().flatten().tolist())) for l in range(NL4)]
+    if not uniq_steps:
+        uniq_steps.append(sg.ids.clone())
+    uniq = [len(set(u[l].cpu().flatten().tolist())) for u in uniq_steps for l in range(NL4)]
+    same_route = sum(bool(torch.equal(uniq_steps[0][l], uniq_steps[1][l])) for l in range(NL4)) if len(uniq_steps) > 1 else None
     finite = bool(torch.isfinite(sg.streams[NL4].float()).all().item())
     log(f"config4: {NL4} layers x {steps} steps in {ms:.1f} ms ({ms * 1000 / steps:.1f} us/step, "
         f"{ms * 1000 / steps / NL4:.2f} us/layer); {emitted} tokens emitted, {tok_s:.0f} tokens/s; "
-        f"mean unique experts {sum(uniq) / NL4:.1f}, stream finite {finite}")
+        f"mean unique experts {sum(uniq) / len(uniq):.1f}, stream finite {finite}, layers routed alike in two "
+        f"sampled steps {same_route}")
     return {"layers": NL4, "steps": steps, "tokens": T, "ms_total": round(ms, 3),
             "us_per_step": round(ms * 1000 / steps, 2), "us_per_layer": round(ms * 1000 / steps / NL4, 3),
             "emitted_tokens": emitted, "acceptance_length": round(rs.acceptance_length, 4),
-            "effective_tokens_per_s": round(tok_s, 1), "unique_experts_mean": round(sum(uniq) / NL4, 2),
+            "effective_tokens_per_s": round(tok_s, 1), "unique_experts_mean": round(sum(uniq) / len(uniq), 2),
+            "layers_routed_alike_in_two_sampled_steps": same_route,
             "stream_finite": finite, "resident_expert_bytes": NL4 * E * 1_769_472,
-            "timing": "one HIP graph of the 48 chained layers (norm and residual add inside each verify launch) per "
-                      "step + greedy acceptance launches, events around the whole loop"}
+            "timing": "per step: a copy of that step's input rows, one HIP graph of the 48 chained layers (norm and "
+                      "residual add inside each verify launch), the greedy acceptance launches; events around the "
+                      "whole loop"}
 
 
 def traffic_of(kernel: str):

@@ -52,3 +52,44 @@ def test_hip_layer_matches_moe_ref_fixture(c):
     same = float(np.mean(bits(y) == Z[f"s{s}_y"]))
     print(f"y rel_l2 {err:.3e}; bf16 bits equal {same:.4f}")
     assert err <= 2e-2
+
+
+RZ = np.load(Path(__file__).resolve().parent / "golden" / "router_ref.npz")
+RCASES = json.loads(bytes(RZ["meta"]).decode())["cases"]
+
+
+@pytest.fixture(scope="module")
+def zero_pool():
+    pool = SlotPool(1, 512, 2048, 512)
+    pool.storage.zero_()                     # zero records: the experts contribute nothing, routing is unchanged
+    pool.place_permuted(9)
+    return pool
+
+
+def test_router_64_reference_seeds_on_gpu(zero_pool):
+    """ssmoe_router and the verify kernel's router phase against the oracle on the 64 seeds of router_ref.npz, with
+    and without the Zipf bias: logits bit for bit, ids and weights bit for bit (the oracle's ids are pinned to the
+    reference's torch CPU router, up to torch's tie order, by tests/test_oracle_pins.py)."""
+    from tests.golden.make_router_golden import inputs
+
+    K = 10
+    for c in RCASES:
+        s = c["seed"]
+        xb, rwb, bias = inputs(s)
+        x, rw, b = _bf16(xb), _bf16(rwb), torch.from_numpy(bias).cuda()
+        want_logits = O.dense_rows(xb, rwb)
+        for bb in (None, b):
+            logits = torch.empty((xb.shape[0], 512), dtype=torch.bfloat16, device="cuda")
+            ids, w = route(x, rw, K, bb, logits=logits)
+            zs = torch.zeros((512, 2048), dtype=torch.bfloat16, device="cuda")
+            layer = MoEVerifyLayer(zero_pool, 0, rw, zs, zs, torch.zeros((2048, 512), dtype=torch.bfloat16,
+                                                                          device="cuda"),
+                                   torch.zeros((1, 2048), dtype=torch.bfloat16, device="cuda"), top_k=K,
+                                   router_bias=bb)
+            _, vids, vw = layer(x)
+            torch.cuda.synchronize()
+            _, rids, rwt = O.router_topk(want_logits, K, None if bb is None else bias)
+            assert np.array_equal(bits(logits), want_logits), s
+            for got_i, got_w in ((ids, w), (vids, vw)):
+                assert np.array_equal(got_i.cpu().numpy(), rids), s
+                assert np.array_equal(got_w.cpu().numpy().view(np.uint32), rwt.view(np.uint32)), s

@@ -201,3 +201,48 @@ def test_combine_shared_bitwise(T, H):
     _lib.check(_lib.lib().ssmoe_combine_shared(routed.data_ptr(), sh.data_ptr(), sgl.data_ptr(), y.data_ptr(), T, H, 0))
     torch.cuda.synchronize()
     assert np.array_equal(bits(y), O.combine_shared(routed.cpu().numpy(), bits(sh), bits(sgl)))
+
+
+def test_moe_prefill_config3_full_size():
+    """BASELINE config 3 at its own size: 2048 tokens through the config-1 layer (E=512, top-10), routed by the
+    oracle's router with the Zipf(1.1) bias, so the head experts hold many 128-row M blocks each (reached through
+    block_expert and the XCD-contiguous tile order) and the tail experts a few rows. Every routed row against the
+    oracle (fused_moe_affine.py:136-172, moe_sweep.py:80-176 semantics), the combine bit for bit, the routed output
+    within the north-star bound of the fp64 exact-dequant reference."""
+    T, K, E, H, I = 2048, 10, 512, 2048, 512
+    print(f"[prefill config3] T={T} K={K} E={E}", flush=True)
+    pool = make_pool(E, H, I, seed=2048)
+    lw = LayerWeights(H, E, 512, seed=2049)
+    bias = zipf_bias(E, 1.1, 1731)
+    x = normal_bf16((T, H), 1.0, 2050)
+    _, _, rids, rwt = O.router(bits(x), bits(lw.router_w), K, bias.cpu().numpy())
+    counts = np.bincount(rids.reshape(-1), minlength=E)
+    print(f"experts touched {int((counts > 0).sum())}, rows of the largest {int(counts.max())}", flush=True)
+    assert counts.max() >= 4 * BLOCK_M                       # an expert spanning at least four M blocks
+    assert ((counts > 0) & (counts < BLOCK_M)).sum() >= 10   # and many single-block experts
+    layer = MoEPrefillLayer(pool, 0, lw.router_w, lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_g, top_k=K,
+                            router_bias=bias, max_tokens=T)
+    ids, w = torch.from_numpy(rids).cuda(), torch.from_numpy(rwt).cuda()
+    routed = layer.routed_experts(x, ids, w)
+    torch.cuda.synchronize()
+    assert _lib.device_error() == 0
+    cache = DenseCache(pool)
+    R = T * K
+    xf = O.bf16_to_f32(bits(x))
+    h_ref, rows_ref = O.prefill_rows(xf, np.arange(R) // K, rwt.reshape(-1), rids.reshape(-1),
+                                     lambda e: O.expert_bf16(cache.record(e), H, I))
+    h = layer.h_buf[:R].float().cpu().numpy()
+    rows = layer.out_rows[:R].cpu().numpy()
+    same_h = float(np.mean(h == h_ref))
+    err_rows = O.rel_l2(rows, rows_ref)
+    worst = max(O.rel_l2(rows[rids.reshape(-1) == e], rows_ref[rids.reshape(-1) == e]) for e in np.nonzero(counts)[0])
+    print(f"h bf16 equal {same_h:.4f}; out_rows rel_l2 {err_rows:.2e}, worst expert {worst:.2e}", flush=True)
+    assert same_h > 0.98
+    assert err_rows < 2e-3 and worst < 4e-3
+    assert np.array_equal(routed.cpu().numpy(), O.combine_rank_order(rows, T, K))
+    del h_ref, rows_ref
+    _, rows64 = O.prefill_rows(xf, np.arange(R) // K, rwt.reshape(-1), rids.reshape(-1),
+                               lambda e: O.expert_dense(cache.record(e), H, I, np.float64))
+    err = O.rel_l2(routed.cpu().numpy(), O.combine_rank_order(rows64, T, K))
+    print(f"routed vs exact-dequant fp64 rel_l2 {err:.2e}")
+    assert err < 2e-2

@@ -167,3 +167,36 @@ def test_head_moe_is_map_layer_nl(step):
     assert torch.equal(y, sg.head_y) and torch.equal(ids, sg.head_ids) and torch.equal(wt, sg.head_weights)
     _, _, rids, _ = O.router(bits(sg.mixed[NL]), bits(w.router_w), K, w.router_bias.cpu().numpy())
     assert np.array_equal(sg.head_ids.cpu().numpy(), rids)
+
+
+def test_chain_at_config4_layer_shape():
+    """BASELINE config 4's layer (E=512, top-10, T=2, Zipf bias, I 512, shared 512) in a chain of 4 fused launches,
+    replayed twice with different inputs, each layer against the oracle on its own input: ids and weights bit for
+    bit, y within the north-star bound, the stream and the final norm bit for bit."""
+    NL4, E4, K4, T = 4, 512, 10, 2
+    print(f"[chain config4] {NL4} layers, E={E4} K={K4} T={T}", flush=True)
+    pool = make_pool(E4, H, I, seed=505, layers=NL4)
+    lws = [LayerWeights(H, E4, 512, seed=510 + l) for l in range(NL4)]
+    mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, zipf_bias(E4, 1.1, 520 + l))
+          for l, w in enumerate(lws)]
+    norms = [normal_bf16((H,), 0.1, 530 + l) + 1 for l in range(NL4 + 1)]
+    sg = MTPStepGraph(pool, mw, None, depth=T - 1, norm_weights=norms, top_k=K4)
+    for trial in range(2):
+        sg.step(normal_bf16((T, H), 1.0, 540 + trial))
+        torch.cuda.synchronize()
+        for l in range(NL4):
+            xb = O.residual_rmsnorm(bits(sg.streams[l]), None, bits(norms[l]))[1]
+            w = mw[l]
+            _, _, rids, rw = O.router(xb, bits(w.router_w), K4, w.router_bias.cpu().numpy())
+            assert np.array_equal(sg.ids[l].cpu().numpy(), rids), (trial, l)
+            assert np.array_equal(sg.weights[l].cpu().numpy().view(np.uint32), rw.view(np.uint32)), (trial, l)
+            routed = O.moe_routed_fp64(O.bf16_to_f32(xb), rids, rw, DenseCache(pool, layer=l)).astype(np.float32)
+            sh, sgl = O.shared_expert(xb, bits(w.sh_gate), bits(w.sh_up), bits(w.sh_down), bits(w.sh_g))
+            ry = O.combine_shared(routed, sh, sgl)
+            err = O.rel_l2(O.bf16_to_f32(bits(sg.ys[l])), O.bf16_to_f32(ry))
+            assert err <= REL_Y, (trial, l, err)
+            so, mx = O.residual_rmsnorm(bits(sg.streams[l]), bits(sg.ys[l]), bits(norms[l + 1]))
+            assert np.array_equal(bits(sg.streams[l + 1]), so), (trial, l)
+        assert np.array_equal(bits(sg.mixed[NL4]), mx)
+        print(f"trial {trial}: unique experts per layer "
+              f"{[len(set(sg.ids[l].cpu().flatten().tolist())) for l in range(NL4)]}", flush=True)

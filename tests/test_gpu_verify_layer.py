@@ -78,3 +78,47 @@ def test_verify_rows_independent():
     for t in range(2):
         y1, i1, w1 = layer(x[t:t + 1].contiguous())
         assert torch.equal(y1[0], y2[t]) and torch.equal(i1[0], i2[t]) and torch.equal(w1[0], w2[t])
+
+
+def test_verify_router_ties_and_non_finite_fallback():
+    """The verify kernel's router tail selects the top K by a threshold when at most 64 entries reach it and by K
+    rounds otherwise; both must give the oracle's ids and weights bit for bit. Router columns 0 and 1 hold a few
+    quantised values, so token 0 (x = e0: three distinct logits, about 170 tied at the top) takes the rounds,
+    token 1 (x = e0 + e1: ten distinct logits, a tie group inside the top K) the threshold with ties, token 2 (a
+    non-finite element: NaN probabilities) the rounds, token 3 (random x) the threshold. The path of each token is
+    the one the numpy emulation of the selection (tests/test_oracle_pins.py) takes on the oracle's probabilities."""
+    from tests.test_oracle_pins import _threshold_select
+
+    E, K, H = 512, 10, 2048
+    pool = make_pool(E, H, 512, seed=61)
+    lw = LayerWeights(H, E, 512, seed=61)
+    rng = np.random.default_rng(63)
+    rw = rng.normal(0, 0.02, (E, H)).astype(np.float32)
+    rw[:, 0] = rng.integers(0, 3, E) / 128
+    rw[:, 1] = rng.integers(0, 8, E) / 128
+    x = np.zeros((4, H), np.float32)
+    x[0, 0] = 1
+    x[1, :2] = 1
+    x[2, :] = 1
+    x[2, 5] = np.inf
+    x[3] = rng.standard_normal(H)
+    rwb, xb = O.f32_to_bf16(rw), O.f32_to_bf16(x)
+    _, probs, rids, rwt = O.router(xb, rwb, K)
+    paths = [_threshold_select(probs[t], K) is not None for t in range(4)]
+    assert paths == [False, True, False, True]
+    assert len(np.unique(probs[1][rids[1]])) < K                 # ties inside token 1's top K
+    dev = lambda a: torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16).cuda()  # noqa: E731
+    layer = MoEVerifyLayer(pool, 0, dev(rwb), lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_g, top_k=K)
+    xt = dev(xb)
+    y, ids, w = layer(xt)
+    torch.cuda.synchronize()
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    got = w.cpu().numpy()
+    assert np.array_equal(np.isnan(got), np.isnan(rwt))
+    assert np.array_equal(np.nan_to_num(got).view(np.uint32), np.nan_to_num(rwt).view(np.uint32))
+    # the finite tokens' layer outputs are the oracle's
+    keep = [0, 1, 3]
+    routed = O.moe_routed_fp64(O.bf16_to_f32(xb[keep]), rids[keep], rwt[keep], DenseCache(pool)).astype(np.float32)
+    sh, sgl = O.shared_expert(xb[keep], bits(lw.sh_gate), bits(lw.sh_up), bits(lw.sh_down), bits(lw.sh_g))
+    ry = O.combine_shared(routed, sh, sgl)
+    assert O.rel_l2(O.bf16_to_f32(bits(y)[keep]), O.bf16_to_f32(ry)) <= REL_Y
