@@ -111,6 +111,19 @@ int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm
                                  uint16_t* stream_out, float* routed_out, int T, int H, int I, int Is, int K, int E,
                                  void* stream);
 
+/* ssmoe_moe_verify_layer without the workspace: the same arguments, outputs and bits, with the scratch in a static
+ * device array of the library (192 KiB per GPU, held until the process ends; shapes needing more, i.e. beyond
+ * I * K <= 8192, are refused with SSMOE_EINVAL). It allocates nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Every call on a GPU shares that GPU's array: calls that overlap on one GPU race, so issue them on one stream. The
+ * first call on a device clears the array with a kernel on `stream` (make that first call outside a capture). */
+int ssmoe_moe_verify_layer_noalloc(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
+                                   const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
+                                   const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,
+                                   const int64_t* slot_ptr, int64_t n_slots, int32_t* ids, float* weights,
+                                   uint16_t* y, float* routed_out, int T, int H, int I, int Is, int K, int E,
+                                   void* stream);
+
 /* Bytes of the workspace the acceptance entry points need (1 <= V <= 1,048,576, 0 <= D <= 60). Its first 16384
  * bytes hold cross-workgroup arrival counters: they must be zero before the first call (allocate
  * the workspace zeroed), and every call leaves them zero. Calls that share a workspace must not overlap. */

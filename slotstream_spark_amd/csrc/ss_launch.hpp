@@ -78,6 +78,9 @@ struct VerifyArgs {
 };
 size_t verify_scratch_bytes(int T, int H, int I, int Is, int K, int E);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
+// Zeroes `bytes` (a multiple of 16) at the 16-byte aligned `p` with vector stores (a kernel, so that it can sit in a
+// captured graph where a memset node could not).
+hipError_t launch_zero16(void* p, size_t bytes, hipStream_t st);
 
 // Prefill (ss_prefill.hip).
 struct AlignArgs {

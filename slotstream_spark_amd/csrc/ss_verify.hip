@@ -1270,6 +1270,20 @@ static hipError_t launch_nj(const VerifyArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+__global__ __launch_bounds__(256) void zero16_kernel(uint4* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+hipError_t launch_zero16(void* p, size_t bytes, hipStream_t st) {
+  const size_t n = bytes / 16;
+  if (n == 0) return hipSuccess;
+  const size_t blocks = (n + 255) / 256;
+  hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)(blocks < 1024 ? blocks : 1024)), dim3(256), 0, st,
+                     static_cast<uint4*>(p), n);
+  return hipGetLastError();
+}
+
 template <int NJG, int NJD>
 static hipError_t launch_x(const VerifyArgs& a, hipStream_t st) {
   return a.x_f32 ? launch_nj<NJG, NJD, true>(a, st) : launch_nj<NJG, NJD, false>(a, st);

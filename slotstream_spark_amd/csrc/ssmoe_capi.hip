@@ -5,6 +5,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <mutex>
 #include <string>
 
 #include "../../include/ssmoe.h"
@@ -19,6 +20,14 @@ __device__ int ss_status_storage;
 // its counters zero. Calls that overlap on one device share it and race.
 constexpr size_t kDecodeScratch = 320 * 1024;
 __device__ __align__(256) unsigned char ss_decode_scratch[kDecodeScratch];
+
+// Scratch of ssmoe_moe_verify_layer_noalloc, the verify layer for callers that cannot allocate: the counters, tagged
+// router logits, shared-expert rows and h fragments that ssmoe_moe_verify_layer keeps in the caller's workspace.
+// 192 KiB holds every (H, I, Is, K, E) the verify kernel takes with I * K <= 8192 (the BASELINE layer, H 2048 / I 512
+// / K 10, needs 127 KiB; the reference model's H 2560 / I 640 / K 10, 150 KiB). Host code never names this array
+// in a launch: it uses the address hipGetSymbolAddress returns for the current device (g_noalloc_scratch).
+constexpr size_t kNoAllocScratch = 192 * 1024;
+__device__ __align__(256) unsigned char ss_noalloc_scratch[kNoAllocScratch];
 
 namespace {
 
@@ -48,6 +57,8 @@ int hip_check(hipError_t e, const char* what) {
 constexpr int kMaxDevices = 64;
 int* g_status[kMaxDevices] = {nullptr};
 void* g_decode_scratch[kMaxDevices] = {nullptr};
+void* g_noalloc_scratch[kMaxDevices] = {nullptr};
+std::mutex g_noalloc_mu;
 
 int current_device(int* dev) {
   hipError_t e = hipGetDevice(dev);
@@ -80,6 +91,25 @@ int decode_scratch_ptr(void** out) {
     g_decode_scratch[dev] = p;
   }
   *out = g_decode_scratch[dev];
+  return ok();
+}
+
+// Device address of ss_noalloc_scratch on the current device. The first call on a device looks it up and clears it
+// with a fill kernel on `st` (ordered before the launch that follows on the same stream): the kernel needs its
+// counters at zero and no tagged logit word of an earlier launch left behind.
+int noalloc_scratch_ptr(void** out, hipStream_t st) {
+  int dev = 0;
+  if (int rc = current_device(&dev)) return rc;
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (!g_noalloc_scratch[dev]) {
+    void* p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(ss_noalloc_scratch));
+    if (e != hipSuccess) return hip_check(e, "hipGetSymbolAddress(no-alloc scratch)");
+    e = ss::launch_zero16(p, kNoAllocScratch, st);
+    if (e != hipSuccess) return hip_check(e, "no-alloc scratch clear");
+    g_noalloc_scratch[dev] = p;
+  }
+  *out = g_noalloc_scratch[dev];
   return ok();
 }
 
@@ -319,6 +349,27 @@ int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm
   return verify_layer_impl(stream_in, router_w, router_bias, sh_gate, sh_up, sh_down, sh_g, layer, map, map_len,
                            slot_ptr, n_slots, workspace, workspace_bytes, ids, weights, y, routed_out, T, H, I, Is, K,
                            E, stream, 1, norm_w, eps, stream_out);
+}
+
+int ssmoe_moe_verify_layer_noalloc(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
+                                   const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
+                                   const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,
+                                   const int64_t* slot_ptr, int64_t n_slots, int32_t* ids, float* weights,
+                                   uint16_t* y, float* routed_out, int T, int H, int I, int Is, int K, int E,
+                                   void* stream) {
+  if (int rc = check_moe_shape(T, H, I, K, E)) return rc;
+  if (Is < 8 || Is % 8 || Is > 512) return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, 512], got %d", Is);
+  if (E > 512) return fail(SSMOE_EINVAL, "need E <= 512, got %d", E);
+  const size_t need = ss::verify_scratch_bytes(kBlock, H, I, Is, K, E);
+  if (need > kNoAllocScratch)
+    return fail(SSMOE_EINVAL, "shape needs %zu bytes of scratch; the no-alloc entry point holds %zu (I * K <= 8192 "
+                "fits); use ssmoe_moe_verify_layer with a workspace", need, kNoAllocScratch);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* scratch = nullptr;
+  if (int rc = noalloc_scratch_ptr(&scratch, st)) return rc;
+  return verify_layer_impl(x, router_w, router_bias, sh_gate, sh_up, sh_down, sh_g, layer, map, map_len, slot_ptr,
+                           n_slots, scratch, (int64_t)kNoAllocScratch, ids, weights, y, routed_out, T, H, I, Is, K, E,
+                           stream, 0, nullptr, 0.f, nullptr);
 }
 
 int64_t ssmoe_accept_workspace_bytes(int D, int V) {
