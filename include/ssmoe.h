@@ -111,6 +111,41 @@ int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm
                                  uint16_t* stream_out, float* routed_out, int T, int H, int I, int Is, int K, int E,
                                  void* stream);
 
+/* One layer of ssmoe_moe_verify_chain: its weights, its map row and its outputs (device pointers). */
+typedef struct {
+  const uint16_t* router_w;  /* bf16 [E, H] */
+  const float* router_bias;  /* fp32 [E] or NULL */
+  const uint16_t* sh_gate;   /* bf16 [Is, H] */
+  const uint16_t* sh_up;     /* bf16 [Is, H] */
+  const uint16_t* sh_down;   /* bf16 [H, Is] */
+  const uint16_t* sh_g;      /* bf16 [1, H] */
+  const uint16_t* norm_w;    /* bf16 [H] or NULL (ones): the RMSNorm weight before the layer */
+  int64_t layer;             /* the layer's experts are at slot_ptr[map[layer * E + e]] */
+  int32_t* ids;              /* int32 [T, K] */
+  float* weights;            /* fp32 [T, K] */
+  uint16_t* y;               /* bf16 [T, H] */
+  uint16_t* stream_out;      /* bf16 [T, H] or NULL: bf16(stream + y), the next layer's residual stream */
+  float* routed_out;         /* fp32 [T, H] or NULL */
+} ssmoe_chain_layer;
+
+/* Bytes of the workspace ssmoe_moe_verify_chain needs (-1 on bad arguments). */
+int64_t ssmoe_verify_chain_workspace_bytes(int T, int H, int I, int Is, int K, int E);
+
+/* n_layers chained MoE layers of a verify step in one launch: layer l runs the layer of ssmoe_moe_verify_layer on
+ * x_l = bf16(rmsnorm(s_l) * norm_w_l), s_0 = stream_in, s_{l+1} = bf16(s_l + y_l) (the residual add of GraphSet._moe,
+ * runtime/graphs.py:160-169, with one stream and unit injection; rmsnorm as ssmoe_residual_rmsnorm). The same bits
+ * as n_layers calls of ssmoe_moe_verify_layer_chain; the next layer's router, shared-expert and table reads are issued
+ * during the current layer, and the stream passes between layers on the device without a launch.
+ * layers_host (host memory) and layers_dev (device memory) hold the same n_layers entries: the host copy is checked
+ * and supplies layer 0, the kernel reads the others from the device copy. 1 <= n_layers <= 4096; H 1024 with
+ * I in {128, 256, 512, 640, 1024}, or H 2048 with I in {128, 256, 512, 640} (other shapes: SSMOE_EINVAL);
+ * E + Is >= 4 * (compute units), so that every wave has a router or shared row in each layer, and H / 8 <= (compute
+ * units), so that the workgroups without output rows can take the shared expert's rows. */
+int ssmoe_moe_verify_chain(const uint16_t* stream_in, float eps, const ssmoe_chain_layer* layers_host,
+                           const ssmoe_chain_layer* layers_dev, int n_layers, const int32_t* map, int64_t map_len,
+                           const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes, int T,
+                           int H, int I, int Is, int K, int E, void* stream);
+
 /* ssmoe_moe_verify_layer without the workspace: the same arguments, outputs and bits, with the scratch in a static
  * device array of the library (192 KiB per GPU, held until the process ends; shapes needing more, i.e. beyond
  * I * K <= 8192, are refused with SSMOE_EINVAL). It allocates nothing. No counterpart in the reference: it is for

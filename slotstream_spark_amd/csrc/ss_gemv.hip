@@ -310,16 +310,10 @@ namespace {
 // One resident wave of work per SIMD slot: the grid is the occupancy of this instantiation times the CU count.
 template <int NJG, bool XF32>
 hipError_t launch_tiles(const GemvArgs& a, hipStream_t st) {
-  static int grid = 0;
-  if (grid == 0) {
-    int dev = 0, cus = 0, per_cu = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess)
-      e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, gemv_affine4_kernel<NJG, XF32>, 256, 0);
-    if (e != hipSuccess) return e;
-    grid = (per_cu > 0 ? per_cu : 1) * cus;
-  }
+  KernelCfg cfg;
+  hipError_t e = kernel_cfg(reinterpret_cast<const void*>(gemv_affine4_kernel<NJG, XF32>), 256, 0, &cfg);
+  if (e != hipSuccess) return e;
+  const int grid = (cfg.per_cu > 0 ? cfg.per_cu : 1) * cfg.cus;
   const int need = (a.ntiles + 3) / 4;
   hipLaunchKernelGGL((gemv_affine4_kernel<NJG, XF32>), dim3(need < grid ? need : grid), dim3(256), 0, st, a);
   return hipGetLastError();

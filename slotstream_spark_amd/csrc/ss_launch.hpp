@@ -6,7 +6,23 @@
 #include <string>
 #include <stdint.h>
 
+#include "../../include/ssmoe.h"
+
 namespace ss {
+
+// Launch configuration of one kernel on the current device, worked out once per (device, kernel) and kept per
+// device (ss_devcfg.hip): its dynamic LDS limit raised to max_dyn, its static LDS, the CU count, and how many
+// workgroups of `threads` threads with max_dyn bytes of dynamic LDS one CU holds at once. A kernel whose workgroups
+// wait on each other is launched with one workgroup per CU, and only when per_cu >= 1 at the largest dynamic LDS it
+// is ever given: then every workgroup of the grid is resident at once on an otherwise idle device.
+struct KernelCfg {
+  int threads;
+  size_t max_dyn;
+  size_t lds_static;
+  int cus;
+  int per_cu;
+};
+hipError_t kernel_cfg(const void* kern, int threads, size_t max_dyn, KernelCfg* out);
 
 // One dense bf16 row segment for launch_dense_rows: rows [0, n) of w (bf16 [n, H], row-major) against
 // every token; the fp32 dot is rounded once to bf16 and stored at out[t * out_ld + row].
@@ -81,6 +97,28 @@ hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
 // Zeroes `bytes` (a multiple of 16) at the 16-byte aligned `p` with vector stores (a kernel, so that it can sit in a
 // captured graph where a memset node could not).
 hipError_t launch_zero16(void* p, size_t bytes, hipStream_t st);
+
+// A chain of verify-mode layers in one persistent launch (ss_chain.hip). Layer 0 comes by value; layers 1 ..
+// NL-1 from `more` (device memory, ssmoe_chain_layer entries).
+struct ChainArgs {
+  const uint16_t* stream_in;     // [T, H] bf16: layer 0's input (norm_in: its residual stream)
+  int norm_in;                   // 1: layer 0 runs on bf16(rmsnorm(stream_in) * norm_w); 0: on stream_in itself
+  float eps;
+  ssmoe_chain_layer l0;
+  const ssmoe_chain_layer* more;  // [NL - 1]
+  int NL;
+  const int32_t* map;
+  int64_t map_len;
+  const int64_t* slot_ptr;
+  int64_t n_slots;
+  void* scratch;                 // chain_scratch_bytes(), counters zero on entry (the kernel leaves them zero)
+  int T, H, I, Is, K, E;
+  int* err;
+  uint64_t* trace;               // null, or [grid][16] phase timestamps of the last layer
+};
+size_t chain_scratch_bytes(int T, int H, int I, int Is, int K, int E);
+bool chain_shape_supported(int H, int I);
+hipError_t launch_chain(const ChainArgs& a, hipStream_t st);
 
 // Prefill (ss_prefill.hip).
 struct AlignArgs {

@@ -578,16 +578,11 @@ hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
   g.b2_off = rec.ub;
   // Grids cover the plan's upper bound of M blocks, rounded to whole XCD rounds; blocks past the device-side
   // count exit at once.
-  static bool attr = false;
-  if (!attr) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gemm_kernel<true>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLdsMax);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(prefill_gemm_kernel<false>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, (int)kGemmLdsMax);
-    if (e != hipSuccess) return e;
-    attr = true;
-  }
+  KernelCfg cfg;
+  hipError_t e = kernel_cfg(reinterpret_cast<const void*>(prefill_gemm_kernel<true>), 256, kGemmLdsMax, &cfg);
+  if (e == hipSuccess)
+    e = kernel_cfg(reinterpret_cast<const void*>(prefill_gemm_kernel<false>), 256, kGemmLdsMax, &cfg);
+  if (e != hipSuccess) return e;
   const int64_t mb = P / kBM;
   const int nt_gu = p.I / kGateUpTileN, nt_d = p.H / kDownTileN;
   auto grid_of = [&](int nt) { return (unsigned)(((mb * nt + 7) / 8) * 8); };

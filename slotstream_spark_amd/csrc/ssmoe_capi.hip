@@ -351,6 +351,79 @@ int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm
                            E, stream, 1, norm_w, eps, stream_out);
 }
 
+int64_t ssmoe_verify_chain_workspace_bytes(int T, int H, int I, int Is, int K, int E) {
+  if (T < 1 || T > kBlock || !ss::chain_shape_supported(H, I) || Is < 8 || Is % 8 || Is > 512 || K < 1 || K > 16 ||
+      E < K || E > 512)
+    return -1;
+  return (int64_t)ss::chain_scratch_bytes(kBlock, H, I, Is, K, E);
+}
+
+int ssmoe_moe_verify_chain(const uint16_t* stream_in, float eps, const ssmoe_chain_layer* layers_host,
+                           const ssmoe_chain_layer* layers_dev, int n_layers, const int32_t* map, int64_t map_len,
+                           const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes, int T,
+                           int H, int I, int Is, int K, int E, void* stream) {
+  if (int rc = check_moe_shape(T, H, I, K, E)) return rc;
+  if (T > kBlock) return fail(SSMOE_EINVAL, "a chain takes at most %d tokens, got %d", kBlock, T);
+  if (!ss::chain_shape_supported(H, I))
+    return fail(SSMOE_EINVAL, "no chain kernel for H=%d, I=%d (H 1024 with I <= 1024, or H 2048 with I <= 640); "
+                "launch the layers one by one (ssmoe_moe_verify_layer_chain)", H, I);
+  if (E > 512 || K > E) return fail(SSMOE_EINVAL, "need K <= E <= 512, got K=%d E=%d", K, E);
+  if (Is < 8 || Is % 8 || Is > 512) return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, 512], got %d", Is);
+  if (n_layers < 1 || n_layers > 4096) return fail(SSMOE_EINVAL, "n_layers must be in [1, 4096], got %d", n_layers);
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(SSMOE_EINVAL, "eps must be finite and >= 0");
+  if (!stream_in || !aligned(stream_in, 16)) return fail(SSMOE_EINVAL, "stream_in must be a 16-byte aligned pointer");
+  if (!layers_host || (n_layers > 1 && !layers_dev))
+    return fail(SSMOE_EINVAL, "layers_host (and, for more than one layer, layers_dev) must be non-null");
+  if (!map || !slot_ptr || !workspace || !aligned(workspace, 256))
+    return fail(SSMOE_EINVAL, "map, slot_ptr and a 256-byte aligned workspace are required");
+  for (int l = 0; l < n_layers; ++l) {
+    const ssmoe_chain_layer& q = layers_host[l];
+    if (!q.router_w || !q.sh_gate || !q.sh_up || !q.sh_down || !q.sh_g || !q.ids || !q.weights || !q.y)
+      return fail(SSMOE_EINVAL, "layer %d: weights, ids, weights and y must be non-null", l);
+    if (!aligned(q.router_w, 16) || !aligned(q.sh_gate, 16) || !aligned(q.sh_up, 16) || !aligned(q.sh_down, 16) ||
+        !aligned(q.sh_g, 16) || (q.norm_w && !aligned(q.norm_w, 16)))
+      return fail(SSMOE_EINVAL, "layer %d: weights must be 16-byte aligned", l);
+    if (q.layer < 0 || (q.layer + 1) * E > map_len)
+      return fail(SSMOE_EINVAL, "layer %d: map holds %lld entries, map row %lld needs %lld", l, (long long)map_len,
+                  (long long)q.layer, (long long)(q.layer + 1) * E);
+    if (q.stream_out && (q.stream_out == q.y || (l == 0 && q.stream_out == stream_in)))
+      return fail(SSMOE_EINVAL, "layer %d: stream_out must not alias y or stream_in", l);
+  }
+  const size_t need = ss::chain_scratch_bytes(kBlock, H, I, Is, K, E);
+  if (workspace_bytes < (int64_t)need)
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes, (long long)need);
+  int dev = 0, cus = 0;
+  if (int rc = current_device(&dev)) return rc;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    return fail(SSMOE_EHIP, "hipDeviceGetAttribute(multiprocessor count) failed");
+  if (E + Is < 4 * cus || H / 8 > cus)
+    return fail(SSMOE_EINVAL, "a chain needs E + Is >= 4 * CUs (one router or shared row per wave) and H / 8 <= CUs "
+                "(%d CUs; E + Is = %d, H = %d); launch the layers one by one", cus, E + Is, H);
+  int* err = nullptr;
+  if (int rc = status_ptr(&err)) return rc;
+  ss::ChainArgs a{};
+  a.stream_in = stream_in;
+  a.norm_in = 1;
+  a.eps = eps;
+  a.l0 = layers_host[0];
+  a.more = n_layers > 1 ? layers_dev + 1 : nullptr;
+  a.NL = n_layers;
+  a.map = map;
+  a.map_len = map_len;
+  a.slot_ptr = slot_ptr;
+  a.n_slots = n_slots;
+  a.scratch = workspace;
+  a.T = T;
+  a.H = H;
+  a.I = I;
+  a.Is = Is;
+  a.K = K;
+  a.E = E;
+  a.err = err;
+  a.trace = g_trace;
+  return hip_check(ss::launch_chain(a, static_cast<hipStream_t>(stream)), "verify chain launch");
+}
+
 int ssmoe_moe_verify_layer_noalloc(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
                                    const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
                                    const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,

@@ -27,7 +27,7 @@ import torch
 from .. import _lib
 from ..kernels.gemv_affine import AffineWeight, LMHeadGreedy
 from .accept import AcceptResult
-from .verify import MoEVerifyLayer
+from .verify import MoEVerifyChain, MoEVerifyLayer
 
 
 @dataclass
@@ -71,14 +71,15 @@ class MTPStepGraph:
     the table, runtime/pool.py:37-38). `norm_weights` (len(layers) + 1 bf16 [H] tensors, or None for ones) are the
     norms before each MoE and before the lm_head. Fill `x_in` [rows, H] bf16 and `drafts` int32 [depth], then
     `step()`; `result()` reads back the AcceptResult. `keep_logits` keeps the fp32 logits [rows, V] in `logits`.
-    `fused` folds each norm and residual add into the verify launch (ssmoe_moe_verify_layer_chain, one launch per
-    layer, `mixed[l]` for l < NL then not written); `fused=False` runs ssmoe_residual_rmsnorm between the layers.
-    Both give the same bits. `lm_head=None` leaves the lm_head and the acceptance out of the graph."""
+    `fused` folds each norm and residual add into the verify launches (`mixed[l]` for l < NL then not written): one
+    launch for all layers (ssmoe_moe_verify_chain) where the shape has a chain kernel and `single_launch`, else one
+    ssmoe_moe_verify_layer_chain launch per layer; `fused=False` runs ssmoe_residual_rmsnorm between the layers. All
+    give the same bits. `lm_head=None` leaves the lm_head and the acceptance out of the graph."""
 
     def __init__(self, pool, layers: list[MoEWeights], lm_head: AffineWeight, depth: int,
                  head: MoEWeights | None = None, norm_weights: list[torch.Tensor | None] | None = None,
                  eps: float = 1e-6, top_k: int = 10, keep_logits: bool = False, fused: bool = True,
-                 device="cuda"):
+                 single_launch: bool = True, device="cuda"):
         if not 1 <= depth <= 3:
             raise ValueError("depth must be 1..3 (the verify kernel takes up to 4 rows)")
         self.depth, self.rows = depth, depth + 1
@@ -117,6 +118,14 @@ class MTPStepGraph:
         self.head_weights = torch.zeros((R, top_k), dtype=torch.float32, device=dev)
         self.logits = (torch.zeros((R, lm_head.n), dtype=torch.float32, device=dev)
                        if keep_logits and lm_head is not None else None)
+        # fused: one launch for every layer where the shape has a chain kernel (ssmoe_moe_verify_chain)
+        self.chain = None
+        l0 = self.layers[0]
+        if self.fused and single_launch and MoEVerifyChain.supported(l0.hidden, l0.inter, l0.shared_inter,
+                                                                     l0.top_k, l0.experts, dev):
+            self.chain = MoEVerifyChain(self.layers, self.ys, list(self.ids), list(self.weights),
+                                        stream_outs=self.streams[1:], norm_weights=self.norm_weights[:self.nl],
+                                        eps=self.eps)
         self.lm_head = LMHeadGreedy(lm_head, depth, device=dev) if lm_head is not None else None
         self.out = self.lm_head.out if lm_head is not None else None
         self.stream = torch.cuda.Stream(device=dev)
@@ -126,9 +135,12 @@ class MTPStepGraph:
         """Every launch of the round on the current stream, reading only the static buffers."""
         w = self.norm_weights
         if self.fused:
-            for l, layer in enumerate(self.layers):
-                layer.chain(self.streams[l], self.ys[l], self.ids[l], self.weights[l], stream_out=self.streams[l + 1],
-                            norm_weight=w[l], eps=self.eps)
+            if self.chain is not None:
+                self.chain.run(self.streams[0])
+            else:
+                for l, layer in enumerate(self.layers):
+                    layer.chain(self.streams[l], self.ys[l], self.ids[l], self.weights[l],
+                                stream_out=self.streams[l + 1], norm_weight=w[l], eps=self.eps)
             residual_rmsnorm(self.streams[self.nl], None, self.mixed[self.nl], weight=w[self.nl], eps=self.eps)
         else:
             residual_rmsnorm(self.x_in, None, self.mixed[0], weight=w[0], eps=self.eps)

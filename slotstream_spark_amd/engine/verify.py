@@ -9,6 +9,8 @@ sync, so a step over many layers can be captured in one HIP graph.
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from .. import _lib
@@ -92,3 +94,79 @@ class MoEVerifyLayer:
             _lib.ptr(stream_out), _lib.ptr(routed), t, self.hidden, self.inter, self.shared_inter, self.top_k,
             self.experts, _lib.stream_of(stream)))
         return y, ids, weights
+
+
+class ChainLayerEntry(ctypes.Structure):
+    """ssmoe_chain_layer (include/ssmoe.h): one layer of a chain launch."""
+    _fields_ = [("router_w", ctypes.c_void_p), ("router_bias", ctypes.c_void_p), ("sh_gate", ctypes.c_void_p),
+                ("sh_up", ctypes.c_void_p), ("sh_down", ctypes.c_void_p), ("sh_g", ctypes.c_void_p),
+                ("norm_w", ctypes.c_void_p), ("layer", ctypes.c_int64), ("ids", ctypes.c_void_p),
+                ("weights", ctypes.c_void_p), ("y", ctypes.c_void_p), ("stream_out", ctypes.c_void_p),
+                ("routed_out", ctypes.c_void_p)]
+
+
+class MoEVerifyChain:
+    """Chained MoE layers of a verify step in one persistent launch (ssmoe_moe_verify_chain): layer l runs on
+    bf16(rmsnorm(s_l) * norm_w_l) with s_0 the input stream and s_{l+1} = bf16(s_l + y_l), the bits of one
+    MoEVerifyLayer.chain call per layer. The output buffers are fixed at construction (the device table holds their
+    addresses): ys[l], ids[l], weights[l] and, when given, stream_outs[l] (the stream after layer l)."""
+
+    def __init__(self, layers: list[MoEVerifyLayer], ys, ids, weights, stream_outs=None, norm_weights=None,
+                 eps: float = 1e-6):
+        if not layers:
+            raise ValueError("need at least one layer")
+        l0 = layers[0]
+        self.pool = l0.pool
+        self.hidden, self.inter, self.shared_inter = l0.hidden, l0.inter, l0.shared_inter
+        self.top_k, self.experts = l0.top_k, l0.experts
+        for q in layers:
+            if (q.pool is not self.pool or q.hidden != self.hidden or q.inter != self.inter or q.top_k != self.top_k
+                    or q.experts != self.experts or q.shared_inter != self.shared_inter):
+                raise ValueError("chained layers must share the pool and the layer shape")
+        n = len(layers)
+        norm_weights = list(norm_weights) if norm_weights is not None else [None] * n
+        stream_outs = list(stream_outs) if stream_outs is not None else [None] * n
+        if not (len(ys) == len(ids) == len(weights) == len(norm_weights) == len(stream_outs) == n):
+            raise ValueError("need one y, ids, weights, norm weight and stream_out entry per layer")
+        self.eps = float(eps)
+        self.layers = layers
+        self._keep = (ys, ids, weights, stream_outs, norm_weights)
+        table = (ChainLayerEntry * n)()
+        for i, q in enumerate(layers):
+            table[i] = ChainLayerEntry(q.router_w.data_ptr(), _lib.ptr(q.router_bias), q.sh_gate.data_ptr(),
+                                       q.sh_up.data_ptr(), q.sh_down.data_ptr(), q.sh_g.data_ptr(),
+                                       _lib.ptr(norm_weights[i]), q.layer, ids[i].data_ptr(), weights[i].data_ptr(),
+                                       ys[i].data_ptr(), _lib.ptr(stream_outs[i]), None)
+        self.table_host = table
+        raw = bytes(table)
+        self.table_dev = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.pool.device)
+        nb = _lib.lib().ssmoe_verify_chain_workspace_bytes(4, self.hidden, self.inter, self.shared_inter, self.top_k,
+                                                            self.experts)
+        if nb < 0:
+            raise ValueError(f"no chain kernel for H={self.hidden}, I={self.inter}")
+        self.workspace = torch.zeros(int(nb), dtype=torch.uint8, device=self.pool.device)
+
+    @staticmethod
+    def supported(hidden: int, inter: int, shared_inter: int, top_k: int, experts: int, device="cuda") -> bool:
+        """True when the shape has a chain kernel, every wave of the grid (one workgroup of 4 waves per CU) owns a
+        router or shared-expert row (E + Is >= 4 * CUs), which the chain's hand-offs rely on, and the workgroups
+        without output rows can take the shared expert's rows (H / 8 <= CUs)."""
+        cus = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
+        return (_lib.lib().ssmoe_verify_chain_workspace_bytes(4, hidden, inter, shared_inter, top_k, experts) > 0
+                and experts + shared_inter >= 4 * cus and hidden // 8 <= cus)
+
+    def run(self, stream_in: torch.Tensor) -> None:
+        """All layers on the current stream; the rows are those of stream_in ([T, H] bf16, T <= 4)."""
+        if (stream_in.dtype != torch.bfloat16 or stream_in.dim() != 2 or stream_in.shape[1] != self.hidden
+                or not stream_in.is_contiguous() or not stream_in.is_cuda):
+            raise ValueError(f"stream_in must be a contiguous bf16 [T, {self.hidden}] GPU tensor")
+        t = stream_in.shape[0]
+        ys = self._keep[0]
+        if t != ys[0].shape[0]:
+            raise ValueError(f"the chain's buffers hold {ys[0].shape[0]} rows, stream_in has {t}")
+        p = self.pool
+        _lib.check(_lib.lib().ssmoe_moe_verify_chain(
+            stream_in.data_ptr(), self.eps, ctypes.addressof(self.table_host), self.table_dev.data_ptr(),
+            len(self.layers), p.map.data_ptr(), p.map.numel(), p.slot_ptr.data_ptr(), p.slot_ptr.numel(),
+            self.workspace.data_ptr(), self.workspace.numel(), t, self.hidden, self.inter, self.shared_inter,
+            self.top_k, self.experts, _lib.stream_of(stream_in)))

@@ -169,11 +169,13 @@ def test_head_moe_is_map_layer_nl(step):
     assert np.array_equal(sg.head_ids.cpu().numpy(), rids)
 
 
-def test_chain_at_config4_layer_shape():
-    """BASELINE config 4's layer (E=512, top-10, T=2, Zipf bias, I 512, shared 512) in a chain of 4 fused launches,
-    replayed twice with different inputs, each layer against the oracle on its own input: ids and weights bit for
-    bit, y within the north-star bound, the stream and the final norm bit for bit."""
-    NL4, E4, K4, T = 4, 512, 10, 2
+@pytest.mark.parametrize("T,NL4", [(2, 4), (4, 3)])
+def test_chain_at_config4_layer_shape(T, NL4):
+    """BASELINE config 4's layer (E=512, top-10, Zipf bias, I 512, shared 512) chained, T = 2 (config 4) and T = 4
+    (config 2's rows), replayed twice with different inputs: the single launch of every layer
+    (ssmoe_moe_verify_chain) equals one launch per layer bit for bit, and each layer matches the oracle on its own
+    input (ids and weights bit for bit, y within the north-star bound, the stream and the final norm bit for bit)."""
+    E4, K4 = 512, 10
     print(f"[chain config4] {NL4} layers, E={E4} K={K4} T={T}", flush=True)
     pool = make_pool(E4, H, I, seed=505, layers=NL4)
     lws = [LayerWeights(H, E4, 512, seed=510 + l) for l in range(NL4)]
@@ -181,9 +183,16 @@ def test_chain_at_config4_layer_shape():
           for l, w in enumerate(lws)]
     norms = [normal_bf16((H,), 0.1, 530 + l) + 1 for l in range(NL4 + 1)]
     sg = MTPStepGraph(pool, mw, None, depth=T - 1, norm_weights=norms, top_k=K4)
+    per_layer = MTPStepGraph(pool, mw, None, depth=T - 1, norm_weights=norms, top_k=K4, single_launch=False)
+    assert sg.chain is not None
     for trial in range(2):
-        sg.step(normal_bf16((T, H), 1.0, 540 + trial))
+        x = normal_bf16((T, H), 1.0, 540 + trial)
+        per_layer.step(x)
+        sg.step(x)
         torch.cuda.synchronize()
+        for l in range(NL4):     # one launch for the chain = one launch per layer, bit for bit
+            assert torch.equal(sg.ids[l], per_layer.ids[l]) and torch.equal(sg.weights[l], per_layer.weights[l])
+            assert torch.equal(sg.ys[l], per_layer.ys[l]) and torch.equal(sg.streams[l + 1], per_layer.streams[l + 1])
         for l in range(NL4):
             xb = O.residual_rmsnorm(bits(sg.streams[l]), None, bits(norms[l]))[1]
             w = mw[l]
