@@ -3,15 +3,18 @@
 
 One step = a T=2 verify through `--layers` distinct full-size MoE layers (hidden 2048, 512 routed experts top-10,
 moe_intermediate 512, shared expert 512, affine-4bit gs64, Zipf(1.1) routing bias, experts in a 512-slot pool
-per layer behind a random slot permutation), captured as one HIP graph. Every layer reads the same bf16 input
-(no attention between layers), so the layers differ only in weights and routing; with 16 layers the touched bytes
-(about 44 MB per layer) exceed the 256 MB Infinity Cache, so each layer is read cold from HBM.
+per layer behind a random slot permutation), chained as in a verify step: a residual stream with an RMSNorm before
+every MoE layer (no attention), all layers in one persistent launch (ssmoe_moe_verify_chain), a fresh input each
+step. With 16 layers the touched bytes (about 33 MB per layer) exceed the 256 MB Infinity Cache, so each layer is
+read cold from HBM.
 
-Reported: value = microseconds per layer step (lower is better). The dominant kernel is the persistent verify
-kernel (one launch per layer), so `roofline` is its algorithmic bytes per launch (the measured unique-expert count
-of each layer) over its average launch time, both from the same HIP-event-timed graph replays. Also reported: the
-routed-only moe_decode launch on the same routing (`--legs` decode) and the CPU baseline, the torch-CPU
-restatement of the reference's moe_ref (oracle.moe_ref) on the same layer, timed on this host.
+Reported: value = microseconds per layer of the step (lower is better). The dominant kernel is the chain kernel (one
+launch per step), so `roofline` is its algorithmic bytes per launch (the sum over its layers of each layer's bytes at
+its measured unique-expert count) over its average launch time, both from HIP events around each replay on the
+launch's stream. Also reported: the same layers as 16 independent single-layer launches on one input (`isolated`),
+the routed-only moe_decode launch (`--legs` decode), measured achievable peaks (device copy, read stream, bf16 GEMM)
+beside the spec peaks, and the CPU baseline: the torch-CPU restatement of the reference's moe_ref (oracle.moe_ref),
+checked against the reference's fixtures first, timed on this host at config 0 and the config-1 shape.
 `--copy-calib` first runs three 256 MiB device-to-device copies, the known-size kernel that scales rocprofv3's
 FETCH_SIZE / WRITE_SIZE counters into bytes.
 """
@@ -132,6 +135,99 @@ def prefill_leg(pool, weights, biases, nl, steps, warmup, dev):
                          "us_per_launch": round(us_g, 2), "flop_per_launch": PREFILL_ROUTED_FLOP,
                          "expert_bytes_per_launch": int(wbytes),
                          "expert_stream_gbs": round(wbytes / (us_g * 1e-6) / 1e9, 1)}}
+
+
+def verify_chain_leg(pool, weights, biases, nl, t, steps, warmup, dev):
+    """BASELINE config 1 as a verify step: T tokens through `nl` chained config-1 layers in one persistent launch
+    (ssmoe_moe_verify_chain; each layer on the RMSNorm of the residual stream, the stream += y after it), a new input
+    copied in before each step (outside the timed interval). HIP events bracket each replay of the launch's graph on
+    its stream. Returns the timing, the layers' unique-expert counts and bytes."""
+    import torch
+
+    from slotstream_spark_amd.engine.step import MoEWeights, MTPStepGraph
+    from slotstream_spark_amd.memory.synth import normal_bf16
+
+    mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, b) for w, b in zip(weights[:nl], biases[:nl])]
+    sg = MTPStepGraph(pool, mw, None, depth=t - 1, top_k=K, device=dev)
+    if sg.chain is None:
+        raise RuntimeError("no chain kernel for the config-1 shape on this device")
+    xs = normal_bf16((8, t, H), 1.0, 1730, dev)
+    s = sg.stream
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        sg.chain.run(sg.streams[0])
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        sg.chain.run(sg.streams[0])
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    snaps = []
+    with torch.cuda.stream(s):
+        for st in range(warmup):
+            sg.x_in.copy_(xs[st % 8])
+            g.replay()
+        for st in range(steps):
+            sg.x_in.copy_(xs[st % 8])
+            evs[st][0].record(s)
+            g.replay()
+            evs[st][1].record(s)
+            if st < 8:
+                snaps.append(sg.ids.clone())
+    torch.cuda.synchronize()
+    ms = sum(a.elapsed_time(b) for a, b in evs)
+    us_step = ms * 1000.0 / steps
+    uniq = [[len(set(sn[l].cpu().flatten().tolist())) for l in range(nl)] for sn in snaps]
+    bytes_launch = sum(sum(layer_bytes(u, t) for u in row) for row in uniq) / len(uniq)
+    u_mean = sum(map(sum, uniq)) / (len(uniq) * nl)
+    gbs = bytes_launch / (us_step * 1e-6) / 1e9
+    finite = bool(torch.isfinite(sg.streams[nl].float()).all().item())
+    log(f"verify chain: {nl} layers in one launch, {us_step:.1f} us per step = {us_step / nl:.2f} us per layer "
+        f"({gbs:.0f} GB/s algorithmic), mean unique experts {u_mean:.1f}, stream finite {finite}")
+    del g, sg
+    return {"us_per_step": us_step, "us_per_layer": us_step / nl, "bytes_per_launch": bytes_launch,
+            "achieved_gbs": gbs, "unique_experts_mean": u_mean, "unique_experts_first_step": uniq[0],
+            "stream_finite": finite}
+
+
+def peaks_leg(dev):
+    """Measured achievable peaks beside the spec ones: a 1 GiB device copy (2 GiB moved), a 1 GiB fp32 sum (read
+    stream) and an 8192^3 bf16 GEMM on the platform BLAS; best of 10 launches each, HIP events."""
+    import torch
+
+    def best(fn, reps=10):
+        fn()
+        torch.cuda.synchronize()
+        out = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            out.append(e0.elapsed_time(e1) * 1e-3)
+        return min(out)
+
+    nb = 1 << 30
+    a = torch.empty(nb, dtype=torch.uint8, device=dev).fill_(1)
+    b = torch.empty_like(a)
+    t_copy = best(lambda: b.copy_(a))
+    del a, b
+    x = torch.ones(nb // 4, dtype=torch.float32, device=dev)
+    t_sum = best(lambda: x.sum())
+    del x
+    n = 8192
+    ga = torch.randn((n, n), device=dev, dtype=torch.bfloat16)
+    gb = torch.randn((n, n), device=dev, dtype=torch.bfloat16)
+    t_mm = best(lambda: torch.matmul(ga, gb), reps=5)
+    del ga, gb
+    torch.cuda.empty_cache()
+    res = {"copy_gbs": round(2 * nb / t_copy / 1e9, 1), "read_gbs": round(nb / t_sum / 1e9, 1),
+           "bf16_gemm_tflops": round(2 * n ** 3 / t_mm / 1e12, 1), "spec_hbm_gbs": HBM_PEAK_GBS,
+           "spec_bf16_tflops": MFMA_BF16_PEAK_TFLOPS,
+           "method": "best of 10 (GEMM: 5) launches, HIP events: 1 GiB copy_ (read + write counted), 1 GiB fp32 "
+                     "sum, 8192^3 bf16 torch.matmul"}
+    log(f"measured peaks: {res}")
+    return res
 
 
 def config2_leg(pool, lw, bias, steps, dev):
@@ -489,15 +585,70 @@ def traffic_of(kernel: str):
 
 
 def cpu_baseline(layer_w, bias, pool, x, layer_idx, budget_s):
-    """Torch-CPU restatement of moe_ref (dequantized fp32 experts cached, as the reference CPU path receives
-    them) on layer `layer_idx`; also the dequant-per-call variant. Returns the cpu_baseline object."""
+    """The reference's CPU path for this layer, restated on torch CPU (oracle.moe_ref, model/reference_torch.py:118-134),
+    timed on this host. First checked against the fixtures written from the reference's own moe_ref (ids and y bit for
+    bit). Then, within about `budget_s` seconds: the config-1 shape (this bench's layer 0, Zipf bias) with
+    dequantized fp32 experts cached (how the reference CPU path receives experts) at n threads (every CPU of the
+    process's affinity, capped by this host's CPU share in OMP_NUM_THREADS) and at 1 thread, the dequant-per-call
+    variant at n threads, and BASELINE config 0 (64 experts, top-4) at n and 1 threads. Medians of >= 15 steps where
+    the budget allows."""
+    import json as _json
+
     import numpy as np
     import torch
 
     from oracle import oracle as O
+    from tests.golden import gen
 
-    threads = min(len(os.sched_getaffinity(0)), 16)
-    torch.set_num_threads(threads)
+    # 1. the restatement against the reference's fixtures
+    Z = np.load(ROOT / "tests" / "golden" / "moe_ref_cases.npz")
+    cases = _json.loads(bytes(Z["meta"]).decode())["cases"]
+    checked = []
+    for c in cases:
+        if c["seed"] not in (0, 4):
+            continue
+        s_, T_, H_, E_, K_, I_, Is_ = (c[k] for k in ("seed", "T", "H", "E", "K", "I", "Is"))
+        xb, rw, sg, su, sd, sgg = (torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+                                   for a in gen.layer_inputs(s_, T_, H_, E_, Is_))
+        ex = {}
+
+        def fx(e, s_=s_, H_=H_, I_=I_, ex=ex):
+            if e not in ex:
+                ex[e] = tuple(torch.from_numpy(d) for d in O.expert_dense(gen.record(s_, e, H_, I_), H_, I_, np.float32))
+            return ex[e]
+
+        y, ti, _ = O.moe_ref(xb, rw, K_, fx, sg, su, sd, sgg)
+        # The fixtures carry the bits of the CPU that wrote them: torch's CPU bf16 GEMM rounds in an order that
+        # depends on the instruction set it dispatches to, so on another host a logit (and a y entry) can move by a
+        # bf16 step. Bit for bit on the fixture host (tests/test_oracle_pins.py); here: the same ids and y within the
+        # north-star bound.
+        yb = y.view(torch.int16).numpy().view(np.uint16)
+        same_ids = np.array_equal(ti.numpy().astype(np.int32), Z[f"s{s_}_ids"])
+        err = O.rel_l2(O.bf16_to_f32(yb), O.bf16_to_f32(Z[f"s{s_}_y"]))
+        if not same_ids or not err <= 2e-2:
+            raise RuntimeError(f"oracle.moe_ref differs from the reference fixture s{s_}: ids equal {same_ids}, "
+                               f"y rel_l2 {err:.3e}")
+        checked.append(f"s{s_} (E={E_}, top-{K_}: ids equal, y rel_l2 {err:.1e}, "
+                       f"{100.0 * float(np.mean(yb == Z[f's{s_}_y'])):.2f} % of y bit-identical)")
+
+    n_aff = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", n_aff) or n_aff)
+    n = max(1, min(n_aff, share))
+
+    def time_steps(fn, threads, seconds, min_steps=15, max_steps=200):
+        torch.set_num_threads(threads)
+        fn()
+        times = []
+        t_end = time.perf_counter() + seconds
+        while (time.perf_counter() < t_end or len(times) < 3) and len(times) < max_steps:
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+            if len(times) >= min_steps and time.perf_counter() > t_end:
+                break
+        return sorted(times)[len(times) // 2] * 1e6, len(times)
+
+    # 2. the config-1 shape: this bench's layer
     xc = x.cpu()
     rw, sg, su, sd, sgw = (t.cpu() for t in (layer_w.router_w, layer_w.sh_gate, layer_w.sh_up, layer_w.sh_down,
                                              layer_w.sh_g))
@@ -520,30 +671,32 @@ def cpu_baseline(layer_w, bias, pool, x, layer_idx, budget_s):
             cache[e] = dequant(e)
         return cache[e]
 
-    O.moe_ref(xc, rw, K, cached, sg, su, sd, sgw, bc)          # warm + fill the cache for the routed experts
-    times = []
-    t_end = time.perf_counter() + budget_s * 0.7
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        O.moe_ref(xc, rw, K, cached, sg, su, sd, sgw, bc)
-        times.append(time.perf_counter() - t0)
-        if len(times) >= 200:
-            break
-    per_call = []
-    t_end = time.perf_counter() + budget_s * 0.3
-    while time.perf_counter() < t_end or len(per_call) < 2:
-        t0 = time.perf_counter()
-        O.moe_ref(xc, rw, K, dequant, sg, su, sd, sgw, bc)
-        per_call.append(time.perf_counter() - t0)
-        if len(per_call) >= 50:
-            break
-    med = sorted(times)[len(times) // 2] * 1e6
-    med_b = sorted(per_call)[len(per_call) // 2] * 1e6
-    return {"value": round(med, 1), "unit": "us per T=2 verify step per MoE layer", "cores": threads,
-            "kind": "port",
-            "sample": f"torch-CPU moe_ref restatement, config-1 layer, T=2, {len(times)} steps (median), "
-                      f"dequantized fp32 experts cached",
-            "dequant_per_call_us": round(med_b, 1), "dequant_per_call_steps": len(per_call)}
+    c1 = lambda: O.moe_ref(xc, rw, K, cached, sg, su, sd, sgw, bc)  # noqa: E731
+    c1_pc = lambda: O.moe_ref(xc, rw, K, dequant, sg, su, sd, sgw, bc)  # noqa: E731
+    v1_n, s1_n = time_steps(c1, n, budget_s * 0.3)
+    v1_1, s1_1 = time_steps(c1, 1, budget_s * 0.25, min_steps=5)
+    vpc_n, spc_n = time_steps(c1_pc, n, budget_s * 0.15, min_steps=3)
+
+    # 3. 64 experts, top-4 (the fixture generator's seed-0 layer)
+    x0, rw0, sg0, su0, sd0, sgg0 = (torch.from_numpy(a.view(np.int16).copy()).view(torch.bfloat16)
+                                    for a in gen.layer_inputs(0, 2, H, 64, IS))
+    ex0 = {e: tuple(torch.from_numpy(d) for d in O.expert_dense(gen.record(0, e, H, I), H, I, np.float32))
+           for e in range(64)}
+    c0 = lambda: O.moe_ref(x0, rw0, 4, ex0.__getitem__, sg0, su0, sd0, sgg0)  # noqa: E731
+    v0_n, s0_n = time_steps(c0, n, budget_s * 0.15)
+    v0_1, s0_1 = time_steps(c0, 1, budget_s * 0.15, min_steps=5)
+    torch.set_num_threads(n)
+    res = {"value": round(v1_n, 1), "unit": "us per T=2 verify step per MoE layer", "cores": n, "kind": "port",
+           "sample": f"torch-CPU moe_ref restatement (checked against the reference fixtures "
+                     f"{', '.join(checked)}), config-1 layer (512 experts top-10, Zipf bias), T=2, dequantized fp32 "
+                     f"experts cached, median of {s1_n} steps at {n} threads",
+           "cores_affinity": n_aff, "cpu_share": share,
+           "config1_1thread_us": round(v1_1, 1), "config1_1thread_steps": s1_1,
+           "config1_dequant_per_call_us": round(vpc_n, 1), "config1_dequant_per_call_steps": spc_n,
+           "config0_us": round(v0_n, 1), "config0_steps": s0_n,
+           "config0_1thread_us": round(v0_1, 1), "config0_1thread_steps": s0_1,
+           "tokens_per_s_config1": round(2 / (v1_n * 1e-6), 1)}
+    return res
 
 
 def main():
@@ -555,9 +708,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="verify,decode,prefill,config2,config4,lm_head,step,pool,ref_decode",
-                    help="comma list of timed legs: verify, decode, prefill, config2, config4, lm_head, step, pool, "
-                         "ref_decode")
+    ap.add_argument("--legs", default="isolated,decode,prefill,config2,config4,lm_head,step,pool,ref_decode,peaks",
+                    help="comma list of legs besides the headline chain: isolated, decode, prefill, config2, "
+                         "config4, lm_head, step, pool, ref_decode, peaks")
     ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--config2-steps", type=int, default=1000)
     ap.add_argument("--config4-layers", type=int, default=48)
@@ -605,41 +758,35 @@ def main():
     ids = [torch.empty((T, K), dtype=torch.int32, device=dev) for _ in range(NL)]
     wts = [torch.empty((T, K), dtype=torch.float32, device=dev) for _ in range(NL)]
 
+    # the headline: the chained verify step, every layer in one launch
+    chain = verify_chain_leg(pool, weights, biases, NL, T, args.steps, args.warmup, dev)
+    us_layer = chain["us_per_layer"]
+    ms_step = chain["us_per_step"] / 1000.0
+    layer_gbs = chain["achieved_gbs"]
+
     def step():
         for l in range(NL):
             layers[l](x, y=ys[l], ids=ids[l], weights=wts[l])
 
     s = torch.cuda.Stream(device=dev)
-    s.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(s):
-        for _ in range(3):
-            step()
-    torch.cuda.current_stream().wait_stream(s)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        step()
-    log("step graph captured")
-    for _ in range(args.warmup):
-        g.replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    ev0.record()
-    for _ in range(args.steps):
-        g.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    ms_step = ev0.elapsed_time(ev1) / args.steps
-    us_layer = ms_step * 1000.0 / NL
-    uniq = [len(set(ids[l].cpu().flatten().tolist())) for l in range(NL)]
-    bytes_step = sum(layer_bytes(u, T) for u in uniq)
-    layer_gbs = bytes_step / (ms_step * 1e-3) / 1e9
-    log(f"layer step {us_layer:.2f} us ({layer_gbs:.0f} GB/s algorithmic), unique experts {uniq}")
+    iso = None
+    uniq = None
+    if "isolated" in legs or "decode" in legs:
+        # the same layers as independent single-layer launches on one input (the round-1 method)
+        ms_iso = timed_graph(step, args.steps, args.warmup, s)
+        uniq = [len(set(ids[l].cpu().flatten().tolist())) for l in range(NL)]
+        bytes_iso = sum(layer_bytes(u, T) for u in uniq)
+        iso = {"us_per_layer": round(ms_iso * 1000.0 / NL, 3),
+               "achieved_gbs": round(bytes_iso / (ms_iso * 1e-3) / 1e9, 1), "unique_experts": uniq,
+               "kernel": "verify_kernel, one launch per layer, every layer on the same input, in one HIP graph"}
+        log(f"isolated layers: {iso['us_per_layer']:.2f} us per layer ({iso['achieved_gbs']:.0f} GB/s), "
+            f"unique experts {uniq}")
 
     us_moe = moe_gbs = moe_bytes = None
     if "decode" in legs:
         # Routed experts only (moe_decode, decode mode of the same kernel) on the routing of the step, one graph of
         # NL calls.
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         hb = [torch.empty((T, K, I), device=dev) for _ in range(NL)]
         ob = [torch.empty((T, K, H), device=dev) for _ in range(NL)]
         outb = [torch.empty((T, H), device=dev) for _ in range(NL)]
@@ -697,6 +844,8 @@ def main():
     if "pool" in legs:
         pl = pool_leg(dev)
 
+    peaks = peaks_leg(dev) if "peaks" in legs else None
+
     cpu = None
     if not args.no_cpu:
         log("timing the CPU baseline")
@@ -716,16 +865,21 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (seeded random affine-4bit experts and bf16 router/shared weights; no checkpoint)",
-        "config": {"workload": f"config1: T={T} verify through one MoE layer (H2048, E512 top-10, I512, shared 512, "
-                               f"affine-4bit gs64, Zipf 1.1), timed over {NL} resident layers per step",
-                   "layers_per_step": NL, "tokens": T, "unique_experts_mean": sum(uniq) / NL,
+        "config": {"workload": f"config1: T={T} verify through the config-1 MoE layer (H2048, E512 top-10, I512, "
+                               f"shared 512, affine-4bit gs64, Zipf 1.1), {NL} distinct layers chained per step "
+                               f"(RMSNorm + residual between them) in one launch, a new input each step",
+                   "layers_per_step": NL, "tokens": T, "unique_experts_mean": round(chain["unique_experts_mean"], 2),
                    "parallelism": "single GPU"},
         "hbm_gbs_layer": round(layer_gbs, 1),
         "tokens_per_s_layer": round(T / (us_layer * 1e-6), 1),
-        "roofline": {"bound": "hbm", "kernel": "verify_kernel (verify mode: router + routed + shared + combine)",
+        "roofline": {"bound": "hbm", "kernel": f"chain_kernel ({NL} layers per launch: norm, router, routed and "
+                                               f"shared experts, combine, residual)",
                      "achieved": round(layer_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of("verify_kernel"),
-                     "us_per_launch": round(us_layer, 3), "bytes_per_launch": int(bytes_step / NL)},
+                     "frac": round(layer_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_of("chain_kernel"),
+                     "us_per_launch": round(chain["us_per_step"], 2), "bytes_per_launch": int(chain["bytes_per_launch"]),
+                     "bytes_per_layer": int(chain["bytes_per_launch"] / NL)},
+        "isolated": iso,
+        "measured_peaks": peaks,
         "moe_decode": None if us_moe is None else {
             "us_per_launch": round(us_moe, 3), "bytes_per_launch": int(moe_bytes), "achieved_gbs": round(moe_gbs, 1)},
         "prefill": prefill,
