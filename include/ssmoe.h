@@ -275,11 +275,70 @@ int64_t ssmoe_lm_head_greedy_workspace_bytes(int D, int N);
 
 /* The lm_head GEMV over the D+1 verify rows fused with the greedy round after it (engine/generate.py:208-229 at
  * temperature 0): each 16-row tile of the vocabulary reduces to one argmax key and a non-finite flag per row, so the
- * round reads no logits. out int32 [D+5] as ssmoe_accept_greedy (n_accept, n_emit, 0, flags 1 = non-finite row,
- * 2 = draft out of range, tokens). logits fp32 [D+1][N] is written too when non-null. 0 <= D <= 60. */
+ * round reads no logits. The logits are lin's result, lin(final, lm_head).float() (runtime/graphs.py:202): for a bf16
+ * x the fp32 dot rounded to bf16, for an fp32 x the dot itself. out int32 [D+5] as ssmoe_accept_greedy (n_accept,
+ * n_emit, 0, flags 1 = non-finite row, 2 = draft out of range, tokens). logits fp32 [D+1][N] (those values) is
+ * written too when non-null. 0 <= D <= 60. */
 int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
                          const uint16_t* b, int N, const int32_t* drafts, void* workspace, int64_t workspace_bytes,
                          float* logits, int32_t* out, void* stream);
+
+/* Bytes of the workspace ssmoe_lm_head_argmax needs (-1 on bad arguments). */
+int64_t ssmoe_lm_head_argmax_workspace_bytes(int R, int N);
+
+/* The draft token of each row: torch.argmax(lin(out, lm_head).float()) of MTPHead.draft (engine/mtp.py:275-276,
+ * logits at engine/mtp.py:232-236). round_bf16 != 0 takes the argmax over the logits rounded to bf16 (lin returns
+ * the dtype of x, bf16 for the head); ties and NaN as torch.argmax (the first maximal index; NaN counts as the
+ * maximum). ids int32 [R] on the device; logits fp32 [R][N] (the values ranked) is written too when non-null.
+ * 1 <= R <= 64, K as ssmoe_gemv_affine4. */
+int ssmoe_lm_head_argmax(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s,
+                         const uint16_t* b, int N, int round_bf16, void* workspace, int64_t workspace_bytes,
+                         float* logits, int32_t* ids, void* stream);
+
+/* ---------------------------------------------------------------- MTP draft head (dense part, no attention) */
+
+/* RMSNorm with folded weight (model/reference_torch.py:30-38): out = bf16((x * r) * w) over each group of `group`
+ * elements of a row, r = 1 / sqrt(sum(x^2) / group + eps) in fp32 (lane l of a wave sums the 8-element chunks l,
+ * l + 64, ... of the group with fmaf from 0, then the xor butterfly). group = n is the plain norm (fuse's
+ * pre_fc_norm_hidden over hc * H, engine/mtp.py:190); group = H is the per-branch norm of hc_mix
+ * (model/layers.py:192). x, out bf16 [R][n], 16-byte aligned, not aliased; w bf16 [n] or NULL (ones); group a
+ * multiple of 8 dividing n. */
+int ssmoe_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int R, int n, int group, uint16_t* out,
+                  void* stream);
+
+/* Elementwise op fused behind ssmoe_dense_gemv_epi: the GEMV rounds its fp32 dot d to bf16 (v = bf16(d), the
+ * result of lin) and then, with torch's bf16 rounding after each step: */
+#define SSMOE_EPI_NONE 0     /* v */
+#define SSMOE_EPI_ADD 1      /* bf16(add[(r / add_div)][n] + v): e.unsqueeze(-2) + h of fuse (engine/mtp.py:192) */
+#define SSMOE_EPI_SILU_DIV 2 /* silu(bf16(v / hc)): hc_mix's low-rank input (model/layers.py:193) */
+#define SSMOE_EPI_SIGMOID 3  /* sigmoid(v): hc_mix's mix weights (model/layers.py:194) */
+#define SSMOE_EPI_INJECT 4   /* 2 * bf16(sigmoid(bf16(v / hc))): hc_mix's injection (model/layers.py:198) */
+
+/* lin for a bf16 weight (model/layers.py:62-76, the batch-invariant dense gemv) with one SSMOE_EPI_* op fused:
+ * out[r][n] = epi(bf16(sum_k x[r][k] w[n][k])), fp32 sum in the order of ssmoe_dense_gemv_bf16 (lane l of a wave sums
+ * the 8-element chunks l, l + 64, ... with fmaf from 0, then the xor butterfly); silu(u) = u / (1 + exp(-u)),
+ * sigmoid(u) = 1 / (1 + exp(-u)) with the fp32 exp of the router. x bf16 [R][K], w bf16 [N][K], out bf16 [R][N],
+ * add bf16 [ceil(R / add_div)][N] (SSMOE_EPI_ADD only). K a multiple of 8, x and w 16-byte aligned. */
+int ssmoe_dense_gemv_epi(const uint16_t* x, int R, int K, const uint16_t* w, int N, int epi, int hc,
+                         const uint16_t* add, int add_div, uint16_t* out, void* stream);
+
+/* The weighted mean of hc_mix (model/layers.py:195): mixed[s][j] = bf16(sum_c bf16(m[s][c H + j] hn[s][c H + j]) /
+ * hc), the sum over c = 0 .. hc-1 in order. m, hn bf16 [S][hc H]; mixed bf16 [S][H]. */
+int ssmoe_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed, void* stream);
+
+/* The hyper-connection residual (engine/mtp.py:226, h + (m.unsqueeze(-2) * inj.unsqueeze(-1)).flatten(-2)):
+ * out[s][c H + j] = bf16(hyp[s][c H + j] + bf16(y[s][j] inj[s][c])). hyp, out bf16 [S][hc H] (out may be hyp),
+ * y bf16 [S][H], inj bf16 [S][hc]. */
+int ssmoe_hc_inject(const uint16_t* hyp, const uint16_t* y, const uint16_t* inj, int S, int hc, int H, uint16_t* out,
+                    void* stream);
+
+/* dst row i = src row idx[i] + idx_add for i < n, read on the device: the embedding lookup of a drafted token
+ * (embed([tok]) of engine/mtp.py:274) and the pick of a kept row after a verify round (StepRecord.restore,
+ * kernels/gdn_step_record.py:48-56), or the last token a round emitted. row_bytes a multiple of 4, src and dst 4-byte
+ * aligned (16-byte pieces when row_bytes and both addresses allow). A row index outside [0, n_src) writes a zero row
+ * and raises SSMOE_ERR_TOKEN in the device status. */
+int ssmoe_gather_rows(const void* src, int64_t n_src, int64_t row_bytes, const int32_t* idx, int n, int idx_add,
+                      void* dst, void* stream);
 
 /* ---------------------------------------------------------------- expert slot pool */
 

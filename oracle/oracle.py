@@ -54,6 +54,10 @@ def lib():
         L.or_residual_rmsnorm.restype = None
         L.or_sample.argtypes = [P, i32, P, i32, f32, f32, i32, f32, f32, f32, P, P]
         L.or_sample.restype = None
+        L.or_rmsnorm_groups.argtypes, L.or_rmsnorm_groups.restype = [P, P, f32, i32, i32, i32, P], None
+        L.or_dense_epi.argtypes, L.or_dense_epi.restype = [P, i32, i32, P, i32, i32, i32, P, i32, P], None
+        L.or_hc_mean.argtypes, L.or_hc_mean.restype = [P, P, i32, i32, i32, P], None
+        L.or_hc_inject.argtypes, L.or_hc_inject.restype = [P, P, P, i32, i32, i32, P], None
         _lib = L
     return _lib
 
@@ -241,6 +245,64 @@ def residual_rmsnorm(resid_bits, y_bits=None, w_bits=None, eps=1e-6):
     lib().or_residual_rmsnorm(_p(x), None if y is None else _p(y), None if w is None else _p(w), eps, R, H, _p(so),
                               _p(mx))
     return so, mx
+
+
+# ---------------------------------------------------------------- MTP head, dense part (or_* in ssmoe_oracle.c)
+EPI_NONE, EPI_ADD, EPI_SILU_DIV, EPI_SIGMOID, EPI_INJECT = range(5)
+
+
+def rmsnorm_groups(x_bits, w_bits=None, eps=1e-6, group=None):
+    """bf16 bits [R, n] -> bf16 bits [R, n]: rmsnorm per group of `group` (default n) elements (or_rmsnorm_groups)."""
+    x = _c(x_bits, np.uint16)
+    x2 = x.reshape(-1, x.shape[-1])
+    R, n = x2.shape
+    G = n if group is None else int(group)
+    w = None if w_bits is None else _c(w_bits, np.uint16)
+    out = np.empty_like(x2)
+    lib().or_rmsnorm_groups(_p(x2), _p(w), float(eps), R, n, G, _p(out))
+    return out.reshape(x.shape)
+
+
+def dense_epi(x_bits, w_bits, epi=EPI_NONE, hc=1, add_bits=None, add_div=1):
+    """lin on a bf16 weight with the op after it fused (or_dense_epi): x [R, K], w [N, K] -> bf16 bits [R, N]."""
+    x = _c(x_bits, np.uint16)
+    w = _c(w_bits, np.uint16)
+    R, K = x.shape
+    N = w.shape[0]
+    add = None if add_bits is None else _c(add_bits, np.uint16)
+    out = np.empty((R, N), np.uint16)
+    lib().or_dense_epi(_p(x), R, K, _p(w), N, int(epi), int(hc), _p(add), int(add_div), _p(out))
+    return out
+
+
+def hc_mean(m_bits, hn_bits, hc):
+    """[S, hc H] x2 -> [S, H]: bf16(sum_c bf16(m hn) / hc) (or_hc_mean)."""
+    m = _c(m_bits, np.uint16)
+    hn = _c(hn_bits, np.uint16)
+    S = m.shape[0]
+    H = m.shape[1] // hc
+    out = np.empty((S, H), np.uint16)
+    lib().or_hc_mean(_p(m), _p(hn), S, hc, H, _p(out))
+    return out
+
+
+def hc_inject(hyp_bits, y_bits, inj_bits):
+    """hyp [S, hc H], y [S, H], inj [S, hc] -> bf16(hyp + bf16(y inj)) (or_hc_inject)."""
+    h = _c(hyp_bits, np.uint16)
+    y = _c(y_bits, np.uint16)
+    inj = _c(inj_bits, np.uint16)
+    S, hc = inj.shape
+    H = y.shape[1]
+    out = np.empty_like(h)
+    lib().or_hc_inject(_p(h), _p(y), _p(inj), S, hc, H, _p(out))
+    return out
+
+
+def argmax_bf16(logits) -> np.ndarray:
+    """torch.argmax(bf16 logits .float()) per row (engine/mtp.py:275): the first maximal index, NaN counting as the
+    maximum (np.argmax and torch.argmax agree on both)."""
+    v = bf16_to_f32(f32_to_bf16(np.asarray(logits, np.float32)))
+    return np.argmax(v.reshape(-1, v.shape[-1]), axis=-1).astype(np.int32)
 
 
 # ---------------------------------------------------------------- affine 4-bit (kernels/affine_ref.py:10-30)

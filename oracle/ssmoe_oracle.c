@@ -19,6 +19,7 @@
  */
 #include <math.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 /* ---------------------------------------------------------------- scalars */
@@ -677,4 +678,81 @@ void or_sample(const float* x, int V, const int32_t* gen, int n_gen, float tempe
     return;
   }
   out[0] = u == 0.0f ? hsearch(p, V, 0.0f, 0) : hsearch(p, V, u * total, 1);
+}
+
+/* ---------------------------------------------------------------- MTP head, dense part (no attention)
+ * RMSNorm over groups (model/reference_torch.py:30-38 with `group`): per group of G elements of a row,
+ * r = 1 / sqrt(sum(x^2) / G + eps) with the sum of lane l over the 8-element chunks l, l + 64, ... of the group by
+ * fmaf from 0, then the butterfly; out = bf16((x r) w) (w NULL: 1). */
+void or_rmsnorm_groups(const uint16_t* x, const uint16_t* w, float eps, int R, int n, int G, uint16_t* out) {
+  for (int t = 0; t < R; ++t)
+    for (int g = 0; g < n / G; ++g) {
+      const uint16_t* xr = x + (size_t)t * n + (size_t)g * G;
+      float lanes[64];
+      for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int k8 = l; k8 < G / 8; k8 += 64)
+          for (int e = 0; e < 8; ++e) {
+            const float v = or_bf16_to_f32(xr[8 * k8 + e]);
+            acc = fmaf(v, v, acc);
+          }
+        lanes[l] = acc;
+      }
+      const float r = 1.0f / sqrtf(butterfly_sum(lanes) / (float)G + eps);
+      for (int k = 0; k < G; ++k)
+        out[(size_t)t * n + (size_t)g * G + k] =
+            or_f32_to_bf16((or_bf16_to_f32(xr[k]) * r) * (w ? or_bf16_to_f32(w[(size_t)g * G + k]) : 1.0f));
+    }
+}
+
+static float sigmoid_f(float v) { return 1.0f / (1.0f + or_expf(-v)); }
+
+/* lin on a bf16 weight with the op after it (model/layers.py:62-76, 192-198; engine/mtp.py:189-192): the dot of
+ * or_dense_rows (any K a multiple of 8), v = bf16(dot), then epi 0: v; 1: bf16(add[r / add_div][n] + v);
+ * 2: silu(bf16(v / hc)); 3: sigmoid(v); 4: 2 bf16(sigmoid(bf16(v / hc))), each rounded to bf16. */
+void or_dense_epi(const uint16_t* x, int R, int K, const uint16_t* w, int N, int epi, int hc, const uint16_t* add,
+                  int add_div, uint16_t* out) {
+  uint16_t* dots = (uint16_t*)malloc((size_t)R * N * sizeof(uint16_t));
+  or_dense_rows(x, w, dots, R, K, N);
+  for (int r = 0; r < R; ++r)
+    for (int n = 0; n < N; ++n) {
+      const float v = or_bf16_to_f32(dots[(size_t)r * N + n]);
+      float o = v;
+      if (epi == 1) {
+        o = or_bf16_to_f32(add[(size_t)(r / add_div) * N + n]) + v;
+      } else if (epi == 2) {
+        const float u = round_bf16(v / (float)hc);
+        o = u / (1.0f + or_expf(-u));
+      } else if (epi == 3) {
+        o = sigmoid_f(v);
+      } else if (epi == 4) {
+        o = 2.0f * round_bf16(sigmoid_f(round_bf16(v / (float)hc)));
+      }
+      out[(size_t)r * N + n] = or_f32_to_bf16(o);
+    }
+  free(dots);
+}
+
+/* hc_mix's mean (model/layers.py:195): mixed[s][j] = bf16(sum_{c = 0..hc-1} bf16(m hn) / hc), sum in order. */
+void or_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed) {
+  for (int s = 0; s < S; ++s)
+    for (int j = 0; j < H; ++j) {
+      float acc = 0.0f;
+      for (int c = 0; c < hc; ++c) {
+        const size_t i = (size_t)s * hc * H + (size_t)c * H + j;
+        acc += round_bf16(or_bf16_to_f32(m[i]) * or_bf16_to_f32(hn[i]));
+      }
+      mixed[(size_t)s * H + j] = or_f32_to_bf16(acc / (float)hc);
+    }
+}
+
+/* HC residual (engine/mtp.py:226): out = bf16(hyp + bf16(y[s][j] inj[s][c])) (out may be hyp). */
+void or_hc_inject(const uint16_t* hyp, const uint16_t* y, const uint16_t* inj, int S, int hc, int H, uint16_t* out) {
+  for (int s = 0; s < S; ++s)
+    for (int c = 0; c < hc; ++c)
+      for (int j = 0; j < H; ++j) {
+        const size_t i = (size_t)s * hc * H + (size_t)c * H + j;
+        const float t = round_bf16(or_bf16_to_f32(y[(size_t)s * H + j]) * or_bf16_to_f32(inj[(size_t)s * hc + c]));
+        out[i] = or_f32_to_bf16(or_bf16_to_f32(hyp[i]) + t);
+      }
 }

@@ -32,6 +32,7 @@ struct GemvArgs {
   float* y;         // [R][N] or null
   uint64_t* rkey;   // [R] argmax keys, combined with atomic max (zeroed before the launch), or null
   int* rbad;        // [R] non-finite flags, combined with atomic or (with rkey)
+  int key_bf16;     // 1 (with rkey): the logits are lin's bf16 result: keys and y take the dot rounded to bf16
 };
 
 SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -226,7 +227,10 @@ __global__ __launch_bounds__(256, 2) void gemv_affine4_kernel(GemvArgs a) {
       }
     }
 #pragma unroll
-    for (int r = 0; r < kGR; ++r) acc[r] = ss_rows_sum(acc[r]);
+    for (int r = 0; r < kGR; ++r) {
+      acc[r] = ss_rows_sum(acc[r]);
+      if (a.key_bf16) acc[r] = ss_round_bf16(acc[r]);
+    }
     if (a.y && g == 0 && row < N) {
 #pragma unroll
       for (int r = 0; r < kGR; ++r)
@@ -305,6 +309,12 @@ __global__ void gemv_greedy_decide_kernel(const uint64_t* rkey, const int* rbad,
   out[3] = fl;
 }
 
+// ids[r] = the index the argmax key of row r names.
+__global__ void gemv_argmax_ids_kernel(const uint64_t* rkey, int R, int32_t* ids) {
+  const int t = threadIdx.x;
+  if (t < R) ids[t] = (int32_t)(0xFFFFFFFFu - (uint32_t)rkey[t]);
+}
+
 namespace {
 
 // One resident wave of work per SIMD slot: the grid is the occupancy of this instantiation times the CU count.
@@ -380,6 +390,7 @@ hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const i
   a.q = reinterpret_cast<const uint32_t*>(q);
   a.s = s;
   a.b = b;
+  a.key_bf16 = x_f32 ? 0 : 1;  // lin returns the dtype of x
   const size_t xrow = (size_t)K * (x_f32 ? 4 : 2);
   for (int r0 = 0; r0 < R; r0 += kGR) {
     a.x = static_cast<const uint8_t*>(x) + (size_t)r0 * xrow;
@@ -391,6 +402,35 @@ hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const i
     if (e != hipSuccess) return e;
   }
   hipLaunchKernelGGL(gemv_greedy_decide_kernel, dim3(1), dim3(64), 0, st, rkey, rbad, drafts, D, N, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_lm_head_argmax(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s,
+                                 const uint16_t* b, int N, int round_bf16, void* work, float* logits, int32_t* ids,
+                                 hipStream_t st) {
+  uint8_t* w = static_cast<uint8_t*>(work);
+  uint64_t* rkey = reinterpret_cast<uint64_t*>(w);
+  int* rbad = reinterpret_cast<int*>(w + ((int64_t)R * 8 + 255) / 256 * 256);
+  hipLaunchKernelGGL(gemv_key_init_kernel, dim3(1), dim3(64), 0, st, rkey, rbad, R);
+  GemvArgs a{};
+  a.K = K;
+  a.N = N;
+  a.ntiles = (int)gemv_tiles(N);
+  a.q = reinterpret_cast<const uint32_t*>(q);
+  a.s = s;
+  a.b = b;
+  a.key_bf16 = round_bf16 ? 1 : 0;
+  const size_t xrow = (size_t)K * (x_f32 ? 4 : 2);
+  for (int r0 = 0; r0 < R; r0 += kGR) {
+    a.x = static_cast<const uint8_t*>(x) + (size_t)r0 * xrow;
+    a.R = R - r0 < kGR ? R - r0 : kGR;
+    a.y = logits ? logits + (size_t)r0 * N : nullptr;
+    a.rkey = rkey + r0;
+    a.rbad = rbad + r0;
+    hipError_t e = launch_chunk(a, x_f32, st);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL(gemv_argmax_ids_kernel, dim3(1), dim3(64), 0, st, rkey, R, ids);
   return hipGetLastError();
 }
 

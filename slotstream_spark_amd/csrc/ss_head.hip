@@ -1,0 +1,244 @@
+// Dense operations of the MTP draft head without its attention (engine/mtp.py:194-227, model/layers.py:190-198):
+// RMSNorm over groups, bf16 GEMV with the elementwise op that follows each `lin` of the head fused into its store,
+// the hyper-connection mean and residual, and a row gather by device index (the embedding lookup of a drafted token,
+// the kept row of a verify round). Every op is row-independent and has one fixed reduction order, so an S-row call
+// equals S one-row calls bit for bit, and the CPU restatement reproduces it exactly.
+#include <hip/hip_runtime.h>
+
+#include "ss_common.hpp"
+#include "ss_launch.hpp"
+
+namespace ss {
+
+namespace {
+
+SS_DEV float lo16(uint32_t v) { return ss_bf16_to_f32(v & 0xFFFFu); }
+SS_DEV float hi16(uint32_t v) { return ss_bf16_to_f32(v >> 16); }
+
+// One wave per (row, group): lane l sums x^2 over the 8-element chunks l, l + 64, ... of the group with fmaf from 0,
+// then the xor butterfly; r = 1 / sqrt(sum / G + eps); out = bf16((x * r) * w).
+__global__ __launch_bounds__(256) void rmsnorm_groups_kernel(const uint16_t* __restrict__ x,
+                                                             const uint16_t* __restrict__ w, float eps, int64_t nseg,
+                                                             int n, int G, uint16_t* __restrict__ out) {
+  const int lane = threadIdx.x & 63;
+  const int64_t seg = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (seg >= nseg) return;  // whole waves; no workgroup barrier follows
+  const int per_row = n / G;
+  const int64_t row = seg / per_row;
+  const int g = (int)(seg - row * per_row);
+  const int64_t base = row * n + (int64_t)g * G;
+  const uint4* xs = reinterpret_cast<const uint4*>(x + base);
+  const uint4* ws = w ? reinterpret_cast<const uint4*>(w + (int64_t)g * G) : nullptr;
+  uint4* os = reinterpret_cast<uint4*>(out + base);
+  const int g8 = G >> 3;
+  float acc = 0.f;
+  for (int k8 = lane; k8 < g8; k8 += 64) {
+    const uint4 a = xs[k8];
+    const uint32_t v[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const float e0 = lo16(v[c]), e1 = hi16(v[c]);
+      acc = fmaf(e0, e0, acc);
+      acc = fmaf(e1, e1, acc);
+    }
+  }
+  const float r = 1.f / sqrtf(ss_wave_sum(acc) / (float)G + eps);
+  for (int k8 = lane; k8 < g8; k8 += 64) {
+    const uint4 a = xs[k8];
+    const uint32_t v[4] = {a.x, a.y, a.z, a.w};
+    uint32_t wv[4] = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
+    if (ws) {
+      const uint4 b = ws[k8];
+      wv[0] = b.x, wv[1] = b.y, wv[2] = b.z, wv[3] = b.w;
+    }
+    uint32_t o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      o[c] = ss_f32_to_bf16((lo16(v[c]) * r) * lo16(wv[c])) | (ss_f32_to_bf16((hi16(v[c]) * r) * hi16(wv[c])) << 16);
+    os[k8] = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
+constexpr int kDR = 4;  // x rows per GEMV launch
+
+struct DenseEpiArgs {
+  const uint16_t* x;    // [R][K] (this launch's rows)
+  const uint16_t* w;    // [N][K]
+  uint16_t* out;        // [R][N]
+  const uint16_t* add;  // SSMOE_EPI_ADD: bf16 rows added after the rounding, row (row0 + r) / add_div
+  int R, K, N, epi, row0, add_div;
+  float hc;
+};
+
+SS_DEV float sigmoid_f(float v) { return 1.0f / (1.0f + ss_expf(-v)); }
+
+// The op after the GEMV, on the fp32 dot d, with torch's bf16 rounding after every step (the head's tensors are bf16).
+SS_DEV uint32_t epilogue(float d, const DenseEpiArgs& a, int r, int n) {
+  const float v = ss_round_bf16(d);
+  switch (a.epi) {
+    case SSMOE_EPI_ADD: {
+      const float e = ss_bf16_to_f32(a.add[(size_t)((a.row0 + r) / a.add_div) * a.N + n]);
+      return ss_f32_to_bf16(e + v);
+    }
+    case SSMOE_EPI_SILU_DIV: {
+      const float u = ss_round_bf16(v / a.hc);
+      return ss_f32_to_bf16(u / (1.0f + ss_expf(-u)));
+    }
+    case SSMOE_EPI_SIGMOID:
+      return ss_f32_to_bf16(sigmoid_f(v));
+    case SSMOE_EPI_INJECT:
+      return ss_f32_to_bf16(2.0f * ss_round_bf16(sigmoid_f(ss_round_bf16(v / a.hc))));
+    default:
+      return ss_f32_to_bf16(v);
+  }
+}
+
+// One wave per weight row n, up to 4 x rows: lane l accumulates the 8-element chunks l, l + 64, ... of row n against
+// each x row with fmaf from 0, then the xor butterfly (the order of the dense router rows). Lane r stores x row r.
+__global__ __launch_bounds__(256) void dense_epi_kernel(DenseEpiArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (n >= a.N) return;  // whole waves; no workgroup barrier follows
+  const int k8n = a.K >> 3;
+  const uint4* wr = reinterpret_cast<const uint4*>(a.w + (size_t)n * a.K);
+  float acc[kDR] = {0.f, 0.f, 0.f, 0.f};
+  for (int k8 = lane; k8 < k8n; k8 += 64) {
+    const uint4 wq = wr[k8];
+    const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+    for (int r = 0; r < kDR; ++r) {
+      if (r < a.R) {
+        const uint4 xq = reinterpret_cast<const uint4*>(a.x + (size_t)r * a.K)[k8];
+        const uint32_t xv[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc[r] = fmaf(lo16(xv[c]), lo16(wv[c]), acc[r]);
+          acc[r] = fmaf(hi16(xv[c]), hi16(wv[c]), acc[r]);
+        }
+      }
+    }
+  }
+  float mine = 0.f;
+#pragma unroll
+  for (int r = 0; r < kDR; ++r) {
+    const float s = ss_wave_sum(acc[r]);
+    mine = lane == r ? s : mine;
+  }
+  if (lane < a.R) a.out[(size_t)lane * a.N + n] = (uint16_t)epilogue(mine, a, lane, n);
+}
+
+// mixed[s][j] = bf16((sum over c = 0 .. hc-1 of bf16(m[s][c H + j] * hn[s][c H + j])) / hc), the sum sequential.
+__global__ __launch_bounds__(256) void hc_mean_kernel(const uint16_t* __restrict__ m, const uint16_t* __restrict__ hn,
+                                                      int S, int hc, int H, uint16_t* __restrict__ mixed) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)S * H) return;
+  const int64_t s = i / H;
+  const int j = (int)(i - s * H);
+  const size_t b = (size_t)s * hc * H + j;
+  float acc = 0.f;
+  for (int c = 0; c < hc; ++c)
+    acc += ss_round_bf16(ss_bf16_to_f32(m[b + (size_t)c * H]) * ss_bf16_to_f32(hn[b + (size_t)c * H]));
+  mixed[i] = (uint16_t)ss_f32_to_bf16(acc / (float)hc);
+}
+
+// out[s][c H + j] = bf16(hyp[s][c H + j] + bf16(y[s][j] * inj[s][c])); out may be hyp (each thread reads its element
+// before writing it).
+__global__ __launch_bounds__(256) void hc_inject_kernel(const uint16_t* hyp, const uint16_t* __restrict__ y,
+                                                        const uint16_t* __restrict__ inj, int S, int hc, int H,
+                                                        uint16_t* out) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int64_t row = (int64_t)hc * H;
+  if (i >= (int64_t)S * row) return;
+  const int64_t s = i / row;
+  const int c = (int)((i - s * row) / H);
+  const int j = (int)(i - s * row - (int64_t)c * H);
+  const float t = ss_round_bf16(ss_bf16_to_f32(y[s * H + j]) * ss_bf16_to_f32(inj[s * hc + c]));
+  out[i] = (uint16_t)ss_f32_to_bf16(ss_bf16_to_f32(hyp[i]) + t);
+}
+
+// dst row i = src row (idx[i] + idx_add) in pieces of U (uint4, or uint32 for rows of 4-byte multiples); an index
+// outside [0, n_src) writes zeros and raises SS_ERR_TOKEN.
+template <typename U>
+__global__ __launch_bounds__(256) void gather_rows_kernel(const U* __restrict__ src, int64_t n_src, int64_t row_u,
+                                                          const int32_t* __restrict__ idx, int n, int idx_add,
+                                                          U* __restrict__ dst, int* err) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)n * row_u) return;
+  const int64_t r = i / row_u;
+  const int64_t c = i - r * row_u;
+  const int64_t k = (int64_t)idx[r] + idx_add;
+  U v{};
+  if (k >= 0 && k < n_src)
+    v = src[k * row_u + c];
+  else if (c == 0)
+    ss_raise(err, SS_ERR_TOKEN);
+  dst[i] = v;
+}
+
+}  // namespace
+
+hipError_t launch_rmsnorm_groups(const uint16_t* x, const uint16_t* w, float eps, int R, int n, int G, uint16_t* out,
+                                 hipStream_t st) {
+  const int64_t nseg = (int64_t)R * (n / G);
+  if (nseg == 0) return hipSuccess;
+  hipLaunchKernelGGL(rmsnorm_groups_kernel, dim3((unsigned)((nseg + 3) / 4)), dim3(256), 0, st, x, w, eps, nseg, n, G,
+                     out);
+  return hipGetLastError();
+}
+
+hipError_t launch_dense_epi(const uint16_t* x, int R, int K, const uint16_t* w, int N, int epi, int hc,
+                            const uint16_t* add, int add_div, uint16_t* out, hipStream_t st) {
+  DenseEpiArgs a{};
+  a.w = w;
+  a.K = K;
+  a.N = N;
+  a.epi = epi;
+  a.hc = (float)hc;
+  a.add = add;
+  a.add_div = add_div > 0 ? add_div : 1;
+  for (int r0 = 0; r0 < R; r0 += kDR) {
+    a.x = x + (size_t)r0 * K;
+    a.out = out + (size_t)r0 * N;
+    a.R = R - r0 < kDR ? R - r0 : kDR;
+    a.row0 = r0;
+    hipLaunchKernelGGL(dense_epi_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed,
+                          hipStream_t st) {
+  const int64_t n = (int64_t)S * H;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(hc_mean_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, m, hn, S, hc, H, mixed);
+  return hipGetLastError();
+}
+
+hipError_t launch_hc_inject(const uint16_t* hyp, const uint16_t* y, const uint16_t* inj, int S, int hc, int H,
+                            uint16_t* out, hipStream_t st) {
+  const int64_t n = (int64_t)S * hc * H;
+  if (n == 0) return hipSuccess;
+  hipLaunchKernelGGL(hc_inject_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, hyp, y, inj, S, hc, H, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gather_rows(const void* src, int64_t n_src, int64_t row_bytes, const int32_t* idx, int n,
+                              int idx_add, void* dst, int* err, hipStream_t st) {
+  const bool wide = row_bytes % 16 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(dst) % 16 == 0;
+  const int64_t row_u = row_bytes / (wide ? 16 : 4);
+  const int64_t total = (int64_t)n * row_u;
+  if (total == 0) return hipSuccess;
+  const dim3 grid((unsigned)((total + 255) / 256));
+  if (wide)
+    hipLaunchKernelGGL(gather_rows_kernel<uint4>, grid, dim3(256), 0, st, static_cast<const uint4*>(src), n_src, row_u,
+                       idx, n, idx_add, static_cast<uint4*>(dst), err);
+  else
+    hipLaunchKernelGGL(gather_rows_kernel<uint32_t>, grid, dim3(256), 0, st, static_cast<const uint32_t*>(src), n_src,
+                       row_u, idx, n, idx_add, static_cast<uint32_t*>(dst), err);
+  return hipGetLastError();
+}
+
+}  // namespace ss

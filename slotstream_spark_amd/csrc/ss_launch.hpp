@@ -196,6 +196,23 @@ int64_t lm_head_greedy_workspace_bytes(int D, int N);
 hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
                                  const uint16_t* b, int N, const int32_t* drafts, void* work, float* logits,
                                  int32_t* out, hipStream_t st);
+// Argmax ids of R rows (R <= 64; workspace lm_head_greedy_workspace_bytes(R - 1, N)).
+hipError_t launch_lm_head_argmax(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s,
+                                 const uint16_t* b, int N, int round_bf16, void* work, float* logits, int32_t* ids,
+                                 hipStream_t st);
+
+// MTP head dense ops (ss_head.hip), as ssmoe_rmsnorm / ssmoe_dense_gemv_epi / ssmoe_hc_mean / ssmoe_hc_inject /
+// ssmoe_gather_rows.
+hipError_t launch_rmsnorm_groups(const uint16_t* x, const uint16_t* w, float eps, int R, int n, int G, uint16_t* out,
+                                 hipStream_t st);
+hipError_t launch_dense_epi(const uint16_t* x, int R, int K, const uint16_t* w, int N, int epi, int hc,
+                            const uint16_t* add, int add_div, uint16_t* out, hipStream_t st);
+hipError_t launch_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed,
+                          hipStream_t st);
+hipError_t launch_hc_inject(const uint16_t* hyp, const uint16_t* y, const uint16_t* inj, int S, int hc, int H,
+                            uint16_t* out, hipStream_t st);
+hipError_t launch_gather_rows(const void* src, int64_t n_src, int64_t row_bytes, const int32_t* idx, int n,
+                              int idx_add, void* dst, int* err, hipStream_t st);
 
 // Acceptance.
 struct AcceptArgs {

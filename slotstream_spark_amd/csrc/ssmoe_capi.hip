@@ -812,6 +812,78 @@ int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* 
                    "lm_head greedy launch");
 }
 
+int64_t ssmoe_lm_head_argmax_workspace_bytes(int R, int N) {
+  if (R < 1 || R > 64 || N < 1) return -1;
+  return ss::lm_head_greedy_workspace_bytes(R - 1, N);
+}
+
+int ssmoe_lm_head_argmax(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s,
+                         const uint16_t* b, int N, int round_bf16, void* workspace, int64_t workspace_bytes,
+                         float* logits, int32_t* ids, void* stream) {
+  if (R < 1 || R > 64) return fail(SSMOE_EINVAL, "R must be in [1, 64], got %d", R);
+  if (int rc = check_gemv(x, K, q, s, b, N)) return rc;
+  if (!ids) return fail(SSMOE_EINVAL, "ids must be non-null");
+  if (!workspace || !aligned(workspace, 256)) return fail(SSMOE_EINVAL, "workspace must be non-null and 256-byte aligned");
+  if (workspace_bytes < ss::lm_head_greedy_workspace_bytes(R - 1, N))
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)ss::lm_head_greedy_workspace_bytes(R - 1, N));
+  return hip_check(ss::launch_lm_head_argmax(x, x_f32 ? 1 : 0, R, K, q, s, b, N, round_bf16, workspace, logits, ids,
+                                             static_cast<hipStream_t>(stream)),
+                   "lm_head argmax launch");
+}
+
+int ssmoe_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int R, int n, int group, uint16_t* out,
+                  void* stream) {
+  if (R < 0 || n < 8 || group < 8 || group % 8 || n % group)
+    return fail(SSMOE_EINVAL, "need R >= 0 and group a multiple of 8 dividing n (R %d, n %d, group %d)", R, n, group);
+  if (!x || !out) return fail(SSMOE_EINVAL, "x and out must be non-null");
+  if (!aligned(x, 16) || !aligned(out, 16) || (w && !aligned(w, 16)))
+    return fail(SSMOE_EINVAL, "x, w and out must be 16-byte aligned");
+  if (x == out) return fail(SSMOE_EINVAL, "out must not alias x");
+  if (!(eps >= 0.f)) return fail(SSMOE_EINVAL, "eps must be >= 0");
+  return hip_check(ss::launch_rmsnorm_groups(x, w, eps, R, n, group, out, static_cast<hipStream_t>(stream)),
+                   "rmsnorm launch");
+}
+
+int ssmoe_dense_gemv_epi(const uint16_t* x, int R, int K, const uint16_t* w, int N, int epi, int hc,
+                         const uint16_t* add, int add_div, uint16_t* out, void* stream) {
+  if (R < 0 || K < 8 || K % 8 || N < 1) return fail(SSMOE_EINVAL, "need R >= 0, K a multiple of 8, N >= 1");
+  if (epi < SSMOE_EPI_NONE || epi > SSMOE_EPI_INJECT) return fail(SSMOE_EINVAL, "unknown epilogue %d", epi);
+  if ((epi == SSMOE_EPI_SILU_DIV || epi == SSMOE_EPI_INJECT) && hc < 1) return fail(SSMOE_EINVAL, "hc must be >= 1");
+  if (epi == SSMOE_EPI_ADD && (!add || add_div < 1)) return fail(SSMOE_EINVAL, "EPI_ADD needs add and add_div >= 1");
+  if (!x || !w || !out) return fail(SSMOE_EINVAL, "x, w and out must be non-null");
+  if (!aligned(x, 16) || !aligned(w, 16)) return fail(SSMOE_EINVAL, "x and w must be 16-byte aligned");
+  return hip_check(ss::launch_dense_epi(x, R, K, w, N, epi, hc, add, add_div, out, static_cast<hipStream_t>(stream)),
+                   "dense gemv launch");
+}
+
+int ssmoe_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed, void* stream) {
+  if (S < 0 || hc < 1 || H < 1) return fail(SSMOE_EINVAL, "need S >= 0, hc >= 1, H >= 1");
+  if (!m || !hn || !mixed) return fail(SSMOE_EINVAL, "m, hn and mixed must be non-null");
+  return hip_check(ss::launch_hc_mean(m, hn, S, hc, H, mixed, static_cast<hipStream_t>(stream)), "hc_mean launch");
+}
+
+int ssmoe_hc_inject(const uint16_t* hyp, const uint16_t* y, const uint16_t* inj, int S, int hc, int H, uint16_t* out,
+                    void* stream) {
+  if (S < 0 || hc < 1 || H < 1) return fail(SSMOE_EINVAL, "need S >= 0, hc >= 1, H >= 1");
+  if (!hyp || !y || !inj || !out) return fail(SSMOE_EINVAL, "hyp, y, inj and out must be non-null");
+  return hip_check(ss::launch_hc_inject(hyp, y, inj, S, hc, H, out, static_cast<hipStream_t>(stream)),
+                   "hc_inject launch");
+}
+
+int ssmoe_gather_rows(const void* src, int64_t n_src, int64_t row_bytes, const int32_t* idx, int n, int idx_add,
+                      void* dst, void* stream) {
+  if (n < 0 || n_src < 1 || row_bytes < 4 || row_bytes % 4)
+    return fail(SSMOE_EINVAL, "need n >= 0, n_src >= 1 and row_bytes a positive multiple of 4");
+  if (!src || !idx || !dst) return fail(SSMOE_EINVAL, "src, idx and dst must be non-null");
+  if (!aligned(src, 4) || !aligned(dst, 4)) return fail(SSMOE_EINVAL, "src and dst must be 4-byte aligned");
+  int* st = nullptr;
+  if (int rc = status_ptr(&st)) return rc;
+  return hip_check(ss::launch_gather_rows(src, n_src, row_bytes, idx, n, idx_add, dst, st,
+                                          static_cast<hipStream_t>(stream)),
+                   "gather launch");
+}
+
 int ssmoe_pool_open(const char* experts_path, int layers, int experts, int64_t record_bytes, int max_slots,
                     int64_t chunk_bytes, int32_t* map, int64_t* slot_ptr, void** pool) {
   if (!experts_path || !map || !slot_ptr || !pool) return fail(SSMOE_EINVAL, "path, map, slot_ptr and pool must be non-null");

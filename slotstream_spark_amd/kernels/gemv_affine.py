@@ -109,3 +109,35 @@ class LMHeadGreedy:
 
     def __call__(self, x, drafts, logits=None) -> AcceptResult:
         return AcceptResult.from_out(self.run_async(x, drafts, logits).cpu())
+
+
+class LMHeadArgmax:
+    """torch.argmax of the lm_head logits per row, the draft token of MTPHead.draft (engine/mtp.py:275): with
+    `round_bf16` the argmax ranks the logits rounded to bf16, as lin returns them for a bf16 x; ties to the first
+    index, NaN as the maximum. The ids stay on the device. Workspace owned here, for up to `max_rows` rows."""
+
+    def __init__(self, w: AffineWeight, max_rows: int = 1, round_bf16: bool = True, device="cuda"):
+        _device_weight(w)
+        self.w, self.max_rows, self.round_bf16 = w, max_rows, round_bf16
+        nb = int(_lib.lib().ssmoe_lm_head_argmax_workspace_bytes(max_rows, w.n))
+        if nb < 0:
+            raise ValueError(f"max_rows must be in [1, 64], got {max_rows}")
+        self.work = torch.empty(nb, dtype=torch.uint8, device=device)
+
+    def __call__(self, x: torch.Tensor, ids: torch.Tensor | None = None,
+                 logits: torch.Tensor | None = None) -> torch.Tensor:
+        _check_x(x, self.w)
+        r = x.shape[0]
+        if not 1 <= r <= self.max_rows:
+            raise ValueError(f"x must hold 1..{self.max_rows} rows, got {r}")
+        ids = torch.empty(r, dtype=torch.int32, device=x.device) if ids is None else ids
+        if ids.dtype != torch.int32 or ids.numel() != r or not ids.is_contiguous():
+            raise ValueError(f"ids must be contiguous int32 [{r}]")
+        if logits is not None and (tuple(logits.shape) != (r, self.w.n) or logits.dtype != torch.float32
+                                   or not logits.is_contiguous()):
+            raise ValueError(f"logits must be contiguous fp32 {(r, self.w.n)}")
+        _lib.check(_lib.lib().ssmoe_lm_head_argmax(
+            x.data_ptr(), 1 if x.dtype == torch.float32 else 0, r, self.w.k, self.w.q.data_ptr(), self.w.s.data_ptr(),
+            self.w.b.data_ptr(), self.w.n, 1 if self.round_bf16 else 0, self.work.data_ptr(), self.work.numel(),
+            _lib.ptr(logits), ids.data_ptr(), _lib.stream_of(x)))
+        return ids

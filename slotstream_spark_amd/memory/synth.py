@@ -53,3 +53,26 @@ def verify_logits(depth: int, vocab: int, seed: int, rho: float = 0.8, std: floa
     z = torch.randn((depth + 1, vocab), generator=g, device=device) * std
     n = torch.randn((depth, vocab), generator=g, device=device) * std
     return z, rho * z[:depth] + math.sqrt(1.0 - rho * rho) * n
+
+
+def head_weights(hidden: int, hc: int, lowrank: int, vocab: int, seed: int, device="cuda"):
+    """Random-init dense weights of the MTP head (engine.mtp.HeadWeights): embedding table N(0, 1) [vocab, H]; norm
+    weights 1 + N(0, 0.1); every projection N(0, 1 / fan_in), so activations keep unit scale through the step."""
+    from ..engine.mtp import HeadWeights, HyperConnection
+
+    n = hc * hidden
+    k = iter(range(seed * 32, seed * 32 + 32))
+
+    def norm_w(size):
+        return (normal_bf16((size,), 0.1, next(k), device).float() + 1).to(torch.bfloat16)
+
+    def proj(rows, cols):
+        return normal_bf16((rows, cols), cols ** -0.5, next(k), device)
+
+    def hcw(inject):
+        return HyperConnection(norm_w(n), proj(lowrank, n), proj(n, lowrank), proj(hc, n) if inject else None)
+
+    return HeadWeights(embed=normal_bf16((vocab, hidden), 1.0, next(k), device),
+                       pre_fc_norm_embedding=norm_w(hidden), fc_embedding=proj(hidden, hidden),
+                       pre_fc_norm_hidden=norm_w(n), fc_hidden=proj(hidden, hidden), mlp_hc=hcw(True),
+                       mixer_hc=hcw(False))

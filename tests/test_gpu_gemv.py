@@ -72,7 +72,7 @@ def test_lm_head_greedy_bitwise(n, depth, accept):
     k = 2560
     w = make_weight(n, k, 11 + n)
     x = torch.randn((depth + 1, k), generator=torch.Generator().manual_seed(n)).to(torch.bfloat16).cuda()
-    logits = gemv(x, w)
+    logits = gemv(x, w).to(torch.bfloat16).float()  # lin's result for a bf16 x
     am = logits.argmax(dim=1).to(torch.int32).cpu()
     drafts = torch.tensor([int(am[i]) if i < accept else (int(am[i]) + 1) % n for i in range(depth)], dtype=torch.int32)
     head = LMHeadGreedy(w, depth)
@@ -92,7 +92,7 @@ def test_lm_head_greedy_nonfinite_row():
     w = make_weight(n, k, 9)
     x = torch.randn((depth + 1, k), generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).cuda()
     x[2, 100] = float("nan")
-    logits = gemv(x, w)
+    logits = gemv(x, w).to(torch.bfloat16).float()
     drafts = logits.argmax(dim=1).to(torch.int32)[:depth].contiguous()
     res = LMHeadGreedy(w, depth)(x, drafts)
     want = O.accept_greedy(logits.cpu().numpy(), drafts.cpu().numpy())

@@ -9,7 +9,7 @@ import torch
 
 from oracle import oracle as O
 from slotstream_spark_amd.engine.step import MoEWeights, MTPStepGraph, residual_rmsnorm
-from slotstream_spark_amd.kernels.gemv_affine import AffineWeight
+from slotstream_spark_amd.kernels.gemv_affine import AffineWeight, gemv
 from slotstream_spark_amd.memory.synth import LayerWeights, normal_bf16, zipf_bias
 from tests.gpu_util import DenseCache, bits, make_pool
 
@@ -148,9 +148,12 @@ def test_round_acceptance_and_logits(step):
         torch.cuda.synchronize()
         assert np.array_equal(out.cpu().numpy(), O.accept_greedy(logits, np.array(drafts, np.int32))), drafts
         assert torch.equal(sg.logits.cpu(), torch.from_numpy(logits))
+    # The round ranks lin's result: the fp32 GEMV of the final norm rounded to bf16.
+    raw = gemv(sg.mixed[NL], lm)
+    assert torch.equal(sg.logits, raw.to(torch.bfloat16).float())
     xm = O.bf16_to_f32(bits(sg.mixed[NL]))
     y64, bound = O.gemv_affine4_fp64(xm, lm.q.cpu().numpy(), bits(lm.s), bits(lm.b))
-    assert np.max(np.abs(logits - y64) / bound) <= 2e-5
+    assert np.max(np.abs(raw.cpu().numpy() - y64) / bound) <= 2e-5
     res = sg.result()
     assert res.n_accept == 0 and res.n_emit == 1
 
