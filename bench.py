@@ -442,6 +442,86 @@ def step_leg(pool, weights, biases, steps, dev):
     return res
 
 
+def _lm_head_weight(dev, n=248320, seed=2721):
+    import torch
+
+    from slotstream_spark_amd.kernels.gemv_affine import AffineWeight
+
+    g = torch.Generator(device=dev).manual_seed(seed)
+    q = torch.randint(-2**31, 2**31 - 1, (n, H // 8), generator=g, device=dev, dtype=torch.int32)
+    sc = (torch.randn((n, H // 64), generator=g, device=dev) * 0.02).abs().to(torch.bfloat16)
+    return AffineWeight(q, sc, (-8 * sc.float()).to(torch.bfloat16), 4, 64, n, H)
+
+
+def draft_leg(pool, weights, biases, steps, dev):
+    """§8(a) row 13 / §8(f) row 4: the MTP head's draft chain (engine/mtp.py, attention excluded) at the config-1
+    shape: hc 4 hyper-connection branches of H 2048 with a 320-wide low rank, the head MoE on map layer 48 (E512
+    top-10, shared 512), the 248,320 x 2048 affine 4-bit lm_head argmax; depth 2 (the reference's DEPTH) and 3, one
+    HIP graph per chain, timed with HIP events around `steps` replays. Then the greedy speculative loop
+    (engine/generate.py mtp_decode) over a 48-layer MoE stack with that head (hc 1 on the stack's one stream): wall
+    time per emitted token with the host's per-round reads included."""
+    import time
+
+    import torch
+
+    from slotstream_spark_amd.engine.generate import MoEStack, mtp_decode
+    from slotstream_spark_amd.engine.mtp import DraftGraph, MTPHead
+    from slotstream_spark_amd.engine.step import MoEWeights
+    from slotstream_spark_amd.engine.verify import MoEVerifyLayer
+    from slotstream_spark_amd.memory.synth import head_weights, normal_bf16
+
+    NL = 48
+    lm = _lm_head_weight(dev)
+    hw_ = weights[NL]
+    moe = MoEVerifyLayer(pool, NL, hw_.router_w, hw_.sh_gate, hw_.sh_up, hw_.sh_down, hw_.sh_g, top_k=K,
+                         router_bias=biases[NL], max_tokens=4)
+    head = MTPHead(head_weights(H, 4, 320, lm.n, seed=2730, device=dev), moe, lm, hc=4)
+    res = {"hc": 4, "lowrank": 320, "head_layer": NL, "lm_head": f"{lm.n} x {H} affine 4-bit gs64"}
+    for k in (2, 3):
+        dg = DraftGraph(head, k)
+        dg.token.fill_(12345)
+        dg.multi.copy_(normal_bf16((1, 4 * H), 1.0, 2731, dev))
+        dg.capture()
+        for _ in range(3):
+            dg.graph.replay()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        for _ in range(steps):
+            dg.graph.replay()
+        ev1.record()
+        torch.cuda.synchronize()
+        us = ev0.elapsed_time(ev1) * 1000.0 / steps
+        res[f"depth{k}"] = {"us_per_chain": round(us, 1), "us_per_draft": round(us / k, 1),
+                            "drafts": dg.out.cpu().tolist()}
+        log(f"draft chain depth {k}: {us:.1f} us ({us / k:.1f} us per drafted token)")
+        del dg
+    del head, moe
+    # the speculative loop over the 48-layer stack
+    mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, b) for w, b in zip(weights[:NL], biases[:NL])]
+    emb = head_weights(H, 1, 320, lm.n, seed=2732, device=dev)
+    stack = MoEStack(pool, mw, lm, emb.embed, depth=2, top_k=K, device=dev)
+    moe1 = MoEVerifyLayer(pool, NL, hw_.router_w, hw_.sh_gate, hw_.sh_up, hw_.sh_down, hw_.sh_g, top_k=K,
+                          router_bias=biases[NL], max_tokens=4)
+    head1 = MTPHead(emb, moe1, lm, hc=1)
+    mtp_decode(stack, head1, [11, 12, 13], 8)  # captures the round graph, warms up
+    stack.reset()
+    head1.reset()
+    n_tok = 64
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    out, secs, st = mtp_decode(stack, head1, [21, 22, 23], n_tok)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    res["loop"] = {"layers": NL, "depth": 2, "tokens": len(out), "rounds": st["rounds"], "accepted": st["accepted"],
+                   "drafted": st["drafted"], "ms_per_round": round(1000 * sum(secs) / max(len(secs), 1), 3),
+                   "tokens_per_s": round(len(out) / wall, 1),
+                   "note": "random-init head and stack: drafts rarely match, so about one token per round"}
+    log(f"speculative loop: {len(out)} tokens in {wall * 1000:.1f} ms, {st['rounds']} rounds, "
+        f"{st['accepted']}/{st['drafted']} drafts accepted, {1000 * sum(secs) / max(len(secs), 1):.2f} ms per round")
+    return res
+
+
 def pool_leg(dev, calls=4):
     """The slot pool loading records from experts.bin (ExpertPool / ssmoe_pool_*): 256 records of the reference's
     2,764,800-byte layout (hidden 2560, moe_intermediate 640) in a 2 x 128 file, a 128-slot pool, and ensures of a
@@ -708,9 +788,10 @@ def main():
     ap.add_argument("--tokens", type=int, default=2)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--legs", default="isolated,decode,prefill,config2,config4,lm_head,step,pool,ref_decode,peaks",
+    ap.add_argument("--legs", default="isolated,decode,prefill,config2,config4,lm_head,step,draft,pool,ref_decode,"
+                                      "peaks",
                     help="comma list of legs besides the headline chain: isolated, decode, prefill, config2, "
-                         "config4, lm_head, step, pool, ref_decode, peaks")
+                         "config4, lm_head, step, draft, pool, ref_decode, peaks")
     ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--config2-steps", type=int, default=1000)
     ap.add_argument("--config4-layers", type=int, default=48)
@@ -744,7 +825,7 @@ def main():
     # The records are placed by a permutation over every slot, so the pool's size fixes which weights each expert
     # gets: config4 and the step graph both allocate one layer past config4's stack (the MTP layer), whichever legs
     # run, so that their routing and unique-expert counts do not depend on the leg list.
-    NP = max(NL, args.config4_layers + 1 if "config4" in legs else 0, 49 if "step" in legs else 0)
+    NP = max(NL, args.config4_layers + 1 if "config4" in legs else 0, 49 if legs & {"step", "draft"} else 0)
     log(f"allocating {NP} layers x {E} experts ({NP * E * 1_769_472 / 2**30:.1f} GiB of records)")
     pool = SlotPool(NP, E, H, I, device=dev)
     pool.fill_random(1729)
@@ -836,6 +917,10 @@ def main():
     if "step" in legs:
         stp = step_leg(pool, weights, biases, max(args.steps // 5, 5), dev)
 
+    drf = None
+    if "draft" in legs:
+        drf = draft_leg(pool, weights, biases, max(args.steps // 5, 5), dev)
+
     rd = None
     if "ref_decode" in legs:
         rd = ref_decode_leg(max(args.steps // 2, 10), dev)
@@ -887,6 +972,7 @@ def main():
         "config4": c4,
         "lm_head": lmh,
         "step_graph": stp,
+        "draft_head": drf,
         "reference_shape_moe_decode": rd,
         "pool": pl,
         "cpu_baseline": cpu,

@@ -45,6 +45,11 @@ class MoEStack:
         self.st = rb.SeqState()
         self.record = rb.StepRecord(self.st, self.rows)
 
+    def reset(self) -> None:
+        """A new sequence (the captured graph and the buffers stay)."""
+        self.st = rb.SeqState()
+        self.record = rb.StepRecord(self.st, self.rows)
+
     @property
     def multi(self) -> torch.Tensor:
         """The final stream rows of the last pass [rows, H] (the pre-mixer rows the head consumes)."""
