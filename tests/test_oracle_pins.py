@@ -2,8 +2,10 @@
 
   * oracle.moe_ref (the timed CPU baseline) against moe_ref_cases.npz, written from the reference's own moe_ref
     (model/reference_torch.py:118-134): top-k ids and y bit for bit;
-  * oracle.moe_align against a brute-force restatement of the spec in kernels/moe_align.py:1-48 (stable order
-    inside an expert, sentinel R in the padding, every block owned by one expert, -1 past num_padded);
+  * oracle.moe_align against the reference's own torch moe_align (moe_align_ref.npz: -1 and out-of-range entries,
+    Zipf skew, block 4/64/128, the config-3 shape) and against a brute-force restatement of the spec in
+    kernels/moe_align.py:1-48 (stable order inside an expert, sentinel R in the padding, every block owned by one
+    expert, -1 past num_padded);
   * oracle.prefill_rows against scalar loops over tiny shapes (exact sums with math.fsum, nibbles read bit by bit),
     with a planted mistake that the comparison must catch;
   * the router over 64 seeds of the reference's CPU router (router_ref.npz, torch F.linear + softmax + topk):
@@ -82,6 +84,20 @@ def test_moe_align_matches_brute_force_spec(R, nl, bm, seed):
     assert n == rn
     assert np.array_equal(s, rs) and np.array_equal(b, rb)
     assert len(s) == O.padded_rows(R, nl, bm) and n % bm == 0
+
+
+ALIGN = np.load(GOLD / "moe_align_ref.npz")
+
+
+@pytest.mark.parametrize("case", ["tiny", "r1", "mid", "oob", "cfg3", "skew64"])
+def test_moe_align_matches_reference_fixture(case):
+    """Against the reference's own torch moe_align (kernels/moe_align.py:17-48) on tests/golden/moe_align_ref.npz,
+    written by tests/golden/make_align_golden.py: every output array equal."""
+    R, nl, bm = (int(v) for v in ALIGN[case + "_meta"])
+    s, b, n = O.moe_align(ALIGN[case + "_le"], nl, bm)
+    assert np.array_equal(s, ALIGN[case + "_sorted"])
+    assert np.array_equal(b, ALIGN[case + "_block"])
+    assert n == int(ALIGN[case + "_num"][0])
 
 
 def test_moe_align_brute_force_catches_an_unstable_sort():
