@@ -5,6 +5,23 @@ runs in libssmoe (`ssmoe_sample`) on a device row of fp32 logits. The generator 
 on the host (`UniformStream`): a draw at temperature > 0 consumes exactly one uniform, a greedy draw none, as in
 Sampler.next. The float32 steps are the reference's; the order of each sum and the exp are the library's, so a draw
 can differ from numpy's only where the uniform falls within rounding of a CDF step.
+
+`SampleParams` and its `sanitized()` clamps follow fortil/slotstream-spark engine/sampler.py:14-64 field for field
+(the public parameter type of the drop-in). That file, itself a port of slotstream's sampler (MIT, Copyright (c)
+2026 Carlos Galarza), is under the MIT License:
+
+    Copyright (c) 2026 William Penagos
+
+    Permission is hereby granted, free of charge, to any person obtaining a copy of this software and associated
+    documentation files (the "Software"), to deal in the Software without restriction, including without limitation
+    the rights to use, copy, modify, merge, publish, distribute, sublicense, and/or sell copies of the Software, and
+    to permit persons to whom the Software is furnished to do so, subject to the following conditions: The above
+    copyright notice and this permission notice shall be included in all copies or substantial portions of the
+    Software. THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS OR IMPLIED, INCLUDING BUT NOT
+    LIMITED TO THE WARRANTIES OF MERCHANTABILITY, FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN NO EVENT
+    SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION
+    OF CONTRACT, TORT OR OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER
+    DEALINGS IN THE SOFTWARE.
 """
 from __future__ import annotations
 
