@@ -37,7 +37,10 @@ int ssmoe_device_error(int* flags, int clear);
 
 /* Diagnostics (no reference counterpart): when buf (device memory, >= 16384 uint64) is non-null, every later
  * persistent MoE launch (ssmoe_moe_decode, ssmoe_moe_verify_layer) writes per-workgroup phase timestamps
- * (s_memrealtime, 100 MHz) to buf[workgroup * 16 + phase]; NULL switches it off. Process-wide, not thread-safe. */
+ * (s_memrealtime, 100 MHz) to buf[workgroup * 16 + phase]; a chain launch (ssmoe_moe_verify_chain) writes its last
+ * layer there, the layer before at row 512 + workgroup, and a few more stamps of each at rows 256 + and 768 +
+ * workgroup. NULL switches it off. Process-wide, not thread-safe; a launch captured in a graph keeps the setting
+ * of its capture. */
 int ssmoe_set_trace(void* buf, int64_t entries);
 
 /* Byte offsets of the nine pieces of one affine-4bit expert record (gate.w gate.s gate.b up.w up.s up.b
@@ -137,8 +140,8 @@ int64_t ssmoe_verify_chain_workspace_bytes(int T, int H, int I, int Is, int K, i
  * as n_layers calls of ssmoe_moe_verify_layer_chain; the next layer's router, shared-expert and table reads are issued
  * during the current layer, and the stream passes between layers on the device without a launch.
  * layers_host (host memory) and layers_dev (device memory) hold the same n_layers entries: the host copy is checked
- * and supplies layer 0, the kernel reads the others from the device copy. 1 <= n_layers <= 4096; H 1024 with
- * I in {128, 256, 512, 640, 1024}, or H 2048 with I in {128, 256, 512, 640} (other shapes: SSMOE_EINVAL);
+ * and supplies layer 0, the kernel reads the others from the device copy. 1 <= n_layers <= 4096; H 2048 and
+ * I 512, the BASELINE layer (other shapes: SSMOE_EINVAL; run them as ssmoe_moe_verify_layer_chain launches);
  * E + Is >= 4 * (compute units), so that every wave has a router or shared row in each layer, and H / 8 <= (compute
  * units), so that the workgroups without output rows can take the shared expert's rows. */
 int ssmoe_moe_verify_chain(const uint16_t* stream_in, float eps, const ssmoe_chain_layer* layers_host,

@@ -296,7 +296,9 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   constexpr int NJX = NJG / 4;
   constexpr int NV = kMaxEv / 64;
   const int J = E + Is, W = G * 4;
-  const int j_first = bid * 4 + w;
+  // Router rows go to the workgroups without output rows: they finish a layer first, so the next layer's logits do
+  // not wait for the workgroups that write its stream.
+  const int j_first = ((bid + G - (H >> 4)) % G) * 4 + w;
   const bool has_tile = bid < (H >> 4);
   const int tiles = I >> 3;
   const int my_half = g >> 1, my_part = g & 1;
@@ -360,10 +362,11 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
 #pragma unroll 1
   for (int l = 0; l < NL; ++l) {
     const uint32_t tag = tag0 + (uint32_t)l;
-    const bool tr = a.trace && l == NL - 1;
-#define SS_TRACE(k)                                                                               \
-  do {                                                                                            \
-    if (tr && tid == 0) a.trace[(size_t)bid * 16 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    const bool tr = a.trace && l >= NL - 2;
+    const size_t trow = (size_t)(l == NL - 1 ? bid : 512 + bid) * 16;
+#define SS_TRACE(k)                                                                  \
+  do {                                                                               \
+    if (tr && tid == 0) a.trace[trow + (k)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
     SS_TRACE(0);
     // Offsets of the dynamic LDS regions, made opaque to the compiler at every layer so that the LDS addresses
@@ -408,6 +411,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       const uint32_t want = tag - 1u;
       const int nw = nt * (H >> 1);
       uint32_t* dst = reinterpret_cast<uint32_t*>(scopy);
+      if (tr && tid == 0) a.trace[trow + 256 * 16 + 2] = __builtin_amdgcn_s_memrealtime();
 #pragma unroll 1
       for (int k0 = 0; k0 < nw; k0 += 256 * 8) {
         uint64_t v[8];
@@ -419,7 +423,11 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
             v[k] = idx < nw ? ld_ag(src + idx) : 0ull;
             fresh = fresh && (idx >= nw || (uint32_t)(v[k] >> 32) == want);
           }
-          if (__all(fresh) || dead()) break;
+          if (tr && tid == 0 && it == 0) a.trace[trow + 256 * 16 + 1] = __builtin_amdgcn_s_memrealtime();
+          if (__all(fresh) || dead()) {
+            if (tr && tid == 0) a.trace[trow + 14] = (uint64_t)it;
+            break;
+          }
           if (it >= kChainSpin) {
             give_up();
             break;
@@ -432,6 +440,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
           if (idx < nw) dst[idx] = (uint32_t)v[k];
         }
       }
+      SS_TRACE(5);
       __syncthreads();
       xsrc = scopy;
       norm = true;
@@ -472,17 +481,19 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
         }
       }
     }
-    // Router rows need no wait (their words carry the tag). A wave with shared rows publishes them as soon as its
-    // own stores are acknowledged.
-    {
-      int ns = 0;
-      for (int j = j_first; j < J; j += W)
-        if (j >= E) ns += j == J - 1 ? 2 : 1;
+    // Router rows need no wait (their words carry the tag). A wave with shared rows publishes them once its own
+    // stores are acknowledged: at once, or, for a wave that runs a router tail, after the tail (the shared rows are
+    // first read after the items, so the tail does not wait for the acknowledgement).
+    int ns = 0;
+    for (int j = j_first; j < J; j += W)
+      if (j >= E) ns += j == J - 1 ? 2 : 1;
+    auto publish_shared = [&]() {
       if (ns) {
         stores_done();
         if (lane == 0) signal_add(ctr, CTR_SHARED, ns);
       }
-    }
+    };
+    if (w >= nt) publish_shared();
     // The slot pointers go out now; the waves without a router tail store the table entries while the tail waves
     // work, the tail waves after their tail (the tables are first read by the unique-expert list).
     load_bases();
@@ -501,7 +512,10 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
 
     // ---------------------------------------------------------- phase B: router tail, unique experts
     if (w < nt && !dead()) router_tail_wave(va, logits, tag, w, s, bias_r);
-    if (w < nt) write_tables();
+    if (w < nt) {
+      write_tables();
+      publish_shared();
+    }
     __syncthreads();
     SS_TRACE(3);
     if (bid == 0 && tid < nt * K) {
@@ -783,6 +797,10 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
             acc[r] = ss_rows_sum(acc[r]);
             if (g == 0) partl[((size_t)u * 16 + n) * kTBv + r] = acc[r];
           }
+          // The shared rows are formed while the experts run: a word that was not yet this layer's is requested
+          // again after each of wave 0's experts (one round trip each), so that a fresh one has landed by the combine.
+          if (w == 0 && tid < 16 * kTBv && (tid & 3) < nt && (uint32_t)(shx_w >> 32) != tag)
+            shx_w = ld_ag(shx + shx_i);
         };
         using Two = std::integral_constant<int, 2>;
         using Four = std::integral_constant<int, kTBv>;
@@ -799,23 +817,34 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       }
       SS_TRACE(10);
       __syncthreads();
+      SS_TRACE(12);
       if (tid < 16 * kTBv) {
         const int c = tid >> 2, r = tid & 3;
         uint32_t sb = 0;
         if (r < nt) {
           constexpr int KM = kMaxQv / kTBv;
-          float ov[KM];
+          // Every LDS read is issued before any is used (two dependent rounds, no branch per term).
+          int uq[KM];
+          float wq[KM], pv[KM], ov[KM];
 #pragma unroll
           for (int k = 0; k < KM; ++k) {
-            const int q = r * K + (k < K ? k : 0), u = s.use_u[q];
-            const float pv = partl[((size_t)(u >= 0 ? u : 0) * 16 + c) * kTBv + r];
-            ov[k] = k < K && u >= 0 ? pv * s.wts[q] : 0.f;
+            const int q = r * K + (k < K ? k : 0);
+            uq[k] = s.use_u[q];
+            wq[k] = s.wts[q];
+          }
+#pragma unroll
+          for (int k = 0; k < KM; ++k) pv[k] = partl[((size_t)(uq[k] >= 0 ? uq[k] : 0) * 16 + c) * kTBv + r];
+#pragma unroll
+          for (int k = 0; k < KM; ++k) {
+            const float prod = pv[k] * wq[k];
+            ov[k] = k < K && uq[k] >= 0 ? prod : 0.f;
           }
           float acc = 0.f;
 #pragma unroll
           for (int k = 0; k < KM; ++k)
             if (k < K) acc = k == 0 ? ov[k] : acc + ov[k];
           if (lp.routed_out) lp.routed_out[(size_t)r * H + 16 * bid + c] = acc;
+          if (tid == 0 && tr) a.trace[trow + 256 * 16 + 3] = __builtin_amdgcn_s_memrealtime();
           for (int it = 0; (uint32_t)(shx_w >> 32) != tag; ++it) {
             if (dead()) break;
             if (it >= kChainSpin) {
@@ -825,6 +854,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
             __builtin_amdgcn_s_sleep(1);
             shx_w = ld_ag(shx + shx_i);
           }
+          if (tid == 0 && tr) a.trace[trow + 15] = __builtin_amdgcn_s_memrealtime();
           const float sh2 = ss_bf16_to_f32((uint32_t)shx_w & 0xFFFFu);
           const uint32_t yb = ss_f32_to_bf16(ss_round_bf16(acc) + sh2);
           lp.y[(size_t)r * H + 16 * bid + c] = (uint16_t)yb;
@@ -836,6 +866,11 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
         if (r < nt && (c & 1) == 0 && l + 1 < NL)
           st_ag(sw_all + (size_t)(l & 1) * kTBv * (H / 2) + (size_t)r * (H / 2) + 8 * bid + (c >> 1),
                 ((uint64_t)tag << 32) | (uint64_t)(sb | (sb_hi << 16)));
+      }
+      SS_TRACE(6);
+      if (tr && tid == 0) {
+        __builtin_amdgcn_s_waitcnt(0);
+        a.trace[trow + 256 * 16 + 0] = __builtin_amdgcn_s_memrealtime();
       }
     }
 
@@ -850,6 +885,22 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       load_map(ln);
       if (w < nt) load_bias(ln);
       lp = ln;
+      if (false) {
+        // Every expert record of the next layer is touched once per XCD (two reads per record: its start and its
+        // down piece), so that the address translations its items need are cached when its router decides. The
+        // workgroups without output rows are idle here until the stream arrives.
+        const int q = ((bid - (H >> 4)) >> 3) * 64 + lane;
+        const int e = q >> 1;
+        const int64_t mi = ln.layer * E + e;
+        if (e < E && mi >= 0 && mi < a.map_len) {
+          const int sl = gp(a.map)[mi];
+          if (sl >= 0 && (int64_t)sl < a.n_slots) {
+            const uint8_t* b = reinterpret_cast<const uint8_t*>(gp(a.slot_ptr)[sl]);
+            const uint32_t v = *reinterpret_cast<const SS_G uint32_t*>(gp(b + ((q & 1) ? rec.dw : 0)));
+            asm volatile("" ::"v"(v));
+          }
+        }
+      }
     }
     __syncthreads();
     SS_TRACE(11);
@@ -893,20 +944,13 @@ static hipError_t launch_chain_nj(const ChainArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-bool chain_shape_supported(int H, int I) {
-  return (H == 1024 && (I == 128 || I == 256 || I == 512 || I == 640 || I == 1024)) ||
-         (H == 2048 && (I == 128 || I == 256 || I == 512 || I == 640));
-}
+bool chain_shape_supported(int H, int I) { return H == 2048 && I == 512; }
 
 hipError_t launch_chain(const ChainArgs& a, hipStream_t st) {
-  // Shapes with instantiated kernels (the ones whose layer loop fits the register file without spilling):
-  // H 1024 x I in {128, 256, 512, 640, 1024}, H 2048 x I in {128, 256, 512, 640}.
+  // One instantiated shape: H 2048 x I 512, the BASELINE layer (the layer loop is sized to the register file for it);
+  // other shapes run one ssmoe_moe_verify_layer_chain launch per layer.
   const int njg = a.H / 128, njd = a.I / 128;
-#define SS_CASE(G_, D_) \
-  if (njg == G_ && njd == D_) return launch_chain_nj<G_, D_>(a, st);
-  SS_CASE(8, 1) SS_CASE(8, 2) SS_CASE(8, 4) SS_CASE(8, 5) SS_CASE(8, 8)
-  SS_CASE(16, 1) SS_CASE(16, 2) SS_CASE(16, 4) SS_CASE(16, 5)
-#undef SS_CASE
+  if (njg == 16 && njd == 4) return launch_chain_nj<16, 4>(a, st);
   return hipErrorInvalidValue;
 }
 
