@@ -69,6 +69,14 @@ int ssmoe_topk_stable(const float* scores, const int32_t* n_valid, int32_t* out_
  * x bf16 [T, H], w bf16 [N, H], out bf16 [T, N]; H % 8 == 0, H <= 8192. */
 int ssmoe_dense_gemv_bf16(const uint16_t* x, const uint16_t* w, uint16_t* out, int T, int H, int N, void* stream);
 
+/* lin on a bf16 weight over many rows (model/layers.py:62-76 inside prefill_gemm(), the dense case of
+ * kernels/gemm_affine.py:20-98): c = bf16(a w^T), a bf16 [M][lda], w bf16 [N][ldw], c bf16 [M][ldc], the dot over
+ * K accumulated in fp32 by the bf16 MFMA unit and rounded once. The prefill's router logits and shared-expert
+ * projections. K a multiple of 256; lda, ldw >= K and ldc >= N, all multiples of 8; a, w, c 16-byte aligned.
+ * Row m of c depends on row m of a only. */
+int ssmoe_dense_gemm(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, uint16_t* c, int64_t ldc, int M,
+                     int N, int K, void* stream);
+
 /* Router: logits = bf16(x router_w^T), scores = logits (+ bias), probs = softmax(scores) in fp32, top-k with
  * ties to the lower index, weights = topk / sum(topk) in rank order.
  * Replaces Segments.seg_router (model/layers.py:336-348) and reference_torch.moe_ref:121-124. bias fp32 [E] or

@@ -26,6 +26,7 @@ SIGNATURES = {
     "ssmoe_moe_decode": (_I, [_P, _I, _P, _P, _I, _P, _I64, _P, _I64, _P, _P, _P, _I, _I, _I, _I, _I, _P]),
     "ssmoe_topk_stable": (_I, [_P, _P, _P, _P, _I, _I, _I, _P]),
     "ssmoe_dense_gemv_bf16": (_I, [_P, _P, _P, _I, _I, _I, _P]),
+    "ssmoe_dense_gemm": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _I, _I, _P]),
     "ssmoe_router": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "ssmoe_router_topk": (_I, [_P, _P, _P, _P, _P, _I, _I, _I, _P]),
     "ssmoe_verify_workspace_bytes": (_I64, [_I, _I, _I, _I, _I, _I]),

@@ -36,6 +36,10 @@ struct DenseSeg {
 // Dot products in the defined order (lane l, chunk j: elements 512j + 8l .. +8, fmaf, then the xor butterfly).
 hipError_t launch_dense_rows(const uint16_t* x, int T, int H, const DenseSeg* segs, int nseg, hipStream_t st);
 
+// Dense bf16 GEMM c = bf16(a b^T) with MFMA fp32 accumulation (ss_gemm.hip): a [M][lda], b [N][ldb], c [M][ldc].
+hipError_t launch_dense_gemm(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, uint16_t* c, int64_t ldc,
+                             int M, int N, int K, hipStream_t st);
+
 // Router tail for T tokens: scores = bf16 logits (+ bias), fp32 softmax, top-k (ties -> lower index,
 // sorted by value desc), renormalised weights. probs may be null.
 hipError_t launch_router_topk(const uint16_t* logits, const float* bias, float* probs, int32_t* ids, float* weights,

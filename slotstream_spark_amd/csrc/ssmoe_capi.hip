@@ -232,6 +232,17 @@ int ssmoe_dense_gemv_bf16(const uint16_t* x, const uint16_t* w, uint16_t* out, i
   return hip_check(ss::launch_dense_rows(x, T, H, &s, 1, static_cast<hipStream_t>(stream)), "dense gemv launch");
 }
 
+int ssmoe_dense_gemm(const uint16_t* a, int64_t lda, const uint16_t* w, int64_t ldw, uint16_t* c, int64_t ldc, int M,
+                     int N, int K, void* stream) {
+  if (M < 0 || N < 0 || K < 256 || K % 256) return fail(SSMOE_EINVAL, "need M, N >= 0 and K a positive multiple of 256");
+  if (lda < K || ldw < K || ldc < N || lda % 8 || ldw % 8 || ldc % 8)
+    return fail(SSMOE_EINVAL, "need lda, ldw >= K, ldc >= N, all multiples of 8");
+  if (!a || !w || !c) return fail(SSMOE_EINVAL, "a, w and c must be non-null");
+  if (!aligned(a, 16) || !aligned(w, 16) || !aligned(c, 16)) return fail(SSMOE_EINVAL, "a, w and c must be 16-byte aligned");
+  return hip_check(ss::launch_dense_gemm(a, lda, w, ldw, c, ldc, M, N, K, static_cast<hipStream_t>(stream)),
+                   "dense gemm launch");
+}
+
 int ssmoe_router(const uint16_t* x, const uint16_t* router_w, const float* bias, uint16_t* logits, float* probs,
                  int32_t* ids, float* weights, int T, int H, int E, int K, void* stream) {
   if (T < 1 || H < 8 || H % 8 || H > 8192) return fail(SSMOE_EINVAL, "need T >= 1, H a multiple of 8 <= 8192");

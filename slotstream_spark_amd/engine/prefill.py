@@ -4,17 +4,18 @@ Mirrors SweepMoE.layer (slotstream_spark/model/moe_sweep.py:80-160) plus the rou
 (model/layers.py:336-348, 398-402): router logits lin(x, W_gate) as a bf16 GEMM, softmax / stable top-k /
 renormalisation on the device (ssmoe_router_topk), the routed experts as one plan over all E experts
 (ssmoe_moe_prefill: moe_align, grouped gate/up, down, rank-order combine), and y = bf16(routed) + shared.
-The dense projections are plain bf16 GEMMs on the platform BLAS through torch: the router, one GEMM for the shared
-expert's gate, up and shared_expert_gate rows together (their weights concatenated once at construction), and the
-shared down projection. The routed experts, the routing, the shared expert's elementwise chain (ssmoe_shared_hs) and
-the final y (ssmoe_combine_shared) run in libssmoe, with the reference's bf16 rounding of every op.
+The dense projections run on libssmoe's bf16 MFMA GEMM (ssmoe_dense_gemm, lin's fp32 dot rounded once to bf16):
+the router, one GEMM for the shared expert's gate, up and shared_expert_gate rows together (their weights
+concatenated once at construction), and the shared down projection. The routed experts, the routing, the shared
+expert's elementwise chain (ssmoe_shared_hs) and the final y (ssmoe_combine_shared) run in libssmoe as well, with the
+reference's bf16 rounding of every op; torch only allocates.
 """
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 
 from .. import _lib
+from ..kernels.router import gemm_bf16
 from ..memory.slot_pool import SlotPool
 
 
@@ -49,7 +50,7 @@ class MoEPrefillLayer:
 
     def route(self, x: torch.Tensor):
         t = x.shape[0]
-        logits = F.linear(x, self.router_w)
+        logits = gemm_bf16(x, self.router_w)
         ids, w = self.ids[:t], self.weights[:t]
         _lib.check(_lib.lib().ssmoe_router_topk(logits.data_ptr(), _lib.ptr(self.router_bias), None, ids.data_ptr(),
                                                 w.data_ptr(), t, self.experts, self.top_k, _lib.stream_of(x)))
@@ -66,14 +67,14 @@ class MoEPrefillLayer:
         return out
 
     def shared(self, x: torch.Tensor):
-        """(sh bf16 [T, H] = F.linear(bf16(silu(g)) * u, sh_down), shared_expert_gate logits bf16 [T])."""
+        """(sh bf16 [T, H] = lin(bf16(silu(g)) * u, sh_down), shared_expert_gate logits bf16 [T])."""
         t = x.shape[0]
-        proj = F.linear(x, self.sh_cat)
+        proj = gemm_bf16(x, self.sh_cat)
         hs = torch.empty((t, self.shared_inter), dtype=torch.bfloat16, device=x.device)
         sgl = torch.empty((t,), dtype=torch.bfloat16, device=x.device)
         _lib.check(_lib.lib().ssmoe_shared_hs(proj.data_ptr(), proj.shape[1], t, self.shared_inter, hs.data_ptr(),
                                               sgl.data_ptr(), _lib.stream_of(x)))
-        return F.linear(hs, self.sh_down), sgl
+        return gemm_bf16(hs, self.sh_down), sgl
 
     def __call__(self, x: torch.Tensor):
         """x bf16 [T, H] -> (y bf16 [T, H], ids int32 [T, K], weights fp32 [T, K], routed fp32 [T, H]);

@@ -33,6 +33,23 @@ def lin_bf16(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) 
     return out
 
 
+def gemm_bf16(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x bf16 [M, K] @ w bf16 [N, K]^T -> bf16 [M, N] on the MFMA GEMM (ssmoe_dense_gemm): lin over a prompt chunk
+    (model/layers.py:62-76 inside prefill_gemm()). K a multiple of 256, N a multiple of 8."""
+    if x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16 or x.dim() != 2 or w.dim() != 2:
+        raise ValueError("x and w must be bf16 2-D tensors")
+    if x.shape[1] != w.shape[1] or not x.is_contiguous() or not w.is_contiguous():
+        raise ValueError("x [M, K] and w [N, K] must be contiguous with the same K")
+    m, n = x.shape[0], w.shape[0]
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    if tuple(out.shape) != (m, n) or out.dtype != torch.bfloat16 or not out.is_contiguous():
+        raise ValueError(f"out must be contiguous bf16 [{m}, {n}]")
+    _lib.check(_lib.lib().ssmoe_dense_gemm(x.data_ptr(), x.shape[1], w.data_ptr(), w.shape[1], out.data_ptr(), n, m, n,
+                                           x.shape[1], _lib.stream_of(x)))
+    return out
+
+
 def route(x: torch.Tensor, router_w: torch.Tensor, k: int, bias: torch.Tensor | None = None, *,
           logits: torch.Tensor | None = None, probs: torch.Tensor | None = None,
           ids: torch.Tensor | None = None, weights: torch.Tensor | None = None):

@@ -1,0 +1,97 @@
+"""The prefill's dense bf16 GEMM (ssmoe_dense_gemm, kernels/router.gemm_bf16) on the GPU:
+
+  * against float64 dots of the same bf16 operands rounded once to bf16: every element within one bf16 step, nearly
+    all bit-identical, at the prefill's three shapes (router 2048 x 512 x 2048, shared gate/up/gate-logit
+    2048 x 1032 x 2048, shared down 2048 x 2048 x 512) and at ragged ones;
+  * row independence: the rows of a shorter call equal the same rows of a longer one bit for bit;
+  * the prefill router at T = 2048 against the reference's CPU router semantics (torch F.linear in bf16, then the
+    routing): the GEMM's logits differ from torch's in a few bf16 roundings (another fp32 summation order), and a row's
+    top-10 may differ only where the experts involved score within that row's largest logit difference of the
+    10th score (a tie within rounding); every other row selects the same experts.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from slotstream_spark_amd.kernels.router import gemm_bf16
+from slotstream_spark_amd.memory.synth import normal_bf16, zipf_bias
+from tests.gpu_util import bits
+
+pytestmark = pytest.mark.gpu
+
+
+def _ref(a, w):
+    """(bf16(float64 dot) of bf16 operands as bf16 bits, float64 dot, sum of |products|)."""
+    a64 = a.float().cpu().double().numpy()
+    w64 = w.float().cpu().double().numpy()
+    d = a64 @ w64.T
+    return O.f32_to_bf16(d.astype(np.float32)), d, np.abs(a64) @ np.abs(w64).T
+
+
+def _steps(a_bits, b_bits):
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    ma = np.where(a & 0x8000, 0x8000 - a, a)
+    mb = np.where(b & 0x8000, 0x8000 - b, b)
+    return np.abs(ma - mb)
+
+
+@pytest.mark.parametrize("M,N,K", [(2048, 512, 2048), (2048, 1032, 2048), (2048, 2048, 512), (130, 1032, 2048),
+                                   (1, 8, 256), (77, 136, 256), (300, 40, 768)])
+def test_dense_gemm_against_float64(M, N, K):
+    print(f"[gemm] M={M} N={N} K={K}", flush=True)
+    a = normal_bf16((M, K), 1.0, M + K)
+    w = normal_bf16((N, K), K ** -0.5, N + K)
+    c = gemm_bf16(a, w)
+    torch.cuda.synchronize()
+    got = bits(c)
+    ref, d64, mag = _ref(a, w)
+    steps = _steps(got, ref)
+    same = float(np.mean(steps == 0))
+    # One bf16 rounding (at most one bf16 step, 2^-8 relative) of an fp32 accumulation whose error is a small
+    # multiple of 2^-24 sum |a w| (2^-16 leaves room for K up to 2048 terms).
+    err = np.abs(O.bf16_to_f32(got).astype(np.float64) - d64)
+    bound = 2.0 ** -8 * np.abs(d64) + 2.0 ** -16 * mag
+    print(f"bit-identical to bf16(fp64 dot): {same:.5f}, max {int(steps.max())} step(s), "
+          f"max err / bound {float((err / bound).max()):.3f}")
+    assert np.all(err <= bound)
+    assert same >= 0.99
+
+
+def test_dense_gemm_rows_do_not_depend_on_the_call():
+    a = normal_bf16((700, 2048), 1.0, 5)
+    w = normal_bf16((1032, 2048), 2048 ** -0.5, 6)
+    full = gemm_bf16(a, w)
+    part = gemm_bf16(a[100:355].contiguous(), w)
+    torch.cuda.synchronize()
+    assert torch.equal(part, full[100:355])
+
+
+def test_prefill_router_against_reference_cpu_router():
+    T, H, E, K = 2048, 2048, 512, 10
+    print(f"[prefill router] T={T} E={E} K={K}", flush=True)
+    x = normal_bf16((T, H), 1.0, 1730)
+    rw = normal_bf16((E, H), 0.02, 1729 * 8 + 1)
+    bias = zipf_bias(E, 1.1, 1731)
+    logits = gemm_bf16(x, rw)
+    torch.cuda.synchronize()
+    mine = bits(logits)
+    ref = bits(torch.nn.functional.linear(x.cpu(), rw.cpu()))  # the reference's router logits (torch CPU, bf16)
+    b = bias.cpu().numpy()
+    _, ids, _ = O.router_topk(mine, K, b)
+    _, ids_r, _ = O.router_topk(ref, K, b)
+    diff_logits = int((mine != ref).sum())
+    steps = _steps(mine, ref)
+    scores_r = O.bf16_to_f32(ref) + b[None, :]
+    dl = np.abs(O.bf16_to_f32(mine) - O.bf16_to_f32(ref)).max(axis=1)
+    n_rows = 0
+    for t in np.nonzero((np.sort(ids, 1) != np.sort(ids_r, 1)).any(1))[0]:
+        n_rows += 1
+        kth = np.sort(scores_r[t])[::-1][K - 1]
+        for e in np.setxor1d(ids[t], ids_r[t]):
+            assert abs(scores_r[t, e] - kth) <= dl[t] + 1e-6, (t, e)
+    print(f"{diff_logits} of {mine.size} logits differ from torch's (max {int(steps.max())} bf16 step(s), near zero); "
+          f"{n_rows} of {T} rows select otherwise, each at a tie within that difference")
+    assert diff_logits <= 2e-3 * mine.size
+    assert n_rows <= 0.01 * T

@@ -10,6 +10,7 @@ from slotstream_spark_amd import _lib
 from slotstream_spark_amd.engine.prefill import MoEPrefillLayer
 from slotstream_spark_amd.kernels.fused_moe_affine import BLOCK_M, align_rows, combine_rank_order, fused_moe_affine
 from slotstream_spark_amd.kernels.moe_align import moe_align
+from slotstream_spark_amd.kernels.router import gemm_bf16
 from slotstream_spark_amd.memory.synth import LayerWeights, normal_bf16, zipf_bias
 from tests.gpu_util import DenseCache, bits, make_pool, rand_ids, rand_weights
 
@@ -150,7 +151,8 @@ def test_prefill_unmapped_expert_flagged():
 
 
 def test_prefill_layer_end_to_end():
-    """Router (bf16 GEMM + device top-k) + routed experts + shared expert at the config-3 shape on a short chunk."""
+    """Router (bf16 MFMA GEMM + device top-k) + routed experts + shared expert at the config-3 shape on a short chunk;
+    the GEMMs themselves are checked in test_gpu_dense_gemm.py."""
     T, K, E, H, I = 128, 10, 512, 2048, 512
     pool = make_pool(E, H, I, seed=31)
     lw = LayerWeights(H, E, 512, seed=32)
@@ -161,18 +163,18 @@ def test_prefill_layer_end_to_end():
     y, ids, w, routed = layer(x)
     torch.cuda.synchronize()
     # routing against the oracle's router tail applied to the GEMM's own logits
-    logits = torch.nn.functional.linear(x, lw.router_w)
+    logits = gemm_bf16(x, lw.router_w)
     _, rids, rw = O.router_topk(bits(logits), K, bias.cpu().numpy())
     assert np.array_equal(ids.cpu().numpy(), rids)
     assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
     _, rows_ref = _oracle_rows(pool, x, ids, w)
     assert O.rel_l2(routed.cpu().numpy(), O.combine_rank_order(rows_ref, T, K)) < 2e-3
     # the shared expert's elementwise chain and y, bit for bit, from the GEMMs' own bf16 outputs
-    proj = torch.nn.functional.linear(x, layer.sh_cat)
+    proj = gemm_bf16(x, layer.sh_cat)
     Is = lw.sh_gate.shape[0]
     pb = bits(proj)
     hs_ref = O.shared_hs(pb[:, :Is], pb[:, Is:2 * Is])
-    sh = torch.nn.functional.linear(torch.from_numpy(hs_ref.view(np.int16)).view(torch.bfloat16).cuda(), lw.sh_down)
+    sh = gemm_bf16(torch.from_numpy(hs_ref.view(np.int16)).view(torch.bfloat16).cuda(), lw.sh_down)
     y_ref = O.combine_shared(routed.cpu().numpy(), bits(sh), pb[:, 2 * Is].copy())
     assert np.array_equal(bits(y), y_ref)
     assert torch.isfinite(y.float()).all()
