@@ -439,6 +439,28 @@ def step_leg(pool, weights, biases, steps, dev):
         log(f"step graph T={depth + 1}: {us:.1f} us per round ({NL} layers + head MoE + lm_head greedy), "
             f"mean unique experts {sum(uniq) / NL:.1f}")
         del sg
+    # the T=4 round with p/q acceptance fused behind the lm_head (temperature 0.7; the draft head's logits of the
+    # round are an input, synthetic here)
+    sg = MTPStepGraph(pool, mw[:NL], lm, 3, head=mw[NL], top_k=K, accept="pq", temperature=0.7, device=dev)
+    g2 = torch.Generator(device=dev).manual_seed(2723)
+    sg.draft_logits.copy_(torch.randn(sg.draft_logits.shape, generator=g2, device=dev) * 3)
+    sg.uniforms.copy_(torch.rand(4, generator=g2, device=dev))
+    drafts = sg.draft_logits.argmax(dim=1).to(torch.int32)
+    sg.step(normal_bf16((4, H), 1.0, 2722, dev), drafts)
+    for _ in range(2):
+        sg.step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record()
+    for _ in range(steps):
+        sg.step()
+    ev1.record()
+    torch.cuda.synchronize()
+    us = ev0.elapsed_time(ev1) * 1000.0 / steps
+    res["T4_pq"] = {"us_per_round": round(us, 1), "temperature": 0.7, "result": sg.out.cpu().tolist()[:4],
+                    "note": "lm_head GEMV writes logits and chunk maxima; the p/q round reads the logits once"}
+    log(f"step graph T=4 with fused p/q: {us:.1f} us per round")
+    del sg
     return res
 
 

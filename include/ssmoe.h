@@ -294,6 +294,19 @@ int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* 
                          const uint16_t* b, int N, const int32_t* drafts, void* workspace, int64_t workspace_bytes,
                          float* logits, int32_t* out, void* stream);
 
+/* Bytes of the workspace ssmoe_lm_head_pq needs (-1 on bad arguments). */
+int64_t ssmoe_lm_head_pq_workspace_bytes(int D, int N);
+
+/* The lm_head GEMV over the D+1 verify rows with the p/q round (as ssmoe_accept_pq) behind it: the GEMV writes the
+ * logits (lin's values, as ssmoe_lm_head_greedy) and, per row and 1024-entry vocabulary chunk, the maximum of
+ * logit / temperature and a non-finite flag, so the round's maximum pass reads only the draft rows and the logits
+ * are read once, for the sums. The same out as ssmoe_accept_pq on those logits, bit for bit. draft fp32 [D][N]
+ * (the draft head's logits), drafts int32 [D], uniforms fp32 [D+1], logits fp32 [D+1][N] (written). 0 <= D <= 3;
+ * the workspace's first 16 KB must be zero before the first call (every call leaves them zero). */
+int ssmoe_lm_head_pq(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s, const uint16_t* b,
+                     int N, const float* draft, const int32_t* drafts, const float* uniforms, float temperature,
+                     void* workspace, int64_t workspace_bytes, float* logits, int32_t* out, void* stream);
+
 /* Bytes of the workspace ssmoe_lm_head_argmax needs (-1 on bad arguments). */
 int64_t ssmoe_lm_head_argmax_workspace_bytes(int R, int N);
 

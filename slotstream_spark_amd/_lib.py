@@ -67,6 +67,8 @@ SIGNATURES = {
     "ssmoe_lm_head_greedy_workspace_bytes": (_I64, [_I, _I]),
     "ssmoe_lm_head_greedy": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P, _P, _I64, _P, _P, _P]),
     "ssmoe_accept_sampled": (_I, [_P, _P, _I, _I, _P, _I, _F, _F, _I, _F, _F, _P, _P, _I64, _P, _P]),
+    "ssmoe_lm_head_pq_workspace_bytes": (_I64, [_I, _I]),
+    "ssmoe_lm_head_pq": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _P, _P, _P, _F, _P, _I64, _P, _P, _P]),
     "ssmoe_lm_head_argmax_workspace_bytes": (_I64, [_I, _I]),
     "ssmoe_lm_head_argmax": (_I, [_P, _I, _I, _I, _P, _P, _P, _I, _I, _P, _I64, _P, _P, _P]),
     "ssmoe_rmsnorm": (_I, [_P, _P, _F, _I, _I, _I, _P, _P]),

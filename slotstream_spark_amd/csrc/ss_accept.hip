@@ -375,6 +375,15 @@ __global__ __launch_bounds__(64) void pq_max_kernel(AcceptArgs a) {
   const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
   const int nch = gridDim.x, rows = gridDim.y;
   Work k = work_of(a.work, rows, nch);
+  if (a.tkey && row <= a.D) {
+    // formed by the lm_head GEMV: the same maximum (order-free), key 0 = a chunk of NaNs only (fmaxf's -inf)
+    if (lane == 0) {
+      const uint32_t key = a.tkey[row * nch + c];
+      k.cmax[row * nch + c] = key ? ss_unkey(key) : -__builtin_inff();
+      k.cbad[row * nch + c] = a.tbad[row * nch + c] ? 1.f : 0.f;
+    }
+    return;
+  }
   const float* x = row_ptr(a, row);
   float v[kSub];
 #pragma unroll

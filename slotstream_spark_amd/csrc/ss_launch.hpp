@@ -200,6 +200,12 @@ int64_t lm_head_greedy_workspace_bytes(int D, int N);
 hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
                                  const uint16_t* b, int N, const int32_t* drafts, void* work, float* logits,
                                  int32_t* out, hipStream_t st);
+// The lm_head GEMV over the D + 1 verify rows with the p/q round behind it: the GEMV writes the logits (lin's
+// values) and each row's chunk maxima, then the p/q launches (ss_accept.hip) read the logits once for the sums.
+int64_t lm_head_pq_workspace_bytes(int D, int N);
+hipError_t launch_lm_head_pq(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
+                             const uint16_t* b, int N, const float* draft, const int32_t* drafts, const float* uniforms,
+                             float temperature, void* work, float* logits, int32_t* out, int* err, hipStream_t st);
 // Argmax ids of R rows (R <= 64; workspace lm_head_greedy_workspace_bytes(R - 1, N)).
 hipError_t launch_lm_head_argmax(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s,
                                  const uint16_t* b, int N, int round_bf16, void* work, float* logits, int32_t* ids,
@@ -229,6 +235,10 @@ struct AcceptArgs {
   int32_t* out;          // [D + 5]: n_accept, n_emit, n_uniform, flags, tokens[D+1]
   float* work;           // workspace floats
   int* err;
+  // p/q: the target rows' chunk maxima of l / T as order keys and their non-finite flags, [D + 1][nch], already
+  // formed by the lm_head GEMV (the max pass then reads only the draft rows), or null.
+  const uint32_t* tkey;
+  const int* tbad;
 };
 int64_t accept_work_floats(int D, int V);
 hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st);

@@ -823,6 +823,32 @@ int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* 
                    "lm_head greedy launch");
 }
 
+int64_t ssmoe_lm_head_pq_workspace_bytes(int D, int N) {
+  if (D < 0 || D > 3 || N < 1 || N > (1 << 20)) return -1;
+  return ss::lm_head_pq_workspace_bytes(D, N);
+}
+
+int ssmoe_lm_head_pq(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s, const uint16_t* b,
+                     int N, const float* draft, const int32_t* drafts, const float* uniforms, float temperature,
+                     void* workspace, int64_t workspace_bytes, float* logits, int32_t* out, void* stream) {
+  if (D < 0 || D > 3) return fail(SSMOE_EINVAL, "D must be in [0, 3], got %d", D);
+  if (N > (1 << 20)) return fail(SSMOE_EINVAL, "N must be <= 1048576, got %d", N);
+  if (int rc = check_gemv(x, K, q, s, b, N)) return rc;
+  if (!logits || !out || !uniforms || (D > 0 && (!draft || !drafts)))
+    return fail(SSMOE_EINVAL, "logits, out, uniforms, draft and drafts must be non-null");
+  if (!(temperature > 0.f) || temperature != temperature)
+    return fail(SSMOE_EINVAL, "temperature must be > 0, got %g", (double)temperature);
+  if (!workspace || !aligned(workspace, 256)) return fail(SSMOE_EINVAL, "workspace must be non-null and 256-byte aligned");
+  if (workspace_bytes < ss::lm_head_pq_workspace_bytes(D, N))
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)ss::lm_head_pq_workspace_bytes(D, N));
+  int* err = nullptr;
+  if (int rc = status_ptr(&err)) return rc;
+  return hip_check(ss::launch_lm_head_pq(x, x_f32 ? 1 : 0, D, K, q, s, b, N, draft, drafts, uniforms, temperature,
+                                         workspace, logits, out, err, static_cast<hipStream_t>(stream)),
+                   "lm_head p/q launch");
+}
+
 int64_t ssmoe_lm_head_argmax_workspace_bytes(int R, int N) {
   if (R < 1 || R > 64 || N < 1) return -1;
   return ss::lm_head_greedy_workspace_bytes(R - 1, N);

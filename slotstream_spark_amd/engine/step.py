@@ -25,7 +25,7 @@ from dataclasses import dataclass
 import torch
 
 from .. import _lib
-from ..kernels.gemv_affine import AffineWeight, LMHeadGreedy
+from ..kernels.gemv_affine import AffineWeight, LMHeadGreedy, LMHeadPQ
 from .accept import AcceptResult
 from .verify import MoEVerifyChain, MoEVerifyLayer
 
@@ -79,7 +79,7 @@ class MTPStepGraph:
     def __init__(self, pool, layers: list[MoEWeights], lm_head: AffineWeight, depth: int,
                  head: MoEWeights | None = None, norm_weights: list[torch.Tensor | None] | None = None,
                  eps: float = 1e-6, top_k: int = 10, keep_logits: bool = False, fused: bool = True,
-                 single_launch: bool = True, device="cuda"):
+                 single_launch: bool = True, accept: str = "greedy", temperature: float = 1.0, device="cuda"):
         if not 1 <= depth <= 3:
             raise ValueError("depth must be 1..3 (the verify kernel takes up to 4 rows)")
         self.depth, self.rows = depth, depth + 1
@@ -126,7 +126,20 @@ class MTPStepGraph:
             self.chain = MoEVerifyChain(self.layers, self.ys, list(self.ids), list(self.weights),
                                         stream_outs=self.streams[1:], norm_weights=self.norm_weights[:self.nl],
                                         eps=self.eps)
-        self.lm_head = LMHeadGreedy(lm_head, depth, device=dev) if lm_head is not None else None
+        if accept not in ("greedy", "pq"):
+            raise ValueError(f"accept must be 'greedy' or 'pq', got {accept!r}")
+        self.accept = accept
+        self.draft_logits = self.uniforms = None
+        if lm_head is None:
+            self.lm_head = None
+        elif accept == "greedy":
+            self.lm_head = LMHeadGreedy(lm_head, depth, device=dev)
+        else:
+            # p/q: the draft head's logits of the round's drafts and the round's uniforms are inputs like the drafts
+            self.lm_head = LMHeadPQ(lm_head, depth, temperature, device=dev)
+            self.draft_logits = torch.zeros((depth, lm_head.n), dtype=torch.float32, device=dev)
+            self.uniforms = torch.zeros(depth + 1, dtype=torch.float32, device=dev)
+            self.logits = self.lm_head.logits
         self.out = self.lm_head.out if lm_head is not None else None
         self.stream = torch.cuda.Stream(device=dev)
         self.graph = None
@@ -148,7 +161,9 @@ class MTPStepGraph:
                 layer(self.mixed[l], y=self.ys[l], ids=self.ids[l], weights=self.weights[l])
                 residual_rmsnorm(self.streams[l], self.ys[l], self.mixed[l + 1], stream_out=self.streams[l + 1],
                                  weight=w[l + 1], eps=self.eps)
-        if self.lm_head is not None:
+        if self.lm_head is not None and self.accept == "pq":
+            self.lm_head.run_async(self.mixed[self.nl], self.draft_logits, self.drafts, self.uniforms)
+        elif self.lm_head is not None:
             self.lm_head.run_async(self.mixed[self.nl], self.drafts, logits=self.logits)
         if self.head is not None:
             self.head(self.mixed[self.nl], y=self.head_y, ids=self.head_ids, weights=self.head_weights)

@@ -4,7 +4,9 @@
 its signature and errors (:214-262) and runs `ssmoe_gemv_affine4` for bits=4, gs=64 (the model's format, e.g. the
 lm_head 248,320 x 2560): fp32 accumulation of exact bf16 products, one fixed order per output element, and row r of
 the result depends on x row r alone, so an R-row call equals R one-row calls bit for bit (kernels/tuning.py:1-10).
-`lm_head_greedy` fuses the lm_head with the greedy round after it (engine/generate.py:208-229).
+`LMHeadGreedy` fuses the lm_head with the greedy round after it (engine/generate.py:208-229), `LMHeadPQ` with the
+p/q round (the GEMV forms the logits' chunk maxima, so the round reads the logits once), and `LMHeadArgmax` gives the
+draft head's token (engine/mtp.py:275).
 """
 from __future__ import annotations
 
@@ -141,3 +143,46 @@ class LMHeadArgmax:
             self.w.b.data_ptr(), self.w.n, 1 if self.round_bf16 else 0, self.work.data_ptr(), self.work.numel(),
             _lib.ptr(logits), ids.data_ptr(), _lib.stream_of(x)))
         return ids
+
+
+class LMHeadPQ:
+    """The lm_head over the D+1 verify rows with the p/q round behind it (ssmoe_lm_head_pq): the GEMV writes the
+    logits (lin's values) and their chunk maxima, and the round reads the logits once, for the sums; the same result
+    as Acceptor.pq on those logits, bit for bit. Workspace, logits [D+1, V] and out [D+5] owned here."""
+
+    def __init__(self, w: AffineWeight, depth: int, temperature: float, device="cuda"):
+        _device_weight(w)
+        if not temperature > 0:
+            raise ValueError("temperature must be > 0")
+        self.w, self.depth, self.temperature = w, depth, float(temperature)
+        nb = int(_lib.lib().ssmoe_lm_head_pq_workspace_bytes(depth, w.n))
+        if nb < 0:
+            raise ValueError(f"depth must be in [0, 3], got {depth}")
+        self.work = torch.zeros(nb, dtype=torch.uint8, device=device)  # the round's counters start at zero
+        self.logits = torch.empty((depth + 1, w.n), dtype=torch.float32, device=device)
+        self.out = torch.empty(depth + 5, dtype=torch.int32, device=device)
+
+    def run_async(self, x: torch.Tensor, draft: torch.Tensor, drafts: torch.Tensor,
+                  uniforms: torch.Tensor) -> torch.Tensor:
+        _check_x(x, self.w)
+        D, V = self.depth, self.w.n
+        if x.shape[0] != D + 1:
+            raise ValueError(f"x must hold {D + 1} rows")
+        if draft.dtype != torch.float32 or tuple(draft.shape) != (D, V) or not draft.is_contiguous():
+            raise ValueError(f"draft must be contiguous fp32 {(D, V)}")
+        if drafts.dtype != torch.int32 or drafts.numel() != D:
+            raise ValueError(f"drafts must be int32 [{D}]")
+        if uniforms.dtype != torch.float32 or uniforms.numel() != D + 1:
+            raise ValueError(f"uniforms must be fp32 [{D + 1}]")
+        _lib.check(_lib.lib().ssmoe_lm_head_pq(
+            x.data_ptr(), 1 if x.dtype == torch.float32 else 0, D, self.w.k, self.w.q.data_ptr(), self.w.s.data_ptr(),
+            self.w.b.data_ptr(), V, draft.data_ptr(), drafts.data_ptr(), uniforms.data_ptr(), self.temperature,
+            self.work.data_ptr(), self.work.numel(), self.logits.data_ptr(), self.out.data_ptr(), _lib.stream_of(x)))
+        return self.out
+
+    def __call__(self, x, draft, drafts, stream) -> AcceptResult:
+        """With the uniforms of a UniformStream (peeked, then advanced by the number the round used)."""
+        u = torch.from_numpy(stream.peek(self.depth + 1)).to(x.device)
+        res = AcceptResult.from_out(self.run_async(x, draft, drafts, u).cpu())
+        stream.advance(res.n_uniform)
+        return res

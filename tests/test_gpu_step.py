@@ -212,3 +212,27 @@ def test_chain_at_config4_layer_shape(T, NL4):
         assert np.array_equal(bits(sg.mixed[NL4]), mx)
         print(f"trial {trial}: unique experts per layer "
               f"{[len(set(sg.ids[l].cpu().flatten().tolist())) for l in range(NL4)]}", flush=True)
+
+
+def test_pq_round_in_the_step_graph(step):
+    """The round with p/q acceptance fused behind the lm_head (accept="pq"): its logits are the greedy graph's on the
+    same rows, and every replay's result equals ssmoe_accept_pq on those logits."""
+    from slotstream_spark_amd.engine.accept import Acceptor
+
+    pool, mw, lm, norms, sg = step
+    pq = MTPStepGraph(pool, mw[:NL], lm, depth=3, norm_weights=norms, top_k=K, accept="pq", temperature=0.7)
+    g = torch.Generator(device="cuda").manual_seed(461)
+    acc = Acceptor(3, V)
+    for rep in range(3):
+        x = normal_bf16((4, H), 1.0, 470 + rep)
+        sg.step(x, torch.zeros(3, dtype=torch.int32, device="cuda"))
+        torch.cuda.synchronize()
+        pq.draft_logits.copy_(0.8 * sg.logits[:3] + torch.randn((3, V), generator=g, device="cuda") * 1.8)
+        pq.uniforms.copy_(torch.rand(4, generator=g, device="cuda"))
+        drafts = pq.draft_logits.argmax(dim=1).to(torch.int32)
+        out = pq.step(x, drafts).clone()
+        torch.cuda.synchronize()
+        assert torch.equal(pq.logits, sg.logits), rep
+        want = acc.pq_async(sg.logits, pq.draft_logits, drafts, pq.uniforms, 0.7)
+        torch.cuda.synchronize()
+        assert torch.equal(out, want), (rep, out.cpu().tolist(), want.cpu().tolist())
