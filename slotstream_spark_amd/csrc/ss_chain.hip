@@ -58,7 +58,8 @@ __host__ __device__ inline CLayout clayout(int T, int H, int I, int Is, int K, i
 }
 
 // Dynamic LDS: per-expert partial dots | one region holding, in turn, the stream copy (x staging), the shared
-// expert's hs (before the routed down rows) and the staged h fragments | the x fragments, then the down prefetch.
+// expert's hs (before the routed down rows) and the staged h fragments | the x fragments and the layer's norm
+// weights, then the down prefetch.
 struct CDLayout {
   size_t part, hreg, pref, total, slot;
   int P, stage_h;
@@ -84,8 +85,8 @@ __host__ __device__ inline CDLayout cdlayout(int T, int H, int I, int Is, int K,
   int P = room > 0 ? (int)(room / (long)d.slot) : 0;
   if (P > nu_max) P = nu_max;
   d.P = P;
-  const size_t pb = (size_t)P * d.slot;
-  d.total = o + (pb > xf ? pb : xf);
+  const size_t pb = (size_t)P * d.slot, xw = xf + (size_t)H * 2;  // x fragments, then the norm weights
+  d.total = o + (pb > xw ? pb : xw);
   return d;
 }
 
@@ -93,7 +94,7 @@ __host__ __device__ inline CDLayout cdlayout(int T, int H, int I, int Is, int K,
 // bf16((x * r_t) * norm_w) when `norm` (r_t = 1 / sqrt(sum(x^2) / H + eps) of token t in the ssmoe_residual_rmsnorm
 // order): the operations of stage_x for bf16 x.
 template <int NJG>
-SS_DEV void stage_x_src(const uint16_t* src, bool norm, const uint16_t* norm_w, float eps, int H, uint4* xfl,
+SS_DEV void stage_x_src(const uint16_t* src, bool norm, const uint16_t* nw_lds, float eps, int H, uint4* xfl,
                         float (*gx)[kTBv], float* rnorm, int nt) {
   const int tid = threadIdx.x;
   constexpr int NJX = NJG / 4;
@@ -142,8 +143,8 @@ SS_DEV void stage_x_src(const uint16_t* src, bool norm, const uint16_t* norm_w, 
     auto scale8 = [&](uint4 v, float r, int k0) {
       const uint32_t x4[4] = {v.x, v.y, v.z, v.w};
       uint32_t o[4];
-      if (norm_w) {
-        const uint4 wv = ldg16(norm_w + k0);
+      if (nw_lds) {
+        const uint4 wv = *reinterpret_cast<const uint4*>(nw_lds + k0);
         const uint32_t w4[4] = {wv.x, wv.y, wv.z, wv.w};
 #pragma unroll
         for (int c = 0; c < 4; ++c)
@@ -257,8 +258,11 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   __shared__ VSmem s0;
   __shared__ int s_dead;
   __shared__ alignas(16) uint32_t s_next[64];  // the next layer's entry, read by a direct-to-LDS load
+  // Trace stamps of the last two layers, kept in LDS and written out at the exit, so that no stamp is a global
+  // store the next wait for memory would include.
+  __shared__ uint64_t s_tr[2][32];
   uint8_t* dl = reinterpret_cast<uint8_t*>(dsm);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int G = gridDim.x, bid = blockIdx.x;
   const int n = lane & 15, g = lane >> 4;
   const int T = a.T, H = a.H, I = a.I, K = a.K, E = a.E, Is = a.Is, NL = a.NL;
@@ -266,6 +270,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   uint8_t* scr = static_cast<uint8_t*>(a.scratch);
   int* ctr = reinterpret_cast<int*>(scr + L.ctr);
   if (tid == 0) s_dead = 0;
+  if (tid < 64) (&s_tr[0][0])[tid] = 0ull;
   __syncthreads();
   auto give_up = [&]() {
     if (lane == 0) {
@@ -296,9 +301,11 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   constexpr int NJX = NJG / 4;
   constexpr int NV = kMaxEv / 64;
   const int J = E + Is, W = G * 4;
-  // Router rows go to the workgroups without output rows: they finish a layer first, so the next layer's logits do
-  // not wait for the workgroups that write its stream.
-  const int j_first = ((bid + G - (H >> 4)) % G) * 4 + w;
+  // Jobs are dealt to the waves 0 and 1 of every workgroup first, then to the waves 2 and 3: at E = 2 G the router
+  // rows (one per wave) land on waves 0 and 1 and the shared rows (two per job) on waves 2 and 3, so a wave that
+  // runs a router tail (w < nt) has a one-row job for nt <= 2, the tails of all workgroups start as soon as the
+  // router rows are in, and the workgroups with output rows do not start their items later than the others.
+  const int j_first = 2 * bid + (w & 1) + (w >> 1) * 2 * G;
   const bool has_tile = bid < (H >> 4);
   const int tiles = I >> 3;
   const int my_half = g >> 1, my_part = g & 1;
@@ -335,14 +342,13 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       slot_e[k] = ok ? v : -1;
     }
   };
-  const uint8_t* base_k[2] = {nullptr, nullptr};
+  // The slot pointers are loaded without a select on the loaded value (an entry outside the table reads slot 0 and
+  // is cleared where the tables are written), so no wait for them follows the load.
+  int64_t base_k[2] = {0, 0};
+  auto slot_ok = [&](int k) { return slot_e[k] >= 0 && (int64_t)slot_e[k] < a.n_slots; };
   auto load_bases = [&]() {
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const bool ok = slot_e[k] >= 0 && (int64_t)slot_e[k] < a.n_slots;
-      const int64_t p = gp(a.slot_ptr)[ok ? slot_e[k] : 0];
-      base_k[k] = ok ? reinterpret_cast<const uint8_t*>(p) : nullptr;
-    }
+    for (int k = 0; k < 2; ++k) base_k[k] = gp(a.slot_ptr)[slot_ok(k) ? slot_e[k] : 0];
   };
   float bias_r[NV];
   auto load_bias = [&](const ssmoe_chain_layer& q) {
@@ -363,10 +369,10 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   for (int l = 0; l < NL; ++l) {
     const uint32_t tag = tag0 + (uint32_t)l;
     const bool tr = a.trace && l >= NL - 2;
-    const size_t trow = (size_t)(l == NL - 1 ? bid : 512 + bid) * 16;
-#define SS_TRACE(k)                                                                  \
-  do {                                                                               \
-    if (tr && tid == 0) a.trace[trow + (k)] = __builtin_amdgcn_s_memrealtime(); \
+    uint64_t* trs = s_tr[l == NL - 1 ? 1 : 0];  // stamps 0-15 go to the layer's row, 16-31 to its extra row
+#define SS_TRACE(k)                                                   \
+  do {                                                                \
+    if (tr && tid == 0) trs[(k)] = __builtin_amdgcn_s_memrealtime(); \
   } while (0)
     SS_TRACE(0);
     // Offsets of the dynamic LDS regions, made opaque to the compiler at every layer so that the LDS addresses
@@ -397,6 +403,11 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
     // register waits for it in between; wave 3 has no stores in flight at the end of a layer).
     if (l + 1 < NL && w == 3 && lane < kLayerDwords)
       dma4(reinterpret_cast<const uint32_t*>(a.more + l) + lane, s_next);
+    // The layer's norm weights go straight into LDS behind the x fragments (wave 2, waited for before the staging),
+    // so the staging that follows the stream's arrival reads no global memory.
+    uint16_t* nwl = reinterpret_cast<uint16_t*>(xfl + NJG * 16 * kTBv);
+    if (lp.norm_w && w == 2)
+      for (int i = 0; i < (H >> 9); ++i) dma16(lp.norm_w + 8 * (64 * i + lane), reinterpret_cast<uint8_t*>(nwl) + 1024 * i);
     for (int i = tid; i < kMaxQv * kTBv; i += 256) (&s.umask[0][0])[i] = 0u;
     if (tid < 4) s.zero_h[tid] = make_uint4(0u, 0u, 0u, 0u);
     if (tid == 0) s.nt = nt;
@@ -411,7 +422,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       const uint32_t want = tag - 1u;
       const int nw = nt * (H >> 1);
       uint32_t* dst = reinterpret_cast<uint32_t*>(scopy);
-      if (tr && tid == 0) a.trace[trow + 256 * 16 + 2] = __builtin_amdgcn_s_memrealtime();
+      SS_TRACE(16 + 2);
 #pragma unroll 1
       for (int k0 = 0; k0 < nw; k0 += 256 * 8) {
         uint64_t v[8];
@@ -423,9 +434,9 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
             v[k] = idx < nw ? ld_ag(src + idx) : 0ull;
             fresh = fresh && (idx >= nw || (uint32_t)(v[k] >> 32) == want);
           }
-          if (tr && tid == 0 && it == 0) a.trace[trow + 256 * 16 + 1] = __builtin_amdgcn_s_memrealtime();
+          if (it == 0) SS_TRACE(16 + 1);
           if (__all(fresh) || dead()) {
-            if (tr && tid == 0) a.trace[trow + 14] = (uint64_t)it;
+            if (tr && tid == 0) trs[14] = (uint64_t)it;
             break;
           }
           if (it >= kChainSpin) {
@@ -445,7 +456,8 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       xsrc = scopy;
       norm = true;
     }
-    stage_x_src<NJG>(xsrc, norm, lp.norm_w, a.eps, H, xfl, s.gx, s.rnorm, nt);
+    if (w == 2) __builtin_amdgcn_s_waitcnt(0);  // the norm weights have landed in LDS
+    stage_x_src<NJG>(xsrc, norm, lp.norm_w ? nwl : nullptr, a.eps, H, xfl, s.gx, s.rnorm, nt);
     // The residual stream value of the combine's (row, token), read before the shared region is reused.
     uint32_t xres = 0;
     if (has_tile && tid < 16 * kTBv && (tid & 3) < nt) xres = xsrc[(size_t)(tid & 3) * H + 16 * bid + (tid >> 2)];
@@ -481,6 +493,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
         }
       }
     }
+    SS_TRACE(16 + 4);
     // Router rows need no wait (their words carry the tag). A wave with shared rows publishes them once its own
     // stores are acknowledged: at once, or, for a wave that runs a router tail, after the tail (the shared rows are
     // first read after the items, so the tail does not wait for the acknowledgement).
@@ -503,7 +516,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
         const int e = tid + 256 * k;
         if (e < E) {
           s.map[e] = slot_e[k];
-          s.base_e[e] = base_k[k];
+          s.base_e[e] = slot_ok(k) ? reinterpret_cast<const uint8_t*>(base_k[k]) : nullptr;
         }
       }
     };
@@ -511,8 +524,9 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
     SS_TRACE(2);
 
     // ---------------------------------------------------------- phase B: router tail, unique experts
-    if (w < nt && !dead()) router_tail_wave(va, logits, tag, w, s, bias_r);
+    if (w < nt && !dead()) router_tail_wave(va, logits, tag, w, s, bias_r, tr && w == 0 ? trs + 24 : nullptr);
     if (w < nt) {
+      SS_TRACE(16 + 10);
       write_tables();
       publish_shared();
     }
@@ -540,111 +554,109 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
     if (wave_items) {
       const int m = lane & 15, at = m & 3, agrp = m >> 2, ahh = agrp >> 1, apart = agrp & 1;
       const bool a_act = ahh == (g >> 1) && at < nt && apart == 0;
-      float* xch = s.xch[w];
+      // One instantiation per token count (2 or 4 accumulators): the dots, row sums and SwiGLU of absent tokens are
+      // not formed.
+      auto run_items = [&](auto ntk_c) {
+        constexpr int NTK = decltype(ntk_c)::value;
 #pragma unroll 1
-      for (int item = gw; item < n_items; item += W) {
-        const int u = item / tiles, p = item - u * tiles;
-        const int r8 = 8 * p + (n & 7);
-        const uint8_t* base = s.base[u];
-        const uint8_t* wrow = base + (n < 8 ? rec.gw : rec.uw) + r8 * row_b + 16 * g;
-        const SS_G uint32_t* srow = (const SS_G uint32_t*)gp(base + (n < 8 ? rec.gs : rec.us) + r8 * sb_b);
-        const SS_G uint32_t* brow = (const SS_G uint32_t*)gp(base + (n < 8 ? rec.gb : rec.ub) + r8 * sb_b);
-        uint4 wv[NJG];
-        uint32_t sv[NJG], bv[NJG];
+        for (int item = gw; item < n_items; item += W) {
+          const int u = item / tiles, p = item - u * tiles;
+          const int r8 = 8 * p + (n & 7);
+          const uint8_t* base = s.base[u];
+          const uint8_t* wrow = base + (n < 8 ? rec.gw : rec.uw) + r8 * row_b + 16 * g;
+          const SS_G uint32_t* srow = (const SS_G uint32_t*)gp(base + (n < 8 ? rec.gs : rec.us) + r8 * sb_b);
+          const SS_G uint32_t* brow = (const SS_G uint32_t*)gp(base + (n < 8 ? rec.gb : rec.ub) + r8 * sb_b);
+          uint4 wv[NJG];
+          uint32_t sv[NJG], bv[NJG];
 #pragma unroll
-        for (int j = 0; j < NJG; ++j) {
-          wv[j] = ldg16(wrow + 64 * j);
-          sv[j] = srow[j];
-          bv[j] = brow[j];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        float acc[kTBv] = {0.f, 0.f, 0.f, 0.f};
-        constexpr int JB = NJG % 4 == 0 ? 4 : 1;
-#pragma unroll
-        for (int j0 = 0; j0 < NJG; j0 += JB) {
-          uint4 av4[JB][4];
-          float4 gxv[JB];
-#pragma unroll
-          for (int jj = 0; jj < JB; ++jj) {
-            const int j = j0 + jj;
-            const uint4* fp = a_act ? xfl + (size_t)(((j * 4) * 4 + g) * kTBv + at)
-                                    : reinterpret_cast<const uint4*>(s.hsum);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) av4[jj][i] = fp[(size_t)i * 16];
-            gxv[jj] = reinterpret_cast<const float4*>(s.gx)[2 * j + my_half];
+          for (int j = 0; j < NJG; ++j) {
+            wv[j] = ldg16(wrow + 64 * j);
+            sv[j] = srow[j];
+            bv[j] = brow[j];
           }
+          __builtin_amdgcn_sched_barrier(0);
+          float acc[NTK];
 #pragma unroll
-          for (int jj = 0; jj < JB; ++jj) {
-            const int j = j0 + jj;
-            ss_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+          for (int r = 0; r < NTK; ++r) acc[r] = 0.f;
+          constexpr int JB = NJG % 4 == 0 ? 4 : 1;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              ss_u32x4 av = as_v(av4[jj][i]);
-              const uint32_t wd = i == 0 ? wv[j].x : i == 1 ? wv[j].y : i == 2 ? wv[j].z : wv[j].w;
-              d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
+          for (int j0 = 0; j0 < NJG; j0 += JB) {
+            uint4 av4[JB][4];
+            float4 gxv[JB];
+#pragma unroll
+            for (int jj = 0; jj < JB; ++jj) {
+              const int j = j0 + jj;
+              const uint4* fp = a_act ? xfl + (size_t)(((j * 4) * 4 + g) * kTBv + at)
+                                      : reinterpret_cast<const uint4*>(s.hsum);
+#pragma unroll
+              for (int i = 0; i < 4; ++i) av4[jj][i] = fp[(size_t)i * 16];
+              gxv[jj] = reinterpret_cast<const float4*>(s.gx)[2 * j + my_half];
             }
-            const float sf = pick_half(sv[j], my_half);
-            const float bf = pick_half(bv[j], my_half);
-            const float s16 = sf * kNibbleScale;
-            const float bp = my_part ? 0.f : __builtin_fmaf(-kNibbleScale, sf, bf);
-            const float gxa[kTBv] = {gxv[jj].x, gxv[jj].y, gxv[jj].z, gxv[jj].w};
 #pragma unroll
-            for (int r = 0; r < kTBv; ++r) {
-              acc[r] = __builtin_fmaf(s16, d[r], acc[r]);
-              acc[r] = __builtin_fmaf(bp, gxa[r], acc[r]);
+            for (int jj = 0; jj < JB; ++jj) {
+              const int j = j0 + jj;
+              ss_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                ss_u32x4 av = as_v(av4[jj][i]);
+                const uint32_t wd = i == 0 ? wv[j].x : i == 1 ? wv[j].y : i == 2 ? wv[j].z : wv[j].w;
+                d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
+              }
+              const float sf = pick_half(sv[j], my_half);
+              const float bf = pick_half(bv[j], my_half);
+              const float s16 = sf * kNibbleScale;
+              const float bp = my_part ? 0.f : __builtin_fmaf(-kNibbleScale, sf, bf);
+              const float gxa[kTBv] = {gxv[jj].x, gxv[jj].y, gxv[jj].z, gxv[jj].w};
+#pragma unroll
+              for (int r = 0; r < NTK; ++r) {
+                acc[r] = __builtin_fmaf(s16, d[r], acc[r]);
+                acc[r] = __builtin_fmaf(bp, gxa[r], acc[r]);
+              }
             }
           }
-        }
+          // Every lane of column n now gets row n's dot of each token (gate row n for n < 8, up row n - 8 above),
+          // and the lanes n < 8 form h = silu(gate) * up of their row c = n from the up dot 8 lanes up: no LDS.
+          float hq[NTK];
 #pragma unroll
-        for (int r = 0; r < kTBv; ++r) {
-          acc[r] = ss_rows_sum(acc[r]);
-          if (g == 0) xch[n * kTBv + r] = acc[r];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        {
-          const int r = lane >> 3, c = lane & 7;
-          if (r < nt) {
-            const float gv = xch[c * kTBv + r], uv = xch[(c + 8) * kTBv + r];
-            xch[c * kTBv + r] = gv / (1.f + ss_expf(-gv)) * uv;
+          for (int r = 0; r < NTK; ++r) {
+            const float gd = ss_rows_sum(acc[r]);
+            const float ud = ss_uf(ss_xor_lane<8>(ss_fu(gd)));
+            hq[r] = gd / (1.f + ss_expf(-gd)) * ud;
           }
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        if (lane < nt) {
-          const int r = lane;
-          float hv[8];
-          float sum8 = 0.f;
-#pragma unroll
-          for (int c = 0; c < 8; ++c) {
-            hv[c] = xch[c * kTBv + r];
-            sum8 = sum8 + hv[c];
-          }
-          uint32_t hw[4], lw[4];
-#pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const uint32_t a0 = ss_f32_to_bf16(hv[d]), a1 = ss_f32_to_bf16(hv[d + 4]);
-            hw[d] = a0 | (a1 << 16);
-            lw[d] = ss_f32_to_bf16(hv[d] - ss_bf16_to_f32(a0)) |
-                    (ss_f32_to_bf16(hv[d + 4] - ss_bf16_to_f32(a1)) << 16);
-          }
-          const uint4 fhi = make_uint4(hw[0], hw[1], hw[2], hw[3]), flo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
           const int jf = p >> 4, gf = (p & 15) >> 2, ifr = p & 3;
-          uint32_t mk = s.umask[u][r];
-          while (mk) {
-            const int k = __ffs(mk) - 1;
-            mk &= mk - 1;
-            const int q = r * K + k;
-            uint4* fpo = hfrag + (((size_t)q * NJD + jf) * 4 + gf) * 8 + ifr;
-            st_ag16(fpo, fhi);
-            st_ag16(fpo + 4, flo);
-            st_ag(reinterpret_cast<uint32_t*>(hsum8) + (size_t)q * (I >> 3) + p, __float_as_uint(sum8));
+          const uint32_t mk_l = lane < nt ? s.umask[u][lane] : 0u;
+#pragma unroll
+          for (int r = 0; r < NTK; ++r) {
+            if (r >= nt) break;
+            uint32_t mk = (uint32_t)__builtin_amdgcn_readlane((int)mk_l, r);
+            if (!mk) continue;
+            // h of token r as bf16 high parts and bf16 residuals: lanes 0-3 hold word c of the high parts (rows c,
+            // c + 4), lanes 4-7 word c - 4 of the residuals; lane 8 the sequential sum of the 8 h values.
+            const float h = hq[r];
+            const uint32_t a0 = ss_f32_to_bf16(h), lo = ss_f32_to_bf16(h - ss_bf16_to_f32(a0));
+            const uint32_t a0p = ss_xor_lane<4>(a0), lop = ss_xor_lane<4>(lo);
+            const uint32_t word = n < 4 ? (a0 | (a0p << 16)) : (lop | (lo << 16));
+            float sum8 = 0.f;
+#pragma unroll
+            for (int c = 0; c < 8; ++c) sum8 = sum8 + ss_readlane_f(h, c);
+            while (mk) {
+              const int k = __ffs(mk) - 1;
+              mk &= mk - 1;
+              const int q = r * K + k;
+              uint32_t* fpo = reinterpret_cast<uint32_t*>(hfrag + (((size_t)q * NJD + jf) * 4 + gf) * 8 + ifr);
+              if (lane < 8)
+                st_ag(fpo + (lane < 4 ? lane : 12 + lane), word);
+              else if (lane == 8)
+                st_ag(reinterpret_cast<uint32_t*>(hsum8) + (size_t)q * (I >> 3) + p, __float_as_uint(sum8));
+            }
           }
+          if (item == gw) SS_TRACE(16 + 7);
         }
-        __builtin_amdgcn_wave_barrier();
-      }
+      };
+      if (nt <= 2)
+        run_items(std::integral_constant<int, 2>{});
+      else
+        run_items(std::integral_constant<int, kTBv>{});
       // Each wave publishes its own items as soon as its stores are acknowledged.
       stores_done();
       if (lane == 0) signal_add(ctr, CTR_ITEMS, wave_items);
@@ -844,7 +856,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
           for (int k = 0; k < KM; ++k)
             if (k < K) acc = k == 0 ? ov[k] : acc + ov[k];
           if (lp.routed_out) lp.routed_out[(size_t)r * H + 16 * bid + c] = acc;
-          if (tid == 0 && tr) a.trace[trow + 256 * 16 + 3] = __builtin_amdgcn_s_memrealtime();
+          SS_TRACE(16 + 3);
           for (int it = 0; (uint32_t)(shx_w >> 32) != tag; ++it) {
             if (dead()) break;
             if (it >= kChainSpin) {
@@ -854,7 +866,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
             __builtin_amdgcn_s_sleep(1);
             shx_w = ld_ag(shx + shx_i);
           }
-          if (tid == 0 && tr) a.trace[trow + 15] = __builtin_amdgcn_s_memrealtime();
+          SS_TRACE(15);
           const float sh2 = ss_bf16_to_f32((uint32_t)shx_w & 0xFFFFu);
           const uint32_t yb = ss_f32_to_bf16(ss_round_bf16(acc) + sh2);
           lp.y[(size_t)r * H + 16 * bid + c] = (uint16_t)yb;
@@ -870,7 +882,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       SS_TRACE(6);
       if (tr && tid == 0) {
         __builtin_amdgcn_s_waitcnt(0);
-        a.trace[trow + 256 * 16 + 0] = __builtin_amdgcn_s_memrealtime();
+        trs[16] = __builtin_amdgcn_s_memrealtime();
       }
     }
 
@@ -885,22 +897,6 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       load_map(ln);
       if (w < nt) load_bias(ln);
       lp = ln;
-      if (false) {
-        // Every expert record of the next layer is touched once per XCD (two reads per record: its start and its
-        // down piece), so that the address translations its items need are cached when its router decides. The
-        // workgroups without output rows are idle here until the stream arrives.
-        const int q = ((bid - (H >> 4)) >> 3) * 64 + lane;
-        const int e = q >> 1;
-        const int64_t mi = ln.layer * E + e;
-        if (e < E && mi >= 0 && mi < a.map_len) {
-          const int sl = gp(a.map)[mi];
-          if (sl >= 0 && (int64_t)sl < a.n_slots) {
-            const uint8_t* b = reinterpret_cast<const uint8_t*>(gp(a.slot_ptr)[sl]);
-            const uint32_t v = *reinterpret_cast<const SS_G uint32_t*>(gp(b + ((q & 1) ? rec.dw : 0)));
-            asm volatile("" ::"v"(v));
-          }
-        }
-      }
     }
     __syncthreads();
     SS_TRACE(11);
@@ -909,6 +905,12 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
 
   // ------------------------------------------------------------ exit: the last workgroup resets the counters
   __syncthreads();
+  if (a.trace && tid < 64) {
+    // Rows: last layer at bid, the layer before at 512 + bid; their extra stamps at 256 + bid and 768 + bid.
+    const int q = lane >> 5, k = lane & 31;
+    const size_t row = (size_t)(q ? 0 : 512) + (k < 16 ? 0 : 256) + bid;
+    if (NL - 2 + q >= 0) a.trace[row * 16 + (k & 15)] = s_tr[q][k];
+  }
   if (tid == 0) {
     const int sh = bid % kShards;
     const int in_shard = (G - sh + kShards - 1) / kShards;

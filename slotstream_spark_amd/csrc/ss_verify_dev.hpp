@@ -255,7 +255,7 @@ SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
 // the K dependent rounds of router_topk_kernel remain for the rows that path does not take. Both give the same
 // ids, and the weights are summed in rank order either way.
 SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32_t tag, int t, VSmem& s,
-                             const float (&bias_r)[kMaxEv / 64]) {
+                             const float (&bias_r)[kMaxEv / 64], uint64_t* stamps = nullptr) {
   const int lane = threadIdx.x & 63;
   const int E = a.E, K = a.K;
   constexpr int NV = kMaxEv / 64;
@@ -279,6 +279,7 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32
     __builtin_amdgcn_s_sleep(1);
   }
   if (a.trace && threadIdx.x == 0) a.trace[(size_t)blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();  // logits in
+  if (stamps && lane == 0) stamps[0] = __builtin_amdgcn_s_memrealtime();
   float v[NV];
 #pragma unroll
   for (int i = 0; i < NV; ++i) v[i] = ss_bf16_to_f32((uint16_t)wv[i]);
@@ -305,6 +306,7 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32
     v[i] = v[i] / z;
     kp[i] = lane + 64 * i < E ? ss_key(v[i]) + 1u : 0u;
   }
+  if (stamps && lane == 0) stamps[1] = __builtin_amdgcn_s_memrealtime();
   // tau: the largest threshold with zero low 16 bits that at least K lane maxima reach. Those K entries are >= tau,
   // so every entry of the top K is too. The entries >= tau (a few more than K on router rows) go to LDS in index
   // order as (kp << 32 | 0xFFFF - e), a key whose order is the selection order; each candidate's rank is the number
