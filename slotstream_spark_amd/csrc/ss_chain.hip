@@ -301,11 +301,9 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   constexpr int NJX = NJG / 4;
   constexpr int NV = kMaxEv / 64;
   const int J = E + Is, W = G * 4;
-  // Jobs are dealt to the waves 0 and 1 of every workgroup first, then to the waves 2 and 3: at E = 2 G the router
-  // rows (one per wave) land on waves 0 and 1 and the shared rows (two per job) on waves 2 and 3, so a wave that
-  // runs a router tail (w < nt) has a one-row job for nt <= 2, the tails of all workgroups start as soon as the
-  // router rows are in, and the workgroups with output rows do not start their items later than the others.
-  const int j_first = 2 * bid + (w & 1) + (w >> 1) * 2 * G;
+  // Router rows go to the workgroups without output rows: they finish a layer first, so the next layer's logits do
+  // not wait for the workgroups that write its stream.
+  const int j_first = ((bid + G - (H >> 4)) % G) * 4 + w;
   const bool has_tile = bid < (H >> 4);
   const int tiles = I >> 3;
   const int my_half = g >> 1, my_part = g & 1;
@@ -614,41 +612,95 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
               }
             }
           }
-          // Every lane of column n now gets row n's dot of each token (gate row n for n < 8, up row n - 8 above),
-          // and the lanes n < 8 form h = silu(gate) * up of their row c = n from the up dot 8 lanes up: no LDS.
-          float hq[NTK];
+          if constexpr (NTK == 2) {
+            // Every lane of column n now gets row n's dot of each token (gate row n for n < 8, up row n - 8 above),
+            // and the lanes n < 8 form h = silu(gate) * up of their row c = n from the up dot 8 lanes up: no LDS.
+            float hq[NTK];
 #pragma unroll
-          for (int r = 0; r < NTK; ++r) {
-            const float gd = ss_rows_sum(acc[r]);
-            const float ud = ss_uf(ss_xor_lane<8>(ss_fu(gd)));
-            hq[r] = gd / (1.f + ss_expf(-gd)) * ud;
-          }
-          const int jf = p >> 4, gf = (p & 15) >> 2, ifr = p & 3;
-          const uint32_t mk_l = lane < nt ? s.umask[u][lane] : 0u;
-#pragma unroll
-          for (int r = 0; r < NTK; ++r) {
-            if (r >= nt) break;
-            uint32_t mk = (uint32_t)__builtin_amdgcn_readlane((int)mk_l, r);
-            if (!mk) continue;
-            // h of token r as bf16 high parts and bf16 residuals: lanes 0-3 hold word c of the high parts (rows c,
-            // c + 4), lanes 4-7 word c - 4 of the residuals; lane 8 the sequential sum of the 8 h values.
-            const float h = hq[r];
-            const uint32_t a0 = ss_f32_to_bf16(h), lo = ss_f32_to_bf16(h - ss_bf16_to_f32(a0));
-            const uint32_t a0p = ss_xor_lane<4>(a0), lop = ss_xor_lane<4>(lo);
-            const uint32_t word = n < 4 ? (a0 | (a0p << 16)) : (lop | (lo << 16));
-            float sum8 = 0.f;
-#pragma unroll
-            for (int c = 0; c < 8; ++c) sum8 = sum8 + ss_readlane_f(h, c);
-            while (mk) {
-              const int k = __ffs(mk) - 1;
-              mk &= mk - 1;
-              const int q = r * K + k;
-              uint32_t* fpo = reinterpret_cast<uint32_t*>(hfrag + (((size_t)q * NJD + jf) * 4 + gf) * 8 + ifr);
-              if (lane < 8)
-                st_ag(fpo + (lane < 4 ? lane : 12 + lane), word);
-              else if (lane == 8)
-                st_ag(reinterpret_cast<uint32_t*>(hsum8) + (size_t)q * (I >> 3) + p, __float_as_uint(sum8));
+            for (int r = 0; r < NTK; ++r) {
+              const float gd = ss_rows_sum(acc[r]);
+              const float ud = ss_uf(ss_xor_lane<8>(ss_fu(gd)));
+              hq[r] = gd / (1.f + ss_expf(-gd)) * ud;
             }
+            const int jf = p >> 4, gf = (p & 15) >> 2, ifr = p & 3;
+            const uint32_t mk_l = lane < nt ? s.umask[u][lane] : 0u;
+#pragma unroll
+            for (int r = 0; r < NTK; ++r) {
+              if (r >= nt) break;
+              uint32_t mk = (uint32_t)__builtin_amdgcn_readlane((int)mk_l, r);
+              if (!mk) continue;
+              // h of token r as bf16 high parts and bf16 residuals: lanes 0-3 hold word c of the high parts (rows c,
+              // c + 4), lanes 4-7 word c - 4 of the residuals; lane 8 the sequential sum of the 8 h values.
+              const float h = hq[r];
+              const uint32_t a0 = ss_f32_to_bf16(h), lo = ss_f32_to_bf16(h - ss_bf16_to_f32(a0));
+              const uint32_t a0p = ss_xor_lane<4>(a0), lop = ss_xor_lane<4>(lo);
+              const uint32_t word = n < 4 ? (a0 | (a0p << 16)) : (lop | (lo << 16));
+              float sum8 = 0.f;
+#pragma unroll
+              for (int c = 0; c < 8; ++c) sum8 = sum8 + ss_readlane_f(h, c);
+              while (mk) {
+                const int k = __ffs(mk) - 1;
+                mk &= mk - 1;
+                const int q = r * K + k;
+                uint32_t* fpo = reinterpret_cast<uint32_t*>(hfrag + (((size_t)q * NJD + jf) * 4 + gf) * 8 + ifr);
+                if (lane < 8)
+                  st_ag(fpo + (lane < 4 ? lane : 12 + lane), word);
+                else if (lane == 8)
+                  st_ag(reinterpret_cast<uint32_t*>(hsum8) + (size_t)q * (I >> 3) + p, __float_as_uint(sum8));
+              }
+            }
+          } else {
+            // more tokens: the SwiGLU and h packing through the wave's LDS rows (one (token, row) per lane)
+            float* xch = s.xch[w];
+#pragma unroll
+            for (int r = 0; r < NTK; ++r) {
+              acc[r] = ss_rows_sum(acc[r]);
+              if (g == 0) xch[n * kTBv + r] = acc[r];
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            {
+              const int r = lane >> 3, c = lane & 7;
+              if (r < nt) {
+                const float gv = xch[c * kTBv + r], uv = xch[(c + 8) * kTBv + r];
+                xch[c * kTBv + r] = gv / (1.f + ss_expf(-gv)) * uv;
+              }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (lane < nt) {
+              const int r = lane;
+              float hv[8];
+              float sum8 = 0.f;
+#pragma unroll
+              for (int c = 0; c < 8; ++c) {
+                hv[c] = xch[c * kTBv + r];
+                sum8 = sum8 + hv[c];
+              }
+              uint32_t hw[4], lw[4];
+#pragma unroll
+              for (int d = 0; d < 4; ++d) {
+                const uint32_t a0 = ss_f32_to_bf16(hv[d]), a1 = ss_f32_to_bf16(hv[d + 4]);
+                hw[d] = a0 | (a1 << 16);
+                lw[d] = ss_f32_to_bf16(hv[d] - ss_bf16_to_f32(a0)) |
+                        (ss_f32_to_bf16(hv[d + 4] - ss_bf16_to_f32(a1)) << 16);
+              }
+              const uint4 fhi = make_uint4(hw[0], hw[1], hw[2], hw[3]), flo = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+              const int jf = p >> 4, gf = (p & 15) >> 2, ifr = p & 3;
+              uint32_t mk = s.umask[u][r];
+              while (mk) {
+                const int k = __ffs(mk) - 1;
+                mk &= mk - 1;
+                const int q = r * K + k;
+                uint4* fpo = hfrag + (((size_t)q * NJD + jf) * 4 + gf) * 8 + ifr;
+                st_ag16(fpo, fhi);
+                st_ag16(fpo + 4, flo);
+                st_ag(reinterpret_cast<uint32_t*>(hsum8) + (size_t)q * (I >> 3) + p, __float_as_uint(sum8));
+              }
+            }
+            __builtin_amdgcn_wave_barrier();
           }
           if (item == gw) SS_TRACE(16 + 7);
         }
