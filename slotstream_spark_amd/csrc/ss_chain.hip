@@ -247,9 +247,10 @@ SS_DEV ssmoe_chain_layer layer_from_lds(const uint32_t* lds) {
 
 size_t chain_scratch_bytes(int T, int H, int I, int Is, int K, int E) { return clayout(T, H, I, Is, K, E).total; }
 
-// A wait of the chain kernel gives up after kChainSpin polls (each a memory round trip plus a short sleep, well under
-// a second in all), raises SS_ERR_TIMEOUT and marks the workgroup dead: every later wait of that workgroup returns at
-// once, so a launch whose hand-offs failed still ends within about a second.
+// A wait of the chain kernel gives up after kChainSpin polls (each a memory round trip, well under a second in all),
+// raises SS_ERR_TIMEOUT and marks the workgroup dead: every later wait of that workgroup returns at once, so a launch
+// whose hand-offs failed still ends within about a second. The polls do not sleep between round trips: measured on
+// MI355X, the hand-offs complete about 0.15 us sooner per layer than with a short sleep in each poll.
 constexpr int kChainSpin = 1 << 18;
 
 template <int NJG, int NJD>
@@ -291,7 +292,6 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
         give_up();
         break;
       }
-      __builtin_amdgcn_s_sleep(1);
     }
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
   };
@@ -441,7 +441,6 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
             give_up();
             break;
           }
-          __builtin_amdgcn_s_sleep(1);
         }
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
@@ -915,7 +914,6 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
               ss_raise(a.err, SS_ERR_TIMEOUT);
               break;
             }
-            __builtin_amdgcn_s_sleep(1);
             shx_w = ld_ag(shx + shx_i);
           }
           SS_TRACE(15);

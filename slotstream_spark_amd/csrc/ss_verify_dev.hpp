@@ -276,7 +276,6 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32
       if (lane == 0) ss_raise(a.err, SS_ERR_TIMEOUT);
       break;
     }
-    __builtin_amdgcn_s_sleep(1);
   }
   if (a.trace && threadIdx.x == 0) a.trace[(size_t)blockIdx.x * 16 + 5] = __builtin_amdgcn_s_memrealtime();  // logits in
   if (stamps && lane == 0) stamps[0] = __builtin_amdgcn_s_memrealtime();
