@@ -3,8 +3,8 @@
     python -m slotstream_spark_amd.chain_trace [T] [layers]
 
 Builds a chain of `layers` (default 16) config-1 MoE layers (H 2048, 512 experts top-10, I 512, shared 512,
-affine-4bit gs64, Zipf 1.1 routing bias) with seeded synthetic weights, times the step graph (HIP events over 20
-steps), then runs one eager launch with the trace on and prints, for the last two layers, the median and maximum
+affine-4bit gs64, Zipf 1.1 routing bias) with seeded synthetic weights, times the step graph (HIP events, median of
+5 x 40 steps), then runs one eager launch with the trace on and prints, for the last two layers, the median and maximum
 time of each stamp over the workgroups that own output rows ("tile") and the others ("free"), in us from the first
 start of the layer before the last. The stamps are kept in LDS by the kernel and written at its exit.
 """
@@ -40,13 +40,17 @@ def run(T: int = 2, nl: int = 16) -> str:
     for i in range(4):
         sg.step(xs[i % 8])
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for i in range(20):
-        sg.step(xs[i % 8])
-    e1.record()
-    torch.cuda.synchronize()
-    out = [f"T={T}: {e0.elapsed_time(e1) * 1000 / 20 / nl:.2f} us per layer (step graph, 20 steps)"]
+    per_layer = []
+    for _ in range(5):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(40):
+            sg.step(xs[i % 8])
+        e1.record()
+        torch.cuda.synchronize()
+        per_layer.append(e0.elapsed_time(e1) * 1000 / 40 / nl)
+    per_layer.sort()
+    out = [f"T={T}: {per_layer[2]:.2f} us per layer (step graph; median of 5 x 40 steps, min {per_layer[0]:.2f})"]
     buf = torch.zeros(1024 * 16, dtype=torch.int64, device="cuda")
     _lib.check(_lib.lib().ssmoe_set_trace(buf.data_ptr(), buf.numel()))
     try:
