@@ -152,6 +152,7 @@ struct PrefillArgs {
   float* out_rows;              // fp32 [R, H]
   int64_t R;
   int T, H, I;                  // T: rows of x (a row_token outside [0, T) reads zeros)
+  uint64_t* trace = nullptr;    // diagnostics: per-block stamps of the two GEMMs (16384 entries), or null
 };
 hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st);
 // out[t] = sum over k (in order) of rows[t * K + k]; a row whose row_local entry is negative counts as +0.

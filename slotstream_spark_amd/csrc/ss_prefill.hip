@@ -13,6 +13,7 @@
 //  * combine: out[t] = ((o[t,0] + o[t,1]) + ...) + o[t,K-1], sequential fp32.
 // Tiles are constants of the kernel (128 rows x 256 weight rows x 64 K), never functions of R.
 #include <type_traits>
+#include <utility>
 
 #include "ss_common.hpp"
 #include "ss_launch.hpp"
@@ -279,6 +280,7 @@ struct GemmArgs {
   int T, H, I;
   int64_t w_off, s_off, b_off;     // gate (or down) pieces
   int64_t w2_off, s2_off, b2_off;  // up pieces (gate/up)
+  uint64_t* trace;                 // per-block stamps (start, end, expert << 32 | valid rows, XCC << 32 | HW_ID) or null
 };
 
 // LDS barrier for data exchanged through LDS only: waits for this wave's LDS operations, not for its global loads
@@ -310,39 +312,54 @@ SS_DEV int a_pos(int m, int c) { return c ^ (m & 7) ^ ((m >> 3) & 1); }
 // Local index of weight row (fragment j, lane row n) of wave w: 64 w + 16 j + n; the (s, b) table row stride is
 // G + 1 dwords, so 16 consecutive rows at one group fall on distinct banks.
 
-// The K loop for NF live 16-row fragments (fragments NF .. 7 are all padding and get no MFMAs).
-template <int NF>
+// f(integral_constant<int, 0>), ..., f(integral_constant<int, N - 1>), in order.
+template <typename F, int... I>
+SS_DEV void ss_static_for_seq(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+SS_DEV void ss_static_for(F&& f) {
+  ss_static_for_seq(f, std::make_integer_sequence<int, N>{});
+}
+
+// The K loop for NF live 16-row fragments (fragments NF .. 7 are all padding and get no loads or MFMAs), with the
+// global loads of step k + PD issued at the end of step k into register slot k % PD: the packed weights are PD steps
+// ahead of their use, the A rows PD - 1 steps ahead of their LDS store (two LDS stages). Blocks with fewer live rows
+// hold fewer accumulators, so they afford a deeper register ring (their steps are shorter, so they need it more).
+// Thread t stages A rows t / 8 + 32 c (c < NF / 2), 16-byte chunk t % 8.
+template <int NF, int PD>
 SS_DEV void gemm_loop(uint8_t* lds, const uint32_t* sbt, int nsteps, int aoff0, int aoff1, ss_f32x4 (&acc)[8][4],
                       const uint16_t* const (&asrc)[4], int arow0, int achunk, const uint8_t* wbase,
                       const int64_t (&wc)[4], uint32_t lw, int sb_lane, int sb_stride) {
-  uint4 areg[4];
-  auto load_a = [&](int k) {
+  static_assert(PD % 2 == 0, "the LDS stage of step k is k & 1 = (k % PD) & 1");
+  constexpr int NA = NF / 2;
+  uint4 areg[PD][NA];
+  ss_u32x2 bw[PD][4];
+  // Loads of step k (the last step again past the end: never used) into register slot S.
+  auto load = [&](int k, auto slot_c) {
+    constexpr int S = decltype(slot_c)::value;
+    const int kk = k < nsteps ? k : nsteps - 1;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) areg[c] = ldg16(asrc[c] + (size_t)k * kBK);
+    for (int c = 0; c < NA; ++c) areg[S][c] = ldg16(asrc[c] + (size_t)kk * kBK);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) bw[S][j] = *(const SS_G ss_u32x2*)(wbase + wc[j] + lw + 32 * kk);
   };
-  auto store_a = [&](int stage) {
+  auto store_a = [&](auto slot_c, int stage) {
+    constexpr int S = decltype(slot_c)::value;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int m = arow0 + 8 * c;
-      *reinterpret_cast<uint4*>(lds + stage * kAStage + m * (kBK * 2) + 16 * a_pos(m, achunk)) = areg[c];
+    for (int c = 0; c < NA; ++c) {
+      const int m = arow0 + 32 * c;
+      *reinterpret_cast<uint4*>(lds + stage * kAStage + m * (kBK * 2) + 16 * a_pos(m, achunk)) = areg[S][c];
     }
   };
-  ss_u32x2 bw[2][4];
-  auto load_b = [&](int k, const int slot) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bw[slot][j] = *(const SS_G ss_u32x2*)(wbase + wc[j] + lw + 32 * k);
-  };
-  load_a(0);
-  load_b(0, 0);
-  store_a(0);
-  load_a(1);
-  load_b(1, 1);
+  ss_static_for<PD>([&](auto p) { load(decltype(p)::value, p); });
+  store_a(std::integral_constant<int, 0>{}, 0);
   lds_barrier();
-  // One K step on register slot SLOT (= k & 1, a constant so that both slots stay in fixed registers and every wait
-  // the compiler inserts covers exactly the loads of this step).
+  // One K step from register slot S (= k % PD) and LDS stage S & 1; then A of step k + 1 into the other stage, the
+  // loads of step k + PD into slot S, and the barrier.
   auto step = [&](int k, auto slot_c) {
-    constexpr int SLOT = decltype(slot_c)::value;
-    const uint8_t* st = lds + SLOT * kAStage;
+    constexpr int S = decltype(slot_c)::value;
+    const uint8_t* st = lds + (S & 1) * kAStage;
     float sc[4], bi[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -354,7 +371,7 @@ SS_DEV void gemm_loop(uint8_t* lds, const uint32_t* sbt, int nsteps, int aoff0, 
     for (int s = 0; s < 2; ++s) {
       ss_u32x4 bf[4];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) bf[j] = dequant8(s ? bw[SLOT][j].y : bw[SLOT][j].x, sc[j], bi[j]);
+      for (int j = 0; j < 4; ++j) bf[j] = dequant8(s ? bw[S][j].y : bw[S][j].x, sc[j], bi[j]);
       const uint8_t* ap = st + (s ? aoff1 : aoff0);
       // A fragments in batches of up to four: one LDS wait per batch. The scheduling barriers keep one slice's
       // operands live at a time (the register budget of two waves per SIMD); the two waves of a SIMD overlap one
@@ -374,18 +391,15 @@ SS_DEV void gemm_loop(uint8_t* lds, const uint32_t* sbt, int nsteps, int aoff0, 
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    // The steps past the end reload the last one (never used): every iteration issues the same loads.
-    store_a(SLOT ^ 1);
-    const int kn = k + 2 < nsteps ? k + 2 : nsteps - 1;
-    load_a(kn);
-    load_b(kn, SLOT);
+    store_a(std::integral_constant<int, (S + 1) % PD>{}, (S & 1) ^ 1);
+    load(k + PD, slot_c);
     lds_barrier();
   };
 #pragma unroll 1
-  for (int k = 0; k < nsteps; k += 2) {
-    step(k, std::integral_constant<int, 0>{});
-    step(k + 1, std::integral_constant<int, 1>{});
-  }
+  for (int k = 0; k < nsteps; k += PD)
+    ss_static_for<PD>([&](auto u) {
+      if (k + decltype(u)::value < nsteps) step(k + decltype(u)::value, u);
+    });
 }
 
 template <bool GATE_UP>
@@ -401,6 +415,7 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs g, int nt
   if (!xcd_tile(mb, nt, pid_m, pid_n)) return;
   const int e = g.block_expert[pid_m];
   if (e < 0) return;
+  const uint64_t t_start = g.trace ? __builtin_amdgcn_s_memrealtime() : 0;
   const uint8_t* base = reinterpret_cast<const uint8_t*>(g.group_ptr[e]);
   const int kdim = GATE_UP ? g.H : g.I;
   const int G = kdim / 64, sb_stride = G + 1;
@@ -460,14 +475,15 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs g, int nt
   // Valid rows are a prefix of the block (each expert's rows come first in its padded range).
   const int nvalid = __syncthreads_count(valid);
 
-  // A staging: load instruction c of thread (w, lane) covers row arow0 + 8 c (arow0 = 32 w + (lane >> 3)), 16-byte
-  // chunk lane & 7. A padding row or a zero row reads the first kdim elements of the expert record (always
-  // present): a padding row's MFMA output row is never stored, and a zero row's h is stored as 0 (silu(0) * 0).
-  const int arow0 = 32 * w + (lane >> 3), achunk = lane & 7;
+  // A staging: load instruction c of thread t covers row arow0 + 32 c (arow0 = t / 8), 16-byte chunk t % 8 (each
+  // instruction of a wave covers 8 whole 128-byte rows). A padding row or a zero row reads the first kdim elements
+  // of the expert record (always present): a padding row's MFMA output row is never stored, and a zero row's h is
+  // stored as 0 (silu(0) * 0).
+  const int arow0 = tid >> 3, achunk = tid & 7;
   const uint16_t* asrc[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) {
-    const int m = arow0 + 8 * c;
+    const int m = arow0 + 32 * c;
     const int64_t off = a_off[m];
     asrc[c] = (m < nvalid && off >= 0 ? g.a + off : reinterpret_cast<const uint16_t*>(base)) + 8 * achunk;
   }
@@ -496,13 +512,13 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs g, int nt
   const int nsteps = kdim / kBK;  // even: kdim is a multiple of 128
   const int nf2 = (nvalid + 31) >> 5;  // live fragment pairs (1..4)
   if (nf2 >= 4)
-    gemm_loop<8>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
+    gemm_loop<8, 2>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
   else if (nf2 == 3)
-    gemm_loop<6>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
+    gemm_loop<6, 2>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
   else if (nf2 == 2)
-    gemm_loop<4>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
+    gemm_loop<4, 4>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
   else
-    gemm_loop<2>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
+    gemm_loop<2, 4>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
 
   if (GATE_UP) {
     // h = bf16(silu(g) * u) into an LDS tile [128 rows][128 columns], then 16-byte row-contiguous stores.
@@ -549,6 +565,18 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs g, int nt
         }
       }
   }
+  // Diagnostics: gate/up blocks at entries [0, 8192), down blocks at [8192, 16384), four per block.
+  if (g.trace && tid == 0) {
+    const size_t at = (GATE_UP ? 0 : 8192) + 4 * (size_t)blockIdx.x;
+    if (at + 4 <= (GATE_UP ? 8192u : 16384u)) {
+      const uint32_t hw = __builtin_amdgcn_s_getreg(4 | (31 << 11));   // HW_ID
+      const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (31 << 11)); // XCC_ID
+      g.trace[at] = t_start;
+      g.trace[at + 1] = __builtin_amdgcn_s_memrealtime();
+      g.trace[at + 2] = ((uint64_t)(uint32_t)e << 32) | (uint32_t)nvalid;
+      g.trace[at + 3] = ((uint64_t)xcc << 32) | hw;
+    }
+  }
 }
 
 hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
@@ -569,6 +597,7 @@ hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
   g.T = p.T;
   g.H = p.H;
   g.I = p.I;
+  g.trace = p.trace;
   g.a = p.x;
   g.w_off = rec.gw;
   g.s_off = rec.gs;

@@ -582,6 +582,7 @@ int ssmoe_fused_moe_affine(const uint16_t* x, const int32_t* row_token, const fl
   p.T = T;
   p.H = H;
   p.I = I;
+  p.trace = g_trace;
   return hip_check(ss::launch_prefill_gemm(p, static_cast<hipStream_t>(stream)), "fused_moe_affine launch");
 }
 
@@ -686,6 +687,7 @@ int ssmoe_moe_prefill(const uint16_t* x, const int32_t* expert_ids, const float*
   p.T = (int)T;
   p.H = H;
   p.I = I;
+  p.trace = g_trace;
   if (int rc = hip_check(ss::launch_prefill_gemm(p, st), "prefill gemm launch")) return rc;
   return hip_check(ss::launch_combine(out_rows, local, (int)T, K, H, out, st), "combine launch");
 }
