@@ -291,19 +291,18 @@ SS_DEV void lds_barrier() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
-// Block index -> (M block, N tile). The plan's M blocks times the N tiles are split into 8 contiguous ranges, one
-// per XCD (workgroups are dealt to the XCDs round-robin, b % 8): the M blocks of one expert, which share its
-// weights, and the N tiles of one M block, which share its activation rows, stay on one XCD and its L2.
+// Block index -> (M block, N tile). The plan's M blocks are dealt round-robin to the XCDs (workgroup b runs on XCD
+// b % 8), in plan order, so every XCD gets an even share of the heavy and the light experts' blocks (the mix also
+// pairs MFMA-bound full blocks with VALU-bound partial ones on a CU); each XCD takes all N tiles of one M block in a
+// row (they share its activation rows in the XCD's L2). Measured on MI355X at BASELINE config 3, this beats both
+// contiguous per-XCD ranges of the plan (XCDs ending 140-180 us apart) and a full-blocks-first order (full blocks
+// sharing a CU slow each other down).
 SS_DEV bool xcd_tile(int mb, int nt, int& pid_m, int& pid_n) {
-  const int b = blockIdx.x;
-  const int total = mb * nt;
-  const int per = (total + 7) >> 3;
-  const int slot = b >> 3;
-  const int L = (b & 7) * per + slot;
-  if (slot >= per || L >= total) return false;
-  pid_m = L / nt;
-  pid_n = L - pid_m * nt;
-  return true;
+  const int b = blockIdx.x, x = b & 7, s = b >> 3;
+  const int sm = s / nt;
+  pid_m = sm * 8 + x;
+  pid_n = s - sm * nt;
+  return pid_m < mb;
 }
 
 // 16-byte chunk c of A row m sits at chunk position a_pos(m, c) of the row's 128 bytes.
@@ -605,8 +604,8 @@ hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
   g.w2_off = rec.uw;
   g.s2_off = rec.us;
   g.b2_off = rec.ub;
-  // Grids cover the plan's upper bound of M blocks, rounded to whole XCD rounds; blocks past the device-side
-  // count exit at once.
+  // Grids cover the plan's upper bound of M blocks (rounded up to a multiple of 8) times the N tiles; blocks past
+  // the device-side count exit at once.
   KernelCfg cfg;
   hipError_t e = kernel_cfg(reinterpret_cast<const void*>(prefill_gemm_kernel<true>), 256, kGemmLdsMax, &cfg);
   if (e == hipSuccess)
@@ -614,7 +613,7 @@ hipError_t launch_prefill_gemm(const PrefillArgs& p, hipStream_t st) {
   if (e != hipSuccess) return e;
   const int64_t mb = P / kBM;
   const int nt_gu = p.I / kGateUpTileN, nt_d = p.H / kDownTileN;
-  auto grid_of = [&](int nt) { return (unsigned)(((mb * nt + 7) / 8) * 8); };
+  auto grid_of = [&](int nt) { return (unsigned)(8 * nt * ((mb + 7) / 8)); };
   hipLaunchKernelGGL(prefill_gemm_kernel<true>, dim3(grid_of(nt_gu)), dim3(256), gemm_lds_bytes(p.H / 64), st, g,
                      nt_gu);
   g.a = p.h_buf;
