@@ -362,7 +362,7 @@ SS_DEV void gemm_loop(uint8_t* lds, const uint32_t* sbt, int nsteps, int aoff0, 
     float sc[4], bi[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t sb = sbt[sb_lane + 16 * j * sb_stride + k];
+      const uint32_t sb = sbt[sb_lane + j * sb_stride + k];
       sc[j] = __uint_as_float(sb << 16) * 512.f;  // s * 2^9, exact
       bi[j] = __uint_as_float(sb & 0xFFFF0000u);
     }
@@ -435,13 +435,15 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs g, int nt
     out_row[tid] = valid ? r : -1;
     if (!GATE_UP) wt_s[tid] = valid ? g.row_weight[r] : 0.f;
   }
-  // Global weight row of local row lr (0 .. 255) and its piece: gate/up local rows 64 w + 16 j + n map to gate rows
-  // (j < 2) or up rows (j >= 2) n0 + 32 w + 16 (j & 1) + n; down local rows are rows n0 + lr.
+  // Column n of B fragment j of wave w is local weight row lr = 64 w + 4 n + j, so a lane's four fragments hold four
+  // adjacent outputs. Global weight row of local row lr and its piece: gate/up local rows map to gate rows (j < 2)
+  // or up rows (j >= 2) n0 + 32 w + 2 n + (j & 1), so g and u of one h column sit in one lane (fragments j and
+  // j + 2) and its two h columns are adjacent; down local rows are rows n0 + lr.
   auto grow = [&](int lr, bool& up) -> int64_t {
     if (GATE_UP) {
-      const int ww = lr >> 6, j = (lr >> 4) & 3, nn = lr & 15;
+      const int ww = lr >> 6, nn = (lr >> 2) & 15, j = lr & 3;
       up = j >= 2;
-      return (int64_t)pid_n * kGateUpTileN + 32 * ww + 16 * (j & 1) + nn;
+      return (int64_t)pid_n * kGateUpTileN + 32 * ww + 2 * nn + (j & 1);
     }
     up = false;
     return (int64_t)pid_n * kDownTileN + lr;
@@ -493,11 +495,12 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs g, int nt
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     bool up;
-    const int64_t row0 = grow(64 * w + 16 * j, up);
+    const int64_t row0 = grow(64 * w + j, up);
     wc[j] = (up ? g.w2_off : g.w_off) + row0 * wrow_b;
   }
-  const uint32_t lw = (uint32_t)(n * wrow_b + 8 * q);
-  const int sb_lane = (64 * w + n) * sb_stride;
+  // lane row n is weight row row0 + 2 n (gate/up) or row0 + 4 n (down) of its fragment
+  const uint32_t lw = (uint32_t)((GATE_UP ? 2 : 4) * n * wrow_b + 8 * q);
+  const int sb_lane = (64 * w + 4 * n) * sb_stride;
 
   ss_f32x4 acc[8][4];
 #pragma unroll
@@ -520,49 +523,60 @@ __global__ __launch_bounds__(256, 2) void prefill_gemm_kernel(GemmArgs g, int nt
     gemm_loop<2, 4>(lds, sbt, nsteps, aoff0, aoff1, acc, asrc, arow0, achunk, base, wc, lw, sb_lane, sb_stride);
 
   if (GATE_UP) {
-    // h = bf16(silu(g) * u) into an LDS tile [128 rows][128 columns], then 16-byte row-contiguous stores.
-    uint16_t* ht = reinterpret_cast<uint16_t*>(lds);
+    // h = bf16(silu(g) * u) of the live fragments into an LDS tile [128 rows][128 columns] (a lane's two adjacent
+    // columns as one dword), then 16-byte row-contiguous stores of the valid rows.
+    uint32_t* ht = reinterpret_cast<uint32_t*>(lds);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i) {
+      if (i >= 2 * nf2) break;
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int r = 0; r < 4; ++r) {
+        const int m = 16 * i + 4 * q + r;
+        const bool live = a_off[m] >= 0;
+        uint32_t hp = 0;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int m = 16 * i + 4 * q + r;
+        for (int j = 0; j < 2; ++j) {
           const float gv = acc[i][j][r], uv = acc[i][j + 2][r];
           // silu with the hardware exp2 and reciprocal (about 1 ulp each): h is rounded to bf16 next, which
           // hides fp32 differences of a few ulp except at a rounding tie.
           const float sig = __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(gv * -1.4426950408889634f));
-          const float hv = a_off[m] >= 0 ? gv * sig * uv : 0.f;
-          ht[m * kGateUpTileN + 32 * w + 16 * j + n] = (uint16_t)ss_f32_to_bf16(hv);
+          const float hv = live ? gv * sig * uv : 0.f;
+          hp |= (uint32_t)ss_f32_to_bf16(hv) << (16 * j);
         }
+        ht[m * (kGateUpTileN / 2) + 16 * w + n] = hp;
+      }
+    }
     lds_barrier();
     const int n0 = pid_n * kGateUpTileN;
 #pragma unroll
     for (int u = 0; u < (kBM * kGateUpTileN * 2) / (16 * 256); ++u) {
       const int id = u * 256 + tid;
       const int m = id >> 4, cc = id & 15;
+      if (m >= nvalid) break;
       const int r = out_row[m];
       if (r >= 0) {
-        const uint4 v = *reinterpret_cast<const uint4*>(ht + m * kGateUpTileN + 8 * cc);
+        const uint4 v = *reinterpret_cast<const uint4*>(ht + m * (kGateUpTileN / 2) + 4 * cc);
         stg16(g.h + (int64_t)r * g.I + n0 + 8 * cc, v);
       }
     }
   } else {
-    const int n0 = pid_n * kDownTileN + 64 * w;
+    // A lane's four fragments are four adjacent outputs: one 16-byte store per row.
+    const int n0 = pid_n * kDownTileN + 64 * w + 4 * n;
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i) {
+      if (i >= 2 * nf2) break;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 16 * i + 4 * q + r;
         const int orow = out_row[m];
         if (orow >= 0) {
           const float wt = wt_s[m];
-          float* dst = g.out_rows + (int64_t)orow * g.H + n0 + n;
-#pragma unroll
-          for (int j = 0; j < 4; ++j) dst[16 * j] = acc[i][j][r] * wt;
+          const uint4 v = make_uint4(__float_as_uint(acc[i][0][r] * wt), __float_as_uint(acc[i][1][r] * wt),
+                                     __float_as_uint(acc[i][2][r] * wt), __float_as_uint(acc[i][3][r] * wt));
+          stg16(g.out_rows + (int64_t)orow * g.H + n0, v);
         }
       }
+    }
   }
   // Diagnostics: gate/up blocks at entries [0, 8192), down blocks at [8192, 16384), four per block.
   if (g.trace && tid == 0) {
