@@ -102,14 +102,13 @@ __global__ __launch_bounds__(256) void dense_epi_kernel(DenseEpiArgs a) {
   const int k8n = a.K >> 3;
   const uint4* wr = reinterpret_cast<const uint4*>(a.w + (size_t)n * a.K);
   float acc[kDR] = {0.f, 0.f, 0.f, 0.f};
-  for (int k8 = lane; k8 < k8n; k8 += 64) {
-    const uint4 wq = wr[k8];
+  // One chunk of every row into acc, in the lane's chunk order.
+  auto fma_chunk = [&](const uint4& wq, const uint4 (&xq)[kDR]) {
     const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
     for (int r = 0; r < kDR; ++r) {
       if (r < a.R) {
-        const uint4 xq = reinterpret_cast<const uint4*>(a.x + (size_t)r * a.K)[k8];
-        const uint32_t xv[4] = {xq.x, xq.y, xq.z, xq.w};
+        const uint32_t xv[4] = {xq[r].x, xq[r].y, xq[r].z, xq[r].w};
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           acc[r] = fmaf(lo16(xv[c]), lo16(wv[c]), acc[r]);
@@ -117,6 +116,28 @@ __global__ __launch_bounds__(256) void dense_epi_kernel(DenseEpiArgs a) {
         }
       }
     }
+  };
+  // Batches of kUB chunks: every load of a batch is issued before its FMAs (one round trip per batch rather than
+  // one per load); the FMAs keep the chunk order.
+  constexpr int kUB = 8;
+  int k8 = lane;
+  for (; k8 + 64 * (kUB - 1) < k8n; k8 += 64 * kUB) {
+    uint4 wq[kUB], xq[kUB][kDR];
+#pragma unroll
+    for (int u = 0; u < kUB; ++u) {
+      wq[u] = wr[k8 + 64 * u];
+#pragma unroll
+      for (int r = 0; r < kDR; ++r)
+        xq[u][r] = reinterpret_cast<const uint4*>(a.x + (size_t)(r < a.R ? r : 0) * a.K)[k8 + 64 * u];
+    }
+#pragma unroll
+    for (int u = 0; u < kUB; ++u) fma_chunk(wq[u], xq[u]);
+  }
+  for (; k8 < k8n; k8 += 64) {
+    uint4 xq[kDR];
+#pragma unroll
+    for (int r = 0; r < kDR; ++r) xq[r] = reinterpret_cast<const uint4*>(a.x + (size_t)(r < a.R ? r : 0) * a.K)[k8];
+    fma_chunk(wr[k8], xq);
   }
   float mine = 0.f;
 #pragma unroll
