@@ -31,9 +31,11 @@ __global__ __launch_bounds__(256) void rmsnorm_groups_kernel(const uint16_t* __r
   const uint4* ws = w ? reinterpret_cast<const uint4*>(w + (int64_t)g * G) : nullptr;
   uint4* os = reinterpret_cast<uint4*>(out + base);
   const int g8 = G >> 3;
+  // Chunks in batches of kUB whose loads are all issued before their arithmetic (one round trip per batch); the
+  // arithmetic keeps the lane's chunk order.
+  constexpr int kUB = 8;
   float acc = 0.f;
-  for (int k8 = lane; k8 < g8; k8 += 64) {
-    const uint4 a = xs[k8];
+  auto square = [&](const uint4& a) {
     const uint32_t v[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
@@ -41,22 +43,39 @@ __global__ __launch_bounds__(256) void rmsnorm_groups_kernel(const uint16_t* __r
       acc = fmaf(e0, e0, acc);
       acc = fmaf(e1, e1, acc);
     }
+  };
+  int k8 = lane;
+  for (; k8 + 64 * (kUB - 1) < g8; k8 += 64 * kUB) {
+    uint4 a[kUB];
+#pragma unroll
+    for (int u = 0; u < kUB; ++u) a[u] = xs[k8 + 64 * u];
+#pragma unroll
+    for (int u = 0; u < kUB; ++u) square(a[u]);
   }
+  for (; k8 < g8; k8 += 64) square(xs[k8]);
   const float r = 1.f / sqrtf(ss_wave_sum(acc) / (float)G + eps);
-  for (int k8 = lane; k8 < g8; k8 += 64) {
-    const uint4 a = xs[k8];
+  auto scale = [&](int k, const uint4& a, const uint4& b) {
     const uint32_t v[4] = {a.x, a.y, a.z, a.w};
-    uint32_t wv[4] = {0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u};  // bf16 1.0 pairs
-    if (ws) {
-      const uint4 b = ws[k8];
-      wv[0] = b.x, wv[1] = b.y, wv[2] = b.z, wv[3] = b.w;
-    }
+    const uint32_t wv[4] = {b.x, b.y, b.z, b.w};
     uint32_t o[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c)
       o[c] = ss_f32_to_bf16((lo16(v[c]) * r) * lo16(wv[c])) | (ss_f32_to_bf16((hi16(v[c]) * r) * hi16(wv[c])) << 16);
-    os[k8] = make_uint4(o[0], o[1], o[2], o[3]);
+    os[k] = make_uint4(o[0], o[1], o[2], o[3]);
+  };
+  const uint4 one = make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);  // bf16 1.0 pairs
+  k8 = lane;
+  for (; k8 + 64 * (kUB - 1) < g8; k8 += 64 * kUB) {
+    uint4 a[kUB], b[kUB];
+#pragma unroll
+    for (int u = 0; u < kUB; ++u) {
+      a[u] = xs[k8 + 64 * u];
+      b[u] = ws ? ws[k8 + 64 * u] : one;
+    }
+#pragma unroll
+    for (int u = 0; u < kUB; ++u) scale(k8 + 64 * u, a[u], b[u]);
   }
+  for (; k8 < g8; k8 += 64) scale(k8, xs[k8], ws ? ws[k8] : one);
 }
 
 constexpr int kDR = 4;  // x rows per GEMV launch
