@@ -39,8 +39,10 @@ int ssmoe_device_error(int* flags, int clear);
  * persistent MoE launch (ssmoe_moe_decode, ssmoe_moe_verify_layer) writes per-workgroup phase timestamps
  * (s_memrealtime, 100 MHz) to buf[workgroup * 16 + phase]; a chain launch (ssmoe_moe_verify_chain) writes its last
  * layer there, the layer before at row 512 + workgroup, and a few more stamps of each at rows 256 + and 768 +
- * workgroup. NULL switches it off. Process-wide, not thread-safe; a launch captured in a graph keeps the setting
- * of its capture. */
+ * workgroup. The prefill grouped GEMM pair (ssmoe_fused_moe_affine, ssmoe_moe_prefill) writes four entries per
+ * block: start and end stamps, expert << 32 | valid rows, XCC_ID << 32 | HW_ID; gate/up blocks at
+ * buf[4 * block], down blocks at buf[8192 + 4 * block] (blocks past 2048 per kernel are not recorded). NULL switches
+ * it off. Process-wide, not thread-safe; a launch captured in a graph keeps the setting of its capture. */
 int ssmoe_set_trace(void* buf, int64_t entries);
 
 /* Byte offsets of the nine pieces of one affine-4bit expert record (gate.w gate.s gate.b up.w up.s up.b
