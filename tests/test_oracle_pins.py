@@ -320,3 +320,24 @@ def test_threshold_selection_equals_stable_sort():
             assert np.array_equal(got, want)
     print(f"threshold path taken on {taken} of {len(rows)} rows")
     assert 1500 < taken < len(rows)                                  # both paths are exercised
+
+
+# ---------------------------------------------------------------- combine_rank_order: the rank order itself
+def test_combine_rank_order_sums_in_rank_order():
+    """((r0 + r1) + r2) + ... in fp32: with r = (2^24, 1, -2^24) the rank order gives 0 (2^24 + 1 rounds to 2^24),
+    any order that adds 1 last gives 1, and one that pairs +-2^24 first gives 1 as well; integer rows small enough to
+    sum exactly in fp32 must give their exact sum."""
+    T, K, H = 3, 3, 4
+    rows = np.zeros((T * K, H), np.float32)
+    rows[0::K] = 2.0 ** 24
+    rows[1::K] = 1.0
+    rows[2::K] = -(2.0 ** 24)
+    out = O.combine_rank_order(rows, T, K)
+    assert out.dtype == np.float32 and np.all(out == 0.0)
+    # the reverse rank order (1 + ...) would not lose the 1: the check above fails for it
+    rev = O.combine_rank_order(rows.reshape(T, K, H)[:, ::-1].reshape(T * K, H), T, K)
+    assert np.all(rev == 1.0)
+    rng = np.random.default_rng(7)
+    ints = rng.integers(-1000, 1000, size=(5 * 10, 6)).astype(np.float32)
+    exact = ints.reshape(5, 10, 6).astype(np.float64).sum(axis=1)
+    assert np.array_equal(O.combine_rank_order(ints, 5, 10).astype(np.float64), exact)
