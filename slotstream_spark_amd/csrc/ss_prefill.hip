@@ -206,18 +206,21 @@ hipError_t launch_moe_align(const AlignArgs& a, hipStream_t st) {
 // quantisation group). Each wave owns 64 weight rows (four 16-column MFMA B fragments) for all 128 rows of the
 // block, so every weight of the block is dequantized exactly once, by the wave that multiplies it, straight into
 // MFMA B registers. Gate/up: wave w owns gate rows n0 + 32 w .. + 31 (fragments 0, 1) and the same up rows
-// (fragments 2, 3), so silu(g) * u is formed in registers. Down: wave w owns rows n0 + 64 w .. + 63.
+// (fragments 2, 3), so silu(g) * u is formed in registers. Down: wave w owns rows n0 + 64 w .. + 63. Column n of
+// fragment j is the wave's weight row 4 n + j (gate/up: h column 2 n + (j & 1)), so a lane's fragments hold adjacent
+// outputs and the epilogues store 16-byte pieces.
 // K order inside a group: lane quad q (lane >> 4) holds packed words 2q, 2q + 1 of its weight row's group
 // (elements 16 q .. 16 q + 15); MFMA slice s (0, 1) uses word 2q + s, i.e. elements 16 q + 8 s .. + 7, and the A
 // fragment of slice s holds the same elements of each row. A dot product does not depend on which MFMA lanes its
 // K terms go to, only on the accumulation, which the MFMA unit fixes.
 // Memory paths:
-//  * A (activations for gate/up, h for down): global -> registers -> LDS, two stages, one K step ahead of the
-//    MFMAs; each load instruction covers 8 whole 128-byte rows (8 lanes per row). The register-staged path keeps
-//    every wait precise (a direct-to-LDS load in flight makes the compiler wait for it before any LDS read).
+//  * A (activations for gate/up, h for down): global -> registers -> LDS (two LDS stages); each load instruction
+//    covers 8 whole 128-byte rows (8 lanes per row), and only the live rows are loaded. The register-staged path
+//    keeps every wait precise (a direct-to-LDS load in flight makes the compiler wait for it before any LDS read).
 //  * Scales and biases of the block's 256 weight rows for the whole K range: read once, coalesced, into LDS as
 //    (s, b) dword pairs.
-//  * Packed weights: 8 bytes per lane per K step straight into registers, two steps ahead.
+//  * Packed weights: 8 bytes per lane per K step straight into registers.
+//  * The loads of a step are issued PD steps ahead of its MFMAs (register slots; see gemm_loop).
 // 16-byte chunk c of A row m sits at chunk position a_pos(m, c) of the row's 128 bytes, so the 16 rows one MFMA
 // operand read touches (and each group of 8 of them) fall on distinct banks. Rows past the block's valid count
 // get no MFMAs beyond the last 32-row pair of fragments that holds a valid row.
