@@ -98,24 +98,6 @@ SS_DEV void arrival_clear(int* ctr, int c) {
   if (lane <= kArrShards) __hip_atomic_store(arrival_ctr(ctr, c, lane), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Copies n floats written by other workgroups (agent-scope loads, 32 per lane in flight) into LDS.
-SS_DEV void stage_ag(const float* src, int n, float* lds) {
-  const int lane = threadIdx.x & 63;
-  for (int b = 0; b < n; b += 64 * 32) {
-    float v[32];
-#pragma unroll
-    for (int q = 0; q < 32; ++q) {
-      const int i = b + lane + 64 * q;
-      v[q] = i < n ? __hip_atomic_load(const_cast<float*>(src) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < 32; ++q) {
-      const int i = b + lane + 64 * q;
-      if (i < n) lds[i] = v[q];
-    }
-  }
-}
-
 SS_DEV bool finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
 
 // Wave-wide helpers over per-chunk arrays of n <= 64 * kMaxPerLane entries (called by all 64 lanes; every lane
@@ -206,16 +188,18 @@ SS_DEV Scan lds_scan(const float* v, int n, float start, float target) {
   return r;
 }
 
-// Stages the same rows of three arrays (as stage_rows_ag) with every load of a batch in flight before any store.
+// Stages the same rows of three arrays (as stage_rows_ag) with every load of a batch (Q per lane and array) in
+// flight before any store.
+template <int Q>
 SS_DEV void stage_rows3_ag(const float* s0, const float* s1, const float* s2, int nr, int nch, int nchp, float* d0,
                            float* d1, float* d2) {
   const int lane = threadIdx.x & 63;
   const int n = nr * nch;
   for (int i = lane; i < nr * nchp; i += 64) d0[i] = d1[i] = d2[i] = 0.f;
-  for (int b = 0; b < n; b += 64 * 16) {
-    float v0[16], v1[16], v2[16];
+  for (int b = 0; b < n; b += 64 * Q) {
+    float v0[Q], v1[Q], v2[Q];
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
+    for (int q = 0; q < Q; ++q) {
       const int i = b + lane + 64 * q;
       const bool in = i < n;
       v0[q] = in ? __hip_atomic_load(const_cast<float*>(s0) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
@@ -223,7 +207,7 @@ SS_DEV void stage_rows3_ag(const float* s0, const float* s1, const float* s2, in
       v2[q] = in ? __hip_atomic_load(const_cast<float*>(s2) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
     }
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
+    for (int q = 0; q < Q; ++q) {
       const int i = b + lane + 64 * q;
       if (i < n) {
         const int r = i / nch, o = r * nchp + (i - r * nch);
@@ -306,9 +290,7 @@ __global__ __launch_bounds__(64) void greedy_kernel(AcceptArgs a) {
   for (int r0 = 0; r0 < rows; r0 += per) {
     const int nr = rows - r0 < per ? rows - r0 : per;
     const size_t o = (size_t)r0 * nch;
-    stage_ag(k.cmax + o, nr * nch, sv);
-    stage_ag(k.ctot + o, nr * nch, si);
-    stage_ag(k.cbad + o, nr * nch, sb);
+    stage_rows3_ag<16>(k.cmax + o, k.ctot + o, k.cbad + o, nr, nch, nch, sv, si, sb);
     __syncthreads();
     for (int rr = 0; rr < nr; ++rr) {
       uint64_t bk = 0;
@@ -457,8 +439,15 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
     s = ss_wave_sum(s);
     if (lane == 0) st_ag(k.ctot + (size_t)row * nch + c, s);
   }
+  // The drafts (lane i holds draft i; D <= 60) arrive with this workgroup's own loads, so the finishing workgroup
+  // requests the draft positions' logits and the uniforms together with its staging.
+  const int xi = lane < a.D ? a.drafts[lane] : 0;
   if (!arrive_last(k.ctr, 1, row * nch + c, nch * rows)) return;
   arrival_clear(k.ctr, 1);
+  const bool xok = lane < a.D && xi >= 0 && xi < a.V;
+  const float lt = xok ? a.target[(size_t)lane * a.V + xi] : 0.f;
+  const float lq = xok ? a.draft[(size_t)lane * a.V + xi] : 0.f;
+  const float uu = lane < a.D ? a.uniforms[lane] : 0.f;
   // Per row: the total (sequential over its chunk totals, from 0), the maximum and the non-finite flag, lane r
   // taking row r of each staged batch.
   const int nchp = (nch + 15) & ~15;
@@ -466,7 +455,9 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
   for (int r0 = 0; r0 < rows; r0 += per) {
     const int nr = rows - r0 < per ? rows - r0 : per;
     const size_t o = (size_t)r0 * nch;
-    stage_rows3_ag(k.ctot + o, k.cmax + o, k.cbad + o, nr, nch, nchp, sv, sm, sb);
+    // 17 per lane: one batch for the seven rows of a depth-3 round at V = 151,936 (1,043 chunks), and 88 VGPRs,
+    // which keep five workgroups per CU (as the LDS does)
+    stage_rows3_ag<17>(k.ctot + o, k.cmax + o, k.cbad + o, nr, nch, nchp, sv, sm, sb);
     __syncthreads();
     for (int rr = lane; rr < nr; rr += 64) {
       const float4* m4 = reinterpret_cast<const float4*>(sm + rr * nchp);
@@ -485,16 +476,14 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
     }
     __syncthreads();
   }
-  // the draft positions' logits, the drafts and the uniforms, requested at once
+  // the drafts, the draft positions' logits and the uniforms
   __shared__ int s_x[64];
   __shared__ float s_lt[64], s_lq[64], s_u[64];
-  for (int i = lane; i < a.D; i += 64) {
-    const int xi = a.drafts[i];
-    const bool xok = xi >= 0 && xi < a.V;
-    s_x[i] = xi;
-    s_lt[i] = xok ? a.target[(size_t)i * a.V + xi] : 0.f;
-    s_lq[i] = xok ? a.draft[(size_t)i * a.V + xi] : 0.f;
-    s_u[i] = a.uniforms[i];
+  if (lane < a.D) {
+    s_x[lane] = xi;
+    s_lt[lane] = lt;
+    s_lq[lane] = lq;
+    s_u[lane] = uu;
   }
   __syncthreads();
   if (lane == 0) {
@@ -543,12 +532,34 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
   }
 }
 
+// The round's state as the p/q sums launch left it, read with one batch of loads.
+struct PqState {
+  int srow, sdraft, uidx, stop, good, flags;
+  float zs, zd, ms, md;
+};
+SS_DEV PqState pq_state(const float* st) {
+  float v[10];
+#pragma unroll
+  for (int i = 0; i < 10; ++i) v[i] = st[i];
+  PqState r;
+  r.srow = __float_as_int(v[0]);
+  r.sdraft = __float_as_int(v[1]);
+  r.uidx = __float_as_int(v[2]);
+  r.stop = __float_as_int(v[3]);
+  r.good = __float_as_int(v[4]);
+  r.flags = __float_as_int(v[5]);
+  r.zs = v[6];
+  r.zd = v[7];
+  r.ms = v[8];
+  r.md = v[9];
+  return r;
+}
+
 // Value of entry j of the sampled distribution: p_j, or max(0, p_j - q_j) after a rejection.
-SS_DEV float sample_value(const AcceptArgs& a, const float* st, int j) {
-  const int srow = __float_as_int(st[0]), sdraft = __float_as_int(st[1]);
-  const float p = ss_expf(a.target[(size_t)srow * a.V + j] / a.temperature - st[8]) / st[6];
-  if (sdraft < 0) return p;
-  const float q = ss_expf(a.draft[(size_t)(sdraft - a.D - 1) * a.V + j] / a.temperature - st[9]) / st[7];
+SS_DEV float sample_value(const AcceptArgs& a, const PqState& st, int j) {
+  const float p = ss_expf(a.target[(size_t)st.srow * a.V + j] / a.temperature - st.ms) / st.zs;
+  if (st.sdraft < 0) return p;
+  const float q = ss_expf(a.draft[(size_t)(st.sdraft - a.D - 1) * a.V + j] / a.temperature - st.md) / st.zd;
   const float d = p - q;
   return d > 0.f ? d : 0.f;
 }
@@ -556,22 +567,26 @@ SS_DEV float sample_value(const AcceptArgs& a, const float* st, int j) {
 // Inverse-CDF search by the finishing workgroup. Every lane forms the same running sums (index order, from the
 // chunk's base) from LDS broadcast reads: the chunk, then the sub-chunk, then the entry, each falling back to the
 // last nonzero one.
-SS_DEV void pq_search(const AcceptArgs& a, const Work& k, int nch, float* srt) {
+SS_DEV void pq_search(const AcceptArgs& a, const Work& k, const PqState& st, int nch, float* srt) {
   __shared__ __attribute__((aligned(16))) float s_st[64];
   __shared__ float s_val[kSub];
+  __shared__ int s_dr[64];
   const int lane = threadIdx.x;
-  const int good = __float_as_int(k.state[4]);
-  int flags = __float_as_int(k.state[5]);
-  const int stop = __float_as_int(k.state[3]);
-  const int uidx = __float_as_int(k.state[2]);
+  const int good = st.good;
+  int flags = st.flags;
+  const int stop = st.stop;
+  const int uidx = st.uidx;
+  // the accepted drafts, requested with the first loads rather than one round trip each at the end
+  for (int i = lane; i < good; i += 64) s_dr[i] = a.drafts[i];
   int emit = good;
   int pick = -1;
   if (!stop) {
+    const float u = a.uniforms[uidx];
     stage_rows_ag(k.rtot, 1, nch, (nch + 15) & ~15, srt);
     __syncthreads();
     const float S = lds_seq_sum(srt, nch, 0.f);
     if (!(S > 0.f)) flags |= FLAG_RESIDUAL_EMPTY;
-    const float target = a.uniforms[uidx] * S;
+    const float target = u * S;
     // chunk: the first whose running total exceeds the target (else the last nonzero one, based at its prefix)
     const Scan ch = lds_scan(srt, nch, 0.f, target);
     int cs = ch.first;
@@ -591,7 +606,7 @@ SS_DEV void pq_search(const AcceptArgs& a, const Work& k, int nch, float* srt) {
       sbase = lds_seq_sum(s_st, bs, base);
     }
     const int j0 = cs * kChunk + bs * kSub;
-    if (lane < kSub) s_val[lane] = j0 + lane < a.V ? sample_value(a, k.state, j0 + lane) : 0.f;
+    if (lane < kSub) s_val[lane] = j0 + lane < a.V ? sample_value(a, st, j0 + lane) : 0.f;
     __syncthreads();
     int last = -1;
     float run = sbase;
@@ -608,8 +623,9 @@ SS_DEV void pq_search(const AcceptArgs& a, const Work& k, int nch, float* srt) {
     }
     if (pick < 0) pick = last >= 0 ? last : min(j0, a.V - 1);
   }
+  __syncthreads();
   if (lane == 0) {
-    for (int i = 0; i < good; ++i) a.out[OUT_TOK + i] = a.drafts[i];
+    for (int i = 0; i < good; ++i) a.out[OUT_TOK + i] = s_dr[i];
     if (!stop) a.out[OUT_TOK + emit++] = pick;
     for (int i = emit; i <= a.D; ++i) a.out[OUT_TOK + i] = -1;
     a.out[OUT_NACC] = good;
@@ -625,13 +641,14 @@ __global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
   __shared__ __attribute__((aligned(16))) float lds[kMaxPerLane * 64 + 64];
   const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nch = gridDim.x;
   Work k = work_of(a.work, 2 * a.D + 1, nch);
-  const bool run = !__float_as_int(k.state[3]);
+  const PqState st = pq_state(k.state);
+  const bool run = !st.stop;
   if (run) {
 #pragma unroll
     for (int ii = 0; ii < kSub / 4; ++ii) {
       const int e = (w * (kSub / 4) + ii) * 64 + lane;
       const int j = c * kChunk + e;
-      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? sample_value(a, k.state, j) : 0.f;
+      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? sample_value(a, st, j) : 0.f;
     }
   }
   __syncthreads();
@@ -645,7 +662,7 @@ __global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
   }
   if (!arrive_last(k.ctr, 2, c, nch)) return;
   arrival_clear(k.ctr, 2);
-  pq_search(a, k, nch, lds);
+  pq_search(a, k, st, nch, lds);
 }
 
 hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st) {
