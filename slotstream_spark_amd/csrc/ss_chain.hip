@@ -172,26 +172,7 @@ SS_DEV void stage_x_src(const uint16_t* src, bool norm, const uint16_t* nw_lds, 
     const uint4 pv = perm_pairs(fv[k]);
     xfl[f] = make_uint4(live ? pv.x : 0u, live ? pv.y : 0u, live ? pv.z : 0u, live ? pv.w : 0u);
   }
-  if (norm) {
-    __syncthreads();
-    if (tid < (H >> 6) * kTBv) {
-      float sum = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint4 v = xfl[xfrag_index(64 * Gi + 8 * k, gt)];
-        sum = sum + bf_lo(v.x);
-        sum = sum + bf_lo(v.y);
-        sum = sum + bf_lo(v.z);
-        sum = sum + bf_lo(v.w);
-        sum = sum + bf_hi(v.x);
-        sum = sum + bf_hi(v.y);
-        sum = sum + bf_hi(v.z);
-        sum = sum + bf_hi(v.w);
-      }
-      gx[Gi][q & 3] = (q & 3) < nt ? sum : 0.f;
-    }
-    return;
-  }
+  if (norm) return;  // the group sums come from the staged fragments later (xfrag_group_sums)
   if (tid < (H >> 6) * kTBv) {
     float sum = 0.f;
 #pragma unroll
@@ -208,6 +189,28 @@ SS_DEV void stage_x_src(const uint16_t* src, bool norm, const uint16_t* nw_lds, 
     }
     gx[Gi][q & 3] = (q & 3) < nt ? sum : 0.f;
   }
+}
+
+// Group sum q (group q >> 2 of token q & 3, sequential in element order) of the normalized x, from the staged
+// fragments: the stage_x_src sums when it normalizes, formed once the fragments are visible to the whole workgroup.
+SS_DEV void xfrag_group_sums(const uint4* xfl, float (*gx)[kTBv], int q, int nt) {
+  const int Gi = q >> 2, gt = (q & 3) < nt ? (q & 3) : 0;
+  uint4 v[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) v[k] = xfl[xfrag_index(64 * Gi + 8 * k, gt)];
+  float sum = 0.f;
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    sum = sum + bf_lo(v[k].x);
+    sum = sum + bf_lo(v[k].y);
+    sum = sum + bf_lo(v[k].z);
+    sum = sum + bf_lo(v[k].w);
+    sum = sum + bf_hi(v[k].x);
+    sum = sum + bf_hi(v[k].y);
+    sum = sum + bf_hi(v[k].z);
+    sum = sum + bf_hi(v[k].w);
+  }
+  gx[Gi][q & 3] = (q & 3) < nt ? sum : 0.f;
 }
 
 // The fields the shared device helpers read, for one layer.
@@ -536,6 +539,10 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
     if (tid < 64) {
       unique_setup(va, s, true);
     } else {
+      // While wave 0 forms the unique list: the x group sums of a normalized stream (first read by the items) and
+      // the zeros of the items' h sums.
+      if (norm)
+        for (int q = tid - 64; q < (H >> 6) * kTBv; q += 192) xfrag_group_sums(xfl, s.gx, q, nt);
       for (int i = tid - 64; i < kXZero; i += 192) reinterpret_cast<uint4*>(s.hsum)[i] = make_uint4(0u, 0u, 0u, 0u);
     }
     __syncthreads();
