@@ -161,14 +161,17 @@ SS_DEV float lds_seq_sum(const float* v, int n, float s) {
   return s;
 }
 // Running sum from `start` over v[0..n): the first index whose running sum exceeds `target` (and the running sum
-// before it), and the last nonzero index.
+// before it; `start` when there is none), and the last nonzero index. The zero padding adds +0 to the running sum
+// and, coming after a miss with the same sum, cannot be the first hit, so no bound check runs per entry: the first
+// hit is the count of leading misses.
 struct Scan {
   int first, last;
   float base;
 };
 SS_DEV Scan lds_scan(const float* v, int n, float start, float target) {
-  Scan r{-1, -1, start};
-  float run = start;
+  float run = start, base = start;
+  int lead = 0, last = -1;
+  bool alive = true;
   const float4* v4 = reinterpret_cast<const float4*>(v);
   for (int b = 0; b < n; b += 16) {
     const float4 a0 = v4[b / 4], a1 = v4[b / 4 + 1], a2 = v4[b / 4 + 2], a3 = v4[b / 4 + 3];
@@ -176,15 +179,18 @@ SS_DEV Scan lds_scan(const float* v, int n, float start, float target) {
                          a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {  // selects only: every lane holds the same values
-      const bool in = b + i < n;
       const float nx = run + t[i];
-      r.last = in && t[i] > 0.f ? b + i : r.last;
-      const bool hit = in && r.first < 0 && nx > target;
-      r.base = hit ? run : r.base;
-      r.first = hit ? b + i : r.first;
-      run = in ? nx : run;
+      alive = alive && !(nx > target);
+      base = alive ? nx : base;
+      lead += alive ? 1 : 0;
+      last = t[i] > 0.f ? b + i : last;
+      run = nx;
     }
   }
+  Scan r;
+  r.first = lead < n ? lead : -1;
+  r.base = r.first >= 0 ? base : start;
+  r.last = last;
   return r;
 }
 
