@@ -823,7 +823,10 @@ __global__ __launch_bounds__(64) void samp_draw_kernel(SampArgs a) {
   const bool ge = u != 0.f;
   const float target = ge ? u * total : 0.f;
   auto hit = [&](float x) { return ge ? x >= target : x > target; };
-  int cs = -1, clast = -1;
+  // The first chunk whose running total hits the target is the count of leading misses: the zero padding adds +0
+  // and, following a miss with the same total, cannot be the first hit, so no bound check runs per entry.
+  int lead = 0, clast = -1;
+  bool alive = true;
   float base = 0.f, run = 0.f;
   const float4* c4 = reinterpret_cast<const float4*>(ct);
   for (int q0 = 0; q0 < nch; q0 += 16) {  // 16 unconditional reads (the padding is zero), then the in-order scan
@@ -832,33 +835,35 @@ __global__ __launch_bounds__(64) void samp_draw_kernel(SampArgs a) {
                          a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const bool in = q0 + i < nch;
       const float nx = run + t[i];
-      const bool found = in && cs < 0 && hit(nx);
-      cs = found ? q0 + i : cs;
-      base = found ? run : base;
-      clast = in && t[i] > 0.f ? q0 + i : clast;
-      run = in ? nx : run;
+      alive = alive && !hit(nx);
+      base = alive ? nx : base;
+      lead += alive ? 1 : 0;
+      clast = t[i] > 0.f ? q0 + i : clast;
+      run = nx;
     }
   }
+  int cs = lead < nch ? lead : -1;
   if (cs < 0) {
     cs = clast < 0 ? 0 : clast;
     base = lds_seq_sum(ct, cs, 0.f);
   }
   const float st = w.stot[cs * 64 + lane];
-  int bs = -1, blast = -1;
+  int slead = 0, blast = -1;
   float sbase = base;
   run = base;
+  alive = true;
+#pragma unroll 16
   for (int b = 0; b < 64; ++b) {
     const float t = ss_readlane_f(st, b);
     const float nx = run + t;
-    if (t > 0.f) blast = b;
-    if (bs < 0 && hit(nx)) {
-      bs = b;
-      sbase = run;
-    }
+    blast = t > 0.f ? b : blast;
+    alive = alive && !hit(nx);
+    sbase = alive ? nx : sbase;
+    slead += alive ? 1 : 0;
     run = nx;
   }
+  int bs = slead < 64 ? slead : -1;
   if (bs < 0) {
     bs = blast < 0 ? 0 : blast;
     sbase = base;
