@@ -145,17 +145,23 @@ SS_DEV bool wave_any_nonzero(const WaveVals& w, int n) {
 
 // Sequential sums and scans over LDS arrays that are 16-byte aligned and padded with zeros to a multiple of 16
 // entries: every 16 entries are read as four unconditional 16-byte loads before their (dependent, in-order) adds,
-// and the bound n is applied by selects.
+// and the bound n is applied by selects in the last, partial group.
 SS_DEV float lds_seq_sum(const float* v, int n, float s) {
+  // whole groups of 16 add without a bound check; only the last, partial group selects
   const float4* v4 = reinterpret_cast<const float4*>(v);
   for (int b = 0; b < n; b += 16) {
     const float4 a0 = v4[b / 4], a1 = v4[b / 4 + 1], a2 = v4[b / 4 + 2], a3 = v4[b / 4 + 3];
     const float t[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
                          a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+    if (b + 16 <= n) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float nx = s + t[i];
-      s = b + i < n ? nx : s;
+      for (int i = 0; i < 16; ++i) s = s + t[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float nx = s + t[i];
+        s = b + i < n ? nx : s;
+      }
     }
   }
   return s;

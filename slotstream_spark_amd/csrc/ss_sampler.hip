@@ -183,17 +183,23 @@ SS_DEV const float* stage(const float* a, int n) {
 }
 
 // ((s + b[0]) + b[1]) + ... + b[n-1] over a zero-padded, 16-byte aligned LDS array: 16 entries read as four
-// unconditional 16-byte loads before their in-order adds, the bound applied by selects.
+// unconditional 16-byte loads before their in-order adds, the bound applied by selects in the last, partial group.
 SS_DEV float lds_seq_sum(const float* b, int n, float s) {
+  // whole groups of 16 add without a bound check; only the last, partial group selects
   const float4* b4 = reinterpret_cast<const float4*>(b);
   for (int q = 0; q < n; q += 16) {
     const float4 a0 = b4[q / 4], a1 = b4[q / 4 + 1], a2 = b4[q / 4 + 2], a3 = b4[q / 4 + 3];
     const float t[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
                          a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
+    if (q + 16 <= n) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const float nx = s + t[i];
-      s = q + i < n ? nx : s;
+      for (int i = 0; i < 16; ++i) s = s + t[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float nx = s + t[i];
+        s = q + i < n ? nx : s;
+      }
     }
   }
   return s;
