@@ -460,8 +460,7 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
   const float lt = xok ? a.target[(size_t)lane * a.V + xi] : 0.f;
   const float lq = xok ? a.draft[(size_t)lane * a.V + xi] : 0.f;
   const float uu = lane < a.D ? a.uniforms[lane] : 0.f;
-  // Per row: the total (sequential over its chunk totals, from 0), the maximum and the non-finite flag, lane r
-  // taking row r of each staged batch.
+  // Per row: the total (sequential over its chunk totals, from 0), the maximum and the non-finite flag.
   const int nchp = (nch + 15) & ~15;
   const int per = kStage / nchp;
   for (int r0 = 0; r0 < rows; r0 += per) {
@@ -471,21 +470,22 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
     // which keep five workgroups per CU (as the LDS does)
     stage_rows3_ag<17>(k.ctot + o, k.cmax + o, k.cbad + o, nr, nch, nchp, sv, sm, sb);
     __syncthreads();
-    for (int rr = lane; rr < nr; rr += 64) {
-      const float4* m4 = reinterpret_cast<const float4*>(sm + rr * nchp);
-      const float4* b4 = reinterpret_cast<const float4*>(sb + rr * nchp);
+    // the maximum and flag of each row across the wave (order-free: a +-0 difference in m changes no exp(x - m));
+    // the totals, which keep their order, lane r taking row r
+    for (int rr = 0; rr < nr; ++rr) {
       float m = -__builtin_inff(), b = 0.f;
-      for (int q = 0; q < nchp / 4; ++q) {
-        const float4 mv = m4[q], bv = b4[q];
-        const float mm[4] = {mv.x, mv.y, mv.z, mv.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) m = 4 * q + e < nch ? fmaxf(m, mm[e]) : m;
-        b = fmaxf(b, fmaxf(fmaxf(bv.x, bv.y), fmaxf(bv.z, bv.w)));  // flags are 0 or 1, the padding 0
+      for (int cc = lane; cc < nch; cc += 64) {
+        m = fmaxf(m, sm[rr * nchp + cc]);
+        b = fmaxf(b, sb[rr * nchp + cc]);  // flags are 0 or 1
       }
-      zrow[r0 + rr] = lds_seq_sum(sv + rr * nchp, nch, 0.f);
-      mrow[r0 + rr] = m;
-      brow[r0 + rr] = b != 0.f;
+      m = ss_wave_max(m);
+      b = ss_wave_max(b);
+      if (lane == 0) {
+        mrow[r0 + rr] = m;
+        brow[r0 + rr] = b != 0.f;
+      }
     }
+    for (int rr = lane; rr < nr; rr += 64) zrow[r0 + rr] = lds_seq_sum(sv + rr * nchp, nch, 0.f);
     __syncthreads();
   }
   // the drafts, the draft positions' logits and the uniforms
