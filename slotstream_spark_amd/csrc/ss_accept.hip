@@ -100,48 +100,8 @@ SS_DEV void arrival_clear(int* ctr, int c) {
 
 SS_DEV bool finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F800000u; }
 
-// Wave-wide helpers over per-chunk arrays of n <= 64 * kMaxPerLane entries (called by all 64 lanes; every lane
-// returns the same value). Entry c is loaded by lane c % 64 into register c / 64, so all loads are in flight at
-// once; a sum that must keep its sequential order is then formed in index order from the lanes' registers.
+// Chunk-array entries per lane when one wave loads an array of per-chunk values (lane c % 64, register c / 64).
 constexpr int kMaxPerLane = 16;  // V <= 16 * 64 * 1024 entries
-struct WaveVals {
-  float v[kMaxPerLane];
-};
-SS_DEV WaveVals wave_load(const float* arr, int n) {
-  WaveVals w;
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int k = 0; k < kMaxPerLane; ++k) {
-    const int c = lane + 64 * k;
-    w.v[k] = c < n ? arr[c] : 0.f;
-  }
-  return w;
-}
-// ((v[0] + v[1]) + ...) + v[n-1] from 0.f, fp32, in index order.
-SS_DEV float wave_seq_sum(const WaveVals& w, int n) {
-  float s = 0.f;
-#pragma unroll
-  for (int k = 0; k < kMaxPerLane; ++k) {
-    if (64 * k >= n) break;
-    const int m = n - 64 * k < 64 ? n - 64 * k : 64;
-    for (int l = 0; l < m; ++l) s = s + ss_readlane_f(w.v[k], l);
-  }
-  return s;
-}
-SS_DEV float wave_max_of(const WaveVals& w, int n) {
-  const int lane = threadIdx.x & 63;
-  float m = -__builtin_inff();
-#pragma unroll
-  for (int k = 0; k < kMaxPerLane; ++k) m = lane + 64 * k < n ? fmaxf(m, w.v[k]) : m;
-  return ss_wave_max(m);
-}
-SS_DEV bool wave_any_nonzero(const WaveVals& w, int n) {
-  const int lane = threadIdx.x & 63;
-  uint32_t b = 0;
-#pragma unroll
-  for (int k = 0; k < kMaxPerLane; ++k) b |= (lane + 64 * k < n && w.v[k] != 0.f) ? 1u : 0u;
-  return ss_wave_or(b) != 0u;
-}
 
 // Sequential sums and scans over LDS arrays that are 16-byte aligned and padded with zeros to a multiple of 16
 // entries: every 16 entries are read as four unconditional 16-byte loads before their (dependent, in-order) adds,
