@@ -256,6 +256,8 @@ __global__ __launch_bounds__(64) void greedy_kernel(AcceptArgs a) {
       st_ag(k.cbad + o, bad ? 1.f : 0.f);
     }
   }
+  // The drafts (lane i holds draft i; D <= 60) arrive with this workgroup's own loads rather than after the reduction.
+  const int dr = lane < a.D ? a.drafts[lane] : 0;
   if (!arrive_last(k.ctr, 0, row * nch + c, nch * rows)) return;
   arrival_clear(k.ctr, 0);
   const int per = kStage / nch;
@@ -284,7 +286,7 @@ __global__ __launch_bounds__(64) void greedy_kernel(AcceptArgs a) {
     __syncthreads();
   }
   __shared__ int s_dr[64];
-  for (int i = lane; i < a.D; i += 64) s_dr[i] = a.drafts[i];
+  if (lane < a.D) s_dr[lane] = dr;
   __syncthreads();
   if (lane == 0) {
     const int D = a.D;
