@@ -230,14 +230,17 @@ def peaks_leg(dev):
     return res
 
 
-def config2_leg(pool, lw, bias, steps, dev):
-    """an MTP chain of depth 3 (T=4 verify) through the config-1 layer, then acceptance over
-    vocab 151,936: greedy argmax-match, p/q at temperature 0.7, and (beside the step, as the reference's own sampled
-    round) the reference sampler at temperature 0.7 with its default top-p 0.95 / top-k 40, on 1000 seeded steps of
-    synthetic fp32 logits
-    (target N(0,3), draft correlated rho=0.8; drafts = the draft rows' argmax; uniforms from the sampler's
-    splitmix64 stream seeded per step). Every step's logits, drafts and uniforms are resident in HBM before the
-    timed region; the steps are captured as HIP graphs (100 steps each) and replayed once, timed with HIP events."""
+def config2_leg(pool, weights, biases, steps, dev, n_layers=8):
+    """an MTP chain of depth 3 (T=4 verify) through config-1 layers, then acceptance over vocab
+    151,936 on 1000 seeded steps of synthetic fp32 logits (target N(0,3), draft correlated rho=0.8): greedy
+    argmax-match with the draft rows' argmax as drafts (the greedy proposal), p/q at temperature 0.7 with drafts
+    drawn from q = softmax(draft / 0.7) on the device (ssmoe_sample_rows, the proposal Leviathan et al. Alg. 1
+    needs), and (beside the step, as the reference's own sampled round) the reference sampler at temperature 0.7 with
+    its default top-p 0.95 / top-k 40. Uniforms come from the sampler's splitmix64 stream seeded per step: the first
+    D draw the drafts, the next D + 1 feed the p/q round. The verify layer is cold: each step has its own input rows
+    and the steps rotate over `n_layers` distinct layers (8 x 906 MB of records, above the 256 MB Infinity Cache).
+    Every step's inputs are resident in HBM before the timed region; the steps are captured as HIP graphs (100
+    steps each) and replayed once, timed with HIP events."""
     import numpy as np
     import torch
 
@@ -248,9 +251,9 @@ def config2_leg(pool, lw, bias, steps, dev):
 
     D, V, TEMP, T = 3, 151936, 0.7, 4
     sp = SampleParams(temperature=TEMP)
-    layer = MoEVerifyLayer(pool, 0, lw.router_w, lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_g, top_k=K,
-                           router_bias=bias, max_tokens=4)
-    x = normal_bf16((T, H), 1.0, 1734, dev)
+    layers = [MoEVerifyLayer(pool, l, weights[l].router_w, weights[l].sh_gate, weights[l].sh_up, weights[l].sh_down,
+                             weights[l].sh_g, top_k=K, router_bias=biases[l], max_tokens=4) for l in range(n_layers)]
+    xs = normal_bf16((steps, T, H), 1.0, 1734, dev)
     y = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
     ids = torch.empty((T, K), dtype=torch.int32, device=dev)
     wts = torch.empty((T, K), dtype=torch.float32, device=dev)
@@ -258,8 +261,12 @@ def config2_leg(pool, lw, bias, steps, dev):
     drf = torch.empty((steps, D, V), device=dev)
     for st in range(steps):
         tgt[st], drf[st] = verify_logits(D, V, 10_000 + st, device=dev)
-    drafts = drf.argmax(dim=2).to(torch.int32).contiguous()
-    uni = torch.from_numpy(np.stack([UniformStream(20_000 + st).peek(D + 1) for st in range(steps)])).to(dev)
+    drafts_g = drf.argmax(dim=2).to(torch.int32).contiguous()
+    un = np.stack([UniformStream(20_000 + st).peek(2 * D + 1) for st in range(steps)])
+    u_draw = torch.from_numpy(np.ascontiguousarray(un[:, :D])).to(dev)
+    u_acc = torch.from_numpy(np.ascontiguousarray(un[:, D:])).to(dev)
+    u_smp = torch.from_numpy(np.ascontiguousarray(un[:, :D + 1])).to(dev)
+    drafts_q = torch.empty((steps, D), dtype=torch.int32, device=dev)
     acc = Acceptor(D, V, device=dev)
     out_g = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
     out_p = torch.empty((steps, D + 5), dtype=torch.int32, device=dev)
@@ -267,22 +274,25 @@ def config2_leg(pool, lw, bias, steps, dev):
     acc_s = Acceptor(D, V, device=dev)
     chunk = 100
 
-    def run(lo, hi, verify=True, greedy=True, pq=True, sampled=False):
+    def run(lo, hi, verify=True, greedy=False, draw=False, pq=False, sampled=False):
         for st in range(lo, hi):
             if verify:
-                layer(x, y=y, ids=ids, weights=wts)
+                layers[st % n_layers](xs[st], y=y, ids=ids, weights=wts)
             if greedy:
-                out_g[st].copy_(acc.greedy_async(tgt[st], drafts[st]))
+                out_g[st].copy_(acc.greedy_async(tgt[st], drafts_g[st]))
+            if draw:
+                acc.draw_drafts_async(drf[st], u_draw[st], TEMP, out=drafts_q[st])
             if pq:
-                out_p[st].copy_(acc.pq_async(tgt[st], drf[st], drafts[st], uni[st], TEMP))
+                out_p[st].copy_(acc.pq_async(tgt[st], drf[st], drafts_q[st], u_acc[st], TEMP))
             if sampled:
-                out_s[st].copy_(acc_s.sampled_async(tgt[st], drafts[st], sp, (), uni[st]))
+                out_s[st].copy_(acc_s.sampled_async(tgt[st], drafts_g[st], sp, (), u_smp[st]))
 
     s_ = torch.cuda.Stream(device=dev)
     res = {}
-    for name, kw in (("step", {}), ("verify", dict(greedy=False, pq=False)), ("greedy", dict(verify=False, pq=False)),
-                     ("pq", dict(verify=False, greedy=False)),
-                     ("sampled", dict(verify=False, greedy=False, pq=False, sampled=True))):
+    legs = (("step_greedy", dict(greedy=True)), ("step_pq", dict(draw=True, pq=True)), ("verify", {}),
+            ("greedy", dict(verify=False, greedy=True)), ("draw", dict(verify=False, draw=True)),
+            ("pq", dict(verify=False, pq=True)), ("sampled", dict(verify=False, sampled=True)))
+    for name, kw in legs:
         total = 0.0
         for lo in range(0, steps, chunk):
             total += timed_graph(lambda: run(lo, min(steps, lo + chunk), **kw), 1, 0, s_) * 1000.0
@@ -297,19 +307,32 @@ def config2_leg(pool, lw, bias, steps, dev):
             st.add(D, r)
         stats[name] = {"acceptance_length": round(st.acceptance_length, 4),
                        "accepted_by_depth": st.accepted_by_depth, "attempts_by_depth": st.attempts_by_depth}
-    tok_s = stats["pq"]["acceptance_length"] / (res["step"] * 1e-6)
-    log(f"config2: step {res['step']:.1f} us (verify T=4 {res['verify']:.1f}, greedy {res['greedy']:.1f}, "
-        f"p/q {res['pq']:.1f}; sampled round {res['sampled']:.1f}); acceptance length greedy "
-        f"{stats['greedy']['acceptance_length']}, p/q {stats['pq']['acceptance_length']}, "
-        f"sampled {stats['sampled']['acceptance_length']}")
-    return {"steps": steps, "depth": D, "vocab": V, "temperature": TEMP,
-            "us_per_step": round(res["step"], 2), "us_verify_T4": round(res["verify"], 2),
-            "us_accept_greedy": round(res["greedy"], 2), "us_accept_pq": round(res["pq"], 2),
-            "tokens_per_s_pq": round(tok_s, 1), "greedy": stats["greedy"], "pq": stats["pq"],
+    # the acceptance rate Alg. 1 predicts for row 0 with sampled drafts: sum_x min(p(x), q(x)), from the first steps
+    pred = []
+    for st in range(min(steps, 32)):
+        p0 = torch.softmax(tgt[st, 0].double() / TEMP, 0)
+        q0 = torch.softmax(drf[st, 0].double() / TEMP, 0)
+        pred.append(float(torch.minimum(p0, q0).sum()))
+    stats["pq"]["predicted_accept_rate_row0"] = round(sum(pred) / len(pred), 4)
+    stats["pq"]["measured_accept_rate_row0"] = round(stats["pq"]["accepted_by_depth"][0] / steps, 4)
+    tok_s = stats["pq"]["acceptance_length"] / (res["step_pq"] * 1e-6)
+    tok_g = stats["greedy"]["acceptance_length"] / (res["step_greedy"] * 1e-6)
+    log(f"config2: step greedy {res['step_greedy']:.1f} us, step p/q {res['step_pq']:.1f} us (verify T=4 cold "
+        f"{res['verify']:.1f}, greedy {res['greedy']:.1f}, draft draw {res['draw']:.1f}, p/q {res['pq']:.1f}; "
+        f"sampled round {res['sampled']:.1f}); acceptance length greedy {stats['greedy']['acceptance_length']}, "
+        f"p/q {stats['pq']['acceptance_length']} (row-0 accept {stats['pq']['measured_accept_rate_row0']} vs "
+        f"predicted {stats['pq']['predicted_accept_rate_row0']}), sampled {stats['sampled']['acceptance_length']}")
+    return {"steps": steps, "depth": D, "vocab": V, "temperature": TEMP, "verify_layers": n_layers,
+            "us_per_step_greedy": round(res["step_greedy"], 2), "us_per_step_pq": round(res["step_pq"], 2),
+            "us_verify_T4": round(res["verify"], 2), "us_accept_greedy": round(res["greedy"], 2),
+            "us_draw_drafts": round(res["draw"], 2), "us_accept_pq": round(res["pq"], 2),
+            "tokens_per_s_pq": round(tok_s, 1), "tokens_per_s_greedy": round(tok_g, 1),
+            "greedy": stats["greedy"], "pq": stats["pq"],
             "us_accept_sampled": round(res["sampled"], 2),
             "sampled": dict(stats["sampled"], params="temperature 0.7, top_p 0.95, top_k 40 (SampleParams defaults)"),
-            "timing": "HIP graphs of 100 steps (verify layer + greedy + p/q per step; the sampled round in graphs "
-                      "of its own), events on the graph stream"}
+            "timing": "HIP graphs of 100 steps, events on the graph stream; step_greedy = cold T=4 verify layer + "
+                      "greedy round; step_pq = cold T=4 verify layer + draft draw from q + p/q round; the parts "
+                      "and the sampled round in graphs of their own"}
 
 
 def lm_head_leg(steps, dev):
@@ -440,12 +463,16 @@ def step_leg(pool, weights, biases, steps, dev):
             f"mean unique experts {sum(uniq) / NL:.1f}")
         del sg
     # the T=4 round with p/q acceptance fused behind the lm_head (temperature 0.7; the draft head's logits of the
-    # round are an input, synthetic here)
+    # round are an input, synthetic here, and the drafts are drawn from q = softmax(draft / 0.7) on the device, the
+    # proposal the p/q rule needs)
+    from slotstream_spark_amd.engine.accept import Acceptor
+
     sg = MTPStepGraph(pool, mw[:NL], lm, 3, head=mw[NL], top_k=K, accept="pq", temperature=0.7, device=dev)
     g2 = torch.Generator(device=dev).manual_seed(2723)
     sg.draft_logits.copy_(torch.randn(sg.draft_logits.shape, generator=g2, device=dev) * 3)
     sg.uniforms.copy_(torch.rand(4, generator=g2, device=dev))
-    drafts = sg.draft_logits.argmax(dim=1).to(torch.int32)
+    drafts = Acceptor(3, N, device=dev).draw_drafts_async(sg.draft_logits, torch.rand(3, generator=g2, device=dev),
+                                                          0.7)
     sg.step(normal_bf16((4, H), 1.0, 2722, dev), drafts)
     for _ in range(2):
         sg.step()
@@ -458,7 +485,8 @@ def step_leg(pool, weights, biases, steps, dev):
     torch.cuda.synchronize()
     us = ev0.elapsed_time(ev1) * 1000.0 / steps
     res["T4_pq"] = {"us_per_round": round(us, 1), "temperature": 0.7, "result": sg.out.cpu().tolist()[:4],
-                    "note": "lm_head GEMV writes logits and chunk maxima; the p/q round reads the logits once"}
+                    "note": "lm_head GEMV writes logits and chunk maxima; the p/q round reads the logits once; "
+                            "drafts drawn from q (ssmoe_sample_rows) before the round, outside the timing"}
     log(f"step graph T=4 with fused p/q: {us:.1f} us per round")
     del sg
     return res
@@ -532,7 +560,7 @@ def draft_leg(pool, weights, biases, steps, dev):
     n_tok = 64
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    out, secs, st = mtp_decode(stack, head1, [21, 22, 23], n_tok)
+    out, _nan, secs, st = mtp_decode(stack, head1, [21, 22, 23], n_tok)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     res["loop"] = {"layers": NL, "depth": 2, "tokens": len(out), "rounds": st["rounds"], "accepted": st["accepted"],
@@ -927,7 +955,7 @@ def main():
 
     c2 = c4 = None
     if "config2" in legs:
-        c2 = config2_leg(pool, weights[0], biases[0], args.config2_steps, dev)
+        c2 = config2_leg(pool, weights, biases, args.config2_steps, dev, n_layers=min(8, NP))
     if "config4" in legs:
         c4 = config4_leg(pool, weights[:args.config4_layers], biases[:args.config4_layers], args.config4_steps, dev)
 

@@ -256,6 +256,17 @@ int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_gen
                  float top_p, int top_k, float min_p, float presence_penalty, const float* u, void* workspace,
                  int64_t workspace_bytes, int32_t* out, void* stream);
 
+/* Bytes of the workspace ssmoe_sample_rows needs (-1 outside 1 <= R <= 64, 1 <= V <= 1,048,576). */
+int64_t ssmoe_sample_rows_workspace_bytes(int R, int V);
+
+/* The draft tokens of a p/q round: x_r ~ softmax(logits[r] / temperature) for the R rows of logits fp32 [R, V],
+ * each drawn as ssmoe_sample with that temperature and no top-k, top-p, min-p or penalty, with uniforms[r]
+ * (tokens int32 [R], on the device). Leviathan et al. 2023 Alg. 1 (ssmoe_accept_pq) requires the drafts to be
+ * drawn from the same q it divides by; the reference drafts greedily (engine/mtp.py:265-277, torch.argmax), which is
+ * the temperature-0 limit and is not a valid proposal for p/q. No reference counterpart. temperature > 0. */
+int ssmoe_sample_rows(const float* logits, int R, int V, float temperature, const float* uniforms, void* workspace,
+                      int64_t workspace_bytes, int32_t* tokens, void* stream);
+
 /* Bytes of the workspace ssmoe_accept_sampled needs (D+1 rows of ssmoe_sample's; -1 on bad arguments). */
 int64_t ssmoe_accept_sampled_workspace_bytes(int D, int V);
 

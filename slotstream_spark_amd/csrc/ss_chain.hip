@@ -1005,6 +1005,8 @@ static hipError_t launch_chain_nj(const ChainArgs& a, hipStream_t st) {
 
 bool chain_shape_supported(int H, int I) { return H == 2048 && I == 512; }
 
+const char* chain_shapes_text() { return "the chain kernel is built for H 2048 with I 512 only"; }
+
 hipError_t launch_chain(const ChainArgs& a, hipStream_t st) {
   // One instantiated shape: H 2048 x I 512, the BASELINE layer (the layer loop is sized to the register file for it);
   // other shapes run one ssmoe_moe_verify_layer_chain launch per layer.

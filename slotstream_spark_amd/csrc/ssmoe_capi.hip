@@ -376,8 +376,8 @@ int ssmoe_moe_verify_chain(const uint16_t* stream_in, float eps, const ssmoe_cha
   if (int rc = check_moe_shape(T, H, I, K, E)) return rc;
   if (T > kBlock) return fail(SSMOE_EINVAL, "a chain takes at most %d tokens, got %d", kBlock, T);
   if (!ss::chain_shape_supported(H, I))
-    return fail(SSMOE_EINVAL, "no chain kernel for H=%d, I=%d (H 1024 with I <= 1024, or H 2048 with I <= 640); "
-                "launch the layers one by one (ssmoe_moe_verify_layer_chain)", H, I);
+    return fail(SSMOE_EINVAL, "no chain kernel for H=%d, I=%d (%s); launch the layers one by one "
+                "(ssmoe_moe_verify_layer_chain)", H, I, ss::chain_shapes_text());
   if (E > 512 || K > E) return fail(SSMOE_EINVAL, "need K <= E <= 512, got K=%d E=%d", K, E);
   if (Is < 8 || Is % 8 || Is > 512) return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, 512], got %d", Is);
   if (n_layers < 1 || n_layers > 4096) return fail(SSMOE_EINVAL, "n_layers must be in [1, 4096], got %d", n_layers);
@@ -763,6 +763,23 @@ int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_gen
   return hip_check(ss::launch_sample(logits, V, generated, n_generated, temperature, top_p, top_k, min_p,
                                      presence_penalty, u, workspace, out, static_cast<hipStream_t>(stream)),
                    "sample launch");
+}
+
+int64_t ssmoe_sample_rows_workspace_bytes(int R, int V) {
+  if (R < 1 || R > 64 || V < 1 || V > (1 << 20)) return -1;
+  return (int64_t)R * ss::sample_workspace_bytes(V);
+}
+
+int ssmoe_sample_rows(const float* logits, int R, int V, float temperature, const float* uniforms, void* workspace,
+                      int64_t workspace_bytes, int32_t* tokens, void* stream) {
+  if (R < 1 || R > 64) return fail(SSMOE_EINVAL, "R must be in [1, 64], got %d", R);
+  if (!(temperature > 0.f) || temperature > 3.4e38f)
+    return fail(SSMOE_EINVAL, "temperature must be finite and > 0 (a proposal is drawn, not taken as the argmax)");
+  if (int rc = check_sample(V, temperature, 1.f, 0, 0.f, 0.f, nullptr, 0, workspace, workspace_bytes, R)) return rc;
+  if (!logits || !uniforms || !tokens) return fail(SSMOE_EINVAL, "logits, uniforms and tokens must be non-null");
+  return hip_check(ss::launch_sample_rows(logits, R, V, temperature, uniforms, workspace, tokens,
+                                          static_cast<hipStream_t>(stream)),
+                   "sample rows launch");
 }
 
 int64_t ssmoe_accept_sampled_workspace_bytes(int D, int V) {

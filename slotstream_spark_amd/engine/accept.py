@@ -5,7 +5,10 @@ Greedy follows the acceptance loop of _mtp_decode (slotstream_spark/engine/gener
 accepts drafts while they equal those tokens and emits tokens 0..good; a row holding a non-finite logit stops the
 round before it (generate.py:210-212). `sampled` is the same loop with the full reference sampler (temperature,
 top-k, top-p, min-p, presence penalty over the tokens seen so far). p/q is Leviathan et al. 2023, Alg. 1, which the
-reference does not have.
+reference does not have. Alg. 1 preserves the target distribution only when each draft token x_i is drawn from the
+q_i it divides by: `draw_drafts_async` draws x_i ~ softmax(draft_i / temperature) on the device (ssmoe_sample_rows)
+and `pq_round` is the whole proposal + acceptance step. The reference's greedy drafts (engine/mtp.py:265-277) are
+the temperature-0 proposal, valid for the greedy round only.
 
 The uniforms come from the reference sampler's splitmix64 stream (engine/sampler.py:20-24, 101-102), drawn on the
 host: decision i consumes uniforms[i], the final sample the next one; `n_uniform` reports how many were used, so
@@ -74,6 +77,7 @@ class Acceptor:
         self.work = torch.zeros(int(nb), dtype=torch.uint8, device=device)  # header zero before the first call
         self.out = torch.empty(depth + 5, dtype=torch.int32, device=device)
         self._swork = None
+        self._dwork = None
 
     def _check(self, target, draft=None):
         d, v = self.depth, self.vocab
@@ -106,6 +110,41 @@ class Acceptor:
                                               self.work.data_ptr(), self.work.numel(), self.out.data_ptr(),
                                               _lib.stream_of(target)))
         return self.out
+
+    def draw_drafts_async(self, draft, uniforms, temperature: float, out=None) -> torch.Tensor:
+        """x_i ~ softmax(draft[i] / temperature) for the D draft rows with uniforms[i] (fp32 [D] on the device) ->
+        int32 [D] on the device: the proposal of the p/q round (ssmoe_sample_rows, the reference sampler's draw with
+        no filter)."""
+        d, v = self.depth, self.vocab
+        if draft.dtype != torch.float32 or tuple(draft.shape) != (d, v) or not draft.is_contiguous():
+            raise ValueError(f"draft must be contiguous fp32 [{d}, {v}]")
+        if uniforms.dtype != torch.float32 or uniforms.numel() < d or not uniforms.is_contiguous():
+            raise ValueError(f"uniforms must be contiguous fp32 [{d}]")
+        if not temperature > 0:
+            raise ValueError("temperature must be > 0")
+        out = torch.empty(d, dtype=torch.int32, device=draft.device) if out is None else out
+        if out.dtype != torch.int32 or out.numel() != d or not out.is_contiguous():
+            raise ValueError(f"out must be contiguous int32 [{d}]")
+        if d == 0:
+            return out
+        if self._dwork is None:
+            nb = int(_lib.lib().ssmoe_sample_rows_workspace_bytes(d, v))
+            self._dwork = torch.empty(nb, dtype=torch.uint8, device=draft.device)
+        _lib.check(_lib.lib().ssmoe_sample_rows(draft.data_ptr(), d, v, float(temperature), uniforms.data_ptr(),
+                                                self._dwork.data_ptr(), self._dwork.numel(), out.data_ptr(),
+                                                _lib.stream_of(draft)))
+        return out
+
+    def pq_round(self, target, draft, stream: UniformStream, temperature: float):
+        """One speculative-sampling round (Leviathan et al. 2023, Alg. 1) as a drafter and verifier run it: the D
+        drafts are drawn from q_i = softmax(draft_i / temperature) with the stream's next D uniforms (the draft
+        phase), then the p/q round consumes its uniforms from the stream -> (drafts int32 [D] on the device,
+        AcceptResult)."""
+        d = self.depth
+        ud = torch.from_numpy(stream.peek(d)).to(target.device)
+        stream.advance(d)
+        drafts = self.draw_drafts_async(draft, ud, temperature)
+        return drafts, self.pq(target, draft, drafts, stream, temperature)
 
     def sampled_async(self, target, drafts, params, seen=(), uniforms=None) -> torch.Tensor:
         """Launch the sampled round; returns the device output int32 [D+5]. `params` is a SampleParams (sanitized

@@ -40,6 +40,9 @@ class MoEStack:
         self.depth, self.rows, self.nl = depth, depth + 1, len(layers)
         self.embed, self.max_ctx, self.device = embed, max_ctx, torch.device(device)
         self.argmax = LMHeadArgmax(lm_head, max_rows=self.rows, round_bf16=True, device=device)
+        # the plain steps' logits, kept for the finiteness check of _mtp_decode's plain loop (generate.py:186-189)
+        self.plain_logits = torch.empty((self.rows, lm_head.n), dtype=torch.float32, device=self.device)
+        self.last_finite: list[bool] = []
         self.tok_rows = torch.zeros(self.rows, dtype=torch.int32, device=self.device)
         self.row_ids = torch.zeros(self.rows, dtype=torch.int32, device=self.device)
         self.st = rb.SeqState()
@@ -75,36 +78,43 @@ class MoEStack:
 
     def forward(self, tokens: list[int]) -> tuple[list[int], torch.Tensor]:
         """Plain steps over `tokens` (at most `rows` at a time): -> (the greedy next token after each, their final
-        stream rows [len, H]). Advances the position by len(tokens)."""
-        nxt, multi = [], []
+        stream rows [len, H]). Advances the position by len(tokens). `last_finite[i]` says whether row i's logits
+        were all finite (a non-finite row's token is torch.argmax's, NaN counting as the maximum)."""
+        nxt, multi, fin = [], [], []
         for c0 in range(0, len(tokens), self.rows):
             chunk = [int(t) for t in tokens[c0:c0 + self.rows]]
             self._pass(chunk)
             g = self.graph
-            self.argmax(g.mixed[self.nl], ids=self.row_ids)
+            self.argmax(g.mixed[self.nl], ids=self.row_ids, logits=self.plain_logits)
             nxt += self.row_ids.cpu().tolist()[:len(chunk)]
+            fin += torch.isfinite(self.plain_logits[:len(chunk)]).all(dim=1).cpu().tolist()
             multi.append(self.multi[:len(chunk)].clone())
             self.st.pos += len(chunk)
             self.st.tokens += chunk
+        self.last_finite = [bool(f) for f in fin]
         return nxt, torch.cat(multi, 0)
 
 
 def mtp_decode(stack: MoEStack, head: mtp_mod.MTPHead, prompt: list[int], max_tokens: int, eos=(), on_token=None,
                draft_fn=None):
-    """Greedy self-speculative decode after `prompt` -> (tokens, round_seconds, stats), the stats of _mtp_decode.
-    `draft_fn(pending, depth, n_out)` replaces the head's drafts when given (as in the reference)."""
+    """Greedy self-speculative decode after `prompt` -> (tokens, nan, round_seconds, stats), as _mtp_decode.
+    `draft_fn(pending, depth, n_out)` replaces the head's drafts when given (as in the reference). Non-finite logits
+    end the loop as in the reference (generate.py:163-164, 186-189, 210-212): no token for that row, `nan` True, and
+    a verify round that met one still rolls back to its good rows and feeds them to the head before returning."""
     D = stack.depth
-    out, step_s = [], []
+    out, step_s, nan = [], [], False
     st = {"rounds": 0, "plain_steps": 0, "drafted": 0, "accepted": 0, "attempts_by_depth": [0] * D,
           "accepted_by_depth": [0] * D, "emitted_by_round": [], "verify_rows": 0}
     nxt, multi = stack.forward(prompt)
     head.consume(prompt, multi)
+    if not stack.last_finite[-1]:
+        return out, True, step_s, st
     tok = nxt[-1]
     out.append(tok)
     if on_token:
         on_token(tok)
     if tok in eos or len(out) == max_tokens:
-        return out, step_s, st
+        return out, nan, step_s, st
     pending, use_mtp = tok, True
     while len(out) < max_tokens:
         if use_mtp:
@@ -119,6 +129,9 @@ def mtp_decode(stack: MoEStack, head: mtp_mod.MTPHead, prompt: list[int], max_to
             tok = stack.forward([pending])[0][0]
             step_s.append(time.perf_counter() - t1)
             st["plain_steps"] += 1
+            if not stack.last_finite[0]:
+                nan = True
+                break
             out.append(tok)
             if on_token:
                 on_token(tok)
@@ -129,8 +142,6 @@ def mtp_decode(stack: MoEStack, head: mtp_mod.MTPHead, prompt: list[int], max_to
         drafts = [int(d) for d in (draft_fn(pending, D, len(out)) if draft_fn else head.draft(pending, D))]
         ck = rb.checkpoint(stack)
         res = stack.step([pending] + drafts)
-        if res.flags & 1 and res.n_emit == 0:
-            raise FloatingPointError("non-finite logits in the first verify row")
         st["rounds"] += 1
         st["drafted"] += len(drafts)
         st["verify_rows"] += 1 + len(drafts)
@@ -152,7 +163,8 @@ def mtp_decode(stack: MoEStack, head: mtp_mod.MTPHead, prompt: list[int], max_to
             nextp = tok
             break
         if nextp is None and not done:
-            raise FloatingPointError("non-finite logits in a verify row")
+            # the greedy round stopped at a non-finite row (flags bit 1): no token for it, as the reference's loop
+            nan, done = True, True
         st["accepted"] += good
         st["emitted_by_round"].append(len(out) - before)
         keep = 1 + good
@@ -162,4 +174,4 @@ def mtp_decode(stack: MoEStack, head: mtp_mod.MTPHead, prompt: list[int], max_to
         if done:
             break
         pending = nextp
-    return out, step_s, st
+    return out, nan, step_s, st

@@ -12,6 +12,23 @@ named live tensor of the sequence state it holds `rows` snapshots, the pass writ
 (those are outside it), so its record is empty and a rollback is position and token bookkeeping; a stack with state
 registers it here. `restore_async` takes `keep` as a device int32 (the n_emit of a greedy round's result vector)
 and restores with the row-gather kernel, so a captured round can roll back without reading the decision.
+
+`Checkpoint`, `checkpoint()` and `rollback()` follow fortil/slotstream-spark engine/rollback.py:15-41 (fields, body,
+checks and error strings: the drop-in contract). That file, itself a port of slotstream's Generate.swift and
+Model.swift (MIT, Copyright (c) 2026 Carlos Galarza), is under the MIT License:
+
+    Copyright (c) 2026 William Penagos
+
+    Permission is hereby granted, free of charge, to any person obtaining a copy of this software and associated
+    documentation files (the "Software"), to deal in the Software without restriction, including without limitation
+    the rights to use, copy, modify, merge, publish, distribute, sublicense, and/or sell copies of the Software, and
+    to permit persons to whom the Software is furnished to do so, subject to the following conditions: The above
+    copyright notice and this permission notice shall be included in all copies or substantial portions of the
+    Software. THE SOFTWARE IS PROVIDED "AS IS", WITHOUT WARRANTY OF ANY KIND, EXPRESS OR IMPLIED, INCLUDING BUT NOT
+    LIMITED TO THE WARRANTIES OF MERCHANTABILITY, FITNESS FOR A PARTICULAR PURPOSE AND NONINFRINGEMENT. IN NO EVENT
+    SHALL THE AUTHORS OR COPYRIGHT HOLDERS BE LIABLE FOR ANY CLAIM, DAMAGES OR OTHER LIABILITY, WHETHER IN AN ACTION
+    OF CONTRACT, TORT OR OTHERWISE, ARISING FROM, OUT OF OR IN CONNECTION WITH THE SOFTWARE OR THE USE OR OTHER
+    DEALINGS IN THE SOFTWARE.
 """
 from __future__ import annotations
 

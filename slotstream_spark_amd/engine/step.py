@@ -74,7 +74,13 @@ class MTPStepGraph:
     `fused` folds each norm and residual add into the verify launches (`mixed[l]` for l < NL then not written): one
     launch for all layers (ssmoe_moe_verify_chain) where the shape has a chain kernel and `single_launch`, else one
     ssmoe_moe_verify_layer_chain launch per layer; `fused=False` runs ssmoe_residual_rmsnorm between the layers. All
-    give the same bits. `lm_head=None` leaves the lm_head and the acceptance out of the graph."""
+    give the same bits. `lm_head=None` leaves the lm_head and the acceptance out of the graph.
+
+    `accept="pq"` fuses the p/q round (Leviathan et al. 2023, Alg. 1) instead of the greedy one. Its inputs are the
+    draft head's logits of the round (`draft_logits` [depth, V]), the round's uniforms and drafts drawn from
+    q = softmax(draft_logits / temperature): the rule divides by q(x), so it preserves the target distribution only
+    for drafts drawn from q. `draw_drafts(uniforms)` draws them into `drafts` on the device (ssmoe_sample_rows);
+    argmax drafts (the greedy proposal) belong to the greedy round."""
 
     def __init__(self, pool, layers: list[MoEWeights], lm_head: AffineWeight, depth: int,
                  head: MoEWeights | None = None, norm_weights: list[torch.Tensor | None] | None = None,
@@ -129,6 +135,8 @@ class MTPStepGraph:
         if accept not in ("greedy", "pq"):
             raise ValueError(f"accept must be 'greedy' or 'pq', got {accept!r}")
         self.accept = accept
+        self.temperature = float(temperature)
+        self._drawer = None
         self.draft_logits = self.uniforms = None
         if lm_head is None:
             self.lm_head = None
@@ -198,6 +206,16 @@ class MTPStepGraph:
         self.graph.replay()
         cur.wait_stream(self.stream)
         return self.out
+
+    def draw_drafts(self, uniforms: torch.Tensor) -> torch.Tensor:
+        """p/q rounds: draft token i ~ softmax(draft_logits[i] / temperature) with uniforms[i] (fp32 [depth] on the
+        device) into `drafts`, on the current stream, before step() (the draft head's side of the round)."""
+        if self.accept != "pq":
+            raise ValueError("draw_drafts belongs to accept='pq' rounds; greedy rounds take argmax drafts")
+        if self._drawer is None:
+            from .accept import Acceptor
+            self._drawer = Acceptor(self.depth, self.draft_logits.shape[1], device=self.device)
+        return self._drawer.draw_drafts_async(self.draft_logits, uniforms, self.temperature, out=self.drafts)
 
     def result(self) -> AcceptResult:
         torch.cuda.current_stream(self.device).synchronize()

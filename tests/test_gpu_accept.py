@@ -97,3 +97,61 @@ def test_pq_small_vocab_edge(acc):
         out = small.pq_async(torch.from_numpy(t).cuda(), torch.from_numpy(q).cuda(), torch.from_numpy(d).cuda(),
                              torch.from_numpy(u).cuda(), 0.7).cpu().numpy()
         assert np.array_equal(out, O.accept_pq(t, q, d, u, 0.7)), i
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_draw_drafts_bitexact(acc, seed):
+    """The proposal draw of the p/q round (ssmoe_sample_rows): row i's token is the reference sampler's draw at the
+    round's temperature with no filter and uniforms[i], bit for bit against the C definition."""
+    _, drf = verify_logits(D, V, 7000 + seed)
+    u = UniformStream(100 + seed).peek(D)
+    got = acc.draw_drafts_async(drf, torch.from_numpy(u).cuda(), 0.7).cpu().numpy()
+    q = drf.cpu().numpy()
+    want = [O.sample(q[i], [], 0.7, 1.0, 0, 0.0, 0.0, u[i])[0] for i in range(D)]
+    assert got.tolist() == want
+
+
+def _chi2(counts, probs):
+    n = counts.sum()
+    e = probs * n
+    return float(((counts - e) ** 2 / e).sum())
+
+
+def test_pq_round_preserves_the_target_distribution():
+    """The p/q path as wired (drafts drawn from q = softmax(draft / T) by ssmoe_sample_rows, then ssmoe_accept_pq):
+    the first emitted token is distributed as p_0 = softmax(target_0 / T), and the token after an accepted first
+    draft as p_1 (Leviathan et al. 2023, Theorem 1), by chi-square over 8000 seeded rounds on a 6-token vocabulary.
+    Critical value 25.7 = the 1e-4 tail of chi-square with 5 degrees of freedom; the argmax-draft procedure this
+    replaces fails the same check on the CPU (tests/test_oracle.py)."""
+    Dd, Vs, N, T = 2, 6, 8000, 0.7
+    t = np.array([[1.2, 0.9, 0.2, -0.1, -0.8, 0.4], [0.1, 1.0, -0.5, 0.6, 0.3, -1.2], [0.0, 0.2, 0.4, 0.6, 0.8, 1.0]],
+                 np.float32)
+    q = np.array([[0.2, 1.6, 0.1, 0.3, -0.6, 0.9], [1.1, 0.2, 0.0, -0.4, 0.9, 0.1]], np.float32)
+    small = Acceptor(Dd, Vs)
+    g = torch.Generator(device="cuda").manual_seed(4242)
+    ud = torch.rand((N, Dd), generator=g, device="cuda")
+    ua = torch.rand((N, Dd + 1), generator=g, device="cuda")
+    tt, qq = torch.from_numpy(t).cuda(), torch.from_numpy(q).cuda()
+    drafts = torch.empty((N, Dd), dtype=torch.int32, device="cuda")
+    res = torch.empty((N, Dd + 5), dtype=torch.int32, device="cuda")
+    for i in range(N):
+        small.draw_drafts_async(qq, ud[i], T, out=drafts[i])
+        res[i].copy_(small.pq_async(tt, qq, drafts[i], ua[i], T))
+    r = res.cpu().numpy()
+    assert (r[:, 3] == 0).all() and (r[:, 1] >= 1).all()
+
+    def p_of(row):
+        z = np.exp((row.astype(np.float64) / T) - (row.astype(np.float64) / T).max())
+        return z / z.sum()
+
+    c0 = np.bincount(r[:, 4], minlength=Vs).astype(np.float64)
+    x0 = _chi2(c0, p_of(t[0]))
+    sel = r[:, 0] >= 1
+    c1 = np.bincount(r[sel, 5], minlength=Vs).astype(np.float64)
+    x1 = _chi2(c1, p_of(t[1]))
+    # the drafts themselves follow q (the proposal is what Alg. 1 divides by)
+    cq = np.bincount(drafts[:, 0].cpu().numpy(), minlength=Vs).astype(np.float64)
+    xq = _chi2(cq, p_of(q[0]))
+    print(f"chi2 first token {x0:.2f}, second token ({int(sel.sum())} rounds) {x1:.2f}, drafts vs q {xq:.2f}; "
+          f"mean accepted {r[:, 0].mean():.3f}")
+    assert x0 < 25.7 and x1 < 25.7 and xq < 25.7

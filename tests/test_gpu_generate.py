@@ -30,8 +30,7 @@ def _lm_head(seed):
     return AffineWeight(q, sc, (-8 * sc.float()).to(torch.bfloat16), 4, 64, V, H)
 
 
-@pytest.fixture(scope="module")
-def model():
+def _build(E, K):
     print(f"[generate] NL={NL} E={E} K={K} V={V} depth={D}", flush=True)
     pool = make_pool(E, H, I, seed=800, layers=NL + 1)
     lws = [LayerWeights(H, E, 512, seed=801 + l) for l in range(NL + 1)]
@@ -55,6 +54,17 @@ def model():
         return f[t]
 
     return make, nxt
+
+
+@pytest.fixture(scope="module")
+def model():
+    return _build(E, K)
+
+
+@pytest.fixture(scope="module")
+def model512():
+    """The BASELINE layer shape (512 experts, top-10): the round's layers run as one ssmoe_moe_verify_chain launch."""
+    return _build(512, 10)
 
 
 def _chain(nxt, first, n):
@@ -83,8 +93,8 @@ def test_loop_emits_the_plain_greedy_chain(model, mode):
             return [right[0], (right[1] + 1) % V]
         return [(t + 1) % V for t in right]
 
-    out, secs, st = mtp_decode(stack, head, prompt, n, draft_fn=None if mode == "head" else draft_fn)
-    assert out == want
+    out, nan, secs, st = mtp_decode(stack, head, prompt, n, draft_fn=None if mode == "head" else draft_fn)
+    assert out == want and not nan
     assert st["rounds"] == len(st["emitted_by_round"]) and sum(st["emitted_by_round"]) == len(out) - 1
     if mode == "right":
         assert all(e == D + 1 for e in st["emitted_by_round"][:-1]) and st["accepted"] >= st["drafted"] - D
@@ -100,11 +110,37 @@ def test_loop_emits_the_plain_greedy_chain(model, mode):
     assert stack.record.outstanding == 0
 
 
+@pytest.mark.parametrize("mode", ["head", "mixed"])
+def test_loop_through_the_single_launch_chain(model512, mode):
+    """At E 512 / K 10 the verify rounds (rows = DEPTH + 1 = 3, the reference's width) go through the chain kernel
+    and the loop still emits the plain greedy chain of one-row steps."""
+    make, nxt = model512
+    print(f"[generate] E=512 chain drafts={mode}", flush=True)
+    stack, head = make()
+    assert stack.graph.chain is not None, "the E 512 stack must run its rounds through ssmoe_moe_verify_chain"
+    prompt, n = [7, 1234], 12
+    want = _chain(nxt, nxt(prompt[-1]), n)
+    calls = []
+
+    def draft_fn(pending, depth, n_out):
+        calls.append(n_out)
+        right = _chain(nxt, nxt(pending), depth)
+        return right if len(calls) % 2 else [right[0], (right[1] + 1) % V]
+
+    out, nan, _, st = mtp_decode(stack, head, prompt, n, draft_fn=None if mode == "head" else draft_fn)
+    assert out == want and not nan
+    assert st["rounds"] > 0 and sum(st["emitted_by_round"]) == len(out) - 1
+    if mode == "mixed":
+        assert 0 < st["accepted"] < st["drafted"]
+    assert stack.st.pos == len(prompt) + len(out) - 1
+    assert head.state.aligned(head.consumed) and head.consumed == stack.st.pos
+
+
 def test_loop_switches_to_plain_steps_near_the_context_end(model):
     make, nxt = model
     stack, head = make(max_ctx=9)
     prompt = [42]
-    out, _, st = mtp_decode(stack, head, prompt, 30)
+    out, nan, _, st = mtp_decode(stack, head, prompt, 30)
     assert out == _chain(nxt, nxt(42), len(out))
     assert st["plain_steps"] > 0 and stack.st.pos <= 9
 

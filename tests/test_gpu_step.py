@@ -172,10 +172,11 @@ def test_head_moe_is_map_layer_nl(step):
     assert np.array_equal(sg.head_ids.cpu().numpy(), rids)
 
 
-@pytest.mark.parametrize("T,NL4", [(2, 4), (4, 3)])
+@pytest.mark.parametrize("T,NL4", [(2, 4), (3, 3), (4, 3)])
 def test_chain_at_config4_layer_shape(T, NL4):
-    """BASELINE config 4's layer (E=512, top-10, Zipf bias, I 512, shared 512) chained, T = 2 (config 4) and T = 4
-    (config 2's rows), replayed twice with different inputs: the single launch of every layer
+    """BASELINE config 4's layer (E=512, top-10, Zipf bias, I 512, shared 512) chained, T = 2 (config 4), T = 3 (the
+    reference's verify width, 1 + DEPTH rows: engine/mtp.py:48, runtime/graphs.py:95-96) and T = 4 (config 2's rows),
+    replayed twice with different inputs: the single launch of every layer
     (ssmoe_moe_verify_chain) equals one launch per layer bit for bit, and each layer matches the oracle on its own
     input (ids and weights bit for bit, y within the north-star bound, the stream and the final norm bit for bit)."""
     E4, K4 = 512, 10
@@ -214,8 +215,48 @@ def test_chain_at_config4_layer_shape(T, NL4):
               f"{[len(set(sg.ids[l].cpu().flatten().tolist())) for l in range(NL4)]}", flush=True)
 
 
+@pytest.mark.parametrize("T", [2, 3])
+def test_chain_of_16_layers_equals_per_layer_launches(T):
+    """The chain as the bench times it: 16 distinct config-1 layers (E 512, top-10, Zipf bias) in one launch, three
+    replays with new inputs, every layer's ids, weights, y and stream equal to one launch per layer bit for bit, and
+    the last layer against the oracle on its own input."""
+    E4, K4, NL16 = 512, 10, 16
+    print(f"[chain 16] {NL16} layers, E={E4} K={K4} T={T}", flush=True)
+    pool = make_pool(E4, H, I, seed=605, layers=NL16)
+    lws = [LayerWeights(H, E4, 512, seed=610 + l) for l in range(NL16)]
+    mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, zipf_bias(E4, 1.1, 640 + l))
+          for l, w in enumerate(lws)]
+    norms = [normal_bf16((H,), 0.1, 660 + l) + 1 for l in range(NL16 + 1)]
+    sg = MTPStepGraph(pool, mw, None, depth=T - 1, norm_weights=norms, top_k=K4)
+    per_layer = MTPStepGraph(pool, mw, None, depth=T - 1, norm_weights=norms, top_k=K4, single_launch=False)
+    assert sg.chain is not None
+    for trial in range(3):
+        x = normal_bf16((T, H), 1.0, 680 + trial)
+        per_layer.step(x)
+        sg.step(x)
+        torch.cuda.synchronize()
+        for l in range(NL16):
+            assert torch.equal(sg.ids[l], per_layer.ids[l]) and torch.equal(sg.weights[l], per_layer.weights[l]), \
+                (trial, l)
+            assert torch.equal(sg.ys[l], per_layer.ys[l]) and torch.equal(sg.streams[l + 1], per_layer.streams[l + 1]), \
+                (trial, l)
+    l = NL16 - 1
+    xb = O.residual_rmsnorm(bits(sg.streams[l]), None, bits(norms[l]))[1]
+    w = mw[l]
+    _, _, rids, rw = O.router(xb, bits(w.router_w), K4, w.router_bias.cpu().numpy())
+    assert np.array_equal(sg.ids[l].cpu().numpy(), rids)
+    assert np.array_equal(sg.weights[l].cpu().numpy().view(np.uint32), rw.view(np.uint32))
+    routed = O.moe_routed_fp64(O.bf16_to_f32(xb), rids, rw, DenseCache(pool, layer=l)).astype(np.float32)
+    sh, sgl = O.shared_expert(xb, bits(w.sh_gate), bits(w.sh_up), bits(w.sh_down), bits(w.sh_g))
+    err = O.rel_l2(O.bf16_to_f32(bits(sg.ys[l])), O.bf16_to_f32(O.combine_shared(routed, sh, sgl)))
+    assert err <= REL_Y, err
+    del pool, sg, per_layer
+    torch.cuda.empty_cache()
+
+
 def test_pq_round_in_the_step_graph(step):
-    """The round with p/q acceptance fused behind the lm_head (accept="pq"): its logits are the greedy graph's on the
+    """The round with p/q acceptance fused behind the lm_head (accept="pq"), drafts drawn from q by draw_drafts (the
+    proposal the rule needs): the drafts equal the sampler's definition, the logits are the greedy graph's on the
     same rows, and every replay's result equals ssmoe_accept_pq on those logits."""
     from slotstream_spark_amd.engine.accept import Acceptor
 
@@ -229,7 +270,10 @@ def test_pq_round_in_the_step_graph(step):
         torch.cuda.synchronize()
         pq.draft_logits.copy_(0.8 * sg.logits[:3] + torch.randn((3, V), generator=g, device="cuda") * 1.8)
         pq.uniforms.copy_(torch.rand(4, generator=g, device="cuda"))
-        drafts = pq.draft_logits.argmax(dim=1).to(torch.int32)
+        ud = torch.rand(3, generator=g, device="cuda")
+        drafts = pq.draw_drafts(ud).clone()
+        ql, un = pq.draft_logits.cpu().numpy(), ud.cpu().numpy()
+        assert drafts.cpu().tolist() == [O.sample(ql[i], [], 0.7, 1.0, 0, 0.0, 0.0, un[i])[0] for i in range(3)]
         out = pq.step(x, drafts).clone()
         torch.cuda.synchronize()
         assert torch.equal(pq.logits, sg.logits), rep

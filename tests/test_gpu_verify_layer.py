@@ -31,8 +31,8 @@ def _oracle_y(pool, lw, x, k, bias):
     return ids, w, routed, O.combine_shared(routed, sh, sgl)
 
 
-@pytest.mark.parametrize("experts,k,bias,t", [(64, 4, False, 2), (512, 10, True, 2), (512, 10, True, 4),
-                                             (512, 10, False, 1)])
+@pytest.mark.parametrize("experts,k,bias,t", [(64, 4, False, 2), (512, 10, True, 2), (512, 10, True, 3),
+                                             (512, 10, True, 4), (512, 10, False, 1)])
 def test_verify_layer_vs_oracle(experts, k, bias, t):
     print(f"[verify] E={experts} K={k} bias={bias} T={t}", flush=True)
     pool, lw, layer, b = _layer(experts, k, 1729 + experts, bias)

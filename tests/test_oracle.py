@@ -332,6 +332,28 @@ def test_accept_pq_emits_target_distribution():
     assert abs(acc / n - expect_acc) < 0.015
 
 
+def test_accept_pq_with_sampled_drafts_and_the_argmax_control():
+    """The p/q path as wired, on the CPU: the draft drawn by the sampler's definition (orc.sample at the round's
+    temperature, no filter, its own uniform), then accept_pq: the first token is distributed as p. The argmax draft
+    (the greedy proposal) fed to the same rule over the same uniforms is biased towards the draft token, and the same
+    chi-square check rejects it by far: the check can see that wiring mistake."""
+    V, temp, n = 6, 0.7, 12_000
+    tl = np.array([[1.2, 0.9, 0.2, -0.1, -0.8, 0.4], [0.1, 1.0, -0.5, 0.6, 0.3, -1.2]], np.float32)
+    dl = np.array([[0.2, 1.6, 0.1, 0.3, -0.6, 0.9]], np.float32)
+    p = _softmax64(tl[0], temp)
+    u = orc.uniforms(77, 3 * n).reshape(n, 3)
+    c_s, c_a = np.zeros(V), np.zeros(V)
+    am = np.array([int(np.argmax(dl[0]))], np.int32)
+    for i in range(n):
+        x = orc.sample(dl[0], [], temp, 1.0, 0, 0.0, 0.0, u[i, 2])[0]
+        c_s[orc.accept_pq(tl, dl, np.array([x], np.int32), u[i, :2], temp)[4]] += 1
+        c_a[orc.accept_pq(tl, dl, am, u[i, :2], temp)[4]] += 1
+    chi_s = float(((c_s - n * p) ** 2 / (n * p)).sum())
+    chi_a = float(((c_a - n * p) ** 2 / (n * p)).sum())
+    assert chi_s < 25.0, (chi_s, c_s / n, p)
+    assert chi_a > 500.0, (chi_a, c_a / n, p)
+
+
 def test_accept_pq_equal_distributions_always_accept():
     rng = np.random.default_rng(4)
     V, D = 50, 3
