@@ -69,6 +69,9 @@ def test_dense_gemm_rows_do_not_depend_on_the_call():
 
 
 def test_prefill_router_against_reference_cpu_router():
+    """The prefill router's logits (MFMA accumulation order) against the reference's CPU router (torch F.linear in
+    bf16, then the routing) at config 3: the contract is that a row may select other experts only at a tie within
+    that row's logit difference (asserted for every such row); on this committed seed no row does (asserted)."""
     T, H, E, K = 2048, 2048, 512, 10
     print(f"[prefill router] T={T} E={E} K={K}", flush=True)
     x = normal_bf16((T, H), 1.0, 1730)
@@ -94,4 +97,4 @@ def test_prefill_router_against_reference_cpu_router():
     print(f"{diff_logits} of {mine.size} logits differ from torch's (max {int(steps.max())} bf16 step(s), near zero); "
           f"{n_rows} of {T} rows select otherwise, each at a tie within that difference")
     assert diff_logits <= 2e-3 * mine.size
-    assert n_rows <= 0.01 * T
+    assert n_rows == 0
