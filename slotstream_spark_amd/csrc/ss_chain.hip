@@ -27,6 +27,16 @@ namespace ss {
 
 namespace {
 
+// Chain counters have one shard per lane of the wave that polls them (64), and each wave adds to shard
+// (4 * workgroup + wave) % 64: with about a thousand waves signalling the items at once, 16 shards queued some 60
+// atomic adds on each line at the memory-side atomic unit, which delayed the moment the count was complete.
+constexpr int kCShards = 64;
+SS_DEV int* cshard(int* ctr, int c, int s) { return ctr + (c * kCShards + s) * kShardStride; }
+SS_DEV void csignal_add(int* ctr, int c, int v, int who) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __hip_atomic_fetch_add(cshard(ctr, c, who % kCShards), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 struct CLayout {
   size_t ctr, logits, sw, shx, gsh, ush, sgl, hfrag, hsum8, total;
 };
@@ -36,7 +46,7 @@ __host__ __device__ inline CLayout clayout(int T, int H, int I, int Is, int K, i
   CLayout l;
   size_t o = 0;
   l.ctr = o;
-  o = al256(o + (size_t)CTR_COUNT * kShards * kShardStride * 4);
+  o = al256(o + (size_t)CTR_COUNT * kCShards * kShardStride * 4);
   l.logits = o;  // [2][kTBv][E] words: tag << 32 | bf16 logit
   o = al256(o + (size_t)2 * kTBv * E * 8);
   l.sw = o;  // [2][kTBv][H / 2] words: tag << 32 | two bf16 of the stream
@@ -285,10 +295,10 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   auto dead = [&]() { return __hip_atomic_load(&s_dead, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0; };
   // One full wave waits until the shards of counter c sum to at least target (the order of wait_ge).
   auto wait_ctr = [&](int c, int target) {
-    int* p = shard(ctr, c, lane < kShards ? lane : 0);
+    int* p = cshard(ctr, c, lane);
     for (int it = 0;; ++it) {
       if (dead()) break;
-      const int v = lane < kShards ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0;
+      const int v = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       const int total = (int)ss_butterfly((uint32_t)v, [](uint32_t x, uint32_t y) { return x + y; });
       if (total >= target) break;
       if (it >= kChainSpin) {
@@ -300,7 +310,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   };
   const int nt = T;
   const CDLayout D = cdlayout(T, H, I, Is, K, E);
-  const uint32_t tag0 = (uint32_t)ld_ag(shard(ctr, CTR_EPOCH, 0)) + 1u;  // layer l's tag: tag0 + l
+  const uint32_t tag0 = (uint32_t)ld_ag(cshard(ctr, CTR_EPOCH, 0)) + 1u;  // layer l's tag: tag0 + l
   constexpr int NJX = NJG / 4;
   constexpr int NV = kMaxEv / 64;
   const int J = E + Is, W = G * 4;
@@ -414,9 +424,16 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
     if (tid == 0) s.nt = nt;
 
     // ---------------------------------------------------------- x: the stream of the previous layer
-    const uint16_t* xsrc = a.stream_in;
-    bool norm = a.norm_in != 0;
-    if (l > 0) {
+    // Always staged from the LDS copy, so that every read of x below is an LDS read (a read through a pointer that
+    // may be global is a flat access, which waits for every load the wave has in flight, the next layer's prefetches
+    // included).
+    const bool norm = l > 0 || a.norm_in != 0;
+    if (l == 0) {
+      const int nw = nt * (H >> 3);  // 16-byte words of the input rows
+      uint4* dst = reinterpret_cast<uint4*>(scopy);
+      for (int idx = tid; idx < nw; idx += 256) dst[idx] = ldg16(a.stream_in + 8 * (size_t)idx);
+      __syncthreads();
+    } else {
       // Copy the previous layer's stream words into LDS as plain bf16 [T][H], polling until each word carries that
       // layer's tag.
       const uint64_t* src = sw_all + (size_t)((l - 1) & 1) * kTBv * (H / 2);
@@ -453,9 +470,8 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       }
       SS_TRACE(5);
       __syncthreads();
-      xsrc = scopy;
-      norm = true;
     }
+    const uint16_t* xsrc = scopy;
     if (w == 2) __builtin_amdgcn_s_waitcnt(0);  // the norm weights have landed in LDS
     stage_x_src<NJG>(xsrc, norm, lp.norm_w ? nwl : nullptr, a.eps, H, xfl, s.gx, s.rnorm, nt);
     // The residual stream value of the combine's (row, token), read before the shared region is reused.
@@ -503,7 +519,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
     auto publish_shared = [&]() {
       if (ns) {
         stores_done();
-        if (lane == 0) signal_add(ctr, CTR_SHARED, ns);
+        if (lane == 0) csignal_add(ctr, CTR_SHARED, ns, 4 * bid + w);
       }
     };
     if (w >= nt) publish_shared();
@@ -533,8 +549,8 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
     __syncthreads();
     SS_TRACE(3);
     if (bid == 0 && tid < nt * K) {
-      lp.ids[tid] = s.ids[tid];
-      lp.weights[tid] = s.wts[tid];
+      gp(lp.ids)[tid] = s.ids[tid];
+      gp(lp.weights)[tid] = s.wts[tid];
     }
     if (tid < 64) {
       unique_setup(va, s, true);
@@ -717,7 +733,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
         run_items(std::integral_constant<int, kTBv>{});
       // Each wave publishes its own items as soon as its stores are acknowledged.
       stores_done();
-      if (lane == 0) signal_add(ctr, CTR_ITEMS, wave_items);
+      if (lane == 0) csignal_add(ctr, CTR_ITEMS, wave_items, 4 * bid + w);
     }
     SS_TRACE(7);
 
@@ -867,16 +883,15 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
             acc[r] = ss_rows_sum(acc[r]);
             if (g == 0) partl[((size_t)u * 16 + n) * kTBv + r] = acc[r];
           }
-          // The shared rows are formed while the experts run: a word that was not yet this layer's is requested
-          // again after each of wave 0's experts (one round trip each), so that a fresh one has landed by the combine.
-          if (w == 0 && tid < 16 * kTBv && (tid & 3) < nt && (uint32_t)(shx_w >> 32) != tag)
-            shx_w = ld_ag(shx + shx_i);
         };
         using Two = std::integral_constant<int, 2>;
         using Four = std::integral_constant<int, kTBv>;
         if (D.stage_h && nt <= 2) {
 #pragma unroll 1
-          for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::true_type{}, Two{});
+          for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) {
+            expert(u, std::true_type{}, Two{});
+            if (u < 12) SS_TRACE(16 + 11 + (u >> 2));
+          }
         } else if (D.stage_h) {
 #pragma unroll 1
           for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::true_type{}, Four{});
@@ -885,6 +900,10 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
           for (int u = u0 + w; u < nu && u < u0 + D.P; u += 4) expert(u, std::false_type{}, Four{});
         }
       }
+      // No global load is issued inside the expert loop: a load in flight there makes every LDS read of the loop
+      // wait for it (the loop's reads may alias the direct-to-LDS prefetch, so the compiler waits for all loads).
+      // The shared word is requested again here, if the first request (issued with the h staging) was stale.
+      if (w == 0 && tid < 16 * kTBv && (tid & 3) < nt && (uint32_t)(shx_w >> 32) != tag) shx_w = ld_ag(shx + shx_i);
       SS_TRACE(10);
       __syncthreads();
       SS_TRACE(12);
@@ -913,7 +932,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
 #pragma unroll
           for (int k = 0; k < KM; ++k)
             if (k < K) acc = k == 0 ? ov[k] : acc + ov[k];
-          if (lp.routed_out) lp.routed_out[(size_t)r * H + 16 * bid + c] = acc;
+          if (lp.routed_out) gp(lp.routed_out)[(size_t)r * H + 16 * bid + c] = acc;
           SS_TRACE(16 + 3);
           for (int it = 0; (uint32_t)(shx_w >> 32) != tag; ++it) {
             if (dead()) break;
@@ -926,9 +945,9 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
           SS_TRACE(15);
           const float sh2 = ss_bf16_to_f32((uint32_t)shx_w & 0xFFFFu);
           const uint32_t yb = ss_f32_to_bf16(ss_round_bf16(acc) + sh2);
-          lp.y[(size_t)r * H + 16 * bid + c] = (uint16_t)yb;
+          gp(lp.y)[(size_t)r * H + 16 * bid + c] = (uint16_t)yb;
           sb = ss_f32_to_bf16(ss_bf16_to_f32(xres) + ss_bf16_to_f32(yb));
-          if (lp.stream_out) lp.stream_out[(size_t)r * H + 16 * bid + c] = (uint16_t)sb;
+          if (lp.stream_out) gp(lp.stream_out)[(size_t)r * H + 16 * bid + c] = (uint16_t)sb;
         }
         // the stream word of rows (c, c + 1) of token r: the partner row sits 4 lanes up
         const uint32_t sb_hi = (uint32_t)__shfl_xor((int)sb, 4);
@@ -969,17 +988,17 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
     if (NL - 2 + q >= 0) a.trace[row * 16 + (k & 15)] = s_tr[q][k];
   }
   if (tid == 0) {
-    const int sh = bid % kShards;
-    const int in_shard = (G - sh + kShards - 1) / kShards;
-    const int t1 = __hip_atomic_fetch_add(shard(ctr, CTR_EXIT, sh), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int sh = bid % kCShards;
+    const int in_shard = (G - sh + kCShards - 1) / kCShards;
+    const int t1 = __hip_atomic_fetch_add(cshard(ctr, CTR_EXIT, sh), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (t1 == in_shard - 1) {
-      const int t2 = __hip_atomic_fetch_add(shard(ctr, CTR_TOP, 0), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (t2 == (G < kShards ? G : kShards) - 1) {
+      const int t2 = __hip_atomic_fetch_add(cshard(ctr, CTR_TOP, 0), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (t2 == (G < kCShards ? G : kCShards) - 1) {
         for (int c = 0; c < CTR_COUNT; ++c)
           if (c != CTR_EPOCH)
-            for (int q = 0; q < kShards; ++q)
-              __hip_atomic_store(shard(ctr, c, q), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_fetch_add(shard(ctr, CTR_EPOCH, 0), NL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            for (int q = 0; q < kCShards; ++q)
+              __hip_atomic_store(cshard(ctr, c, q), 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(cshard(ctr, CTR_EPOCH, 0), NL, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
   }
