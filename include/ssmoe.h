@@ -256,6 +256,18 @@ int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_gen
                  float top_p, int top_k, float min_p, float presence_penalty, const float* u, void* workspace,
                  int64_t workspace_bytes, int32_t* out, void* stream);
 
+/* ---------------------------------------------------------------- achievable peaks (measurement only) */
+
+/* No reference counterpart: the ceilings this build's roofline fractions are stated against beside the published
+ * MI355X peaks (the method of the reference's micro-benchmarks, bench/m0/gemv_bench.py:228-268). A streaming read of
+ * `bytes` (a positive multiple of 16) from src (16-byte aligned) by `grid` 256-thread workgroups with 16-byte loads,
+ * folded into out uint32 [grid] (xor; zero it first). */
+int ssmoe_bench_stream_read(const void* src, int64_t bytes, uint32_t* out, int grid, void* stream);
+
+/* `grid` workgroups of 4 waves, each wave `iters` rounds of 8 independent v_mfma_f32_16x16x32_bf16 on register
+ * operands from seed uint32 [8]: 2 * 16 * 16 * 32 * 8 * iters flop per wave. out fp32 [grid * 4] (the wave sums). */
+int ssmoe_bench_mfma_bf16(const uint32_t* seed, int iters, float* out, int grid, void* stream);
+
 /* Bytes of the workspace ssmoe_sample_rows needs (-1 outside 1 <= R <= 64, 1 <= V <= 1,048,576). */
 int64_t ssmoe_sample_rows_workspace_bytes(int R, int V);
 

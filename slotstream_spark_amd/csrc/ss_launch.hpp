@@ -176,6 +176,10 @@ hipError_t launch_accept_sampled(const float* target, const int32_t* drafts, int
                                  int n_seen, float temperature, float top_p, int top_k, float min_p, float pp,
                                  const float* uniforms, void* work, int32_t* out, hipStream_t st);
 
+// Achievable-peak kernels (ss_peaks.hip).
+hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* out, int grid, hipStream_t st);
+hipError_t launch_mfma_loop(const uint32_t* seed, int iters, float* out, int grid, hipStream_t st);
+
 // Expert slot pool (ss_pool.hip).
 struct Pool;
 enum class PoolStatus { Ok, Invalid, Exhausted, Io };

@@ -765,6 +765,20 @@ int ssmoe_sample(const float* logits, int V, const int32_t* generated, int n_gen
                    "sample launch");
 }
 
+int ssmoe_bench_stream_read(const void* src, int64_t bytes, uint32_t* out, int grid, void* stream) {
+  if (!src || !out) return fail(SSMOE_EINVAL, "src and out must be non-null");
+  if (!aligned(src, 16) || bytes < 16 || bytes % 16) return fail(SSMOE_EINVAL, "src must be 16-byte aligned and bytes a positive multiple of 16");
+  if (grid < 1 || grid > (1 << 20)) return fail(SSMOE_EINVAL, "grid must be in [1, 1048576], got %d", grid);
+  return hip_check(ss::launch_stream_read(src, (size_t)bytes, out, grid, static_cast<hipStream_t>(stream)),
+                   "stream read launch");
+}
+
+int ssmoe_bench_mfma_bf16(const uint32_t* seed, int iters, float* out, int grid, void* stream) {
+  if (!seed || !out) return fail(SSMOE_EINVAL, "seed and out must be non-null");
+  if (iters < 1 || grid < 1 || grid > (1 << 20)) return fail(SSMOE_EINVAL, "iters >= 1 and grid in [1, 1048576]");
+  return hip_check(ss::launch_mfma_loop(seed, iters, out, grid, static_cast<hipStream_t>(stream)), "mfma loop launch");
+}
+
 int64_t ssmoe_sample_rows_workspace_bytes(int R, int V) {
   if (R < 1 || R > 64 || V < 1 || V > (1 << 20)) return -1;
   return (int64_t)R * ss::sample_workspace_bytes(V);
