@@ -124,6 +124,39 @@ int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm
                                  uint16_t* stream_out, float* routed_out, int T, int H, int I, int Is, int K, int E,
                                  void* stream);
 
+/* The scales and biases of an affine 4-bit (gs 64) shared expert (the checkpoint's quantized
+ * shared_expert.{gate,up,down}_proj, AffineWeight of model/weights.py:84-92, applied by lin -> gemv,
+ * model/layers.py:62-76): bf16 [Is, H/64] (gate, up) and [H, Is/64] (down), device pointers. With them the
+ * entry points below take sh_gate, sh_up and sh_down as packed words, uint32 [Is, H/8], [Is, H/8] and [H, Is/8]
+ * (nibble i of a word at bits 4i), and form each projection as the or_dense_rows order over weights dequantized in
+ * fp32 (q * s, then + b); the shared_expert_gate row sh_g stays bf16. H and Is multiples of 64. */
+typedef struct {
+  const uint16_t* gate_s;
+  const uint16_t* gate_b;
+  const uint16_t* up_s;
+  const uint16_t* up_b;
+  const uint16_t* down_s;
+  const uint16_t* down_b;
+} ssmoe_shared_q4;
+
+/* ssmoe_moe_verify_layer with an affine 4-bit shared expert (sh_q4 non-null, see ssmoe_shared_q4). */
+int ssmoe_moe_verify_layer_q4s(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
+                               const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
+                               const uint16_t* sh_g, const ssmoe_shared_q4* sh_q4, int layer, const int32_t* map,
+                               int64_t map_len, const int64_t* slot_ptr, int64_t n_slots, void* workspace,
+                               int64_t workspace_bytes, int32_t* ids, float* weights, uint16_t* y, float* routed_out,
+                               int T, int H, int I, int Is, int K, int E, void* stream);
+
+/* ssmoe_moe_verify_layer_chain with an affine 4-bit shared expert (sh_q4 non-null, see ssmoe_shared_q4). */
+int ssmoe_moe_verify_layer_chain_q4s(const uint16_t* stream_in, const uint16_t* norm_w, float eps,
+                                     const uint16_t* router_w, const float* router_bias, const uint16_t* sh_gate,
+                                     const uint16_t* sh_up, const uint16_t* sh_down, const uint16_t* sh_g,
+                                     const ssmoe_shared_q4* sh_q4, int layer, const int32_t* map, int64_t map_len,
+                                     const int64_t* slot_ptr, int64_t n_slots, void* workspace,
+                                     int64_t workspace_bytes, int32_t* ids, float* weights, uint16_t* y,
+                                     uint16_t* stream_out, float* routed_out, int T, int H, int I, int Is, int K,
+                                     int E, void* stream);
+
 /* One layer of ssmoe_moe_verify_chain: its weights, its map row and its outputs (device pointers). */
 typedef struct {
   const uint16_t* router_w;  /* bf16 [E, H] */
@@ -139,6 +172,15 @@ typedef struct {
   uint16_t* y;               /* bf16 [T, H] */
   uint16_t* stream_out;      /* bf16 [T, H] or NULL: bf16(stream + y), the next layer's residual stream */
   float* routed_out;         /* fp32 [T, H] or NULL */
+  /* Affine 4-bit (gs 64) shared expert (the checkpoint's quantized shared_expert.{gate,up,down}_proj, AffineWeight
+   * of model/weights.py:84-92): all six NULL for bf16 weights; all six set and sh_gate / sh_up / sh_down then hold
+   * packed words, uint32 [Is, H/8], [Is, H/8], [H, Is/8] (nibble i of a word at bits 4i). bf16 scales and biases: */
+  const uint16_t* sh_gate_s; /* [Is, H/64] */
+  const uint16_t* sh_gate_b;
+  const uint16_t* sh_up_s;   /* [Is, H/64] */
+  const uint16_t* sh_up_b;
+  const uint16_t* sh_down_s; /* [H, Is/64] */
+  const uint16_t* sh_down_b;
 } ssmoe_chain_layer;
 
 /* Bytes of the workspace ssmoe_moe_verify_chain needs (-1 on bad arguments). */

@@ -49,6 +49,7 @@ def lib():
         L.or_accept_pq.argtypes, L.or_accept_pq.restype = [P, P, P, P, i32, i32, f32, P, P], None
         L.or_row_z.argtypes, L.or_row_z.restype = [P, i32, f32], f32
         L.or_shared_hs.argtypes, L.or_shared_hs.restype = [P, P, P, i32], None
+        L.or_dense_rows_q4.argtypes, L.or_dense_rows_q4.restype = [P, P, P, P, P, i32, i32, i32], None
         L.or_combine_shared.argtypes, L.or_combine_shared.restype = [P, P, P, P, i32, i32], None
         L.or_residual_rmsnorm.argtypes = [P, P, P, f32, i32, i32, P, P]
         L.or_residual_rmsnorm.restype = None
@@ -158,6 +159,33 @@ def accept_pq(target, draft, drafts, uniforms, temperature) -> np.ndarray:
 def row_z(x, temperature) -> float:
     x = _c(x, np.float32)
     return float(lib().or_row_z(_p(x), x.size, float(temperature)))
+
+
+def dense_rows_q4(x_bits, words, s_bits, b_bits) -> np.ndarray:
+    """bf16 [T, K] x affine 4-bit (gs 64) [N, K]^T -> bf16 bits [T, N] (or_dense_rows_q4: the or_dense_rows order,
+    each weight q * s + b in fp32 first). words uint32/int32 [N, K/8], s, b bf16 bits [N, K/64]."""
+    x = _c(x_bits, np.uint16)
+    wd = np.ascontiguousarray(words).view(np.uint32)
+    sb, bb = _c(s_bits, np.uint16), _c(b_bits, np.uint16)
+    T, K = x.shape
+    N = wd.shape[0]
+    if wd.shape[1] * 8 != K or sb.shape != (N, K // 64) or bb.shape != (N, K // 64):
+        raise ValueError("words [N, K/8], s and b [N, K/64]")
+    out = np.empty((T, N), dtype=np.uint16)
+    lib().or_dense_rows_q4(_p(x), _p(wd), _p(sb), _p(bb), _p(out), T, K, N)
+    return out
+
+
+def shared_expert_q4(x_bits, gate, up, down, sg_bits):
+    """The shared expert's bf16 chain with affine 4-bit gate/up/down projections (each a (words, s bits, b bits)
+    triple; the gate logit row sg stays bf16) -> (sh bf16 bits [T, H], gate projection bf16 bits [T])."""
+    g = dense_rows_q4(x_bits, *gate)
+    u = dense_rows_q4(x_bits, *up)
+    hs = np.empty_like(g)
+    lib().or_shared_hs(_p(g), _p(u), _p(hs), g.size)
+    sh = dense_rows_q4(hs, *down)
+    sgl = dense_rows(x_bits, sg_bits)[:, 0].copy()
+    return sh, sgl
 
 
 def shared_expert(x_bits, gate_bits, up_bits, down_bits, sg_bits):

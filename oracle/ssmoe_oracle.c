@@ -116,6 +116,42 @@ void or_dense_rows(const uint16_t* x, const uint16_t* w, uint16_t* out, int T, i
   }
 }
 
+/* Dense rows over affine 4-bit (gs 64) weights, the dot products of the shared expert when the checkpoint keeps it
+ * quantized (reference: lin -> gemv on an AffineWeight, model/layers.py:62-76, kernels/gemv_affine.py:214-262,
+ * w = q * s + b of kernels/affine_ref.py:10-30). words uint32 [N][K/8] (nibble i of a word at bits 4i), s, b bf16
+ * [N][K/64]. The or_dense_rows order with each weight dequantized in fp32 first (a multiply, then an add: two
+ * roundings): lane l accumulates elements 512 j + 8 l .. + 7 by fmaf from 0, then the butterfly, one rounding to
+ * bf16. With s = 1 and b = 0 every weight is the integer q and the result equals or_dense_rows on bf16(q) bit for
+ * bit. */
+void or_dense_rows_q4(const uint16_t* x, const uint32_t* words, const uint16_t* s, const uint16_t* b, uint16_t* out,
+                      int T, int K, int N) {
+  const int k8 = K / 8, nj = (K + 511) / 512, ng = K / 64;
+  for (int t = 0; t < T; ++t) {
+    for (int n = 0; n < N; ++n) {
+      float lanes[64];
+      for (int l = 0; l < 64; ++l) {
+        float acc = 0.0f;
+        for (int j = 0; j < nj; ++j) {
+          const int w8 = 64 * j + l;
+          if (w8 >= k8) break;
+          const uint32_t wd = words[(size_t)n * k8 + w8];
+          const int grp = (8 * w8) / 64;
+          const float sc = or_bf16_to_f32(s[(size_t)n * ng + grp]), bi = or_bf16_to_f32(b[(size_t)n * ng + grp]);
+          for (int e = 0; e < 8; ++e) {
+            const int k = 8 * w8 + e;
+            const float q = (float)((wd >> (4 * e)) & 0xFu);
+            const float prod = q * sc;
+            const float wgt = prod + bi;
+            acc = fmaf(or_bf16_to_f32(x[(size_t)t * K + k]), wgt, acc);
+          }
+        }
+        lanes[l] = acc;
+      }
+      out[(size_t)t * N + n] = or_f32_to_bf16(butterfly_sum(lanes));
+    }
+  }
+}
+
 /* ---------------------------------------------------------------- router tail
  * model/layers.py:340-347, reference_torch.py:122-124. scores s = bf16 logit (+ bias, one fp32 add);
  * m = max (NaN ignored); e = exp(s - m); Z: lane l sums e[l], e[l+64], ... sequentially from 0, then the butterfly;

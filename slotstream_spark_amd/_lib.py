@@ -34,6 +34,10 @@ SIGNATURES = {
                                     _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "ssmoe_moe_verify_layer_chain": (_I, [_P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _P, _I64, _P, _I64,
                                           _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "ssmoe_moe_verify_layer_q4s": (_I, [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _P, _I64, _P, _I64,
+                                        _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
+    "ssmoe_moe_verify_layer_chain_q4s": (_I, [_P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _P, _I64, _P,
+                                              _I64, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _P]),
     "ssmoe_verify_chain_workspace_bytes": (_I64, [_I, _I, _I, _I, _I, _I]),
     "ssmoe_moe_verify_chain": (_I, [_P, _F, _P, _P, _I, _P, _I64, _P, _I64, _P, _I64, _I, _I, _I, _I, _I, _I, _P]),
     "ssmoe_moe_verify_layer_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I64, _P, _I64,

@@ -228,6 +228,13 @@ SS_DEV VerifyArgs helper_args(const ChainArgs& a, const ssmoe_chain_layer& lp) {
   VerifyArgs v{};
   v.mode = 0;
   v.bias = lp.router_bias;
+  v.sh_down = lp.sh_down;
+  v.sh_gs = lp.sh_gate_s;
+  v.sh_gb = lp.sh_gate_b;
+  v.sh_us = lp.sh_up_s;
+  v.sh_ub = lp.sh_up_b;
+  v.sh_ds = lp.sh_down_s;
+  v.sh_db = lp.sh_down_b;
   v.map = a.map;
   v.map_len = a.map_len;
   v.slot_ptr = a.slot_ptr;
@@ -266,7 +273,7 @@ size_t chain_scratch_bytes(int T, int H, int I, int Is, int K, int E) { return c
 // MI355X, the hand-offs complete about 0.15 us sooner per layer than with a short sleep in each poll.
 constexpr int kChainSpin = 1 << 18;
 
-template <int NJG, int NJD>
+template <int NJG, int NJD, bool SHQ4>
 __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   extern __shared__ uint4 dsm[];
   __shared__ VSmem s0;
@@ -329,13 +336,23 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   // Dense-row jobs: j < E is router row j; E <= j < E + Is the shared gate and up rows j - E; the last job also takes
   // the shared_expert_gate row (as the single-layer kernel).
   auto load_job = [&](const ssmoe_chain_layer& q, int j) {
-    const uint16_t* w0 = j < E ? q.router_w + (size_t)j * H : q.sh_gate + (size_t)(j - E) * H;
+    if (SHQ4 && j >= E) {
+      // affine 4-bit shared gate and up rows: q4_chunk registers
+      const size_t r = (size_t)(j - E);
 #pragma unroll
-    for (int jj = 0; jj < NJX; ++jj) r0[jj] = ldg16(w0 + 8 * (64 * jj + lane));
-    if (j >= E) {
-      const uint16_t* w1 = q.sh_up + (size_t)(j - E) * H;
+      for (int jj = 0; jj < NJX; ++jj) {
+        r0[jj] = q4_chunk(q.sh_gate + r * (H / 4), q.sh_gate_s + r * (H / 64), q.sh_gate_b + r * (H / 64), jj, lane);
+        r1[jj] = q4_chunk(q.sh_up + r * (H / 4), q.sh_up_s + r * (H / 64), q.sh_up_b + r * (H / 64), jj, lane);
+      }
+    } else {
+      const uint16_t* w0 = j < E ? q.router_w + (size_t)j * H : q.sh_gate + (size_t)(j - E) * H;
 #pragma unroll
-      for (int jj = 0; jj < NJX; ++jj) r1[jj] = ldg16(w1 + 8 * (64 * jj + lane));
+      for (int jj = 0; jj < NJX; ++jj) r0[jj] = ldg16(w0 + 8 * (64 * jj + lane));
+      if (j >= E) {
+        const uint16_t* w1 = q.sh_up + (size_t)(j - E) * H;
+#pragma unroll
+        for (int jj = 0; jj < NJX; ++jj) r1[jj] = ldg16(w1 + 8 * (64 * jj + lane));
+      }
     }
     if (j == J - 1) {
 #pragma unroll
@@ -369,7 +386,8 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       bias_r[i] = q.router_bias ? gp(q.router_bias)[e < E ? e : 0] : 0.f;
     }
   };
-  uint4 shw[4];
+  constexpr int NSC = NJD > 4 ? 2 : 1;  // 512-element chunks of a shared down row per lane (Is <= 512 * NSC)
+  uint4 shw[4][NSC];
 
   if (j_first < J) load_job(lp, j_first);
   load_map(lp);
@@ -489,7 +507,10 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
 #pragma unroll 1
       for (int q = 0; q < nrow; ++q) {
         float d[kTBv];
-        dense_dot<NJX>(r0, xfl, nt, d);
+        if (SHQ4 && j >= E && q < 2)
+          affine_dot<NJX>(r0, xfl, nt, d);
+        else
+          dense_dot<NJX>(r0, xfl, nt, d);
         if (lane == 0) {
           if (j < E) {
 #pragma unroll 1
@@ -743,16 +764,14 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       // ---------------------------------------------------------- the shared expert's rows of workgroup bid - H/16
       // (the operations of the single-layer kernel's shared rows), gated and published for that workgroup's combine
       const int ob = bid - (H >> 4);
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        shw[rr] = ldg16(lp.sh_down + (size_t)(16 * ob + 4 * w + rr) * Is + 8 * (8 * lane < Is ? lane : 0));
+      load_shared_down<4, NSC>(va, 16 * ob + 4 * w, shw);
       wait_ctr(CTR_SHARED, (l + 1) * (Is + 1));
       const SharedIn shin = shared_load(va, gsh, ush, nt);
       const uint16_t sgl_t = ld_ag(sgl + ((lane & 3) < nt ? (lane & 3) : 0));
-      shared_hs_part(va, shin, w, nt, hsl);
+      shared_hs_all<NSC>(va, shin, gsh, ush, w, nt, hsl);
       __syncthreads();
       float o[4][kTBv];
-      shared_down_rows<4>(va, hsl, shw, nt, o);
+      shared_down_rows<4, NSC>(va, hsl, shw, nt, o);
       // lane 4 rr + t publishes row 16 ob + 4 w + rr of token t
       const int rr = (lane >> 2) & 3, t = lane & 3;
       float shv = 0.f;
@@ -1004,10 +1023,10 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
   }
 }
 
-template <int NJG, int NJD>
+template <int NJG, int NJD, bool SHQ4>
 static hipError_t launch_chain_nj(const ChainArgs& a, hipStream_t st) {
   const SsRecord rec = ss_record_layout(a.H, a.I);
-  auto kern = chain_kernel<NJG, NJD>;
+  auto kern = chain_kernel<NJG, NJD, SHQ4>;
   const CDLayout dly = cdlayout(a.T, a.H, a.I, a.Is, a.K, a.E);
   // Every workgroup waits on the others: one workgroup per CU, launched only if a workgroup with the largest dynamic
   // LDS the kernel takes fits on a CU (checked once per device).
@@ -1030,7 +1049,8 @@ hipError_t launch_chain(const ChainArgs& a, hipStream_t st) {
   // One instantiated shape: H 2048 x I 512, the BASELINE layer (the layer loop is sized to the register file for it);
   // other shapes run one ssmoe_moe_verify_layer_chain launch per layer.
   const int njg = a.H / 128, njd = a.I / 128;
-  if (njg == 16 && njd == 4) return launch_chain_nj<16, 4>(a, st);
+  const bool q4 = a.l0.sh_gate_s != nullptr;  // every layer alike (checked by the entry point)
+  if (njg == 16 && njd == 4) return q4 ? launch_chain_nj<16, 4, true>(a, st) : launch_chain_nj<16, 4, false>(a, st);
   return hipErrorInvalidValue;
 }
 

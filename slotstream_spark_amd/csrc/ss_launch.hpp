@@ -71,6 +71,9 @@ struct VerifyArgs {
   const uint16_t* sh_up;    // [Is, H]
   const uint16_t* sh_down;  // [H, Is]
   const uint16_t* sh_g;     // [1, H]
+  // Affine 4-bit (gs 64) shared expert: with sh_gs non-null, sh_gate / sh_up / sh_down hold packed words (uint32
+  // [Is, H/8], [Is, H/8], [H, Is/8]) and these their bf16 scales and biases ([Is, H/64] twice, [H, Is/64]).
+  const uint16_t *sh_gs, *sh_gb, *sh_us, *sh_ub, *sh_ds, *sh_db;
   const int32_t* map;
   int64_t map_len;
   const int64_t* slot_ptr;

@@ -77,14 +77,25 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   const int j_first = bid * 4 + w;
   const bool has_tile = bid < (H >> 4);
   uint4 r0[NJX], r1[NJX], r2[NJX];
+  const bool sh_q4 = a.sh_gs != nullptr;
   auto load_job = [&](int j) {
-    const uint16_t* w0 = j < E ? a.router_w + (size_t)j * H : a.sh_gate + (size_t)(j - E) * H;
+    if (j >= E && sh_q4) {
+      // affine 4-bit shared gate and up rows: q4_chunk registers
+      const size_t r = (size_t)(j - E);
 #pragma unroll
-    for (int jj = 0; jj < NJX; ++jj) r0[jj] = ldg16(w0 + 8 * (64 * jj + lane));
-    if (j >= E) {
-      const uint16_t* w1 = a.sh_up + (size_t)(j - E) * H;
+      for (int jj = 0; jj < NJX; ++jj) {
+        r0[jj] = q4_chunk(a.sh_gate + r * (H / 4), a.sh_gs + r * (H / 64), a.sh_gb + r * (H / 64), jj, lane);
+        r1[jj] = q4_chunk(a.sh_up + r * (H / 4), a.sh_us + r * (H / 64), a.sh_ub + r * (H / 64), jj, lane);
+      }
+    } else {
+      const uint16_t* w0 = j < E ? a.router_w + (size_t)j * H : a.sh_gate + (size_t)(j - E) * H;
 #pragma unroll
-      for (int jj = 0; jj < NJX; ++jj) r1[jj] = ldg16(w1 + 8 * (64 * jj + lane));
+      for (int jj = 0; jj < NJX; ++jj) r0[jj] = ldg16(w0 + 8 * (64 * jj + lane));
+      if (j >= E) {
+        const uint16_t* w1 = a.sh_up + (size_t)(j - E) * H;
+#pragma unroll
+        for (int jj = 0; jj < NJX; ++jj) r1[jj] = ldg16(w1 + 8 * (64 * jj + lane));
+      }
     }
     if (j == J - 1) {
 #pragma unroll
@@ -116,7 +127,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
 #pragma unroll 1
       for (int q = 0; q < nrow; ++q) {
         float d[kTBv];
-        dense_dot<NJX>(r0, xfl, nt, d);
+        if (sh_q4 && j >= E && q < 2)
+          affine_dot<NJX>(r0, xfl, nt, d);
+        else
+          dense_dot<NJX>(r0, xfl, nt, d);
         if (lane == 0) {
           if (j < E) {
 #pragma unroll 1
@@ -364,13 +378,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
   // requested only now, after the gate/up items are published (requested earlier they would queue ahead of the
   // items' own loads); the gate / up inputs follow the DMAs, and the rows are computed after the down experts, when
   // every load has landed, so nothing here waits on the critical path.
-  uint4 shw[4];
+  constexpr int NSC = NJD > 4 ? 2 : 1;  // 512-element chunks of a shared down row per lane (Is <= 512 * NSC)
+  uint4 shw[4][NSC];
   SharedIn shin;
-  if (verify && has_tile) {
-#pragma unroll
-    for (int rr = 0; rr < 4; ++rr)
-      shw[rr] = ldg16(a.sh_down + (size_t)(16 * bid + 4 * w + rr) * a.Is + 8 * (8 * lane < a.Is ? lane : 0));
-  }
+  if (verify && has_tile) load_shared_down<4, NSC>(a, 16 * bid + 4 * w, shw);
   if (has_tile) {
 #pragma unroll 1
     for (int u = w; u < nu && u < D.P; u += 4) issue_down(u, u);
@@ -497,10 +508,10 @@ __global__ __launch_bounds__(256) void verify_kernel(VerifyArgs a, SsRecord rec)
       // The prefetch region is free once every wave is past its down experts; hs goes there.
       __syncthreads();
       float* hsl = reinterpret_cast<float*>(prefl);
-      shared_hs_part(a, shin, w, nt, hsl);
+      shared_hs_all<NSC>(a, shin, gsh, ush, w, nt, hsl);
       __syncthreads();
       float o[4][kTBv];
-      shared_down_rows<4>(a, hsl, shw, nt, o);
+      shared_down_rows<4, NSC>(a, hsl, shw, nt, o);
       if (a.trace && tid == 0) a.trace[(size_t)bid * 16 + 13] = __builtin_amdgcn_s_memrealtime();
       if (lane == 0)
 #pragma unroll

@@ -598,30 +598,70 @@ SS_DEV void dense_dot(const uint4 (&wv)[NJX], const uint4* xfl, int nt, float ou
   }
 }
 
+// Affine 4-bit (gs 64) dense rows (the shared expert's projections when the checkpoint keeps them quantized): the
+// dense-row register of chunk jj holds {the word of elements 512 jj + 8 lane .. + 7 (nibble e at bits 4e), its
+// group's bf16 scale | bf16 bias << 16, 0, 0}. q4_chunk loads it from words uint32 [K/8] and s, b bf16 [K/64] of
+// one row.
+SS_DEV uint4 q4_chunk(const uint16_t* words, const uint16_t* sc, const uint16_t* bi, int jj, int lane) {
+  const int w8 = 64 * jj + lane, grp = w8 >> 3;
+  const uint32_t wd = *gp(reinterpret_cast<const uint32_t*>(words + 2 * (size_t)w8));
+  const uint32_t sv = *gp(sc + grp);
+  const uint32_t bv = *gp(bi + grp);
+  return make_uint4(wd, sv | (bv << 16), 0u, 0u);
+}
+
+// dense_dot over q4_chunk registers: each weight dequantized in fp32 first (q * s, then + b), then the dense_dot
+// order (or_dense_rows_q4).
+template <int NJX>
+SS_DEV void affine_dot(const uint4 (&wv)[NJX], const uint4* xfl, int nt, float out[kTBv]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int t = 0; t < kTBv; ++t) {
+    if (t >= nt) break;
+    float ac = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < NJX; ++jj) {
+      const uint4 xv = xfl[xfrag_index(512 * jj + 8 * lane, t)];
+      const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+      const float sc = bf_lo(wv[jj].y), bi = bf_hi(wv[jj].y);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float q = (float)((wv[jj].x >> (4 * e)) & 0xFu);
+        const float wf = q * sc + bi;
+        const float xf = (e >> 2) ? bf_hi(xx[e & 3]) : bf_lo(xx[e & 3]);
+        ac = __builtin_fmaf(xf, wf, ac);
+      }
+    }
+    out[t] = ss_wave_sum(ac);
+  }
+}
+
 // The shared-expert gate / up projections of this lane's 8 elements for every token (tokens >= nt read token 0).
 struct SharedIn {
   uint4 g[kTBv], u[kTBv];
 };
 
-SS_DEV SharedIn shared_load(const VerifyArgs& a, const uint16_t* gsh, const uint16_t* ush, int nt) {
+// Chunk c (elements 512 c + 8 l .. + 7 of lane l; Is <= 1024) of the projections.
+SS_DEV SharedIn shared_load(const VerifyArgs& a, const uint16_t* gsh, const uint16_t* ush, int nt, int c = 0) {
   const int lane = threadIdx.x & 63;
-  const int li = 8 * lane < a.Is ? lane : 0;
+  const int e0 = 512 * c + 8 * lane < a.Is ? 512 * c + 8 * lane : 0;
   SharedIn in;
 #pragma unroll
   for (int t = 0; t < kTBv; ++t) {
     const int tt = t < nt ? t : 0;
-    in.g[t] = ld_ag16(gsh + (size_t)tt * a.Is + 8 * li);
-    in.u[t] = ld_ag16(ush + (size_t)tt * a.Is + 8 * li);
+    in.g[t] = ld_ag16(gsh + (size_t)tt * a.Is + e0);
+    in.u[t] = ld_ag16(ush + (size_t)tt * a.Is + e0);
   }
   return in;
 }
 
 // hs = bf16(bf16(silu(g)) * u) of the shared expert (the F.silu and product of the reference, in bf16), split over
-// the workgroup's four waves: wave w computes elements 8 l + 2 w and 8 l + 2 w + 1 of lane l's eight for every
-// token and stores them to hsl [nt][Is] (LDS).
-SS_DEV void shared_hs_part(const VerifyArgs& a, const SharedIn& in, int w, int nt, float* hsl) {
+// the workgroup's four waves: wave w computes elements e0 + 2 w and e0 + 2 w + 1 of lane l's eight (e0 = 512 c + 8 l)
+// for every token and stores them to hsl [nt][Is] (LDS).
+SS_DEV void shared_hs_part(const VerifyArgs& a, const SharedIn& in, int w, int nt, float* hsl, int c = 0) {
   const int lane = threadIdx.x & 63;
-  if (8 * lane >= a.Is) return;
+  const int e0 = 512 * c + 8 * lane;
+  if (e0 >= a.Is) return;
 #pragma unroll
   for (int t = 0; t < kTBv; ++t) {
     if (t >= nt) break;
@@ -634,15 +674,46 @@ SS_DEV void shared_hs_part(const VerifyArgs& a, const SharedIn& in, int w, int n
       const float gv = h ? bf_hi(gw) : bf_lo(gw);
       const float uv = h ? bf_hi(uw) : bf_lo(uw);
       const float sv = ss_round_bf16(gv / (1.f + ss_expf(-gv)));
-      hsl[t * a.Is + 8 * lane + 2 * w + h] = ss_round_bf16(sv * uv);
+      hsl[t * a.Is + e0 + 2 * w + h] = ss_round_bf16(sv * uv);
     }
   }
 }
 
-// Shared-expert down rows of one wave, in the dense_rows order: the dot of hs (hsl) with the bf16 down rows;
-// out[rr][t] receives the fp32 sums (every lane). sh_w holds each row's 8 elements of this lane (Is <= 512).
-template <int NR>
-SS_DEV void shared_down_rows(const VerifyArgs& a, const float* hsl, const uint4 (&sh_w)[NR], int nt,
+// All of hs (both chunks when Is > 512; the second chunk's projections are loaded here, one more round trip).
+template <int NSC>
+SS_DEV void shared_hs_all(const VerifyArgs& a, const SharedIn& in0, const uint16_t* gsh, const uint16_t* ush, int w,
+                          int nt, float* hsl) {
+  shared_hs_part(a, in0, w, nt, hsl, 0);
+  if (NSC > 1 && a.Is > 512) {
+    const SharedIn in1 = shared_load(a, gsh, ush, nt, 1);
+    shared_hs_part(a, in1, w, nt, hsl, 1);
+  }
+}
+
+// The shared-expert down row registers of one wave, chunk c of row r in sh_w[r][c]: bf16 rows (the lane's 8
+// elements 512 c + 8 l .. + 7), or with an affine 4-bit down projection the q4_chunk register of those elements.
+// NSC chunks per row (512 * NSC >= Is): the kernels take NSC = 2 with I > 512, else 1.
+template <int NR, int NSC>
+SS_DEV void load_shared_down(const VerifyArgs& a, int row0, uint4 (&sh_w)[NR][NSC]) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int rr = 0; rr < NR; ++rr)
+#pragma unroll
+    for (int c = 0; c < NSC; ++c) {
+      const int w8 = 64 * c + lane;
+      const bool ok = 8 * w8 < a.Is;
+      const size_t row = (size_t)(row0 + rr);
+      sh_w[rr][c] = !ok ? make_uint4(0u, 0u, 0u, 0u)
+                    : a.sh_ds ? q4_chunk(a.sh_down + row * (a.Is / 4), a.sh_ds + row * (a.Is / 64),
+                                         a.sh_db + row * (a.Is / 64), c, lane)
+                              : ldg16(a.sh_down + row * a.Is + 8 * w8);
+    }
+}
+
+// Shared-expert down rows of one wave, in the dense_rows order (lane l: chunk 0's elements, then chunk 1's, by fma
+// from 0; then the butterfly): the dot of hs (hsl) with the down rows; out[rr][t] receives the fp32 sums (every lane).
+template <int NR, int NSC>
+SS_DEV void shared_down_rows(const VerifyArgs& a, const float* hsl, const uint4 (&sh_w)[NR][NSC], int nt,
                              float (&out)[NR][kTBv]) {
   const int lane = threadIdx.x & 63;
   float sacc[NR][kTBv];
@@ -650,19 +721,35 @@ SS_DEV void shared_down_rows(const VerifyArgs& a, const float* hsl, const uint4 
   for (int rr = 0; rr < NR; ++rr)
 #pragma unroll
     for (int t = 0; t < kTBv; ++t) sacc[rr][t] = 0.f;
-  if (8 * lane < a.Is) {
+#pragma unroll
+  for (int c = 0; c < NSC; ++c) {
+    const int e0 = 512 * c + 8 * lane;
+    if (e0 >= a.Is) break;
 #pragma unroll
     for (int t = 0; t < kTBv; ++t) {
       if (t >= nt) break;
       float hsv[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) hsv[e] = hsl[t * a.Is + 8 * lane + e];
+      for (int e = 0; e < 8; ++e) hsv[e] = hsl[t * a.Is + e0 + e];
 #pragma unroll
       for (int rr = 0; rr < NR; ++rr) {
-        const uint32_t ww[4] = {sh_w[rr].x, sh_w[rr].y, sh_w[rr].z, sh_w[rr].w};
+        const uint32_t ww[4] = {sh_w[rr][c].x, sh_w[rr][c].y, sh_w[rr][c].z, sh_w[rr][c].w};
         float ac = 0.f;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) ac = __builtin_fmaf(hsv[e], (e & 1) ? bf_hi(ww[e >> 1]) : bf_lo(ww[e >> 1]), ac);
+        for (int q = 0; q < kTBv; ++q)
+          if (q == t) ac = sacc[rr][q];
+        if (a.sh_ds) {
+          const float sc = bf_lo(ww[1]), bi = bf_hi(ww[1]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float q = (float)((ww[0] >> (4 * e)) & 0xFu);
+            const float wf = q * sc + bi;
+            ac = __builtin_fmaf(hsv[e], wf, ac);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ac = __builtin_fmaf(hsv[e], (e & 1) ? bf_hi(ww[e >> 1]) : bf_lo(ww[e >> 1]), ac);
+        }
 #pragma unroll
         for (int q = 0; q < kTBv; ++q)
           if (q == t) sacc[rr][q] = ac;

@@ -271,16 +271,30 @@ int64_t ssmoe_verify_workspace_bytes(int T, int H, int I, int Is, int K, int E) 
   return (int64_t)ss::verify_scratch_bytes(kBlock, H, I, Is, K, E);
 }
 
+// The affine 4-bit shared expert's scales and biases: all six or none; with them the weights hold packed words.
+static int check_shared_q4(const ssmoe_shared_q4* q4, int H, int Is) {
+  if (!q4) return ok();
+  if (!q4->gate_s || !q4->gate_b || !q4->up_s || !q4->up_b || !q4->down_s || !q4->down_b)
+    return fail(SSMOE_EINVAL, "an affine 4-bit shared expert needs all six scale and bias pointers");
+  if (H % 64 || Is % 64) return fail(SSMOE_EINVAL, "an affine 4-bit (gs 64) shared expert needs H and Is multiples of 64");
+  if (!aligned(q4->gate_s, 2) || !aligned(q4->gate_b, 2) || !aligned(q4->up_s, 2) || !aligned(q4->up_b, 2) ||
+      !aligned(q4->down_s, 2) || !aligned(q4->down_b, 2))
+    return fail(SSMOE_EINVAL, "scales and biases must be 2-byte aligned");
+  return ok();
+}
+
 static int verify_layer_impl(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
                              const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
                              const uint16_t* sh_g, int layer, const int32_t* map, int64_t map_len,
                              const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes,
                              int32_t* ids, float* weights, uint16_t* y, float* routed_out, int T, int H, int I, int Is,
                              int K, int E, void* stream, int norm_in, const uint16_t* norm_w, float norm_eps,
-                             uint16_t* x_plus_y) {
+                             uint16_t* x_plus_y, const ssmoe_shared_q4* q4 = nullptr) {
   if (int rc = check_moe_shape(T, H, I, K, E)) return rc;
   if (E > 512 || K > E) return fail(SSMOE_EINVAL, "need K <= E <= 512, got K=%d E=%d", K, E);
-  if (Is < 8 || Is % 8 || Is > 512) return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, 512], got %d", Is);
+  if (Is < 8 || Is % 8 || Is > (I > 512 ? 1024 : 512))
+    return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, %d] (I = %d), got %d", I > 512 ? 1024 : 512, I, Is);
+  if (int rc = check_shared_q4(q4, H, Is)) return rc;
   if (!x || !router_w || !sh_gate || !sh_up || !sh_down || !sh_g || !map || !slot_ptr || !workspace || !ids ||
       !weights || !y)
     return fail(SSMOE_EINVAL, "every pointer except router_bias and routed_out must be non-null");
@@ -306,6 +320,14 @@ static int verify_layer_impl(const uint16_t* x, const uint16_t* router_w, const 
     a.sh_up = sh_up;
     a.sh_down = sh_down;
     a.sh_g = sh_g;
+    if (q4) {
+      a.sh_gs = q4->gate_s;
+      a.sh_gb = q4->gate_b;
+      a.sh_us = q4->up_s;
+      a.sh_ub = q4->up_b;
+      a.sh_ds = q4->down_s;
+      a.sh_db = q4->down_b;
+    }
     a.map = map;
     a.map_len = map_len;
     a.slot_ptr = slot_ptr;
@@ -362,8 +384,41 @@ int ssmoe_moe_verify_layer_chain(const uint16_t* stream_in, const uint16_t* norm
                            E, stream, 1, norm_w, eps, stream_out);
 }
 
+int ssmoe_moe_verify_layer_q4s(const uint16_t* x, const uint16_t* router_w, const float* router_bias,
+                               const uint16_t* sh_gate, const uint16_t* sh_up, const uint16_t* sh_down,
+                               const uint16_t* sh_g, const ssmoe_shared_q4* sh_q4, int layer, const int32_t* map,
+                               int64_t map_len, const int64_t* slot_ptr, int64_t n_slots, void* workspace,
+                               int64_t workspace_bytes, int32_t* ids, float* weights, uint16_t* y, float* routed_out,
+                               int T, int H, int I, int Is, int K, int E, void* stream) {
+  if (!sh_q4) return fail(SSMOE_EINVAL, "sh_q4 must be non-null (bf16 shared weights: ssmoe_moe_verify_layer)");
+  return verify_layer_impl(x, router_w, router_bias, sh_gate, sh_up, sh_down, sh_g, layer, map, map_len, slot_ptr,
+                           n_slots, workspace, workspace_bytes, ids, weights, y, routed_out, T, H, I, Is, K, E, stream,
+                           0, nullptr, 0.f, nullptr, sh_q4);
+}
+
+int ssmoe_moe_verify_layer_chain_q4s(const uint16_t* stream_in, const uint16_t* norm_w, float eps,
+                                     const uint16_t* router_w, const float* router_bias, const uint16_t* sh_gate,
+                                     const uint16_t* sh_up, const uint16_t* sh_down, const uint16_t* sh_g,
+                                     const ssmoe_shared_q4* sh_q4, int layer, const int32_t* map, int64_t map_len,
+                                     const int64_t* slot_ptr, int64_t n_slots, void* workspace,
+                                     int64_t workspace_bytes, int32_t* ids, float* weights, uint16_t* y,
+                                     uint16_t* stream_out, float* routed_out, int T, int H, int I, int Is, int K,
+                                     int E, void* stream) {
+  if (!sh_q4) return fail(SSMOE_EINVAL, "sh_q4 must be non-null (bf16 shared weights: ssmoe_moe_verify_layer_chain)");
+  if (H % 512 != 0) return fail(SSMOE_EINVAL, "chained layers need H a multiple of 512, got %d", H);
+  if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(SSMOE_EINVAL, "eps must be finite and >= 0");
+  if (norm_w && !aligned(norm_w, 16)) return fail(SSMOE_EINVAL, "norm_w must be 16-byte aligned");
+  if (stream_out && (stream_out == stream_in || stream_out == y))
+    return fail(SSMOE_EINVAL, "stream_out must not alias stream_in or y (other workgroups still read stream_in)");
+  if (stream_out && !aligned(stream_out, 16)) return fail(SSMOE_EINVAL, "stream_out must be 16-byte aligned");
+  return verify_layer_impl(stream_in, router_w, router_bias, sh_gate, sh_up, sh_down, sh_g, layer, map, map_len,
+                           slot_ptr, n_slots, workspace, workspace_bytes, ids, weights, y, routed_out, T, H, I, Is, K,
+                           E, stream, 1, norm_w, eps, stream_out, sh_q4);
+}
+
 int64_t ssmoe_verify_chain_workspace_bytes(int T, int H, int I, int Is, int K, int E) {
-  if (T < 1 || T > kBlock || !ss::chain_shape_supported(H, I) || Is < 8 || Is % 8 || Is > 512 || K < 1 || K > 16 ||
+  if (T < 1 || T > kBlock || !ss::chain_shape_supported(H, I) || Is < 8 || Is % 8 || Is > (I > 512 ? 1024 : 512) ||
+      K < 1 || K > 16 ||
       E < K || E > 512)
     return -1;
   return (int64_t)ss::chain_scratch_bytes(kBlock, H, I, Is, K, E);
@@ -379,7 +434,8 @@ int ssmoe_moe_verify_chain(const uint16_t* stream_in, float eps, const ssmoe_cha
     return fail(SSMOE_EINVAL, "no chain kernel for H=%d, I=%d (%s); launch the layers one by one "
                 "(ssmoe_moe_verify_layer_chain)", H, I, ss::chain_shapes_text());
   if (E > 512 || K > E) return fail(SSMOE_EINVAL, "need K <= E <= 512, got K=%d E=%d", K, E);
-  if (Is < 8 || Is % 8 || Is > 512) return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, 512], got %d", Is);
+  if (Is < 8 || Is % 8 || Is > (I > 512 ? 1024 : 512))
+    return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, %d] (I = %d), got %d", I > 512 ? 1024 : 512, I, Is);
   if (n_layers < 1 || n_layers > 4096) return fail(SSMOE_EINVAL, "n_layers must be in [1, 4096], got %d", n_layers);
   if (!(eps >= 0.f) || !std::isfinite(eps)) return fail(SSMOE_EINVAL, "eps must be finite and >= 0");
   if (!stream_in || !aligned(stream_in, 16)) return fail(SSMOE_EINVAL, "stream_in must be a 16-byte aligned pointer");
@@ -399,6 +455,16 @@ int ssmoe_moe_verify_chain(const uint16_t* stream_in, float eps, const ssmoe_cha
                   (long long)q.layer, (long long)(q.layer + 1) * E);
     if (q.stream_out && (q.stream_out == q.y || (l == 0 && q.stream_out == stream_in)))
       return fail(SSMOE_EINVAL, "layer %d: stream_out must not alias y or stream_in", l);
+    const bool any_q4 = q.sh_gate_s || q.sh_gate_b || q.sh_up_s || q.sh_up_b || q.sh_down_s || q.sh_down_b;
+    if (any_q4 != (layers_host[0].sh_gate_s != nullptr))
+      return fail(SSMOE_EINVAL, "layer %d: every layer of a chain has an affine 4-bit shared expert, or none", l);
+    if (any_q4) {
+      const ssmoe_shared_q4 q4{q.sh_gate_s, q.sh_gate_b, q.sh_up_s, q.sh_up_b, q.sh_down_s, q.sh_down_b};
+      if (check_shared_q4(&q4, H, Is)) {
+        const std::string m = ssmoe_last_error();
+        return fail(SSMOE_EINVAL, "layer %d: %s", l, m.c_str());
+      }
+    }
   }
   const size_t need = ss::chain_scratch_bytes(kBlock, H, I, Is, K, E);
   if (workspace_bytes < (int64_t)need)
@@ -442,7 +508,8 @@ int ssmoe_moe_verify_layer_noalloc(const uint16_t* x, const uint16_t* router_w, 
                                    uint16_t* y, float* routed_out, int T, int H, int I, int Is, int K, int E,
                                    void* stream) {
   if (int rc = check_moe_shape(T, H, I, K, E)) return rc;
-  if (Is < 8 || Is % 8 || Is > 512) return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, 512], got %d", Is);
+  if (Is < 8 || Is % 8 || Is > (I > 512 ? 1024 : 512))
+    return fail(SSMOE_EINVAL, "Is must be a multiple of 8 in [8, %d] (I = %d), got %d", I > 512 ? 1024 : 512, I, Is);
   if (E > 512) return fail(SSMOE_EINVAL, "need E <= 512, got %d", E);
   const size_t need = ss::verify_scratch_bytes(kBlock, H, I, Is, K, E);
   if (need > kNoAllocScratch)

@@ -6,6 +6,10 @@ renormalisation, the routed experts (moe_decode), the shared expert gated by sig
 y = routed.to(bf16) + shared, with the reference's bf16 rounding of every shared-expert projection. The whole layer
 is one persistent launch per block of up to 4 tokens on the caller's stream (csrc/ss_verify.hip) with no host
 sync, so a step over many layers can be captured in one HIP graph.
+
+The shared expert's gate, up and down projections are bf16 tensors or, as the reference checkpoint keeps them, affine
+4-bit (gs 64) AffineWeights (model/weights.py:84-92; lin -> gemv, model/layers.py:62-76); the router and the
+shared_expert_gate row are bf16 (dense in the checkpoint).
 """
 from __future__ import annotations
 
@@ -14,7 +18,23 @@ import ctypes
 import torch
 
 from .. import _lib
+from ..kernels.gemv_affine import AffineWeight
 from ..memory.slot_pool import SlotPool
+
+
+class SharedQ4(ctypes.Structure):
+    """ssmoe_shared_q4 (include/ssmoe.h): the scales and biases of an affine 4-bit shared expert."""
+    _fields_ = [("gate_s", ctypes.c_void_p), ("gate_b", ctypes.c_void_p), ("up_s", ctypes.c_void_p),
+                ("up_b", ctypes.c_void_p), ("down_s", ctypes.c_void_p), ("down_b", ctypes.c_void_p)]
+
+
+def _wptr(w) -> int:
+    """Device address of a shared-expert weight: the packed words of an AffineWeight, else the bf16 tensor."""
+    return w.q.data_ptr() if isinstance(w, AffineWeight) else w.data_ptr()
+
+
+def _shape(w):
+    return (w.n, w.k) if isinstance(w, AffineWeight) else tuple(w.shape)
 
 
 class MoEVerifyLayer:
@@ -25,14 +45,28 @@ class MoEVerifyLayer:
         self.router_bias = router_bias
         self.hidden, self.inter = pool.hidden, pool.inter
         self.experts = router_w.shape[0]
-        self.shared_inter = sh_gate.shape[0]
-        if router_w.shape != (self.experts, self.hidden) or sh_down.shape != (self.hidden, self.shared_inter):
+        self.shared_inter = _shape(sh_gate)[0]
+        if tuple(router_w.shape) != (self.experts, self.hidden) or _shape(sh_down) != (self.hidden, self.shared_inter):
             raise ValueError("router_w must be [E, H] and sh_down [H, Is]")
-        if sh_up.shape != sh_gate.shape or tuple(sh_g.shape) != (1, self.hidden):
+        if _shape(sh_up) != _shape(sh_gate) or tuple(sh_g.shape) != (1, self.hidden):
             raise ValueError("sh_up must match sh_gate [Is, H] and sh_g must be [1, H]")
-        for t in (router_w, sh_gate, sh_up, sh_down, sh_g):
+        q4 = [isinstance(w, AffineWeight) for w in (sh_gate, sh_up, sh_down)]
+        if any(q4) and not all(q4):
+            raise ValueError("the shared expert's gate, up and down projections are all AffineWeight or all bf16")
+        self.sh_q4 = None
+        if all(q4):
+            for w in (sh_gate, sh_up, sh_down):
+                if w.bits != 4 or w.gs != 64:
+                    raise NotImplementedError(f"affine shared expert: bits 4, gs 64 (got bits={w.bits}, gs={w.gs})")
+                for t in (w.q, w.s, w.b):
+                    if not t.is_contiguous() or not t.is_cuda:
+                        raise ValueError("shared-expert weights must be contiguous GPU tensors")
+            self.sh_q4 = SharedQ4(sh_gate.s.data_ptr(), sh_gate.b.data_ptr(), sh_up.s.data_ptr(), sh_up.b.data_ptr(),
+                                  sh_down.s.data_ptr(), sh_down.b.data_ptr())
+        dense = (router_w, sh_g) if self.sh_q4 is not None else (router_w, sh_gate, sh_up, sh_down, sh_g)
+        for t in dense:
             if t.dtype != torch.bfloat16 or not t.is_contiguous():
-                raise ValueError("router and shared-expert weights must be contiguous bf16")
+                raise ValueError("router, shared_expert_gate and bf16 shared-expert weights must be contiguous bf16")
         if self.experts != pool.experts:
             raise ValueError(f"router has {self.experts} experts, the pool {pool.experts}")
         self.max_tokens = max_tokens
@@ -56,13 +90,16 @@ class MoEVerifyLayer:
         if routed is not None and (tuple(routed.shape) != (t, self.hidden) or routed.dtype != torch.float32):
             raise ValueError(f"routed must be fp32 [{t}, {self.hidden}]")
         L = _lib.lib()
-        _lib.check(L.ssmoe_moe_verify_layer(
-            x.data_ptr(), self.router_w.data_ptr(), _lib.ptr(self.router_bias), self.sh_gate.data_ptr(),
-            self.sh_up.data_ptr(), self.sh_down.data_ptr(), self.sh_g.data_ptr(), self.layer,
-            self.pool.map.data_ptr(), self.pool.map.numel(), self.pool.slot_ptr.data_ptr(), self.pool.slot_ptr.numel(),
-            self.workspace.data_ptr(), self.workspace.numel(), ids.data_ptr(), weights.data_ptr(), y.data_ptr(),
-            _lib.ptr(routed), t, self.hidden, self.inter, self.shared_inter, self.top_k, self.experts,
-            _lib.stream_of(x)))
+        head = (x.data_ptr(), self.router_w.data_ptr(), _lib.ptr(self.router_bias), _wptr(self.sh_gate),
+                _wptr(self.sh_up), _wptr(self.sh_down), self.sh_g.data_ptr())
+        tail = (self.layer, self.pool.map.data_ptr(), self.pool.map.numel(), self.pool.slot_ptr.data_ptr(),
+                self.pool.slot_ptr.numel(), self.workspace.data_ptr(), self.workspace.numel(), ids.data_ptr(),
+                weights.data_ptr(), y.data_ptr(), _lib.ptr(routed), t, self.hidden, self.inter, self.shared_inter,
+                self.top_k, self.experts, _lib.stream_of(x))
+        if self.sh_q4 is None:
+            _lib.check(L.ssmoe_moe_verify_layer(*head, *tail))
+        else:
+            _lib.check(L.ssmoe_moe_verify_layer_q4s(*head, ctypes.addressof(self.sh_q4), *tail))
         return y, ids, weights
 
     def chain(self, stream: torch.Tensor, y: torch.Tensor, ids: torch.Tensor, weights: torch.Tensor,
@@ -86,13 +123,18 @@ class MoEVerifyLayer:
             raise ValueError(f"norm_weight must be bf16 [{self.hidden}]")
         if routed is not None and (tuple(routed.shape) != (t, self.hidden) or routed.dtype != torch.float32):
             raise ValueError(f"routed must be fp32 [{t}, {self.hidden}]")
-        _lib.check(_lib.lib().ssmoe_moe_verify_layer_chain(
-            stream.data_ptr(), _lib.ptr(norm_weight), float(eps), self.router_w.data_ptr(), _lib.ptr(self.router_bias),
-            self.sh_gate.data_ptr(), self.sh_up.data_ptr(), self.sh_down.data_ptr(), self.sh_g.data_ptr(), self.layer,
-            self.pool.map.data_ptr(), self.pool.map.numel(), self.pool.slot_ptr.data_ptr(), self.pool.slot_ptr.numel(),
-            self.workspace.data_ptr(), self.workspace.numel(), ids.data_ptr(), weights.data_ptr(), y.data_ptr(),
-            _lib.ptr(stream_out), _lib.ptr(routed), t, self.hidden, self.inter, self.shared_inter, self.top_k,
-            self.experts, _lib.stream_of(stream)))
+        L = _lib.lib()
+        head = (stream.data_ptr(), _lib.ptr(norm_weight), float(eps), self.router_w.data_ptr(),
+                _lib.ptr(self.router_bias), _wptr(self.sh_gate), _wptr(self.sh_up), _wptr(self.sh_down),
+                self.sh_g.data_ptr())
+        tail = (self.layer, self.pool.map.data_ptr(), self.pool.map.numel(), self.pool.slot_ptr.data_ptr(),
+                self.pool.slot_ptr.numel(), self.workspace.data_ptr(), self.workspace.numel(), ids.data_ptr(),
+                weights.data_ptr(), y.data_ptr(), _lib.ptr(stream_out), _lib.ptr(routed), t, self.hidden, self.inter,
+                self.shared_inter, self.top_k, self.experts, _lib.stream_of(stream))
+        if self.sh_q4 is None:
+            _lib.check(L.ssmoe_moe_verify_layer_chain(*head, *tail))
+        else:
+            _lib.check(L.ssmoe_moe_verify_layer_chain_q4s(*head, ctypes.addressof(self.sh_q4), *tail))
         return y, ids, weights
 
 
@@ -102,7 +144,9 @@ class ChainLayerEntry(ctypes.Structure):
                 ("sh_up", ctypes.c_void_p), ("sh_down", ctypes.c_void_p), ("sh_g", ctypes.c_void_p),
                 ("norm_w", ctypes.c_void_p), ("layer", ctypes.c_int64), ("ids", ctypes.c_void_p),
                 ("weights", ctypes.c_void_p), ("y", ctypes.c_void_p), ("stream_out", ctypes.c_void_p),
-                ("routed_out", ctypes.c_void_p)]
+                ("routed_out", ctypes.c_void_p), ("sh_gate_s", ctypes.c_void_p), ("sh_gate_b", ctypes.c_void_p),
+                ("sh_up_s", ctypes.c_void_p), ("sh_up_b", ctypes.c_void_p), ("sh_down_s", ctypes.c_void_p),
+                ("sh_down_b", ctypes.c_void_p)]
 
 
 class MoEVerifyChain:
@@ -133,10 +177,13 @@ class MoEVerifyChain:
         self._keep = (ys, ids, weights, stream_outs, norm_weights)
         table = (ChainLayerEntry * n)()
         for i, q in enumerate(layers):
-            table[i] = ChainLayerEntry(q.router_w.data_ptr(), _lib.ptr(q.router_bias), q.sh_gate.data_ptr(),
-                                       q.sh_up.data_ptr(), q.sh_down.data_ptr(), q.sh_g.data_ptr(),
+            qs = q.sh_q4
+            table[i] = ChainLayerEntry(q.router_w.data_ptr(), _lib.ptr(q.router_bias), _wptr(q.sh_gate),
+                                       _wptr(q.sh_up), _wptr(q.sh_down), q.sh_g.data_ptr(),
                                        _lib.ptr(norm_weights[i]), q.layer, ids[i].data_ptr(), weights[i].data_ptr(),
-                                       ys[i].data_ptr(), _lib.ptr(stream_outs[i]), None)
+                                       ys[i].data_ptr(), _lib.ptr(stream_outs[i]), None,
+                                       *((qs.gate_s, qs.gate_b, qs.up_s, qs.up_b, qs.down_s, qs.down_b)
+                                         if qs is not None else (None,) * 6))
         self.table_host = table
         raw = bytes(table)
         self.table_dev = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(self.pool.device)

@@ -33,18 +33,39 @@ def zipf_bias(experts: int, s: float = 1.1, seed: int = 1731, device="cuda") -> 
     return bias.to(torch.float32).to(device)
 
 
-class LayerWeights:
-    """Router and shared-expert weights of one synthetic MoE layer."""
+def affine4(rows: int, cols: int, seed: int, scale: float = 0.02 / 4.6, device="cuda"):
+    """A synthetic affine 4-bit (gs 64) weight [rows, cols] in the layout of the reference checkpoint's quantized
+    linears (model/weights.py:84-92): q uniform in 0..15 (random words), s = bf16(|N(0, scale)|), b = bf16(-8 s),
+    so w = s (q - 8) has about the spread of N(0, 4.6 scale)."""
+    from ..kernels.gemv_affine import AffineWeight
 
-    def __init__(self, hidden: int, experts: int, shared_inter: int, seed: int, device="cuda"):
+    g = _gen(seed, device)
+    q = torch.randint(-2**31, 2**31 - 1, (rows, cols // 8), generator=g, device=device, dtype=torch.int32)
+    s = (torch.randn((rows, cols // 64), generator=g, device=device) * scale).abs().to(torch.bfloat16)
+    return AffineWeight(q, s, (-8 * s.float()).to(torch.bfloat16), 4, 64, rows, cols)
+
+
+class LayerWeights:
+    """Router and shared-expert weights of one synthetic MoE layer; `shared_q4` makes the shared expert's gate, up
+    and down projections affine 4-bit AffineWeights (the router and the shared_expert_gate row stay bf16, dense in
+    the reference checkpoint)."""
+
+    def __init__(self, hidden: int, experts: int, shared_inter: int, seed: int, device="cuda", shared_q4=False):
         self.router_w = normal_bf16((experts, hidden), 0.02, seed * 8 + 1, device)
-        self.sh_gate = normal_bf16((shared_inter, hidden), 0.02, seed * 8 + 2, device)
-        self.sh_up = normal_bf16((shared_inter, hidden), 0.02, seed * 8 + 3, device)
-        self.sh_down = normal_bf16((hidden, shared_inter), 0.02, seed * 8 + 4, device)
+        if shared_q4:
+            self.sh_gate = affine4(shared_inter, hidden, seed * 8 + 2, device=device)
+            self.sh_up = affine4(shared_inter, hidden, seed * 8 + 3, device=device)
+            self.sh_down = affine4(hidden, shared_inter, seed * 8 + 4, device=device)
+        else:
+            self.sh_gate = normal_bf16((shared_inter, hidden), 0.02, seed * 8 + 2, device)
+            self.sh_up = normal_bf16((shared_inter, hidden), 0.02, seed * 8 + 3, device)
+            self.sh_down = normal_bf16((hidden, shared_inter), 0.02, seed * 8 + 4, device)
         self.sh_g = normal_bf16((1, hidden), 0.02, seed * 8 + 5, device)
 
     def nbytes(self) -> int:
-        return sum(t.numel() * 2 for t in (self.router_w, self.sh_gate, self.sh_up, self.sh_down, self.sh_g))
+        def nb(t):
+            return t.q.numel() * 4 + t.s.numel() * 4 if hasattr(t, "q") else t.numel() * 2
+        return sum(nb(t) for t in (self.router_w, self.sh_gate, self.sh_up, self.sh_down, self.sh_g))
 
 
 def verify_logits(depth: int, vocab: int, seed: int, rho: float = 0.8, std: float = 3.0, device="cuda"):
