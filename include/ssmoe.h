@@ -192,10 +192,11 @@ int64_t ssmoe_verify_chain_workspace_bytes(int T, int H, int I, int Is, int K, i
  * as n_layers calls of ssmoe_moe_verify_layer_chain; the next layer's router, shared-expert and table reads are issued
  * during the current layer, and the stream passes between layers on the device without a launch.
  * layers_host (host memory) and layers_dev (device memory) hold the same n_layers entries: the host copy is checked
- * and supplies layer 0, the kernel reads the others from the device copy. 1 <= n_layers <= 4096; H 2048 and
- * I 512, the BASELINE layer (other shapes: SSMOE_EINVAL; run them as ssmoe_moe_verify_layer_chain launches);
- * E + Is >= 4 * (compute units), so that every wave has a router or shared row in each layer, and H / 8 <= (compute
- * units), so that the workgroups without output rows can take the shared expert's rows. */
+ * and supplies layer 0, the kernel reads the others from the device copy. 1 <= n_layers <= 4096; (H, I) = (2048,
+ * 512), the BASELINE layer, or (2560, 640), the reference model's (other shapes: SSMOE_EINVAL; run them as
+ * ssmoe_moe_verify_layer_chain launches); E + Is >= 4 * (compute units), so that every wave has a router or shared
+ * row in each layer, and H / 16 < (compute units), so that some workgroups have no output rows and form the shared
+ * expert's rows. The shared expert is bf16 or affine 4-bit (the sh_*_s / sh_*_b fields), the same in every layer. */
 int ssmoe_moe_verify_chain(const uint16_t* stream_in, float eps, const ssmoe_chain_layer* layers_host,
                            const ssmoe_chain_layer* layers_dev, int n_layers, const int32_t* map, int64_t map_len,
                            const int64_t* slot_ptr, int64_t n_slots, void* workspace, int64_t workspace_bytes, int T,

@@ -597,8 +597,9 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       const bool a_act = ahh == (g >> 1) && at < nt && apart == 0;
       // One instantiation per token count (2 or 4 accumulators): the dots, row sums and SwiGLU of absent tokens are
       // not formed.
-      auto run_items = [&](auto ntk_c) {
+      auto run_items = [&](auto ntk_c, auto lds_c) {
         constexpr int NTK = decltype(ntk_c)::value;
+        constexpr bool LDS_SWIGLU = decltype(lds_c)::value;
 #pragma unroll 1
         for (int item = gw; item < n_items; item += W) {
           const int u = item / tiles, p = item - u * tiles;
@@ -655,7 +656,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
               }
             }
           }
-          if constexpr (NTK == 2) {
+          if constexpr (!LDS_SWIGLU) {
             // Every lane of column n now gets row n's dot of each token (gate row n for n < 8, up row n - 8 above),
             // and the lanes n < 8 form h = silu(gate) * up of their row c = n from the up dot 8 lanes up: no LDS.
             float hq[NTK];
@@ -748,10 +749,14 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
           if (item == gw) SS_TRACE(16 + 7);
         }
       };
+      // Up to two tokens: SwiGLU and h packing in registers. More: through the wave's LDS rows, which measured
+      // faster at H 2048; at H 2560 the register file holds only the register form.
       if (nt <= 2)
-        run_items(std::integral_constant<int, 2>{});
+        run_items(std::integral_constant<int, 2>{}, std::false_type{});
+      else if constexpr (NJG > 16)
+        run_items(std::integral_constant<int, kTBv>{}, std::false_type{});
       else
-        run_items(std::integral_constant<int, kTBv>{});
+        run_items(std::integral_constant<int, kTBv>{}, std::true_type{});
       // Each wave publishes its own items as soon as its stores are acknowledged.
       stores_done();
       if (lane == 0) csignal_add(ctr, CTR_ITEMS, wave_items, 4 * bid + w);
@@ -760,30 +765,36 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
 
     __syncthreads();  // every wave is past its items: the x fragments are dead, the prefetch slots may be written
 
-    if (!has_tile && bid < 2 * (H >> 4)) {
-      // ---------------------------------------------------------- the shared expert's rows of workgroup bid - H/16
-      // (the operations of the single-layer kernel's shared rows), gated and published for that workgroup's combine
-      const int ob = bid - (H >> 4);
+    if (!has_tile) {
+      // ---------------------------------------------------------- the shared expert's rows of output blocks
+      // ob = bid - H/16, + (G - H/16), ... (< H/16; the operations of the single-layer kernel's shared rows), gated and
+      // published for the combines of those workgroups
+      const int nfree = G - (H >> 4);
+      int ob = bid - (H >> 4);
       load_shared_down<4, NSC>(va, 16 * ob + 4 * w, shw);
       wait_ctr(CTR_SHARED, (l + 1) * (Is + 1));
       const SharedIn shin = shared_load(va, gsh, ush, nt);
       const uint16_t sgl_t = ld_ag(sgl + ((lane & 3) < nt ? (lane & 3) : 0));
       shared_hs_all<NSC>(va, shin, gsh, ush, w, nt, hsl);
       __syncthreads();
-      float o[4][kTBv];
-      shared_down_rows<4, NSC>(va, hsl, shw, nt, o);
-      // lane 4 rr + t publishes row 16 ob + 4 w + rr of token t
-      const int rr = (lane >> 2) & 3, t = lane & 3;
-      float shv = 0.f;
+      const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-ss_bf16_to_f32(sgl_t))));
+#pragma unroll 1
+      for (; ob < (H >> 4); ob += nfree) {
+        if (ob != bid - (H >> 4)) load_shared_down<4, NSC>(va, 16 * ob + 4 * w, shw);
+        float o[4][kTBv];
+        shared_down_rows<4, NSC>(va, hsl, shw, nt, o);
+        // lane 4 rr + t publishes row 16 ob + 4 w + rr of token t
+        const int rr = (lane >> 2) & 3, t = lane & 3;
+        float shv = 0.f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
-        for (int u = 0; u < kTBv; ++u) shv = (q == rr && u == t) ? o[q][u] : shv;
-      if (lane < 16 && t < nt) {
-        const float shb = ss_round_bf16(shv);
-        const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-ss_bf16_to_f32(sgl_t))));
-        const uint32_t sh2 = ss_f32_to_bf16(sgv * shb);
-        st_ag(shx + (size_t)t * H + 16 * ob + 4 * w + rr, ((uint64_t)tag << 32) | (uint64_t)sh2);
+          for (int u = 0; u < kTBv; ++u) shv = (q == rr && u == t) ? o[q][u] : shv;
+        if (lane < 16 && t < nt) {
+          const float shb = ss_round_bf16(shv);
+          const uint32_t sh2 = ss_f32_to_bf16(sgv * shb);
+          st_ag(shx + (size_t)t * H + 16 * ob + 4 * w + rr, ((uint64_t)tag << 32) | (uint64_t)sh2);
+        }
       }
       SS_TRACE(13);
     }
@@ -1036,14 +1047,16 @@ static hipError_t launch_chain_nj(const ChainArgs& a, hipStream_t st) {
   if (cfg.per_cu < 1) return hipErrorCooperativeLaunchTooLarge;
   if (dly.P < 1 || dly.total > kLdsBudget || cfg.lds_static + dly.total > 160 * 1024) return hipErrorInvalidConfiguration;
   const int grid = cfg.cus;
-  if (grid < 2 * (a.H / 16) || a.E + a.Is < 4 * grid) return hipErrorInvalidConfiguration;
+  if (grid <= a.H / 16 || a.E + a.Is < 4 * grid) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(256), dly.total, st, a, rec);
   return hipGetLastError();
 }
 
-bool chain_shape_supported(int H, int I) { return H == 2048 && I == 512; }
+bool chain_shape_supported(int H, int I) { return (H == 2048 && I == 512) || (H == 2560 && I == 640); }
 
-const char* chain_shapes_text() { return "the chain kernel is built for H 2048 with I 512 only"; }
+const char* chain_shapes_text() {
+  return "the chain kernel is built for H 2048 with I 512 (BASELINE) and H 2560 with I 640 (the reference model)";
+}
 
 hipError_t launch_chain(const ChainArgs& a, hipStream_t st) {
   // One instantiated shape: H 2048 x I 512, the BASELINE layer (the layer loop is sized to the register file for it);
@@ -1051,6 +1064,7 @@ hipError_t launch_chain(const ChainArgs& a, hipStream_t st) {
   const int njg = a.H / 128, njd = a.I / 128;
   const bool q4 = a.l0.sh_gate_s != nullptr;  // every layer alike (checked by the entry point)
   if (njg == 16 && njd == 4) return q4 ? launch_chain_nj<16, 4, true>(a, st) : launch_chain_nj<16, 4, false>(a, st);
+  if (njg == 20 && njd == 5) return q4 ? launch_chain_nj<20, 5, true>(a, st) : launch_chain_nj<20, 5, false>(a, st);
   return hipErrorInvalidValue;
 }
 

@@ -473,9 +473,10 @@ int ssmoe_moe_verify_chain(const uint16_t* stream_in, float eps, const ssmoe_cha
   if (int rc = current_device(&dev)) return rc;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     return fail(SSMOE_EHIP, "hipDeviceGetAttribute(multiprocessor count) failed");
-  if (E + Is < 4 * cus || H / 8 > cus)
-    return fail(SSMOE_EINVAL, "a chain needs E + Is >= 4 * CUs (one router or shared row per wave) and H / 8 <= CUs "
-                "(%d CUs; E + Is = %d, H = %d); launch the layers one by one", cus, E + Is, H);
+  if (E + Is < 4 * cus || H / 16 >= cus)
+    return fail(SSMOE_EINVAL, "a chain needs E + Is >= 4 * CUs (one router or shared row per wave) and H / 16 < CUs "
+                "(workgroups without output rows for the shared expert's rows; %d CUs; E + Is = %d, H = %d); launch "
+                "the layers one by one", cus, E + Is, H);
   int* err = nullptr;
   if (int rc = status_ptr(&err)) return rc;
   ss::ChainArgs a{};

@@ -196,11 +196,11 @@ class MoEVerifyChain:
     @staticmethod
     def supported(hidden: int, inter: int, shared_inter: int, top_k: int, experts: int, device="cuda") -> bool:
         """True when the shape has a chain kernel, every wave of the grid (one workgroup of 4 waves per CU) owns a
-        router or shared-expert row (E + Is >= 4 * CUs), which the chain's hand-offs rely on, and the workgroups
-        without output rows can take the shared expert's rows (H / 8 <= CUs)."""
+        router or shared-expert row (E + Is >= 4 * CUs), which the chain's hand-offs rely on, and some workgroups
+        have no output rows (H / 16 < CUs): they form the shared expert's rows."""
         cus = torch.cuda.get_device_properties(torch.device(device)).multi_processor_count
         return (_lib.lib().ssmoe_verify_chain_workspace_bytes(4, hidden, inter, shared_inter, top_k, experts) > 0
-                and experts + shared_inter >= 4 * cus and hidden // 8 <= cus)
+                and experts + shared_inter >= 4 * cus and hidden // 16 < cus)
 
     def run(self, stream_in: torch.Tensor) -> None:
         """All layers on the current stream; the rows are those of stream_in ([T, H] bf16, T <= 4)."""

@@ -101,3 +101,41 @@ def test_chain_with_q4_shared_expert(T):
         torch.cuda.synchronize()
         assert torch.equal(y, sg.ys[l]) and torch.equal(ids, sg.ids[l]), l
         _check_layer(pool, lws[l], l, xb, y, ids, wts, routed, K, mw[l].router_bias, map_layer=l)
+
+
+@pytest.mark.parametrize("T,q4", [(2, True), (3, True), (4, True), (3, False)])
+def test_chain_at_the_reference_model_shape(T, q4):
+    """The single-launch chain at the reference model's MoE layer (config.py:8-21: H 2560, 512 experts top-10,
+    moe_intermediate 640, shared 640; the shared expert affine 4-bit as the checkpoint keeps it, or bf16): equal to
+    one launch per layer bit for bit, each layer against the oracle on its own input."""
+    H, I, E, K, NL = 2560, 640, 512, 10, 3
+    print(f"[ref-shape chain] H={H} I={I} T={T} q4={q4}", flush=True)
+    pool = make_pool(E, H, I, seed=961, layers=NL)
+    lws = [LayerWeights(H, E, I, seed=962 + l, shared_q4=q4) for l in range(NL)]
+    mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, zipf_bias(E, 1.1, 970 + l))
+          for l, w in enumerate(lws)]
+    norms = [normal_bf16((H,), 0.1, 980 + l) + 1 for l in range(NL + 1)]
+    sg = MTPStepGraph(pool, mw, None, depth=T - 1, norm_weights=norms, top_k=K)
+    per_layer = MTPStepGraph(pool, mw, None, depth=T - 1, norm_weights=norms, top_k=K, single_launch=False)
+    assert sg.chain is not None
+    for trial in range(2):
+        x = normal_bf16((T, H), 1.0, 990 + trial)
+        per_layer.step(x)
+        sg.step(x)
+        torch.cuda.synchronize()
+        for l in range(NL):
+            assert torch.equal(sg.ids[l], per_layer.ids[l]) and torch.equal(sg.weights[l], per_layer.weights[l])
+            assert torch.equal(sg.ys[l], per_layer.ys[l]) and torch.equal(sg.streams[l + 1], per_layer.streams[l + 1])
+    for l in range(NL):
+        xb_bits = O.residual_rmsnorm(bits(sg.streams[l]), None, bits(norms[l]))[1]
+        w = lws[l]
+        _, _, rids, rw = O.router(xb_bits, bits(w.router_w), K, mw[l].router_bias.cpu().numpy())
+        assert np.array_equal(sg.ids[l].cpu().numpy(), rids), l
+        assert np.array_equal(sg.weights[l].cpu().numpy().view(np.uint32), rw.view(np.uint32)), l
+        r64 = O.moe_routed_fp64(O.bf16_to_f32(xb_bits), rids, rw, DenseCache(pool, layer=l)).astype(np.float32)
+        if q4:
+            sh, sgl = O.shared_expert_q4(xb_bits, _q4(w.sh_gate), _q4(w.sh_up), _q4(w.sh_down), bits(w.sh_g))
+        else:
+            sh, sgl = O.shared_expert(xb_bits, bits(w.sh_gate), bits(w.sh_up), bits(w.sh_down), bits(w.sh_g))
+        err = O.rel_l2(O.bf16_to_f32(bits(sg.ys[l])), O.bf16_to_f32(O.combine_shared(r64, sh, sgl)))
+        assert err <= REL_Y, (l, err)
