@@ -189,6 +189,56 @@ def verify_chain_leg(pool, weights, biases, nl, t, steps, warmup, dev):
             "stream_finite": finite}
 
 
+def ref_chain_leg(steps, warmup, dev, nl=16):
+    """The verify step at the reference model's MoE layer (model/config.py:8-21: H 2560, 512 experts top-10,
+    moe_intermediate 640, shared 640 as affine 4-bit gs64 like the checkpoint's shared_expert projections, bf16 router
+    and shared_expert_gate, Zipf 1.1 routing bias), `nl` distinct layers, T = 2 and T = 3 (the reference's verify
+    width, 1 + DEPTH): one persistent launch for all layers (ssmoe_moe_verify_chain) against one launch per layer
+    (ssmoe_moe_verify_layer_chain), each replayed as a HIP graph with a new input per step."""
+    import torch
+
+    from slotstream_spark_amd.engine.step import MoEWeights, MTPStepGraph
+    from slotstream_spark_amd.memory.slot_pool import SlotPool
+    from slotstream_spark_amd.memory.synth import LayerWeights, normal_bf16, zipf_bias
+
+    HR, IR, ER = 2560, 640, 512
+    pool = SlotPool(nl, ER, HR, IR, device=dev)
+    pool.fill_random(5101)
+    pool.place_permuted(5102)
+    mw = []
+    for l in range(nl):
+        w = LayerWeights(HR, ER, IR, seed=5103 + l, device=dev, shared_q4=True)
+        mw.append(MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, zipf_bias(ER, 1.1, 5200 + l,
+                                                                                              device=dev)))
+    res = {"shape": "H 2560, E 512 top-10, I 640, shared 640 affine 4-bit gs64 (records of 2,764,800 B)",
+           "layers": nl}
+    for t in (2, 3):
+        xs = normal_bf16((8, t, HR), 1.0, 5300 + t, dev)
+        out = {}
+        for name, single in (("single_launch", True), ("per_layer", False)):
+            sg = MTPStepGraph(pool, mw, None, depth=t - 1, top_k=K, single_launch=single, device=dev)
+            if single and sg.chain is None:
+                raise RuntimeError("no chain kernel at the reference shape on this device")
+            for i in range(warmup):
+                sg.step(xs[i % 8])
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for i in range(steps):
+                sg.step(xs[i % 8])
+            e1.record()
+            torch.cuda.synchronize()
+            out[name] = round(e0.elapsed_time(e1) * 1000.0 / steps / nl, 3)
+            del sg
+        out["speedup"] = round(out["per_layer"] / out["single_launch"], 3)
+        res[f"T{t}_us_per_layer"] = out
+        log(f"reference-shape chain T={t}: single launch {out['single_launch']} us/layer, one launch per layer "
+            f"{out['per_layer']} us/layer")
+    del pool
+    torch.cuda.empty_cache()
+    return res
+
+
 def peaks_leg(dev):
     """Measured achievable peaks beside the spec ones: a 1 GiB device copy (2 GiB moved), a 1 GiB fp32 sum (read
     stream) and an 8192^3 bf16 GEMM on the platform BLAS; best of 10 launches each, HIP events."""
@@ -859,9 +909,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--legs", default="isolated,decode,prefill,config2,config4,lm_head,step,draft,pool,ref_decode,"
-                                      "peaks",
+                                      "ref_chain,peaks",
                     help="comma list of legs besides the headline chain: isolated, decode, prefill, config2, "
-                         "config4, lm_head, step, draft, pool, ref_decode, peaks")
+                         "config4, lm_head, step, draft, pool, ref_decode, ref_chain, peaks")
     ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--config2-steps", type=int, default=1000)
     ap.add_argument("--config4-layers", type=int, default=48)
@@ -999,6 +1049,10 @@ def main():
     if "pool" in legs:
         pl = pool_leg(dev)
 
+    rc_ = None
+    if "ref_chain" in legs:
+        rc_ = ref_chain_leg(max(args.steps // 2, 10), 3, dev)
+
     peaks = peaks_leg(dev) if "peaks" in legs else None
     if peaks is not None:
         # the same achieved figures against this build's own ceilings
@@ -1052,6 +1106,7 @@ def main():
         "step_graph": stp,
         "draft_head": drf,
         "reference_shape_moe_decode": rd,
+        "reference_shape_chain": rc_,
         "pool": pl,
         "cpu_baseline": cpu,
     }
