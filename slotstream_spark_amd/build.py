@@ -30,7 +30,20 @@ def _compile(src: Path) -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     noise = ("is not a recognized feature for this target", "kernel-resource-usage")
     lines = (r.stderr or "").splitlines()
-    err = "\n".join(l for l in lines if not any(n in l for n in noise))
+    # Drop the resource remarks with their include-stack and source-snippet lines; keep every other diagnostic whole.
+    kept, pending, drop = [], [], False
+    for l in lines:
+        if l.startswith("In file included from"):
+            pending.append(l)
+        elif re.match(r"^\s*\d*\s*\|", l):
+            if not drop:
+                kept.append(l)
+        else:
+            drop = any(n in l for n in noise)
+            if not drop:
+                kept += pending + [l]
+            pending = []
+    err = "\n".join(kept)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
     if err.strip():

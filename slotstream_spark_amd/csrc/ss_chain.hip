@@ -771,7 +771,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       // published for the combines of those workgroups
       const int nfree = G - (H >> 4);
       int ob = bid - (H >> 4);
-      load_shared_down<4, NSC>(va, 16 * ob + 4 * w, shw);
+      load_shared_down<4, NSC, SHQ4>(va, 16 * ob + 4 * w, shw);
       wait_ctr(CTR_SHARED, (l + 1) * (Is + 1));
       const SharedIn shin = shared_load(va, gsh, ush, nt);
       const uint16_t sgl_t = ld_ag(sgl + ((lane & 3) < nt ? (lane & 3) : 0));
@@ -780,9 +780,9 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
       const float sgv = ss_round_bf16(1.f / (1.f + ss_expf(-ss_bf16_to_f32(sgl_t))));
 #pragma unroll 1
       for (; ob < (H >> 4); ob += nfree) {
-        if (ob != bid - (H >> 4)) load_shared_down<4, NSC>(va, 16 * ob + 4 * w, shw);
+        if (ob != bid - (H >> 4)) load_shared_down<4, NSC, SHQ4>(va, 16 * ob + 4 * w, shw);
         float o[4][kTBv];
-        shared_down_rows<4, NSC>(va, hsl, shw, nt, o);
+        shared_down_rows<4, NSC, SHQ4>(va, hsl, shw, nt, o);
         // lane 4 rr + t publishes row 16 ob + 4 w + rr of token t
         const int rr = (lane >> 2) & 3, t = lane & 3;
         float shv = 0.f;

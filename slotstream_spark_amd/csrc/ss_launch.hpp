@@ -101,6 +101,8 @@ struct VerifyArgs {
 };
 size_t verify_scratch_bytes(int T, int H, int I, int Is, int K, int E);
 hipError_t launch_verify(const VerifyArgs& a, hipStream_t st);
+// The affine 4-bit shared-expert instantiations (ss_verify_q4.hip); launch_verify calls it when sh_gs is set.
+hipError_t launch_verify_q4(const VerifyArgs& a, hipStream_t st);
 // Zeroes `bytes` (a multiple of 16) at the 16-byte aligned `p` with vector stores (a kernel, so that it can sit in a
 // captured graph where a memset node could not).
 hipError_t launch_zero16(void* p, size_t bytes, hipStream_t st);

@@ -691,9 +691,9 @@ SS_DEV void shared_hs_all(const VerifyArgs& a, const SharedIn& in0, const uint16
 }
 
 // The shared-expert down row registers of one wave, chunk c of row r in sh_w[r][c]: bf16 rows (the lane's 8
-// elements 512 c + 8 l .. + 7), or with an affine 4-bit down projection the q4_chunk register of those elements.
-// NSC chunks per row (512 * NSC >= Is): the kernels take NSC = 2 with I > 512, else 1.
-template <int NR, int NSC>
+// elements 512 c + 8 l .. + 7), or with an affine 4-bit down projection (Q4: sh_ds, sh_db set) the q4_chunk register
+// of those elements. NSC chunks per row (512 * NSC >= Is): the kernels take NSC = 2 with I > 512, else 1.
+template <int NR, int NSC, bool Q4>
 SS_DEV void load_shared_down(const VerifyArgs& a, int row0, uint4 (&sh_w)[NR][NSC]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
@@ -704,7 +704,7 @@ SS_DEV void load_shared_down(const VerifyArgs& a, int row0, uint4 (&sh_w)[NR][NS
       const bool ok = 8 * w8 < a.Is;
       const size_t row = (size_t)(row0 + rr);
       sh_w[rr][c] = !ok ? make_uint4(0u, 0u, 0u, 0u)
-                    : a.sh_ds ? q4_chunk(a.sh_down + row * (a.Is / 4), a.sh_ds + row * (a.Is / 64),
+                    : Q4 ? q4_chunk(a.sh_down + row * (a.Is / 4), a.sh_ds + row * (a.Is / 64),
                                          a.sh_db + row * (a.Is / 64), c, lane)
                               : ldg16(a.sh_down + row * a.Is + 8 * w8);
     }
@@ -712,7 +712,7 @@ SS_DEV void load_shared_down(const VerifyArgs& a, int row0, uint4 (&sh_w)[NR][NS
 
 // Shared-expert down rows of one wave, in the dense_rows order (lane l: chunk 0's elements, then chunk 1's, by fma
 // from 0; then the butterfly): the dot of hs (hsl) with the down rows; out[rr][t] receives the fp32 sums (every lane).
-template <int NR, int NSC>
+template <int NR, int NSC, bool Q4>
 SS_DEV void shared_down_rows(const VerifyArgs& a, const float* hsl, const uint4 (&sh_w)[NR][NSC], int nt,
                              float (&out)[NR][kTBv]) {
   const int lane = threadIdx.x & 63;
@@ -738,7 +738,7 @@ SS_DEV void shared_down_rows(const VerifyArgs& a, const float* hsl, const uint4 
 #pragma unroll
         for (int q = 0; q < kTBv; ++q)
           if (q == t) ac = sacc[rr][q];
-        if (a.sh_ds) {
+        if (Q4) {
           const float sc = bf_lo(ww[1]), bi = bf_hi(ww[1]);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
