@@ -41,7 +41,8 @@ int ssmoe_device_error(int* flags, int clear);
  * layer there, the layer before at row 512 + workgroup, and a few more stamps of each at rows 256 + and 768 +
  * workgroup. The prefill grouped GEMM pair (ssmoe_fused_moe_affine, ssmoe_moe_prefill) writes four entries per
  * block: start and end stamps, expert << 32 | valid rows, XCC_ID << 32 | HW_ID; gate/up blocks at
- * buf[4 * block], down blocks at buf[8192 + 4 * block] (blocks past 2048 per kernel are not recorded). NULL switches
+ * buf[4 * block], down blocks at buf[8192 + 4 * block] (blocks past 2048 per kernel are not recorded). The one-launch
+ * p/q round (ssmoe_accept_pq) writes 16 stamps per workgroup at buf[workgroup * 16 + k]. NULL switches
  * it off. Process-wide, not thread-safe; a launch captured in a graph keeps the setting of its capture. */
 int ssmoe_set_trace(void* buf, int64_t entries);
 

@@ -287,23 +287,6 @@ void or_accept_greedy(const float* target, const int32_t* drafts, int D, int V, 
   out[3] = flags;
 }
 
-typedef struct {
-  const float* row;
-  float m, z;
-} PRow;
-
-static float row_max_div(const float* x, int V, float temp) {
-  float m = -INFINITY;
-  for (int j = 0; j < V; ++j) m = fmaxf(m, x[j] / temp);
-  return m;
-}
-
-static int row_bad(const float* x, int V) {
-  for (int j = 0; j < V; ++j)
-    if (!is_finite_f(x[j])) return 1;
-  return 0;
-}
-
 /* Hierarchical sum of f(j): sub-chunk totals (sequential from 0), chunk totals (butterfly), row (sequential). */
 typedef float (*ValFn)(const void* ctx, int j);
 
@@ -321,48 +304,146 @@ static float chunk_total(ValFn f, const void* ctx, int c, int V, float* sub /* [
   return butterfly_sum(lanes);
 }
 
-typedef struct {
-  const float* x;
-  float temp, m;
-} ExpCtx;
+/* ---------------------------------------------------------------- p/q acceptance (Leviathan et al. 2023, Alg. 1)
+ * No reference counterpart. Every sum has a fixed order made of two pieces, so that the kernels form it with
+ * lane-parallel operations:
+ *   scan64: the inclusive prefix of 64 values by Hillis-Steele steps d = 1, 2, 4, .., 32 (P_l += P_{l-d} for l >= d,
+ *   each step from the previous step's values); total64 = the last prefix.
+ *   a "lane layout" of n values with k per lane: lane l holds values k l .. k l + k - 1 (those < n); its local sum is
+ *   the sequential sum from 0; the layout's prefixes are scan64 of the local sums.
+ * Per row (logits x, V entries, 1024-entry chunks c, invT = 1 / T in fp32):
+ *   y_j = x_j * invT; m_c = max of y_j over the chunk (NaN ignored); e_j = exp(y_j - m_c);
+ *   s_c = total64 of the chunk's 64 sub-chunks of 16 (lane layout k = 16: sub-chunk l = entries 16 l .. 16 l + 15);
+ *   M = max m_c; g_c = exp(m_c - M); Z = total64 of t_c = s_c * g_c in the lane layout k = ceil(nch / 64);
+ *   a_c = g_c / Z; p_j = e_j * a_c.
+ * The drafts: x_i is accepted iff u_i * q_i(x_i) < p_i(x_i) (p, q of target row i and draft row i); the first
+ * rejection samples from v_j = max(0, p_j - q_j) of row i, and every draft accepted from v_j = p_j of row D. A
+ * non-finite logit in a row the round reaches stops it; a draft outside [0, V) is flagged and rejected.
+ * The sample: r_c = total64 of the chunk's sub-chunk sums of v; S = total64 of r_c in the chunk lane layout;
+ * target u * S. descend() on the chunk layout gives the chunk cs and its base b; descend() on chunk cs's
+ * sub-chunks with target (u * S - b) gives the entry. */
+#define PQ_MAX_NCH 1024
 
-static float val_exp(const void* c, int j) {
-  const ExpCtx* e = (const ExpCtx*)c;
-  return or_expf(e->x[j] / e->temp - e->m);
+static void scan64(const float* L, float* P) {
+  float a[64], b[64];
+  memcpy(a, L, sizeof a);
+  for (int d = 1; d < 64; d <<= 1) {
+    for (int l = 0; l < 64; ++l) b[l] = l >= d ? a[l] + a[l - d] : a[l];
+    memcpy(a, b, sizeof a);
+  }
+  memcpy(P, a, sizeof a);
+}
+
+/* Local sums of a lane layout of n values with k per lane. */
+static void lane_sums(const float* v, int n, int k, float* L) {
+  for (int l = 0; l < 64; ++l) {
+    float s = 0.0f;
+    for (int i = 0; i < k && k * l + i < n; ++i) s = s + v[k * l + i];
+    L[l] = s;
+  }
+}
+
+/* The search over a lane layout (n values, k per lane) for target t: the first lane whose prefix exceeds t (else
+ * the last lane with a nonzero local sum, else lane 0), then inside it the first value whose running sum from the
+ * lane's exclusive prefix exceeds t (else its last nonzero value, else its first); *base receives the running sum
+ * before the chosen value. Returns the value's index, clamped to n - 1. */
+static int descend(const float* v, int n, int k, float t, float* base) {
+  float L[64], P[64];
+  lane_sums(v, n, k, L);
+  scan64(L, P);
+  int ls = -1;
+  for (int l = 0; l < 64 && ls < 0; ++l)
+    if (P[l] > t) ls = l;
+  if (ls < 0) {
+    for (int l = 0; l < 64; ++l)
+      if (L[l] > 0.0f) ls = l;
+    if (ls < 0) ls = 0;
+  }
+  const float e = ls > 0 ? P[ls - 1] : 0.0f;
+  float run = e;
+  int pick = -1, last = -1;
+  for (int i = 0; i < k && k * ls + i < n; ++i) {
+    const float x = v[k * ls + i];
+    if (x > 0.0f) last = i;
+    const float nx = run + x;
+    if (nx > t) {
+      pick = i;
+      break;
+    }
+    run = nx;
+  }
+  if (pick < 0) {
+    pick = last >= 0 ? last : 0;
+    run = e;
+    for (int i = 0; i < pick; ++i) run = run + v[k * ls + i];
+  }
+  *base = run;
+  const int idx = k * ls + pick;
+  return idx < n ? idx : n - 1;
 }
 
 typedef struct {
-  const float* p;
-  const float* q; /* NULL: plain p */
-  float temp, mp, zp, mq, zq;
-} SampCtx;
+  float m[PQ_MAX_NCH], a[PQ_MAX_NCH];
+  float M, Z;
+  int bad;
+} PqRow;
 
-static float val_sample(const void* c, int j) {
-  const SampCtx* s = (const SampCtx*)c;
-  const float p = or_expf(s->p[j] / s->temp - s->mp) / s->zp;
-  if (!s->q) return p;
-  const float q = or_expf(s->q[j] / s->temp - s->mq) / s->zq;
-  const float d = p - q;
-  return d > 0.0f ? d : 0.0f;
+static float pq_inv(float temp) { return 1.0f / temp; }
+
+/* e_j of chunk c's maximum for one row (y = x * invT). */
+static float pq_e(const float* x, int j, float invT, float mc) { return or_expf(x[j] * invT - mc); }
+
+static void pq_row(const float* x, int V, float invT, PqRow* r) {
+  const int nch = (V + CHUNK - 1) / CHUNK, kc = (nch + 63) / 64;
+  float s[PQ_MAX_NCH], t[PQ_MAX_NCH], g[PQ_MAX_NCH];
+  r->bad = 0;
+  r->M = -INFINITY;
+  for (int c = 0; c < nch; ++c) {
+    float mc = -INFINITY;
+    for (int j = c * CHUNK; j < V && j < (c + 1) * CHUNK; ++j) {
+      if (!is_finite_f(x[j])) r->bad = 1;
+      mc = fmaxf(mc, x[j] * invT);
+    }
+    float e[CHUNK], L[64], P[64];
+    for (int i = 0; i < CHUNK; ++i) {
+      const int j = c * CHUNK + i;
+      e[i] = j < V ? pq_e(x, j, invT, mc) : 0.0f;
+    }
+    lane_sums(e, CHUNK, SUB, L);
+    scan64(L, P);
+    r->m[c] = mc;
+    s[c] = P[63];
+    r->M = fmaxf(r->M, mc);
+  }
+  for (int c = 0; c < nch; ++c) {
+    g[c] = or_expf(r->m[c] - r->M);
+    t[c] = s[c] * g[c];
+  }
+  float L[64], P[64];
+  lane_sums(t, nch, kc, L);
+  scan64(L, P);
+  r->Z = P[63];
+  for (int c = 0; c < nch; ++c) r->a[c] = g[c] / r->Z;
 }
 
-static float row_z(const float* x, int V, float temp, float m) {
-  ExpCtx c = {x, temp, m};
-  const int nch = (V + CHUNK - 1) / CHUNK;
-  float z = 0.0f;
-  for (int k = 0; k < nch; ++k) z = z + chunk_total(val_exp, &c, k, V, NULL);
-  return z;
+static float pq_p(const float* x, int j, float invT, const PqRow* r) {
+  const int c = j / CHUNK;
+  return pq_e(x, j, invT, r->m[c]) * r->a[c];
 }
 
-/* p/q acceptance, Leviathan et al. 2023 Alg. 1 (no reference counterpart). out as ssmoe.h; work: >= nch*65 floats. */
+/* out as ssmoe.h; work is unused (kept for the binding). */
 void or_accept_pq(const float* target, const float* draft, const int32_t* drafts, const float* uniforms, int D,
                   int V, float temp, int32_t* out, float* work) {
-  const int nch = (V + CHUNK - 1) / CHUNK;
+  (void)work;
+  const int nch = (V + CHUNK - 1) / CHUNK, kc = (nch + 63) / 64;
+  const float invT = pq_inv(temp);
+  PqRow* rt = (PqRow*)malloc(sizeof(PqRow) * (size_t)(D + 1));
+  PqRow* rd = (PqRow*)malloc(sizeof(PqRow) * (size_t)(D > 0 ? D : 1));
+  for (int i = 0; i <= D; ++i) pq_row(target + (size_t)i * V, V, invT, &rt[i]);
+  for (int i = 0; i < D; ++i) pq_row(draft + (size_t)i * V, V, invT, &rd[i]);
   int good = 0, flags = 0, stop = 0, srow = D, sdraft = -1;
   for (int i = 0; i < D; ++i) {
-    const float* t = target + (size_t)i * V;
-    const float* d = draft + (size_t)i * V;
-    if (row_bad(t, V) || row_bad(d, V)) {
+    if (rt[i].bad || rd[i].bad) {
       flags |= 1;
       stop = 1;
       break;
@@ -374,10 +455,8 @@ void or_accept_pq(const float* target, const float* draft, const int32_t* drafts
       sdraft = i;
       break;
     }
-    const float mp = row_max_div(t, V, temp), mq = row_max_div(d, V, temp);
-    const float zp = row_z(t, V, temp, mp), zq = row_z(d, V, temp, mq);
-    const float p = or_expf(t[x] / temp - mp) / zp;
-    const float q = or_expf(d[x] / temp - mq) / zq;
+    const float p = pq_p(target + (size_t)i * V, x, invT, &rt[i]);
+    const float q = pq_p(draft + (size_t)i * V, x, invT, &rd[i]);
     if (uniforms[i] * q < p) {
       ++good;
       continue;
@@ -386,7 +465,7 @@ void or_accept_pq(const float* target, const float* draft, const int32_t* drafts
     sdraft = i;
     break;
   }
-  if (!stop && sdraft < 0 && row_bad(target + (size_t)D * V, V)) {
+  if (!stop && sdraft < 0 && rt[D].bad) {
     flags |= 1;
     stop = 1;
   }
@@ -394,83 +473,60 @@ void or_accept_pq(const float* target, const float* draft, const int32_t* drafts
   for (int i = 0; i < good; ++i) out[4 + i] = drafts[i];
   int emit = good;
   if (!stop) {
-    SampCtx sc;
-    sc.p = target + (size_t)srow * V;
-    sc.q = sdraft >= 0 ? draft + (size_t)sdraft * V : NULL;
-    sc.temp = temp;
-    sc.mp = row_max_div(sc.p, V, temp);
-    sc.zp = row_z(sc.p, V, temp, sc.mp);
-    sc.mq = sc.q ? row_max_div(sc.q, V, temp) : 0.0f;
-    sc.zq = sc.q ? row_z(sc.q, V, temp, sc.mq) : 0.0f;
-    float* stot = work;            /* [nch][64] */
-    float* rtot = work + nch * 64; /* [nch] */
-    for (int c = 0; c < nch; ++c) rtot[c] = chunk_total(val_sample, &sc, c, V, stot + c * 64);
-    float S = 0.0f;
-    for (int c = 0; c < nch; ++c) S = S + rtot[c];
-    if (!(S > 0.0f)) flags |= 4;
-    const float target_u = uniforms[uidx] * S;
-    int cs = -1, clast = -1;
-    float base = 0.0f, run = 0.0f;
+    const float* tp = target + (size_t)srow * V;
+    const float* dq = sdraft >= 0 ? draft + (size_t)sdraft * V : NULL;
+    float* v = (float*)malloc(sizeof(float) * (size_t)nch * CHUNK);
+    float r[PQ_MAX_NCH];
     for (int c = 0; c < nch; ++c) {
-      const float nx = run + rtot[c];
-      if (rtot[c] > 0.0f) clast = c;
-      if (cs < 0 && nx > target_u) {
-        cs = c;
-        base = run;
+      for (int i = 0; i < CHUNK; ++i) {
+        const int j = c * CHUNK + i;
+        float x = 0.0f;
+        if (j < V) {
+          const float p = pq_p(tp, j, invT, &rt[srow]);
+          if (dq) {
+            const float d = p - pq_p(dq, j, invT, &rd[sdraft]);
+            x = d > 0.0f ? d : 0.0f;
+          } else {
+            x = p;
+          }
+        }
+        v[(size_t)c * CHUNK + i] = x;
       }
-      run = nx;
+      float L[64], P[64];
+      lane_sums(v + (size_t)c * CHUNK, CHUNK, SUB, L);
+      scan64(L, P);
+      r[c] = P[63];
     }
-    if (cs < 0) {
-      cs = clast < 0 ? 0 : clast;
-      base = 0.0f;
-      for (int c = 0; c < cs; ++c) base = base + rtot[c];
-    }
-    int bs = -1, blast = -1;
-    float sbase = base;
-    run = base;
-    for (int b = 0; b < 64; ++b) {
-      const float t = stot[cs * 64 + b];
-      const float nx = run + t;
-      if (t > 0.0f) blast = b;
-      if (bs < 0 && nx > target_u) {
-        bs = b;
-        sbase = run;
-      }
-      run = nx;
-    }
-    if (bs < 0) {
-      bs = blast < 0 ? 0 : blast;
-      sbase = base;
-      for (int b = 0; b < bs; ++b) sbase = sbase + stot[cs * 64 + b];
-    }
-    int pick = -1, last = -1;
-    run = sbase;
-    for (int i = 0; i < SUB; ++i) {
-      const int j = cs * CHUNK + bs * SUB + i;
-      if (j >= V) break;
-      const float v = val_sample(&sc, j);
-      if (v > 0.0f) last = j;
-      run = run + v;
-      if (run > target_u) {
-        pick = j;
-        break;
-      }
-    }
-    if (pick < 0) {
-      const int first = cs * CHUNK + bs * SUB;
-      pick = last >= 0 ? last : (first < V - 1 ? first : V - 1);
-    }
-    out[4 + emit++] = pick;
+    float L[64], P[64];
+    lane_sums(r, nch, kc, L);
+    scan64(L, P);
+    const float S = P[63];
+    if (!(S > 0.0f)) flags |= 4;
+    const float tu = uniforms[uidx] * S;
+    float cbase = 0.0f, ebase = 0.0f;
+    const int cs = descend(r, nch, kc, tu, &cbase);
+    const int n_in = V - cs * CHUNK < CHUNK ? V - cs * CHUNK : CHUNK;
+    const int e = descend(v + (size_t)cs * CHUNK, n_in, SUB, tu - cbase, &ebase);
+    out[4 + emit++] = cs * CHUNK + e;
+    free(v);
   }
   for (int i = emit; i <= D; ++i) out[4 + i] = -1;
   out[0] = good;
   out[1] = emit;
   out[2] = stop ? uidx : uidx + 1;
   out[3] = flags;
+  free(rt);
+  free(rd);
 }
 
-/* Hierarchical total of exp(x/T - m) for one row (exposed for the sum-order tests). */
-float or_row_z(const float* x, int V, float temp) { return row_z(x, V, temp, row_max_div(x, V, temp)); }
+/* Row total Z of the p/q rows at temperature temp (exposed for the sum-order tests). */
+float or_row_z(const float* x, int V, float temp) {
+  PqRow* r = (PqRow*)malloc(sizeof(PqRow));
+  pq_row(x, V, pq_inv(temp), r);
+  const float z = r->Z;
+  free(r);
+  return z;
+}
 
 /* ---------------------------------------------------------------- shared expert (bf16 chain)
  * reference_torch.py:132-133 / model/layers.py:398-402 in bf16: g, u = bf16 projections (or_dense_rows);

@@ -6,13 +6,8 @@
 //
 // p/q (Leviathan et al. 2023, Alg. 1; not in the reference): p_i = softmax(target_i / T), q_i = softmax(draft_i / T);
 // draft x_i is accepted iff u_i * q_i(x_i) < p_i(x_i). The first rejection samples from norm(max(0, p_i - q_i))
-// with the next uniform; when every draft is accepted a bonus token is sampled from p_D.
-//
-// Every reduction has a fixed order, which the CPU restatement replays bit for bit:
-//   chunk = 1024 entries = 64 sub-chunks of 16; a sub-chunk total is the sequential fp32 sum of its entries
-//   (from 0); a chunk total is the xor-butterfly sum of its 64 sub-chunk totals; a row total is the sequential
-//   sum of the chunk totals. Inverse-CDF search: the first chunk whose running total exceeds u*S, then inside
-//   it the first sub-chunk (running total started at the chunk's base), then the first entry.
+// with the next uniform; when every draft is accepted a bonus token is sampled from p_D. Its sums are in a
+// lane-parallel fixed order, described with the p/q kernels below, which the CPU restatement replays bit for bit.
 #include "ss_common.hpp"
 #include "ss_launch.hpp"
 
@@ -36,30 +31,41 @@ SS_DEV int nchunks_of(int V) { return (V + kChunk - 1) / kChunk; }
 int64_t accept_work_floats(int D, int V) {
   const int nch = (V + kChunk - 1) / kChunk;
   const int rows = 2 * D + 1;
-  return kHeadFloats + (int64_t)rows * nch * 3 + (int64_t)nch * 65 + 64;
+  return kHeadFloats + (int64_t)rows * nch * 7 + (int64_t)nch * 3 + 64;
 }
 
 // Workspace layout (floats). The header holds the arrival counters of the launches whose last workgroup finishes
 // the round; it must be zero before the first call, and every launch sequence leaves it zero.
+// The one-launch p/q round hands its chunk results over as 64-bit words tagged with the launch: the high half is
+// the tag (bits 32-62; bit 63 of wd0 is the chunk's non-finite flag), the low half the float. The tag is the
+// workspace's launch epoch + 1 (mod 2^31); the epoch (header int kEpochInt, never reset) is advanced once every
+// workgroup has published, so words left by an earlier launch never match.
+constexpr int kEpochInt = 3200;
+static_assert(kArrCounters * (kArrShards + 1) * kArrStride <= kEpochInt && kEpochInt < kHeadFloats, "epoch word");
 struct Work {
-  int* ctr;         // arrival counters (header)
+  int* ctr;         // arrival counters and the epoch (header)
+  uint64_t* wd0;    // [rows][nch] tagged chunk maxima (one-launch round)
+  uint64_t* wd1;    // [rows][nch] tagged chunk totals (one-launch round)
+  uint64_t* wr;     // [nch]       tagged chunk totals of the sampled values (one-launch round)
   float* cmax;      // [rows][nch] chunk maxima (greedy: the maximum's value)
   float* cbad;      // [rows][nch] chunk holds a non-finite value
   float* ctot;      // [rows][nch] chunk totals (greedy: the maximum's index)
-  float* stot;      // [nch][64]  sub-chunk totals of the sampled row
-  float* rtot;      // [nch]      chunk totals of the sampled row
+  float* rtot;      // [nch]       chunk totals of the sampled values
   float* state;     // [64]
 };
 
 SS_DEV Work work_of(float* w, int rows, int nch) {
   Work k;
   k.ctr = reinterpret_cast<int*>(w);
-  float* b = w + kHeadFloats;
-  k.cmax = b;
-  k.cbad = b + (size_t)rows * nch;
-  k.ctot = b + (size_t)rows * nch * 2;
-  k.stot = b + (size_t)rows * nch * 3;
-  k.rtot = k.stot + (size_t)nch * 64;
+  float* b = w + kHeadFloats;  // 16 KB into the 256-byte aligned workspace: 8-byte aligned
+  k.wd0 = reinterpret_cast<uint64_t*>(b);
+  k.wd1 = k.wd0 + (size_t)rows * nch;
+  k.wr = k.wd1 + (size_t)rows * nch;
+  float* f = reinterpret_cast<float*>(k.wr + nch);
+  k.cmax = f;
+  k.cbad = f + (size_t)rows * nch;
+  k.ctot = f + (size_t)rows * nch * 2;
+  k.rtot = f + (size_t)rows * nch * 3;
   k.state = k.rtot + nch;
   return k;
 }
@@ -103,65 +109,8 @@ SS_DEV bool finite(float v) { return (__float_as_uint(v) & 0x7F800000u) != 0x7F8
 // Chunk-array entries per lane when one wave loads an array of per-chunk values (lane c % 64, register c / 64).
 constexpr int kMaxPerLane = 16;  // V <= 16 * 64 * 1024 entries
 
-// Sequential sums and scans over LDS arrays that are 16-byte aligned and padded with zeros to a multiple of 16
-// entries: every 16 entries are read as four unconditional 16-byte loads before their (dependent, in-order) adds,
-// and the bound n is applied by selects in the last, partial group.
-SS_DEV float lds_seq_sum(const float* v, int n, float s) {
-  // whole groups of 16 add without a bound check; only the last, partial group selects
-  const float4* v4 = reinterpret_cast<const float4*>(v);
-  for (int b = 0; b < n; b += 16) {
-    const float4 a0 = v4[b / 4], a1 = v4[b / 4 + 1], a2 = v4[b / 4 + 2], a3 = v4[b / 4 + 3];
-    const float t[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
-    if (b + 16 <= n) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s = s + t[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float nx = s + t[i];
-        s = b + i < n ? nx : s;
-      }
-    }
-  }
-  return s;
-}
-// Running sum from `start` over v[0..n): the first index whose running sum exceeds `target` (and the running sum
-// before it; `start` when there is none), and the last nonzero index. The zero padding adds +0 to the running sum
-// and, coming after a miss with the same sum, cannot be the first hit, so no bound check runs per entry: the first
-// hit is the count of leading misses.
-struct Scan {
-  int first, last;
-  float base;
-};
-SS_DEV Scan lds_scan(const float* v, int n, float start, float target) {
-  float run = start, base = start;
-  int lead = 0, last = -1;
-  bool alive = true;
-  const float4* v4 = reinterpret_cast<const float4*>(v);
-  for (int b = 0; b < n; b += 16) {
-    const float4 a0 = v4[b / 4], a1 = v4[b / 4 + 1], a2 = v4[b / 4 + 2], a3 = v4[b / 4 + 3];
-    const float t[16] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w,
-                         a2.x, a2.y, a2.z, a2.w, a3.x, a3.y, a3.z, a3.w};
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {  // selects only: every lane holds the same values
-      const float nx = run + t[i];
-      alive = alive && !(nx > target);
-      base = alive ? nx : base;
-      lead += alive ? 1 : 0;
-      last = t[i] > 0.f ? b + i : last;
-      run = nx;
-    }
-  }
-  Scan r;
-  r.first = lead < n ? lead : -1;
-  r.base = r.first >= 0 ? base : start;
-  r.last = last;
-  return r;
-}
-
-// Stages the same rows of three arrays (as stage_rows_ag) with every load of a batch (Q per lane and array) in
-// flight before any store.
+// Stages rows [nr][nch] of three arrays written by other workgroups (agent-scope loads, every load of a batch, Q per
+// lane and array, in flight before any store) into LDS at a row stride of nchp (nch rounded up to 16).
 template <int Q>
 SS_DEV void stage_rows3_ag(const float* s0, const float* s1, const float* s2, int nr, int nch, int nchp, float* d0,
                            float* d1, float* d2) {
@@ -186,30 +135,6 @@ SS_DEV void stage_rows3_ag(const float* s0, const float* s1, const float* s2, in
         d0[o] = v0[q];
         d1[o] = v1[q];
         d2[o] = v2[q];
-      }
-    }
-  }
-}
-
-// Stages rows [nr][nch] written by other workgroups (agent-scope loads, 32 per lane in flight) into LDS at a row
-// stride of nchp = nch rounded up to 16, the padding zeroed.
-SS_DEV void stage_rows_ag(const float* src, int nr, int nch, int nchp, float* lds) {
-  const int lane = threadIdx.x & 63;
-  const int n = nr * nch;
-  for (int i = lane; i < nr * nchp; i += 64) lds[i] = 0.f;
-  for (int b = 0; b < n; b += 64 * 32) {
-    float v[32];
-#pragma unroll
-    for (int q = 0; q < 32; ++q) {
-      const int i = b + lane + 64 * q;
-      v[q] = i < n ? __hip_atomic_load(const_cast<float*>(src) + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : 0.f;
-    }
-#pragma unroll
-    for (int q = 0; q < 32; ++q) {
-      const int i = b + lane + 64 * q;
-      if (i < n) {
-        const int r = i / nch;
-        lds[r * nchp + (i - r * nch)] = v[q];
       }
     }
   }
@@ -319,99 +244,504 @@ hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st) {
 }
 
 // ---------------------------------------------------------------- p/q
-// Three launches: (1) chunk maxima of l / T and non-finite flags; (2) e = exp(l / T - m) chunk totals, then the
-// last workgroup forms each row's total (sequential over its chunk totals), maximum and flag and decides the
-// drafts; (3) the chunk and sub-chunk totals of the sampled distribution, then the last workgroup searches them and
-// writes the round. Logical rows: target i -> i (0..D), draft i -> D + 1 + i.
-SS_DEV const float* row_ptr(const AcceptArgs& a, int row) {
-  return row <= a.D ? a.target + (size_t)row * a.V : a.draft + (size_t)(row - a.D - 1) * a.V;
+// Leviathan et al. 2023, Alg. 1 (no reference counterpart), with every sum in a lane-parallel fixed order that the
+// CPU restatement (or_accept_pq) replays bit for bit:
+//   wave_scan: the inclusive prefix of one value per lane by Hillis-Steele steps d = 1, 2, .., 32.
+//   lane layout of n values, k per lane: lane l holds values k l .. k l + k - 1; its local sum is sequential from 0;
+//   the layout's total is the last lane's prefix.
+// Per row and 1024-entry chunk c (lane l: entries 16 l .. 16 l + 15): y = x * (1 / T), m_c = max y, e = exp(y - m_c),
+// s_c = the layout total of e (k = 16). Per row: M = max m_c, g_c = exp(m_c - M), Z = the layout total of s_c g_c
+// (k = ceil(nch / 64)), a_c = g_c / Z, p_j = e_j a_c. Draft x_i is accepted iff u_i q_i(x_i) < p_i(x_i); the first
+// rejection samples from max(0, p_i - q_i), every draft accepted from p_D: wave_descend over the chunk totals of the
+// sampled values, then over the chosen chunk's entries. A non-finite row the round reaches stops it.
+// Logical rows: target i -> i (0..D), draft i -> D + 1 + i.
+//
+// Two forms, the same bits: pq_round_kernel, one persistent launch, when every unit (target row i with draft row i,
+// or the bonus target row D, over one chunk) has a wave of a resident grid: the unit's e values stay in registers;
+// the chunk parts are published as tagged words, which every workgroup polls directly (no counter) before it forms
+// the row statistics and the decision itself; the waves of the sampled row form its values and publish their chunk
+// totals the same way; every such wave finds the chunk of the sample and the wave holding it finds the entry.
+// Otherwise two launches: pq_sum_kernel (chunk parts; the last workgroup decides) and pq_residual_kernel (chunk
+// totals of the sampled values; the last workgroup searches).
+
+SS_DEV float wave_scan(float v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const float o = __shfl_up(v, d, 64);
+    if (lane >= d) v = v + o;
+  }
+  return v;
 }
 
-__global__ __launch_bounds__(64) void pq_max_kernel(AcceptArgs a) {
-  const int row = blockIdx.y, c = blockIdx.x, lane = threadIdx.x;
-  const int nch = gridDim.x, rows = gridDim.y;
-  Work k = work_of(a.work, rows, nch);
-  if (a.tkey && row <= a.D) {
-    // formed by the lm_head GEMV: the same maximum (order-free), key 0 = a chunk of NaNs only (fmaxf's -inf)
-    if (lane == 0) {
-      const uint32_t key = a.tkey[row * nch + c];
-      k.cmax[row * nch + c] = key ? ss_unkey(key) : -__builtin_inff();
-      k.cbad[row * nch + c] = a.tbad[row * nch + c] ? 1.f : 0.f;
+// The layout total of v (k per lane, n values): every lane returns it.
+template <int KMAX>
+SS_DEV float wave_total(const float (&v)[KMAX], int k, int n) {
+  const int lane = threadIdx.x & 63;
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i)
+    if (i < k && k * lane + i < n) L = L + v[i];
+  return ss_readlane_f(wave_scan(L), 63);
+}
+
+// The search over a lane layout for target t (whole wave, uniform result): the first lane whose prefix exceeds t
+// (else the last lane with a nonzero local sum, else lane 0), then inside it the first value whose running sum from
+// the lane's exclusive prefix exceeds t (else its last nonzero value, else its first); *base receives the running
+// sum before the chosen value. Returns the value's index, at most n - 1.
+template <int KMAX>
+SS_DEV int wave_descend(const float (&v)[KMAX], int k, int n, float t, float* base) {
+  const int lane = threadIdx.x & 63;
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i)
+    if (i < k && k * lane + i < n) L = L + v[i];
+  const float P = wave_scan(L);
+  const uint64_t gt = __ballot(P > t);
+  int ls;
+  if (gt) {
+    ls = __builtin_ctzll(gt);
+  } else {
+    const uint64_t nz = __ballot(L > 0.f);
+    ls = nz ? 63 - __builtin_clzll(nz) : 0;
+  }
+  const float e = ls > 0 ? ss_readlane_f(P, ls - 1) : 0.f;
+  float run = e;
+  int pick = -1, last = -1;
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    const bool in = i < k && k * lane + i < n;
+    const float x = in ? v[i] : 0.f;
+    if (in && x > 0.f) last = i;
+    if (in && pick < 0) {
+      const float nx = run + x;
+      if (nx > t)
+        pick = i;
+      else
+        run = nx;
     }
-    return;
   }
-  const float* x = row_ptr(a, row);
-  float v[kSub];
+  if (pick < 0) {
+    pick = last >= 0 ? last : 0;
+    run = e;
 #pragma unroll
-  for (int i = 0; i < kSub; ++i) {
-    const int j = c * kChunk + i * 64 + lane;
-    v[i] = j < a.V ? x[j] : 0.f;
+    for (int i = 0; i < KMAX; ++i)
+      if (i < pick) run = run + v[i];
   }
+  const int pb = __builtin_amdgcn_readlane(pick, ls);
+  *base = ss_readlane_f(run, ls);
+  const int idx = k * ls + pb;
+  return idx < n ? idx : n - 1;
+}
+
+// One chunk of one row in a wave: lane l holds entries j0 .. j0 + 15 of v (j0 = 1024 c + 16 l; entries >= V
+// excluded), which become e; returns m_c, s_c and the non-finite flag.
+struct ChunkPart {
+  float m, s;
+  int bad;
+};
+SS_DEV ChunkPart chunk_part(float (&v)[kSub], int j0, int V, float invT) {
   float m = -__builtin_inff();
-  int bad = 0;
+  uint32_t bad = 0;
 #pragma unroll
-  for (int i = 0; i < kSub; ++i) {
-    const int j = c * kChunk + i * 64 + lane;
-    if (j < a.V) {
-      bad |= !finite(v[i]);
-      m = fmaxf(m, v[i] / a.temperature);
+  for (int e = 0; e < kSub; ++e)
+    if (j0 + e < V) {
+      bad |= !finite(v[e]);
+      v[e] = v[e] * invT;
+      m = fmaxf(m, v[e]);
+    }
+  ChunkPart r;
+  r.m = ss_wave_max(m);
+  r.bad = (int)ss_wave_or(bad);
+  float sub = 0.f;
+#pragma unroll
+  for (int e = 0; e < kSub; ++e) {
+    v[e] = j0 + e < V ? ss_expf(v[e] - r.m) : 0.f;
+    sub = sub + v[e];
+  }
+  r.s = ss_readlane_f(wave_scan(sub), 63);
+  return r;
+}
+
+// Row statistics from the row's staged chunk parts (LDS: m at sm, s at sv, flags at sb), one wave: M, Z and the
+// flag; sv receives a_c in place of s_c.
+SS_DEV void row_stats(float* sv, const float* sm, const float* sb, int nch, float* M, float* Z, int* bad) {
+  const int lane = threadIdx.x & 63, kc = (nch + 63) >> 6;
+  float mv[kMaxPerLane], g[kMaxPerLane];
+  float m = -__builtin_inff(), b = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    if (i >= kc) break;
+    const int c = kc * lane + i;
+    const bool in = c < nch;
+    mv[i] = in ? sm[c] : -__builtin_inff();
+    if (in) {
+      m = fmaxf(m, mv[i]);
+      b = fmaxf(b, sb[c]);  // flags are 0 or 1
     }
   }
   m = ss_wave_max(m);
-  bad = (int)ss_wave_or((uint32_t)bad);
-  if (lane == 0) {
-    k.cmax[row * nch + c] = m;
-    k.cbad[row * nch + c] = bad ? 1.f : 0.f;
+  b = ss_wave_max(b);
+  float L = 0.f;
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    if (i >= kc) break;  // kc is the same in every lane
+    const int c = kc * lane + i;
+    g[i] = ss_expf(mv[i] - m);
+    if (c < nch) L = L + sv[c] * g[i];
+  }
+  const float z = ss_readlane_f(wave_scan(L), 63);
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    if (i >= kc) break;
+    const int c = kc * lane + i;
+    if (c < nch) sv[c] = g[i] / z;
+  }
+  *M = m;
+  *Z = z;
+  *bad = b != 0.f;
+}
+
+// The round's decision (one thread): s_* hold, per draft i, the draft, the target and draft logits at it, the
+// uniform, and m_c and a_c of target row i and draft row i at the draft's chunk.
+struct PqIn {
+  int x[64];
+  float lt[64], lq[64], u[64], mt[64], at[64], md[64], ad[64];
+};
+struct PqState {
+  int srow, sdraft, uidx, stop, good, flags;
+  float ms, zs, md, zd;
+};
+SS_DEV PqState pq_decide(const AcceptArgs& a, float invT, const float* mrow, const float* zrow, const int* brow,
+                         const PqIn& in, bool raise) {
+  const int D = a.D;
+  int good = 0, flags = 0, stop = 0;
+  int srow = D, sdraft = -1;
+  for (int i = 0; i < D; ++i) {
+    const int dr = D + 1 + i;
+    if (brow[i] || brow[dr]) {
+      flags |= FLAG_NONFINITE;
+      stop = 1;
+      break;
+    }
+    const int x = in.x[i];
+    if (x < 0 || x >= a.V) {
+      flags |= FLAG_BAD_DRAFT;
+      if (raise) ss_raise(a.err, SS_ERR_TOKEN);
+      srow = i;
+      sdraft = dr;
+      break;
+    }
+    const float p = ss_expf(in.lt[i] * invT - in.mt[i]) * in.at[i];
+    const float q = ss_expf(in.lq[i] * invT - in.md[i]) * in.ad[i];
+    if (in.u[i] * q < p) {
+      ++good;
+      continue;
+    }
+    srow = i;
+    sdraft = dr;
+    break;
+  }
+  if (!stop && sdraft < 0 && brow[D]) {
+    flags |= FLAG_NONFINITE;
+    stop = 1;
+  }
+  PqState st;
+  st.srow = srow;
+  st.sdraft = sdraft;
+  st.uidx = good + (sdraft >= 0 ? 1 : 0);
+  st.stop = stop;
+  st.good = good;
+  st.flags = flags;
+  st.ms = mrow[srow];
+  st.zs = zrow[srow];
+  st.md = sdraft >= 0 ? mrow[sdraft] : 0.f;
+  st.zd = sdraft >= 0 ? zrow[sdraft] : 1.f;
+  return st;
+}
+
+// Writes the round: the accepted drafts, then the sampled token unless the round stopped.
+SS_DEV void pq_write_out(const AcceptArgs& a, const PqState& st, const int* drafts, int pick, int flags) {
+  int emit = st.good;
+  for (int i = 0; i < st.good; ++i) a.out[OUT_TOK + i] = drafts[i];
+  if (!st.stop) a.out[OUT_TOK + emit++] = pick;
+  for (int i = emit; i <= a.D; ++i) a.out[OUT_TOK + i] = -1;
+  a.out[OUT_NACC] = st.good;
+  a.out[OUT_NEMIT] = emit;
+  a.out[OUT_NUNI] = st.stop ? st.uidx : st.uidx + 1;
+  a.out[OUT_FLAGS] = flags;
+}
+
+// Lane l's 16 entries j0 .. j0 + 15 of row x (zeros past V), as four 16-byte loads when the row allows them.
+SS_DEV void load16(const float* x, int j0, int V, bool vec, float (&v)[kSub]) {
+  if (vec && j0 + kSub <= V) {
+    const float4* p = reinterpret_cast<const float4*>(x + j0);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float4 t = p[q];
+      v[4 * q] = t.x;
+      v[4 * q + 1] = t.y;
+      v[4 * q + 2] = t.z;
+      v[4 * q + 3] = t.w;
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < kSub; ++e) v[e] = j0 + e < V ? x[j0 + e] : 0.f;
   }
 }
 
+// The sampled distribution's value from e of the target and draft rows and their a_c.
+SS_DEV float sampled_value(float et, float ed, float at, float ad, bool rejected) {
+  const float p = et * at;
+  if (!rejected) return p;
+  const float d = p - ed * ad;
+  return d > 0.f ? d : 0.f;
+}
+
+// A tagged word's tag and value.
+SS_DEV uint32_t tag_of(uint64_t w) { return (uint32_t)(w >> 32) & 0x7FFFFFFFu; }
+SS_DEV float val_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
+SS_DEV uint64_t tagged(uint32_t tag, float v) { return ((uint64_t)tag << 32) | __float_as_uint(v); }
+constexpr int kSpin = 1 << 22;  // bound of every wait for tagged words (then SS_ERR_TIMEOUT and on)
+
+constexpr int kFastUnits = 1024;                            // units of the one-launch round (one wave each)
+constexpr int kFastStage = 2 * kFastUnits + 15 * kMaxRows;  // rows x nchp chunk parts staged per workgroup
+
+__global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) {
+  __shared__ __attribute__((aligned(16))) float sv[kFastStage], sm[kFastStage], sb[kFastStage];
+  __shared__ float mrow[kMaxRows], zrow[kMaxRows];
+  __shared__ int brow[kMaxRows];
+  __shared__ PqIn s_in;
+  __shared__ PqState s_st;
+  __shared__ uint64_t s_tr[16];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int D = a.D, V = a.V, nch = nchunks_of(V), rows = 2 * D + 1, nchp = (nch + 15) & ~15;
+  const int kc = (nch + 63) >> 6;
+  const float invT = 1.0f / a.temperature;
+  // phase stamps, kept in LDS and written at the exit: slot k by thread 0, slots 8 + k by lane 0 of a sampled-row wave
+#define PQ_TRACE(k, who)                                               \
+  do {                                                                 \
+    if (a.trace && (who)) s_tr[k] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+  if (tid < 16) s_tr[tid] = 0;
+  PQ_TRACE(0, tid == 0);
+  Work k = work_of(a.work, rows, nch);
+  const int gw = blockIdx.x * 4 + w;
+  const bool has = gw < units;
+  const int ui = has ? gw / nch : 0, c = has ? gw - ui * nch : 0;
+  const int j0 = c * kChunk + kSub * lane;
+  const bool vec = (V & 3) == 0 && (reinterpret_cast<uintptr_t>(a.target) & 15) == 0 &&
+                   (D == 0 || (reinterpret_cast<uintptr_t>(a.draft) & 15) == 0);
+  // the unit's logits (target row ui; draft row ui when ui < D), and the drafts, their logits and the uniforms
+  float vt[kSub], vd[kSub];
+  if (has) load16(a.target + (size_t)ui * V, j0, V, vec, vt);
+  if (has && ui < D) load16(a.draft + (size_t)ui * V, j0, V, vec, vd);
+  if (w == 0) {
+    const int xi = lane < D ? a.drafts[lane] : 0;
+    const bool xok = lane < D && xi >= 0 && xi < V;
+    s_in.x[lane] = xi;
+    s_in.lt[lane] = xok ? a.target[(size_t)lane * V + xi] : 0.f;
+    s_in.lq[lane] = xok ? a.draft[(size_t)lane * V + xi] : 0.f;
+    s_in.u[lane] = lane <= D ? a.uniforms[lane] : 0.f;
+  }
+  // The epoch, read once per workgroup (with the loads above in flight) and shared, so that every thread's tag was
+  // read before any wave of the workgroup publishes.
+  __shared__ uint32_t s_epoch;
+  if (tid == 0) s_epoch = (uint32_t)ld_ag(k.ctr + kEpochInt);
+  __syncthreads();
+  const uint32_t epoch = s_epoch;
+  const uint32_t tag = (epoch + 1u) & 0x7FFFFFFFu;
+  // phase 1: the unit's chunk parts (vt, vd become e), published as tagged words
+  if (has) {
+    const ChunkPart pt = chunk_part(vt, j0, V, invT);
+    if (lane == 0) {
+      const size_t o = (size_t)ui * nch + c;
+      st_ag(k.wd0 + o, tagged(tag | (pt.bad ? 0x80000000u : 0u), pt.m));
+      st_ag(k.wd1 + o, tagged(tag, pt.s));
+    }
+    if (ui < D) {
+      const ChunkPart pd = chunk_part(vd, j0, V, invT);
+      if (lane == 0) {
+        const size_t o = (size_t)(D + 1 + ui) * nch + c;
+        st_ag(k.wd0 + o, tagged(tag | (pd.bad ? 0x80000000u : 0u), pd.m));
+        st_ag(k.wd1 + o, tagged(tag, pd.s));
+      }
+    }
+  }
+  PQ_TRACE(1, tid == 0);
+  // phase 2: every workgroup polls every row's chunk words until all carry this launch's tag (rows x nch <= 2048:
+  // eight pairs per thread), stages them, forms the row statistics and decides
+  {
+    const int n = rows * nch;
+    uint64_t w0[8], w1[8];
+    for (int it = 0;; ++it) {
+      int ok = 1;
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int i = tid + 256 * q;
+        w0[q] = i < n ? ld_ag(k.wd0 + i) : 0;
+        w1[q] = i < n ? ld_ag(k.wd1 + i) : 0;
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q)
+        if (tid + 256 * q < n) ok &= tag_of(w0[q]) == tag && tag_of(w1[q]) == tag;
+      if (__syncthreads_and(ok)) break;
+      if (it >= kSpin) {
+        if (tid == 0) ss_raise(a.err, SS_ERR_TIMEOUT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    // every workgroup has published, so every one has read the epoch: the next launch's tag may follow
+    if (blockIdx.x == 0 && tid == 0) st_ag(k.ctr + kEpochInt, (int)(epoch + 1u));
+    PQ_TRACE(2, tid == 0);
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int i = tid + 256 * q;
+      if (i < n) {
+        const int r = i / nch, o = r * nchp + (i - r * nch);
+        sv[o] = val_of(w1[q]);
+        sm[o] = val_of(w0[q]);
+        sb[o] = (w0[q] >> 63) ? 1.f : 0.f;
+      }
+    }
+    __syncthreads();
+    PQ_TRACE(3, tid == 0);
+    for (int r = w; r < rows; r += 4) {
+      float M, Z;
+      int bad;
+      row_stats(sv + r * nchp, sm + r * nchp, sb + r * nchp, nch, &M, &Z, &bad);
+      if (lane == 0) {
+        mrow[r] = M;
+        zrow[r] = Z;
+        brow[r] = bad;
+      }
+    }
+    __syncthreads();
+    PQ_TRACE(4, tid == 0);
+    if (tid < D) {
+      const int xi = s_in.x[tid];
+      const int cx = xi >= 0 && xi < V ? xi >> 10 : 0;
+      s_in.mt[tid] = sm[tid * nchp + cx];
+      s_in.at[tid] = sv[tid * nchp + cx];
+      s_in.md[tid] = sm[(D + 1 + tid) * nchp + cx];
+      s_in.ad[tid] = sv[(D + 1 + tid) * nchp + cx];
+    }
+    __syncthreads();
+    if (tid == 0) s_st = pq_decide(a, invT, mrow, zrow, brow, s_in, blockIdx.x == 0);
+    __syncthreads();
+    PQ_TRACE(5, tid == 0);
+  }
+  const PqState st = s_st;
+  if (st.stop) {
+    if (blockIdx.x == 0 && tid == 0) pq_write_out(a, st, s_in.x, -1, st.flags);
+  } else if (has && ui == (st.srow < D ? st.srow : D)) {
+    // phase 3: the sampled row's values (in place of vt) and this chunk's total
+    const bool rej = st.sdraft >= 0;
+    const float at = sv[st.srow * nchp + c], ad = rej ? sv[st.sdraft * nchp + c] : 0.f;
+#pragma unroll
+    for (int e = 0; e < kSub; ++e) vt[e] = j0 + e < V ? sampled_value(vt[e], vd[e], at, ad, rej) : 0.f;
+    const float ct = wave_total(vt, kSub, kChunk);
+    if (lane == 0) st_ag(k.wr + c, tagged(tag, ct));
+    PQ_TRACE(8, lane == 0);
+    // phase 4: every wave of the row polls the chunk totals, finds the chunk of the sample; the wave holding it
+    // finds the entry
+    float rv[kMaxPerLane];
+    for (int it = 0;; ++it) {
+      int ok = 1;
+#pragma unroll
+      for (int i = 0; i < kMaxPerLane; ++i) {
+        const int cc = kc * lane + i;
+        const bool in = i < kc && cc < nch;
+        const uint64_t wv = in ? ld_ag(k.wr + cc) : 0;
+        ok &= !in || tag_of(wv) == tag;
+        rv[i] = in ? val_of(wv) : 0.f;
+      }
+      if (__all(ok)) break;
+      if (it >= kSpin) {
+        if (lane == 0) ss_raise(a.err, SS_ERR_TIMEOUT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    PQ_TRACE(9, lane == 0);
+    int flags = st.flags;
+    const float S = wave_total(rv, kc, nch);
+    if (!(S > 0.f)) flags |= FLAG_RESIDUAL_EMPTY;
+    const float t = s_in.u[st.uidx] * S;
+    float cbase;
+    const int cs = wave_descend(rv, kc, nch, t, &cbase);
+    PQ_TRACE(10, lane == 0);
+    if (c == cs) {
+      const int n_in = V - cs * kChunk < kChunk ? V - cs * kChunk : kChunk;
+      float ebase;
+      const int e = wave_descend(vt, kSub, n_in, t - cbase, &ebase);
+      if (lane == 0) pq_write_out(a, st, s_in.x, cs * kChunk + e, flags);
+      PQ_TRACE(11, lane == 0);
+    }
+  }
+  __syncthreads();
+  PQ_TRACE(6, tid == 0);
+  if (a.trace && tid < 16) a.trace[(size_t)blockIdx.x * 16 + tid] = s_tr[tid];
+#undef PQ_TRACE
+}
+
+// Two-launch form, first launch: each (chunk, row) workgroup forms its chunk part (four waves, a quarter of the
+// chunk each, staged in the sub-chunk layout of stride 17); the last workgroup forms every row's statistics and
+// decides the drafts; the round's state goes to the workspace.
 __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
   __shared__ float lds[64 * (kSub + 1)];
   __shared__ __attribute__((aligned(16))) float sv[kStage], sm[kStage], sb[kStage];
   __shared__ float zrow[kMaxRows], mrow[kMaxRows];
   __shared__ int brow[kMaxRows];
-  __shared__ float s_m;
+  __shared__ float s_m[4];
+  __shared__ int s_b[4];
+  __shared__ PqIn s_in;
   const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nch = gridDim.x, rows = gridDim.y;
+  const float invT = 1.0f / a.temperature;
   Work k = work_of(a.work, rows, nch);
   {
-    // wave 0: the row maximum over the chunk maxima (order-free); all waves: a quarter of the chunk each
-    const float* x = row_ptr(a, row);
+    const float* x = row < a.D + 1 ? a.target + (size_t)row * a.V : a.draft + (size_t)(row - a.D - 1) * a.V;
     constexpr int NQ = kSub / 4;
-    float xv[NQ];
+    float yv[NQ];
+    float m = -__builtin_inff();
+    uint32_t bad = 0;
 #pragma unroll
     for (int ii = 0; ii < NQ; ++ii) {
       const int j = c * kChunk + (w * NQ + ii) * 64 + lane;
-      xv[ii] = j < a.V ? x[j] : 0.f;
-    }
-    if (w == 0) {
-      float cm[kMaxPerLane];
-#pragma unroll
-      for (int q = 0; q < kMaxPerLane; ++q) {
-        const int cc = lane + 64 * q;
-        cm[q] = cc < nch ? k.cmax[row * nch + cc] : -__builtin_inff();
+      const float v = j < a.V ? x[j] : 0.f;
+      yv[ii] = v * invT;
+      if (j < a.V) {
+        bad |= !finite(v);
+        m = fmaxf(m, yv[ii]);
       }
-      float m = -__builtin_inff();
-#pragma unroll
-      for (int q = 0; q < kMaxPerLane; ++q) m = fmaxf(m, cm[q]);
-      m = ss_wave_max(m);
-      if (lane == 0) s_m = m;
+    }
+    m = ss_wave_max(m);
+    bad = ss_wave_or(bad);
+    if (lane == 0) {
+      s_m[w] = m;
+      s_b[w] = (int)bad;
     }
     __syncthreads();
-    const float m = s_m;
-    // e = exp(l/T - m) staged with a 17-float stride per sub-chunk of 16
+    const float mc = fmaxf(fmaxf(s_m[0], s_m[1]), fmaxf(s_m[2], s_m[3]));
 #pragma unroll
     for (int ii = 0; ii < NQ; ++ii) {
       const int e = (w * NQ + ii) * 64 + lane;
       const int j = c * kChunk + e;
-      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? ss_expf(xv[ii] / a.temperature - m) : 0.f;
+      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? ss_expf(yv[ii] - mc) : 0.f;
     }
     __syncthreads();
     if (w != 0) return;
     float s = 0.f;
     for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
-    s = ss_wave_sum(s);
-    if (lane == 0) st_ag(k.ctot + (size_t)row * nch + c, s);
+    s = ss_readlane_f(wave_scan(s), 63);
+    if (lane == 0) {
+      const size_t o = (size_t)row * nch + c;
+      st_ag(k.cmax + o, mc);
+      st_ag(k.ctot + o, s);
+      st_ag(k.cbad + o, (s_b[0] | s_b[1] | s_b[2] | s_b[3]) ? 1.f : 0.f);
+    }
   }
   // The drafts (lane i holds draft i; D <= 60) arrive with this workgroup's own loads, so the finishing workgroup
   // requests the draft positions' logits and the uniforms together with its staging.
@@ -419,98 +749,61 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
   if (!arrive_last(k.ctr, 1, row * nch + c, nch * rows)) return;
   arrival_clear(k.ctr, 1);
   const bool xok = lane < a.D && xi >= 0 && xi < a.V;
+  const int cx = xok ? xi >> 10 : 0;
   const float lt = xok ? a.target[(size_t)lane * a.V + xi] : 0.f;
   const float lq = xok ? a.draft[(size_t)lane * a.V + xi] : 0.f;
-  const float uu = lane < a.D ? a.uniforms[lane] : 0.f;
-  // Per row: the total (sequential over its chunk totals, from 0), the maximum and the non-finite flag.
+  const float mt = lane < a.D ? ld_ag(k.cmax + (size_t)lane * nch + cx) : 0.f;
+  const float md = lane < a.D ? ld_ag(k.cmax + (size_t)(a.D + 1 + lane) * nch + cx) : 0.f;
+  const float uu = lane <= a.D ? a.uniforms[lane] : 0.f;
+  // Per row: M, Z and the flag.
   const int nchp = (nch + 15) & ~15;
   const int per = kStage / nchp;
   for (int r0 = 0; r0 < rows; r0 += per) {
     const int nr = rows - r0 < per ? rows - r0 : per;
     const size_t o = (size_t)r0 * nch;
-    // 17 per lane: one batch for the seven rows of a depth-3 round at V = 151,936 (1,043 chunks), and 88 VGPRs,
-    // which keep five workgroups per CU (as the LDS does)
+    // 17 per lane: one batch for the seven rows of a depth-3 round at V = 151,936 (1,043 chunks)
     stage_rows3_ag<17>(k.ctot + o, k.cmax + o, k.cbad + o, nr, nch, nchp, sv, sm, sb);
     __syncthreads();
-    // the maximum and flag of each row across the wave (order-free: a +-0 difference in m changes no exp(x - m));
-    // the totals, which keep their order, lane r taking row r
     for (int rr = 0; rr < nr; ++rr) {
-      float m = -__builtin_inff(), b = 0.f;
-      for (int cc = lane; cc < nch; cc += 64) {
-        m = fmaxf(m, sm[rr * nchp + cc]);
-        b = fmaxf(b, sb[rr * nchp + cc]);  // flags are 0 or 1
-      }
-      m = ss_wave_max(m);
-      b = ss_wave_max(b);
+      float M, Z;
+      int bad;
+      row_stats(sv + rr * nchp, sm + rr * nchp, sb + rr * nchp, nch, &M, &Z, &bad);
       if (lane == 0) {
-        mrow[r0 + rr] = m;
-        brow[r0 + rr] = b != 0.f;
+        mrow[r0 + rr] = M;
+        zrow[r0 + rr] = Z;
+        brow[r0 + rr] = bad;
       }
     }
-    for (int rr = lane; rr < nr; rr += 64) zrow[r0 + rr] = lds_seq_sum(sv + rr * nchp, nch, 0.f);
     __syncthreads();
   }
-  // the drafts, the draft positions' logits and the uniforms
-  __shared__ int s_x[64];
-  __shared__ float s_lt[64], s_lq[64], s_u[64];
+  s_in.x[lane] = xi;
+  s_in.lt[lane] = lt;
+  s_in.lq[lane] = lq;
+  s_in.u[lane] = uu;
   if (lane < a.D) {
-    s_x[lane] = xi;
-    s_lt[lane] = lt;
-    s_lq[lane] = lq;
-    s_u[lane] = uu;
+    // a_c at the draft's chunk, as row_stats forms it: exp(m_c - M) / Z
+    s_in.mt[lane] = mt;
+    s_in.at[lane] = ss_expf(mt - mrow[lane]) / zrow[lane];
+    s_in.md[lane] = md;
+    s_in.ad[lane] = ss_expf(md - mrow[a.D + 1 + lane]) / zrow[a.D + 1 + lane];
   }
   __syncthreads();
   if (lane == 0) {
-    const int D = a.D;
-    int good = 0, flags = 0, stop = 0;
-    int srow = D, sdraft = -1;
-    for (int i = 0; i < D; ++i) {
-      const int dr = D + 1 + i;
-      if (brow[i] || brow[dr]) {
-        flags |= FLAG_NONFINITE;
-        stop = 1;
-        break;
-      }
-      const int x = s_x[i];
-      if (x < 0 || x >= a.V) {
-        flags |= FLAG_BAD_DRAFT;
-        ss_raise(a.err, SS_ERR_TOKEN);
-        srow = i;
-        sdraft = dr;
-        break;
-      }
-      const float p = ss_expf(s_lt[i] / a.temperature - mrow[i]) / zrow[i];
-      const float q = ss_expf(s_lq[i] / a.temperature - mrow[dr]) / zrow[dr];
-      if (s_u[i] * q < p) {
-        ++good;
-        continue;
-      }
-      srow = i;
-      sdraft = dr;
-      break;
-    }
-    if (!stop && sdraft < 0 && brow[D]) {
-      flags |= FLAG_NONFINITE;
-      stop = 1;
-    }
-    k.state[0] = __int_as_float(srow);
-    k.state[1] = __int_as_float(sdraft);
-    k.state[2] = __int_as_float(good + (sdraft >= 0 ? 1 : 0));
-    k.state[3] = __int_as_float(stop);
-    k.state[4] = __int_as_float(good);
-    k.state[5] = __int_as_float(flags);
-    k.state[6] = zrow[srow];
-    k.state[7] = sdraft >= 0 ? zrow[sdraft] : 0.f;
-    k.state[8] = mrow[srow];
-    k.state[9] = sdraft >= 0 ? mrow[sdraft] : 0.f;
+    const PqState st = pq_decide(a, invT, mrow, zrow, brow, s_in, true);
+    k.state[0] = __int_as_float(st.srow);
+    k.state[1] = __int_as_float(st.sdraft);
+    k.state[2] = __int_as_float(st.uidx);
+    k.state[3] = __int_as_float(st.stop);
+    k.state[4] = __int_as_float(st.good);
+    k.state[5] = __int_as_float(st.flags);
+    k.state[6] = st.ms;
+    k.state[7] = st.zs;
+    k.state[8] = st.md;
+    k.state[9] = st.zd;
   }
 }
 
-// The round's state as the p/q sums launch left it, read with one batch of loads.
-struct PqState {
-  int srow, sdraft, uidx, stop, good, flags;
-  float zs, zd, ms, md;
-};
+// The round's state as pq_sum_kernel left it, read with one batch of loads.
 SS_DEV PqState pq_state(const float* st) {
   float v[10];
 #pragma unroll
@@ -522,127 +815,99 @@ SS_DEV PqState pq_state(const float* st) {
   r.stop = __float_as_int(v[3]);
   r.good = __float_as_int(v[4]);
   r.flags = __float_as_int(v[5]);
-  r.zs = v[6];
-  r.zd = v[7];
-  r.ms = v[8];
-  r.md = v[9];
+  r.ms = v[6];
+  r.zs = v[7];
+  r.md = v[8];
+  r.zd = v[9];
   return r;
 }
 
-// Value of entry j of the sampled distribution: p_j, or max(0, p_j - q_j) after a rejection.
-SS_DEV float sample_value(const AcceptArgs& a, const PqState& st, int j) {
-  const float p = ss_expf(a.target[(size_t)st.srow * a.V + j] / a.temperature - st.ms) / st.zs;
-  if (st.sdraft < 0) return p;
-  const float q = ss_expf(a.draft[(size_t)(st.sdraft - a.D - 1) * a.V + j] / a.temperature - st.md) / st.zd;
-  const float d = p - q;
-  return d > 0.f ? d : 0.f;
-}
+// e of entry j of a row from its logit and its chunk's maximum.
+SS_DEV float e_of(float x, float invT, float mc) { return ss_expf(x * invT - mc); }
 
-// Inverse-CDF search by the finishing workgroup. Every lane forms the same running sums (index order, from the
-// chunk's base) from LDS broadcast reads: the chunk, then the sub-chunk, then the entry, each falling back to the
-// last nonzero one.
-SS_DEV void pq_search(const AcceptArgs& a, const Work& k, const PqState& st, int nch, float* srt) {
-  __shared__ __attribute__((aligned(16))) float s_st[64];
-  __shared__ float s_val[kSub];
-  __shared__ int s_dr[64];
-  const int lane = threadIdx.x;
-  const int good = st.good;
-  int flags = st.flags;
-  const int stop = st.stop;
-  const int uidx = st.uidx;
-  // the accepted drafts, requested with the first loads rather than one round trip each at the end
-  for (int i = lane; i < good; i += 64) s_dr[i] = a.drafts[i];
-  int emit = good;
-  int pick = -1;
-  if (!stop) {
-    const float u = a.uniforms[uidx];
-    stage_rows_ag(k.rtot, 1, nch, (nch + 15) & ~15, srt);
-    __syncthreads();
-    const float S = lds_seq_sum(srt, nch, 0.f);
-    if (!(S > 0.f)) flags |= FLAG_RESIDUAL_EMPTY;
-    const float target = u * S;
-    // chunk: the first whose running total exceeds the target (else the last nonzero one, based at its prefix)
-    const Scan ch = lds_scan(srt, nch, 0.f, target);
-    int cs = ch.first;
-    float base = ch.base;
-    if (cs < 0) {
-      cs = ch.last < 0 ? 0 : ch.last;
-      base = lds_seq_sum(srt, cs, 0.f);
-    }
-    __syncthreads();
-    s_st[lane] = __hip_atomic_load(k.stot + cs * 64 + lane, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    const Scan sc = lds_scan(s_st, 64, base, target);
-    int bs = sc.first;
-    float sbase = sc.base;
-    if (bs < 0) {
-      bs = sc.last < 0 ? 0 : sc.last;
-      sbase = lds_seq_sum(s_st, bs, base);
-    }
-    const int j0 = cs * kChunk + bs * kSub;
-    if (lane < kSub) s_val[lane] = j0 + lane < a.V ? sample_value(a, st, j0 + lane) : 0.f;
-    __syncthreads();
-    int last = -1;
-    float run = sbase;
-    for (int i = 0; i < kSub; ++i) {
-      const int j = j0 + i;
-      if (j >= a.V) break;
-      const float v = s_val[i];
-      if (v > 0.f) last = j;
-      run = run + v;
-      if (run > target) {
-        pick = j;
-        break;
-      }
-    }
-    if (pick < 0) pick = last >= 0 ? last : min(j0, a.V - 1);
-  }
-  __syncthreads();
-  if (lane == 0) {
-    for (int i = 0; i < good; ++i) a.out[OUT_TOK + i] = s_dr[i];
-    if (!stop) a.out[OUT_TOK + emit++] = pick;
-    for (int i = emit; i <= a.D; ++i) a.out[OUT_TOK + i] = -1;
-    a.out[OUT_NACC] = good;
-    a.out[OUT_NEMIT] = emit;
-    a.out[OUT_NUNI] = stop ? uidx : uidx + 1;
-    a.out[OUT_FLAGS] = flags;
-  }
-}
-
-// Four waves per chunk compute the sampled distribution's values (its divisions and exps are the chunk's latency);
-// wave 0 then forms the sub-chunk and chunk totals and, in the last workgroup, runs the search.
+// Two-launch form, second launch: each chunk's workgroup forms the sampled values of its chunk (a_c from the
+// chunk's maxima and the sampled rows' M and Z, as row_stats forms it) and their total; the last workgroup finds
+// the chunk of the sample over the totals, then recomputes that chunk's values and finds the entry.
 __global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
-  __shared__ __attribute__((aligned(16))) float lds[kMaxPerLane * 64 + 64];
+  __shared__ float lds[64 * (kSub + 1)];
+  __shared__ int s_dr[64];
   const int c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nch = gridDim.x;
-  Work k = work_of(a.work, 2 * a.D + 1, nch);
+  const int V = a.V, D = a.D;
+  const float invT = 1.0f / a.temperature;
+  Work k = work_of(a.work, 2 * D + 1, nch);
   const PqState st = pq_state(k.state);
-  const bool run = !st.stop;
-  if (run) {
+  const bool rej = st.sdraft >= 0;
+  const float* xt = a.target + (size_t)st.srow * V;
+  const float* xd = rej ? a.draft + (size_t)(st.sdraft - D - 1) * V : xt;
+  if (!st.stop) {
+    const float mt = ld_ag(k.cmax + (size_t)st.srow * nch + c);
+    const float md = rej ? ld_ag(k.cmax + (size_t)st.sdraft * nch + c) : 0.f;
+    const float at = ss_expf(mt - st.ms) / st.zs, ad = rej ? ss_expf(md - st.md) / st.zd : 0.f;
 #pragma unroll
     for (int ii = 0; ii < kSub / 4; ++ii) {
       const int e = (w * (kSub / 4) + ii) * 64 + lane;
       const int j = c * kChunk + e;
-      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = j < a.V ? sample_value(a, st, j) : 0.f;
+      float v = 0.f;
+      if (j < V) v = sampled_value(e_of(xt[j], invT, mt), rej ? e_of(xd[j], invT, md) : 0.f, at, ad, rej);
+      lds[(e >> 4) * (kSub + 1) + (e & (kSub - 1))] = v;
     }
   }
   __syncthreads();
   if (w != 0) return;
-  if (run) {
+  if (!st.stop) {
     float s = 0.f;
     for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
-    st_ag(k.stot + c * 64 + lane, s);
-    s = ss_wave_sum(s);
+    s = ss_readlane_f(wave_scan(s), 63);
     if (lane == 0) st_ag(k.rtot + c, s);
   }
+  for (int i = lane; i < st.good; i += 64) s_dr[i] = a.drafts[i];
   if (!arrive_last(k.ctr, 2, c, nch)) return;
   arrival_clear(k.ctr, 2);
-  pq_search(a, k, st, nch, lds);
+  int pick = -1, flags = st.flags;
+  if (!st.stop) {
+    const int kc = (nch + 63) >> 6;
+    float rv[kMaxPerLane];
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+      const int cc = kc * lane + i;
+      rv[i] = i < kc && cc < nch ? ld_ag(k.rtot + cc) : 0.f;
+    }
+    const float S = wave_total(rv, kc, nch);
+    if (!(S > 0.f)) flags |= FLAG_RESIDUAL_EMPTY;
+    const float t = a.uniforms[st.uidx] * S;
+    float cbase;
+    const int cs = wave_descend(rv, kc, nch, t, &cbase);
+    // the values of chunk cs, lane l holding entries 16 l .. 16 l + 15
+    const float mt = ld_ag(k.cmax + (size_t)st.srow * nch + cs);
+    const float md = rej ? ld_ag(k.cmax + (size_t)st.sdraft * nch + cs) : 0.f;
+    const float at = ss_expf(mt - st.ms) / st.zs, ad = rej ? ss_expf(md - st.md) / st.zd : 0.f;
+    const int j0 = cs * kChunk + kSub * lane;
+    float vt[kSub];
+#pragma unroll
+    for (int e = 0; e < kSub; ++e) {
+      const int j = j0 + e;
+      vt[e] = j < V ? sampled_value(e_of(xt[j], invT, mt), rej ? e_of(xd[j], invT, md) : 0.f, at, ad, rej) : 0.f;
+    }
+    const int n_in = V - cs * kChunk < kChunk ? V - cs * kChunk : kChunk;
+    float ebase;
+    pick = cs * kChunk + wave_descend(vt, kSub, n_in, t - cbase, &ebase);
+  }
+  if (lane == 0) pq_write_out(a, st, s_dr, pick, flags);
 }
 
 hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st) {
   const int nch = (a.V + kChunk - 1) / kChunk;
   const int rows = 2 * a.D + 1;
-  hipLaunchKernelGGL(pq_max_kernel, dim3(nch, rows), dim3(64), 0, st, a);
+  const int units = (a.D + 1) * nch;
+  // One launch when every unit has a wave of a grid that is resident at once (one workgroup per CU at most).
+  KernelCfg cfg;
+  hipError_t e = kernel_cfg(reinterpret_cast<const void*>(pq_round_kernel), 256, 0, &cfg);
+  if (e != hipSuccess) return e;
+  const int grid = (units + 3) / 4;
+  if (units <= kFastUnits && ((nch + 15) & ~15) <= kFastStage / 4 && cfg.per_cu >= 1 && grid <= cfg.cus) {
+    hipLaunchKernelGGL(pq_round_kernel, dim3(grid), dim3(256), 0, st, a, units);
+    return hipGetLastError();
+  }
   hipLaunchKernelGGL(pq_sum_kernel, dim3(nch, rows), dim3(256), 0, st, a);
   hipLaunchKernelGGL(pq_residual_kernel, dim3(nch), dim3(256), 0, st, a);
   return hipGetLastError();

@@ -19,6 +19,7 @@ enum {
   SS_ERR_SLOT = 2,         // a map entry outside [0, n_slots) (an unmapped expert)
   SS_ERR_TOKEN = 4,        // a draft token outside [0, V)
   SS_ERR_NONFINITE = 8,    // non-finite logits reached a p/q decision
+  SS_ERR_TIMEOUT = 16,     // a persistent launch's bounded wait for other workgroups ran out
 };
 
 // ---------------------------------------------------------------- global-space access

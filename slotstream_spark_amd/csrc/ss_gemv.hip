@@ -32,13 +32,7 @@ struct GemvArgs {
   float* y;         // [R][N] or null
   uint64_t* rkey;   // [R] argmax keys, combined with atomic max (zeroed before the launch), or null
   int* rbad;        // [R] non-finite flags, combined with atomic or (with rkey)
-  int key_bf16;     // 1: the logits are lin's bf16 result: keys, chunk maxima and y take the dot rounded to bf16
-  // p/q fused behind the GEMV: per x row and 1024-entry vocabulary chunk, the key of the largest logit / temp
-  // (atomic max; NaN counts as the lowest) and a non-finite flag (atomic or), or null.
-  uint32_t* ckey;   // [R][nch]
-  int* cbad;        // [R][nch]
-  float temp;
-  int nch;
+  int key_bf16;     // 1: the logits are lin's bf16 result: keys and y take the dot rounded to bf16
 };
 
 SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -242,21 +236,6 @@ __global__ __launch_bounds__(256, 2) void gemv_affine4_kernel(GemvArgs a) {
       for (int r = 0; r < kGR; ++r)
         if (r < nt) a.y[(size_t)r * N + row] = acc[r];
     }
-    if (a.ckey) {
-      // This tile's 16 rows lie in one chunk (1024 = 64 tiles): one atomic per x row and tile.
-      const int c = tile >> 6;
-#pragma unroll
-      for (int r = 0; r < kGR; ++r) {
-        const bool valid = g == 0 && row < N && r < nt;
-        const uint32_t key = valid ? ss_key(acc[r] / a.temp) : 0u;
-        const uint32_t bad = valid && (__float_as_uint(acc[r]) & 0x7F800000u) == 0x7F800000u ? 1u : 0u;
-        const uint32_t km = ss_wave_max_u32(key), bm = ss_wave_or(bad);
-        if (lane == 0 && r < nt) {
-          atomicMax(a.ckey + (size_t)r * a.nch + c, km);
-          if (bm) atomicOr(a.cbad + (size_t)r * a.nch + c, 1);
-        }
-      }
-    }
     if (a.rkey) {
 #pragma unroll
       for (int r = 0; r < kGR; ++r) {
@@ -426,24 +405,11 @@ hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const i
   return hipGetLastError();
 }
 
-int64_t lm_head_pq_workspace_bytes(int D, int N) {
-  const int64_t nch = (N + 1023) / 1024;
-  const int64_t acc = (accept_work_floats(D, N) * 4 + 255) / 256 * 256;
-  const int64_t keys = ((D + 1) * nch * 4 + 255) / 256 * 256;
-  return acc + 2 * keys;
-}
+int64_t lm_head_pq_workspace_bytes(int D, int N) { return (accept_work_floats(D, N) * 4 + 255) / 256 * 256; }
 
 hipError_t launch_lm_head_pq(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
                              const uint16_t* b, int N, const float* draft, const int32_t* drafts, const float* uniforms,
                              float temperature, void* work, float* logits, int32_t* out, int* err, hipStream_t st) {
-  const int nch = (N + 1023) / 1024;
-  uint8_t* w = static_cast<uint8_t*>(work);
-  const int64_t acc = (accept_work_floats(D, N) * 4 + 255) / 256 * 256;
-  const int64_t keys = ((int64_t)(D + 1) * nch * 4 + 255) / 256 * 256;
-  uint32_t* ckey = reinterpret_cast<uint32_t*>(w + acc);
-  int* cbad = reinterpret_cast<int*>(w + acc + keys);
-  hipError_t e = launch_zero16(ckey, (size_t)(2 * keys), st);
-  if (e != hipSuccess) return e;
   GemvArgs a{};
   a.K = K;
   a.N = N;
@@ -452,17 +418,13 @@ hipError_t launch_lm_head_pq(const void* x, int x_f32, int D, int K, const int32
   a.s = s;
   a.b = b;
   a.key_bf16 = x_f32 ? 0 : 1;  // lin returns the dtype of x
-  a.temp = temperature;
-  a.nch = nch;
   const size_t xrow = (size_t)K * (x_f32 ? 4 : 2);
   const int R = D + 1;
   for (int r0 = 0; r0 < R; r0 += kGR) {
     a.x = static_cast<const uint8_t*>(x) + (size_t)r0 * xrow;
     a.R = R - r0 < kGR ? R - r0 : kGR;
     a.y = logits + (size_t)r0 * N;
-    a.ckey = ckey + (size_t)r0 * nch;
-    a.cbad = cbad + (size_t)r0 * nch;
-    e = launch_chunk(a, x_f32, st);
+    hipError_t e = launch_chunk(a, x_f32, st);
     if (e != hipSuccess) return e;
   }
   AcceptArgs p{};
@@ -474,10 +436,8 @@ hipError_t launch_lm_head_pq(const void* x, int x_f32, int D, int K, const int32
   p.V = N;
   p.temperature = temperature;
   p.out = out;
-  p.work = reinterpret_cast<float*>(w);
+  p.work = static_cast<float*>(work);
   p.err = err;
-  p.tkey = ckey;
-  p.tbad = cbad;
   return launch_accept_pq(p, st);
 }
 

@@ -249,10 +249,7 @@ struct AcceptArgs {
   int32_t* out;          // [D + 5]: n_accept, n_emit, n_uniform, flags, tokens[D+1]
   float* work;           // workspace floats
   int* err;
-  // p/q: the target rows' chunk maxima of l / T as order keys and their non-finite flags, [D + 1][nch], already
-  // formed by the lm_head GEMV (the max pass then reads only the draft rows), or null.
-  const uint32_t* tkey;
-  const int* tbad;
+  uint64_t* trace;       // diagnostics: per-workgroup phase stamps of the one-launch p/q round, or null
 };
 int64_t accept_work_floats(int D, int V);
 hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st);

@@ -14,7 +14,6 @@ constexpr int kMaxEv = 512;      // experts per layer (LDS tables)
 constexpr int kMaxQv = 64;       // kTBv * K, K <= 16
 constexpr int kSpinMax = 1 << 22;
 constexpr int kXZero = 98;       // uint4 zeros an inactive A lane reads in phase C: offsets 0 .. 48 * 2 (fp32 x)
-constexpr int SS_ERR_TIMEOUT = 16;
 constexpr size_t kLdsBudget = 160 * 1024 - 16 * 1024;  // dynamic LDS left after the static part (< 16 KB)
 
 // Counters are sharded: workgroup b adds to shard b % kShards of a counter, and a waiter sums the shards. Each

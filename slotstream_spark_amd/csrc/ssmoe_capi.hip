@@ -574,6 +574,7 @@ int ssmoe_accept_pq(const float* target, const float* draft, const int32_t* draf
   a.out = out;
   a.work = static_cast<float*>(workspace);
   a.err = err;
+  a.trace = g_trace;
   return hip_check(ss::launch_accept_pq(a, static_cast<hipStream_t>(stream)), "accept pq launch");
 }
 

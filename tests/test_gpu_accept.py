@@ -99,6 +99,23 @@ def test_pq_small_vocab_edge(acc):
         assert np.array_equal(out, O.accept_pq(t, q, d, u, 0.7)), i
 
 
+@pytest.mark.parametrize("d,v,seed", [(3, 307200, 1), (3, 307200, 2), (0, 151936, 3), (5, 100003, 4), (5, 100003, 5)])
+def test_pq_launch_forms(d, v, seed):
+    """Both forms of the round against the C definition: (3, 307200) has 1,200 (row pair, chunk) units, more than
+    the one-launch round's 1,024 waves, so it runs the two-launch form; D = 0 samples the bonus row only; V = 100,003
+    ends in a partial chunk and rows that are not 16-byte aligned (element loads)."""
+    small = Acceptor(d, v)
+    tgt, drf = verify_logits(d, v, 8000 + seed)
+    t, q = tgt.cpu().numpy(), drf.cpu().numpy()
+    g = np.random.default_rng(seed)
+    dr = np.where(g.random(d) < 0.7, q.argmax(axis=1), g.integers(0, v, d)).astype(np.int32) if d else \
+        np.zeros(0, np.int32)
+    u = UniformStream(seed).peek(d + 1)
+    for _ in range(2):  # a second call on the same workspace: the counters were left at zero
+        out = small.pq_async(tgt, drf, torch.from_numpy(dr).cuda(), torch.from_numpy(u).cuda(), 0.7).cpu().numpy()
+        assert np.array_equal(out, O.accept_pq(t, q, dr, u, 0.7)), out
+
+
 @pytest.mark.parametrize("seed", range(4))
 def test_draw_drafts_bitexact(acc, seed):
     """The proposal draw of the p/q round (ssmoe_sample_rows): row i's token is the reference sampler's draw at the
