@@ -307,8 +307,10 @@ static float chunk_total(ValFn f, const void* ctx, int c, int V, float* sub /* [
 /* ---------------------------------------------------------------- p/q acceptance (Leviathan et al. 2023, Alg. 1)
  * No reference counterpart. Every sum has a fixed order made of two pieces, so that the kernels form it with
  * lane-parallel operations:
- *   scan64: the inclusive prefix of 64 values by Hillis-Steele steps d = 1, 2, 4, .., 32 (P_l += P_{l-d} for l >= d,
- *   each step from the previous step's values); total64 = the last prefix.
+ *   scan64: the inclusive prefix of 64 nonnegative values: Hillis-Steele steps d = 1, 2, 4, 8 inside each row of
+ *   16 (P_l += P_{l-d} when l - d is in the row, each step from the previous step's values), then rows 1 and 3 add
+ *   the last value of the row before (P_15, P_47), then rows 2 and 3 add P_31 of that step; every addition is
+ *   (own + other); total64 = the last prefix. (The kernels form it with DPP row shifts and row broadcasts.)
  *   a "lane layout" of n values with k per lane: lane l holds values k l .. k l + k - 1 (those < n); its local sum is
  *   the sequential sum from 0; the layout's prefixes are scan64 of the local sums.
  * Per row (logits x, V entries, 1024-entry chunks c, invT = 1 / T in fp32):
@@ -327,11 +329,14 @@ static float chunk_total(ValFn f, const void* ctx, int c, int V, float* sub /* [
 static void scan64(const float* L, float* P) {
   float a[64], b[64];
   memcpy(a, L, sizeof a);
-  for (int d = 1; d < 64; d <<= 1) {
-    for (int l = 0; l < 64; ++l) b[l] = l >= d ? a[l] + a[l - d] : a[l];
+  for (int d = 1; d < 16; d <<= 1) {
+    for (int l = 0; l < 64; ++l) b[l] = (l & 15) >= d ? a[l] + a[l - d] : a[l];
     memcpy(a, b, sizeof a);
   }
-  memcpy(P, a, sizeof a);
+  for (int l = 0; l < 64; ++l) b[l] = (l >> 4) == 1 ? a[l] + a[15] : (l >> 4) == 3 ? a[l] + a[47] : a[l];
+  memcpy(a, b, sizeof a);
+  for (int l = 0; l < 64; ++l) b[l] = (l >> 4) >= 2 ? a[l] + a[31] : a[l];
+  memcpy(P, b, sizeof b);
 }
 
 /* Local sums of a lane layout of n values with k per lane. */

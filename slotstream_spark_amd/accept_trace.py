@@ -18,7 +18,7 @@ from . import _lib
 from .engine.accept import Acceptor, UniformStream
 from .memory.synth import verify_logits
 
-NAMES = [(0, "start"), (1, "chunk parts stored"), (2, "all chunk parts seen"), (3, "parts staged"),
+NAMES = [(0, "start"), (12, "logits loaded"), (13, "target chunk part"), (1, "chunk parts stored"), (2, "all chunk parts seen"), (3, "parts staged"),
          (4, "row statistics"), (5, "decision"), (8, "sampled values stored"), (9, "all sampled totals seen"),
          (10, "chunk of the sample found"), (11, "round written"), (6, "workgroup done")]
 

@@ -246,7 +246,9 @@ hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st) {
 // ---------------------------------------------------------------- p/q
 // Leviathan et al. 2023, Alg. 1 (no reference counterpart), with every sum in a lane-parallel fixed order that the
 // CPU restatement (or_accept_pq) replays bit for bit:
-//   wave_scan: the inclusive prefix of one value per lane by Hillis-Steele steps d = 1, 2, .., 32.
+//   wave_scan: the inclusive prefix of one nonnegative value per lane: Hillis-Steele steps d = 1, 2, 4, 8 inside each
+//   row of 16 lanes (R), then rows 1 and 3 add the last lane of the row before (R_15, R_47), then rows 2 and 3 add
+//   lane 31's value of that step (R_31 + R_15); every addition is (own + other).
 //   lane layout of n values, k per lane: lane l holds values k l .. k l + k - 1; its local sum is sequential from 0;
 //   the layout's total is the last lane's prefix.
 // Per row and 1024-entry chunk c (lane l: entries 16 l .. 16 l + 15): y = x * (1 / T), m_c = max y, e = exp(y - m_c),
@@ -264,13 +266,20 @@ hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st) {
 // Otherwise two launches: pq_sum_kernel (chunk parts; the last workgroup decides) and pq_residual_kernel (chunk
 // totals of the sampled values; the last workgroup searches).
 
+// DPP (GFX9 encodings): row_shr:d = 0x110 + d reads lane l - d of the same row (0 past the row's start, bound_ctrl);
+// row_bcast:15 = 0x142 gives rows 1 and 3 (row_mask 0xA) lane 15 / 47; row_bcast:31 = 0x143 gives rows 2 and 3
+// (row_mask 0xC) lane 31. Rows a step leaves out read 0, and v + 0 = v for v >= +0. VALU only, whole wave active.
+template <int CTRL, int ROWS, bool BOUND>
+SS_DEV float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, ROWS, 0xF, BOUND));
+}
 SS_DEV float wave_scan(float v) {
-  const int lane = threadIdx.x & 63;
-#pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const float o = __shfl_up(v, d, 64);
-    if (lane >= d) v = v + o;
-  }
+  v = v + dpp_f<0x111, 0xF, true>(v);
+  v = v + dpp_f<0x112, 0xF, true>(v);
+  v = v + dpp_f<0x114, 0xF, true>(v);
+  v = v + dpp_f<0x118, 0xF, true>(v);
+  v = v + dpp_f<0x142, 0xA, false>(v);
+  v = v + dpp_f<0x143, 0xC, false>(v);
   return v;
 }
 
@@ -306,30 +315,33 @@ SS_DEV int wave_descend(const float (&v)[KMAX], int k, int n, float t, float* ba
     ls = nz ? 63 - __builtin_clzll(nz) : 0;
   }
   const float e = ls > 0 ? ss_readlane_f(P, ls - 1) : 0.f;
+  // Branch-free inside the lane: the running sums R_i = e + v_0 + .. + v_i (sequential; an entry past n adds
+  // nothing), the first valid i with R_i > t, else the last valid nonzero value, else 0; the base is R before it.
+  float R[KMAX];
   float run = e;
-  int pick = -1, last = -1;
 #pragma unroll
   for (int i = 0; i < KMAX; ++i) {
     const bool in = i < k && k * lane + i < n;
-    const float x = in ? v[i] : 0.f;
-    if (in && x > 0.f) last = i;
-    if (in && pick < 0) {
-      const float nx = run + x;
-      if (nx > t)
-        pick = i;
-      else
-        run = nx;
-    }
+    run = in ? run + v[i] : run;
+    R[i] = run;
   }
-  if (pick < 0) {
-    pick = last >= 0 ? last : 0;
-    run = e;
+  int pick = -1, last = -1;
 #pragma unroll
-    for (int i = 0; i < KMAX; ++i)
-      if (i < pick) run = run + v[i];
+  for (int i = KMAX - 1; i >= 0; --i) {
+    const bool in = i < k && k * lane + i < n;
+    pick = in && R[i] > t ? i : pick;
   }
+#pragma unroll
+  for (int i = 0; i < KMAX; ++i) {
+    const bool in = i < k && k * lane + i < n;
+    last = in && v[i] > 0.f ? i : last;
+  }
+  pick = pick >= 0 ? pick : (last >= 0 ? last : 0);
+  float bse = e;
+#pragma unroll
+  for (int i = 1; i < KMAX; ++i) bse = pick == i ? R[i - 1] : bse;
   const int pb = __builtin_amdgcn_readlane(pick, ls);
-  *base = ss_readlane_f(run, ls);
+  *base = ss_readlane_f(bse, ls);
   const int idx = k * ls + pb;
   return idx < n ? idx : n - 1;
 }
@@ -343,115 +355,136 @@ struct ChunkPart {
 SS_DEV ChunkPart chunk_part(float (&v)[kSub], int j0, int V, float invT) {
   float m = -__builtin_inff();
   uint32_t bad = 0;
+  const int nv = V - j0;  // entries of this lane inside the row (every one in all but the last chunk)
 #pragma unroll
-  for (int e = 0; e < kSub; ++e)
-    if (j0 + e < V) {
-      bad |= !finite(v[e]);
-      v[e] = v[e] * invT;
-      m = fmaxf(m, v[e]);
-    }
+  for (int e = 0; e < kSub; ++e) {
+    const bool in = e < nv;
+    bad |= in && (__float_as_uint(v[e]) & 0x7F800000u) == 0x7F800000u;
+    v[e] = v[e] * invT;
+    m = in ? fmaxf(m, v[e]) : m;
+  }
   ChunkPart r;
   r.m = ss_wave_max(m);
   r.bad = (int)ss_wave_or(bad);
   float sub = 0.f;
 #pragma unroll
   for (int e = 0; e < kSub; ++e) {
-    v[e] = j0 + e < V ? ss_expf(v[e] - r.m) : 0.f;
+    v[e] = e < nv ? ss_expf_le0(v[e] - r.m) : 0.f;  // v - m <= 0 (NaN aside)
     sub = sub + v[e];
   }
   r.s = ss_readlane_f(wave_scan(sub), 63);
   return r;
 }
 
-// Row statistics from the row's staged chunk parts (LDS: m at sm, s at sv, flags at sb), one wave: M, Z and the
-// flag; sv receives a_c in place of s_c.
-SS_DEV void row_stats(float* sv, const float* sm, const float* sb, int nch, float* M, float* Z, int* bad) {
-  const int lane = threadIdx.x & 63, kc = (nch + 63) >> 6;
-  float mv[kMaxPerLane], g[kMaxPerLane];
-  float m = -__builtin_inff(), b = 0.f;
+// Statistics of NR rows (interleaved, so that their dependent chains overlap) from their staged chunk parts (LDS at
+// row r: m at sm + r nchp, s at sv + r nchp, flags at sb + r nchp), one wave; rows r[q] with q >= nr are skipped.
+// M, Z and the flag go to mrow, zrow, brow; sv receives a_c in place of s_c.
+// KM: chunks per lane the code is built for (kc = ceil(nch / 64) <= KM; KM == kc lets every loop bound be constant).
+template <int NR, int KM>
+SS_DEV void rows_stats(float* sv, const float* sm, const float* sb, const int (&r)[NR], int nr, int nch, int nchp,
+                       float* mrow, float* zrow, int* brow) {
+  const int lane = threadIdx.x & 63, kc = KM < kMaxPerLane ? KM : (nch + 63) >> 6;
+  float mv[NR][KM], g[NR][KM], m[NR], b[NR], L[NR];
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    if (i >= kc) break;
+  for (int q = 0; q < NR; ++q) {
+    m[q] = -__builtin_inff();
+    b[q] = 0.f;
+    L[q] = 0.f;
+  }
+#pragma unroll
+  for (int i = 0; i < KM; ++i) {
     const int c = kc * lane + i;
-    const bool in = c < nch;
-    mv[i] = in ? sm[c] : -__builtin_inff();
-    if (in) {
-      m = fmaxf(m, mv[i]);
-      b = fmaxf(b, sb[c]);  // flags are 0 or 1
+    const bool in = i < kc && c < nch;  // i < kc: the same in every lane
+#pragma unroll
+    for (int q = 0; q < NR; ++q) {
+      const int o = (q < nr ? r[q] : 0) * nchp + c;
+      mv[q][i] = in ? sm[o] : -__builtin_inff();
+      if (in) {
+        m[q] = fmaxf(m[q], mv[q][i]);
+        b[q] = fmaxf(b[q], sb[o]);  // flags are 0 or 1
+      }
     }
   }
-  m = ss_wave_max(m);
-  b = ss_wave_max(b);
-  float L = 0.f;
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    if (i >= kc) break;  // kc is the same in every lane
-    const int c = kc * lane + i;
-    g[i] = ss_expf(mv[i] - m);
-    if (c < nch) L = L + sv[c] * g[i];
+  for (int q = 0; q < NR; ++q) {
+    m[q] = ss_wave_max(m[q]);
+    b[q] = ss_wave_max(b[q]);
   }
-  const float z = ss_readlane_f(wave_scan(L), 63);
 #pragma unroll
-  for (int i = 0; i < kMaxPerLane; ++i) {
-    if (i >= kc) break;
-    const int c = kc * lane + i;
-    if (c < nch) sv[c] = g[i] / z;
+  for (int i = 0; i < KM; ++i) {
+    if (i < kc) {
+      const int c = kc * lane + i;
+#pragma unroll
+      for (int q = 0; q < NR; ++q) {
+        g[q][i] = ss_expf_le0(mv[q][i] - m[q]);  // m_c - M <= 0
+        if (c < nch) L[q] = L[q] + sv[(q < nr ? r[q] : 0) * nchp + c] * g[q][i];
+      }
+    }
   }
-  *M = m;
-  *Z = z;
-  *bad = b != 0.f;
+  float z[NR];
+#pragma unroll
+  for (int q = 0; q < NR; ++q) z[q] = ss_readlane_f(wave_scan(L[q]), 63);
+#pragma unroll
+  for (int i = 0; i < KM; ++i) {
+    const int c = kc * lane + i;
+    if (i < kc && c < nch) {
+#pragma unroll
+      for (int q = 0; q < NR; ++q)
+        if (q < nr) sv[r[q] * nchp + c] = g[q][i] / z[q];
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int q = 0; q < NR; ++q)
+      if (q < nr) {
+        mrow[r[q]] = m[q];
+        zrow[r[q]] = z[q];
+        brow[r[q]] = b[q] != 0.f;
+      }
+  }
 }
 
-// The round's decision (one thread): s_* hold, per draft i, the draft, the target and draft logits at it, the
-// uniform, and m_c and a_c of target row i and draft row i at the draft's chunk.
-struct PqIn {
-  int x[64];
-  float lt[64], lq[64], u[64], mt[64], at[64], md[64], ad[64];
-};
+// The round's decision, by one wave: lane i < D holds draft i's p_i(x_i), q_i(x_i) (exp(l x invT - m_c) a_c of
+// target row i and draft row i at the draft's chunk: the values the sampled distribution would take there), its
+// uniform, whether either row is non-finite and whether the draft is outside [0, V). The first draft that is not
+// accepted ends the round: a non-finite row stops it, a draft outside [0, V) is flagged (and raised) and rejected,
+// otherwise it is rejected; with every draft accepted, a non-finite row D stops it. Every lane returns the state.
 struct PqState {
   int srow, sdraft, uidx, stop, good, flags;
   float ms, zs, md, zd;
 };
-SS_DEV PqState pq_decide(const AcceptArgs& a, float invT, const float* mrow, const float* zrow, const int* brow,
-                         const PqIn& in, bool raise) {
-  const int D = a.D;
-  int good = 0, flags = 0, stop = 0;
-  int srow = D, sdraft = -1;
-  for (int i = 0; i < D; ++i) {
-    const int dr = D + 1 + i;
-    if (brow[i] || brow[dr]) {
+SS_DEV float p_at(float l, float invT, float mc, float ac) { return ss_expf(l * invT - mc) * ac; }
+SS_DEV PqState pq_decide(const AcceptArgs& a, bool bad_i, bool xbad_i, float p, float q, float u, const float* mrow,
+                         const float* zrow, const int* brow, bool raise) {
+  const int lane = threadIdx.x & 63, D = a.D;
+  const bool acc = lane < D && !bad_i && !xbad_i && u * q < p;
+  const uint64_t nacc = __ballot(lane < D && !acc);
+  const int f = nacc ? __builtin_ctzll(nacc) : D;
+  int flags = 0, stop = 0, srow = D, sdraft = -1;
+  if (f < D) {
+    const bool bf = __builtin_amdgcn_readlane((int)bad_i, f) != 0;
+    const bool xf = __builtin_amdgcn_readlane((int)xbad_i, f) != 0;
+    if (bf) {
       flags |= FLAG_NONFINITE;
       stop = 1;
-      break;
+    } else {
+      if (xf) {
+        flags |= FLAG_BAD_DRAFT;
+        if (raise && lane == 0) ss_raise(a.err, SS_ERR_TOKEN);
+      }
+      srow = f;
+      sdraft = D + 1 + f;
     }
-    const int x = in.x[i];
-    if (x < 0 || x >= a.V) {
-      flags |= FLAG_BAD_DRAFT;
-      if (raise) ss_raise(a.err, SS_ERR_TOKEN);
-      srow = i;
-      sdraft = dr;
-      break;
-    }
-    const float p = ss_expf(in.lt[i] * invT - in.mt[i]) * in.at[i];
-    const float q = ss_expf(in.lq[i] * invT - in.md[i]) * in.ad[i];
-    if (in.u[i] * q < p) {
-      ++good;
-      continue;
-    }
-    srow = i;
-    sdraft = dr;
-    break;
-  }
-  if (!stop && sdraft < 0 && brow[D]) {
+  } else if (brow[D]) {
     flags |= FLAG_NONFINITE;
     stop = 1;
   }
   PqState st;
   st.srow = srow;
   st.sdraft = sdraft;
-  st.uidx = good + (sdraft >= 0 ? 1 : 0);
+  st.good = f;
+  st.uidx = f + (sdraft >= 0 ? 1 : 0);
   st.stop = stop;
-  st.good = good;
   st.flags = flags;
   st.ms = mrow[srow];
   st.zs = zrow[srow];
@@ -459,6 +492,12 @@ SS_DEV PqState pq_decide(const AcceptArgs& a, float invT, const float* mrow, con
   st.zd = sdraft >= 0 ? zrow[sdraft] : 1.f;
   return st;
 }
+
+// Per draft i (lane i of wave 0): the draft, the target and draft logits at it, and the uniform.
+struct PqIn {
+  int x[64];
+  float lt[64], lq[64], u[64];
+};
 
 // Writes the round: the accepted drafts, then the sampled token unless the round stopped.
 SS_DEV void pq_write_out(const AcceptArgs& a, const PqState& st, const int* drafts, int pick, int flags) {
@@ -507,6 +546,7 @@ constexpr int kSpin = 1 << 22;  // bound of every wait for tagged words (then SS
 constexpr int kFastUnits = 1024;                            // units of the one-launch round (one wave each)
 constexpr int kFastStage = 2 * kFastUnits + 15 * kMaxRows;  // rows x nchp chunk parts staged per workgroup
 
+template <int KM>
 __global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) {
   __shared__ __attribute__((aligned(16))) float sv[kFastStage], sm[kFastStage], sb[kFastStage];
   __shared__ float mrow[kMaxRows], zrow[kMaxRows];
@@ -516,7 +556,7 @@ __global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) 
   __shared__ uint64_t s_tr[16];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int D = a.D, V = a.V, nch = nchunks_of(V), rows = 2 * D + 1, nchp = (nch + 15) & ~15;
-  const int kc = (nch + 63) >> 6;
+  const int kc = KM < kMaxPerLane ? KM : (nch + 63) >> 6;  // chunks per lane of the chunk layout
   const float invT = 1.0f / a.temperature;
   // phase stamps, kept in LDS and written at the exit: slot k by thread 0, slots 8 + k by lane 0 of a sampled-row wave
 #define PQ_TRACE(k, who)                                               \
@@ -552,8 +592,13 @@ __global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) 
   const uint32_t epoch = s_epoch;
   const uint32_t tag = (epoch + 1u) & 0x7FFFFFFFu;
   // phase 1: the unit's chunk parts (vt, vd become e), published as tagged words
+  if (a.trace && tid == 0) {
+    __builtin_amdgcn_s_waitcnt(0);  // traced launches only: the stamp after this wave's loads have landed
+    s_tr[12] = __builtin_amdgcn_s_memrealtime();
+  }
   if (has) {
     const ChunkPart pt = chunk_part(vt, j0, V, invT);
+    PQ_TRACE(13, tid == 0);
     if (lane == 0) {
       const size_t o = (size_t)ui * nch + c;
       st_ag(k.wd0 + o, tagged(tag | (pt.bad ? 0x80000000u : 0u), pt.m));
@@ -607,28 +652,23 @@ __global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) 
     }
     __syncthreads();
     PQ_TRACE(3, tid == 0);
-    for (int r = w; r < rows; r += 4) {
-      float M, Z;
-      int bad;
-      row_stats(sv + r * nchp, sm + r * nchp, sb + r * nchp, nch, &M, &Z, &bad);
-      if (lane == 0) {
-        mrow[r] = M;
-        zrow[r] = Z;
-        brow[r] = bad;
-      }
+    for (int r0 = w; r0 < rows; r0 += 8) {
+      const int rr[2] = {r0, r0 + 4};
+      rows_stats<2, KM>(sv, sm, sb, rr, r0 + 4 < rows ? 2 : 1, nch, nchp, mrow, zrow, brow);
     }
     __syncthreads();
     PQ_TRACE(4, tid == 0);
-    if (tid < D) {
-      const int xi = s_in.x[tid];
-      const int cx = xi >= 0 && xi < V ? xi >> 10 : 0;
-      s_in.mt[tid] = sm[tid * nchp + cx];
-      s_in.at[tid] = sv[tid * nchp + cx];
-      s_in.md[tid] = sm[(D + 1 + tid) * nchp + cx];
-      s_in.ad[tid] = sv[(D + 1 + tid) * nchp + cx];
+    if (w == 0) {
+      const int xi = s_in.x[lane];
+      const bool xbad = lane < D && (xi < 0 || xi >= V);
+      const int cx = lane < D && !xbad ? xi >> 10 : 0;
+      const int ti = lane < D ? lane : 0, di = lane < D ? D + 1 + lane : 0;
+      const bool bad = lane < D && (brow[ti] || brow[di]);
+      const float p = p_at(s_in.lt[lane], invT, sm[ti * nchp + cx], sv[ti * nchp + cx]);
+      const float q = p_at(s_in.lq[lane], invT, sm[di * nchp + cx], sv[di * nchp + cx]);
+      const PqState st = pq_decide(a, bad, xbad, p, q, s_in.u[lane], mrow, zrow, brow, blockIdx.x == 0);
+      if (lane == 0) s_st = st;
     }
-    __syncthreads();
-    if (tid == 0) s_st = pq_decide(a, invT, mrow, zrow, brow, s_in, blockIdx.x == 0);
     __syncthreads();
     PQ_TRACE(5, tid == 0);
   }
@@ -646,11 +686,11 @@ __global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) 
     PQ_TRACE(8, lane == 0);
     // phase 4: every wave of the row polls the chunk totals, finds the chunk of the sample; the wave holding it
     // finds the entry
-    float rv[kMaxPerLane];
+    float rv[KM];
     for (int it = 0;; ++it) {
       int ok = 1;
 #pragma unroll
-      for (int i = 0; i < kMaxPerLane; ++i) {
+      for (int i = 0; i < KM; ++i) {
         const int cc = kc * lane + i;
         const bool in = i < kc && cc < nch;
         const uint64_t wv = in ? ld_ag(k.wr + cc) : 0;
@@ -696,7 +736,6 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
   __shared__ int brow[kMaxRows];
   __shared__ float s_m[4];
   __shared__ int s_b[4];
-  __shared__ PqIn s_in;
   const int row = blockIdx.y, c = blockIdx.x, tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int nch = gridDim.x, rows = gridDim.y;
   const float invT = 1.0f / a.temperature;
@@ -764,42 +803,32 @@ __global__ __launch_bounds__(256) void pq_sum_kernel(AcceptArgs a) {
     // 17 per lane: one batch for the seven rows of a depth-3 round at V = 151,936 (1,043 chunks)
     stage_rows3_ag<17>(k.ctot + o, k.cmax + o, k.cbad + o, nr, nch, nchp, sv, sm, sb);
     __syncthreads();
-    for (int rr = 0; rr < nr; ++rr) {
-      float M, Z;
-      int bad;
-      row_stats(sv + rr * nchp, sm + rr * nchp, sb + rr * nchp, nch, &M, &Z, &bad);
-      if (lane == 0) {
-        mrow[r0 + rr] = M;
-        zrow[r0 + rr] = Z;
-        brow[r0 + rr] = bad;
-      }
+    for (int rr = 0; rr < nr; rr += 2) {
+      const int ri[2] = {rr, rr + 1};
+      rows_stats<2, kMaxPerLane>(sv, sm, sb, ri, rr + 1 < nr ? 2 : 1, nch, nchp, mrow + r0, zrow + r0, brow + r0);
     }
     __syncthreads();
   }
-  s_in.x[lane] = xi;
-  s_in.lt[lane] = lt;
-  s_in.lq[lane] = lq;
-  s_in.u[lane] = uu;
-  if (lane < a.D) {
-    // a_c at the draft's chunk, as row_stats forms it: exp(m_c - M) / Z
-    s_in.mt[lane] = mt;
-    s_in.at[lane] = ss_expf(mt - mrow[lane]) / zrow[lane];
-    s_in.md[lane] = md;
-    s_in.ad[lane] = ss_expf(md - mrow[a.D + 1 + lane]) / zrow[a.D + 1 + lane];
-  }
-  __syncthreads();
-  if (lane == 0) {
-    const PqState st = pq_decide(a, invT, mrow, zrow, brow, s_in, true);
-    k.state[0] = __int_as_float(st.srow);
-    k.state[1] = __int_as_float(st.sdraft);
-    k.state[2] = __int_as_float(st.uidx);
-    k.state[3] = __int_as_float(st.stop);
-    k.state[4] = __int_as_float(st.good);
-    k.state[5] = __int_as_float(st.flags);
-    k.state[6] = st.ms;
-    k.state[7] = st.zs;
-    k.state[8] = st.md;
-    k.state[9] = st.zd;
+  {
+    // a_c at the draft's chunk, as rows_stats forms it: exp(m_c - M) / Z
+    const int ti = lane < a.D ? lane : 0, di = lane < a.D ? a.D + 1 + lane : 0;
+    const bool xbad = lane < a.D && !xok;
+    const bool bad = lane < a.D && (brow[ti] || brow[di]);
+    const float p = p_at(lt, invT, mt, ss_expf_le0(mt - mrow[ti]) / zrow[ti]);
+    const float q = p_at(lq, invT, md, ss_expf_le0(md - mrow[di]) / zrow[di]);
+    const PqState st = pq_decide(a, bad, xbad, p, q, uu, mrow, zrow, brow, true);
+    if (lane == 0) {
+      k.state[0] = __int_as_float(st.srow);
+      k.state[1] = __int_as_float(st.sdraft);
+      k.state[2] = __int_as_float(st.uidx);
+      k.state[3] = __int_as_float(st.stop);
+      k.state[4] = __int_as_float(st.good);
+      k.state[5] = __int_as_float(st.flags);
+      k.state[6] = st.ms;
+      k.state[7] = st.zs;
+      k.state[8] = st.md;
+      k.state[9] = st.zd;
+    }
   }
 }
 
@@ -900,12 +929,15 @@ hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st) {
   const int rows = 2 * a.D + 1;
   const int units = (a.D + 1) * nch;
   // One launch when every unit has a wave of a grid that is resident at once (one workgroup per CU at most).
+  const int kc = (nch + 63) >> 6;
+  auto kern = kc == 1 ? pq_round_kernel<1> : kc == 2 ? pq_round_kernel<2> : kc == 3 ? pq_round_kernel<3>
+            : kc == 4 ? pq_round_kernel<4> : pq_round_kernel<kMaxPerLane>;
   KernelCfg cfg;
-  hipError_t e = kernel_cfg(reinterpret_cast<const void*>(pq_round_kernel), 256, 0, &cfg);
+  hipError_t e = kernel_cfg(reinterpret_cast<const void*>(kern), 256, 0, &cfg);
   if (e != hipSuccess) return e;
   const int grid = (units + 3) / 4;
-  if (units <= kFastUnits && ((nch + 15) & ~15) <= kFastStage / 4 && cfg.per_cu >= 1 && grid <= cfg.cus) {
-    hipLaunchKernelGGL(pq_round_kernel, dim3(grid), dim3(256), 0, st, a, units);
+  if (units <= kFastUnits && cfg.per_cu >= 1 && grid <= cfg.cus) {
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), 0, st, a, units);
     return hipGetLastError();
   }
   hipLaunchKernelGGL(pq_sum_kernel, dim3(nch, rows), dim3(256), 0, st, a);

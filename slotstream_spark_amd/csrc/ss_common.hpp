@@ -89,6 +89,29 @@ SS_DEV float ss_expf(float x) {
   return x != x ? x : y;
 }
 
+// ss_expf for x <= 0 (and NaN), with the same bits: there n <= 0, so the clamp's upper bound, the 2^128 range step and
+// the overflow select never act and are left out (a softmax of values minus their maximum only needs this range).
+SS_DEV float ss_expf_le0(float x) {
+  const float n = __builtin_rintf(x * 1.44269502162933349609375f);
+  float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+  r = __builtin_fmaf(-n, 1.428606765330187045037746429443359375e-06f, r);
+  float p = 1.98412701138295233249664306640625e-04f;
+  p = __builtin_fmaf(p, r, 1.38888892251998186111450195312500e-03f);
+  p = __builtin_fmaf(p, r, 8.33333376795053482055664062500000e-03f);
+  p = __builtin_fmaf(p, r, 4.16666679084300994873046875000000e-02f);
+  p = __builtin_fmaf(p, r, 1.66666671633720397949218750000000e-01f);
+  p = __builtin_fmaf(p, r, 0.5f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  p = __builtin_fmaf(p, r, 1.0f);
+  int ni = (int)__builtin_fmaxf(n, -160.f);
+  const bool tiny = ni < -120;
+  p = tiny ? p * 5.42101086242752217003726400434970855712890625e-20f : p;  // 2^-64
+  ni = tiny ? ni + 64 : ni;
+  float y = p * __uint_as_float((uint32_t)(ni + 127) << 23);
+  y = x < -103.97208404541015625f ? 0.0f : y;
+  return x != x ? x : y;
+}
+
 // ---------------------------------------------------------------- order-preserving keys
 // Positive floats: flip the sign bit; negative: bitwise not; NaN: key 0 (lowest).
 // (kernels/topk_stable.py:1-13 semantics: -0.0 sorts just below +0.0.)

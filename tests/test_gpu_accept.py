@@ -99,11 +99,14 @@ def test_pq_small_vocab_edge(acc):
         assert np.array_equal(out, O.accept_pq(t, q, d, u, 0.7)), i
 
 
-@pytest.mark.parametrize("d,v,seed", [(3, 307200, 1), (3, 307200, 2), (0, 151936, 3), (5, 100003, 4), (5, 100003, 5)])
+@pytest.mark.parametrize("d,v,seed", [(3, 307200, 1), (3, 307200, 2), (0, 151936, 3), (5, 100003, 4), (5, 100003, 5),
+                                      (2, 200000, 6), (1, 400000, 7)])
 def test_pq_launch_forms(d, v, seed):
     """Both forms of the round against the C definition: (3, 307200) has 1,200 (row pair, chunk) units, more than
     the one-launch round's 1,024 waves, so it runs the two-launch form; D = 0 samples the bonus row only; V = 100,003
-    ends in a partial chunk and rows that are not 16-byte aligned (element loads)."""
+    ends in a partial chunk and rows that are not 16-byte aligned (element loads). The chunk layout holds 1, 2, 3 or
+    4 chunks per lane in builds of their own and more in a generic one: V = 200,000 (196 chunks: 4 per lane) and
+    V = 400,000 (391 chunks: 7 per lane, the generic build) cover the last two."""
     small = Acceptor(d, v)
     tgt, drf = verify_logits(d, v, 8000 + seed)
     t, q = tgt.cpu().numpy(), drf.cpu().numpy()
