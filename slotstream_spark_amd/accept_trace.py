@@ -3,7 +3,8 @@
     python -m slotstream_spark_amd.accept_trace [D] [V]
 
 Runs BASELINE config 2's round (depth D = 3, vocab V = 151,936, temperature 0.7) on seeded synthetic logits with
-drafts drawn from q, times 200 rounds in one HIP graph (HIP events), then runs one eager round with the trace on and
+drafts drawn from q, times 200 rounds in one HIP graph (HIP events; the greedy round on the same target rows
+likewise), then runs one eager round with the trace on and
 prints, for every stamp, the median and maximum over the workgroups that wrote it, in us from the first workgroup
 start. Stamps 0-6 are per workgroup; 8-11 come from the waves that hold a chunk of the sampled row.
 """
@@ -49,6 +50,21 @@ def run(D: int = 3, V: int = 151936, temp: float = 0.7) -> str:
         times.append(e0.elapsed_time(e1) * 1000 / 200)
     times.sort()
     out = [f"D={D} V={V}: {times[2]:.2f} us per round (graph of 200 rounds; median of 5, min {times[0]:.2f})"]
+    gg = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(gg, stream=s):
+            for _ in range(200):
+                acc.greedy_async(tgt, drafts)
+    gt = []
+    for _ in range(5):
+        with torch.cuda.stream(s):
+            e0.record(s)
+            gg.replay()
+            e1.record(s)
+        torch.cuda.synchronize()
+        gt.append(e0.elapsed_time(e1) * 1000 / 200)
+    gt.sort()
+    out.append(f"greedy round: {gt[2]:.2f} us (graph of 200 rounds; median of 5, min {gt[0]:.2f})")
     buf = torch.zeros(1024 * 16, dtype=torch.int64, device="cuda")
     _lib.check(_lib.lib().ssmoe_set_trace(buf.data_ptr(), buf.numel()))
     try:

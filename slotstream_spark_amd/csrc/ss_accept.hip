@@ -237,11 +237,6 @@ __global__ __launch_bounds__(64) void greedy_kernel(AcceptArgs a) {
   }
 }
 
-hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st) {
-  const int nch = (a.V + kChunk - 1) / kChunk;
-  hipLaunchKernelGGL(greedy_kernel, dim3(nch, a.D + 1), dim3(64), 0, st, a);
-  return hipGetLastError();
-}
 
 // ---------------------------------------------------------------- p/q
 // Leviathan et al. 2023, Alg. 1 (no reference counterpart), with every sum in a lane-parallel fixed order that the
@@ -542,6 +537,115 @@ SS_DEV uint32_t tag_of(uint64_t w) { return (uint32_t)(w >> 32) & 0x7FFFFFFFu; }
 SS_DEV float val_of(uint64_t w) { return __uint_as_float((uint32_t)w); }
 SS_DEV uint64_t tagged(uint32_t tag, float v) { return ((uint64_t)tag << 32) | __float_as_uint(v); }
 constexpr int kSpin = 1 << 22;  // bound of every wait for tagged words (then SS_ERR_TIMEOUT and on)
+
+// ---------------------------------------------------------------- greedy, one launch
+// Used when every (row, chunk) unit has a wave of a resident grid: each wave forms its chunk's first maximum (the
+// greedy_kernel key: order key of the value, +-0 equal, then the complemented index) and non-finite flag and
+// publishes them as two tagged words; workgroup 0 polls them, reduces each row (order-free), decides and writes the
+// round. No counter and no arrival: the epoch is advanced by workgroup 0 once every word has been seen.
+__global__ __launch_bounds__(256) void greedy_round_kernel(AcceptArgs a, int units) {
+  __shared__ uint32_t s_epoch;
+  __shared__ int s_tok[kMaxRows], s_bad[kMaxRows];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int D = a.D, V = a.V, nch = nchunks_of(V), rows = D + 1;
+  Work k = work_of(a.work, 2 * D + 1, nch);
+  const int gw = blockIdx.x * 4 + w;
+  const bool has = gw < units;
+  const int row = has ? gw / nch : 0, c = has ? gw - row * nch : 0;
+  const int j0 = c * kChunk + kSub * lane;
+  const bool vec = (V & 3) == 0 && (reinterpret_cast<uintptr_t>(a.target) & 15) == 0;
+  float v[kSub];
+  if (has) load16(a.target + (size_t)row * V, j0, V, vec, v);
+  // the drafts (lane i: draft i), with the first loads
+  const int dr = w == 0 && blockIdx.x == 0 && lane < D ? a.drafts[lane] : 0;
+  if (tid == 0) s_epoch = (uint32_t)ld_ag(k.ctr + kEpochInt);
+  __syncthreads();
+  const uint32_t epoch = s_epoch;
+  const uint32_t tag = (epoch + 1u) & 0x7FFFFFFFu;
+  if (has) {
+    uint64_t bk = 0;
+    uint32_t bad = 0;
+    const int nv = V - j0;
+#pragma unroll
+    for (int e = 0; e < kSub; ++e) {
+      const bool in = e < nv;
+      bad |= in && (__float_as_uint(v[e]) & 0x7F800000u) == 0x7F800000u;
+      const uint64_t kv = ((uint64_t)ss_key(v[e] == 0.f ? 0.f : v[e]) << 32) | (0xFFFFFFFFu - (uint32_t)(j0 + e));
+      bk = in && kv > bk ? kv : bk;
+    }
+    bk = ss_wave_max_u64(bk);
+    bad = ss_wave_or(bad);
+    if (lane == 0) {
+      const size_t o = (size_t)row * nch + c;
+      st_ag(k.wd0 + o, ((uint64_t)(tag | (bad ? 0x80000000u : 0u)) << 32) | (uint32_t)(bk >> 32));
+      st_ag(k.wd1 + o, ((uint64_t)tag << 32) | (uint32_t)bk);
+    }
+  }
+  if (blockIdx.x != 0) return;
+  // workgroup 0: wave w reduces rows w, w + 4, .. once all their chunk words carry this launch's tag
+  for (int r = w; r < rows; r += 4) {
+    uint64_t bk = 0;
+    uint32_t bad = 0;
+    for (int it = 0;; ++it) {
+      int ok = 1;
+      bk = 0;
+      bad = 0;
+      uint64_t w0[kMaxPerLane], w1[kMaxPerLane];  // every load of the poll in flight before any is used
+#pragma unroll
+      for (int q = 0; q < kMaxPerLane; ++q) {
+        const int cc = lane + 64 * q;
+        w0[q] = cc < nch ? ld_ag(k.wd0 + (size_t)r * nch + cc) : 0;
+        w1[q] = cc < nch ? ld_ag(k.wd1 + (size_t)r * nch + cc) : 0;
+      }
+#pragma unroll
+      for (int q = 0; q < kMaxPerLane; ++q) {
+        if (lane + 64 * q >= nch) continue;
+        ok &= tag_of(w0[q]) == tag && tag_of(w1[q]) == tag;
+        const uint64_t kv = ((uint64_t)(uint32_t)w0[q] << 32) | (uint32_t)w1[q];
+        bk = kv > bk ? kv : bk;
+        bad |= (uint32_t)(w0[q] >> 63);
+      }
+      if (__all(ok)) break;
+      if (it >= kSpin) {
+        if (lane == 0) ss_raise(a.err, SS_ERR_TIMEOUT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+    }
+    bk = ss_wave_max_u64(bk);
+    bad = ss_wave_or(bad);
+    if (lane == 0) {
+      s_tok[r] = (int)(0xFFFFFFFFu - (uint32_t)bk);
+      s_bad[r] = (int)bad;
+    }
+  }
+  __shared__ int s_dr[64];
+  if (w == 0 && lane < D) s_dr[lane] = dr;
+  __syncthreads();
+  if (tid == 0) {
+    // every workgroup has published, so every one has read the epoch
+    st_ag(k.ctr + kEpochInt, (int)(epoch + 1u));
+    int good = 0, emit = 0, flags = 0;
+    for (int i = 0; i <= D; ++i) {
+      if (s_bad[i]) {
+        flags |= FLAG_NONFINITE;
+        break;
+      }
+      const int t = s_tok[i];
+      a.out[OUT_TOK + emit++] = t;
+      if (i < D && t == s_dr[i]) {
+        ++good;
+        continue;
+      }
+      break;
+    }
+    for (int i = emit; i <= D; ++i) a.out[OUT_TOK + i] = -1;
+    a.out[OUT_NACC] = good;
+    a.out[OUT_NEMIT] = emit;
+    a.out[OUT_NUNI] = 0;
+    a.out[OUT_FLAGS] = flags;
+  }
+}
 
 constexpr int kFastUnits = 1024;                            // units of the one-launch round (one wave each)
 constexpr int kFastStage = 2 * kFastUnits + 15 * kMaxRows;  // rows x nchp chunk parts staged per workgroup
@@ -922,6 +1026,21 @@ __global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
     pick = cs * kChunk + wave_descend(vt, kSub, n_in, t - cbase, &ebase);
   }
   if (lane == 0) pq_write_out(a, st, s_dr, pick, flags);
+}
+
+hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st) {
+  const int nch = (a.V + kChunk - 1) / kChunk;
+  const int units = (a.D + 1) * nch;
+  KernelCfg cfg;
+  hipError_t e = kernel_cfg(reinterpret_cast<const void*>(greedy_round_kernel), 256, 0, &cfg);
+  if (e != hipSuccess) return e;
+  const int grid = (units + 3) / 4;
+  if (units <= kFastUnits && cfg.per_cu >= 1 && grid <= cfg.cus) {
+    hipLaunchKernelGGL(greedy_round_kernel, dim3(grid), dim3(256), 0, st, a, units);
+    return hipGetLastError();
+  }
+  hipLaunchKernelGGL(greedy_kernel, dim3(nch, a.D + 1), dim3(64), 0, st, a);
+  return hipGetLastError();
 }
 
 hipError_t launch_accept_pq(const AcceptArgs& a, hipStream_t st) {

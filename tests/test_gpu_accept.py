@@ -39,6 +39,23 @@ def test_greedy_bitexact(acc, seed):
     assert out[0] == seed % (D + 1)
 
 
+@pytest.mark.parametrize("d,v,seed", [(3, 307200, 1), (0, 151936, 2), (5, 100003, 3), (5, 100003, 4)])
+def test_greedy_launch_forms(d, v, seed):
+    """Both forms of the greedy round: (3, 307200) has 1,200 (row, chunk) units, more than the one-launch round's
+    1,024 waves (the per-chunk launch with an arrival count); D = 0 emits the argmax of one row; V = 100,003 ends in
+    a partial chunk of rows that are not 16-byte aligned. Two calls on one workspace each."""
+    small = Acceptor(d, v)
+    tgt, _ = verify_logits(d, v, 9000 + seed)
+    t = tgt.cpu().numpy()
+    g = np.random.default_rng(seed)
+    am = t.argmax(axis=1)
+    dr = g.integers(0, v, d).astype(np.int32)
+    dr[:seed % (d + 1)] = am[:seed % (d + 1)]
+    for _ in range(2):
+        out = small.greedy_async(tgt, torch.from_numpy(dr).cuda()).cpu().numpy()
+        assert np.array_equal(out, O.accept_greedy(t, dr)), out
+
+
 def test_greedy_nonfinite_stops(acc):
     tgt, _ = verify_logits(D, V, 77)
     t = tgt.cpu().numpy()
