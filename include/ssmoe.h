@@ -312,14 +312,17 @@ int ssmoe_bench_stream_read(const void* src, int64_t bytes, uint32_t* out, int g
  * operands from seed uint32 [8]: 2 * 16 * 16 * 32 * 8 * iters flop per wave. out fp32 [grid * 4] (the wave sums). */
 int ssmoe_bench_mfma_bf16(const uint32_t* seed, int iters, float* out, int grid, void* stream);
 
-/* Bytes of the workspace ssmoe_sample_rows needs (-1 outside 1 <= R <= 64, 1 <= V <= 1,048,576). */
+/* Bytes of the workspace ssmoe_sample_rows needs (-1 outside 1 <= R <= 64, 1 <= V <= 1,048,576); zero it before
+ * its first use (it keeps a launch counter). */
 int64_t ssmoe_sample_rows_workspace_bytes(int R, int V);
 
-/* The draft tokens of a p/q round: x_r ~ softmax(logits[r] / temperature) for the R rows of logits fp32 [R, V],
- * each drawn as ssmoe_sample with that temperature and no top-k, top-p, min-p or penalty, with uniforms[r]
- * (tokens int32 [R], on the device). Leviathan et al. 2023 Alg. 1 (ssmoe_accept_pq) requires the drafts to be
- * drawn from the same q it divides by; the reference drafts greedily (engine/mtp.py:265-277, torch.argmax), which is
- * the temperature-0 limit and is not a valid proposal for p/q. No reference counterpart. temperature > 0. */
+/* The draft tokens of a p/q round: x_r ~ softmax(logits[r] / temperature) for the R rows of logits fp32 [R, V]
+ * with uniforms[r] (tokens int32 [R], on the device), with the p/q round's row statistics (ssmoe_accept_pq's sum
+ * order): the chunk by its mass, then the entry inside it; one persistent launch per group of rows whose
+ * (row, 1024-entry chunk) units fit a resident grid. A row with a non-finite logit yields an index in [0, V) of no
+ * meaning (ssmoe_accept_pq stops at that row). Leviathan et al. 2023 Alg. 1 requires the drafts to be drawn from the
+ * same q it divides by; the reference drafts greedily (engine/mtp.py:265-277, torch.argmax), which is the
+ * temperature-0 limit and is not a valid proposal for p/q. No reference counterpart. temperature > 0. */
 int ssmoe_sample_rows(const float* logits, int R, int V, float temperature, const float* uniforms, void* workspace,
                       int64_t workspace_bytes, int32_t* tokens, void* stream);
 

@@ -47,6 +47,7 @@ def lib():
         L.or_topk_stable.argtypes, L.or_topk_stable.restype = [P, P, P, P, i32, i32, i32, P], None
         L.or_accept_greedy.argtypes, L.or_accept_greedy.restype = [P, P, i32, i32, P], None
         L.or_accept_pq.argtypes, L.or_accept_pq.restype = [P, P, P, P, i32, i32, f32, P, P], None
+        L.or_draw_rows.argtypes, L.or_draw_rows.restype = [P, i32, i32, f32, P, P], None
         L.or_row_z.argtypes, L.or_row_z.restype = [P, i32, f32], f32
         L.or_shared_hs.argtypes, L.or_shared_hs.restype = [P, P, P, i32], None
         L.or_dense_rows_q4.argtypes, L.or_dense_rows_q4.restype = [P, P, P, P, P, i32, i32, i32], None
@@ -153,6 +154,16 @@ def accept_pq(target, draft, drafts, uniforms, temperature) -> np.ndarray:
     nch = (V + 1023) // 1024
     work = np.empty(nch * 65 + 64, np.float32)
     lib().or_accept_pq(_p(t), _p(q), _p(d), _p(u), D, V, float(temperature), _p(out), _p(work))
+    return out
+
+
+def draw_rows(logits, temperature, uniforms) -> np.ndarray:
+    """x_r ~ softmax(logits[r] / temperature) with uniforms[r]: the proposal draw of the p/q round (or_draw_rows)."""
+    x = _c(logits, np.float32)
+    u = _c(uniforms, np.float32)
+    R, V = x.shape
+    out = np.empty(R, np.int32)
+    lib().or_draw_rows(_p(x), R, V, float(temperature), _p(u), _p(out))
     return out
 
 

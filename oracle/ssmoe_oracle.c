@@ -348,16 +348,17 @@ static void lane_sums(const float* v, int n, int k, float* L) {
   }
 }
 
-/* The search over a lane layout (n values, k per lane) for target t: the first lane whose prefix exceeds t (else
- * the last lane with a nonzero local sum, else lane 0), then inside it the first value whose running sum from the
- * lane's exclusive prefix exceeds t (else its last nonzero value, else its first); *base receives the running sum
- * before the chosen value. Returns the value's index, clamped to n - 1. */
+/* The search over a lane layout (n values, k per lane) for target t: the first lane holding values whose prefix
+ * exceeds t (else the last lane with a nonzero local sum, else lane 0), then inside it the first value whose running
+ * sum from the lane's exclusive prefix exceeds t (else its last nonzero value, else its first); *base receives the
+ * running sum before the chosen value. Returns the value's index, clamped to n - 1. (The scan's prefixes need not
+ * rise with l by the last ulp, so an empty lane past the values could otherwise be the first to exceed t.) */
 static int descend(const float* v, int n, int k, float t, float* base) {
   float L[64], P[64];
   lane_sums(v, n, k, L);
   scan64(L, P);
   int ls = -1;
-  for (int l = 0; l < 64 && ls < 0; ++l)
+  for (int l = 0; l < 64 && ls < 0 && k * l < n; ++l)
     if (P[l] > t) ls = l;
   if (ls < 0) {
     for (int l = 0; l < 64; ++l)
@@ -388,7 +389,7 @@ static int descend(const float* v, int n, int k, float t, float* base) {
 }
 
 typedef struct {
-  float m[PQ_MAX_NCH], a[PQ_MAX_NCH];
+  float m[PQ_MAX_NCH], a[PQ_MAX_NCH], s[PQ_MAX_NCH];
   float M, Z;
   int bad;
 } PqRow;
@@ -418,6 +419,7 @@ static void pq_row(const float* x, int V, float invT, PqRow* r) {
     scan64(L, P);
     r->m[c] = mc;
     s[c] = P[63];
+    r->s[c] = s[c];
     r->M = fmaxf(r->M, mc);
   }
   for (int c = 0; c < nch; ++c) {
@@ -522,6 +524,32 @@ void or_accept_pq(const float* target, const float* draft, const int32_t* drafts
   out[3] = flags;
   free(rt);
   free(rd);
+}
+
+/* Draws x_r ~ softmax(logits[r] / temp) for R rows (ssmoe_sample_rows, the proposal of the p/q round; no reference
+ * counterpart), with the p/q round's row statistics: the chunk by descend() over the chunk masses r_c = s_c * a_c
+ * (k = ceil(nch / 64)) with target t = u_r * S, S their layout total; inside chunk cs the entry by descend() over its
+ * e values (k = 16) with target (t - base) / a_cs. A row with a non-finite logit yields an index in [0, V) of no
+ * meaning (the p/q round stops at that row). */
+void or_draw_rows(const float* logits, int R, int V, float temp, const float* uniforms, int32_t* tokens) {
+  const int nch = (V + CHUNK - 1) / CHUNK, kc = (nch + 63) / 64;
+  const float invT = pq_inv(temp);
+  PqRow* pr = (PqRow*)malloc(sizeof(PqRow));
+  for (int r = 0; r < R; ++r) {
+    const float* x = logits + (size_t)r * V;
+    pq_row(x, V, invT, pr);
+    float rc[PQ_MAX_NCH], L[64], P[64], e[CHUNK];
+    for (int c = 0; c < nch; ++c) rc[c] = pr->s[c] * pr->a[c];
+    lane_sums(rc, nch, kc, L);
+    scan64(L, P);
+    const float t = uniforms[r] * P[63];
+    float cbase = 0.0f, ebase = 0.0f;
+    const int cs = descend(rc, nch, kc, t, &cbase);
+    const int n_in = V - cs * CHUNK < CHUNK ? V - cs * CHUNK : CHUNK;
+    for (int i = 0; i < n_in; ++i) e[i] = pq_e(x, cs * CHUNK + i, invT, pr->m[cs]);
+    tokens[r] = cs * CHUNK + descend(e, n_in, SUB, (t - cbase) / pr->a[cs], &ebase);
+  }
+  free(pr);
 }
 
 /* Row total Z of the p/q rows at temperature temp (exposed for the sum-order tests). */

@@ -289,10 +289,10 @@ SS_DEV float wave_total(const float (&v)[KMAX], int k, int n) {
   return ss_readlane_f(wave_scan(L), 63);
 }
 
-// The search over a lane layout for target t (whole wave, uniform result): the first lane whose prefix exceeds t
-// (else the last lane with a nonzero local sum, else lane 0), then inside it the first value whose running sum from
-// the lane's exclusive prefix exceeds t (else its last nonzero value, else its first); *base receives the running
-// sum before the chosen value. Returns the value's index, at most n - 1.
+// The search over a lane layout for target t (whole wave, uniform result): the first lane holding values whose
+// prefix exceeds t (else the last lane with a nonzero local sum, else lane 0), then inside it the first value whose
+// running sum from the lane's exclusive prefix exceeds t (else its last nonzero value, else its first); *base
+// receives the running sum before the chosen value. Returns the value's index, at most n - 1.
 template <int KMAX>
 SS_DEV int wave_descend(const float (&v)[KMAX], int k, int n, float t, float* base) {
   const int lane = threadIdx.x & 63;
@@ -301,7 +301,7 @@ SS_DEV int wave_descend(const float (&v)[KMAX], int k, int n, float t, float* ba
   for (int i = 0; i < KMAX; ++i)
     if (i < k && k * lane + i < n) L = L + v[i];
   const float P = wave_scan(L);
-  const uint64_t gt = __ballot(P > t);
+  const uint64_t gt = __ballot(P > t && k * lane < n);  // lanes holding values only
   int ls;
   if (gt) {
     ls = __builtin_ctzll(gt);
@@ -1026,6 +1026,147 @@ __global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
     pick = cs * kChunk + wave_descend(vt, kSub, n_in, t - cbase, &ebase);
   }
   if (lane == 0) pq_write_out(a, st, s_dr, pick, flags);
+}
+
+// ---------------------------------------------------------------- draws from softmax(x / T)
+// The proposal draw of the p/q round (ssmoe_sample_rows), one persistent launch per group of rows whose (row, chunk)
+// units have a wave each: the chunk parts as in the p/q round (tagged words), the row statistics in every
+// workgroup, then each row's chunk by wave_descend over the chunk masses r_c = s_c a_c (one rounding) and, in the
+// wave holding the chosen chunk, the entry by wave_descend over its e values (registers) with target
+// (t - base) / a_c. One hand-off in all. A row with a non-finite logit still yields an index in [0, V), of no meaning.
+int64_t draw_work_floats(int R, int V) {
+  const int nch = (V + kChunk - 1) / kChunk;
+  return kHeadFloats + (int64_t)R * nch * 7 + (int64_t)nch * 3 + 64;
+}
+
+struct DrawArgs {
+  const float* x;  // [R, V]
+  const float* u;  // [R]
+  int32_t* tokens;
+  float* work;
+  int* err;
+  int R, V;
+  float temperature;
+};
+
+constexpr int kDrawStage = 2048;  // R x nchp chunk parts staged per workgroup (R nch <= 1024, R <= 64)
+
+template <int KM>
+__global__ __launch_bounds__(256) void draw_rows_kernel(DrawArgs a, int units) {
+  __shared__ __attribute__((aligned(16))) float sv[kDrawStage], sm[kDrawStage], sb[kDrawStage], sc[kDrawStage];
+  __shared__ float mrow[64], zrow[64];
+  __shared__ int brow[64];
+  __shared__ uint32_t s_epoch;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int R = a.R, V = a.V, nch = nchunks_of(V), nchp = (nch + 15) & ~15;
+  const int kc = KM < kMaxPerLane ? KM : (nch + 63) >> 6;
+  const float invT = 1.0f / a.temperature;
+  Work k = work_of(a.work, R, nch);
+  const int gw = blockIdx.x * 4 + w;
+  const bool has = gw < units;
+  const int ui = has ? gw / nch : 0, c = has ? gw - ui * nch : 0;
+  const int j0 = c * kChunk + kSub * lane;
+  const bool vec = (V & 3) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0;
+  float v[kSub];
+  if (has) load16(a.x + (size_t)ui * V, j0, V, vec, v);
+  const float u = has ? a.u[ui] : 0.f;
+  if (tid == 0) s_epoch = (uint32_t)ld_ag(k.ctr + kEpochInt);
+  __syncthreads();
+  const uint32_t epoch = s_epoch;
+  const uint32_t tag = (epoch + 1u) & 0x7FFFFFFFu;
+  if (has) {
+    const ChunkPart pt = chunk_part(v, j0, V, invT);
+    if (lane == 0) {
+      const size_t o = (size_t)ui * nch + c;
+      st_ag(k.wd0 + o, tagged(tag | (pt.bad ? 0x80000000u : 0u), pt.m));
+      st_ag(k.wd1 + o, tagged(tag, pt.s));
+    }
+  }
+  // every workgroup polls every row's chunk words (R nch <= 1024: four pairs per thread)
+  const int n = R * nch;
+  uint64_t w0[4], w1[4];
+  for (int it = 0;; ++it) {
+    int ok = 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int i = tid + 256 * q;
+      w0[q] = i < n ? ld_ag(k.wd0 + i) : 0;
+      w1[q] = i < n ? ld_ag(k.wd1 + i) : 0;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (tid + 256 * q < n) ok &= tag_of(w0[q]) == tag && tag_of(w1[q]) == tag;
+    if (__syncthreads_and(ok)) break;
+    if (it >= kSpin) {
+      if (tid == 0) ss_raise(a.err, SS_ERR_TIMEOUT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  if (blockIdx.x == 0 && tid == 0) st_ag(k.ctr + kEpochInt, (int)(epoch + 1u));
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int i = tid + 256 * q;
+    if (i < n) {
+      const int r = i / nch, o = r * nchp + (i - r * nch);
+      sv[o] = sc[o] = val_of(w1[q]);
+      sm[o] = val_of(w0[q]);
+      sb[o] = (w0[q] >> 63) ? 1.f : 0.f;
+    }
+  }
+  __syncthreads();
+  for (int r0 = w; r0 < R; r0 += 8) {
+    const int rr[2] = {r0, r0 + 4};
+    rows_stats<2, KM>(sv, sm, sb, rr, r0 + 4 < R ? 2 : 1, nch, nchp, mrow, zrow, brow);
+  }
+  __syncthreads();
+  if (!has) return;
+  // the row's chunk: masses r_c = s_c a_c in the chunk layout
+  float rv[KM];
+#pragma unroll
+  for (int i = 0; i < KM; ++i) {
+    const int cc = kc * lane + i;
+    rv[i] = i < kc && cc < nch ? sc[ui * nchp + cc] * sv[ui * nchp + cc] : 0.f;
+  }
+  const float t = u * wave_total(rv, kc, nch);
+  float cbase;
+  const int cs = wave_descend(rv, kc, nch, t, &cbase);
+  if (c != cs) return;
+  const int n_in = V - cs * kChunk < kChunk ? V - cs * kChunk : kChunk;
+  float eb;
+  const int e = wave_descend(v, kSub, n_in, (t - cbase) / sv[ui * nchp + cs], &eb);
+  if (lane == 0) a.tokens[ui] = cs * kChunk + e;
+}
+
+hipError_t launch_draw_rows(const float* x, int R, int V, float temperature, const float* u, void* work,
+                            int32_t* tokens, int* err, hipStream_t st) {
+  const int nch = (V + kChunk - 1) / kChunk;
+  const int kc = (nch + 63) >> 6;
+  auto kern = kc == 1 ? draw_rows_kernel<1> : kc == 2 ? draw_rows_kernel<2> : kc == 3 ? draw_rows_kernel<3>
+            : kc == 4 ? draw_rows_kernel<4> : draw_rows_kernel<kMaxPerLane>;
+  KernelCfg cfg;
+  hipError_t e = kernel_cfg(reinterpret_cast<const void*>(kern), 256, 0, &cfg);
+  if (e != hipSuccess) return e;
+  // rows per launch: every unit a wave of a grid resident at once (one workgroup per CU at most)
+  const int cap = 4 * cfg.cus < kFastUnits ? 4 * cfg.cus : kFastUnits;
+  const int per = cap / nch < 64 ? cap / nch : 64;
+  if (cfg.per_cu < 1 || per < 1) return hipErrorInvalidConfiguration;
+  for (int r0 = 0; r0 < R; r0 += per) {
+    DrawArgs d;
+    d.R = R - r0 < per ? R - r0 : per;
+    d.V = V;
+    d.x = x + (size_t)r0 * V;
+    d.u = u + r0;
+    d.tokens = tokens + r0;
+    d.work = static_cast<float*>(work);
+    d.err = err;
+    d.temperature = temperature;
+    const int units = d.R * nch;
+    hipLaunchKernelGGL(kern, dim3((units + 3) / 4), dim3(256), 0, st, d, units);
+    e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_accept_greedy(const AcceptArgs& a, hipStream_t st) {

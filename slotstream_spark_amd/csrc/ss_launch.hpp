@@ -174,9 +174,12 @@ hipError_t launch_prefill_tables(const int32_t* map, int64_t map_base, int64_t m
 int64_t sample_workspace_bytes(int V);
 hipError_t launch_sample(const float* x, int V, const int32_t* gen, int n_gen, float temperature, float top_p,
                          int top_k, float min_p, float pp, const float* u, void* work, int32_t* out, hipStream_t st);
-// R rows drawn at once at temperature > 0 with no filter (the proposal draw of the p/q round): draws[r] = row r's token.
-hipError_t launch_sample_rows(const float* x, int R, int V, float temperature, const float* u, void* work,
-                             int32_t* draws, hipStream_t st);
+// The proposal draw of the p/q round (ss_accept.hip): tokens[r] ~ softmax(x[r] / temperature) with u[r], R rows in
+// as few persistent launches as a resident grid allows; the workspace holds draw_work_floats(R, V) floats, zeroed
+// before its first use.
+int64_t draw_work_floats(int R, int V);
+hipError_t launch_draw_rows(const float* x, int R, int V, float temperature, const float* u, void* work,
+                            int32_t* tokens, int* err, hipStream_t st);
 hipError_t launch_accept_sampled(const float* target, const int32_t* drafts, int D, int V, const int32_t* seen,
                                  int n_seen, float temperature, float top_p, int top_k, float min_p, float pp,
                                  const float* uniforms, void* work, int32_t* out, hipStream_t st);

@@ -133,7 +133,6 @@ struct SampArgs {
   int top_k;
   const float* u;  // [R]
   int32_t* out;    // single row: [2] (token, flags); accept mode: [R + 4]
-  int32_t* draws;  // rows mode: [R], the token of each row (no flags)
   int accept;
   void* work;
 };
@@ -795,9 +794,7 @@ __global__ __launch_bounds__(64) void samp_draw_kernel(SampArgs a) {
   const int nch = a.nch;
   auto finish = [&](int tok, int fb, int nonfinite) {
     if (lane != 0) return;
-    if (a.draws) {
-      a.draws[row] = tok;
-    } else if (a.accept) {
+    if (a.accept) {
       w.res[0] = tok;
       w.res[1] = fb;
       w.res[2] = nonfinite;
@@ -991,16 +988,6 @@ hipError_t launch_sample(const float* x, int V, const int32_t* gen, int n_gen, f
   a.x = x;
   a.u = u;
   a.out = out;
-  launch_rows(a, st);
-  return hipGetLastError();
-}
-
-hipError_t launch_sample_rows(const float* x, int R, int V, float temperature, const float* u, void* work,
-                             int32_t* draws, hipStream_t st) {
-  SampArgs a = args_of(V, R, nullptr, 0, temperature, 1.f, 0, 0.f, 0.f, work);
-  a.x = x;
-  a.u = u;
-  a.draws = draws;
   launch_rows(a, st);
   return hipGetLastError();
 }

@@ -850,18 +850,25 @@ int ssmoe_bench_mfma_bf16(const uint32_t* seed, int iters, float* out, int grid,
 
 int64_t ssmoe_sample_rows_workspace_bytes(int R, int V) {
   if (R < 1 || R > 64 || V < 1 || V > (1 << 20)) return -1;
-  return (int64_t)R * ss::sample_workspace_bytes(V);
+  return ss::draw_work_floats(R, V) * 4;
 }
 
 int ssmoe_sample_rows(const float* logits, int R, int V, float temperature, const float* uniforms, void* workspace,
                       int64_t workspace_bytes, int32_t* tokens, void* stream) {
   if (R < 1 || R > 64) return fail(SSMOE_EINVAL, "R must be in [1, 64], got %d", R);
+  if (V < 1 || V > (1 << 20)) return fail(SSMOE_EINVAL, "V must be in [1, 1048576], got %d", V);
   if (!(temperature > 0.f) || temperature > 3.4e38f)
     return fail(SSMOE_EINVAL, "temperature must be finite and > 0 (a proposal is drawn, not taken as the argmax)");
-  if (int rc = check_sample(V, temperature, 1.f, 0, 0.f, 0.f, nullptr, 0, workspace, workspace_bytes, R)) return rc;
-  if (!logits || !uniforms || !tokens) return fail(SSMOE_EINVAL, "logits, uniforms and tokens must be non-null");
-  return hip_check(ss::launch_sample_rows(logits, R, V, temperature, uniforms, workspace, tokens,
-                                          static_cast<hipStream_t>(stream)),
+  if (!logits || !uniforms || !tokens || !workspace)
+    return fail(SSMOE_EINVAL, "logits, uniforms, tokens and workspace must be non-null");
+  if (!aligned(workspace, 256)) return fail(SSMOE_EINVAL, "workspace must be 256-byte aligned");
+  if (workspace_bytes < ss::draw_work_floats(R, V) * 4)
+    return fail(SSMOE_EINVAL, "workspace holds %lld bytes, need %lld", (long long)workspace_bytes,
+                (long long)(ss::draw_work_floats(R, V) * 4));
+  int* err = nullptr;
+  if (int rc = status_ptr(&err)) return rc;
+  return hip_check(ss::launch_draw_rows(logits, R, V, temperature, uniforms, workspace, tokens, err,
+                                        static_cast<hipStream_t>(stream)),
                    "sample rows launch");
 }
 

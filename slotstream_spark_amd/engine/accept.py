@@ -113,8 +113,8 @@ class Acceptor:
 
     def draw_drafts_async(self, draft, uniforms, temperature: float, out=None) -> torch.Tensor:
         """x_i ~ softmax(draft[i] / temperature) for the D draft rows with uniforms[i] (fp32 [D] on the device) ->
-        int32 [D] on the device: the proposal of the p/q round (ssmoe_sample_rows, the reference sampler's draw with
-        no filter)."""
+        int32 [D] on the device: the proposal of the p/q round (ssmoe_sample_rows: the p/q round's softmax in one
+        launch; the draw is exact in distribution, its bits are or_draw_rows', not the reference sampler's)."""
         d, v = self.depth, self.vocab
         if draft.dtype != torch.float32 or tuple(draft.shape) != (d, v) or not draft.is_contiguous():
             raise ValueError(f"draft must be contiguous fp32 [{d}, {v}]")
@@ -129,7 +129,7 @@ class Acceptor:
             return out
         if self._dwork is None:
             nb = int(_lib.lib().ssmoe_sample_rows_workspace_bytes(d, v))
-            self._dwork = torch.empty(nb, dtype=torch.uint8, device=draft.device)
+            self._dwork = torch.zeros(nb, dtype=torch.uint8, device=draft.device)  # zero before the first call
         _lib.check(_lib.lib().ssmoe_sample_rows(draft.data_ptr(), d, v, float(temperature), uniforms.data_ptr(),
                                                 self._dwork.data_ptr(), self._dwork.numel(), out.data_ptr(),
                                                 _lib.stream_of(draft)))

@@ -138,14 +138,30 @@ def test_pq_launch_forms(d, v, seed):
 
 @pytest.mark.parametrize("seed", range(4))
 def test_draw_drafts_bitexact(acc, seed):
-    """The proposal draw of the p/q round (ssmoe_sample_rows): row i's token is the reference sampler's draw at the
-    round's temperature with no filter and uniforms[i], bit for bit against the C definition."""
+    """The proposal draw of the p/q round (ssmoe_sample_rows): row i's token is x ~ softmax(draft_i / T) with
+    uniforms[i], bit for bit against the C definition (or_draw_rows); a second call on the same workspace too."""
     _, drf = verify_logits(D, V, 7000 + seed)
     u = UniformStream(100 + seed).peek(D)
-    got = acc.draw_drafts_async(drf, torch.from_numpy(u).cuda(), 0.7).cpu().numpy()
-    q = drf.cpu().numpy()
-    want = [O.sample(q[i], [], 0.7, 1.0, 0, 0.0, 0.0, u[i])[0] for i in range(D)]
-    assert got.tolist() == want
+    want = O.draw_rows(drf.cpu().numpy(), 0.7, u).tolist()
+    for _ in range(2):
+        assert acc.draw_drafts_async(drf, torch.from_numpy(u).cuda(), 0.7).cpu().tolist() == want
+
+
+@pytest.mark.parametrize("r,v,seed", [(16, 151936, 1), (64, 4096, 2), (5, 100003, 3), (2, 400000, 4), (1, 37, 5)])
+def test_draw_rows_shapes(r, v, seed):
+    """ssmoe_sample_rows at other shapes, bit for bit against or_draw_rows: 16 rows of 149 chunks run as three launches
+    of at most six rows (every (row, chunk) unit a wave of a resident grid), 64 rows of four chunks in one; V = 100,003
+    ends in a partial chunk of rows that are not 16-byte aligned; V = 400,000 has 391 chunks (seven per lane of the
+    chunk layout, the generic build); V = 37 has one partial chunk."""
+    x = torch.randn((r, v), generator=torch.Generator(device="cuda").manual_seed(seed), device="cuda") * 3.0
+    u = np.random.default_rng(seed).random(r).astype(np.float32)
+    ws = torch.zeros(int(_lib.lib().ssmoe_sample_rows_workspace_bytes(r, v)), dtype=torch.uint8, device="cuda")
+    out = torch.empty(r, dtype=torch.int32, device="cuda")
+    want = O.draw_rows(x.cpu().numpy(), 0.7, u).tolist()
+    for _ in range(2):
+        _lib.check(_lib.lib().ssmoe_sample_rows(x.data_ptr(), r, v, 0.7, torch.from_numpy(u).cuda().data_ptr(),
+                                                ws.data_ptr(), ws.numel(), out.data_ptr(), _lib.stream_of(x)))
+        assert out.cpu().tolist() == want
 
 
 def _chi2(counts, probs):

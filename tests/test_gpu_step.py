@@ -273,7 +273,7 @@ def test_pq_round_in_the_step_graph(step):
         ud = torch.rand(3, generator=g, device="cuda")
         drafts = pq.draw_drafts(ud).clone()
         ql, un = pq.draft_logits.cpu().numpy(), ud.cpu().numpy()
-        assert drafts.cpu().tolist() == [O.sample(ql[i], [], 0.7, 1.0, 0, 0.0, 0.0, un[i])[0] for i in range(3)]
+        assert drafts.cpu().tolist() == O.draw_rows(ql, 0.7, un).tolist()
         out = pq.step(x, drafts).clone()
         torch.cuda.synchronize()
         assert torch.equal(pq.logits, sg.logits), rep
