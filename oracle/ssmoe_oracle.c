@@ -321,9 +321,10 @@ static float chunk_total(ValFn f, const void* ctx, int c, int V, float* sub /* [
  * The drafts: x_i is accepted iff u_i * q_i(x_i) < p_i(x_i) (p, q of target row i and draft row i); the first
  * rejection samples from v_j = max(0, p_j - q_j) of row i, and every draft accepted from v_j = p_j of row D. A
  * non-finite logit in a row the round reaches stops it; a draft outside [0, V) is flagged and rejected.
- * The sample: r_c = total64 of the chunk's sub-chunk sums of v; S = total64 of r_c in the chunk lane layout;
- * target u * S. descend() on the chunk layout gives the chunk cs and its base b; descend() on chunk cs's
- * sub-chunks with target (u * S - b) gives the entry. */
+ * The sample after a rejection: r_c = total64 of the chunk's sub-chunk sums of v; S = total64 of r_c in the chunk
+ * lane layout; target u * S. descend() on the chunk layout gives the chunk cs and its base b; descend() on chunk cs's
+ * sub-chunks with target (u * S - b) gives the entry. With every draft accepted, the sample from p_D is drawn as
+ * or_draw_rows draws: the chunk by its mass r_c = s_c * a_c, the entry by its e with target (u * S - b) / a_cs. */
 #define PQ_MAX_NCH 1024
 
 static void scan64(const float* L, float* P) {
@@ -444,8 +445,8 @@ void or_accept_pq(const float* target, const float* draft, const int32_t* drafts
   (void)work;
   const int nch = (V + CHUNK - 1) / CHUNK, kc = (nch + 63) / 64;
   const float invT = pq_inv(temp);
-  PqRow* rt = (PqRow*)malloc(sizeof(PqRow) * (size_t)(D + 1));
-  PqRow* rd = (PqRow*)malloc(sizeof(PqRow) * (size_t)(D > 0 ? D : 1));
+  PqRow* rt = (PqRow*)calloc((size_t)(D + 1), sizeof(PqRow));
+  PqRow* rd = (PqRow*)calloc((size_t)(D > 0 ? D : 1), sizeof(PqRow));
   for (int i = 0; i <= D; ++i) pq_row(target + (size_t)i * V, V, invT, &rt[i]);
   for (int i = 0; i < D; ++i) pq_row(draft + (size_t)i * V, V, invT, &rd[i]);
   int good = 0, flags = 0, stop = 0, srow = D, sdraft = -1;
@@ -479,9 +480,23 @@ void or_accept_pq(const float* target, const float* draft, const int32_t* drafts
   const int uidx = good + (sdraft >= 0 ? 1 : 0);
   for (int i = 0; i < good; ++i) out[4 + i] = drafts[i];
   int emit = good;
-  if (!stop) {
+  if (!stop && sdraft < 0) {
+    const PqRow* pr = &rt[D];
+    const float* x = target + (size_t)D * V;
+    float rc[PQ_MAX_NCH], L[64], P[64], e[CHUNK];
+    for (int c = 0; c < nch; ++c) rc[c] = pr->s[c] * pr->a[c];
+    lane_sums(rc, nch, kc, L);
+    scan64(L, P);
+    if (!(P[63] > 0.0f)) flags |= 4;
+    const float tu = uniforms[uidx] * P[63];
+    float cbase = 0.0f, ebase = 0.0f;
+    const int cs = descend(rc, nch, kc, tu, &cbase);
+    const int n_in = V - cs * CHUNK < CHUNK ? V - cs * CHUNK : CHUNK;
+    for (int i = 0; i < n_in; ++i) e[i] = pq_e(x, cs * CHUNK + i, invT, pr->m[cs]);
+    out[4 + emit++] = cs * CHUNK + descend(e, n_in, SUB, (tu - cbase) / pr->a[cs], &ebase);
+  } else if (!stop) {
     const float* tp = target + (size_t)srow * V;
-    const float* dq = sdraft >= 0 ? draft + (size_t)sdraft * V : NULL;
+    const float* dq = draft + (size_t)sdraft * V;
     float* v = (float*)malloc(sizeof(float) * (size_t)nch * CHUNK);
     float r[PQ_MAX_NCH];
     for (int c = 0; c < nch; ++c) {
@@ -489,13 +504,8 @@ void or_accept_pq(const float* target, const float* draft, const int32_t* drafts
         const int j = c * CHUNK + i;
         float x = 0.0f;
         if (j < V) {
-          const float p = pq_p(tp, j, invT, &rt[srow]);
-          if (dq) {
-            const float d = p - pq_p(dq, j, invT, &rd[sdraft]);
-            x = d > 0.0f ? d : 0.0f;
-          } else {
-            x = p;
-          }
+          const float d = pq_p(tp, j, invT, &rt[srow]) - pq_p(dq, j, invT, &rd[sdraft]);
+          x = d > 0.0f ? d : 0.0f;
         }
         v[(size_t)c * CHUNK + i] = x;
       }

@@ -1,12 +1,13 @@
 """Phase trace of the one-launch p/q acceptance round (ssmoe_accept_pq) through ssmoe_set_trace.
 
-    python -m slotstream_spark_amd.accept_trace [D] [V]
+    python -m slotstream_spark_amd.accept_trace [D] [V] [bonus]
 
 Runs BASELINE config 2's round (depth D = 3, vocab V = 151,936, temperature 0.7) on seeded synthetic logits with
 drafts drawn from q, times 200 rounds in one HIP graph (HIP events; the greedy round on the same target rows
 likewise), then runs one eager round with the trace on and
 prints, for every stamp, the median and maximum over the workgroups that wrote it, in us from the first workgroup
-start. Stamps 0-6 are per workgroup; 8-11 come from the waves that hold a chunk of the sampled row.
+start. Stamps 0-6 are per workgroup; 8-11 come from the waves that hold a chunk of the sampled row. With bonus = 1 the
+draft rows equal the target rows, so every draft is accepted and the bonus row is sampled.
 """
 from __future__ import annotations
 
@@ -24,9 +25,11 @@ NAMES = [(0, "start"), (12, "logits loaded"), (13, "target chunk part"), (1, "ch
          (10, "chunk of the sample found"), (11, "round written"), (6, "workgroup done")]
 
 
-def run(D: int = 3, V: int = 151936, temp: float = 0.7) -> str:
+def run(D: int = 3, V: int = 151936, bonus: int = 0, temp: float = 0.7) -> str:
     acc = Acceptor(D, V)
     tgt, drf = verify_logits(D, V, 4242)
+    if bonus:
+        drf = tgt[:D].contiguous()
     u = torch.from_numpy(UniformStream(7).peek(D + 1)).cuda()
     drafts = acc.draw_drafts_async(drf, u[:D].contiguous(), temp)
     for _ in range(20):

@@ -256,10 +256,12 @@ __global__ __launch_bounds__(64) void greedy_kernel(AcceptArgs a) {
 // Two forms, the same bits: pq_round_kernel, one persistent launch, when every unit (target row i with draft row i,
 // or the bonus target row D, over one chunk) has a wave of a resident grid: the unit's e values stay in registers;
 // the chunk parts are published as tagged words, which every workgroup polls directly (no counter) before it forms
-// the row statistics and the decision itself; the waves of the sampled row form its values and publish their chunk
-// totals the same way; every such wave finds the chunk of the sample and the wave holding it finds the entry.
-// Otherwise two launches: pq_sum_kernel (chunk parts; the last workgroup decides) and pq_residual_kernel (chunk
-// totals of the sampled values; the last workgroup searches).
+// the row statistics and the decision itself; after a rejection the waves of the sampled row form its values and
+// publish their chunk totals the same way, every such wave finds the chunk of the sample and the wave holding it
+// finds the entry; with every draft accepted the bonus row is sampled as the proposal draw samples (chunk by its mass
+// s_c a_c, entry by e against (t - base) / a_c), with no second hand-off. Otherwise two launches: pq_sum_kernel
+// (chunk parts; the last workgroup decides) and pq_residual_kernel (chunk totals of the sampled values; the last
+// workgroup searches).
 
 // DPP (GFX9 encodings): row_shr:d = 0x110 + d reads lane l - d of the same row (0 past the row's start, bound_ctrl);
 // row_bcast:15 = 0x142 gives rows 1 and 3 (row_mask 0xA) lane 15 / 47; row_bcast:31 = 0x143 gives rows 2 and 3
@@ -652,7 +654,7 @@ constexpr int kFastStage = 2 * kFastUnits + 15 * kMaxRows;  // rows x nchp chunk
 
 template <int KM>
 __global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) {
-  __shared__ __attribute__((aligned(16))) float sv[kFastStage], sm[kFastStage], sb[kFastStage];
+  __shared__ __attribute__((aligned(16))) float sv[kFastStage], sm[kFastStage], sb[kFastStage], sc[kFastStage];
   __shared__ float mrow[kMaxRows], zrow[kMaxRows];
   __shared__ int brow[kMaxRows];
   __shared__ PqIn s_in;
@@ -749,7 +751,7 @@ __global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) 
       const int i = tid + 256 * q;
       if (i < n) {
         const int r = i / nch, o = r * nchp + (i - r * nch);
-        sv[o] = val_of(w1[q]);
+        sv[o] = sc[o] = val_of(w1[q]);
         sm[o] = val_of(w0[q]);
         sb[o] = (w0[q] >> 63) ? 1.f : 0.f;
       }
@@ -779,12 +781,34 @@ __global__ __launch_bounds__(256) void pq_round_kernel(AcceptArgs a, int units) 
   const PqState st = s_st;
   if (st.stop) {
     if (blockIdx.x == 0 && tid == 0) pq_write_out(a, st, s_in.x, -1, st.flags);
-  } else if (has && ui == (st.srow < D ? st.srow : D)) {
-    // phase 3: the sampled row's values (in place of vt) and this chunk's total
-    const bool rej = st.sdraft >= 0;
-    const float at = sv[st.srow * nchp + c], ad = rej ? sv[st.sdraft * nchp + c] : 0.f;
+  } else if (has && ui == D && st.sdraft < 0) {
+    // every draft accepted: the bonus row's sample as the proposal draw takes it (chunk by mass s_c a_c, then the
+    // entry from the holding wave's e values), with no second hand-off
+    float rv[KM];
 #pragma unroll
-    for (int e = 0; e < kSub; ++e) vt[e] = j0 + e < V ? sampled_value(vt[e], vd[e], at, ad, rej) : 0.f;
+    for (int i = 0; i < KM; ++i) {
+      const int cc = kc * lane + i;
+      rv[i] = i < kc && cc < nch ? sc[D * nchp + cc] * sv[D * nchp + cc] : 0.f;
+    }
+    int flags = st.flags;
+    const float S = wave_total(rv, kc, nch);
+    if (!(S > 0.f)) flags |= FLAG_RESIDUAL_EMPTY;
+    const float t = s_in.u[st.uidx] * S;
+    float cbase;
+    const int cs = wave_descend(rv, kc, nch, t, &cbase);
+    PQ_TRACE(10, lane == 0);
+    if (c == cs) {
+      const int n_in = V - cs * kChunk < kChunk ? V - cs * kChunk : kChunk;
+      float ebase;
+      const int e = wave_descend(vt, kSub, n_in, (t - cbase) / sv[D * nchp + cs], &ebase);
+      if (lane == 0) pq_write_out(a, st, s_in.x, cs * kChunk + e, flags);
+      PQ_TRACE(11, lane == 0);
+    }
+  } else if (has && ui == st.srow && st.sdraft >= 0) {
+    // phase 3: the sampled row's values (in place of vt) and this chunk's total
+    const float at = sv[st.srow * nchp + c], ad = sv[st.sdraft * nchp + c];
+#pragma unroll
+    for (int e = 0; e < kSub; ++e) vt[e] = j0 + e < V ? sampled_value(vt[e], vd[e], at, ad, true) : 0.f;
     const float ct = wave_total(vt, kSub, kChunk);
     if (lane == 0) st_ag(k.wr + c, tagged(tag, ct));
     PQ_TRACE(8, lane == 0);
@@ -972,10 +996,16 @@ __global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
   const bool rej = st.sdraft >= 0;
   const float* xt = a.target + (size_t)st.srow * V;
   const float* xd = rej ? a.draft + (size_t)(st.sdraft - D - 1) * V : xt;
-  if (!st.stop) {
+  if (!st.stop && !rej) {
+    // every draft accepted: the chunk's mass s_c a_c (the proposal draw's form)
+    if (tid == 0) {
+      const float mt = ld_ag(k.cmax + (size_t)st.srow * nch + c);
+      st_ag(k.rtot + c, ld_ag(k.ctot + (size_t)st.srow * nch + c) * (ss_expf_le0(mt - st.ms) / st.zs));
+    }
+  } else if (!st.stop) {
     const float mt = ld_ag(k.cmax + (size_t)st.srow * nch + c);
-    const float md = rej ? ld_ag(k.cmax + (size_t)st.sdraft * nch + c) : 0.f;
-    const float at = ss_expf(mt - st.ms) / st.zs, ad = rej ? ss_expf(md - st.md) / st.zd : 0.f;
+    const float md = ld_ag(k.cmax + (size_t)st.sdraft * nch + c);
+    const float at = ss_expf_le0(mt - st.ms) / st.zs, ad = ss_expf_le0(md - st.md) / st.zd;
 #pragma unroll
     for (int ii = 0; ii < kSub / 4; ++ii) {
       const int e = (w * (kSub / 4) + ii) * 64 + lane;
@@ -987,7 +1017,7 @@ __global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
   }
   __syncthreads();
   if (w != 0) return;
-  if (!st.stop) {
+  if (!st.stop && rej) {
     float s = 0.f;
     for (int i = 0; i < kSub; ++i) s = s + lds[lane * (kSub + 1) + i];
     s = ss_readlane_f(wave_scan(s), 63);
@@ -1010,20 +1040,22 @@ __global__ __launch_bounds__(256) void pq_residual_kernel(AcceptArgs a) {
     const float t = a.uniforms[st.uidx] * S;
     float cbase;
     const int cs = wave_descend(rv, kc, nch, t, &cbase);
-    // the values of chunk cs, lane l holding entries 16 l .. 16 l + 15
+    // the values of chunk cs, lane l holding entries 16 l .. 16 l + 15: the sampled values after a rejection, e
+    // (against (t - base) / a_cs) with every draft accepted
     const float mt = ld_ag(k.cmax + (size_t)st.srow * nch + cs);
     const float md = rej ? ld_ag(k.cmax + (size_t)st.sdraft * nch + cs) : 0.f;
-    const float at = ss_expf(mt - st.ms) / st.zs, ad = rej ? ss_expf(md - st.md) / st.zd : 0.f;
+    const float at = ss_expf_le0(mt - st.ms) / st.zs, ad = rej ? ss_expf_le0(md - st.md) / st.zd : 0.f;
     const int j0 = cs * kChunk + kSub * lane;
     float vt[kSub];
 #pragma unroll
     for (int e = 0; e < kSub; ++e) {
       const int j = j0 + e;
-      vt[e] = j < V ? sampled_value(e_of(xt[j], invT, mt), rej ? e_of(xd[j], invT, md) : 0.f, at, ad, rej) : 0.f;
+      const float et = j < V ? e_of(xt[j], invT, mt) : 0.f;
+      vt[e] = !rej ? et : j < V ? sampled_value(et, e_of(xd[j], invT, md), at, ad, true) : 0.f;
     }
     const int n_in = V - cs * kChunk < kChunk ? V - cs * kChunk : kChunk;
     float ebase;
-    pick = cs * kChunk + wave_descend(vt, kSub, n_in, t - cbase, &ebase);
+    pick = cs * kChunk + wave_descend(vt, kSub, n_in, rej ? t - cbase : (t - cbase) / at, &ebase);
   }
   if (lane == 0) pq_write_out(a, st, s_dr, pick, flags);
 }

@@ -134,6 +134,12 @@ def test_pq_launch_forms(d, v, seed):
     for _ in range(2):  # a second call on the same workspace: the counters were left at zero
         out = small.pq_async(tgt, drf, torch.from_numpy(dr).cuda(), torch.from_numpy(u).cuda(), 0.7).cpu().numpy()
         assert np.array_equal(out, O.accept_pq(t, q, dr, u, 0.7)), out
+    if d:
+        # q = p: every draft accepted, the bonus row sampled (its own form, without the residual pass)
+        same = tgt[:d].contiguous()
+        out = small.pq_async(tgt, same, torch.from_numpy(dr).cuda(), torch.from_numpy(u).cuda(), 0.7).cpu().numpy()
+        assert np.array_equal(out, O.accept_pq(t, t[:d], dr, u, 0.7)), out
+        assert out[0] == d and out[1] == d + 1
 
 
 @pytest.mark.parametrize("seed", range(4))
