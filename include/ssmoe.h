@@ -418,6 +418,45 @@ int ssmoe_rmsnorm(const uint16_t* x, const uint16_t* w, float eps, int R, int n,
 int ssmoe_dense_gemv_epi(const uint16_t* x, int R, int K, const uint16_t* w, int N, int epi, int hc,
                          const uint16_t* add, int add_div, uint16_t* out, void* stream);
 
+/* One launch for a run of the head's dense ops, with the bits of the separate calls (ssmoe_gather_rows,
+ * ssmoe_hc_inject, ssmoe_rmsnorm, ssmoe_dense_gemv_epi, ssmoe_hc_mean): the steps of engine/mtp.py:184-227 and
+ * model/layers.py:190-198 between two head MoE / lm_head calls. No reference counterpart as one call.
+ *   source: S rows of n (bf16 [S][n] at src), or rows src_idx[s] of the table src [n_src][n] (src_idx int32 on the
+ *     device; an index outside [0, n_src) reads zeros and raises SSMOE_ERR_TOKEN);
+ *   inject (inj non-null): h = bf16(src + bf16(inj_y[s][j % (n / inj_hc)] * inj[s][j / (n / inj_hc)]));
+ *   norm (group > 0): x = ssmoe_rmsnorm(h, norm_w, eps, group) (norm_w NULL: 1);
+ *   the GEMV of ssmoe_dense_gemv_epi over x viewed as S n / K rows of K: weight rows w [N][K] with epi, hc, add,
+ *     add_div into out, and rows w2 [N2][K] with epi2 into out2 (N2 may be 0);
+ *   or, with mean_out non-null (hc == 4, N = 4 H, no w2): also mean_out [S][H] = ssmoe_hc_mean(out, mean_hn, 4).
+ *   h_out / x_out (bf16 [S][n], or NULL) receive h and x.
+ * n a multiple of K and of group, K and n multiples of 8, n <= 32768, n / K <= 4, n / group <= 64; pointers
+ * 16-byte aligned. */
+typedef struct {
+  const uint16_t* src;
+  const int32_t* src_idx;
+  int64_t n_src;
+  const uint16_t* inj_y;
+  const uint16_t* inj;
+  int inj_hc;
+  const uint16_t* norm_w;
+  float eps;
+  int group;
+  int S, n, K;
+  const uint16_t* w;
+  int N, epi, hc;
+  const uint16_t* add;
+  int add_div;
+  uint16_t* out;
+  const uint16_t* w2;
+  int N2, epi2;
+  uint16_t* out2;
+  uint16_t* h_out;
+  uint16_t* x_out;
+  const uint16_t* mean_hn;
+  uint16_t* mean_out;
+} ssmoe_head_gemv_args;
+int ssmoe_head_gemv(const ssmoe_head_gemv_args* a, void* stream);
+
 /* The weighted mean of hc_mix (model/layers.py:195): mixed[s][j] = bf16(sum_c bf16(m[s][c H + j] hn[s][c H + j]) /
  * hc), the sum over c = 0 .. hc-1 in order. m, hn bf16 [S][hc H]; mixed bf16 [S][H]. */
 int ssmoe_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed, void* stream);

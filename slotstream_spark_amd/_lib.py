@@ -82,6 +82,7 @@ SIGNATURES = {
     "ssmoe_rmsnorm": (_I, [_P, _P, _F, _I, _I, _I, _P, _P]),
     "ssmoe_dense_gemv_epi": (_I, [_P, _I, _I, _P, _I, _I, _I, _P, _I, _P, _P]),
     "ssmoe_hc_mean": (_I, [_P, _P, _I, _I, _I, _P, _P]),
+    "ssmoe_head_gemv": (_I, [_P, _P]),
     "ssmoe_hc_inject": (_I, [_P, _P, _P, _I, _I, _I, _P, _P]),
     "ssmoe_gather_rows": (_I, [_P, _I64, _I64, _P, _I, _I, _P, _P]),
 }

@@ -167,6 +167,185 @@ __global__ __launch_bounds__(256) void dense_epi_kernel(DenseEpiArgs a) {
   if (lane < a.R) a.out[(size_t)lane * a.N + n] = (uint16_t)epilogue(mine, a, lane, n);
 }
 
+// ---------------------------------------------------------------- the fused head GEMV
+// One launch for what the head otherwise runs as a row gather, hc_inject, an RMSNorm and one or two GEMVs, or a GEMV
+// and the branch mean, with the same bits as those kernels (the same operations in the same order):
+//   pre-step, in every workgroup: the launch's source rows (src rows, or table rows src_idx[s]) into LDS; optionally
+//   h = bf16(src + bf16(y[s][j % Hy] * inj[s][j / Hy])) (hc_inject); optionally x = bf16((h * r_g) * norm_w) with
+//   r_g = 1 / sqrt(sum over group g of h^2 / G + eps), the sum in rmsnorm_groups_kernel's order (one wave per group:
+//   lane l over the 8-element chunks l, l + 64, .. with fmaf from 0, then the xor butterfly); workgroup 0 writes h
+//   and x out when asked;
+//   then the GEMV of dense_epi_kernel over x viewed as R = Sl n / K rows of K (x from LDS): weight rows [0, N) of w
+//   with epilogue epi into out, rows [N, N + N2) of w2 with epi2 into out2;
+//   or, with mean_out, the branch mean of hc_mean_kernel fused behind the GEMV (hc == 4): workgroup j takes weight
+//   rows c H + j (wave c), and mean_out[r][j] = bf16((sum over c of bf16(v_c * mean_hn[r][c H + j])) / hc).
+struct HeadGemvArgs {
+  const uint16_t* src;
+  const int32_t* src_idx;
+  int64_t n_src;
+  const uint16_t* inj_y;
+  const uint16_t* inj;
+  int inj_hc;
+  const uint16_t* norm_w;
+  float eps;
+  int G;
+  int Sl, n, K;  // this launch's source rows, their width, the GEMV's K
+  DenseEpiArgs g;  // w, out, add, N, epi, hc, row0, add_div (x and R are set by the kernel)
+  const uint16_t* w2;
+  int N2, epi2;
+  uint16_t* out2;
+  uint16_t* h_out;
+  uint16_t* x_out;
+  const uint16_t* mean_hn;
+  uint16_t* mean_out;
+  int mean_H;
+  int* err;
+};
+
+constexpr int kHeadLds = 4 * 8192;  // bf16 elements of the staged source rows (Sl n <= 32768)
+
+__global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
+  __shared__ uint4 xs[kHeadLds / 8];
+  __shared__ float rs[64];
+  __shared__ uint32_t mw[4][kDR];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n = a.n, E = a.Sl * n, E8 = E >> 3;
+  // pre-step 1: the source rows (and the injection) into LDS, h out from workgroup 0
+  for (int i = tid; i < E8; i += 256) {
+    const int s = (i << 3) / n, j8 = (i << 3) - s * n;
+    int64_t row = s;
+    if (a.src_idx) {
+      row = a.src_idx[s];
+      if (row < 0 || row >= a.n_src) {
+        if (j8 == 0) ss_raise(a.err, SS_ERR_TOKEN);
+        row = -1;
+      }
+    }
+    uint4 v = row >= 0 ? reinterpret_cast<const uint4*>(a.src + row * n)[j8 >> 3] : make_uint4(0u, 0u, 0u, 0u);
+    if (a.inj) {
+      const int Hy = n / a.inj_hc, c = j8 / Hy;
+      const uint4 yv = reinterpret_cast<const uint4*>(a.inj_y + (size_t)s * Hy)[(j8 - c * Hy) >> 3];
+      const float g = ss_bf16_to_f32(a.inj[s * a.inj_hc + c]);
+      const uint32_t hv[4] = {v.x, v.y, v.z, v.w}, yy[4] = {yv.x, yv.y, yv.z, yv.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float t0 = ss_round_bf16(lo16(yy[q]) * g), t1 = ss_round_bf16(hi16(yy[q]) * g);
+        o[q] = ss_f32_to_bf16(lo16(hv[q]) + t0) | (ss_f32_to_bf16(hi16(hv[q]) + t1) << 16);
+      }
+      v = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+    xs[i] = v;
+    if (a.h_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.h_out)[i] = v;
+  }
+  __syncthreads();
+  if (a.G > 0) {
+    // pre-step 2: r of every group (one wave per group, rmsnorm_groups_kernel's order)
+    const int ng = E / a.G, g8 = a.G >> 3;
+    for (int g = w; g < ng; g += 4) {
+      float acc = 0.f;
+      for (int k8 = lane; k8 < g8; k8 += 64) {
+        const uint4 q = xs[g * g8 + k8];
+        const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float e0 = lo16(v[c]), e1 = hi16(v[c]);
+          acc = fmaf(e0, e0, acc);
+          acc = fmaf(e1, e1, acc);
+        }
+      }
+      const float r = 1.f / sqrtf(ss_wave_sum(acc) / (float)a.G + a.eps);
+      if (lane == 0) rs[g] = r;
+    }
+    __syncthreads();
+    // pre-step 3: x = bf16((h * r) * norm_w) in place, x out from workgroup 0
+    for (int i = tid; i < E8; i += 256) {
+      const int e = i << 3, g = e / a.G, j = e - (e / n) * n;
+      const float r = rs[g];
+      const uint4 q = xs[i];
+      const uint4 b = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w)[j >> 3]
+                               : make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+      const uint32_t v[4] = {q.x, q.y, q.z, q.w}, wv[4] = {b.x, b.y, b.z, b.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        o[c] = ss_f32_to_bf16((lo16(v[c]) * r) * lo16(wv[c])) | (ss_f32_to_bf16((hi16(v[c]) * r) * hi16(wv[c])) << 16);
+      const uint4 x = make_uint4(o[0], o[1], o[2], o[3]);
+      xs[i] = x;
+      if (a.x_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.x_out)[i] = x;
+    }
+    __syncthreads();
+  }
+  // the GEMV: one wave per weight row, the launch's x rows from LDS
+  const int R = E / a.K, k8n = a.K >> 3;
+  int nrow;
+  const uint16_t* wrow_base;
+  bool second = false;
+  if (a.mean_out) {
+    nrow = w * a.mean_H + blockIdx.x;
+    wrow_base = a.g.w;
+  } else {
+    nrow = blockIdx.x * 4 + w;
+    if (nrow >= a.g.N + a.N2) return;  // whole waves; no workgroup barrier follows
+    second = nrow >= a.g.N;
+    wrow_base = second ? a.w2 : a.g.w;
+  }
+  const int wn = second ? nrow - a.g.N : nrow;
+  const uint4* wr = reinterpret_cast<const uint4*>(wrow_base + (size_t)wn * a.K);
+  float acc[kDR] = {0.f, 0.f, 0.f, 0.f};
+  constexpr int kUB = 8;
+  int k8 = lane;
+  auto fma_chunk = [&](const uint4& wq, int kk) {
+    const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
+#pragma unroll
+    for (int r = 0; r < kDR; ++r) {
+      if (r < R) {
+        const uint4 xq = xs[r * k8n + kk];
+        const uint32_t xv[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          acc[r] = fmaf(lo16(xv[c]), lo16(wv[c]), acc[r]);
+          acc[r] = fmaf(hi16(xv[c]), hi16(wv[c]), acc[r]);
+        }
+      }
+    }
+  };
+  for (; k8 + 64 * (kUB - 1) < k8n; k8 += 64 * kUB) {
+    uint4 wq[kUB];
+#pragma unroll
+    for (int u = 0; u < kUB; ++u) wq[u] = wr[k8 + 64 * u];
+#pragma unroll
+    for (int u = 0; u < kUB; ++u) fma_chunk(wq[u], k8 + 64 * u);
+  }
+  for (; k8 < k8n; k8 += 64) fma_chunk(wr[k8], k8);
+  float mine = 0.f;
+#pragma unroll
+  for (int r = 0; r < kDR; ++r) {
+    const float s = ss_wave_sum(acc[r]);
+    mine = lane == r ? s : mine;
+  }
+  DenseEpiArgs ea = a.g;
+  ea.R = R;
+  if (second) {
+    ea.epi = a.epi2;
+    ea.N = a.N2;
+    ea.out = a.out2;
+  }
+  const uint32_t v = lane < R ? epilogue(mine, ea, lane, wn) : 0u;
+  if (lane < R) ea.out[(size_t)lane * ea.N + wn] = (uint16_t)v;
+  if (!a.mean_out) return;
+  if (lane < R) mw[w][lane] = v;
+  __syncthreads();
+  if (w == 0 && lane < R) {
+    const int j = blockIdx.x, H = a.mean_H;
+    const uint16_t* hn = a.mean_hn + (size_t)lane * 4 * H;
+    float m = 0.f;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) m += ss_round_bf16(ss_bf16_to_f32(mw[c][lane]) * ss_bf16_to_f32(hn[(size_t)c * H + j]));
+    a.mean_out[(size_t)lane * H + j] = (uint16_t)ss_f32_to_bf16(m / 4.0f);
+  }
+}
+
 // mixed[s][j] = bf16((sum over c = 0 .. hc-1 of bf16(m[s][c H + j] * hn[s][c H + j])) / hc), the sum sequential.
 __global__ __launch_bounds__(256) void hc_mean_kernel(const uint16_t* __restrict__ m, const uint16_t* __restrict__ hn,
                                                       int S, int hc, int H, uint16_t* __restrict__ mixed) {
@@ -242,6 +421,55 @@ hipError_t launch_dense_epi(const uint16_t* x, int R, int K, const uint16_t* w, 
     a.R = R - r0 < kDR ? R - r0 : kDR;
     a.row0 = r0;
     hipLaunchKernelGGL(dense_epi_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, st, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
+}
+
+hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st) {
+  // source rows per launch: the staged rows fit the LDS, their x rows one GEMV pass (<= kDR) and their norm groups
+  // the table of 64
+  int per = kDR * in.K / in.n < kHeadLds / in.n ? kDR * in.K / in.n : kHeadLds / in.n;
+  if (in.G > 0 && 64 * in.G / in.n < per) per = 64 * in.G / in.n;
+  if (per < 1) return hipErrorInvalidValue;
+  HeadGemvArgs a{};
+  a.src_idx = nullptr;
+  a.n_src = in.n_src;
+  a.inj_hc = in.inj_hc;
+  a.norm_w = in.norm_w;
+  a.eps = in.eps;
+  a.G = in.G;
+  a.n = in.n;
+  a.K = in.K;
+  a.g.K = in.K;
+  a.g.epi = in.epi;
+  a.g.hc = (float)in.hc;
+  a.g.add_div = in.add_div > 0 ? in.add_div : 1;
+  a.g.N = in.N;
+  a.N2 = in.N2;
+  a.epi2 = in.epi2;
+  a.mean_H = in.mean_H;
+  a.err = in.err;
+  const int xr = in.n / in.K;  // x rows per source row
+  for (int s0 = 0; s0 < in.S; s0 += per) {
+    a.Sl = in.S - s0 < per ? in.S - s0 : per;
+    a.src = in.src_idx ? in.src : in.src + (size_t)s0 * in.n;
+    a.src_idx = in.src_idx ? in.src_idx + s0 : nullptr;
+    a.inj_y = in.inj_y ? in.inj_y + (size_t)s0 * (in.n / in.inj_hc) : nullptr;
+    a.inj = in.inj ? in.inj + (size_t)s0 * in.inj_hc : nullptr;
+    a.g.w = in.w;
+    a.g.out = in.out + (size_t)s0 * xr * in.N;
+    a.g.add = in.add;
+    a.g.row0 = s0 * xr;
+    a.w2 = in.w2;
+    a.out2 = in.out2 ? in.out2 + (size_t)s0 * xr * in.N2 : nullptr;
+    a.h_out = in.h_out ? in.h_out + (size_t)s0 * in.n : nullptr;
+    a.x_out = in.x_out ? in.x_out + (size_t)s0 * in.n : nullptr;
+    a.mean_hn = in.mean_hn ? in.mean_hn + (size_t)s0 * in.n : nullptr;
+    a.mean_out = in.mean_out ? in.mean_out + (size_t)s0 * xr * in.mean_H : nullptr;
+    const int grid = in.mean_out ? in.mean_H : (in.N + in.N2 + 3) / 4;
+    hipLaunchKernelGGL(head_gemv_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

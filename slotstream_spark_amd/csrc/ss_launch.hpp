@@ -234,6 +234,36 @@ hipError_t launch_rmsnorm_groups(const uint16_t* x, const uint16_t* w, float eps
                                  hipStream_t st);
 hipError_t launch_dense_epi(const uint16_t* x, int R, int K, const uint16_t* w, int N, int epi, int hc,
                             const uint16_t* add, int add_div, uint16_t* out, hipStream_t st);
+// The fused head GEMV (ss_head.hip): source rows (or table rows by device index), optional hc_inject and RMSNorm,
+// then the GEMV with one or two weight ranges, or the GEMV with the branch mean fused behind it. Fields as the C
+// entry point ssmoe_head_gemv; mean_H = N / 4 in mean mode.
+struct HeadGemvIn {
+  const uint16_t* src;
+  const int32_t* src_idx;
+  int64_t n_src;
+  const uint16_t* inj_y;
+  const uint16_t* inj;
+  int inj_hc;
+  const uint16_t* norm_w;
+  float eps;
+  int G;
+  int S, n, K;
+  const uint16_t* w;
+  int N, epi, hc;
+  const uint16_t* add;
+  int add_div;
+  uint16_t* out;
+  const uint16_t* w2;
+  int N2, epi2;
+  uint16_t* out2;
+  uint16_t* h_out;
+  uint16_t* x_out;
+  const uint16_t* mean_hn;
+  uint16_t* mean_out;
+  int mean_H;
+  int* err;
+};
+hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st);
 hipError_t launch_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed,
                           hipStream_t st);
 hipError_t launch_hc_inject(const uint16_t* hyp, const uint16_t* y, const uint16_t* inj, int S, int hc, int H,

@@ -1003,6 +1003,70 @@ int ssmoe_dense_gemv_epi(const uint16_t* x, int R, int K, const uint16_t* w, int
                    "dense gemv launch");
 }
 
+int ssmoe_head_gemv(const ssmoe_head_gemv_args* p, void* stream) {
+  if (!p) return fail(SSMOE_EINVAL, "args must be non-null");
+  const ssmoe_head_gemv_args& a = *p;
+  if (a.S < 0 || a.n < 8 || a.K < 8 || a.n % 8 || a.K % 8 || a.n % a.K)
+    return fail(SSMOE_EINVAL, "need S >= 0, n and K multiples of 8, n a multiple of K (n=%d K=%d)", a.n, a.K);
+  if (a.n > 32768 || (a.n / a.K) > 4) return fail(SSMOE_EINVAL, "need n <= 32768 and n / K <= 4");
+  if (a.group < 0 || (a.group > 0 && (a.n % a.group || a.group % 8)))
+    return fail(SSMOE_EINVAL, "group must be 0 (no norm) or a multiple of 8 dividing n, got %d", a.group);
+  if (a.group > 0 && a.n / a.group > 64)
+    return fail(SSMOE_EINVAL, "at most 64 norm groups per row, got n %d, group %d", a.n, a.group);
+  if (a.N < 1 || a.N2 < 0) return fail(SSMOE_EINVAL, "need N >= 1 and N2 >= 0");
+  for (int e : {a.epi, a.epi2})
+    if (e < SSMOE_EPI_NONE || e > SSMOE_EPI_INJECT) return fail(SSMOE_EINVAL, "unknown epilogue %d", e);
+  if ((a.epi == SSMOE_EPI_SILU_DIV || a.epi == SSMOE_EPI_INJECT || a.epi2 == SSMOE_EPI_SILU_DIV ||
+       a.epi2 == SSMOE_EPI_INJECT) && a.hc < 1)
+    return fail(SSMOE_EINVAL, "hc must be >= 1");
+  if (a.epi == SSMOE_EPI_ADD && (!a.add || a.add_div < 1)) return fail(SSMOE_EINVAL, "EPI_ADD needs add, add_div >= 1");
+  if (a.epi2 == SSMOE_EPI_ADD) return fail(SSMOE_EINVAL, "the second weight range takes no EPI_ADD");
+  if (!a.src || !a.w || !a.out || (a.N2 > 0 && (!a.w2 || !a.out2)))
+    return fail(SSMOE_EINVAL, "src, w and out (and w2, out2 with N2 > 0) must be non-null");
+  if (a.inj && (!a.inj_y || a.inj_hc < 1 || a.n % a.inj_hc || (a.n / a.inj_hc) % 8))
+    return fail(SSMOE_EINVAL, "the injection needs inj_y and inj_hc dividing n into multiples of 8");
+  if (a.mean_out && (!a.mean_hn || a.hc != 4 || a.N % 4 || a.N2 > 0 || a.n != a.K))
+    return fail(SSMOE_EINVAL, "the fused mean needs mean_hn, hc == 4, N a multiple of 4, no w2 and n == K");
+  if (a.src_idx && a.n_src < 1) return fail(SSMOE_EINVAL, "a table source needs n_src >= 1");
+  if (!aligned(a.src, 16) || !aligned(a.w, 16) || (a.w2 && !aligned(a.w2, 16)) || (a.norm_w && !aligned(a.norm_w, 16)) ||
+      (a.inj_y && !aligned(a.inj_y, 16)) || (a.h_out && !aligned(a.h_out, 16)) || (a.x_out && !aligned(a.x_out, 16)))
+    return fail(SSMOE_EINVAL, "src, w, w2, norm_w, inj_y, h_out and x_out must be 16-byte aligned");
+  if (a.S == 0) return ok();
+  int* err = nullptr;
+  if (int rc = status_ptr(&err)) return rc;
+  ss::HeadGemvIn in{};
+  in.src = a.src;
+  in.src_idx = a.src_idx;
+  in.n_src = a.n_src;
+  in.inj_y = a.inj ? a.inj_y : nullptr;
+  in.inj = a.inj;
+  in.inj_hc = a.inj ? a.inj_hc : 1;
+  in.norm_w = a.norm_w;
+  in.eps = a.eps;
+  in.G = a.group;
+  in.S = a.S;
+  in.n = a.n;
+  in.K = a.K;
+  in.w = a.w;
+  in.N = a.N;
+  in.epi = a.epi;
+  in.hc = a.hc;
+  in.add = a.add;
+  in.add_div = a.add_div;
+  in.out = a.out;
+  in.w2 = a.w2;
+  in.N2 = a.N2;
+  in.epi2 = a.epi2;
+  in.out2 = a.out2;
+  in.h_out = a.h_out;
+  in.x_out = a.x_out;
+  in.mean_hn = a.mean_hn;
+  in.mean_out = a.mean_out;
+  in.mean_H = a.N / 4;
+  in.err = err;
+  return hip_check(ss::launch_head_gemv(in, static_cast<hipStream_t>(stream)), "head gemv launch");
+}
+
 int ssmoe_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed, void* stream) {
   if (S < 0 || hc < 1 || H < 1) return fail(SSMOE_EINVAL, "need S >= 0, hc >= 1, H >= 1");
   if (!m || !hn || !mixed) return fail(SSMOE_EINVAL, "m, hn and mixed must be non-null");

@@ -10,9 +10,11 @@ One head step over S rows, as MTPHead.step (engine/mtp.py:209-227) with the atte
     out   = hc_mix(hyper_connection_mixer, h)                  engine/mtp.py:229-230
 
 Every op is a libssmoe.so launch (kernels/head_ops.py, the verify layer for the MoE, the affine lm_head argmax).
-`draft(token, k)` chains k steps on the device: each step's embedding row is gathered by a kernel that reads the
-token where the previous step's lm_head argmax wrote it, so the k drafts reach the host once, at the end, and the
-chain can be captured in a HIP graph (DraftGraph).
+With hc = 4 the dense ops between the MoE and the lm_head run as six fused launches (ssmoe_head_gemv: each RMSNorm,
+the embedding lookup and the injection inside the GEMV that consumes them, the inject rows beside the down rows, the
+branch mean behind the up GEMV), with the bits of the separate ops. `draft(token, k)` chains k steps on the device:
+each step's embedding row is read by the first launch at the token the previous step's lm_head argmax wrote, so the
+k drafts reach the host once, at the end, and the chain can be captured in a HIP graph (DraftGraph).
 
 Out of this path: the attention segment (hc_mix of attn_hyper_connection, QSA over the head's own KV/indexer cache,
 its residual). MTPState keeps the position bookkeeping of the reference's state (pos, aligned, fork, reset) with no
@@ -26,7 +28,7 @@ import torch
 
 from ..kernels.gemv_affine import AffineWeight, LMHeadArgmax, gemv
 from ..kernels.head_ops import (EPI_ADD, EPI_INJECT, EPI_SIGMOID, EPI_SILU_DIV, gather_rows, hc_inject, hc_mean,
-                                lin_epi, rmsnorm)
+                                head_gemv, lin_epi, rmsnorm)
 from .verify import MoEVerifyLayer
 
 MAP_ROW = 48   # the head's layer index in the 49-row expert map (engine/mtp.py:38)
@@ -154,15 +156,17 @@ class MTPHead:
         return _Rows(steps, S, self.H, self.hc, self.w.mlp_hc.down.shape[0], self.w.mixer_hc.down.shape[0],
                      self.topk, self.w.embed.device)
 
-    def fuse(self, embedded: torch.Tensor, multi: torch.Tensor, r: _Rows | None = None, i: int = 0) -> torch.Tensor:
-        """embedded bf16 [S, H], multi bf16 [S, hc H] -> bf16 [S, hc H] (engine/mtp.py:184-192)."""
-        S, H, hc, w = embedded.shape[0], self.H, self.hc, self.w
+    def fuse(self, embedded: torch.Tensor | None, multi: torch.Tensor, r: _Rows | None = None, i: int = 0,
+             idx: torch.Tensor | None = None) -> torch.Tensor:
+        """embedded bf16 [S, H] (or, with idx, the embedding rows idx: int32 [S] on the device), multi bf16
+        [S, hc H] -> bf16 [S, hc H] (engine/mtp.py:184-192): two launches, each RMSNorm inside the GEMV after it."""
+        S, H, hc, w = multi.shape[0], self.H, self.hc, self.w
         r = r if r is not None else self._rows(1, S)
-        rmsnorm(embedded, w.pre_fc_norm_embedding, self.eps, out=r.e_norm[i])
-        lin_epi(r.e_norm[i], w.fc_embedding, out=r.e_proj[i])
-        rmsnorm(multi, w.pre_fc_norm_hidden, self.eps, out=r.m_norm[i])
-        lin_epi(r.m_norm[i].view(S * hc, H), w.fc_hidden, EPI_ADD, add=r.e_proj[i], add_div=hc,
-                out=r.fused[i].view(S * hc, H))
+        src = w.embed if idx is not None else embedded
+        head_gemv(src, w.fc_embedding, r.e_proj[i], S=S, n=H, K=H, src_idx=idx, norm_w=w.pre_fc_norm_embedding,
+                  eps=self.eps, group=H, x_out=r.e_norm[i], h_out=r.emb[i] if idx is not None else None)
+        head_gemv(multi, w.fc_hidden, r.fused[i].view(S * hc, H), S=S, n=hc * H, K=H, norm_w=w.pre_fc_norm_hidden,
+                  eps=self.eps, group=hc * H, epi=EPI_ADD, add=r.e_proj[i], add_div=hc, x_out=r.m_norm[i])
         return r.fused[i]
 
     def hc_mix(self, hcw: HyperConnection, hyp: torch.Tensor, hn: torch.Tensor, low: torch.Tensor,
@@ -179,12 +183,29 @@ class MTPHead:
         lin_epi(hn, hcw.inject, EPI_INJECT, hc=self.hc, out=inj)
         return mixed, inj
 
-    def _step_rows(self, embedded, multi, r: _Rows, i: int):
-        h = self.fuse(embedded, multi, r, i)
-        self.hc_mix(self.w.mlp_hc, h, r.hn[i], r.low[i], r.mix_w[i], r.mixed[i], r.inj[i])
+    def _step_rows(self, embedded, multi, r: _Rows, i: int, idx: torch.Tensor | None = None):
+        h = self.fuse(embedded, multi, r, i, idx)
+        if self.hc != 4:
+            # the separate launches (the fused branch mean takes four branches)
+            self.hc_mix(self.w.mlp_hc, h, r.hn[i], r.low[i], r.mix_w[i], r.mixed[i], r.inj[i])
+            self.moe(r.mixed[i], y=r.y[i], ids=r.ids[i], weights=r.weights[i])
+            hc_inject(h, r.y[i], r.inj[i], out=r.h[i])
+            self.hc_mix(self.w.mixer_hc, r.h[i], r.hn2[i], r.low2[i], r.mix_w2[i], r.out[i])
+            return r.out[i], r.h[i]
+        S, H, hc, n, mlp, mix = h.shape[0], self.H, self.hc, self.hc * self.H, self.w.mlp_hc, self.w.mixer_hc
+        # hc_mix of the MLP: norm + down rows + inject rows, then up + the branch mean (model/layers.py:190-198)
+        head_gemv(h, mlp.down, r.low[i], S=S, n=n, K=n, norm_w=mlp.hc_norm, eps=self.eps, group=H,
+                  epi=EPI_SILU_DIV, hc=hc, w2=mlp.inject, out2=r.inj[i], epi2=EPI_INJECT, x_out=r.hn[i])
+        L = mlp.down.shape[0]
+        head_gemv(r.low[i], mlp.up, r.mix_w[i], S=S, n=L, K=L, epi=EPI_SIGMOID, hc=hc, mean_hn=r.hn[i],
+                  mean_out=r.mixed[i])
         self.moe(r.mixed[i], y=r.y[i], ids=r.ids[i], weights=r.weights[i])
-        hc_inject(h, r.y[i], r.inj[i], out=r.h[i])
-        self.hc_mix(self.w.mixer_hc, r.h[i], r.hn2[i], r.low2[i], r.mix_w2[i], r.out[i])
+        # the injection (engine/mtp.py:226), then hc_mix of the mixer
+        head_gemv(h, mix.down, r.low2[i], S=S, n=n, K=n, inj=r.inj[i], inj_y=r.y[i], inj_hc=hc, norm_w=mix.hc_norm,
+                  eps=self.eps, group=H, epi=EPI_SILU_DIV, hc=hc, h_out=r.h[i], x_out=r.hn2[i])
+        L2 = mix.down.shape[0]
+        head_gemv(r.low2[i], mix.up, r.mix_w2[i], S=S, n=L2, K=L2, epi=EPI_SIGMOID, hc=hc, mean_hn=r.hn2[i],
+                  mean_out=r.out[i])
         return r.out[i], r.h[i]
 
     def step(self, embedded: torch.Tensor, multi: torch.Tensor, state: MTPState, state_only: bool = False):
@@ -260,8 +281,7 @@ class MTPHead:
         prev_h = multi
         for i in range(k):
             src = token if i == 0 else out[i - 1:i]
-            gather_rows(self.w.embed, src, out=r.emb[i])
-            o, prev_h = self._step_rows(r.emb[i], prev_h, r, i)
+            o, prev_h = self._step_rows(None, prev_h, r, i, idx=src)
             self.argmax(o, ids=out[i:i + 1])
         st.pos += k
         return out

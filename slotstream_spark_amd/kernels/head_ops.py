@@ -12,6 +12,8 @@ so an S-row call equals S one-row calls bit for bit:
 """
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from .. import _lib
@@ -61,6 +63,45 @@ def lin_epi(x: torch.Tensor, w: torch.Tensor, epi: int = EPI_NONE, hc: int = 1, 
     _bf16("out", out, (R, N))
     _lib.check(_lib.lib().ssmoe_dense_gemv_epi(x.data_ptr(), R, x.shape[1], w.data_ptr(), N, int(epi), int(hc),
                                                _lib.ptr(add), int(add_div), out.data_ptr(), _lib.stream_of(x)))
+    return out
+
+
+class _HeadGemvArgs(ctypes.Structure):
+    _fields_ = [("src", ctypes.c_void_p), ("src_idx", ctypes.c_void_p), ("n_src", ctypes.c_int64),
+                ("inj_y", ctypes.c_void_p), ("inj", ctypes.c_void_p), ("inj_hc", ctypes.c_int),
+                ("norm_w", ctypes.c_void_p), ("eps", ctypes.c_float), ("group", ctypes.c_int), ("S", ctypes.c_int),
+                ("n", ctypes.c_int), ("K", ctypes.c_int), ("w", ctypes.c_void_p), ("N", ctypes.c_int),
+                ("epi", ctypes.c_int), ("hc", ctypes.c_int), ("add", ctypes.c_void_p), ("add_div", ctypes.c_int),
+                ("out", ctypes.c_void_p), ("w2", ctypes.c_void_p), ("N2", ctypes.c_int), ("epi2", ctypes.c_int),
+                ("out2", ctypes.c_void_p), ("h_out", ctypes.c_void_p), ("x_out", ctypes.c_void_p),
+                ("mean_hn", ctypes.c_void_p), ("mean_out", ctypes.c_void_p)]
+
+
+def head_gemv(src: torch.Tensor, w: torch.Tensor, out: torch.Tensor, *, S: int, n: int, K: int,
+              src_idx: torch.Tensor | None = None, inj: torch.Tensor | None = None, inj_y: torch.Tensor | None = None,
+              inj_hc: int = 1, norm_w: torch.Tensor | None = None, eps: float = 1e-6, group: int = 0,
+              epi: int = EPI_NONE, hc: int = 1, add: torch.Tensor | None = None, add_div: int = 1,
+              w2: torch.Tensor | None = None, out2: torch.Tensor | None = None, epi2: int = EPI_NONE,
+              h_out: torch.Tensor | None = None, x_out: torch.Tensor | None = None,
+              mean_hn: torch.Tensor | None = None, mean_out: torch.Tensor | None = None) -> torch.Tensor:
+    """One launch of the head's fused dense step (ssmoe_head_gemv): S source rows of n (src [S, n], or rows
+    src_idx of the table src), optionally injected (hc_inject) and normalized (rmsnorm over groups of `group`), then
+    the GEMV over them viewed as [S n / K, K] with w (and w2 for extra rows into out2), or with the branch mean
+    (hc_mean with mean_hn) into mean_out. Bit for bit the separate calls."""
+    for name, t in (("src", src), ("w", w), ("out", out)):
+        _bf16(name, t)
+    for name, t in (("inj_y", inj_y), ("norm_w", norm_w), ("add", add), ("w2", w2), ("out2", out2),
+                    ("h_out", h_out), ("x_out", x_out), ("mean_hn", mean_hn), ("mean_out", mean_out), ("inj", inj)):
+        if t is not None:
+            _bf16(name, t)
+    if src_idx is not None and (src_idx.dtype != torch.int32 or not src_idx.is_cuda or src_idx.numel() < S):
+        raise ValueError(f"src_idx must be a GPU int32 tensor of at least {S} entries")
+    a = _HeadGemvArgs(src.data_ptr(), _lib.ptr(src_idx), src.shape[0] if src_idx is not None else 0,
+                      _lib.ptr(inj_y), _lib.ptr(inj), int(inj_hc), _lib.ptr(norm_w), float(eps), int(group), int(S),
+                      int(n), int(K), w.data_ptr(), w.shape[0], int(epi), int(hc), _lib.ptr(add), int(add_div),
+                      out.data_ptr(), _lib.ptr(w2), w2.shape[0] if w2 is not None else 0, int(epi2), _lib.ptr(out2),
+                      _lib.ptr(h_out), _lib.ptr(x_out), _lib.ptr(mean_hn), _lib.ptr(mean_out))
+    _lib.check(_lib.lib().ssmoe_head_gemv(ctypes.byref(a), _lib.stream_of(src)))
     return out
 
 

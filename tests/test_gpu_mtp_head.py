@@ -144,6 +144,69 @@ def _np_weights(hw):
             "mlp_hc": hcd(hw.mlp_hc), "mixer_hc": hcd(hw.mixer_hc)}
 
 
+@pytest.mark.parametrize("S,n,K,group,inject,two", [(1, 8192, 8192, 2048, False, True), (3, 8192, 8192, 2048, True, False),
+                                                     (1, 2048, 2048, 2048, False, False), (4, 8192, 2048, 8192, False,
+                                                                                              False),
+                                                     (2, 520, 520, 40, False, True), (5, 96, 32, 32, True, False)])
+def test_head_gemv_equals_the_separate_ops(S, n, K, group, inject, two):
+    """ssmoe_head_gemv against the separate launches it replaces (hc_inject, rmsnorm, dense_gemv_epi, twice),
+    bit for bit, at the head's shapes and at ragged ones: h, x, both outputs."""
+    print(f"[head_gemv] S={S} n={n} K={K} group={group} inject={inject} two={two}", flush=True)
+    hcj = 4
+    src = _dev(_rand_bits((S, n), 2.0, S + n))
+    nw = _dev(_rand_bits((n,), 0.1, n + 1, 1.0))
+    w = _dev(_rand_bits((77, K), K ** -0.5 * 3, K + 2))
+    w2 = _dev(_rand_bits((4, K), K ** -0.5 * 3, K + 3)) if two else None
+    y = _dev(_rand_bits((S, n // hcj), 1.0, 9)) if inject else None
+    inj = _dev(_rand_bits((S, hcj), 0.5, 10, 1.0)) if inject else None
+    R = S * n // K
+    out, hout, xout = (torch.empty((R, 77), dtype=torch.bfloat16, device="cuda"),
+                       torch.empty((S, n), dtype=torch.bfloat16, device="cuda"),
+                       torch.empty((S, n), dtype=torch.bfloat16, device="cuda"))
+    out2 = torch.empty((R, 4), dtype=torch.bfloat16, device="cuda") if two else None
+    HO.head_gemv(src, w, out, S=S, n=n, K=K, inj=inj, inj_y=y, inj_hc=hcj, norm_w=nw, eps=1e-6, group=group,
+                 epi=HO.EPI_SILU_DIV, hc=4, w2=w2, out2=out2, epi2=HO.EPI_INJECT, h_out=hout, x_out=xout)
+    h = HO.hc_inject(src, y, inj) if inject else src
+    x = HO.rmsnorm(h, nw, 1e-6, group=group)
+    ref = HO.lin_epi(x.view(R, K), w, HO.EPI_SILU_DIV, hc=4)
+    torch.cuda.synchronize()
+    assert torch.equal(hout, h) and torch.equal(xout, x) and torch.equal(out, ref)
+    if two:
+        assert torch.equal(out2, HO.lin_epi(x.view(R, K), w2, HO.EPI_INJECT, hc=4))
+
+
+@pytest.mark.parametrize("S,L,H4", [(1, 64, 2048), (3, 320, 512), (2, 40, 96)])
+def test_head_gemv_mean_and_table_rows(S, L, H4):
+    """The up GEMV with the branch mean fused behind it equals lin_epi + hc_mean; table rows by device index equal
+    gather_rows + rmsnorm + lin_epi, and an index outside the table reads zeros and raises the token error."""
+    print(f"[head_gemv mean] S={S} L={L} H={H4}", flush=True)
+    low = _dev(_rand_bits((S, L), 1.0, L))
+    up = _dev(_rand_bits((4 * H4, L), L ** -0.5 * 3, L + 1))
+    hn = _dev(_rand_bits((S, 4 * H4), 1.0, L + 2))
+    mw, mixed = (torch.empty((S, 4 * H4), dtype=torch.bfloat16, device="cuda"),
+                 torch.empty((S, H4), dtype=torch.bfloat16, device="cuda"))
+    HO.head_gemv(low, up, mw, S=S, n=L, K=L, epi=HO.EPI_SIGMOID, hc=4, mean_hn=hn, mean_out=mixed)
+    ref = HO.lin_epi(low, up, HO.EPI_SIGMOID)
+    torch.cuda.synchronize()
+    assert torch.equal(mw, ref) and torch.equal(mixed, HO.hc_mean(ref, hn, 4))
+    table = _dev(_rand_bits((50, H4), 1.0, 3))
+    nw = _dev(_rand_bits((H4,), 0.1, 4, 1.0))
+    w = _dev(_rand_bits((33, H4), H4 ** -0.5, 5))
+    idx = torch.tensor([7, 49, 0][:S] if S <= 3 else [7] * S, dtype=torch.int32, device="cuda")
+    out, emb = (torch.empty((S, 33), dtype=torch.bfloat16, device="cuda"),
+                torch.empty((S, H4), dtype=torch.bfloat16, device="cuda"))
+    HO.head_gemv(table, w, out, S=S, n=H4, K=H4, src_idx=idx, norm_w=nw, eps=1e-6, group=H4, h_out=emb)
+    g = HO.gather_rows(table, idx)
+    ref = HO.lin_epi(HO.rmsnorm(g, nw, 1e-6), w)
+    torch.cuda.synchronize()
+    assert torch.equal(emb, g) and torch.equal(out, ref)
+    _lib.device_error(clear=True)
+    bad = torch.tensor([50] * S, dtype=torch.int32, device="cuda")
+    HO.head_gemv(table, w, out, S=S, n=H4, K=H4, src_idx=bad, norm_w=nw, eps=1e-6, group=H4, h_out=emb)
+    torch.cuda.synchronize()
+    assert _lib.device_error(clear=True) & 4 and not emb.float().abs().sum().item()
+
+
 def test_draft_chain_teacher_forced(head):
     h, pool, lw, hw = head
     k = 3
