@@ -427,7 +427,8 @@ int ssmoe_dense_gemv_epi(const uint16_t* x, int R, int K, const uint16_t* w, int
  *   norm (group > 0): x = ssmoe_rmsnorm(h, norm_w, eps, group) (norm_w NULL: 1);
  *   the GEMV of ssmoe_dense_gemv_epi over x viewed as S n / K rows of K: weight rows w [N][K] with epi, hc, add,
  *     add_div into out, and rows w2 [N2][K] with epi2 into out2 (N2 may be 0);
- *   or, with mean_out non-null (hc == 4, N = 4 H, no w2): also mean_out [S][H] = ssmoe_hc_mean(out, mean_hn, 4).
+ *   or, with mean_out non-null (hc == 4, N = 4 H, no w2, n == K <= 512): also mean_out [S][H] =
+ *     ssmoe_hc_mean(out, mean_hn, 4).
  *   h_out / x_out (bf16 [S][n], or NULL) receive h and x.
  * n a multiple of K and of group, K and n multiples of 8, n <= 32768, n / K <= 4, n / group <= 64; pointers
  * 16-byte aligned. */

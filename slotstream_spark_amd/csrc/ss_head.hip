@@ -177,8 +177,9 @@ __global__ __launch_bounds__(256) void dense_epi_kernel(DenseEpiArgs a) {
 //   and x out when asked;
 //   then the GEMV of dense_epi_kernel over x viewed as R = Sl n / K rows of K (x from LDS): weight rows [0, N) of w
 //   with epilogue epi into out, rows [N, N + N2) of w2 with epi2 into out2;
-//   or, with mean_out, the branch mean of hc_mean_kernel fused behind the GEMV (hc == 4): workgroup j takes weight
-//   rows c H + j (wave c), and mean_out[r][j] = bf16((sum over c of bf16(v_c * mean_hn[r][c H + j])) / hc).
+//   or, with mean_out, the branch mean of hc_mean_kernel fused behind the GEMV (hc == 4, K <= 512): one wave takes
+//   the four weight rows c H + j of output j (each the dense order: one chunk per lane, then the butterfly), and
+//   mean_out[r][j] = bf16((sum over c of bf16(v_c * mean_hn[r][c H + j])) / hc), with no barrier.
 struct HeadGemvArgs {
   const uint16_t* src;
   const int32_t* src_idx;
@@ -200,18 +201,56 @@ struct HeadGemvArgs {
   uint16_t* mean_out;
   int mean_H;
   int* err;
+  uint64_t* trace;  // diagnostics: per-workgroup phase stamps (thread 0), or null
 };
 
 constexpr int kHeadLds = 4 * 8192;  // bf16 elements of the staged source rows (Sl n <= 32768)
 
 __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
-  __shared__ uint4 xs[kHeadLds / 8];
+  extern __shared__ uint4 xs[];  // the staged source rows: Sl n bf16 (sized per launch)
   __shared__ float rs[64];
-  __shared__ uint32_t mw[4][kDR];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // stamps 0 start, 1 staged, 2 norm factors, 3 normalized, 4 dot products, 5 stored (wave 0 of the workgroup)
+#define HG_TRACE(k)                                                                                    \
+  do {                                                                                                 \
+    if (a.trace && tid == 0) a.trace[(size_t)blockIdx.x * 8 + (k)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+  HG_TRACE(0);
   const int n = a.n, E = a.Sl * n, E8 = E >> 3;
-  // pre-step 1: the source rows (and the injection) into LDS, h out from workgroup 0
-  for (int i = tid; i < E8; i += 256) {
+  // This wave's weight row, and its first kUB chunks requested before the pre-step (they do not depend on x). In
+  // mean mode the wave takes the four branch rows c H + j of one output j instead (K <= 512: one chunk per lane).
+  const int R = E / a.K, k8n = a.K >> 3;
+  const int nrow = blockIdx.x * 4 + w;
+  const bool second = !a.mean_out && nrow >= a.g.N;
+  const bool has_row = a.mean_out ? nrow < a.mean_H : nrow < a.g.N + a.N2;
+  const int wn = second ? nrow - a.g.N : nrow;
+  const uint4* wr = reinterpret_cast<const uint4*>((second ? a.w2 : a.g.w) + (size_t)(has_row ? wn : 0) * a.K);
+  constexpr int kUB = 16;  // a lane's 16 weight chunks of a K = 8192 row in flight at once
+  uint4 wq0[kUB];
+  if (a.mean_out) {
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      wq0[c] = has_row && lane < k8n
+                   ? reinterpret_cast<const uint4*>(a.g.w + ((size_t)c * a.mean_H + nrow) * a.K)[lane]
+                   : make_uint4(0u, 0u, 0u, 0u);
+  } else {
+#pragma unroll
+    for (int u = 0; u < kUB; ++u)
+      wq0[u] = has_row && lane + 64 * u < k8n ? wr[lane + 64 * u] : make_uint4(0u, 0u, 0u, 0u);
+  }
+  // the norm weights of this thread's chunks, with the source loads
+  uint4 nwq[kHeadLds / 8 / 256];
+  // pre-step 1: the source rows (and the injection) into LDS, h out from workgroup 0 (chunk i = tid + 256 k:
+  // unrolled, so that the norm weights stay in registers)
+#pragma unroll
+  for (int kq = 0; kq < kHeadLds / 8 / 256; ++kq) {
+    const int i = tid + 256 * kq;
+    if (i >= E8) break;
+    if (a.G > 0) {
+      const int j = (i << 3) - ((i << 3) / n) * n;
+      nwq[kq] = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w)[j >> 3]
+                         : make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+    }
     const int s = (i << 3) / n, j8 = (i << 3) - s * n;
     int64_t row = s;
     if (a.src_idx) {
@@ -239,32 +278,44 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
     if (a.h_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.h_out)[i] = v;
   }
   __syncthreads();
+  HG_TRACE(1);
   if (a.G > 0) {
     // pre-step 2: r of every group (one wave per group, rmsnorm_groups_kernel's order)
     const int ng = E / a.G, g8 = a.G >> 3;
     for (int g = w; g < ng; g += 4) {
       float acc = 0.f;
-      for (int k8 = lane; k8 < g8; k8 += 64) {
-        const uint4 q = xs[g * g8 + k8];
-        const uint32_t v[4] = {q.x, q.y, q.z, q.w};
+      // the LDS reads of 16 chunks issued before their FMAs (which keep the lane's chunk order)
+      for (int k0 = lane; k0 < g8; k0 += 64 * 16) {
+        uint4 q[16];
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const float e0 = lo16(v[c]), e1 = hi16(v[c]);
-          acc = fmaf(e0, e0, acc);
-          acc = fmaf(e1, e1, acc);
+        for (int u = 0; u < 16; ++u) q[u] = k0 + 64 * u < g8 ? xs[g * g8 + k0 + 64 * u] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+          if (k0 + 64 * u < g8) {
+            const uint32_t v[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              const float e0 = lo16(v[c]), e1 = hi16(v[c]);
+              acc = fmaf(e0, e0, acc);
+              acc = fmaf(e1, e1, acc);
+            }
+          }
         }
       }
       const float r = 1.f / sqrtf(ss_wave_sum(acc) / (float)a.G + a.eps);
       if (lane == 0) rs[g] = r;
     }
     __syncthreads();
+    HG_TRACE(2);
     // pre-step 3: x = bf16((h * r) * norm_w) in place, x out from workgroup 0
-    for (int i = tid; i < E8; i += 256) {
-      const int e = i << 3, g = e / a.G, j = e - (e / n) * n;
+#pragma unroll
+    for (int kq = 0; kq < kHeadLds / 8 / 256; ++kq) {
+      const int i = tid + 256 * kq;
+      if (i >= E8) break;
+      const int e = i << 3, g = e / a.G;
       const float r = rs[g];
       const uint4 q = xs[i];
-      const uint4 b = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w)[j >> 3]
-                               : make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+      const uint4 b = nwq[kq];
       const uint32_t v[4] = {q.x, q.y, q.z, q.w}, wv[4] = {b.x, b.y, b.z, b.w};
       uint32_t o[4];
 #pragma unroll
@@ -275,26 +326,54 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
       if (a.x_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.x_out)[i] = x;
     }
     __syncthreads();
+    HG_TRACE(3);
   }
   // the GEMV: one wave per weight row, the launch's x rows from LDS
-  const int R = E / a.K, k8n = a.K >> 3;
-  int nrow;
-  const uint16_t* wrow_base;
-  bool second = false;
+  if (!has_row) return;  // whole waves; no workgroup barrier follows
   if (a.mean_out) {
-    nrow = w * a.mean_H + blockIdx.x;
-    wrow_base = a.g.w;
-  } else {
-    nrow = blockIdx.x * 4 + w;
-    if (nrow >= a.g.N + a.N2) return;  // whole waves; no workgroup barrier follows
-    second = nrow >= a.g.N;
-    wrow_base = second ? a.w2 : a.g.w;
+    // the four branch rows of output j = nrow (one chunk per lane each), their epilogues, then the mean
+    const int j = nrow, H = a.mean_H;
+    float v[4][kDR];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float ac[kDR] = {0.f, 0.f, 0.f, 0.f};
+      if (lane < k8n) {
+        const uint32_t wv[4] = {wq0[c].x, wq0[c].y, wq0[c].z, wq0[c].w};
+#pragma unroll
+        for (int r = 0; r < kDR; ++r) {
+          if (r < R) {
+            const uint4 xq = xs[r * k8n + lane];
+            const uint32_t xv[4] = {xq.x, xq.y, xq.z, xq.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              ac[r] = fmaf(lo16(xv[q]), lo16(wv[q]), ac[r]);
+              ac[r] = fmaf(hi16(xv[q]), hi16(wv[q]), ac[r]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < kDR; ++r) v[c][r] = ss_wave_sum(ac[r]);
+    }
+    if (lane < R) {
+      DenseEpiArgs ea = a.g;
+      ea.R = R;
+      float m = 0.f;
+      const uint16_t* hn = a.mean_hn + (size_t)lane * 4 * H;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float d = v[c][0];
+#pragma unroll
+        for (int r = 1; r < kDR; ++r) d = lane == r ? v[c][r] : d;
+        const uint32_t e = epilogue(d, ea, lane, c * H + j);
+        ea.out[(size_t)lane * ea.N + c * H + j] = (uint16_t)e;
+        m += ss_round_bf16(ss_bf16_to_f32(e) * ss_bf16_to_f32(hn[(size_t)c * H + j]));
+      }
+      a.mean_out[(size_t)lane * H + j] = (uint16_t)ss_f32_to_bf16(m / 4.0f);
+    }
+    return;
   }
-  const int wn = second ? nrow - a.g.N : nrow;
-  const uint4* wr = reinterpret_cast<const uint4*>(wrow_base + (size_t)wn * a.K);
   float acc[kDR] = {0.f, 0.f, 0.f, 0.f};
-  constexpr int kUB = 8;
-  int k8 = lane;
   auto fma_chunk = [&](const uint4& wq, int kk) {
     const uint32_t wv[4] = {wq.x, wq.y, wq.z, wq.w};
 #pragma unroll
@@ -310,6 +389,10 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
       }
     }
   };
+#pragma unroll
+  for (int u = 0; u < kUB; ++u)
+    if (lane + 64 * u < k8n) fma_chunk(wq0[u], lane + 64 * u);
+  int k8 = lane + 64 * kUB;
   for (; k8 + 64 * (kUB - 1) < k8n; k8 += 64 * kUB) {
     uint4 wq[kUB];
 #pragma unroll
@@ -324,6 +407,7 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
     const float s = ss_wave_sum(acc[r]);
     mine = lane == r ? s : mine;
   }
+  HG_TRACE(4);
   DenseEpiArgs ea = a.g;
   ea.R = R;
   if (second) {
@@ -331,19 +415,9 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
     ea.N = a.N2;
     ea.out = a.out2;
   }
-  const uint32_t v = lane < R ? epilogue(mine, ea, lane, wn) : 0u;
-  if (lane < R) ea.out[(size_t)lane * ea.N + wn] = (uint16_t)v;
-  if (!a.mean_out) return;
-  if (lane < R) mw[w][lane] = v;
-  __syncthreads();
-  if (w == 0 && lane < R) {
-    const int j = blockIdx.x, H = a.mean_H;
-    const uint16_t* hn = a.mean_hn + (size_t)lane * 4 * H;
-    float m = 0.f;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) m += ss_round_bf16(ss_bf16_to_f32(mw[c][lane]) * ss_bf16_to_f32(hn[(size_t)c * H + j]));
-    a.mean_out[(size_t)lane * H + j] = (uint16_t)ss_f32_to_bf16(m / 4.0f);
-  }
+  if (lane < R) ea.out[(size_t)lane * ea.N + wn] = (uint16_t)epilogue(mine, ea, lane, wn);
+  HG_TRACE(5);
+#undef HG_TRACE
 }
 
 // mixed[s][j] = bf16((sum over c = 0 .. hc-1 of bf16(m[s][c H + j] * hn[s][c H + j])) / hc), the sum sequential.
@@ -433,6 +507,9 @@ hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st) {
   int per = kDR * in.K / in.n < kHeadLds / in.n ? kDR * in.K / in.n : kHeadLds / in.n;
   if (in.G > 0 && 64 * in.G / in.n < per) per = 64 * in.G / in.n;
   if (per < 1) return hipErrorInvalidValue;
+  KernelCfg cfg;  // allows the largest staging (64 KB) as dynamic LDS, once per device
+  hipError_t ce = kernel_cfg(reinterpret_cast<const void*>(head_gemv_kernel), 256, (size_t)kHeadLds * 2, &cfg);
+  if (ce != hipSuccess) return ce;
   HeadGemvArgs a{};
   a.src_idx = nullptr;
   a.n_src = in.n_src;
@@ -451,6 +528,7 @@ hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st) {
   a.epi2 = in.epi2;
   a.mean_H = in.mean_H;
   a.err = in.err;
+  a.trace = in.trace;
   const int xr = in.n / in.K;  // x rows per source row
   for (int s0 = 0; s0 < in.S; s0 += per) {
     a.Sl = in.S - s0 < per ? in.S - s0 : per;
@@ -468,8 +546,8 @@ hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st) {
     a.x_out = in.x_out ? in.x_out + (size_t)s0 * in.n : nullptr;
     a.mean_hn = in.mean_hn ? in.mean_hn + (size_t)s0 * in.n : nullptr;
     a.mean_out = in.mean_out ? in.mean_out + (size_t)s0 * xr * in.mean_H : nullptr;
-    const int grid = in.mean_out ? in.mean_H : (in.N + in.N2 + 3) / 4;
-    hipLaunchKernelGGL(head_gemv_kernel, dim3((unsigned)grid), dim3(256), 0, st, a);
+    const int grid = in.mean_out ? (in.mean_H + 3) / 4 : (in.N + in.N2 + 3) / 4;
+    hipLaunchKernelGGL(head_gemv_kernel, dim3((unsigned)grid), dim3(256), (size_t)a.Sl * in.n * 2, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

@@ -262,6 +262,7 @@ struct HeadGemvIn {
   uint16_t* mean_out;
   int mean_H;
   int* err;
+  uint64_t* trace;
 };
 hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st);
 hipError_t launch_hc_mean(const uint16_t* m, const uint16_t* hn, int S, int hc, int H, uint16_t* mixed,

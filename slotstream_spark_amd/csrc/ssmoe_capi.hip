@@ -1025,8 +1025,8 @@ int ssmoe_head_gemv(const ssmoe_head_gemv_args* p, void* stream) {
     return fail(SSMOE_EINVAL, "src, w and out (and w2, out2 with N2 > 0) must be non-null");
   if (a.inj && (!a.inj_y || a.inj_hc < 1 || a.n % a.inj_hc || (a.n / a.inj_hc) % 8))
     return fail(SSMOE_EINVAL, "the injection needs inj_y and inj_hc dividing n into multiples of 8");
-  if (a.mean_out && (!a.mean_hn || a.hc != 4 || a.N % 4 || a.N2 > 0 || a.n != a.K))
-    return fail(SSMOE_EINVAL, "the fused mean needs mean_hn, hc == 4, N a multiple of 4, no w2 and n == K");
+  if (a.mean_out && (!a.mean_hn || a.hc != 4 || a.N % 4 || a.N2 > 0 || a.n != a.K || a.K > 512))
+    return fail(SSMOE_EINVAL, "the fused mean needs mean_hn, hc == 4, N a multiple of 4, no w2 and n == K <= 512");
   if (a.src_idx && a.n_src < 1) return fail(SSMOE_EINVAL, "a table source needs n_src >= 1");
   if (!aligned(a.src, 16) || !aligned(a.w, 16) || (a.w2 && !aligned(a.w2, 16)) || (a.norm_w && !aligned(a.norm_w, 16)) ||
       (a.inj_y && !aligned(a.inj_y, 16)) || (a.h_out && !aligned(a.h_out, 16)) || (a.x_out && !aligned(a.x_out, 16)))
@@ -1064,6 +1064,7 @@ int ssmoe_head_gemv(const ssmoe_head_gemv_args* p, void* stream) {
   in.mean_out = a.mean_out;
   in.mean_H = a.N / 4;
   in.err = err;
+  in.trace = g_trace;
   return hip_check(ss::launch_head_gemv(in, static_cast<hipStream_t>(stream)), "head gemv launch");
 }
 
