@@ -25,7 +25,7 @@ MAIN = [(0, "layer start"), (5, "stream polled"), (1, "x staged"), (2, "A signal
         (4, "unique"), (7, "items done"), (13, "shared rows"), (8, "items seen"), (9, "h staged"), (10, "down done"),
         (12, "combine start"), (15, "shx seen"), (6, "stream stored"), (11, "layer end")]
 EXTRA = [(2, "poll start"), (1, "first poll back"), (4, "dense done"), (8, "logits in"), (9, "probs"),
-         (10, "topk done"), (7, "first item"), (3, "combine summed"), (0, "stream acked"),
+         (10, "topk done"), (5, "item loads issued"), (6, "item loads landed"), (14, "item dots"), (7, "first item"), (3, "combine summed"), (0, "stream acked"),
          (11, "down expert 1"), (12, "down expert 2"), (13, "down expert 3")]
 
 

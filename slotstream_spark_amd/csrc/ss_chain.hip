@@ -610,13 +610,30 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
           const SS_G uint32_t* brow = (const SS_G uint32_t*)gp(base + (n < 8 ? rec.gb : rec.ub) + r8 * sb_b);
           uint4 wv[NJG];
           uint32_t sv[NJG], bv[NJG];
+          // The row's scales and biases in 16-byte loads first (four dwords each: a quarter of the requests of
+          // dword loads), then the packed words in chunk order.
+          static_assert(NJG % 4 == 0, "whole 16-byte scale loads");
 #pragma unroll
-          for (int j = 0; j < NJG; ++j) {
-            wv[j] = ldg16(wrow + 64 * j);
-            sv[j] = srow[j];
-            bv[j] = brow[j];
+          for (int j4 = 0; j4 < NJG / 4; ++j4) {
+            const ss_u32x4 s4 = *(const SS_G ss_u32x4*)(srow + 4 * j4), b4 = *(const SS_G ss_u32x4*)(brow + 4 * j4);
+            sv[4 * j4] = s4.x;
+            sv[4 * j4 + 1] = s4.y;
+            sv[4 * j4 + 2] = s4.z;
+            sv[4 * j4 + 3] = s4.w;
+            bv[4 * j4] = b4.x;
+            bv[4 * j4 + 1] = b4.y;
+            bv[4 * j4 + 2] = b4.z;
+            bv[4 * j4 + 3] = b4.w;
           }
+#pragma unroll
+          for (int j = 0; j < NJG; ++j) wv[j] = ldg16(wrow + 64 * j);
           __builtin_amdgcn_sched_barrier(0);
+          if (NJG == 16 && tr && item == gw) {
+            // diagnostics (traced layers of the BASELINE shape only): the item's loads issued, then landed
+            SS_TRACE(16 + 5);
+            __builtin_amdgcn_s_waitcnt(0);
+            SS_TRACE(16 + 6);
+          }
           float acc[NTK];
 #pragma unroll
           for (int r = 0; r < NTK; ++r) acc[r] = 0.f;
@@ -656,6 +673,7 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
               }
             }
           }
+          if (NJG == 16 && tr && item == gw) SS_TRACE(16 + 14);  // the item's dots formed
           if constexpr (!LDS_SWIGLU) {
             // Every lane of column n now gets row n's dot of each token (gate row n for n < 8, up row n - 8 above),
             // and the lanes n < 8 form h = silu(gate) * up of their row c = n from the up dot 8 lanes up: no LDS.
