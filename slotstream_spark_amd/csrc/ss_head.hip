@@ -206,6 +206,7 @@ struct HeadGemvArgs {
 
 constexpr int kHeadLds = 4 * 8192;  // bf16 elements of the staged source rows (Sl n <= 32768)
 
+template <int CPG, bool INJ>
 __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
   extern __shared__ uint4 xs[];  // the staged source rows: Sl n bf16 (sized per launch)
   __shared__ float rs[64];
@@ -224,8 +225,42 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
   const bool second = !a.mean_out && nrow >= a.g.N;
   const bool has_row = a.mean_out ? nrow < a.mean_H : nrow < a.g.N + a.N2;
   const int wn = second ? nrow - a.g.N : nrow;
-  const uint4* wr = reinterpret_cast<const uint4*>((second ? a.w2 : a.g.w) + (size_t)(has_row ? wn : 0) * a.K);
+  // a wave without a row reads row 0 of w (w2 may be absent), whose loads are never used
+  const uint4* wr = reinterpret_cast<const uint4*>((second && has_row ? a.w2 : a.g.w) + (size_t)(has_row ? wn : 0) * a.K);
   constexpr int kUB = 16;  // a lane's 16 weight chunks of a K = 8192 row in flight at once
+  // CPG > 0: the grouped pre-step (n and G multiples of 512, at most four norm groups of CPG chunks per lane, norm
+  // weights given): wave w takes norm group w, whose chunks in lane l are i = l + 64 u, u = w CPG .. w CPG + CPG - 1
+  // (the rmsnorm_groups order), all requested before the weight rows and without branches, so that the group's
+  // arithmetic waits for its own loads only. Waves past the last group repeat its loads and drop them.
+  constexpr int CQ = CPG > 0 ? CPG : 1;
+  uint4 xg[CQ], nwg[CQ], yg[INJ ? CQ : 1];
+  float gg[INJ ? CQ : 1];
+  bool bad_row = false;
+  if constexpr (CPG > 0) {
+    const int ng = E / a.G, gw = w < ng ? w : ng - 1;
+    const int s2 = (512 * gw * CPG) / n;  // a group lies in one source row
+    int64_t row = s2;
+    if (a.src_idx) {
+      row = a.src_idx[s2];
+      bad_row = row < 0 || row >= a.n_src;
+      if (bad_row) {
+        if (lane == 0 && blockIdx.x == 0 && w < ng) ss_raise(a.err, SS_ERR_TOKEN);
+        row = 0;
+      }
+    }
+    const int Hy = INJ ? n / a.inj_hc : n;
+#pragma unroll
+    for (int m = 0; m < CPG; ++m) {
+      const int u = gw * CPG + m, j8 = 512 * u + 8 * lane - s2 * n;
+      xg[m] = reinterpret_cast<const uint4*>(a.src + row * n)[j8 >> 3];
+      nwg[m] = reinterpret_cast<const uint4*>(a.norm_w)[j8 >> 3];
+      if constexpr (INJ) {
+        const int c = (512 * u - s2 * n) / Hy;
+        yg[m] = reinterpret_cast<const uint4*>(a.inj_y + (size_t)s2 * Hy)[(j8 - c * Hy) >> 3];
+        gg[m] = ss_bf16_to_f32(a.inj[s2 * a.inj_hc + c]);
+      }
+    }
+  }
   uint4 wq0[kUB];
   if (a.mean_out) {
 #pragma unroll
@@ -234,99 +269,147 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
                    ? reinterpret_cast<const uint4*>(a.g.w + ((size_t)c * a.mean_H + nrow) * a.K)[lane]
                    : make_uint4(0u, 0u, 0u, 0u);
   } else {
+    // clamped inside the row, so that every load is issued (a chunk past K is never used)
 #pragma unroll
-    for (int u = 0; u < kUB; ++u)
-      wq0[u] = has_row && lane + 64 * u < k8n ? wr[lane + 64 * u] : make_uint4(0u, 0u, 0u, 0u);
+    for (int u = 0; u < kUB; ++u) wq0[u] = wr[lane + 64 * u < k8n ? lane + 64 * u : k8n - 1];
   }
-  // the norm weights of this thread's chunks, with the source loads
-  uint4 nwq[kHeadLds / 8 / 256];
-  // pre-step 1: the source rows (and the injection) into LDS, h out from workgroup 0 (chunk i = tid + 256 k:
-  // unrolled, so that the norm weights stay in registers)
+  if constexpr (CPG > 0) {
+    if (w < E / a.G) {
 #pragma unroll
-  for (int kq = 0; kq < kHeadLds / 8 / 256; ++kq) {
-    const int i = tid + 256 * kq;
-    if (i >= E8) break;
-    if (a.G > 0) {
-      const int j = (i << 3) - ((i << 3) / n) * n;
-      nwq[kq] = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w)[j >> 3]
-                         : make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
-    }
-    const int s = (i << 3) / n, j8 = (i << 3) - s * n;
-    int64_t row = s;
-    if (a.src_idx) {
-      row = a.src_idx[s];
-      if (row < 0 || row >= a.n_src) {
-        if (j8 == 0) ss_raise(a.err, SS_ERR_TOKEN);
-        row = -1;
-      }
-    }
-    uint4 v = row >= 0 ? reinterpret_cast<const uint4*>(a.src + row * n)[j8 >> 3] : make_uint4(0u, 0u, 0u, 0u);
-    if (a.inj) {
-      const int Hy = n / a.inj_hc, c = j8 / Hy;
-      const uint4 yv = reinterpret_cast<const uint4*>(a.inj_y + (size_t)s * Hy)[(j8 - c * Hy) >> 3];
-      const float g = ss_bf16_to_f32(a.inj[s * a.inj_hc + c]);
-      const uint32_t hv[4] = {v.x, v.y, v.z, v.w}, yy[4] = {yv.x, yv.y, yv.z, yv.w};
-      uint32_t o[4];
+      for (int m = 0; m < CPG; ++m) {
+        if (bad_row) xg[m] = make_uint4(0u, 0u, 0u, 0u);
+        if constexpr (INJ) {
+          const uint32_t hv[4] = {xg[m].x, xg[m].y, xg[m].z, xg[m].w}, yy[4] = {yg[m].x, yg[m].y, yg[m].z, yg[m].w};
+          uint32_t o[4];
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float t0 = ss_round_bf16(lo16(yy[q]) * g), t1 = ss_round_bf16(hi16(yy[q]) * g);
-        o[q] = ss_f32_to_bf16(lo16(hv[q]) + t0) | (ss_f32_to_bf16(hi16(hv[q]) + t1) << 16);
-      }
-      v = make_uint4(o[0], o[1], o[2], o[3]);
-    }
-    xs[i] = v;
-    if (a.h_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.h_out)[i] = v;
-  }
-  __syncthreads();
-  HG_TRACE(1);
-  if (a.G > 0) {
-    // pre-step 2: r of every group (one wave per group, rmsnorm_groups_kernel's order)
-    const int ng = E / a.G, g8 = a.G >> 3;
-    for (int g = w; g < ng; g += 4) {
-      float acc = 0.f;
-      // the LDS reads of 16 chunks issued before their FMAs (which keep the lane's chunk order)
-      for (int k0 = lane; k0 < g8; k0 += 64 * 16) {
-        uint4 q[16];
-#pragma unroll
-        for (int u = 0; u < 16; ++u) q[u] = k0 + 64 * u < g8 ? xs[g * g8 + k0 + 64 * u] : make_uint4(0u, 0u, 0u, 0u);
-#pragma unroll
-        for (int u = 0; u < 16; ++u) {
-          if (k0 + 64 * u < g8) {
-            const uint32_t v[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              const float e0 = lo16(v[c]), e1 = hi16(v[c]);
-              acc = fmaf(e0, e0, acc);
-              acc = fmaf(e1, e1, acc);
-            }
+          for (int q = 0; q < 4; ++q) {
+            const float t0 = ss_round_bf16(lo16(yy[q]) * gg[m]), t1 = ss_round_bf16(hi16(yy[q]) * gg[m]);
+            o[q] = ss_f32_to_bf16(lo16(hv[q]) + t0) | (ss_f32_to_bf16(hi16(hv[q]) + t1) << 16);
           }
+          xg[m] = make_uint4(o[0], o[1], o[2], o[3]);
+        }
+      }
+      float acc = 0.f;
+#pragma unroll
+      for (int m = 0; m < CPG; ++m) {
+        if (a.h_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.h_out)[64 * (w * CPG + m) + lane] = xg[m];
+        const uint32_t v[4] = {xg[m].x, xg[m].y, xg[m].z, xg[m].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const float e0 = lo16(v[c]), e1 = hi16(v[c]);
+          acc = fmaf(e0, e0, acc);
+          acc = fmaf(e1, e1, acc);
         }
       }
       const float r = 1.f / sqrtf(ss_wave_sum(acc) / (float)a.G + a.eps);
-      if (lane == 0) rs[g] = r;
+#pragma unroll
+      for (int m = 0; m < CPG; ++m) {
+        const uint32_t v[4] = {xg[m].x, xg[m].y, xg[m].z, xg[m].w};
+        const uint32_t wv[4] = {nwg[m].x, nwg[m].y, nwg[m].z, nwg[m].w};
+        uint32_t o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          o[c] = ss_f32_to_bf16((lo16(v[c]) * r) * lo16(wv[c])) | (ss_f32_to_bf16((hi16(v[c]) * r) * hi16(wv[c])) << 16);
+        const uint4 x = make_uint4(o[0], o[1], o[2], o[3]);
+        const int i = 64 * (w * CPG + m) + lane;
+        xs[i] = x;
+        if (a.x_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.x_out)[i] = x;
+      }
     }
     __syncthreads();
-    HG_TRACE(2);
-    // pre-step 3: x = bf16((h * r) * norm_w) in place, x out from workgroup 0
+    HG_TRACE(3);
+  } else {
+    (void)bad_row;
+    // the norm weights of this thread's chunks, with the source loads
+    uint4 nwq[kHeadLds / 8 / 256];
+    // pre-step 1: the source rows (and the injection) into LDS, h out from workgroup 0 (chunk i = tid + 256 k:
+    // unrolled, so that the norm weights stay in registers)
 #pragma unroll
     for (int kq = 0; kq < kHeadLds / 8 / 256; ++kq) {
       const int i = tid + 256 * kq;
       if (i >= E8) break;
-      const int e = i << 3, g = e / a.G;
-      const float r = rs[g];
-      const uint4 q = xs[i];
-      const uint4 b = nwq[kq];
-      const uint32_t v[4] = {q.x, q.y, q.z, q.w}, wv[4] = {b.x, b.y, b.z, b.w};
-      uint32_t o[4];
+      if (a.G > 0) {
+        const int j = (i << 3) - ((i << 3) / n) * n;
+        nwq[kq] = a.norm_w ? reinterpret_cast<const uint4*>(a.norm_w)[j >> 3]
+                           : make_uint4(0x3F803F80u, 0x3F803F80u, 0x3F803F80u, 0x3F803F80u);
+      }
+      const int s = (i << 3) / n, j8 = (i << 3) - s * n;
+      int64_t row = s;
+      if (a.src_idx) {
+        row = a.src_idx[s];
+        if (row < 0 || row >= a.n_src) {
+          if (j8 == 0) ss_raise(a.err, SS_ERR_TOKEN);
+          row = -1;
+        }
+      }
+      uint4 v = row >= 0 ? reinterpret_cast<const uint4*>(a.src + row * n)[j8 >> 3] : make_uint4(0u, 0u, 0u, 0u);
+      if (a.inj) {
+        const int Hy = n / a.inj_hc, c = j8 / Hy;
+        const uint4 yv = reinterpret_cast<const uint4*>(a.inj_y + (size_t)s * Hy)[(j8 - c * Hy) >> 3];
+        const float g = ss_bf16_to_f32(a.inj[s * a.inj_hc + c]);
+        const uint32_t hv[4] = {v.x, v.y, v.z, v.w}, yy[4] = {yv.x, yv.y, yv.z, yv.w};
+        uint32_t o[4];
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
-        o[c] = ss_f32_to_bf16((lo16(v[c]) * r) * lo16(wv[c])) | (ss_f32_to_bf16((hi16(v[c]) * r) * hi16(wv[c])) << 16);
-      const uint4 x = make_uint4(o[0], o[1], o[2], o[3]);
-      xs[i] = x;
-      if (a.x_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.x_out)[i] = x;
+        for (int q = 0; q < 4; ++q) {
+          const float t0 = ss_round_bf16(lo16(yy[q]) * g), t1 = ss_round_bf16(hi16(yy[q]) * g);
+          o[q] = ss_f32_to_bf16(lo16(hv[q]) + t0) | (ss_f32_to_bf16(hi16(hv[q]) + t1) << 16);
+        }
+        v = make_uint4(o[0], o[1], o[2], o[3]);
+      }
+      xs[i] = v;
+      if (a.h_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.h_out)[i] = v;
     }
     __syncthreads();
-    HG_TRACE(3);
+    HG_TRACE(1);
+    if (a.G > 0) {
+      // pre-step 2: r of every group (one wave per group, rmsnorm_groups_kernel's order)
+      const int ng = E / a.G, g8 = a.G >> 3;
+      for (int g = w; g < ng; g += 4) {
+        float acc = 0.f;
+        // the LDS reads of 16 chunks issued before their FMAs (which keep the lane's chunk order)
+        for (int k0 = lane; k0 < g8; k0 += 64 * 16) {
+          uint4 q[16];
+#pragma unroll
+          for (int u = 0; u < 16; ++u) q[u] = k0 + 64 * u < g8 ? xs[g * g8 + k0 + 64 * u] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+          for (int u = 0; u < 16; ++u) {
+            if (k0 + 64 * u < g8) {
+              const uint32_t v[4] = {q[u].x, q[u].y, q[u].z, q[u].w};
+#pragma unroll
+              for (int c = 0; c < 4; ++c) {
+                const float e0 = lo16(v[c]), e1 = hi16(v[c]);
+                acc = fmaf(e0, e0, acc);
+                acc = fmaf(e1, e1, acc);
+              }
+            }
+          }
+        }
+        const float r = 1.f / sqrtf(ss_wave_sum(acc) / (float)a.G + a.eps);
+        if (lane == 0) rs[g] = r;
+      }
+      __syncthreads();
+      HG_TRACE(2);
+      // pre-step 3: x = bf16((h * r) * norm_w) in place, x out from workgroup 0
+#pragma unroll
+      for (int kq = 0; kq < kHeadLds / 8 / 256; ++kq) {
+        const int i = tid + 256 * kq;
+        if (i >= E8) break;
+        const int e = i << 3, g = e / a.G;
+        const float r = rs[g];
+        const uint4 q = xs[i];
+        const uint4 b = nwq[kq];
+        const uint32_t v[4] = {q.x, q.y, q.z, q.w}, wv[4] = {b.x, b.y, b.z, b.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          o[c] = ss_f32_to_bf16((lo16(v[c]) * r) * lo16(wv[c])) | (ss_f32_to_bf16((hi16(v[c]) * r) * hi16(wv[c])) << 16);
+        const uint4 x = make_uint4(o[0], o[1], o[2], o[3]);
+        xs[i] = x;
+        if (a.x_out && blockIdx.x == 0) reinterpret_cast<uint4*>(a.x_out)[i] = x;
+      }
+      __syncthreads();
+      HG_TRACE(3);
+    }
   }
   // the GEMV: one wave per weight row, the launch's x rows from LDS
   if (!has_row) return;  // whole waves; no workgroup barrier follows
@@ -507,9 +590,6 @@ hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st) {
   int per = kDR * in.K / in.n < kHeadLds / in.n ? kDR * in.K / in.n : kHeadLds / in.n;
   if (in.G > 0 && 64 * in.G / in.n < per) per = 64 * in.G / in.n;
   if (per < 1) return hipErrorInvalidValue;
-  KernelCfg cfg;  // allows the largest staging (64 KB) as dynamic LDS, once per device
-  hipError_t ce = kernel_cfg(reinterpret_cast<const void*>(head_gemv_kernel), 256, (size_t)kHeadLds * 2, &cfg);
-  if (ce != hipSuccess) return ce;
   HeadGemvArgs a{};
   a.src_idx = nullptr;
   a.n_src = in.n_src;
@@ -546,8 +626,17 @@ hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st) {
     a.x_out = in.x_out ? in.x_out + (size_t)s0 * in.n : nullptr;
     a.mean_hn = in.mean_hn ? in.mean_hn + (size_t)s0 * in.n : nullptr;
     a.mean_out = in.mean_out ? in.mean_out + (size_t)s0 * xr * in.mean_H : nullptr;
+    // the grouped pre-step: every norm group of this launch to one wave (at most four groups of 2048 elements, norm
+    // weights given, an injection width of whole 512-element pieces). Larger groups stay staged: one wave over a
+    // group of 8192 measured twice the staged time (18 against 9.5 us for the head's fc_hidden launch).
+    bool grouped = !in.mean_out && in.G == 2048 && in.norm_w && in.n % 512 == 0 && a.Sl * in.n <= 4 * in.G &&
+                   (!in.inj || (in.n / in.inj_hc) % 512 == 0);
+    auto kern = !grouped ? head_gemv_kernel<0, false> : (in.inj ? head_gemv_kernel<4, true> : head_gemv_kernel<4, false>);
+    KernelCfg cfg;  // allows the largest staging (64 KB) as dynamic LDS, once per device and instantiation
+    hipError_t ce = kernel_cfg(reinterpret_cast<const void*>(kern), 256, (size_t)kHeadLds * 2, &cfg);
+    if (ce != hipSuccess) return ce;
     const int grid = in.mean_out ? (in.mean_H + 3) / 4 : (in.N + in.N2 + 3) / 4;
-    hipLaunchKernelGGL(head_gemv_kernel, dim3((unsigned)grid), dim3(256), (size_t)a.Sl * in.n * 2, st, a);
+    hipLaunchKernelGGL(kern, dim3((unsigned)grid), dim3(256), (size_t)a.Sl * in.n * 2, st, a);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

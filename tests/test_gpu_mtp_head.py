@@ -144,7 +144,12 @@ def _np_weights(hw):
             "mlp_hc": hcd(hw.mlp_hc), "mixer_hc": hcd(hw.mixer_hc)}
 
 
-@pytest.mark.parametrize("S,n,K,group,inject,two", [(1, 8192, 8192, 2048, False, True), (3, 8192, 8192, 2048, True, False),
+# Launches with norm groups of 2048 elements, at most four per launch, take the grouped pre-step (the first,
+# second, fourth and seventh shapes here); the others the staged one.
+@pytest.mark.parametrize("S,n,K,group,inject,two", [(1, 8192, 8192, 2048, False, True), (1, 8192, 8192, 2048, True, False),
+                                                     (1, 8192, 2048, 8192, False, False), (2, 2048, 2048, 2048, True, True),
+                                                     (3, 2048, 2048, 512, False, False),
+                                                     (3, 8192, 8192, 2048, True, False),
                                                      (1, 2048, 2048, 2048, False, False), (4, 8192, 2048, 8192, False,
                                                                                               False),
                                                      (2, 520, 520, 40, False, True), (5, 96, 32, 32, True, False)])
