@@ -206,7 +206,7 @@ struct HeadGemvArgs {
 
 constexpr int kHeadLds = 4 * 8192;  // bf16 elements of the staged source rows (Sl n <= 32768)
 
-template <int CPG, bool INJ>
+template <int CPG, bool INJ, int KU>
 __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
   extern __shared__ uint4 xs[];  // the staged source rows: Sl n bf16 (sized per launch)
   __shared__ float rs[64];
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
   const bool second = !a.mean_out && nrow >= a.g.N;
   const bool has_row = a.mean_out ? nrow < a.mean_H : nrow < a.g.N + a.N2;
   const int wn = second ? nrow - a.g.N : nrow;
-  // a wave without a row reads row 0 of w (w2 may be absent), whose loads are never used
+  // a wave without a row points at row 0 of w (w2 may be absent)
   const uint4* wr = reinterpret_cast<const uint4*>((second && has_row ? a.w2 : a.g.w) + (size_t)(has_row ? wn : 0) * a.K);
   constexpr int kUB = 16;  // a lane's 16 weight chunks of a K = 8192 row in flight at once
   // CPG > 0: the grouped pre-step (n and G multiples of 512, at most four norm groups of CPG chunks per lane, norm
@@ -268,10 +268,14 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
       wq0[c] = has_row && lane < k8n
                    ? reinterpret_cast<const uint4*>(a.g.w + ((size_t)c * a.mean_H + nrow) * a.K)[lane]
                    : make_uint4(0u, 0u, 0u, 0u);
-  } else {
-    // clamped inside the row, so that every load is issued (a chunk past K is never used)
+  } else if constexpr (CPG > 0) {
+    // K = 512 KU: every chunk in range, so the loads need no branch (chunks KU .. kUB - 1 are never used)
 #pragma unroll
-    for (int u = 0; u < kUB; ++u) wq0[u] = wr[lane + 64 * u < k8n ? lane + 64 * u : k8n - 1];
+    for (int u = 0; u < KU; ++u) wq0[u] = wr[lane + 64 * u];
+  } else {
+#pragma unroll
+    for (int u = 0; u < kUB; ++u)
+      wq0[u] = has_row && lane + 64 * u < k8n ? wr[lane + 64 * u] : make_uint4(0u, 0u, 0u, 0u);
   }
   if constexpr (CPG > 0) {
     if (w < E / a.G) {
@@ -627,11 +631,14 @@ hipError_t launch_head_gemv(const HeadGemvIn& in, hipStream_t st) {
     a.mean_hn = in.mean_hn ? in.mean_hn + (size_t)s0 * in.n : nullptr;
     a.mean_out = in.mean_out ? in.mean_out + (size_t)s0 * xr * in.mean_H : nullptr;
     // the grouped pre-step: every norm group of this launch to one wave (at most four groups of 2048 elements, norm
-    // weights given, an injection width of whole 512-element pieces). Larger groups stay staged: one wave over a
-    // group of 8192 measured twice the staged time (18 against 9.5 us for the head's fc_hidden launch).
-    bool grouped = !in.mean_out && in.G == 2048 && in.norm_w && in.n % 512 == 0 && a.Sl * in.n <= 4 * in.G &&
-                   (!in.inj || (in.n / in.inj_hc) % 512 == 0);
-    auto kern = !grouped ? head_gemv_kernel<0, false> : (in.inj ? head_gemv_kernel<4, true> : head_gemv_kernel<4, false>);
+    // weights given, K 2048 or 8192, an injection width of whole 512-element pieces). Larger groups stay staged: one
+    // wave over a group of 8192 measured slower than the staged step (10.5 against 9.6 us for the head's fc_hidden
+    // launch).
+    const bool grouped = !in.mean_out && in.G == 2048 && in.norm_w && in.n % 512 == 0 && a.Sl * in.n <= 4 * in.G &&
+                         (in.K == 2048 || in.K == 8192) && (!in.inj || (in.n / in.inj_hc) % 512 == 0);
+    auto kern = !grouped       ? head_gemv_kernel<0, false, 16>
+                : in.K == 2048 ? (in.inj ? head_gemv_kernel<4, true, 4> : head_gemv_kernel<4, false, 4>)
+                               : (in.inj ? head_gemv_kernel<4, true, 16> : head_gemv_kernel<4, false, 16>);
     KernelCfg cfg;  // allows the largest staging (64 KB) as dynamic LDS, once per device and instantiation
     hipError_t ce = kernel_cfg(reinterpret_cast<const void*>(kern), 256, (size_t)kHeadLds * 2, &cfg);
     if (ce != hipSuccess) return ce;
