@@ -361,7 +361,8 @@ int64_t ssmoe_lm_head_greedy_workspace_bytes(int D, int N);
  * round reads no logits. The logits are lin's result, lin(final, lm_head).float() (runtime/graphs.py:202): for a bf16
  * x the fp32 dot rounded to bf16, for an fp32 x the dot itself. out int32 [D+5] as ssmoe_accept_greedy (n_accept,
  * n_emit, 0, flags 1 = non-finite row, 2 = draft out of range, tokens). logits fp32 [D+1][N] (those values) is
- * written too when non-null. 0 <= D <= 60. */
+ * written too when non-null. 0 <= D <= 60. The workspace must be zero before the first call; every call leaves it
+ * zero (the GEMV's last workgroup forms the round and clears the keys: one launch per 4 rows, nothing after). */
 int ssmoe_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
                          const uint16_t* b, int N, const int32_t* drafts, void* workspace, int64_t workspace_bytes,
                          float* logits, int32_t* out, void* stream);
@@ -386,7 +387,8 @@ int64_t ssmoe_lm_head_argmax_workspace_bytes(int R, int N);
  * logits at engine/mtp.py:232-236). round_bf16 != 0 takes the argmax over the logits rounded to bf16 (lin returns
  * the dtype of x, bf16 for the head); ties and NaN as torch.argmax (the first maximal index; NaN counts as the
  * maximum). ids int32 [R] on the device; logits fp32 [R][N] (the values ranked) is written too when non-null.
- * 1 <= R <= 64, K as ssmoe_gemv_affine4. */
+ * 1 <= R <= 64, K as ssmoe_gemv_affine4. The workspace must be zero before the first call; every call leaves it
+ * zero. */
 int ssmoe_lm_head_argmax(const void* x, int x_f32, int R, int K, const int32_t* q, const uint16_t* s,
                          const uint16_t* b, int N, int round_bf16, void* workspace, int64_t workspace_bytes,
                          float* logits, int32_t* ids, void* stream);

@@ -30,10 +30,46 @@ struct GemvArgs {
   const uint16_t* s;
   const uint16_t* b;
   float* y;         // [R][N] or null
-  uint64_t* rkey;   // [R] argmax keys, combined with atomic max (zeroed before the launch), or null
+  uint64_t* rkey;   // [R] argmax keys, combined with atomic max (zero on entry), or null
   int* rbad;        // [R] non-finite flags, combined with atomic or (with rkey)
   int key_bf16;     // 1: the logits are lin's bf16 result: keys and y take the dot rounded to bf16
+  // With rkey: the workgroups count their arrivals on `arrive` (zero on entry); the last one finishes the call when
+  // `fin` (the call's last launch): the ids of all R_all rows (ids non-null) or the greedy round (gout non-null),
+  // then zeroes every row's key and flag. The last workgroup of every launch zeroes `arrive`.
+  int* arrive;
+  int fin, R_all;
+  uint64_t* rkey0;
+  int* rbad0;
+  int32_t* ids;
+  const int32_t* drafts;
+  int32_t* gout;
 };
+
+// The greedy round (engine/generate.py:208-229 at temperature 0) from the rows' argmax keys: row i's token is its
+// argmax; a row holding a non-finite logit ends the round before it (flag 1); drafts are accepted while equal. out as
+// ssmoe_accept_greedy. One thread.
+SS_DEV void greedy_decide(const uint64_t* rkey, const int* rbad, const int32_t* drafts, int D, int V, int32_t* out) {
+  int na = 0, ne = 0, fl = 0;
+  for (int i = 0; i <= D; ++i) {
+    if (rbad[i]) {
+      fl |= 1;
+      break;
+    }
+    const int tok = (int)(0xFFFFFFFFu - (uint32_t)rkey[i]);
+    out[4 + i] = tok;
+    ne = i + 1;
+    if (i == D) break;
+    const int d = drafts[i];
+    if (d < 0 || d >= V) fl |= 2;
+    if (tok != d) break;
+    na = i + 1;
+  }
+  for (int i = ne; i <= D; ++i) out[4 + i] = -1;
+  out[0] = na;
+  out[1] = ne;
+  out[2] = 0;
+  out[3] = fl;
+}
 
 SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 SS_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
@@ -266,53 +302,36 @@ __global__ __launch_bounds__(256, 2) void gemv_affine4_kernel(GemvArgs a) {
         m = wkey[ww][tid] > m ? wkey[ww][tid] : m;
         b |= wbad[ww];
       }
-      atomicMax(reinterpret_cast<unsigned long long*>(a.rkey + tid), (unsigned long long)m);
-      if ((b >> tid) & 1u) atomicOr(a.rbad + tid, 1);
+      __hip_atomic_fetch_max(reinterpret_cast<unsigned long long*>(a.rkey + tid), (unsigned long long)m,
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((b >> tid) & 1u) __hip_atomic_fetch_or(a.rbad + tid, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);  // the combines are performed (acknowledged) before the arrival below
+    }
+    // Every key, flag and the count are touched only by agent-scope atomics, which are performed at one coherent
+    // point: a combine acknowledged before its workgroup's arrival is seen by the last workgroup's loads, with no
+    // cache writeback or invalidation.
+    __shared__ int s_last;
+    __syncthreads();
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(a.arrive, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (int)gridDim.x - 1;
+    __syncthreads();
+    if (s_last) {
+      if (a.fin) {
+        __shared__ uint64_t fkey[64];
+        __shared__ int fbad[64];
+        if (tid < a.R_all) {
+          fkey[tid] = __hip_atomic_load(a.rkey0 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          fbad[tid] = __hip_atomic_load(a.rbad0 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (a.ids) a.ids[tid] = (int32_t)(0xFFFFFFFFu - (uint32_t)fkey[tid]);
+          __hip_atomic_store(a.rkey0 + tid, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(a.rbad0 + tid, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (a.gout && tid == 0) greedy_decide(fkey, fbad, a.drafts, a.R_all - 1, a.N, a.gout);
+      }
+      if (tid == 0) __hip_atomic_store(a.arrive, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-}
-
-// Zeroes the per-row argmax keys and flags before the GEMV combines into them (a kernel, not a memset, so the
-// launch sequence is safe to capture).
-__global__ void gemv_key_init_kernel(uint64_t* rkey, int* rbad, int R) {
-  const int t = threadIdx.x;
-  if (t < R) {
-    rkey[t] = 0;
-    rbad[t] = 0;
-  }
-}
-
-// The greedy round (engine/generate.py:208-229 at temperature 0): row i's token is its argmax; a row holding a
-// non-finite logit ends the round before it (flag 1); drafts are accepted while equal. out as ssmoe_accept_greedy.
-__global__ void gemv_greedy_decide_kernel(const uint64_t* rkey, const int* rbad, const int32_t* drafts, int D, int V,
-                                          int32_t* out) {
-  if (threadIdx.x != 0) return;
-  int na = 0, ne = 0, fl = 0;
-  for (int i = 0; i <= D; ++i) {
-    if (rbad[i]) {
-      fl |= 1;
-      break;
-    }
-    const int tok = (int)(0xFFFFFFFFu - (uint32_t)rkey[i]);
-    out[4 + i] = tok;
-    ne = i + 1;
-    if (i == D) break;
-    const int d = drafts[i];
-    if (d < 0 || d >= V) fl |= 2;
-    if (tok != d) break;
-    na = i + 1;
-  }
-  for (int i = ne; i <= D; ++i) out[4 + i] = -1;
-  out[0] = na;
-  out[1] = ne;
-  out[2] = 0;
-  out[3] = fl;
-}
-
-// ids[r] = the index the argmax key of row r names.
-__global__ void gemv_argmax_ids_kernel(const uint64_t* rkey, int R, int32_t* ids) {
-  const int t = threadIdx.x;
-  if (t < R) ids[t] = (int32_t)(0xFFFFFFFFu - (uint32_t)rkey[t]);
 }
 
 namespace {
@@ -370,9 +389,11 @@ hipError_t launch_gemv_affine4(const void* x, int x_f32, int R, int K, const int
   return hipSuccess;
 }
 
+// Workspace of the argmax and greedy launches: keys [R] (8 bytes), flags [R], the arrival count; zero before the
+// first call, and every call leaves it zero.
 int64_t lm_head_greedy_workspace_bytes(int D, int N) {
   (void)N;
-  return ((int64_t)(D + 1) * 8 + 255) / 256 * 256 + ((int64_t)(D + 1) * 4 + 255) / 256 * 256;
+  return ((int64_t)(D + 1) * 8 + 255) / 256 * 256 + ((int64_t)(D + 1) * 4 + 255) / 256 * 256 + 256;
 }
 
 hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const int32_t* q, const uint16_t* s,
@@ -380,10 +401,16 @@ hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const i
                                  int32_t* out, hipStream_t st) {
   uint8_t* w = static_cast<uint8_t*>(work);
   uint64_t* rkey = reinterpret_cast<uint64_t*>(w);
-  int* rbad = reinterpret_cast<int*>(w + ((int64_t)(D + 1) * 8 + 255) / 256 * 256);
+  const int64_t ob = ((int64_t)(D + 1) * 8 + 255) / 256 * 256;
+  int* rbad = reinterpret_cast<int*>(w + ob);
   const int R = D + 1;
-  hipLaunchKernelGGL(gemv_key_init_kernel, dim3(1), dim3(64), 0, st, rkey, rbad, R);
   GemvArgs a{};
+  a.arrive = reinterpret_cast<int*>(w + ob + ((int64_t)R * 4 + 255) / 256 * 256);
+  a.R_all = R;
+  a.rkey0 = rkey;
+  a.rbad0 = rbad;
+  a.drafts = drafts;
+  a.gout = out;
   a.K = K;
   a.N = N;
   a.ntiles = (int)gemv_tiles(N);
@@ -398,11 +425,11 @@ hipError_t launch_lm_head_greedy(const void* x, int x_f32, int D, int K, const i
     a.y = logits ? logits + (size_t)r0 * N : nullptr;
     a.rkey = rkey + r0;
     a.rbad = rbad + r0;
+    a.fin = r0 + kGR >= R;
     hipError_t e = launch_chunk(a, x_f32, st);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(gemv_greedy_decide_kernel, dim3(1), dim3(64), 0, st, rkey, rbad, drafts, D, N, out);
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 int64_t lm_head_pq_workspace_bytes(int D, int N) { return (accept_work_floats(D, N) * 4 + 255) / 256 * 256; }
@@ -446,9 +473,14 @@ hipError_t launch_lm_head_argmax(const void* x, int x_f32, int R, int K, const i
                                  hipStream_t st) {
   uint8_t* w = static_cast<uint8_t*>(work);
   uint64_t* rkey = reinterpret_cast<uint64_t*>(w);
-  int* rbad = reinterpret_cast<int*>(w + ((int64_t)R * 8 + 255) / 256 * 256);
-  hipLaunchKernelGGL(gemv_key_init_kernel, dim3(1), dim3(64), 0, st, rkey, rbad, R);
+  const int64_t ob = ((int64_t)R * 8 + 255) / 256 * 256;
+  int* rbad = reinterpret_cast<int*>(w + ob);
   GemvArgs a{};
+  a.arrive = reinterpret_cast<int*>(w + ob + ((int64_t)R * 4 + 255) / 256 * 256);
+  a.R_all = R;
+  a.rkey0 = rkey;
+  a.rbad0 = rbad;
+  a.ids = ids;
   a.K = K;
   a.N = N;
   a.ntiles = (int)gemv_tiles(N);
@@ -463,11 +495,11 @@ hipError_t launch_lm_head_argmax(const void* x, int x_f32, int R, int K, const i
     a.y = logits ? logits + (size_t)r0 * N : nullptr;
     a.rkey = rkey + r0;
     a.rbad = rbad + r0;
+    a.fin = r0 + kGR >= R;
     hipError_t e = launch_chunk(a, x_f32, st);
     if (e != hipSuccess) return e;
   }
-  hipLaunchKernelGGL(gemv_argmax_ids_kernel, dim3(1), dim3(64), 0, st, rkey, R, ids);
-  return hipGetLastError();
+  return hipSuccess;
 }
 
 }  // namespace ss

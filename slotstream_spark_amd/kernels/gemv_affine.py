@@ -91,7 +91,7 @@ class LMHeadGreedy:
         nb = int(_lib.lib().ssmoe_lm_head_greedy_workspace_bytes(depth, w.n))
         if nb < 0:
             raise ValueError(f"depth must be in [0, 60], got {depth}")
-        self.work = torch.empty(nb, dtype=torch.uint8, device=device)
+        self.work = torch.zeros(nb, dtype=torch.uint8, device=device)  # zero before the first call (calls leave it so)
         self.out = torch.empty(depth + 5, dtype=torch.int32, device=device)
 
     def run_async(self, x: torch.Tensor, drafts: torch.Tensor, logits: torch.Tensor | None = None) -> torch.Tensor:
@@ -124,7 +124,7 @@ class LMHeadArgmax:
         nb = int(_lib.lib().ssmoe_lm_head_argmax_workspace_bytes(max_rows, w.n))
         if nb < 0:
             raise ValueError(f"max_rows must be in [1, 64], got {max_rows}")
-        self.work = torch.empty(nb, dtype=torch.uint8, device=device)
+        self.work = torch.zeros(nb, dtype=torch.uint8, device=device)  # zero before the first call (calls leave it so)
 
     def __call__(self, x: torch.Tensor, ids: torch.Tensor | None = None,
                  logits: torch.Tensor | None = None) -> torch.Tensor:
