@@ -40,7 +40,9 @@ def log(msg):
 
 
 def layer_bytes(u: int, t: int) -> int:
-    """Algorithmic HBM bytes of one verify layer."""
+    """Algorithmic HBM bytes of one verify layer: u unique experts' affine 4-bit records (1,769,472 B each at H 2048
+    / I 512), the router (512 x 2048 bf16), the shared expert's three projections (bf16), the shared gate row and
+    the T rows of x read and y written."""
     return u * 1_769_472 + 2_097_152 + 6_291_456 + 4_096 + t * H * 4
 
 
@@ -495,7 +497,7 @@ def ref_decode_leg(steps, dev):
 
 
 def step_leg(pool, weights, biases, steps, dev):
-    """§8(f) row 1: the whole verify round in one HIP graph (engine/step.py MTPStepGraph) at full size: 48 chained
+    """The whole verify round in one HIP graph (engine/step.py MTPStepGraph) at full size: 48 chained
     config-1 layers (residual + RMSNorm between them), the 248,320 x 2048 affine 4-bit lm_head fused with the greedy
     round, and the MTP head's MoE (map layer 48), for depth 1 (T = 2) and depth 3 (T = 4). Timed with HIP events
     around `steps` replays; one int32 result vector per round is the only thing the host would read back."""
@@ -574,7 +576,7 @@ def _lm_head_weight(dev, n=248320, seed=2721):
 
 
 def draft_leg(pool, weights, biases, steps, dev):
-    """§8(a) row 13 / §8(f) row 4: the MTP head's draft chain (engine/mtp.py, attention excluded) at the config-1
+    """The MTP head's draft chain (engine/mtp.py, attention excluded) at the config-1
     shape: hc 4 hyper-connection branches of H 2048 with a 320-wide low rank, the head MoE on map layer 48 (E512
     top-10, shared 512), the 248,320 x 2048 affine 4-bit lm_head argmax; depth 2 (the reference's DEPTH) and 3, one
     HIP graph per chain, timed with HIP events around `steps` replays. Then the greedy speculative loop
@@ -919,8 +921,8 @@ def main():
     ap.add_argument("--copy-calib", action="store_true", help="run 3 x 256 MiB device copies first (PMC scaling)")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one; the multi-GPU "
-                                   "sharding of the path is a design described in DESIGN.md"}))
+        print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one; sharding the path "
+                                   "over several GPUs is designed but not built"}))
         sys.exit(2)
 
     import torch

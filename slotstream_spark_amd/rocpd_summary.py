@@ -2,6 +2,8 @@
 
   python -m slotstream_spark_amd.rocpd_summary kernels RUN_results.db        per-kernel calls / avg / min / max (us)
   python -m slotstream_spark_amd.rocpd_summary counters RUN_results.db [pat]  per-kernel average of each counter
+  python -m slotstream_spark_amd.rocpd_summary grids RUN_results.db [pat]     per kernel and launch shape (workgroups
+                                                                              x threads), names like pat
 """
 from __future__ import annotations
 
@@ -20,6 +22,20 @@ def kernels(db: str) -> str:
     return "\n".join(out)
 
 
+def grids(db: str, pattern: str = "%") -> str:
+    """One line per (kernel, workgroups, threads per workgroup): a kernel launched at several shapes (the draft head's
+    GEMV instantiations) splits into its launch kinds."""
+    c = sqlite3.connect(db)
+    rows = c.execute("""select name, grid_x, workgroup_x, count(*), avg(end - start), min(end - start),
+                               max(end - start) from kernels where name like ? group by name, grid_x, workgroup_x
+                        order by sum(end - start) desc""", (pattern,))
+    out = [f"{'kernel':72s} {'wgs':>6s} {'thr':>4s} {'calls':>6s} {'avg_us':>8s} {'min_us':>8s} {'max_us':>8s}"]
+    for n, gx, wx, cnt, avg, mn, mx in rows:
+        n = n.replace("(anonymous namespace)::", "").replace("ss::", "")
+        out.append(f"{n[:72]:72s} {gx // max(wx, 1):6d} {wx:4d} {cnt:6d} {avg / 1e3:8.2f} {mn / 1e3:8.2f} {mx / 1e3:8.2f}")
+    return "\n".join(out)
+
+
 def counters(db: str, pattern: str = "%") -> str:
     c = sqlite3.connect(db)
     rows = c.execute("""select kernel_name, counter_name, avg(value), min(value), max(value), count(*)
@@ -31,4 +47,5 @@ def counters(db: str, pattern: str = "%") -> str:
 
 if __name__ == "__main__":
     what, db = sys.argv[1], sys.argv[2]
-    print(kernels(db) if what == "kernels" else counters(db, sys.argv[3] if len(sys.argv) > 3 else "%"))
+    pat = sys.argv[3] if len(sys.argv) > 3 else "%"
+    print(kernels(db) if what == "kernels" else grids(db, pat) if what == "grids" else counters(db, pat))
