@@ -651,16 +651,25 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
               for (int i = 0; i < 4; ++i) av4[jj][i] = fp[(size_t)i * 16];
               gxv[jj] = reinterpret_cast<const float4*>(s.gx)[2 * j + my_half];
             }
+            // The JB chunks' MFMA chains interleaved (slice i of every chunk, then slice i + 1), so that a chunk's
+            // dependent MFMAs overlap the other chunks' instead of waiting on each other; each chunk's sum and the
+            // accumulation below keep their order.
+            ss_f32x4 dj[JB];
+#pragma unroll
+            for (int jj = 0; jj < JB; ++jj) dj[jj] = ss_f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+#pragma unroll
+              for (int jj = 0; jj < JB; ++jj) {
+                const int j = j0 + jj;
+                const uint32_t wd = i == 0 ? wv[j].x : i == 1 ? wv[j].y : i == 2 ? wv[j].z : wv[j].w;
+                dj[jj] = ss_mfma(as_v(av4[jj][i]), ss_nibbles_to_bf16(wd), dj[jj]);
+              }
+            }
 #pragma unroll
             for (int jj = 0; jj < JB; ++jj) {
               const int j = j0 + jj;
-              ss_f32x4 d = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-              for (int i = 0; i < 4; ++i) {
-                ss_u32x4 av = as_v(av4[jj][i]);
-                const uint32_t wd = i == 0 ? wv[j].x : i == 1 ? wv[j].y : i == 2 ? wv[j].z : wv[j].w;
-                d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
-              }
+              const ss_f32x4 d = dj[jj];
               const float sf = pick_half(sv[j], my_half);
               const float bf = pick_half(bv[j], my_half);
               const float s16 = sf * kNibbleScale;
@@ -906,16 +915,24 @@ __global__ __launch_bounds__(256) void chain_kernel(ChainArgs a, SsRecord rec) {
             for (int r = 0; r < NTK; ++r) hsv[j][r] = s.hsum[qr[r]][2 * j + my_half];
           }
           float acc[kTBv] = {0.f, 0.f, 0.f, 0.f};
+          // The NJD chunks' MFMA chains interleaved (slice i of every chunk, then slice i + 1); each chunk's sum and
+          // the accumulation below keep their order.
+          ss_f32x4 dj[NJD];
 #pragma unroll
-          for (int j = 0; j < NJD; ++j) {
-            ss_f32x4 d = {0.f, 0.f, 0.f, 0.f};
+          for (int j = 0; j < NJD; ++j) dj[j] = ss_f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
+          for (int i = 0; i < 4; ++i) {
+#pragma unroll
+            for (int j = 0; j < NJD; ++j) {
               ss_u32x4 av = as_v(av4[j][i]);
               if (!STAGED && !am) av = ss_u32x4{0u, 0u, 0u, 0u};
               const uint32_t wd = i == 0 ? wq[j].x : i == 1 ? wq[j].y : i == 2 ? wq[j].z : wq[j].w;
-              d = ss_mfma(av, ss_nibbles_to_bf16(wd), d);
+              dj[j] = ss_mfma(av, ss_nibbles_to_bf16(wd), dj[j]);
             }
+          }
+#pragma unroll
+          for (int j = 0; j < NJD; ++j) {
+            const ss_f32x4 d = dj[j];
             const float sf = pick_half(svw[j], my_half);
             const float bf = pick_half(bvw[j], my_half);
             const float s16 = sf * kNibbleScale;
