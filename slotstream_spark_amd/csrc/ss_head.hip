@@ -170,11 +170,14 @@ __global__ __launch_bounds__(256) void dense_epi_kernel(DenseEpiArgs a) {
 // ---------------------------------------------------------------- the fused head GEMV
 // One launch for what the head otherwise runs as a row gather, hc_inject, an RMSNorm and one or two GEMVs, or a GEMV
 // and the branch mean, with the same bits as those kernels (the same operations in the same order):
-//   pre-step, in every workgroup: the launch's source rows (src rows, or table rows src_idx[s]) into LDS; optionally
+//   pre-step, in every workgroup: the launch's source rows (src rows, or table rows src_idx[s]); optionally
 //   h = bf16(src + bf16(y[s][j % Hy] * inj[s][j / Hy])) (hc_inject); optionally x = bf16((h * r_g) * norm_w) with
 //   r_g = 1 / sqrt(sum over group g of h^2 / G + eps), the sum in rmsnorm_groups_kernel's order (one wave per group:
-//   lane l over the 8-element chunks l, l + 64, .. with fmaf from 0, then the xor butterfly); workgroup 0 writes h
-//   and x out when asked;
+//   lane l over the 8-element chunks l, l + 64, .. with fmaf from 0, then the xor butterfly); x into LDS, and
+//   workgroup 0 writes h and x out when asked. Staged form (CPG = 0): all threads copy the rows (and inject) into
+//   LDS, the group sums read LDS, all threads normalize in place. Grouped form (CPG > 0, groups of CPG 512-element
+//   pieces, at most four): wave w loads, injects, sums and normalizes group w in registers and stores x once;
+//
 //   then the GEMV of dense_epi_kernel over x viewed as R = Sl n / K rows of K (x from LDS): weight rows [0, N) of w
 //   with epilogue epi into out, rows [N, N + N2) of w2 with epi2 into out2;
 //   or, with mean_out, the branch mean of hc_mean_kernel fused behind the GEMV (hc == 4, K <= 512): one wave takes
@@ -218,8 +221,9 @@ __global__ __launch_bounds__(256) void head_gemv_kernel(HeadGemvArgs a) {
   } while (0)
   HG_TRACE(0);
   const int n = a.n, E = a.Sl * n, E8 = E >> 3;
-  // This wave's weight row, and its first kUB chunks requested before the pre-step (they do not depend on x). In
-  // mean mode the wave takes the four branch rows c H + j of one output j instead (K <= 512: one chunk per lane).
+  // This wave's weight row, its first kUB chunks requested before the pre-step's arithmetic (they do not depend on
+  // x). In mean mode the wave takes the four branch rows c H + j of one output j instead (K <= 512: one chunk per
+  // lane).
   const int R = E / a.K, k8n = a.K >> 3;
   const int nrow = blockIdx.x * 4 + w;
   const bool second = !a.mean_out && nrow >= a.g.N;
