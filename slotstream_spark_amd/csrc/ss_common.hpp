@@ -183,6 +183,28 @@ SS_DEV float ss_wave_sum(float v) {
   return ss_uf(ss_butterfly(ss_fu(v), [](uint32_t a, uint32_t b) { return ss_fu(ss_uf(a) + ss_uf(b)); }));
 }
 
+// Two independent ss_wave_sum butterflies with their steps interleaved (each value gets the bits ss_wave_sum gives
+// it; the two exchange chains overlap instead of running back to back).
+SS_DEV void ss_wave_sum2(float& a, float& b) {
+  uint32_t l0, h0, l1, h1;
+  ss_pair<32>(ss_fu(a), l0, h0);
+  ss_pair<32>(ss_fu(b), l1, h1);
+  a = ss_uf(l0) + ss_uf(h0);
+  b = ss_uf(l1) + ss_uf(h1);
+  ss_pair<16>(ss_fu(a), l0, h0);
+  ss_pair<16>(ss_fu(b), l1, h1);
+  a = ss_uf(l0) + ss_uf(h0);
+  b = ss_uf(l1) + ss_uf(h1);
+  a = a + ss_uf(ss_xor_lane<8>(ss_fu(a)));
+  b = b + ss_uf(ss_xor_lane<8>(ss_fu(b)));
+  a = a + ss_uf(ss_xor_lane<4>(ss_fu(a)));
+  b = b + ss_uf(ss_xor_lane<4>(ss_fu(b)));
+  a = a + ss_uf(ss_xor_lane<2>(ss_fu(a)));
+  b = b + ss_uf(ss_xor_lane<2>(ss_fu(b)));
+  a = a + ss_uf(ss_xor_lane<1>(ss_fu(a)));
+  b = b + ss_uf(ss_xor_lane<1>(ss_fu(b)));
+}
+
 SS_DEV float ss_wave_max(float v) {
   return ss_uf(ss_butterfly(ss_fu(v), [](uint32_t a, uint32_t b) { return ss_fu(fmaxf(ss_uf(a), ss_uf(b))); }));
 }

@@ -573,27 +573,35 @@ SS_DEV void stage_x(const VerifyArgs& a, uint4* xfl, float (*gx)[kTBv], float* r
 
 // One dense bf16 row (16-byte words wv[jj] = elements 512 jj + 8 lane .. +7, already in registers) against the
 // staged bf16 x fragments, in the dense_rows_kernel order: per lane, fused multiply-adds over its elements in order,
-// then the wave butterfly.
+// then the wave butterfly. Tokens go in pairs, two independent chains side by side (a token t >= nt of a pair holds
+// token 0's fragments; its sum is formed and not used).
 template <int NJX>
 SS_DEV void dense_dot(const uint4 (&wv)[NJX], const uint4* xfl, int nt, float out[kTBv]) {
+  static_assert(kTBv % 2 == 0, "token pairs");
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int t = 0; t < kTBv; ++t) {
+  for (int t = 0; t < kTBv; t += 2) {
     if (t >= nt) break;
-    float ac = 0.f;
+    float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int jj = 0; jj < NJX; ++jj) {
-      const uint4 xv = xfl[xfrag_index(512 * jj + 8 * lane, t)];
+      const uint4 x0 = xfl[xfrag_index(512 * jj + 8 * lane, t)];
+      const uint4 x1 = xfl[xfrag_index(512 * jj + 8 * lane, t + 1)];
       const uint32_t ww[4] = {wv[jj].x, wv[jj].y, wv[jj].z, wv[jj].w};
-      const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+      const uint32_t xx0[4] = {x0.x, x0.y, x0.z, x0.w};
+      const uint32_t xx1[4] = {x1.x, x1.y, x1.z, x1.w};
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float wf = (e & 1) ? bf_hi(ww[e >> 1]) : bf_lo(ww[e >> 1]);
-        const float xf = (e >> 2) ? bf_hi(xx[e & 3]) : bf_lo(xx[e & 3]);
-        ac = __builtin_fmaf(xf, wf, ac);
+        const float xf0 = (e >> 2) ? bf_hi(xx0[e & 3]) : bf_lo(xx0[e & 3]);
+        const float xf1 = (e >> 2) ? bf_hi(xx1[e & 3]) : bf_lo(xx1[e & 3]);
+        a0 = __builtin_fmaf(xf0, wf, a0);
+        a1 = __builtin_fmaf(xf1, wf, a1);
       }
     }
-    out[t] = ss_wave_sum(ac);
+    ss_wave_sum2(a0, a1);
+    out[t] = a0;
+    out[t + 1] = a1;
   }
 }
 
@@ -615,23 +623,29 @@ template <int NJX>
 SS_DEV void affine_dot(const uint4 (&wv)[NJX], const uint4* xfl, int nt, float out[kTBv]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
-  for (int t = 0; t < kTBv; ++t) {
+  for (int t = 0; t < kTBv; t += 2) {
     if (t >= nt) break;
-    float ac = 0.f;
+    float a0 = 0.f, a1 = 0.f;
 #pragma unroll
     for (int jj = 0; jj < NJX; ++jj) {
-      const uint4 xv = xfl[xfrag_index(512 * jj + 8 * lane, t)];
-      const uint32_t xx[4] = {xv.x, xv.y, xv.z, xv.w};
+      const uint4 x0 = xfl[xfrag_index(512 * jj + 8 * lane, t)];
+      const uint4 x1 = xfl[xfrag_index(512 * jj + 8 * lane, t + 1)];
+      const uint32_t xx0[4] = {x0.x, x0.y, x0.z, x0.w};
+      const uint32_t xx1[4] = {x1.x, x1.y, x1.z, x1.w};
       const float sc = bf_lo(wv[jj].y), bi = bf_hi(wv[jj].y);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float q = (float)((wv[jj].x >> (4 * e)) & 0xFu);
         const float wf = q * sc + bi;
-        const float xf = (e >> 2) ? bf_hi(xx[e & 3]) : bf_lo(xx[e & 3]);
-        ac = __builtin_fmaf(xf, wf, ac);
+        const float xf0 = (e >> 2) ? bf_hi(xx0[e & 3]) : bf_lo(xx0[e & 3]);
+        const float xf1 = (e >> 2) ? bf_hi(xx1[e & 3]) : bf_lo(xx1[e & 3]);
+        a0 = __builtin_fmaf(xf0, wf, a0);
+        a1 = __builtin_fmaf(xf1, wf, a1);
       }
     }
-    out[t] = ss_wave_sum(ac);
+    ss_wave_sum2(a0, a1);
+    out[t] = a0;
+    out[t + 1] = a1;
   }
 }
 
