@@ -171,7 +171,6 @@ struct VSmem {
   float shv[16][kTBv];
   float rnorm[kTBv];              // 1 / rms of each token (chained layers)
   float xch[4][16 * kTBv];        // per-wave exchange of one item's 16 columns x 4 tokens
-  alignas(16) int ekey[64];       // unique_setup keys
   alignas(16) uint4 zero_h[4];    // zeros: the h operand of A rows that do not use the expert (phase D)
   int nt, nu;
 };
@@ -202,16 +201,20 @@ SS_DEV ss_u32x4 as_v(uint4 v) {
 }
 
 // Unique experts of the block in first-occurrence order from s.ids. Wave 0 only; caller syncs.
-// Each lane publishes a key (its expert, or a negative value no other lane has when the entry is unusable) and
-// finds the first lane with the same key by broadcast LDS reads.
+// The lanes holding the same expert come from ballots of the expert id's bits (ids < kMaxEv = 2^9; an unusable
+// entry matches no lane), so the step has no LDS exchange and no branch per entry: the first lane of each expert
+// takes the next unique index, stores its record pointer and the expert's (token, rank) bits for every token, and
+// errors are raised from one uniform branch.
 SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
+  static_assert(kMaxEv <= 512 && kMaxQv <= 64, "9 id bits, one wave of entries");
   const int lane = threadIdx.x;
   const int nq = s.nt * a.K;
   int e = -1, slot = -1;
-  bool valid = false;
+  bool in_e = false, valid = false;
   if (lane < nq) {
     e = s.ids[lane];
-    if (e >= 0 && e < a.E) {
+    in_e = e >= 0 && e < a.E;
+    if (in_e) {
       if (tables_in_lds) {
         slot = s.map[e];
       } else {
@@ -219,34 +222,30 @@ SS_DEV void unique_setup(const VerifyArgs& a, VSmem& s, bool tables_in_lds) {
         if (mi >= 0 && mi < a.map_len) slot = a.map[mi];
       }
       valid = slot >= 0 && (int64_t)slot < a.n_slots;
-      if (!valid) ss_raise(a.err, SS_ERR_SLOT);
-    } else {
-      ss_raise(a.err, SS_ERR_EXPERT_ID);
     }
   }
-  const int key = valid ? e : -1 - lane;
-  s.ekey[lane] = key;
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  int j0 = 64;
-#pragma unroll 4
-  for (int j = 0; j < nq; j += 4) {
-    const int4 k4 = *reinterpret_cast<const int4*>(&s.ekey[j]);
-    if (j0 == 64 && k4.x == key) j0 = j;
-    if (j0 == 64 && k4.y == key) j0 = j + 1;
-    if (j0 == 64 && k4.z == key) j0 = j + 2;
-    if (j0 == 64 && k4.w == key) j0 = j + 3;
+  const uint64_t bad_e = __ballot(lane < nq && !in_e), bad_s = __ballot(in_e && !valid);
+  if ((bad_e | bad_s) != 0ull && lane == 0)
+    ss_raise(a.err, (bad_e ? SS_ERR_EXPERT_ID : 0) | (bad_s ? SS_ERR_SLOT : 0));
+  uint64_t same = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 9; ++b) {
+    const bool bit = ((e >> b) & 1) != 0;
+    const uint64_t bb = __ballot(valid && bit);
+    same &= bit ? bb : ~bb;
   }
+  const int j0 = valid ? (int)__builtin_ctzll(same) : 64;  // a valid lane is in its own set
   const bool first = valid && j0 == lane;
-  const uint64_t mask = __ballot(first);
-  const int uidx = valid ? __popcll(mask & ((1ull << j0) - 1ull)) : -1;
-  if (first) s.base[uidx] = tables_in_lds ? s.base_e[e] : reinterpret_cast<const uint8_t*>(a.slot_ptr[slot]);
-  if (lane < nq) {
-    s.use_u[lane] = uidx;
-    if (valid) atomicOr(&s.umask[uidx][lane / a.K], 1u << (lane % a.K));
+  const uint64_t fm = __ballot(first);
+  const int uidx = valid ? __popcll(fm & ((1ull << j0) - 1ull)) : -1;
+  if (first) {
+    s.base[uidx] = tables_in_lds ? s.base_e[e] : reinterpret_cast<const uint8_t*>(a.slot_ptr[slot]);
+    const uint32_t km = (uint32_t)((1ull << a.K) - 1ull);
+#pragma unroll
+    for (int t = 0; t < kTBv; ++t) s.umask[uidx][t] = t * a.K < 64 ? (uint32_t)(same >> (t * a.K)) & km : 0u;
   }
-  if (lane == 0) s.nu = __popcll(mask);
+  if (lane < nq) s.use_u[lane] = uidx;
+  if (lane == 0) s.nu = __popcll(fm);
 }
 
 // Router tail of token t in one wave (the operations and order of router_topk_kernel): lane l holds the entries
