@@ -290,19 +290,37 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32
   for (int i = 0; i < NV; ++i) m = lane + 64 * i < E ? fmaxf(m, v[i]) : m;
   m = ss_wave_max(m);
   float acc = 0.f;
+  float ve[NV];  // the exponentials, kept for the rare entries whose quotient takes the division
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
     v[i] = ss_expf(v[i] - m);
+    ve[i] = v[i];
     acc = acc + (lane + 64 * i < E ? v[i] : 0.f);
   }
   const float z = ss_wave_sum(acc);
+  // v / z for every entry from one division: q = RN(v * RN(1/z)) is within an ulp of v / z, the remainder
+  // v - q z is exact (fma), and RN(q + rem * RN(1/z)) is the correctly rounded quotient (Markstein's theorem; here
+  // v is in [0, 1] and z in [1, E], and a v in (0, 2^-64), where the remainder could underflow, takes the
+  // division itself). NaN inputs give NaN either way.
+  const float rz = 1.f / z;
+  bool tiny = false;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const float vi = v[i];
+    const float q = vi * rz;
+    const float rem = __builtin_fmaf(-q, z, vi);
+    v[i] = __builtin_fmaf(rem, rz, q);
+    tiny = tiny || (vi > 0.f && vi < 0x1p-64f);
+  }
+  if (__any(tiny)) {
+    // rare (a probability below 2^-64 somewhere in the wave): every entry of the wave takes the division
+#pragma unroll
+    for (int i = 0; i < NV; ++i) v[i] = ve[i] / z;
+  }
   // kp = key + 1 for a present, untaken entry (NaN probabilities have key 0, so kp 1), 0 once taken or absent.
   uint32_t kp[NV];
 #pragma unroll
-  for (int i = 0; i < NV; ++i) {
-    v[i] = v[i] / z;
-    kp[i] = lane + 64 * i < E ? ss_key(v[i]) + 1u : 0u;
-  }
+  for (int i = 0; i < NV; ++i) kp[i] = lane + 64 * i < E ? ss_key(v[i]) + 1u : 0u;
   if (stamps && lane == 0) stamps[1] = __builtin_amdgcn_s_memrealtime();
   // tau: the largest threshold with zero low 16 bits that at least K lane maxima reach. Those K entries are >= tau,
   // so every entry of the top K is too. The entries >= tau (a few more than K on router rows) go to LDS in index
