@@ -312,6 +312,11 @@ int ssmoe_bench_stream_read(const void* src, int64_t bytes, uint32_t* out, int g
  * operands from seed uint32 [8]: 2 * 16 * 16 * 32 * 8 * iters flop per wave. out fp32 [grid * 4] (the wave sums). */
 int ssmoe_bench_mfma_bf16(const uint32_t* seed, int iters, float* out, int grid, void* stream);
 
+/* No reference counterpart: the fp32 -> bf16 rounding every kernel of this library applies (round to nearest even;
+ * a NaN keeps its top bits with the quiet bit set: torch's .to(torch.bfloat16) and the reference's weight and
+ * activation casts), exported so that it can be checked on any bit pattern. x fp32 [n], y bf16 bits [n]. */
+int ssmoe_bf16_round(const float* x, uint16_t* y, int64_t n, void* stream);
+
 /* Bytes of the workspace ssmoe_sample_rows needs (-1 outside 1 <= R <= 64, 1 <= V <= 1,048,576); zero it before
  * its first use (it keeps a launch counter). */
 int64_t ssmoe_sample_rows_workspace_bytes(int R, int V);

@@ -61,6 +61,7 @@ SIGNATURES = {
     "ssmoe_sample_rows_workspace_bytes": (_I64, [_I, _I]),
     "ssmoe_bench_stream_read": (_I, [_P, _I64, _P, _I, _P]),
     "ssmoe_bench_mfma_bf16": (_I, [_P, _I, _P, _I, _P]),
+    "ssmoe_bf16_round": (_I, [_P, _P, _I64, _P]),
     "ssmoe_sample_rows": (_I, [_P, _I, _I, _F, _P, _P, _I64, _P, _P]),
     "ssmoe_pool_open": (_I, [ctypes.c_char_p, _I, _I, _I64, _I, _I64, _P, _P, ctypes.POINTER(_P)]),
     "ssmoe_pool_close": (_I, [_P]),

@@ -47,14 +47,10 @@ SS_DEV void stg16(void* p, uint4 v) {
 // ---------------------------------------------------------------- bf16 <-> fp32
 SS_DEV float ss_bf16_to_f32(uint32_t b) { return __uint_as_float((b & 0xFFFFu) << 16); }
 
-// Round to nearest even; NaN stays a quiet NaN with its sign.
-// Round to nearest even with the hardware conversion (v_cvt_pk_bf16_f32), NaN -> the input's high half with the
-// quiet bit set (selected, not branched on).
-SS_DEV uint32_t ss_f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t h = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
-  return (u & 0x7FFFFFFFu) > 0x7F800000u ? (((u >> 16) | 0x40u) & 0xFFFFu) : h;
-}
+// Round to nearest even; a NaN keeps its sign and top bits with the quiet bit set ((u >> 16) | 0x40), torch's rule.
+// gfx950's conversion (v_cvt_pk_bf16_f32) is exactly that rule on every fp32 pattern, NaNs included, so no select
+// follows it; ssmoe_bf16_round exports this function so that the rule is tested on the device.
+SS_DEV uint32_t ss_f32_to_bf16(float f) { return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f)); }
 
 SS_DEV float ss_round_bf16(float f) { return ss_bf16_to_f32(ss_f32_to_bf16(f)); }
 

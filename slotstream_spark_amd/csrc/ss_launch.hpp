@@ -187,6 +187,7 @@ hipError_t launch_accept_sampled(const float* target, const int32_t* drafts, int
 // Achievable-peak kernels (ss_peaks.hip).
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* out, int grid, hipStream_t st);
 hipError_t launch_mfma_loop(const uint32_t* seed, int iters, float* out, int grid, hipStream_t st);
+hipError_t launch_bf16_round(const float* x, uint16_t* y, int64_t n, hipStream_t st);
 
 // Expert slot pool (ss_pool.hip).
 struct Pool;

@@ -59,7 +59,22 @@ __global__ __launch_bounds__(256) void mfma_loop_kernel(const uint32_t* __restri
   if (lane == 0) out[blockIdx.x * 4 + (threadIdx.x >> 6)] = s;
 }
 
+// y[i] = ss_f32_to_bf16(x[i]): the rounding every kernel of the library applies, exported so that tests can hold it
+// to the reference's rule (round to nearest even; NaN: the top bits with the quiet bit set) on any bit pattern.
+__global__ __launch_bounds__(256) void bf16_round_kernel(const float* __restrict__ x, uint16_t* __restrict__ y,
+                                                         int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) y[i] = (uint16_t)ss_f32_to_bf16(x[i]);
+}
+
 }  // namespace
+
+hipError_t launch_bf16_round(const float* x, uint16_t* y, int64_t n, hipStream_t st) {
+  const int64_t blocks = (n + 255) / 256;
+  const int grid = (int)(blocks < 4096 ? (blocks > 0 ? blocks : 1) : 4096);
+  hipLaunchKernelGGL(bf16_round_kernel, dim3(grid), dim3(256), 0, st, x, y, n);
+  return hipGetLastError();
+}
 
 hipError_t launch_stream_read(const void* src, size_t bytes, uint32_t* out, int grid, hipStream_t st) {
   hipLaunchKernelGGL(stream_read_kernel, dim3(grid), dim3(256), 0, st, static_cast<const uint4*>(src), bytes / 16, out);

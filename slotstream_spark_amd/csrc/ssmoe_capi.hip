@@ -848,6 +848,13 @@ int ssmoe_bench_mfma_bf16(const uint32_t* seed, int iters, float* out, int grid,
   return hip_check(ss::launch_mfma_loop(seed, iters, out, grid, static_cast<hipStream_t>(stream)), "mfma loop launch");
 }
 
+int ssmoe_bf16_round(const float* x, uint16_t* y, int64_t n, void* stream) {
+  if (n < 0) return fail(SSMOE_EINVAL, "n must be >= 0, got %lld", (long long)n);
+  if (n == 0) return SSMOE_OK;
+  if (!x || !y) return fail(SSMOE_EINVAL, "x and y must be non-null");
+  return hip_check(ss::launch_bf16_round(x, y, n, static_cast<hipStream_t>(stream)), "bf16 round launch");
+}
+
 int64_t ssmoe_sample_rows_workspace_bytes(int R, int V) {
   if (R < 1 || R > 64 || V < 1 || V > (1 << 20)) return -1;
   return ss::draw_work_floats(R, V) * 4;
