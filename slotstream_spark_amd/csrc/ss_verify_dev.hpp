@@ -293,7 +293,7 @@ SS_DEV void router_tail_wave(const VerifyArgs& a, const uint64_t* logits, uint32
   float ve[NV];  // the exponentials, kept for the rare entries whose quotient takes the division
 #pragma unroll
   for (int i = 0; i < NV; ++i) {
-    v[i] = ss_expf(v[i] - m);
+    v[i] = ss_expf_le0(v[i] - m);  // v - m <= 0 (an absent entry holds entry 0's value, which is at most m)
     ve[i] = v[i];
     acc = acc + (lane + 64 * i < E ? v[i] : 0.f);
   }
