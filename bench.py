@@ -913,13 +913,18 @@ def main():
     ap.add_argument("--legs", default="isolated,decode,prefill,config2,config4,lm_head,step,draft,pool,ref_decode,"
                                       "ref_chain,peaks",
                     help="comma list of legs besides the headline chain: isolated, decode, prefill, config2, "
-                         "config4, lm_head, step, draft, pool, ref_decode, ref_chain, peaks")
+                         "config4, lm_head, step, draft, pool, ref_decode, ref_chain, peaks (chain alone: chain)")
     ap.add_argument("--prefill-layers", type=int, default=4)
     ap.add_argument("--config2-steps", type=int, default=1000)
     ap.add_argument("--config4-layers", type=int, default=48)
     ap.add_argument("--config4-steps", type=int, default=256)
     ap.add_argument("--copy-calib", action="store_true", help="run 3 x 256 MiB device copies first (PMC scaling)")
     args = ap.parse_args()
+    known = {"isolated", "decode", "prefill", "config2", "config4", "lm_head", "step", "draft", "pool", "ref_decode",
+             "ref_chain", "peaks", "chain"}  # "chain": the headline leg alone (it always runs)
+    unknown = sorted(set(args.legs.split(",")) - known - {""})
+    if unknown:
+        ap.error(f"unknown legs {unknown}; known: {sorted(known)}")
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU: every GPU box here has one; sharding the path "
                                    "over several GPUs is designed but not built"}))
