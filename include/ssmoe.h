@@ -56,7 +56,9 @@ int ssmoe_record_layout(int H, int I, int64_t* off);
  * _rank_sum :100-110). x: [R, H] bf16 (x_is_f32 = 0) or fp32 (1); expert_ids int32 [R, K]; weights fp32 [R, K];
  * the record of expert e is at slot_ptr[map[layer * E + e]] (map int32 [map_len], slot_ptr int64 [n_slots]).
  * Writes h_buf fp32 [R, K, I], o_buf fp32 [R, K, H] (o = (Wd h) * w), out fp32 [R, H] (rank-order sum).
- * Constraints: H % 128 == 0, H <= 4096, I % 128 == 0, I <= 1024, 1 <= K <= 16. */
+ * Constraints: H % 128 == 0, H <= 4096, I % 128 == 0, I <= 1024, 1 <= K <= 16.
+ * Takes no workspace (as the reference's): the library's static scratch has one slot per stream for the first 8
+ * streams that call it on a device, so calls on different streams may overlap; a ninth stream shares a slot. */
 int ssmoe_moe_decode(const void* x, int x_is_f32, const int32_t* expert_ids, const float* weights, int layer,
                      const int32_t* map, int64_t map_len, const int64_t* slot_ptr, int64_t n_slots, float* h_buf,
                      float* o_buf, float* out, int R, int H, int I, int K, int E, void* stream);

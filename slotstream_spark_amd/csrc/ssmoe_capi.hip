@@ -17,9 +17,12 @@ __device__ int ss_status_storage;
 
 // Scratch of ssmoe_moe_decode, which (like the reference's moe_decode) takes no workspace argument: h fragments,
 // h partial sums and the persistent kernel's counters for one block of <= 4 rows. Zero at load; every launch leaves
-// its counters zero. Calls that overlap on one device share it and race.
+// its counters zero. One slot per stream for the first kDecodeSlots streams that call it on a device (a host table
+// assigns them), so calls on different streams do not share a slot; calls on one stream run in order. A stream past
+// the first kDecodeSlots shares a slot with an earlier one.
 constexpr size_t kDecodeScratch = 320 * 1024;
-__device__ __align__(256) unsigned char ss_decode_scratch[kDecodeScratch];
+constexpr int kDecodeSlots = 8;
+__device__ __align__(256) unsigned char ss_decode_scratch[kDecodeSlots][kDecodeScratch];
 
 // Scratch of ssmoe_moe_verify_layer_noalloc, the verify layer for callers that cannot allocate: the counters, tagged
 // router logits, shared-expert rows and h fragments that ssmoe_moe_verify_layer keeps in the caller's workspace.
@@ -81,16 +84,31 @@ int status_ptr(int** out) {
   return ok();
 }
 
-int decode_scratch_ptr(void** out) {
+// The decode scratch slot of `stream` on the current device: the stream's own slot once it has one, else the next
+// free one, else (more streams than slots) the slot its handle hashes to.
+hipStream_t g_decode_streams[kMaxDevices][kDecodeSlots];
+int g_decode_used[kMaxDevices] = {0};
+std::mutex g_decode_mu;
+
+int decode_scratch_ptr(hipStream_t stream, void** out) {
   int dev = 0;
   if (int rc = current_device(&dev)) return rc;
+  std::lock_guard<std::mutex> lock(g_decode_mu);
   if (!g_decode_scratch[dev]) {
     void* p = nullptr;
     hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(ss_decode_scratch));
     if (e != hipSuccess) return hip_check(e, "hipGetSymbolAddress(decode scratch)");
     g_decode_scratch[dev] = p;
   }
-  *out = g_decode_scratch[dev];
+  int slot = -1;
+  for (int i = 0; i < g_decode_used[dev] && slot < 0; ++i)
+    if (g_decode_streams[dev][i] == stream) slot = i;
+  if (slot < 0 && g_decode_used[dev] < kDecodeSlots) {
+    slot = g_decode_used[dev]++;
+    g_decode_streams[dev][slot] = stream;
+  }
+  if (slot < 0) slot = (int)((reinterpret_cast<uintptr_t>(stream) >> 4) % kDecodeSlots);
+  *out = static_cast<unsigned char*>(g_decode_scratch[dev]) + (size_t)slot * kDecodeScratch;
   return ok();
 }
 
@@ -182,8 +200,8 @@ int ssmoe_moe_decode(const void* x, int x_is_f32, const int32_t* expert_ids, con
   int* err = nullptr;
   void* scratch = nullptr;
   if (int rc = status_ptr(&err)) return rc;
-  if (int rc = decode_scratch_ptr(&scratch)) return rc;
   hipStream_t st = static_cast<hipStream_t>(stream);
+  if (int rc = decode_scratch_ptr(st, &scratch)) return rc;
   const size_t xsz = x_is_f32 ? 4 : 2;
   for (int r0 = 0; r0 < R; r0 += kBlock) {
     ss::VerifyArgs a{};

@@ -147,3 +147,28 @@ def test_validation_errors(pool_b):
         moe_decode(x, ids, w, 0, pool_b.map, pool_b.slot_ptr, h, o[:, :9], out)
     with pytest.raises(ValueError):
         moe_decode(x, ids, w, 0, pool_b.map, pool_b.slot_ptr, h, o, out, cfg={"bk": 96})
+
+
+def test_two_streams_overlap(pool_b):
+    """Calls on two streams at once (each stream has its own slot of the static scratch): every result equals the
+    same call run alone, bit for bit."""
+    print("[moe_decode] two streams", flush=True)
+    dev = pool_b.device
+    cases = [(rand_x(4, 2048, seed), rand_ids(4, 8, pool_b.experts, seed + 1), rand_weights(4, 8, seed + 2))
+             for seed in (11, 21)]
+    alone = [_run(pool_b, *c)[2] for c in cases]
+    cases = [tuple(t.to(dev) for t in c) for c in cases]
+    streams = [torch.cuda.Stream(device=dev), torch.cuda.Stream(device=dev)]
+    torch.cuda.synchronize()
+    outs = []
+    for _ in range(20):
+        for st, (x, ids, w) in zip(streams, cases):
+            with torch.cuda.stream(st):
+                h = torch.empty((4, 8, pool_b.inter), device=dev)
+                o = torch.empty((4, 8, pool_b.hidden), device=dev)
+                out = torch.empty((4, pool_b.hidden), device=dev)
+                moe_decode(x, ids, w, 0, pool_b.map, pool_b.slot_ptr, h, o, out, experts_per_layer=pool_b.experts)
+                outs.append(out)
+    torch.cuda.synchronize()
+    for i, out in enumerate(outs):
+        assert torch.equal(out, alone[i % 2]), i
