@@ -51,6 +51,25 @@ def test_verify_layer_vs_oracle(experts, k, bias, t):
     assert err_y <= REL_Y
 
 
+def test_verify_layer_extreme_router_logits():
+    """Router logits spread over about +-130 (router weights x 50): in every token's row some probabilities fall in
+    (0, 2^-64), where the kernel's softmax quotient takes the IEEE division instead of its one-division form, and
+    many underflow to 0; ids and weights bit for bit against the oracle."""
+    print("[verify] extreme router logits", flush=True)
+    pool = make_pool(512, 2048, 512, seed=2201)
+    lw = LayerWeights(2048, 512, 512, seed=2201)
+    router_w = (lw.router_w.float() * 50.0).to(torch.bfloat16)
+    layer = MoEVerifyLayer(pool, 0, router_w, lw.sh_gate, lw.sh_up, lw.sh_down, lw.sh_g, top_k=10)
+    x = normal_bf16((2, 2048), 1.0, 2202)
+    y, ids, w = layer(x)
+    torch.cuda.synchronize()
+    _, probs, rids, rw = O.router(bits(x), bits(router_w), 10)
+    assert ((probs > 0) & (probs < 2.0 ** -64)).any(axis=1).all()
+    assert (probs == 0).any(axis=1).all()
+    assert np.array_equal(ids.cpu().numpy(), rids)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
+
+
 def test_verify_layer_vs_torch_moe_ref():
     """Against the torch CPU restatement of reference_torch.moe_ref (config 0 shape, no bias)."""
     pool, lw, layer, _ = _layer(64, 4, 99, False)
