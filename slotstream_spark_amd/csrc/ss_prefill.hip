@@ -397,10 +397,15 @@ SS_DEV void gemm_loop(uint8_t* lds, const uint32_t* sbt, int nsteps, int aoff0, 
     load(k + PD, slot_c);
     lds_barrier();
   };
+  // Whole groups of PD steps with no guard inside, so that every path into the loop head has the same loads in
+  // flight (a guarded step gave the head a second path without the last slot's loads, and the compiler then waited
+  // for every load at the head: the next steps' prefetches included); the nsteps % PD last steps after it.
+  const int nfull = nsteps - nsteps % PD;
 #pragma unroll 1
-  for (int k = 0; k < nsteps; k += PD)
+  for (int k = 0; k < nfull; k += PD) ss_static_for<PD>([&](auto u) { step(k + decltype(u)::value, u); });
+  if (nfull < nsteps)
     ss_static_for<PD>([&](auto u) {
-      if (k + decltype(u)::value < nsteps) step(k + decltype(u)::value, u);
+      if (nfull + decltype(u)::value < nsteps) step(nfull + decltype(u)::value, u);
     });
 }
 
