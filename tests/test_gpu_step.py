@@ -9,6 +9,7 @@ import torch
 
 from oracle import oracle as O
 from slotstream_spark_amd.engine.step import MoEWeights, MTPStepGraph, residual_rmsnorm
+from slotstream_spark_amd.engine.verify import MoEVerifyChain, MoEVerifyLayer
 from slotstream_spark_amd.kernels.gemv_affine import AffineWeight, gemv
 from slotstream_spark_amd.memory.synth import LayerWeights, normal_bf16, zipf_bias
 from tests.gpu_util import DenseCache, bits, make_pool
@@ -213,6 +214,47 @@ def test_chain_at_config4_layer_shape(T, NL4):
         assert np.array_equal(bits(sg.mixed[NL4]), mx)
         print(f"trial {trial}: unique experts per layer "
               f"{[len(set(sg.ids[l].cpu().flatten().tolist())) for l in range(NL4)]}", flush=True)
+
+
+def test_chain_one_row_equals_per_layer_launches():
+    """The chain launch at T = 1 (MoEVerifyChain directly: a step graph always verifies at least two rows), where the
+    dense rows' token pairs and the two-token item paths run with an absent token: three E 512 / top-10 layers in one
+    launch equal one ssmoe_moe_verify_layer_chain launch per layer bit for bit, and layer 0 routes as the oracle."""
+    E4, K4, NL = 512, 10, 3
+    print(f"[chain T=1] {NL} layers, E={E4} K={K4}", flush=True)
+    pool = make_pool(E4, H, I, seed=705, layers=NL)
+    lws = [LayerWeights(H, E4, 512, seed=710 + l) for l in range(NL)]
+    layers = [MoEVerifyLayer(pool, l, w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, top_k=K4,
+                             router_bias=zipf_bias(E4, 1.1, 720 + l)) for l, w in enumerate(lws)]
+    if not MoEVerifyChain.supported(H, I, 512, K4, E4):
+        pytest.skip("the chain needs E + Is >= 4 x CUs and H / 16 < CUs")
+    norms = [normal_bf16((H,), 0.1, 730 + l) + 1 for l in range(NL)]
+    dev = pool.device
+
+    def bufs():
+        return ([torch.empty((1, H), dtype=torch.bfloat16, device=dev) for _ in range(NL)],
+                [torch.empty((1, K4), dtype=torch.int32, device=dev) for _ in range(NL)],
+                [torch.empty((1, K4), dtype=torch.float32, device=dev) for _ in range(NL)],
+                [torch.empty((1, H), dtype=torch.bfloat16, device=dev) for _ in range(NL)])
+
+    ys, ids, ws, so = bufs()
+    chain = MoEVerifyChain(layers, ys, ids, ws, stream_outs=so, norm_weights=norms)
+    for trial in range(2):
+        x = normal_bf16((1, H), 1.0, 740 + trial).to(dev)
+        chain.run(x)
+        ys1, ids1, ws1, so1 = bufs()
+        s = x
+        for l in range(NL):
+            layers[l].chain(s, ys1[l], ids1[l], ws1[l], stream_out=so1[l], norm_weight=norms[l])
+            s = so1[l]
+        torch.cuda.synchronize()
+        for l in range(NL):
+            assert torch.equal(ids[l], ids1[l]) and torch.equal(ws[l], ws1[l]), (trial, l)
+            assert torch.equal(ys[l], ys1[l]) and torch.equal(so[l], so1[l]), (trial, l)
+        xb = O.residual_rmsnorm(bits(x), None, bits(norms[0]))[1]
+        _, _, rids, rw = O.router(xb, bits(lws[0].router_w), K4, layers[0].router_bias.cpu().numpy())
+        assert np.array_equal(ids[0].cpu().numpy(), rids)
+        assert np.array_equal(ws[0].cpu().numpy().view(np.uint32), rw.view(np.uint32))
 
 
 @pytest.mark.parametrize("T", [2, 3])
