@@ -499,7 +499,8 @@ def ref_decode_leg(steps, dev):
 def step_leg(pool, weights, biases, steps, dev):
     """The whole verify round in one HIP graph (engine/step.py MTPStepGraph) at full size: 48 chained
     config-1 layers (residual + RMSNorm between them), the 248,320 x 2048 affine 4-bit lm_head fused with the greedy
-    round, and the MTP head's MoE (map layer 48), for depth 1 (T = 2) and depth 3 (T = 4). Timed with HIP events
+    round, and the MTP head's MoE (map layer 48), for depth 1 (T = 2), depth 2 (T = 3, the reference's own verify
+    width, engine/mtp.py:48) and depth 3 (T = 4). Timed with HIP events
     around `steps` replays; one int32 result vector per round is the only thing the host would read back."""
     import torch
 
@@ -514,7 +515,7 @@ def step_leg(pool, weights, biases, steps, dev):
     lm = AffineWeight(q, sc, (-8 * sc.float()).to(torch.bfloat16), 4, 64, N, H)
     mw = [MoEWeights(w.router_w, w.sh_gate, w.sh_up, w.sh_down, w.sh_g, b) for w, b in zip(weights, biases)]
     res = {"layers": NL, "head_layer": NL, "lm_head": f"{N} x {H} affine 4-bit gs64"}
-    for depth in (1, 3):
+    for depth in (1, 2, 3):
         sg = MTPStepGraph(pool, mw[:NL], lm, depth, head=mw[NL], top_k=K, device=dev)
         sg.step(normal_bf16((depth + 1, H), 1.0, 2722, dev), torch.zeros(depth, dtype=torch.int32, device=dev))
         for _ in range(2):
