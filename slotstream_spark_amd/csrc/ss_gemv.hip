@@ -73,7 +73,11 @@ SS_DEV void greedy_decide(const uint64_t* rkey, const int* rbad, const int32_t* 
 
 SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 SS_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
-SS_DEV float pick_half(uint32_t pair, int hi) { return hi ? bf_hi(pair) : bf_lo(pair); }
+// The high or low bf16 of a pair as fp32 in one byte permute (bytes 3, 2 or 1, 0 of the pair to the top, zeros
+// below; the selector depends on hi only).
+SS_DEV float pick_half(uint32_t pair, int hi) {
+  return __uint_as_float(__builtin_amdgcn_perm(pair, pair, hi ? 0x07060C0Cu : 0x05040C0Cu));
+}
 
 // bf16 pair (element d, element d+4) of 8 consecutive bf16 held as 4 words (e0e1, e2e3, e4e5, e6e7): the element
 // order ss_nibbles_to_bf16 gives the weights.

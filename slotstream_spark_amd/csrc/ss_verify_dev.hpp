@@ -179,7 +179,11 @@ static_assert(kXZero * sizeof(uint4) <= sizeof(float) * kMaxQv * 16, "phase C ze
 
 SS_DEV float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 SS_DEV float bf_hi(uint32_t w) { return __uint_as_float(w & 0xFFFF0000u); }
-SS_DEV float pick_half(uint32_t pair, int hi) { return hi ? bf_hi(pair) : bf_lo(pair); }
+// The high or low bf16 of a pair as fp32 in one byte permute (the selector depends on hi only, so it is formed once
+// per lane): bytes 3, 2 or 1, 0 of the pair to the top, zeros below.
+SS_DEV float pick_half(uint32_t pair, int hi) {
+  return __uint_as_float(__builtin_amdgcn_perm(pair, pair, hi ? 0x07060C0Cu : 0x05040C0Cu));
+}
 
 // bf16 pair (element d, element d+4) of 8 consecutive bf16 held as 4 words (e0e1, e2e3, e4e5, e6e7).
 SS_DEV uint4 perm_pairs(uint4 v) {
