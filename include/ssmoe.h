@@ -24,6 +24,10 @@ extern "C" {
 #define SSMOE_ERR_EXPERT_ID 1 /* expert id outside [0, E) */
 #define SSMOE_ERR_SLOT 2      /* map entry outside [0, n_slots): expert not resident */
 #define SSMOE_ERR_TOKEN 4     /* draft token outside [0, V) */
+#define SSMOE_ERR_NONFINITE 8 /* non-finite logits reached a p/q decision */
+#define SSMOE_ERR_TIMEOUT 16  /* a persistent launch's bounded wait (2^22 polls) for another workgroup ran out: its
+                               * workgroups were not all resident at once, e.g. because a kernel on another stream
+                               * held CUs. The launch still finishes; its outputs are not valid. */
 
 /* Text of the last error on this host thread ("" if none). */
 const char* ssmoe_last_error(void);

@@ -37,6 +37,15 @@ def test_exports_every_declared_symbol(L):
     assert sorted(_lib.SIGNATURES) == names  # the ctypes table binds exactly the header's list
 
 
+def test_status_bits_match_the_kernels():
+    """The status bits include/ssmoe.h publishes are the values the kernels raise (csrc/ss_common.hpp)."""
+    hdr = dict((k, int(v)) for k, v in re.findall(r"#define SSMOE_ERR_(\w+)\s+(\d+)", HEADER.read_text()))
+    src = (ROOT / "slotstream_spark_amd" / "csrc" / "ss_common.hpp").read_text()
+    dev = dict((k, int(v)) for k, v in re.findall(r"\bSS_ERR_(\w+)\s*=\s*(\d+)", src))
+    assert dev and hdr == dev
+    assert all(v & (v - 1) == 0 for v in hdr.values())  # one bit each
+
+
 def test_version_and_error_text(L):
     assert L.ssmoe_version() == _lib.ABI_VERSION
     assert L.ssmoe_record_layout(100, 512, (ctypes.c_int64 * 10)()) == EINVAL
