@@ -4,6 +4,10 @@
   python -m slotstream_spark_amd.rocpd_summary counters RUN_results.db [pat]  per-kernel average of each counter
   python -m slotstream_spark_amd.rocpd_summary grids RUN_results.db [pat]     per kernel and launch shape (workgroups
                                                                               x threads), names like pat
+  python -m slotstream_spark_amd.rocpd_summary sequence RUN_results.db pat n1,n2,...
+                                                 the dispatches of kernels named like pat in launch order, split into
+                                                 consecutive groups of n1, n2, ... dispatches (one group per phase of
+                                                 the program, e.g. per bench configuration), median / min / max each
 """
 from __future__ import annotations
 
@@ -45,7 +49,25 @@ def counters(db: str, pattern: str = "%") -> str:
                      for k, n, v, lo, hi, cnt in rows)
 
 
+def sequence(db: str, pattern: str, sizes: list[int]) -> str:
+    c = sqlite3.connect(db)
+    d = [r[0] for r in c.execute("select end - start from kernels where name like ? order by start", (pattern,))]
+    if sum(sizes) != len(d):
+        raise SystemExit(f"{len(d)} dispatches named like {pattern!r}, groups cover {sum(sizes)}")
+    out = [f"{'group':>5s} {'calls':>6s} {'median_us':>10s} {'min_us':>9s} {'max_us':>9s}"]
+    i = 0
+    for g, n in enumerate(sizes):
+        v = sorted(d[i:i + n])
+        i += n
+        med = v[n // 2] if n % 2 else (v[n // 2 - 1] + v[n // 2]) / 2
+        out.append(f"{g:5d} {n:6d} {med / 1e3:10.2f} {v[0] / 1e3:9.2f} {v[-1] / 1e3:9.2f}")
+    return "\n".join(out)
+
+
 if __name__ == "__main__":
     what, db = sys.argv[1], sys.argv[2]
     pat = sys.argv[3] if len(sys.argv) > 3 else "%"
-    print(kernels(db) if what == "kernels" else grids(db, pat) if what == "grids" else counters(db, pat))
+    if what == "sequence":
+        print(sequence(db, pat, [int(x) for x in sys.argv[4].split(",")]))
+    else:
+        print(kernels(db) if what == "kernels" else grids(db, pat) if what == "grids" else counters(db, pat))
