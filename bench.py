@@ -981,7 +981,7 @@ def main():
     iso = None
     uniq = None
     if "isolated" in legs or "decode" in legs:
-        # the same layers as independent single-layer launches on one input (the round-1 method)
+        # the same layers as independent single-layer launches on one input (verify_kernel, one launch per layer)
         ms_iso = timed_graph(step, args.steps, args.warmup, s)
         uniq = [len(set(ids[l].cpu().flatten().tolist())) for l in range(NL)]
         bytes_iso = sum(layer_bytes(u, T) for u in uniq)
